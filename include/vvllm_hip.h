@@ -1,0 +1,251 @@
+/*
+ * vvllm_hip.h -- C ABI of the MI355X (gfx950) INT8 per-channel linear path.
+ *
+ * This is the drop-in boundary that sits under a vvllm `Backend`
+ * implementation (see vvllm_amd/host/backend_hip.h): plain pointers, sizes
+ * and integer status codes, no C++ or HIP types in any signature.  Each entry
+ * names the reference interface it replaces (paths relative to the vvllm
+ * source tree).  In the reference those functions return void and call
+ * exit(1) on any CUDA error (src/backend/cuda_kernels.cu:11-21); here every
+ * entry returns a vvh_status and never exits.
+ *
+ * Conventions
+ *   - "device pointer" = memory from vvh_malloc / vvh_pool_alloc (or any
+ *     HIP device allocation); "host pointer" = ordinary CPU memory.
+ *   - Weights are [N, K] row-major int8 codes with per-row fp32 scales
+ *     (the QuantizedWeight layout, include/vvllm/quantize/quantize.h:10-14).
+ *   - Activations are [M, K] row-major, outputs and residuals [M, N]
+ *     row-major, in the dtype given by act_dtype / out_dtype.
+ *   - `stream` is a hipStream_t passed as void*; NULL = the null stream.
+ *     Launches are asynchronous on it; errors of the launch itself are
+ *     reported, errors of the kernel's execution surface at the next
+ *     synchronising call.
+ *   - All calls may be made from one host thread at a time per device
+ *     (as the reference, which is single-threaded, README.md:282); the
+ *     allocator and registries are internally locked.
+ */
+#ifndef VVLLM_HIP_H
+#define VVLLM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(__GNUC__)
+#define VVH_API __attribute__((visibility("default")))
+#else
+#define VVH_API
+#endif
+
+/* ---- status codes ---------------------------------------------------- */
+typedef enum vvh_status {
+    VVH_OK = 0,
+    VVH_ERR_INVALID_ARG = 1,      /* null pointer, bad dtype, size overflow, ... */
+    VVH_ERR_NO_DEVICE = 2,        /* no HIP device / bad device index */
+    VVH_ERR_OUT_OF_MEMORY = 3,    /* device allocation failed after cache release */
+    VVH_ERR_HIP = 4,              /* any other HIP runtime error */
+    VVH_ERR_NOT_INITIALIZED = 5,  /* vvh_init has not succeeded yet */
+    VVH_ERR_UNKNOWN_HANDLE = 6,   /* weight / plan handle not registered */
+    VVH_ERR_UNSUPPORTED = 7,      /* valid call the library cannot serve */
+} vvh_status;
+
+/* Element types of activations / outputs / residuals. */
+typedef enum vvh_dtype {
+    VVH_F32 = 0,
+    VVH_F16 = 1,
+} vvh_dtype;
+
+/* Human-readable name of a status code (static storage). */
+VVH_API const char* vvh_status_string(int status);
+/* Message describing the most recent failure on the calling thread
+ * (empty string if none).  Valid until the next failing call. */
+VVH_API const char* vvh_last_error(void);
+/* Library version string, e.g. "vvllm-hip 0.1 gfx950". */
+VVH_API const char* vvh_version(void);
+
+/* ---- device ------------------------------------------------------------ */
+/* Selects HIP device `device` for this process and writes its name.
+ * Replaces cuda_init_device (src/backend/cuda_kernels.h:21-22,
+ * src/backend/cuda_kernels.cu:583-595), which exits the process when no
+ * device is present; this returns VVH_ERR_NO_DEVICE instead. */
+VVH_API int vvh_init(int device, char* name_buf, size_t name_buf_size);
+/* Waits for all work on the device.  Replaces cuda_sync
+ * (src/backend/cuda_kernels.h:19). */
+VVH_API int vvh_sync(void);
+/* Number of compute units of the current device (0 before vvh_init). */
+VVH_API int vvh_device_cu_count(void);
+
+/* ---- raw device memory ------------------------------------------------ */
+/* Replace cuda_malloc / cuda_free / cuda_malloc_host / cuda_free_host /
+ * cuda_memcpy_{h2d,d2h,d2d} (src/backend/cuda_kernels.h:11-17,
+ * src/backend/cuda_kernels.cu:543-579).  Copies are synchronous, as there. */
+VVH_API int vvh_malloc(void** ptr, size_t bytes);
+VVH_API int vvh_free(void* ptr);
+VVH_API int vvh_malloc_host(void** ptr, size_t bytes);
+VVH_API int vvh_free_host(void* ptr);
+VVH_API int vvh_memcpy_h2d(void* dst, const void* src, size_t bytes);
+VVH_API int vvh_memcpy_d2h(void* dst, const void* src, size_t bytes);
+VVH_API int vvh_memcpy_d2d(void* dst, const void* src, size_t bytes);
+
+/* ---- caching allocator -------------------------------------------------- */
+/* Stream-ordered-free caching allocator behind device_allocate /
+ * device_deallocate for the GPU device.  Replaces cuda_pool_alloc /
+ * cuda_pool_free and the CUDA branch of device_allocate / device_deallocate
+ * (src/tensor/tensor.cc:35-68, :72-96).  Unlike the reference's exact-size
+ * free list it rounds requests to size classes, reuses best-fit cached
+ * blocks, and on a failed hipMalloc returns every cached block to the
+ * driver and retries once before reporting VVH_ERR_OUT_OF_MEMORY.
+ * vvh_pool_alloc(&p, 0) yields p = NULL (as device_allocate, tensor.cc:74). */
+VVH_API int vvh_pool_alloc(void** ptr, size_t bytes);
+/* Returns a block to the cache.  Pointers that did not come from the pool
+ * are freed with hipFree, as tensor.cc:58-66 does.  NULL is a no-op. */
+VVH_API int vvh_pool_free(void* ptr);
+/* hipFree every cached (free) block. */
+VVH_API int vvh_pool_release_cached(void);
+
+typedef struct vvh_pool_stats {
+    uint64_t bytes_in_use;      /* rounded bytes handed out and not yet freed */
+    uint64_t bytes_cached;      /* rounded bytes held in the free lists */
+    uint64_t bytes_reserved;    /* bytes_in_use + bytes_cached */
+    uint64_t peak_reserved;
+    uint64_t alloc_calls;
+    uint64_t cache_hits;        /* allocations served without hipMalloc */
+    uint64_t driver_allocs;     /* hipMalloc calls made by the pool */
+    uint64_t oom_releases;      /* times the cache was flushed to satisfy a request */
+} vvh_pool_stats;
+VVH_API int vvh_pool_get_stats(vvh_pool_stats* out);
+
+/* ---- weight mirror ------------------------------------------------------ */
+/* Device-resident copy of one quantized weight (codes + scales + optional
+ * bias), uploaded once.  Replaces BackendCUDA::cache_weight /
+ * cache_weight_fp16 (src/backend/backend_cuda.cc:51-77) and the
+ * int8->fp16 dequantisation it triggers (src/backend/cuda_kernels.cu:804-814,
+ * :833-840): the mirror keeps the raw int8 codes (1 byte/weight, not the
+ * reference's int8 + fp16 = 3 bytes) and scales are applied in the kernels'
+ * epilogue.
+ *
+ * The reference keys its cache by host address only, forever, so a freed and
+ * reused host buffer would hit a stale copy.  Here the key is the full tuple
+ * (weight ptr, scales ptr, bias ptr, N, K); registering an existing host
+ * weight pointer with a different tuple replaces (frees and re-uploads) the
+ * old mirror.  vvh_weight_release drops a mirror explicitly.
+ * Handles are never 0. */
+typedef uint64_t vvh_weight;
+VVH_API int vvh_weight_register(const int8_t* host_weight, const float* host_scales,
+                                const float* host_bias, size_t N, size_t K,
+                                vvh_weight* handle);
+/* Same, for codes/scales/bias already in device memory (not copied, not
+ * owned: the caller keeps them alive until vvh_weight_release). */
+VVH_API int vvh_weight_register_device(const int8_t* dev_weight, const float* dev_scales,
+                                       const float* dev_bias, size_t N, size_t K,
+                                       vvh_weight* handle);
+/* Finds the mirror of a host weight pointer; VVH_ERR_UNKNOWN_HANDLE if none. */
+VVH_API int vvh_weight_find(const int8_t* host_weight, vvh_weight* handle);
+VVH_API int vvh_weight_release(vvh_weight handle);
+/* Device pointers of a mirror (bias NULL if it has none). */
+VVH_API int vvh_weight_device_ptrs(vvh_weight handle, const int8_t** dev_weight,
+                                   const float** dev_scales, const float** dev_bias,
+                                   size_t* N, size_t* K);
+/* Number of live mirrors and their total device bytes. */
+VVH_API int vvh_weight_stats(uint64_t* count, uint64_t* bytes);
+
+/* ---- the linear path ---------------------------------------------------- */
+/* out[M,N] = (inp[M,K] . weight[N,K]^T) * scales[N] + bias[N] (+ residual[M,N])
+ *
+ * Replaces Backend::linear_q8 / linear_q8_add
+ * (include/vvllm/backend/backend.h:62-65, :75-78) as implemented by
+ * BackendCUDA (src/backend/backend_cuda.cc:188-213, :246-275) and the
+ * unused cuda_linear_q8 / cuda_linear_q8_add launchers
+ * (src/backend/cuda_kernels.h:25-26, :51-52).
+ *   - inp, out, residual: device pointers of act_dtype / out_dtype /
+ *     out_dtype; residual may be NULL; out == residual is allowed (the
+ *     in-place residual connection of include/vvllm/model/transformer.h:
+ *     165-166, 187-188).  Any other overlap of out with inp is undefined.
+ *   - The dot product is accumulated in fp32 from the exact int8 codes;
+ *     fp16 activations are used as given (no re-rounding); fp32 activations
+ *     stay fp32 (the reference's CUDA fp32 mode rounds them to fp16 first,
+ *     backend_cuda.cc:205-211; this library does not).
+ *   - Epilogue in fp32, one rounding to out_dtype:
+ *     out = acc*scale + bias + residual.
+ *   - M == 0 or N == 0 is a no-op; K == 0 gives bias (+ residual). */
+VVH_API int vvh_linear_q8(void* out, const void* inp, vvh_weight weight, const void* residual,
+                          size_t M, size_t N, size_t K, int act_dtype, int out_dtype,
+                          void* stream);
+/* Same, with the weight given as device pointers (bias may be NULL). */
+VVH_API int vvh_linear_q8_dev(void* out, const void* inp, const int8_t* dev_weight,
+                              const float* dev_scales, const float* dev_bias,
+                              const void* residual, size_t M, size_t N, size_t K,
+                              int act_dtype, int out_dtype, void* stream);
+
+/* ---- grouped launch ------------------------------------------------------ */
+/* A plan is a fixed list of independent linear_q8 problems of one
+ * (act_dtype, out_dtype) pair, resolved once (kernel choice, tile
+ * decomposition, device-resident descriptor table) and launched with
+ * vvh_plan_run as a single kernel when every problem takes the decode path
+ * (M <= 16), else as one launch per problem.  It is the counterpart of the
+ * reference IR's pre-resolved op list (src/ir/executable.cc:192-354) for the
+ * int8 linears that share an input (q/k/v, transformer.h:139-144) or are
+ * otherwise independent.  Problems must not write memory another problem of
+ * the same plan reads. */
+typedef struct vvh_q8_problem {
+    void* out;
+    const void* inp;
+    const void* residual;      /* may be NULL */
+    const int8_t* weight;      /* device */
+    const float* scales;       /* device */
+    const float* bias;         /* device, may be NULL */
+    uint64_t M, N, K;
+} vvh_q8_problem;
+typedef uint64_t vvh_plan;
+VVH_API int vvh_plan_create(const vvh_q8_problem* problems, size_t count, int act_dtype,
+                            int out_dtype, vvh_plan* plan);
+VVH_API int vvh_plan_run(vvh_plan plan, void* stream);
+VVH_API int vvh_plan_destroy(vvh_plan plan);
+/* Number of kernel launches one vvh_plan_run makes. */
+VVH_API int vvh_plan_launches(vvh_plan plan, int* launches);
+
+/* ---- quantizer and data movement ----------------------------------------- */
+/* Device restatement of quantize_per_channel (src/quantize/quantize.cc:9-48):
+ * per row absmax -> scale = absmax/127 (IEEE division), codes =
+ * clamp(round(w * (1/scale))) with ties away from zero, NaN -> 127; zero
+ * rows get scale 0 and codes 0.  Codes and scales are bit-identical to the
+ * host routine.  All pointers are device pointers. */
+VVH_API int vvh_quantize_per_channel(const float* dev_weight, size_t N, size_t K,
+                                     int8_t* dev_codes, float* dev_scales, void* stream);
+/* Element type conversion on the device (f32<->f16, round to nearest even).
+ * Replaces cuda_fp32_to_fp16 / cuda_fp16_to_fp32
+ * (src/backend/cuda_kernels.h:69, :106). */
+VVH_API int vvh_convert(void* dst, int dst_dtype, const void* src, int src_dtype, size_t n,
+                        void* stream);
+/* Fills n elements of dtype with mean + std * N(0,1) draws from a
+ * counter-based generator (splitmix64 of seed and index, Box-Muller in fp32).
+ * Deterministic for a given (seed, n); used to make synthetic weights and
+ * activations resident in HBM without host traffic. */
+VVH_API int vvh_fill_normal(void* dst, int dtype, size_t n, uint64_t seed, float mean, float std,
+                            void* stream);
+
+/* ---- dispatch introspection ---------------------------------------------- */
+/* Kernel families of the linear path. */
+typedef enum vvh_kernel {
+    VVH_KERNEL_AUTO = 0,      /* size-based choice (default) */
+    VVH_KERNEL_GENERIC = 1,   /* any shape / alignment, one thread per output */
+    VVH_KERNEL_GEMV_F32 = 2,  /* fp32 activations, VALU dot products */
+    VVH_KERNEL_SKINNY = 3,    /* fp16 activations, M <= 16, MFMA 16x16x32 */
+    VVH_KERNEL_GEMM = 4,      /* fp16 activations, LDS-tiled MFMA 32x32x16 */
+} vvh_kernel;
+/* Which kernel family vvh_linear_q8 would use for this call (after the
+ * override below); returns a vvh_kernel value, or a negative status. */
+VVH_API int vvh_linear_q8_choice(size_t M, size_t N, size_t K, int act_dtype, int out_dtype);
+/* Forces one kernel family for subsequent calls on this process (testing and
+ * measurement); VVH_KERNEL_AUTO restores the size-based choice.  A forced
+ * family that cannot serve a call falls back to GENERIC. */
+VVH_API int vvh_set_kernel_override(int kernel);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VVLLM_HIP_H */

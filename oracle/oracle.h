@@ -1,0 +1,66 @@
+/*
+ * CPU oracle for the INT8 per-channel linear path -- TEST INFRASTRUCTURE ONLY.
+ *
+ * This library is the checker, never the product: only tests/, the smoke()
+ * entry of __graft_entry__.py and the cpu_baseline leg of bench.py may load
+ * it.  The product path (libvvllm_hip.so / BackendHIP) never calls it and has
+ * no CPU fallback.
+ *
+ * Every function restates one reference routine (file:line relative to the
+ * vvllm source tree) operation for operation, so that its results can be
+ * compared bit-for-bit with the reference compiled from its own sources
+ * (oracle/_ref, see oracle/Makefile) and with the committed golden vectors.
+ *
+ * Pinning status (see tests/test_oracle.py):
+ *   orc_quantize_per_channel  pinned: reference KATs (quantize_test.cc),
+ *                             closed-form tie/NaN/Inf cases, bit-exact vs _ref
+ *   orc_linear_q8             pinned: reference KATs (backend_naive_test.cc),
+ *                             exact-integer closed forms, fp64 brute force,
+ *                             bit-exact vs _ref and the golden vectors
+ *   orc_linear_q8_add         pinned: bit-exact vs _ref and golden vectors,
+ *                             identity with orc_linear_q8 + fp32 add
+ *   orc_linear_q8_f64         pinned: exact on integer-valued inputs (closed
+ *                             form), agreement with orc_linear_q8 within the
+ *                             fp32 error bound
+ */
+#ifndef VVLLM_ORACLE_H
+#define VVLLM_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* quantize_per_channel, src/quantize/quantize.cc:9-48.
+ * q: [N*K] int8 codes, scales: [N]. */
+void orc_quantize_per_channel(const float* weight, size_t N, size_t K, int8_t* q, float* scales);
+
+/* BackendCPU::linear_q8, src/backend/backend_naive.cc:155-291 (x86 AVX2+FMA
+ * branch :216-274 and epilogue :283-288, the branch selected by the -mavx2
+ * -mfma copts of src/backend/BUILD.bazel:5-8).  bias may be NULL. */
+void orc_linear_q8(float* out, const float* inp, const int8_t* weight, const float* scales,
+                   const float* bias, size_t M, size_t N, size_t K);
+
+/* BackendCPU::linear_q8_add, src/backend/backend_naive.cc:322-335:
+ * linear_q8 into out, then out = out + residual (two fp32 roundings);
+ * out == residual is allowed (the residual is snapshotted first). */
+void orc_linear_q8_add(float* out, const float* inp, const int8_t* weight, const float* scales,
+                       const float* bias, const float* residual, size_t M, size_t N, size_t K);
+
+/* Same contract as orc_linear_q8_add (residual may be NULL) evaluated in
+ * double precision: out = scale*sum(x*q) + bias + residual.  Used for the
+ * error-bound checks, not for parity. */
+void orc_linear_q8_f64(double* out, const float* inp, const int8_t* weight, const float* scales,
+                       const float* bias, const float* residual, size_t M, size_t N, size_t K);
+
+/* Number of threads the oracle uses: always 1 (the reference is
+ * single-threaded, README.md:282). */
+int orc_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

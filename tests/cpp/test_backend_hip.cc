@@ -1,0 +1,238 @@
+// GPU test of BackendHIP through the vvllm Backend interface.
+//
+// The first two cases restate the reference's own tests of the path,
+// src/backend/backend_naive_test.cc:355-405 (LinearQ8MatchesFp32) and
+// :407-425 (LinearQ8WithBias), run on the MI355X backend in fp32 and in fp16
+// mode.  The others cover what the model relies on and the reference never
+// tests: linear_q8_add with out == residual (include/vvllm/model/
+// transformer.h:165-166), M > 1, and the weight mirror refreshing after
+// forget_weight.
+#include <cmath>
+#include <cstdio>
+#include <algorithm>
+#include <cstring>
+#include <stdexcept>
+#include <vector>
+
+#include "backend_hip.h"
+#include "vvllm_hip.h"
+
+using vvllm::BackendHIP;
+
+namespace
+{
+
+int g_failures = 0;
+#define EXPECT_NEAR(a, b, tol, what)                                                   \
+    do {                                                                               \
+        const double _a = (a), _b = (b);                                               \
+        if (!(std::fabs(_a - _b) <= (tol))) {                                          \
+            std::fprintf(stderr, "%s:%d: %s: %.9g vs %.9g (tol %.3g)\n", __FILE__, __LINE__, \
+                         what, _a, _b, (double)(tol));                                 \
+            g_failures++;                                                              \
+        }                                                                              \
+    } while (0)
+
+// IEEE binary16 <-> binary32, round to nearest even (gcc 11 has no _Float16 on x86).
+std::uint16_t to_half(float f)
+{
+    std::uint32_t x;
+    std::memcpy(&x, &f, 4);
+    const std::uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7fffffffu;
+    if (ax >= 0x7f800000u) return (std::uint16_t)(sign | (ax > 0x7f800000u ? 0x7e00u : 0x7c00u));
+    if (ax >= 0x477ff000u) return (std::uint16_t)(sign | 0x7c00u);  // rounds past 65504
+    if (ax < 0x38800000u) {                                          // half subnormal range
+        float af;
+        std::memcpy(&af, &ax, 4);
+        return (std::uint16_t)(sign | (std::uint32_t)std::nearbyint(af * 16777216.0f));
+    }
+    std::uint32_t h = ((((ax >> 23) - 127 + 15) << 10) | ((ax & 0x7fffffu) >> 13));
+    const std::uint32_t rem = ax & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+    return (std::uint16_t)(sign | h);
+}
+float from_half(std::uint16_t h)
+{
+    const std::uint32_t sign = (std::uint32_t)(h & 0x8000u) << 16;
+    const std::uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+    if (e == 0) {
+        const float v = std::ldexp((float)m, -24);
+        return sign ? -v : v;
+    }
+    const std::uint32_t bits = sign | (e == 31 ? (0x7f800000u | (m << 13)) : (((e - 15 + 127) << 23) | (m << 13)));
+    float f;
+    std::memcpy(&f, &bits, 4);
+    return f;
+}
+
+// Activations in the backend's compute dtype, device resident.
+struct Act {
+    bool fp16;
+    std::size_t n;
+    void* dev = nullptr;
+    Act(bool f, std::size_t count) : fp16(f), n(count) { dev = vvllm::hip_device_allocate(n * (f ? 2 : 4)); }
+    ~Act() { vvllm::hip_device_deallocate(dev); }
+    void upload(const std::vector<float>& v)
+    {
+        if (fp16) {
+            std::vector<std::uint16_t> h(n);
+            for (std::size_t i = 0; i < n; i++) h[i] = to_half(v[i]);
+            vvllm::hip_copy_h2d(dev, h.data(), n * 2);
+        } else {
+            vvllm::hip_copy_h2d(dev, v.data(), n * 4);
+        }
+    }
+    std::vector<float> download()
+    {
+        std::vector<float> v(n);
+        if (fp16) {
+            std::vector<std::uint16_t> h(n);
+            vvllm::hip_copy_d2h(h.data(), dev, n * 2);
+            for (std::size_t i = 0; i < n; i++) v[i] = from_half(h[i]);
+        } else {
+            vvllm::hip_copy_d2h(v.data(), dev, n * 4);
+        }
+        return v;
+    }
+    float* f() { return static_cast<float*>(dev); }
+};
+
+// backend_naive_test.cc:355-405, on the HIP backend.
+void linear_q8_matches_fp32(bool fp16)
+{
+    BackendHIP backend(fp16);
+    const std::vector<float> weight_fp32 = {0.5f, -0.3f, 0.1f, 0.9f, 1.0f, 0.0f,
+                                            -1.0f, 0.5f, 0.0f, 0.2f, 0.4f, -0.8f};
+    const std::vector<float> input = {1.0f, 2.0f, 3.0f, 4.0f};
+    const std::size_t N = 3, K = 4;
+    std::vector<float> out_fp32(N, 0.0f);
+    for (std::size_t j = 0; j < N; j++)
+        for (std::size_t k = 0; k < K; k++) out_fp32[j] += input[k] * weight_fp32[j * K + k];
+    std::vector<int8_t> weight_q8(N * K);
+    std::vector<float> scales(N);
+    for (std::size_t j = 0; j < N; j++) {
+        float absmax = 0.0f;
+        for (std::size_t k = 0; k < K; k++) absmax = std::max(absmax, std::fabs(weight_fp32[j * K + k]));
+        scales[j] = absmax / 127.0f;
+        for (std::size_t k = 0; k < K; k++) {
+            float val = weight_fp32[j * K + k] / scales[j];
+            val = std::max(-128.0f, std::min(127.0f, std::round(val)));
+            weight_q8[j * K + k] = static_cast<int8_t>(val);
+        }
+    }
+    Act in(fp16, K), out(fp16, N);
+    in.upload(input);
+    backend.linear_q8(out.f(), in.f(), weight_q8.data(), scales.data(), nullptr, 1, N, K);
+    const std::vector<float> got = out.download();
+    for (std::size_t j = 0; j < N; j++) {
+        float tol = scales[j] * static_cast<float>(K) * 0.5f + 1e-5f;
+        if (fp16) tol += std::fabs(out_fp32[j]) * 1e-3f;  // fp16 output rounding
+        EXPECT_NEAR(got[j], out_fp32[j], tol, fp16 ? "MatchesFp32 fp16" : "MatchesFp32 fp32");
+    }
+}
+
+// backend_naive_test.cc:407-425, on the HIP backend.
+void linear_q8_with_bias(bool fp16)
+{
+    BackendHIP backend(fp16);
+    const std::size_t N = 2, K = 2;
+    const std::vector<int8_t> weight = {127, 0, 0, 127};
+    const std::vector<float> scales = {1.0f / 127.0f, 1.0f / 127.0f};
+    const std::vector<float> bias = {10.0f, 20.0f};
+    Act in(fp16, K), out(fp16, N);
+    in.upload({3.0f, 5.0f});
+    backend.linear_q8(out.f(), in.f(), weight.data(), scales.data(), bias.data(), 1, N, K);
+    const std::vector<float> got = out.download();
+    const float tol = fp16 ? 1e-2f : 1e-4f;  // 25 in fp16 has an ulp of 1/64
+    EXPECT_NEAR(got[0], 13.0f, tol, "WithBias[0]");
+    EXPECT_NEAR(got[1], 25.0f, tol, "WithBias[1]");
+}
+
+// o_proj / down_proj style call: out == residual, M rows, K a multiple of 64.
+void linear_q8_add_inplace(bool fp16, std::size_t M)
+{
+    BackendHIP backend(fp16);
+    const std::size_t N = 96, K = 192;
+    std::vector<int8_t> q(N * K);
+    std::vector<float> scales(N), bias(N), x(M * K), res(M * N);
+    unsigned s = 12345u;
+    auto rnd = [&]() { s = s * 1664525u + 1013904223u; return (int)((s >> 8) % 255) - 127; };
+    for (auto& v : q) v = (int8_t)rnd();
+    for (std::size_t j = 0; j < N; j++) { scales[j] = 0.001f * (1 + j % 7); bias[j] = 0.01f * rnd(); }
+    for (auto& v : x) v = 0.05f * rnd();
+    for (auto& v : res) v = 0.02f * rnd();
+    if (fp16) {  // the device sees fp16 values; use them for the expectation too
+        for (auto& v : x) v = from_half(to_half(v));
+        for (auto& v : res) v = from_half(to_half(v));
+    }
+    Act in(fp16, M * K), xo(fp16, M * N);
+    in.upload(x);
+    xo.upload(res);
+    backend.linear_q8_add(xo.f(), in.f(), q.data(), scales.data(), bias.data(), xo.f(), M, N, K);
+    const std::vector<float> got = xo.download();
+    double maxref = 0, maxerr = 0;
+    for (std::size_t i = 0; i < M; i++)
+        for (std::size_t j = 0; j < N; j++) {
+            double acc = 0;
+            for (std::size_t k = 0; k < K; k++) acc += (double)x[i * K + k] * q[j * K + k];
+            const double r = acc * scales[j] + bias[j] + res[i * N + j];
+            maxref = std::max(maxref, std::fabs(r));
+            maxerr = std::max(maxerr, std::fabs(got[i * N + j] - r));
+        }
+    EXPECT_NEAR(maxerr / maxref, 0.0, fp16 ? 2e-3 : 1e-4, "linear_q8_add in place (normalized)");
+}
+
+// A host weight buffer whose contents change after forget_weight is re-mirrored.
+void mirror_refresh()
+{
+    BackendHIP backend(false);
+    const std::size_t N = 16, K = 64;
+    std::vector<int8_t> q(N * K, 1);
+    std::vector<float> scales(N, 1.0f);
+    std::vector<float> x(K, 1.0f);
+    Act in(false, K), out(false, N);
+    in.upload(x);
+    backend.linear_q8(out.f(), in.f(), q.data(), scales.data(), nullptr, 1, N, K);
+    EXPECT_NEAR(out.download()[0], 64.0, 0.0, "mirror first use");
+    std::fill(q.begin(), q.end(), (int8_t)2);
+    backend.forget_weight(q.data());
+    backend.linear_q8(out.f(), in.f(), q.data(), scales.data(), nullptr, 1, N, K);
+    EXPECT_NEAR(out.download()[0], 128.0, 0.0, "mirror after forget_weight");
+}
+
+void outside_path_throws()
+{
+    BackendHIP backend(false);
+    bool threw = false;
+    try {
+        backend.rms_norm(nullptr, nullptr, nullptr, 0, 0.0f);
+    } catch (const std::logic_error&) {
+        threw = true;
+    }
+    if (!threw) { std::fprintf(stderr, "rms_norm did not throw\n"); g_failures++; }
+}
+
+}  // namespace
+
+int main()
+{
+    for (bool fp16 : {false, true}) {
+        std::printf("[case] LinearQ8MatchesFp32 fp16=%d\n", fp16); std::fflush(stdout);
+        linear_q8_matches_fp32(fp16);
+        std::printf("[case] LinearQ8WithBias fp16=%d\n", fp16); std::fflush(stdout);
+        linear_q8_with_bias(fp16);
+        for (std::size_t M : {1, 5, 40}) {
+            std::printf("[case] linear_q8_add in place fp16=%d M=%zu\n", fp16, M); std::fflush(stdout);
+            linear_q8_add_inplace(fp16, M);
+        }
+    }
+    std::printf("[case] mirror refresh\n"); std::fflush(stdout);
+    mirror_refresh();
+    outside_path_throws();
+    if (g_failures) {
+        std::fprintf(stderr, "test_backend_hip: %d failure(s)\n", g_failures);
+        return 1;
+    }
+    std::printf("test_backend_hip: all passed\n");
+    return 0;
+}

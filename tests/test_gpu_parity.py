@@ -1,0 +1,326 @@
+"""GPU parity of the linear_q8 path against the CPU oracle, through the C ABI.
+
+Bars: int8 codes and scales bit-exact; normalized max
+error max|y - r| / max|r| <= 1e-4 for fp32 activations and <= 2e-3 for fp16
+activations (or fp16 outputs), where r is the oracle (the reference's
+BackendCPU::linear_q8 restated, oracle/oracle.c) on the same inputs; fp16
+activations are handed to the oracle widened to fp32, which is exact.
+
+Every kernel family is forced over shapes that hit its edges (K tails,
+N % 16 != 0, M around the 16-row crossover, K == 0, misaligned pointers), and
+the automatic dispatch is run at every BASELINE.json config shape.
+"""
+import ctypes
+import functools
+import os
+
+import numpy as np
+import pytest
+
+from vvllm_amd import capi
+
+pytestmark = pytest.mark.gpu
+
+F32, F16 = capi.F32, capi.F16
+TOL_F32, TOL_F16 = 1e-4, 2e-3
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+@functools.lru_cache(maxsize=None)
+def weights(N, K, seed, oracle_mod):
+    rng = np.random.default_rng(seed)
+    w = rng.normal(0.0, 0.02, (N, K)).astype(np.float32)
+    q, s = oracle_mod.quantize_per_channel(w)
+    b = rng.normal(0.0, 0.01, N).astype(np.float32)
+    return q, s, b
+
+
+def npd(d):
+    return np.float32 if d == F32 else np.float16
+
+
+def run_case(oracle, M, N, K, act=F16, outd=F16, bias=True, res=None, kernel=capi.KERNEL_AUTO,
+             seed=0, rows=None, x_offset=0):
+    """res: None | "sep" | "inplace".  rows: subset of rows checked against
+    the oracle (all rows when None).  x_offset: byte offset of the activation
+    base (misalignment test)."""
+    print(f"[case] M={M} N={N} K={K} act={act} out={outd} bias={bias} res={res} "
+          f"kernel={capi.KERNEL_NAMES[kernel]} seed={seed}", flush=True)
+    q, s, b = weights(N, K, seed, oracle)
+    rng = np.random.default_rng(seed + 1000)
+    x = rng.normal(0.0, 1.0, (M, K)).astype(np.float32).astype(npd(act))
+    r = rng.normal(0.0, 1.0, (M, N)).astype(np.float32).astype(npd(outd)) if res else None
+    d_q, d_s = capi.DevBuf.from_array(q), capi.DevBuf.from_array(s)
+    d_b = capi.DevBuf.from_array(b) if bias else None
+    d_x = capi.DevBuf(x.nbytes + 64)
+    capi.call("vvh_memcpy_h2d", d_x.addr(x_offset), x.ctypes.data, x.nbytes) if x.nbytes else None
+    d_r = capi.DevBuf.from_array(r) if res == "sep" else None
+    d_y = capi.DevBuf.from_array(r) if res == "inplace" else capi.DevBuf(max(M * N * np.dtype(npd(outd)).itemsize, 1))
+    capi.set_kernel(kernel)
+    try:
+        capi.linear_q8_dev(d_y, d_x.addr(x_offset), d_q, d_s, d_b, d_y if res == "inplace" else d_r,
+                           M, N, K, act, outd)
+        capi.sync()
+    finally:
+        capi.set_kernel(capi.KERNEL_AUTO)
+    y = d_y.to_array(npd(outd), (M, N)).astype(np.float32)
+    sel = np.arange(M) if rows is None else np.asarray(rows)
+    ref = oracle.linear_q8(x[sel].astype(np.float32), q, s, b if bias else None,
+                           None if r is None else r[sel].astype(np.float32))
+    got = y[sel]
+    scale = max(float(np.abs(ref).max()), 1e-30)
+    err = float(np.abs(got - ref).max()) / scale
+    tol = TOL_F32 if (act == F32 and outd == F32) else TOL_F16
+    assert np.isfinite(got).all()
+    assert err <= tol, f"normalized max error {err:.3e} > {tol:.0e}"
+    return err
+
+
+# ---------------------------------------------------------------------------
+# BASELINE.json configs, automatic dispatch
+# ---------------------------------------------------------------------------
+def test_config1_fp32_decode(gpu, oracle):
+    """M=1, K=N=896, fp32 activations/outputs, bias."""
+    assert capi.kernel_choice(1, 896, 896, F32, F32) == "gemv_f32"
+    run_case(oracle, 1, 896, 896, F32, F32, bias=True, seed=11)
+
+
+QWEN05_LAYER = [  # (name, N, K, bias, residual)
+    ("q", 896, 896, True, None), ("k", 128, 896, True, None), ("v", 128, 896, True, None),
+    ("o", 896, 896, False, "inplace"), ("gate", 4864, 896, False, None), ("up", 4864, 896, False, None),
+    ("gate_up", 9728, 896, False, None), ("down", 896, 4864, False, "inplace"),
+]
+
+
+@pytest.mark.parametrize("outd", [F16, F32])
+@pytest.mark.parametrize("proj", QWEN05_LAYER, ids=[p[0] for p in QWEN05_LAYER])
+def test_config2_qwen05_decode(gpu, oracle, proj, outd):
+    name, N, K, bias, res = proj
+    run_case(oracle, 1, N, K, F16, outd, bias=bias, res=res, seed=hash(name) % 1000)
+
+
+def test_config3_lm_head(gpu, oracle):
+    """M=1, K=896, N=151936, fp16 activations, fp32 logits."""
+    run_case(oracle, 1, 151936, 896, F16, F32, bias=False, seed=33)
+
+
+@pytest.mark.parametrize("M", [128, 512, 2048])
+@pytest.mark.parametrize("shape", [(4864, 896), (896, 4864)], ids=["gate_up", "down"])
+def test_config4_prefill(gpu, oracle, M, shape):
+    N, K = shape
+    rows = None if M <= 512 else [0, 1, 127, 128, 129, 511, 1023, 1024, 1500, 2046, 2047]
+    run_case(oracle, M, N, K, F16, F16, bias=False, res="inplace" if K == 4864 else None, seed=44, rows=rows)
+
+
+QWEN15 = [("qo", 1536, 1536), ("kv", 256, 1536), ("gate_up", 8960, 1536), ("down", 1536, 8960)]
+
+
+@pytest.mark.parametrize("M", [1, 4, 16, 64, 256])
+@pytest.mark.parametrize("proj", QWEN15, ids=[p[0] for p in QWEN15])
+def test_config5_qwen15_sweep(gpu, oracle, proj, M):
+    name, N, K = proj
+    rows = None if M * N * K < 2e9 else list(range(0, M, 17))
+    run_case(oracle, M, N, K, F16, F16, bias=(name == "kv"), seed=55, rows=rows)
+
+
+# ---------------------------------------------------------------------------
+# every kernel family over its edges
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("act,outd", [(F32, F32), (F16, F16), (F16, F32)])
+@pytest.mark.parametrize("M,N,K", [(1, 3, 4), (1, 2, 2), (2, 17, 33), (3, 40, 100), (1, 5, 0), (4, 64, 896)])
+def test_generic_kernel(gpu, oracle, M, N, K, act, outd):
+    run_case(oracle, M, N, K, act, outd, bias=True, res="sep", kernel=capi.KERNEL_GENERIC, seed=M + N + K)
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8, 9, 20])
+@pytest.mark.parametrize("N,K", [(1, 16), (17, 80), (896, 896), (130, 4864)])
+def test_gemv_f32_kernel(gpu, oracle, M, N, K):
+    run_case(oracle, M, N, K, F32, F32, bias=True, res="inplace" if M % 2 else None,
+             kernel=capi.KERNEL_GEMV_F32, seed=7 * M + N)
+
+
+@pytest.mark.parametrize("outd", [F16, F32])
+@pytest.mark.parametrize("M", [1, 2, 4, 7, 15, 16])
+@pytest.mark.parametrize("N,K", [(1, 16), (17, 48), (128, 896), (896, 4864), (300, 1040)])
+def test_skinny_kernel(gpu, oracle, M, N, K, outd):
+    run_case(oracle, M, N, K, F16, outd, bias=bool(M % 2), res=["sep", "inplace", None][M % 3],
+             kernel=capi.KERNEL_SKINNY, seed=3 * M + K)
+
+
+@pytest.mark.parametrize("outd", [F16, F32])
+@pytest.mark.parametrize("M", [1, 17, 64, 130, 300])
+@pytest.mark.parametrize("N,K", [(17, 16), (128, 80), (896, 896), (250, 4864)])
+def test_gemm_kernel(gpu, oracle, M, N, K, outd):
+    run_case(oracle, M, N, K, F16, outd, bias=bool(M % 2), res=["sep", "inplace", None][M % 3],
+             kernel=capi.KERNEL_GEMM, seed=5 * M + N)
+
+
+def test_misaligned_activations_fall_back(gpu, oracle):
+    """A 2-byte-offset fp16 activation base cannot take 16-byte loads: the
+    dispatcher must route it to the generic kernel and stay correct."""
+    run_case(oracle, 1, 64, 896, F16, F16, x_offset=2, seed=9)
+    run_case(oracle, 20, 64, 896, F16, F16, x_offset=2, seed=9)
+
+
+# ---------------------------------------------------------------------------
+# device quantizer: bit-exact codes and scales
+# ---------------------------------------------------------------------------
+def _quantize_dev(w):
+    N, K = w.shape
+    d_w = capi.DevBuf.from_array(w)
+    d_q, d_s = capi.DevBuf(max(N * K, 1)), capi.DevBuf(N * 4)
+    capi.call("vvh_quantize_per_channel", d_w.ptr, N, K, d_q.ptr, d_s.ptr, None)
+    capi.sync()
+    return d_q.to_array(np.int8, (N, K)), d_s.to_array(np.float32, (N,))
+
+
+def test_device_quantizer_golden(gpu):
+    d = np.load(os.path.join(GOLDEN, "quantize_ref.npz"))
+    for name in sorted({k[2:-2] for k in d.files if k.endswith("_w")}):
+        print(f"[case] quantize golden {name}", flush=True)
+        q, s = _quantize_dev(d[f"q_{name}_w"])
+        np.testing.assert_array_equal(q, d[f"q_{name}_codes"], err_msg=name)
+        np.testing.assert_array_equal(s.view(np.uint32), d[f"q_{name}_scales"].view(np.uint32), err_msg=name)
+
+
+@pytest.mark.parametrize("N,K,std", [(300, 1000, 0.02), (4864, 896, 0.02), (64, 5000, 3.0), (3, 1, 1.0)])
+def test_device_quantizer_matches_oracle(gpu, oracle, N, K, std):
+    print(f"[case] quantize N={N} K={K}", flush=True)
+    rng = np.random.default_rng(N + K)
+    w = rng.normal(0, std, (N, K)).astype(np.float32)
+    w[0, : min(K, 3)] = [np.float32(127.0 * 0.5)] * min(K, 3)
+    q, s = _quantize_dev(w)
+    q_ref, s_ref = oracle.quantize_per_channel(w)
+    np.testing.assert_array_equal(q, q_ref)
+    np.testing.assert_array_equal(s.view(np.uint32), s_ref.view(np.uint32))
+
+
+# ---------------------------------------------------------------------------
+# weight mirror, plans, allocator, conversion, generator
+# ---------------------------------------------------------------------------
+def test_weight_mirror_handles(gpu, oracle):
+    q, s, b = weights(896, 896, 21, oracle)
+    q, s, b = q.copy(), s.copy(), b.copy()
+    h = ctypes.c_uint64()
+    capi.call("vvh_weight_register", q.ctypes.data, s.ctypes.data, b.ctypes.data, 896, 896, ctypes.byref(h))
+    h2 = ctypes.c_uint64()
+    capi.call("vvh_weight_register", q.ctypes.data, s.ctypes.data, b.ctypes.data, 896, 896, ctypes.byref(h2))
+    assert h.value == h2.value  # same tuple -> same mirror
+    found = ctypes.c_uint64()
+    capi.call("vvh_weight_find", q.ctypes.data, ctypes.byref(found))
+    assert found.value == h.value
+    x = np.random.default_rng(1).normal(0, 1, (1, 896)).astype(np.float16)
+    d_x, d_y = capi.DevBuf.from_array(x), capi.DevBuf(896 * 4)
+    capi.call("vvh_linear_q8", d_y.ptr, d_x.ptr, h.value, None, 1, 896, 896, F16, F32, None)
+    capi.sync()
+    ref = oracle.linear_q8(x.astype(np.float32), q, s, b)
+    y = d_y.to_array(np.float32, (1, 896))
+    assert np.abs(y - ref).max() / np.abs(ref).max() <= TOL_F16
+    # shape mismatch against the mirror is rejected
+    assert capi.status_of("vvh_linear_q8", d_y.ptr, d_x.ptr, h.value, None, 1, 448, 896, F16, F32, None) == 1
+    # same host pointer, different shape -> replaced mirror, new handle
+    h3 = ctypes.c_uint64()
+    capi.call("vvh_weight_register", q.ctypes.data, s.ctypes.data, None, 448, 896, ctypes.byref(h3))
+    assert h3.value != h.value
+    assert capi.status_of("vvh_linear_q8", d_y.ptr, d_x.ptr, h.value, None, 1, 896, 896, F16, F32, None) == 6
+    capi.call("vvh_weight_release", h3.value)
+    assert capi.status_of("vvh_weight_find", q.ctypes.data, ctypes.byref(found)) == 6
+
+
+def test_grouped_plan_matches_single_calls(gpu, oracle):
+    """One decode layer of Qwen2.5-0.5B (q/k/v with bias, o and down in place,
+    gate and up) x 3 layers as one grouped launch."""
+    rng = np.random.default_rng(77)
+    probs, keep, checks = [], [], []
+    for layer in range(3):
+        for name, N, K, bias, res in QWEN05_LAYER:
+            if name == "gate_up":
+                continue
+            q, s, b = weights(N, K, 100 + layer, oracle)
+            x = rng.normal(0, 1, (1, K)).astype(np.float16)
+            r = rng.normal(0, 1, (1, N)).astype(np.float16) if res else None
+            d = dict(q=capi.DevBuf.from_array(q), s=capi.DevBuf.from_array(s),
+                     b=capi.DevBuf.from_array(b) if bias else None, x=capi.DevBuf.from_array(x),
+                     y=capi.DevBuf.from_array(r) if res else capi.DevBuf(N * 2))
+            keep.append(d)
+            p = capi.Q8Problem(out=d["y"].ptr, inp=d["x"].ptr, residual=d["y"].ptr if res else None,
+                               weight=d["q"].ptr, scales=d["s"].ptr, bias=d["b"].ptr if bias else None,
+                               M=1, N=N, K=K)
+            probs.append(p)
+            checks.append((d["y"], x, q, s, b if bias else None, r, N))
+    arr = (capi.Q8Problem * len(probs))(*probs)
+    plan = ctypes.c_uint64()
+    capi.call("vvh_plan_create", arr, len(probs), F16, F16, ctypes.byref(plan))
+    n = ctypes.c_int()
+    capi.call("vvh_plan_launches", plan.value, ctypes.byref(n))
+    assert n.value == 1
+    print("[case] grouped plan run", flush=True)
+    capi.call("vvh_plan_run", plan.value, None)
+    capi.sync()
+    for d_y, x, q, s, b, r, N in checks:
+        y = d_y.to_array(np.float16, (1, N)).astype(np.float32)
+        ref = oracle.linear_q8(x.astype(np.float32), q, s, b, None if r is None else r.astype(np.float32))
+        assert np.abs(y - ref).max() / np.abs(ref).max() <= TOL_F16
+    capi.call("vvh_plan_destroy", plan.value)
+
+
+def test_plan_with_prefill_problem_runs_per_call(gpu, oracle):
+    q, s, b = weights(256, 512, 5, oracle)
+    rng = np.random.default_rng(5)
+    xs = [rng.normal(0, 1, (M, 512)).astype(np.float16) for M in (1, 40)]
+    d_q, d_s = capi.DevBuf.from_array(q), capi.DevBuf.from_array(s)
+    d_x = [capi.DevBuf.from_array(x) for x in xs]
+    d_y = [capi.DevBuf(x.shape[0] * 256 * 2) for x in xs]
+    probs = [capi.Q8Problem(out=d_y[i].ptr, inp=d_x[i].ptr, residual=None, weight=d_q.ptr, scales=d_s.ptr,
+                            bias=None, M=xs[i].shape[0], N=256, K=512) for i in range(2)]
+    arr = (capi.Q8Problem * 2)(*probs)
+    plan = ctypes.c_uint64()
+    capi.call("vvh_plan_create", arr, 2, F16, F16, ctypes.byref(plan))
+    n = ctypes.c_int()
+    capi.call("vvh_plan_launches", plan.value, ctypes.byref(n))
+    assert n.value == 2
+    capi.call("vvh_plan_run", plan.value, None)
+    capi.sync()
+    for i, x in enumerate(xs):
+        y = d_y[i].to_array(np.float16, (x.shape[0], 256)).astype(np.float32)
+        ref = oracle.linear_q8(x.astype(np.float32), q, s)
+        assert np.abs(y - ref).max() / np.abs(ref).max() <= TOL_F16
+    capi.call("vvh_plan_destroy", plan.value)
+
+
+def test_pool_on_device(gpu):
+    before = capi.PoolStats()
+    capi.call("vvh_pool_get_stats", ctypes.byref(before))
+    p = ctypes.c_void_p()
+    capi.call("vvh_pool_alloc", ctypes.byref(p), 1 << 20)
+    first = p.value
+    capi.call("vvh_pool_free", first)
+    capi.call("vvh_pool_alloc", ctypes.byref(p), (1 << 20) - 100)
+    assert p.value == first
+    after = capi.PoolStats()
+    capi.call("vvh_pool_get_stats", ctypes.byref(after))
+    assert after.cache_hits == before.cache_hits + 1
+    capi.call("vvh_pool_free", p.value)
+    capi.call("vvh_pool_release_cached")
+    z = ctypes.c_void_p(1)
+    capi.call("vvh_pool_alloc", ctypes.byref(z), 0)
+    assert z.value is None
+
+
+def test_convert_and_fill(gpu):
+    x = np.random.default_rng(0).normal(0, 10, 10007).astype(np.float32)
+    d_x, d_h, d_f = capi.DevBuf.from_array(x), capi.DevBuf(10007 * 2), capi.DevBuf(10007 * 4)
+    capi.call("vvh_convert", d_h.ptr, F16, d_x.ptr, F32, 10007, None)
+    capi.call("vvh_convert", d_f.ptr, F32, d_h.ptr, F16, 10007, None)
+    capi.sync()
+    np.testing.assert_array_equal(d_h.to_array(np.float16, 10007), x.astype(np.float16))
+    np.testing.assert_array_equal(d_f.to_array(np.float32, 10007), x.astype(np.float16).astype(np.float32))
+    n = 1 << 20
+    d = capi.DevBuf(n * 4)
+    capi.call("vvh_fill_normal", d.ptr, F32, n, 1234, 0.5, 0.02, None)
+    capi.sync()
+    a = d.to_array(np.float32, n)
+    assert abs(a.mean() - 0.5) < 1e-3 and abs(a.std() - 0.02) < 1e-3
+    capi.call("vvh_fill_normal", d.ptr, F32, n, 1234, 0.5, 0.02, None)
+    capi.sync()
+    np.testing.assert_array_equal(d.to_array(np.float32, n), a)

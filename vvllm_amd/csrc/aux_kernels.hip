@@ -1,0 +1,131 @@
+// Auxiliary device kernels of the linear path: the per-channel quantizer,
+// dtype conversion, and a counter-based normal generator for synthetic data.
+#include <hip/hip_runtime.h>
+
+#include "common.h"
+
+namespace vvh {
+
+typedef _Float16 f16;
+
+// ---------------------------------------------------------------------------
+// quantize_per_channel on the device (src/quantize/quantize.cc:9-48).
+// One block per row.  The absmax uses the reference's comparison
+// `std::max(absmax, |w|)` == (absmax < |w|) ? |w| : absmax, which ignores NaN;
+// max is exact, so the reduction order cannot change the result.  The scale
+// and its reciprocal are IEEE-correct fp32 divisions (this file is compiled
+// with -fhip-fp32-correctly-rounded-divide-sqrt and without fast-math), the
+// code is round-half-away-from-zero (roundf) of w * (1/scale), clamped with
+// the reference's argument order so NaN becomes +127.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float ref_max(float a, float b) { return (a < b) ? b : a; }
+__device__ __forceinline__ float ref_min(float a, float b) { return (b < a) ? b : a; }
+
+__global__ __launch_bounds__(256) void k_quantize(const float* __restrict__ w, int64_t N, int64_t K,
+                                                  int8_t* __restrict__ q, float* __restrict__ scales)
+{
+    __shared__ float part[4];
+    __shared__ float row_scale;
+    for (int64_t row = blockIdx.x; row < N; row += gridDim.x) {
+        const float* wr = w + row * K;
+        float mx = 0.0f;
+        for (int64_t k = threadIdx.x; k < K; k += 256) mx = ref_max(mx, __builtin_fabsf(wr[k]));
+        for (int off = 32; off > 0; off >>= 1) mx = ref_max(mx, __shfl_xor(mx, off));
+        if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = mx;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float absmax = ref_max(ref_max(part[0], part[1]), ref_max(part[2], part[3]));
+            const float scale = absmax / 127.0f;
+            scales[row] = scale;
+            row_scale = scale;
+        }
+        __syncthreads();
+        const float scale = row_scale;
+        int8_t* qr = q + row * K;
+        if (scale == 0.0f) {
+            for (int64_t k = threadIdx.x; k < K; k += 256) qr[k] = 0;
+        } else {
+            const float inv_scale = 1.0f / scale;
+            for (int64_t k = threadIdx.x; k < K; k += 256) {
+                float val = wr[k] * inv_scale;
+                val = ref_max(-128.0f, ref_min(127.0f, roundf(val)));
+                qr[k] = (int8_t)val;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+int launch_quantize(const float* w, int64_t N, int64_t K, int8_t* q, float* scales, void* stream)
+{
+    const int64_t grid = N < 65536 ? N : 65536;
+    hipLaunchKernelGGL(k_quantize, dim3((unsigned)grid), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       w, N, K, q, scales);
+    return (int)hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// dtype conversion (round to nearest even), grid-stride.
+// ---------------------------------------------------------------------------
+template <typename DT, typename ST>
+__global__ __launch_bounds__(256) void k_convert(DT* __restrict__ d, const ST* __restrict__ s, int64_t n)
+{
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+        d[i] = (DT)(float)s[i];
+}
+
+int launch_convert(void* dst, int dst_dtype, const void* src, int src_dtype, int64_t n, void* stream)
+{
+    const int64_t want = (n + 255) / 256;
+    const dim3 grid((unsigned)(want < 16384 ? (want > 0 ? want : 1) : 16384));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (dst_dtype == VVH_F16 && src_dtype == VVH_F32)
+        hipLaunchKernelGGL((k_convert<f16, float>), grid, dim3(256), 0, s, (f16*)dst, (const float*)src, n);
+    else if (dst_dtype == VVH_F32 && src_dtype == VVH_F16)
+        hipLaunchKernelGGL((k_convert<float, f16>), grid, dim3(256), 0, s, (float*)dst, (const f16*)src, n);
+    else if (dst_dtype == VVH_F32)
+        hipLaunchKernelGGL((k_convert<float, float>), grid, dim3(256), 0, s, (float*)dst, (const float*)src, n);
+    else
+        hipLaunchKernelGGL((k_convert<f16, f16>), grid, dim3(256), 0, s, (f16*)dst, (const f16*)src, n);
+    return (int)hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Synthetic N(mean, std) data: element i draws h = splitmix64(seed ^ i*phi),
+// u1 = (top 24 bits + 0.5) / 2^24 in (0, 1), u2 = next 24 bits / 2^24, and
+// takes the Box-Muller cosine branch in fp32.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint64_t splitmix64(uint64_t z)
+{
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_fill_normal(T* __restrict__ d, int64_t n, uint64_t seed, float mean,
+                                                     float std)
+{
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+        const uint64_t h = splitmix64(seed ^ ((uint64_t)i * 0x9E3779B97F4A7C15ull));
+        const float u1 = ((float)(h >> 40) + 0.5f) * (1.0f / 16777216.0f);
+        const float u2 = (float)((h >> 16) & 0xFFFFFFull) * (1.0f / 16777216.0f);
+        const float z = sqrtf(-2.0f * logf(u1)) * cosf(6.283185307179586f * u2);
+        d[i] = (T)(mean + std * z);
+    }
+}
+
+int launch_fill_normal(void* dst, int dtype, int64_t n, uint64_t seed, float mean, float std, void* stream)
+{
+    const int64_t want = (n + 255) / 256;
+    const dim3 grid((unsigned)(want < 16384 ? (want > 0 ? want : 1) : 16384));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (dtype == VVH_F32)
+        hipLaunchKernelGGL((k_fill_normal<float>), grid, dim3(256), 0, s, (float*)dst, n, seed, mean, std);
+    else
+        hipLaunchKernelGGL((k_fill_normal<f16>), grid, dim3(256), 0, s, (f16*)dst, n, seed, mean, std);
+    return (int)hipGetLastError();
+}
+
+}  // namespace vvh

@@ -1,0 +1,705 @@
+// C ABI of libvvllm_hip.so (include/vvllm_hip.h): device init, memory,
+// caching allocator, weight mirror, dispatch of the linear path, grouped
+// plans.  Every entry validates its arguments on the host, returns a
+// vvh_status and records a message for vvh_last_error(); nothing exits the
+// process (the reference exits on any CUDA error,
+// src/backend/cuda_kernels.cu:11-21).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "common.h"
+#include "pool.h"
+
+using namespace vvh;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int status, const char* fmt, ...)
+{
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return status;
+}
+
+int fail_hip(hipError_t e, const char* what)
+{
+    if (e == hipErrorOutOfMemory)
+        return fail(VVH_ERR_OUT_OF_MEMORY, "%s: %s", what, hipGetErrorString(e));
+    return fail(VVH_ERR_HIP, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+std::atomic<bool> g_init{false};
+int g_device = -1;
+int g_cu_count = 0;
+std::atomic<int> g_override{K_AUTO};
+
+#define REQUIRE_INIT()                                                              \
+    do {                                                                            \
+        if (!g_init.load()) return fail(VVH_ERR_NOT_INITIALIZED, "vvh_init has not succeeded"); \
+    } while (0)
+
+// ---- caching allocator over hipMalloc -------------------------------------
+struct HipRaw final : RawAllocator {
+    int alloc(void** p, std::size_t bytes) override
+    {
+        hipError_t e = hipMalloc(p, bytes);
+        if (e == hipSuccess) return 0;
+        (void)hipGetLastError();  // clear the sticky error of the failed allocation
+        return e == hipErrorOutOfMemory ? 1 : 2;
+    }
+    int free(void* p) override { return hipFree(p) == hipSuccess ? 0 : 2; }
+};
+HipRaw g_raw;
+CachingPool g_pool(&g_raw);
+
+// ---- weight mirror --------------------------------------------------------
+struct WeightEntry {
+    const void* host_w = nullptr;      // key (null for device registrations)
+    const void* host_scales = nullptr;
+    const void* host_bias = nullptr;
+    std::size_t N = 0, K = 0;
+    void* base = nullptr;              // owned allocation (null if not owned)
+    std::size_t bytes = 0;
+    const int8_t* w = nullptr;
+    const float* scales = nullptr;
+    const float* bias = nullptr;
+};
+std::mutex g_wmu;
+std::unordered_map<vvh_weight, WeightEntry> g_weights;
+std::unordered_map<const void*, vvh_weight> g_weight_by_host;
+vvh_weight g_next_weight = 1;
+
+// ---- plans ------------------------------------------------------------------
+struct Plan {
+    std::vector<LinArgs> args;   // host copy, launch order
+    LinArgs* dev_table = nullptr;
+    int act = 0, out = 0;
+    bool grouped = false;
+    int64_t total_blocks = 0;
+};
+std::mutex g_pmu;
+std::unordered_map<vvh_plan, Plan> g_plans;
+vvh_plan g_next_plan = 1;
+
+constexpr std::size_t kAlign = 256;
+inline std::size_t align_up(std::size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+inline bool valid_dtype(int d) { return d == VVH_F32 || d == VVH_F16; }
+inline std::size_t dsize(int d) { return d == VVH_F32 ? 4 : 2; }
+
+// a*b without overflow past 2^62
+bool mul_ok(uint64_t a, uint64_t b, uint64_t* r)
+{
+    if (a != 0 && b > (uint64_t(1) << 62) / a) return false;
+    *r = a * b;
+    return true;
+}
+
+int natural_kernel(std::size_t M, int act)
+{
+    if (act == VVH_F32) return K_GEMV_F32;
+    return M <= (std::size_t)kSkinnyMaxM ? K_SKINNY : K_GEMM;
+}
+
+// Kernel family for a call; `aligned` = K % 16 == 0 and 16-byte aligned
+// weight and activation bases.
+int choose_kernel(std::size_t M, std::size_t K, int act, bool aligned)
+{
+    if (K == 0 || !aligned) return K_GENERIC;
+    const int ov = g_override.load();
+    const int k = ov == K_AUTO ? natural_kernel(M, act) : ov;
+    switch (k) {
+        case K_GEMV_F32: return act == VVH_F32 ? K_GEMV_F32 : K_GENERIC;
+        case K_SKINNY: return (act == VVH_F16 && M <= (std::size_t)kSkinnyMaxM) ? K_SKINNY : K_GENERIC;
+        case K_GEMM: return act == VVH_F16 ? K_GEMM : K_GENERIC;
+        default: return K_GENERIC;
+    }
+}
+
+// Waves of a block that split one tile's k range: enough waves in flight to
+// cover every CU several times, never more than the k steps available.
+int choose_ksplit(int64_t tiles, int64_t K)
+{
+    const int64_t target = (int64_t)(g_cu_count > 0 ? g_cu_count : 256) * 8;
+    int ks = tiles >= target ? 1 : (tiles * 2 >= target ? 2 : 4);
+    const int64_t steps = (K + 63) / 64;
+    while (ks > 1 && ks > steps) ks >>= 1;
+    return ks;
+}
+
+int validate_call(const void* out, const void* inp, const int8_t* w, const float* scales,
+                  std::size_t M, std::size_t N, std::size_t K, int act, int outd)
+{
+    if (!valid_dtype(act) || !valid_dtype(outd))
+        return fail(VVH_ERR_INVALID_ARG, "bad dtype (act %d, out %d)", act, outd);
+    uint64_t mk, nk, mn;
+    if (!mul_ok(M, K, &mk) || !mul_ok(N, K, &nk) || !mul_ok(M, N, &mn))
+        return fail(VVH_ERR_INVALID_ARG, "size overflow (M %zu, N %zu, K %zu)", M, N, K);
+    if (M == 0 || N == 0) return VVH_OK;
+    if (!out) return fail(VVH_ERR_INVALID_ARG, "out is null");
+    if (!scales) return fail(VVH_ERR_INVALID_ARG, "scales is null");
+    if (K > 0 && (!inp || !w)) return fail(VVH_ERR_INVALID_ARG, "inp or weight is null");
+    return VVH_OK;
+}
+
+int run_call(const LinArgs& base, int kernel, int act, int outd, void* stream)
+{
+    LinArgs a = base;
+    int e = 0;
+    switch (kernel) {
+        case K_GEMV_F32: {
+            a.ksplit = choose_ksplit((a.N + kDecodeTileN - 1) / kDecodeTileN, a.K);
+            const int64_t mt = a.M <= 1 ? 1 : a.M <= 2 ? 2 : a.M <= 4 ? 4 : kGemvF32MaxM;
+            if (decode_blocks(a) > INT32_MAX || (a.M + mt - 1) / mt > 65535)
+                return fail(VVH_ERR_UNSUPPORTED, "problem too large for the decode grid");
+            e = launch_gemv_f32(a, outd, stream);
+            break;
+        }
+        case K_SKINNY: {
+            a.ksplit = choose_ksplit((a.N + kDecodeTileN - 1) / kDecodeTileN, a.K);
+            if (decode_blocks(a) > INT32_MAX)
+                return fail(VVH_ERR_UNSUPPORTED, "problem too large for the decode grid");
+            e = launch_skinny(a, outd, stream);
+            break;
+        }
+        case K_GEMM: {
+            const int64_t nb = ((a.M + kGemmBM - 1) / kGemmBM) * ((a.N + kGemmBN - 1) / kGemmBN);
+            if (nb > INT32_MAX) return fail(VVH_ERR_UNSUPPORTED, "problem too large for the GEMM grid");
+            e = launch_gemm(a, outd, stream);
+            break;
+        }
+        default: {
+            if ((a.M * a.N + 255) / 256 > INT32_MAX)
+                return fail(VVH_ERR_UNSUPPORTED, "problem too large for the generic kernel");
+            e = launch_generic(a, act, outd, stream);
+            break;
+        }
+    }
+    if (e != 0) return fail_hip((hipError_t)e, "kernel launch");
+    return VVH_OK;
+}
+
+int linear_dev(void* out, const void* inp, const int8_t* w, const float* scales, const float* bias,
+               const void* res, std::size_t M, std::size_t N, std::size_t K, int act, int outd,
+               void* stream)
+{
+    int st = validate_call(out, inp, w, scales, M, N, K, act, outd);
+    if (st != VVH_OK || M == 0 || N == 0) return st;
+    REQUIRE_INIT();
+    LinArgs a{};
+    a.out = out;
+    a.inp = inp;
+    a.res = res;
+    a.w = w;
+    a.scales = scales;
+    a.bias = bias;
+    a.M = (int64_t)M;
+    a.N = (int64_t)N;
+    a.K = (int64_t)K;
+    a.ksplit = 1;
+    const bool aligned = K % 16 == 0 && aligned16(w) && aligned16(inp);
+    return run_call(a, choose_kernel(M, K, act, aligned), act, outd, stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+VVH_API const char* vvh_status_string(int status)
+{
+    switch (status) {
+        case VVH_OK: return "VVH_OK";
+        case VVH_ERR_INVALID_ARG: return "VVH_ERR_INVALID_ARG";
+        case VVH_ERR_NO_DEVICE: return "VVH_ERR_NO_DEVICE";
+        case VVH_ERR_OUT_OF_MEMORY: return "VVH_ERR_OUT_OF_MEMORY";
+        case VVH_ERR_HIP: return "VVH_ERR_HIP";
+        case VVH_ERR_NOT_INITIALIZED: return "VVH_ERR_NOT_INITIALIZED";
+        case VVH_ERR_UNKNOWN_HANDLE: return "VVH_ERR_UNKNOWN_HANDLE";
+        case VVH_ERR_UNSUPPORTED: return "VVH_ERR_UNSUPPORTED";
+        default: return "VVH_ERR_UNKNOWN_STATUS";
+    }
+}
+
+VVH_API const char* vvh_last_error(void) { return g_last_error.c_str(); }
+
+VVH_API const char* vvh_version(void) { return "vvllm-hip 0.1 gfx950"; }
+
+VVH_API int vvh_init(int device, char* name_buf, size_t name_buf_size)
+{
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count <= 0) {
+        (void)hipGetLastError();
+        return fail(VVH_ERR_NO_DEVICE, "no HIP device (%s)", hipGetErrorString(e));
+    }
+    if (device < 0 || device >= count)
+        return fail(VVH_ERR_NO_DEVICE, "device %d out of range [0, %d)", device, count);
+    if ((e = hipSetDevice(device)) != hipSuccess) return fail_hip(e, "hipSetDevice");
+    hipDeviceProp_t prop;
+    if ((e = hipGetDeviceProperties(&prop, device)) != hipSuccess)
+        return fail_hip(e, "hipGetDeviceProperties");
+    g_device = device;
+    g_cu_count = prop.multiProcessorCount;
+    if (name_buf && name_buf_size > 0) {
+        snprintf(name_buf, name_buf_size, "%s (%s, %d CUs)", prop.name[0] ? prop.name : "AMD GPU",
+                 prop.gcnArchName, prop.multiProcessorCount);
+    }
+    g_init.store(true);
+    return VVH_OK;
+}
+
+VVH_API int vvh_sync(void)
+{
+    REQUIRE_INIT();
+    hipError_t e = hipDeviceSynchronize();
+    return e == hipSuccess ? VVH_OK : fail_hip(e, "hipDeviceSynchronize");
+}
+
+VVH_API int vvh_device_cu_count(void) { return g_init.load() ? g_cu_count : 0; }
+
+// ---- raw memory ---------------------------------------------------------------
+VVH_API int vvh_malloc(void** ptr, size_t bytes)
+{
+    if (!ptr) return fail(VVH_ERR_INVALID_ARG, "ptr is null");
+    *ptr = nullptr;
+    REQUIRE_INIT();
+    if (bytes == 0) return VVH_OK;
+    hipError_t e = hipMalloc(ptr, bytes);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        *ptr = nullptr;
+        return fail_hip(e, "hipMalloc");
+    }
+    return VVH_OK;
+}
+
+VVH_API int vvh_free(void* ptr)
+{
+    if (!ptr) return VVH_OK;
+    REQUIRE_INIT();
+    hipError_t e = hipFree(ptr);
+    return e == hipSuccess ? VVH_OK : fail_hip(e, "hipFree");
+}
+
+VVH_API int vvh_malloc_host(void** ptr, size_t bytes)
+{
+    if (!ptr) return fail(VVH_ERR_INVALID_ARG, "ptr is null");
+    *ptr = nullptr;
+    REQUIRE_INIT();
+    if (bytes == 0) return VVH_OK;
+    hipError_t e = hipHostMalloc(ptr, bytes, hipHostMallocDefault);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        *ptr = nullptr;
+        return fail_hip(e, "hipHostMalloc");
+    }
+    return VVH_OK;
+}
+
+VVH_API int vvh_free_host(void* ptr)
+{
+    if (!ptr) return VVH_OK;
+    REQUIRE_INIT();
+    hipError_t e = hipHostFree(ptr);
+    return e == hipSuccess ? VVH_OK : fail_hip(e, "hipHostFree");
+}
+
+static int copy(void* dst, const void* src, size_t bytes, hipMemcpyKind kind, const char* what)
+{
+    if (bytes == 0) return VVH_OK;
+    if (!dst || !src) return fail(VVH_ERR_INVALID_ARG, "%s: null pointer", what);
+    REQUIRE_INIT();
+    hipError_t e = hipMemcpy(dst, src, bytes, kind);
+    return e == hipSuccess ? VVH_OK : fail_hip(e, what);
+}
+
+VVH_API int vvh_memcpy_h2d(void* d, const void* s, size_t n) { return copy(d, s, n, hipMemcpyHostToDevice, "memcpy h2d"); }
+VVH_API int vvh_memcpy_d2h(void* d, const void* s, size_t n) { return copy(d, s, n, hipMemcpyDeviceToHost, "memcpy d2h"); }
+VVH_API int vvh_memcpy_d2d(void* d, const void* s, size_t n) { return copy(d, s, n, hipMemcpyDeviceToDevice, "memcpy d2d"); }
+
+// ---- caching allocator -------------------------------------------------------------
+VVH_API int vvh_pool_alloc(void** ptr, size_t bytes)
+{
+    if (!ptr) return fail(VVH_ERR_INVALID_ARG, "ptr is null");
+    *ptr = nullptr;
+    REQUIRE_INIT();
+    const int rc = g_pool.alloc(ptr, bytes);
+    if (rc == 0) return VVH_OK;
+    if (rc == 1) return fail(VVH_ERR_OUT_OF_MEMORY, "pool: out of device memory for %zu bytes", bytes);
+    if (rc == 3) return fail(VVH_ERR_INVALID_ARG, "pool: size %zu too large", bytes);
+    return fail(VVH_ERR_HIP, "pool: hipMalloc failed for %zu bytes", bytes);
+}
+
+VVH_API int vvh_pool_free(void* ptr)
+{
+    if (!ptr) return VVH_OK;
+    REQUIRE_INIT();
+    if (g_pool.free(ptr) == 0) return VVH_OK;
+    hipError_t e = hipFree(ptr);  // not from the pool: a real free (tensor.cc:58-66)
+    return e == hipSuccess ? VVH_OK : fail_hip(e, "hipFree");
+}
+
+VVH_API int vvh_pool_release_cached(void)
+{
+    REQUIRE_INIT();
+    const int failures = g_pool.release_cached();
+    return failures == 0 ? VVH_OK : fail(VVH_ERR_HIP, "pool: %d hipFree calls failed", failures);
+}
+
+VVH_API int vvh_pool_get_stats(vvh_pool_stats* out)
+{
+    if (!out) return fail(VVH_ERR_INVALID_ARG, "out is null");
+    const PoolStats s = g_pool.stats();
+    out->bytes_in_use = s.bytes_in_use;
+    out->bytes_cached = s.bytes_cached;
+    out->bytes_reserved = s.bytes_in_use + s.bytes_cached;
+    out->peak_reserved = s.peak_reserved;
+    out->alloc_calls = s.alloc_calls;
+    out->cache_hits = s.cache_hits;
+    out->driver_allocs = s.driver_allocs;
+    out->oom_releases = s.oom_releases;
+    return VVH_OK;
+}
+
+// ---- weight mirror ---------------------------------------------------------------
+static void drop_weight_locked(vvh_weight h)
+{
+    auto it = g_weights.find(h);
+    if (it == g_weights.end()) return;
+    if (it->second.base) (void)hipFree(it->second.base);
+    if (it->second.host_w) {
+        auto hb = g_weight_by_host.find(it->second.host_w);
+        if (hb != g_weight_by_host.end() && hb->second == h) g_weight_by_host.erase(hb);
+    }
+    g_weights.erase(it);
+}
+
+VVH_API int vvh_weight_register(const int8_t* host_weight, const float* host_scales,
+                                const float* host_bias, size_t N, size_t K, vvh_weight* handle)
+{
+    if (!handle) return fail(VVH_ERR_INVALID_ARG, "handle is null");
+    *handle = 0;
+    if (!host_weight || !host_scales) return fail(VVH_ERR_INVALID_ARG, "weight or scales is null");
+    uint64_t nk;
+    if (N == 0 || !mul_ok(N, K, &nk)) return fail(VVH_ERR_INVALID_ARG, "bad shape N %zu K %zu", N, K);
+    REQUIRE_INIT();
+    std::lock_guard<std::mutex> lock(g_wmu);
+    auto hb = g_weight_by_host.find(host_weight);
+    if (hb != g_weight_by_host.end()) {
+        const WeightEntry& e = g_weights.at(hb->second);
+        if (e.host_scales == host_scales && e.host_bias == host_bias && e.N == N && e.K == K) {
+            *handle = hb->second;
+            return VVH_OK;
+        }
+        drop_weight_locked(hb->second);  // same host buffer, new contents/shape
+    }
+    const std::size_t off_s = align_up(nk);
+    const std::size_t off_b = off_s + align_up(N * sizeof(float));
+    const std::size_t bytes = off_b + (host_bias ? align_up(N * sizeof(float)) : 0);
+    void* base = nullptr;
+    hipError_t e = hipMalloc(&base, bytes);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        if (g_pool.release_cached() == 0 && hipMalloc(&base, bytes) == hipSuccess) {
+            e = hipSuccess;
+        } else {
+            (void)hipGetLastError();
+            return fail_hip(e, "weight mirror hipMalloc");
+        }
+    }
+    char* b = static_cast<char*>(base);
+    if ((nk && (e = hipMemcpy(b, host_weight, nk, hipMemcpyHostToDevice)) != hipSuccess) ||
+        (e = hipMemcpy(b + off_s, host_scales, N * sizeof(float), hipMemcpyHostToDevice)) != hipSuccess ||
+        (host_bias && (e = hipMemcpy(b + off_b, host_bias, N * sizeof(float), hipMemcpyHostToDevice)) != hipSuccess)) {
+        (void)hipFree(base);
+        return fail_hip(e, "weight mirror upload");
+    }
+    WeightEntry w;
+    w.host_w = host_weight;
+    w.host_scales = host_scales;
+    w.host_bias = host_bias;
+    w.N = N;
+    w.K = K;
+    w.base = base;
+    w.bytes = bytes;
+    w.w = reinterpret_cast<const int8_t*>(b);
+    w.scales = reinterpret_cast<const float*>(b + off_s);
+    w.bias = host_bias ? reinterpret_cast<const float*>(b + off_b) : nullptr;
+    const vvh_weight h = g_next_weight++;
+    g_weights.emplace(h, w);
+    g_weight_by_host[host_weight] = h;
+    *handle = h;
+    return VVH_OK;
+}
+
+VVH_API int vvh_weight_register_device(const int8_t* dev_weight, const float* dev_scales,
+                                       const float* dev_bias, size_t N, size_t K, vvh_weight* handle)
+{
+    if (!handle) return fail(VVH_ERR_INVALID_ARG, "handle is null");
+    *handle = 0;
+    uint64_t nk;
+    if ((K > 0 && !dev_weight) || !dev_scales) return fail(VVH_ERR_INVALID_ARG, "weight or scales is null");
+    if (N == 0 || !mul_ok(N, K, &nk)) return fail(VVH_ERR_INVALID_ARG, "bad shape N %zu K %zu", N, K);
+    REQUIRE_INIT();
+    std::lock_guard<std::mutex> lock(g_wmu);
+    WeightEntry w;
+    w.N = N;
+    w.K = K;
+    w.w = dev_weight;
+    w.scales = dev_scales;
+    w.bias = dev_bias;
+    const vvh_weight h = g_next_weight++;
+    g_weights.emplace(h, w);
+    *handle = h;
+    return VVH_OK;
+}
+
+VVH_API int vvh_weight_find(const int8_t* host_weight, vvh_weight* handle)
+{
+    if (!handle) return fail(VVH_ERR_INVALID_ARG, "handle is null");
+    *handle = 0;
+    std::lock_guard<std::mutex> lock(g_wmu);
+    auto hb = g_weight_by_host.find(host_weight);
+    if (hb == g_weight_by_host.end()) return fail(VVH_ERR_UNKNOWN_HANDLE, "host weight not mirrored");
+    *handle = hb->second;
+    return VVH_OK;
+}
+
+VVH_API int vvh_weight_release(vvh_weight handle)
+{
+    std::lock_guard<std::mutex> lock(g_wmu);
+    if (!g_weights.count(handle)) return fail(VVH_ERR_UNKNOWN_HANDLE, "unknown weight handle %llu", (unsigned long long)handle);
+    drop_weight_locked(handle);
+    return VVH_OK;
+}
+
+VVH_API int vvh_weight_device_ptrs(vvh_weight handle, const int8_t** dev_weight, const float** dev_scales,
+                                   const float** dev_bias, size_t* N, size_t* K)
+{
+    std::lock_guard<std::mutex> lock(g_wmu);
+    auto it = g_weights.find(handle);
+    if (it == g_weights.end()) return fail(VVH_ERR_UNKNOWN_HANDLE, "unknown weight handle %llu", (unsigned long long)handle);
+    if (dev_weight) *dev_weight = it->second.w;
+    if (dev_scales) *dev_scales = it->second.scales;
+    if (dev_bias) *dev_bias = it->second.bias;
+    if (N) *N = it->second.N;
+    if (K) *K = it->second.K;
+    return VVH_OK;
+}
+
+VVH_API int vvh_weight_stats(uint64_t* count, uint64_t* bytes)
+{
+    std::lock_guard<std::mutex> lock(g_wmu);
+    uint64_t b = 0;
+    for (auto& kv : g_weights) b += kv.second.bytes;
+    if (count) *count = g_weights.size();
+    if (bytes) *bytes = b;
+    return VVH_OK;
+}
+
+// ---- linear -----------------------------------------------------------------------
+VVH_API int vvh_linear_q8_dev(void* out, const void* inp, const int8_t* dev_weight, const float* dev_scales,
+                              const float* dev_bias, const void* residual, size_t M, size_t N, size_t K,
+                              int act_dtype, int out_dtype, void* stream)
+{
+    return linear_dev(out, inp, dev_weight, dev_scales, dev_bias, residual, M, N, K, act_dtype, out_dtype, stream);
+}
+
+VVH_API int vvh_linear_q8(void* out, const void* inp, vvh_weight weight, const void* residual, size_t M,
+                          size_t N, size_t K, int act_dtype, int out_dtype, void* stream)
+{
+    REQUIRE_INIT();
+    const int8_t* w;
+    const float *s, *b;
+    {
+        std::lock_guard<std::mutex> lock(g_wmu);
+        auto it = g_weights.find(weight);
+        if (it == g_weights.end())
+            return fail(VVH_ERR_UNKNOWN_HANDLE, "unknown weight handle %llu", (unsigned long long)weight);
+        if (it->second.N != N || it->second.K != K)
+            return fail(VVH_ERR_INVALID_ARG, "weight is [%zu, %zu], call asks for [%zu, %zu]", it->second.N,
+                        it->second.K, N, K);
+        w = it->second.w;
+        s = it->second.scales;
+        b = it->second.bias;
+    }
+    return linear_dev(out, inp, w, s, b, residual, M, N, K, act_dtype, out_dtype, stream);
+}
+
+// ---- plans --------------------------------------------------------------------------
+VVH_API int vvh_plan_create(const vvh_q8_problem* problems, size_t count, int act_dtype, int out_dtype,
+                            vvh_plan* plan)
+{
+    if (!plan) return fail(VVH_ERR_INVALID_ARG, "plan is null");
+    *plan = 0;
+    if (!problems || count == 0) return fail(VVH_ERR_INVALID_ARG, "empty problem list");
+    if (count > (size_t)INT32_MAX) return fail(VVH_ERR_INVALID_ARG, "too many problems");
+    Plan p;
+    p.act = act_dtype;
+    p.out = out_dtype;
+    bool all_skinny = true;
+    int64_t total_tiles = 0;
+    for (size_t i = 0; i < count; i++) {
+        const vvh_q8_problem& q = problems[i];
+        int st = validate_call(q.out, q.inp, q.weight, q.scales, q.M, q.N, q.K, act_dtype, out_dtype);
+        if (st != VVH_OK) return fail(st, "problem %zu: %s", i, vvh_last_error());
+        if (q.M == 0 || q.N == 0) continue;
+        LinArgs a{};
+        a.out = q.out;
+        a.inp = q.inp;
+        a.res = q.residual;
+        a.w = q.weight;
+        a.scales = q.scales;
+        a.bias = q.bias;
+        a.M = (int64_t)q.M;
+        a.N = (int64_t)q.N;
+        a.K = (int64_t)q.K;
+        a.ksplit = 1;
+        const bool aligned = q.K % 16 == 0 && aligned16(q.weight) && aligned16(q.inp);
+        if (choose_kernel(q.M, q.K, act_dtype, aligned) != K_SKINNY) all_skinny = false;
+        total_tiles += (a.N + kDecodeTileN - 1) / kDecodeTileN;
+        p.args.push_back(a);
+    }
+    if (p.args.empty()) return fail(VVH_ERR_INVALID_ARG, "every problem is empty");
+    REQUIRE_INIT();
+    p.grouped = all_skinny;
+    if (p.grouped) {
+        // longest rows first, so the last blocks dispatched are the short ones
+        std::stable_sort(p.args.begin(), p.args.end(),
+                         [](const LinArgs& x, const LinArgs& y) { return x.K > y.K; });
+        int64_t blk = 0;
+        for (LinArgs& a : p.args) {
+            a.ksplit = choose_ksplit(total_tiles, a.K);
+            if (blk > INT32_MAX) return fail(VVH_ERR_UNSUPPORTED, "plan too large");
+            a.block_begin = (int32_t)blk;
+            blk += decode_blocks(a);
+        }
+        if (blk > INT32_MAX) return fail(VVH_ERR_UNSUPPORTED, "plan too large");
+        p.total_blocks = blk;
+        const size_t bytes = p.args.size() * sizeof(LinArgs);
+        hipError_t e = hipMalloc(reinterpret_cast<void**>(&p.dev_table), bytes);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            return fail_hip(e, "plan table hipMalloc");
+        }
+        if ((e = hipMemcpy(p.dev_table, p.args.data(), bytes, hipMemcpyHostToDevice)) != hipSuccess) {
+            (void)hipFree(p.dev_table);
+            return fail_hip(e, "plan table upload");
+        }
+    }
+    std::lock_guard<std::mutex> lock(g_pmu);
+    const vvh_plan h = g_next_plan++;
+    g_plans.emplace(h, std::move(p));
+    *plan = h;
+    return VVH_OK;
+}
+
+VVH_API int vvh_plan_run(vvh_plan plan, void* stream)
+{
+    REQUIRE_INIT();
+    const Plan* p;
+    {
+        std::lock_guard<std::mutex> lock(g_pmu);
+        auto it = g_plans.find(plan);
+        if (it == g_plans.end()) return fail(VVH_ERR_UNKNOWN_HANDLE, "unknown plan %llu", (unsigned long long)plan);
+        p = &it->second;
+    }
+    if (p->grouped) {
+        const int e = launch_skinny_grouped(p->dev_table, (int)p->args.size(), p->total_blocks, p->out, stream);
+        return e == 0 ? VVH_OK : fail_hip((hipError_t)e, "grouped launch");
+    }
+    for (const LinArgs& a : p->args) {
+        const bool aligned = a.K % 16 == 0 && aligned16(a.w) && aligned16(a.inp);
+        const int st = run_call(a, choose_kernel(a.M, a.K, p->act, aligned), p->act, p->out, stream);
+        if (st != VVH_OK) return st;
+    }
+    return VVH_OK;
+}
+
+VVH_API int vvh_plan_destroy(vvh_plan plan)
+{
+    std::lock_guard<std::mutex> lock(g_pmu);
+    auto it = g_plans.find(plan);
+    if (it == g_plans.end()) return fail(VVH_ERR_UNKNOWN_HANDLE, "unknown plan %llu", (unsigned long long)plan);
+    if (it->second.dev_table) (void)hipFree(it->second.dev_table);
+    g_plans.erase(it);
+    return VVH_OK;
+}
+
+VVH_API int vvh_plan_launches(vvh_plan plan, int* launches)
+{
+    if (!launches) return fail(VVH_ERR_INVALID_ARG, "launches is null");
+    std::lock_guard<std::mutex> lock(g_pmu);
+    auto it = g_plans.find(plan);
+    if (it == g_plans.end()) return fail(VVH_ERR_UNKNOWN_HANDLE, "unknown plan %llu", (unsigned long long)plan);
+    *launches = it->second.grouped ? 1 : (int)it->second.args.size();
+    return VVH_OK;
+}
+
+// ---- quantizer, conversion, synthetic data ---------------------------------------------------
+VVH_API int vvh_quantize_per_channel(const float* dev_weight, size_t N, size_t K, int8_t* dev_codes,
+                                     float* dev_scales, void* stream)
+{
+    uint64_t nk;
+    if (!mul_ok(N, K, &nk)) return fail(VVH_ERR_INVALID_ARG, "size overflow");
+    if (N == 0) return VVH_OK;
+    if (!dev_scales || (K > 0 && (!dev_weight || !dev_codes)))
+        return fail(VVH_ERR_INVALID_ARG, "null pointer");
+    REQUIRE_INIT();
+    const int e = launch_quantize(dev_weight, (int64_t)N, (int64_t)K, dev_codes, dev_scales, stream);
+    return e == 0 ? VVH_OK : fail_hip((hipError_t)e, "quantize launch");
+}
+
+VVH_API int vvh_convert(void* dst, int dst_dtype, const void* src, int src_dtype, size_t n, void* stream)
+{
+    if (!valid_dtype(dst_dtype) || !valid_dtype(src_dtype)) return fail(VVH_ERR_INVALID_ARG, "bad dtype");
+    if (n == 0) return VVH_OK;
+    if (!dst || !src) return fail(VVH_ERR_INVALID_ARG, "null pointer");
+    if (n > (uint64_t(1) << 61)) return fail(VVH_ERR_INVALID_ARG, "size overflow");
+    REQUIRE_INIT();
+    const int e = launch_convert(dst, dst_dtype, src, src_dtype, (int64_t)n, stream);
+    return e == 0 ? VVH_OK : fail_hip((hipError_t)e, "convert launch");
+}
+
+VVH_API int vvh_fill_normal(void* dst, int dtype, size_t n, uint64_t seed, float mean, float std, void* stream)
+{
+    if (!valid_dtype(dtype)) return fail(VVH_ERR_INVALID_ARG, "bad dtype");
+    if (n == 0) return VVH_OK;
+    if (!dst) return fail(VVH_ERR_INVALID_ARG, "null pointer");
+    if (n > (uint64_t(1) << 61)) return fail(VVH_ERR_INVALID_ARG, "size overflow");
+    REQUIRE_INIT();
+    const int e = launch_fill_normal(dst, dtype, (int64_t)n, seed, mean, std, stream);
+    return e == 0 ? VVH_OK : fail_hip((hipError_t)e, "fill launch");
+}
+
+// ---- dispatch introspection --------------------------------------------------------------------
+VVH_API int vvh_linear_q8_choice(size_t M, size_t N, size_t K, int act_dtype, int out_dtype)
+{
+    (void)N;
+    if (!valid_dtype(act_dtype) || !valid_dtype(out_dtype)) return -fail(VVH_ERR_INVALID_ARG, "bad dtype");
+    return choose_kernel(M, K, act_dtype, K % 16 == 0);
+}
+
+VVH_API int vvh_set_kernel_override(int kernel)
+{
+    if (kernel < K_AUTO || kernel > K_GEMM) return fail(VVH_ERR_INVALID_ARG, "bad kernel %d", kernel);
+    g_override.store(kernel);
+    return VVH_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,92 @@
+// BackendHIP: the MI355X backend of the INT8 per-channel linear path.
+//
+// A drop-in for the int8 linears of BackendCUDA (src/backend/backend_cuda.h:
+// 14-84): linear_q8 / linear_q8_add run hand-written gfx950 kernels through
+// the C ABI of libvvllm_hip.so (include/vvllm_hip.h); weights, scales and
+// biases are host pointers mirrored to HBM on first use; activations are
+// device pointers (fp32, or fp16 when constructed with fp16 = true, like
+// BackendCUDA(bool fp16), backend_cuda.cc:13-26).
+//
+// Operators outside the int8 linear path (norms, RoPE, attention, fp32
+// linear, ...) are not part of this backend and throw std::logic_error.
+// Failures of the C ABI are raised as std::runtime_error carrying the
+// library's message (the reference exits the process instead).
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "vvllm/backend/backend.h"
+
+namespace vvllm
+{
+
+class BackendHIP : public Backend
+{
+public:
+    explicit BackendHIP(bool fp16 = false, int device = 0);
+    ~BackendHIP() override;
+
+    BackendHIP(const BackendHIP&) = delete;
+    BackendHIP& operator=(const BackendHIP&) = delete;
+
+    bool fp16() const { return fp16_; }
+    const std::string& device_name() const { return name_; }
+
+    // pinned host staging memory (BackendCUDA::allocate, backend_cuda.cc:40-41)
+    void* allocate(std::size_t bytes) override;
+    void deallocate(void* ptr) override;
+
+    // ---- the int8 path ----
+    void linear_q8(float* out, const float* inp, const int8_t* weight, const float* scales,
+                   const float* bias, std::size_t M, std::size_t N, std::size_t K) override;
+    void linear_q8_add(float* out, const float* inp, const int8_t* weight, const float* scales,
+                       const float* bias, const float* residual, std::size_t M, std::size_t N,
+                       std::size_t K) override;
+    bool is_fp16() const override { return fp16_; }
+    Device device() const override { return Device::HIP; }
+    void fp32_to_fp16(void* dst, const float* src, std::size_t n) override;
+    void fp16_to_fp32(float* dst, const void* src, std::size_t n) override;
+
+    // Drops the HBM mirror of a host weight (e.g. before its buffer is freed
+    // and reused); the next linear_q8 on that pointer uploads again.
+    void forget_weight(const int8_t* host_weight);
+
+    // ---- outside the int8 path ----
+    void matmul(float*, const float*, const float*, std::size_t, std::size_t, std::size_t) override;
+    void add(float*, const float*, const float*, std::size_t) override;
+    void mul(float*, const float*, const float*, std::size_t) override;
+    void silu(float*, const float*, std::size_t) override;
+    void rms_norm(float*, const float*, const float*, std::size_t, float) override;
+    void softmax(float*, const float*, std::size_t) override;
+    void rope(float*, float*, std::size_t, std::size_t, std::size_t, std::size_t, std::size_t,
+              float) override;
+    void linear(float*, const float*, const float*, const float*, std::size_t, std::size_t,
+                std::size_t) override;
+    void silu_mul(float*, const float*, const float*, std::size_t) override;
+    void linear_add(float*, const float*, const float*, const float*, const float*, std::size_t,
+                    std::size_t, std::size_t) override;
+    void embedding(float*, const float*, std::size_t, std::size_t, std::size_t) override;
+    void causal_attention(float*, const float*, std::size_t, const float*, const float*,
+                          std::size_t, std::size_t, std::size_t, std::size_t, float) override;
+
+private:
+    std::uint64_t mirror(const int8_t* weight, const float* scales, const float* bias,
+                         std::size_t N, std::size_t K);
+    int act_dtype() const;
+
+    bool fp16_;
+    std::string name_;
+};
+
+// Tensor-layer hooks for Device::HIP: the bodies of device_allocate /
+// device_deallocate / device_copy (src/tensor/tensor.cc:72-116) for the GPU
+// device, backed by the caching allocator of libvvllm_hip.
+void* hip_device_allocate(std::size_t bytes);
+void hip_device_deallocate(void* ptr);
+void hip_copy_h2d(void* dst, const void* src, std::size_t bytes);
+void hip_copy_d2h(void* dst, const void* src, std::size_t bytes);
+void hip_copy_d2d(void* dst, const void* src, std::size_t bytes);
+
+}  // namespace vvllm
