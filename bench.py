@@ -1,0 +1,428 @@
+"""Benchmark of the INT8 per-channel linear path on one MI355X.
+
+Headline: the full Qwen2.5-0.5B decode projection
+set at M=1 -- per layer q 896->896 (+bias), k 896->128 (+bias), v 896->128
+(+bias), o 896->896 (+residual, in place), gate 896->4864, up 896->4864,
+down 4864->896 (+residual, in place) -- for 24 layers of independent seeded
+int8 per-channel weights, fp16 activations and outputs, fp32 accumulation.
+
+A step is one pass over the 168 projections, issued as one grouped launch
+(vvh_plan_run) over weights already resident in HBM.  Three replicas of the
+whole set (3 x 360 MB) are rotated step by step so that no step finds its
+weights in the 256 MB Infinity Cache.  `value` is algorithmic HBM bytes per
+step / measured step time (GB/s); the algorithmic bytes of one projection are
+N*K (codes) + 4N (scales) + 4N (bias) + 2K (activation row) + 2N (output)
++ 2N (residual read).  Timing: W untimed warm-up steps, then K steps
+bracketed by device synchronisation and HIP events on the stream the kernels
+run on.
+
+Also reported (same JSON line, key "extras"): the same set in model order
+(q/k/v grouped, o, gate+up grouped, down: 96 launches per step), per-call
+times of single launches, the LM-head GEMV, prefill GEMM TFLOPS
+(configs[3]) and the Qwen2.5-1.5B M sweep; and the reference CPU
+path (BackendCPU::linear_q8 compiled from the reference's sources,
+oracle/_ref) timed single-threaded on a bounded sample of the same workload.
+
+All inputs are synthetic (vvh_fill_normal + the device quantizer).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from vvllm_amd import capi  # noqa: E402
+
+F16, F32 = capi.F16, capi.F32
+HBM_PEAK_GBS = 8000.0           # MI355X HBM3E, AMD public spec
+MFMA_F16_PEAK_TFLOPS = 2500.0   # MI355X dense fp16 MFMA, AMD public spec
+
+QWEN05 = dict(hidden=896, kv=128, inter=4864, layers=24)
+# (name, N, K, bias, residual)
+def layer_projs(h, kv, inter):
+    return [("q", h, h, True, False), ("k", kv, h, True, False), ("v", kv, h, True, False),
+            ("o", h, h, False, True), ("gate", inter, h, False, False), ("up", inter, h, False, False),
+            ("down", h, inter, False, True)]
+
+
+def algo_bytes(M, N, K, bias, residual, act_bytes=2, out_bytes=2):
+    return N * K + 4 * N + (4 * N if bias else 0) + M * K * act_bytes + M * N * out_bytes + \
+        (M * N * out_bytes if residual else 0)
+
+
+# ---------------------------------------------------------------------------
+# HIP events on the null stream (the stream every launch below uses)
+# ---------------------------------------------------------------------------
+class HipEvents:
+    def __init__(self):
+        for name in ("libamdhip64.so.7", "libamdhip64.so", "/opt/rocm/lib/libamdhip64.so"):
+            try:
+                self.hip = ctypes.CDLL(name)
+                break
+            except OSError:
+                continue
+        h = self.hip
+        h.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        h.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        h.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        h.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        h.hipEventDestroy.argtypes = [ctypes.c_void_p]
+
+    def create(self):
+        e = ctypes.c_void_p()
+        assert self.hip.hipEventCreate(ctypes.byref(e)) == 0
+        return e
+
+    def record(self, e):
+        assert self.hip.hipEventRecord(e, None) == 0
+
+    def elapsed_ms(self, a, b):
+        assert self.hip.hipEventSynchronize(b) == 0
+        ms = ctypes.c_float()
+        assert self.hip.hipEventElapsedTime(ctypes.byref(ms), a, b) == 0
+        return ms.value
+
+
+def timed(ev, fn, reps):
+    """Average ms per call of fn() over reps calls, HIP events around the loop."""
+    capi.sync()
+    a, b = ev.create(), ev.create()
+    ev.record(a)
+    for i in range(reps):
+        fn(i)
+    ev.record(b)
+    ms = ev.elapsed_ms(a, b)
+    capi.sync()
+    return ms / reps
+
+
+# ---------------------------------------------------------------------------
+# device-resident synthetic workload
+# ---------------------------------------------------------------------------
+class Arena:
+    """One device allocation carved into 256-byte aligned pieces."""
+
+    def __init__(self, nbytes):
+        self.buf = capi.DevBuf(nbytes)
+        self.off = 0
+
+    def take(self, nbytes):
+        p = self.buf.ptr + self.off
+        self.off += (nbytes + 255) // 256 * 256
+        assert self.off <= self.buf.nbytes
+        return p
+
+
+def arena_size(items):
+    return sum((n + 255) // 256 * 256 for n in items)
+
+
+class Linear:
+    """One quantized projection resident in HBM with its input/output rows."""
+
+    def __init__(self, arena, tmp_w, M, N, K, bias, residual, seed, act=F16, outd=F16):
+        self.M, self.N, self.K, self.has_bias, self.has_res = M, N, K, bias, residual
+        self.act, self.outd = act, outd
+        ab, ob = (2 if act == F16 else 4), (2 if outd == F16 else 4)
+        self.w = arena.take(N * K)
+        self.s = arena.take(4 * N)
+        self.b = arena.take(4 * N) if bias else None
+        self.x = arena.take(M * K * ab)
+        self.y = arena.take(M * N * ob)
+        capi.call("vvh_fill_normal", tmp_w, F32, N * K, seed, 0.0, 0.02, None)
+        capi.call("vvh_quantize_per_channel", tmp_w, N, K, self.w, self.s, None)
+        if bias:
+            capi.call("vvh_fill_normal", self.b, F32, N, seed + 1, 0.0, 0.01, None)
+        capi.call("vvh_fill_normal", self.x, act, M * K, seed + 2, 0.0, 1.0, None)
+        capi.call("vvh_fill_normal", self.y, outd, M * N, seed + 3, 0.0, 1.0, None)
+        self.bytes = algo_bytes(M, N, K, bias, residual, ab, ob)
+        self.flops = 2 * M * N * K
+
+    @staticmethod
+    def sizes(M, N, K, bias, act=F16, outd=F16):
+        ab, ob = (2 if act == F16 else 4), (2 if outd == F16 else 4)
+        return [N * K, 4 * N] + ([4 * N] if bias else []) + [M * K * ab, M * N * ob]
+
+    def problem(self):
+        return capi.Q8Problem(out=self.y, inp=self.x, residual=self.y if self.has_res else None, weight=self.w,
+                              scales=self.s, bias=self.b, M=self.M, N=self.N, K=self.K)
+
+    def run(self):
+        capi.call("vvh_linear_q8_dev", self.y, self.x, self.w, self.s, self.b,
+                  self.y if self.has_res else None, self.M, self.N, self.K, self.act, self.outd, None)
+
+
+def make_plan(linears, act=F16, outd=F16):
+    arr = (capi.Q8Problem * len(linears))(*[l.problem() for l in linears])
+    h = ctypes.c_uint64()
+    capi.call("vvh_plan_create", arr, len(linears), act, outd, ctypes.byref(h))
+    return h.value
+
+
+def build_decode_set(replicas, layers, projs, tmp_w, M=1):
+    sets = []
+    for r in range(replicas):
+        sizes = []
+        for _ in range(layers):
+            for (_, N, K, bias, _res) in projs:
+                sizes += Linear.sizes(M, N, K, bias)
+        arena = Arena(arena_size(sizes))
+        lins = []
+        for l in range(layers):
+            for pid, (name, N, K, bias, res) in enumerate(projs):
+                seed = 0x5EED + 16 * l + pid + 100003 * r
+                lins.append(Linear(arena, tmp_w, M, N, K, bias, res, seed))
+        sets.append((arena, lins))
+    capi.sync()
+    return sets
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: reference BackendCPU::linear_q8 on the host, one thread
+# ---------------------------------------------------------------------------
+def cpu_baseline(lins, budget_s):
+    from oracle import oracle as O
+
+    kind = "reference" if O.available("reference") else "port"
+    if not O.available(kind):
+        O.build(ref=False)
+    host, host_keep = [], []
+    for l in lins:
+        q = np.empty((l.N, l.K), np.int8)
+        capi.call("vvh_memcpy_d2h", q.ctypes.data, l.w, q.nbytes)
+        s = np.empty(l.N, np.float32)
+        capi.call("vvh_memcpy_d2h", s.ctypes.data, l.s, s.nbytes)
+        b = None
+        if l.b:
+            b = np.empty(l.N, np.float32)
+            capi.call("vvh_memcpy_d2h", b.ctypes.data, l.b, b.nbytes)
+        x16 = np.empty((1, l.K), np.float16)
+        capi.call("vvh_memcpy_d2h", x16.ctypes.data, l.x, x16.nbytes)
+        r = np.zeros((1, l.N), np.float32) if l.has_res else None
+        host.append((x16.astype(np.float32), q, s, b, r, l))
+    # the reference takes fp32 activations/outputs (widened fp16 inputs are exact);
+    # call its entry points directly with preallocated buffers
+    lib = O._lib(kind)
+    pre = "ref_" if kind == "reference" else "orc_"
+    f_lin, f_add = getattr(lib, pre + "linear_q8"), getattr(lib, pre + "linear_q8_add")
+    calls = []
+    for x, q, s, b, r, l in host:
+        y = r if r is not None else np.empty((1, l.N), np.float32)
+        bp = None if b is None else b.ctypes.data
+        if r is not None:  # linear_q8_add in place, as the model calls it
+            calls.append((f_add, (y.ctypes.data, x.ctypes.data, q.ctypes.data, s.ctypes.data, bp, y.ctypes.data,
+                                  1, l.N, l.K)))
+        else:
+            calls.append((f_lin, (y.ctypes.data, x.ctypes.data, q.ctypes.data, s.ctypes.data, bp, 1, l.N, l.K)))
+        host_keep.append(y)
+    per_pass = sum(algo_bytes(1, l.N, l.K, l.has_bias, l.has_res, 4, 4) for *_, l in host)
+    passes, t0 = 0, time.perf_counter()
+    while True:
+        for f, a in calls:
+            f(*a)
+        passes += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    return dict(value=round(per_pass * passes / el / 1e9, 3), unit="GB/s", cores=1, kind=kind,
+                ms_per_step=round(el / passes * 1e3, 3),
+                sample=(f"{passes} full passes of the 24-layer decode projection set (168 linear_q8 calls, "
+                        f"same int8 weights as the GPU run, fp32 activations) in {el:.1f} s, one thread; "
+                        f"{'reference BackendCPU::linear_q8 compiled from its sources -O2 -mavx2 -mfma' if kind == 'reference' else 'oracle restatement of BackendCPU::linear_q8'}"))
+
+
+# ---------------------------------------------------------------------------
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--replicas", type=int, default=3)
+    ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build targets one MI355X; the int8 linear path is measured on one GPU "
+              "(multi-GPU sharding is design-only). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    name = capi.init(0)
+    ev = HipEvents()
+    h, kv, inter, L = QWEN05["hidden"], QWEN05["kv"], QWEN05["inter"], QWEN05["layers"]
+    projs = layer_projs(h, kv, inter)
+    tmp_w = capi.DevBuf(max(inter * h, 151936 * 896, 8960 * 1536) * 4)
+
+    t_setup = time.perf_counter()
+    sets = build_decode_set(args.replicas, L, projs, tmp_w.ptr)
+    plans = [make_plan(lins) for _, lins in sets]
+    step_bytes = sum(l.bytes for l in sets[0][1])
+    print(f"[bench] {name}: {args.replicas} x {len(sets[0][1])} projections, "
+          f"{step_bytes / 1e6:.1f} MB/step, setup {time.perf_counter() - t_setup:.1f}s", file=sys.stderr, flush=True)
+
+    def step(i):
+        capi.call("vvh_plan_run", plans[i % len(plans)], None)
+
+    for i in range(args.warmup):
+        step(i)
+    ms = timed(ev, lambda i: step(args.warmup + i), args.steps)
+    value = step_bytes / (ms * 1e-3) / 1e9
+    launches = ctypes.c_int()
+    capi.call("vvh_plan_launches", plans[0], ctypes.byref(launches))
+    print(f"[bench] grouped step {ms * 1e3:.1f} us, {value:.0f} GB/s", file=sys.stderr, flush=True)
+
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", "traffic_decode_set.json")
+    if os.path.exists(tfile):
+        t = json.load(open(tfile))
+        traffic = t.get("hbm_bytes_per_launch")
+
+    result = {
+        "metric": "linear_q8 GEMV µs + HBM GB/s at Qwen2.5-0.5B shapes; prefill GEMM TFLOPS",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 weights x f16 activations, f32 accumulate",
+        "data": "synthetic (seeded N(0,0.02) fp32 weights quantized per channel on device; N(0,1) fp16 activations)",
+        "config": {"workload": "configs[1]: Qwen2.5-0.5B decode projection set, 24 layers x "
+                               "{q,k,v,o,gate,up,down}, M=1, one grouped launch per step",
+                   "M": 1, "layers": L, "projections_per_step": len(sets[0][1]),
+                   "algorithmic_bytes_per_step": step_bytes, "weight_replicas_rotated": args.replicas,
+                   "launches_per_step": launches.value, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": "k_skinny_grouped<f16>", "achieved": round(value, 2),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(value / HBM_PEAK_GBS, 4),
+                     "traffic": traffic},
+    }
+
+    if not args.no_extras:
+        result["extras"] = extras(ev, sets, projs, tmp_w.ptr, args)
+    if not args.no_cpu:
+        print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_baseline(sets[0][1], args.cpu_seconds)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+
+
+def extras(ev, sets, projs, tmp_w, args):
+    out = {}
+    L = QWEN05["layers"]
+    # (1) model order: q/k/v grouped, o, gate+up grouped, down -> 4 launches/layer
+    order_plans = []
+    for _, lins in sets:
+        seq = []
+        for l in range(L):
+            q, k, v, o, g, u, d = lins[7 * l: 7 * l + 7]
+            seq += [("plan", make_plan([q, k, v])), ("lin", o), ("plan", make_plan([g, u])), ("lin", d)]
+        order_plans.append(seq)
+
+    def model_step(i):
+        for kind, item in order_plans[i % len(order_plans)]:
+            if kind == "plan":
+                capi.call("vvh_plan_run", item, None)
+            else:
+                item.run()
+
+    for i in range(5):
+        model_step(i)
+    reps = max(args.steps // 4, 20)
+    ms = timed(ev, model_step, reps)
+    step_bytes = sum(l.bytes for l in sets[0][1])
+    out["model_order"] = {"launches_per_step": 4 * L, "ms_per_step": round(ms, 5),
+                          "GBps": round(step_bytes / (ms * 1e-3) / 1e9, 2)}
+    print(f"[bench] model order {ms * 1e3:.1f} us", file=sys.stderr, flush=True)
+
+    # (2) single launches per projection, events between consecutive calls
+    nproj = len(projs)
+    events = [ev.create() for _ in range(nproj * L + 1)]
+    per = {p[0]: [] for p in projs}
+    for rep in range(6):
+        lins = sets[rep % len(sets)][1]
+        capi.sync()
+        ev.record(events[0])
+        for i, l in enumerate(lins):
+            l.run()
+            ev.record(events[i + 1])
+        capi.sync()
+        if rep < 2:
+            continue  # warm-up passes
+        for i in range(len(lins)):
+            per[projs[i % nproj][0]].append(ev.elapsed_ms(events[i], events[i + 1]) * 1e3)
+    calls = {}
+    for (name, N, K, bias, res) in projs:
+        us = float(np.median(per[name]))
+        b = algo_bytes(1, N, K, bias, res)
+        calls[name] = {"N": N, "K": K, "us": round(us, 2), "GBps": round(b / (us * 1e-6) / 1e9, 1),
+                       "kernel": capi.kernel_choice(1, N, K, F16, F16)}
+    out["per_call_in_sequence"] = calls
+
+    # (3) LM head GEMV, configs[2]: K=896, N=151936, fp16 act, fp32 logits
+    N, K = 151936, 896
+    heads = []
+    for r in range(3):
+        ar = Arena(arena_size(Linear.sizes(1, N, K, False, F16, F32)))
+        heads.append((ar, Linear(ar, tmp_w, 1, N, K, False, False, 777 + r, F16, F32)))
+    for i in range(6):
+        heads[i % 3][1].run()
+    us = timed(ev, lambda i: heads[i % 3][1].run(), 60) * 1e3
+    b = heads[0][1].bytes
+    out["lm_head"] = {"N": N, "K": K, "us": round(us, 2), "GBps": round(b / (us * 1e-6) / 1e9, 1),
+                      "hbm_frac": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                      "kernel": capi.kernel_choice(1, N, K, F16, F32)}
+    del heads
+    print(f"[bench] lm head {us:.1f} us", file=sys.stderr, flush=True)
+
+    # (4) prefill GEMM, configs[3]
+    gemm = {}
+    for M in (128, 512, 2048):
+        for name, N, K, res in (("gate_up", QWEN05["inter"], QWEN05["hidden"], False),
+                                ("down", QWEN05["hidden"], QWEN05["inter"], True)):
+            reps = []
+            for r in range(2):
+                ar = Arena(arena_size(Linear.sizes(M, N, K, False)))
+                reps.append((ar, Linear(ar, tmp_w, M, N, K, False, res, 900 + r)))
+            for i in range(4):
+                reps[i % 2][1].run()
+            us = timed(ev, lambda i: reps[i % 2][1].run(), 40) * 1e3
+            tf = reps[0][1].flops / (us * 1e-6) / 1e12
+            gemm[f"{name}_M{M}"] = {"M": M, "N": N, "K": K, "us": round(us, 2), "TFLOPS": round(tf, 1),
+                                    "mfma_frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
+                                    "kernel": capi.kernel_choice(M, N, K, F16, F16)}
+    out["prefill_gemm"] = gemm
+    print(f"[bench] gemm M512 gate_up {gemm['gate_up_M512']['us']} us", file=sys.stderr, flush=True)
+
+    # (5) Qwen2.5-1.5B shapes, M sweep
+    sweep = {}
+    for M in (1, 4, 16, 64, 256):
+        for name, N, K in (("qo", 1536, 1536), ("kv", 256, 1536), ("gate_up", 8960, 1536), ("down", 1536, 8960)):
+            reps = []
+            for r in range(2):
+                ar = Arena(arena_size(Linear.sizes(M, N, K, False)))
+                reps.append((ar, Linear(ar, tmp_w, M, N, K, False, False, 1300 + r)))
+            for i in range(4):
+                reps[i % 2][1].run()
+            us = timed(ev, lambda i: reps[i % 2][1].run(), 30) * 1e3
+            l = reps[0][1]
+            sweep[f"{name}_M{M}"] = {"us": round(us, 2), "GBps": round(l.bytes / (us * 1e-6) / 1e9, 1),
+                                     "TFLOPS": round(l.flops / (us * 1e-6) / 1e12, 2),
+                                     "kernel": capi.kernel_choice(M, N, K, F16, F16)}
+    out["qwen15_sweep"] = sweep
+    return out
+
+
+if __name__ == "__main__":
+    main()
