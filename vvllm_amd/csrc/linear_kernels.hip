@@ -24,6 +24,9 @@
 //               fused scale/bias/residual epilogue.
 #include <hip/hip_runtime.h>
 
+#include <cstdlib>
+#include <utility>
+
 #include "common.h"
 
 namespace vvh {
@@ -79,6 +82,21 @@ __device__ __forceinline__ void store_out(const LinArgs& a, int64_t m, int64_t n
     const int64_t o = m * a.N + n;
     if (a.res) v += ld_f(static_cast<const OT*>(a.res) + o);
     st_f(static_cast<OT*>(a.out) + o, v);
+}
+
+// LDS reads done (lgkmcnt(0)), then s_barrier, without waiting on vector
+// memory loads.  Written with builtins so the compiler's wait-count tracking
+// sees the lgkmcnt(0); the empty asm with a memory clobber keeps the
+// compiler from moving memory accesses across the barrier.
+// The scheduling barriers keep the instruction scheduler from hoisting work
+// of the next pipeline step (which only depends on registers) above it.
+__device__ __forceinline__ void lds_barrier()
+{
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // vmcnt 63, expcnt 7: no wait; lgkmcnt 0
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
 }
 
 // Weight rows are streamed exactly once: load them non-temporally so they do
@@ -231,74 +249,111 @@ __global__ __launch_bounds__(256) void k_gemv_f32(LinArgs a)
 // A 16-byte chunk of 16 codes feeds two MFMAs (codes 0-7, then 8-15); the
 // activations are read with the same k mapping, so the sum is unchanged.
 // Lanes whose row m >= M feed zeros.
+//
+// Memory pipeline: the weight stream is the only HBM traffic, so each wave
+// keeps two chunks of kDecodeDepth 16-byte loads per lane in flight (the
+// next chunk is issued before the current one is consumed).  When the
+// activations are small (M*K*2 <= kXLdsBytes) the block stages them once in
+// LDS (rows padded by 16 bytes so the 16 rows of an MFMA operand fall in
+// distinct banks); otherwise they are read through the L1/L2 caches.
 // ---------------------------------------------------------------------------
-template <typename OT>
-__device__ __forceinline__ void skinny_body(const LinArgs& a, int64_t block)
+constexpr int kDecodeDepth = 8;
+constexpr int kXLdsBytes = 16384;
+constexpr int kXLdsHalves = kXLdsBytes / 2 + 16 * 8;
+
+struct DecodeShared {
+    f4 red[4][64];
+    __attribute__((aligned(16))) f16 xs[kXLdsHalves];
+};
+
+__device__ __forceinline__ bool decode_x_in_lds(const LinArgs& a) { return a.M * a.K * 2 <= kXLdsBytes; }
+
+template <typename OT, bool XLDS>
+__device__ __forceinline__ void skinny_body(const LinArgs& a, int64_t block, DecodeShared& sh)
 {
-    __shared__ f4 red[4][64];
+    constexpr int D = kDecodeDepth;
     const DecodeCoord c = decode_coord(a, block);
     const int64_t n0 = c.tile * kDecodeTileN;
     const int64_t nrow = n0 + (c.lane & 15) < a.N ? n0 + (c.lane & 15) : a.N - 1;
     const int chunk = c.lane >> 4;
     const int m = c.lane & 15;
     const bool mvalid = m < a.M;
+    const bool active = n0 < a.N;
     const int8_t* wp = a.w + nrow * a.K + chunk * 16;
-    const f16* xp = static_cast<const f16*>(a.inp) + (mvalid ? m : 0) * a.K + chunk * 16;
+    const int64_t ldx = a.K + 8;  // padded LDS row stride of the staged activations
+    const f16* xg = static_cast<const f16*>(a.inp);
+    const f16* xp = XLDS ? sh.xs + (mvalid ? m : 0) * ldx + chunk * 16
+                         : xg + (mvalid ? m : 0) * a.K + chunk * 16;
 
+    u4 wa[D], wb[D];
+    auto issue = [&](u4 (&buf)[D], int64_t s) {
+#pragma unroll
+        for (int u = 0; u < D; u++) {
+            const int64_t st = s + u;
+            buf[u] = u4{0u, 0u, 0u, 0u};
+            if (active && st < c.s1 && st * 64 + chunk * 16 < a.K) buf[u] = ld_stream(wp + st * 64);
+        }
+    };
     f4 acc0 = {0.f, 0.f, 0.f, 0.f};
     f4 acc1 = {0.f, 0.f, 0.f, 0.f};
-    if (n0 < a.N) {
-        constexpr int U = 8;
-        int64_t s = c.s0;
-        const int64_t kfull = a.K / 64;  // steps whose 64 codes are all in range
-        // main loop: U full steps per batch, loads first
-        for (; s + U <= c.s1 && s + U <= kfull; s += U) {
-            u4 wv[U];
-            h8 xa[U], xb[U];
+    auto consume = [&](const u4 (&buf)[D], int64_t s) {
 #pragma unroll
-            for (int u = 0; u < U; u++) wv[u] = ld_stream(wp + (s + u) * 64);
-#pragma unroll
-            for (int u = 0; u < U; u++) {
-                if (mvalid) {
-                    xa[u] = *reinterpret_cast<const h8*>(xp + (s + u) * 64);
-                    xb[u] = *reinterpret_cast<const h8*>(xp + (s + u) * 64 + 8);
-                } else {
-                    xa[u] = h8{};
-                    xb[u] = h8{};
+        for (int u = 0; u < D; u++) {
+            const int64_t st = s + u;
+            if (st < c.s1) {
+                h8 xa = {}, xb = {};
+                if (mvalid && st * 64 + chunk * 16 < a.K) {
+                    xa = *reinterpret_cast<const h8*>(xp + st * 64);
+                    xb = *reinterpret_cast<const h8*>(xp + st * 64 + 8);
                 }
-            }
-#pragma unroll
-            for (int u = 0; u < U; u++) {
                 h8 b0, b1;
-                i8x16_to_h8x2(wv[u], b0, b1);
-                acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[u], b0, acc0, 0, 0, 0);
-                acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xb[u], b1, acc1, 0, 0, 0);
+                i8x16_to_h8x2(buf[u], b0, b1);
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, b0, acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xb, b1, acc1, 0, 0, 0);
             }
         }
-        // remainder steps (including a partial last step when K % 64 != 0)
-        for (; s < c.s1; s++) {
-            const int64_t k = s * 64 + chunk * 16;
-            u4 wv = {0u, 0u, 0u, 0u};
-            h8 xa = {}, xb = {};
-            if (k < a.K) {
-                wv = ld_stream(wp + s * 64);
-                if (mvalid) {
-                    xa = *reinterpret_cast<const h8*>(xp + s * 64);
-                    xb = *reinterpret_cast<const h8*>(xp + s * 64 + 8);
-                }
+    };
+
+    if (XLDS) {
+        // activation loads first, then the first weight chunk, so both are in
+        // flight while the activations are written to LDS
+        constexpr int XL = kXLdsBytes / (256 * 16);
+        const int64_t xchunks = a.M * a.K / 8;
+        u4 xr[XL];
+#pragma unroll
+        for (int i = 0; i < XL; i++) {
+            const int64_t idx = threadIdx.x + 256 * i;
+            xr[i] = idx < xchunks ? *reinterpret_cast<const u4*>(xg + idx * 8) : u4{0u, 0u, 0u, 0u};
+        }
+        issue(wa, c.s0);
+#pragma unroll
+        for (int i = 0; i < XL; i++) {
+            const int64_t idx = threadIdx.x + 256 * i;
+            if (idx < xchunks) {
+                const int64_t row = idx * 8 / a.K, col = idx * 8 - row * a.K;
+                *reinterpret_cast<u4*>(sh.xs + row * ldx + col) = xr[i];
             }
-            h8 b0, b1;
-            i8x16_to_h8x2(wv, b0, b1);
-            acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, b0, acc0, 0, 0, 0);
-            acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xb, b1, acc1, 0, 0, 0);
+        }
+        // LDS writes done and visible to the block; the weight loads stay in flight
+        lds_barrier();
+    } else {
+        issue(wa, c.s0);
+    }
+
+    if (active) {
+        for (int64_t s = c.s0; s < c.s1; s += 2 * D) {
+            issue(wb, s + D);
+            consume(wa, s);
+            if (s + 2 * D < c.s1) issue(wa, s + 2 * D);
+            consume(wb, s + D);
         }
     }
     f4 acc = acc0 + acc1;
     if (c.ksplit > 1) {
-        red[c.wave][c.lane] = acc;
+        sh.red[c.wave][c.lane] = acc;
         __syncthreads();
         if (c.ks == 0) {
-            for (int j = 1; j < c.ksplit; j++) acc += red[c.wave + j][c.lane];
+            for (int j = 1; j < c.ksplit; j++) acc += sh.red[c.wave + j][c.lane];
         }
     }
     if (c.ks == 0) {
@@ -316,7 +371,9 @@ __device__ __forceinline__ void skinny_body(const LinArgs& a, int64_t block)
 template <typename OT>
 __global__ __launch_bounds__(256) void k_skinny(LinArgs a)
 {
-    skinny_body<OT>(a, blockIdx.x);
+    __shared__ DecodeShared sh;
+    if (decode_x_in_lds(a)) skinny_body<OT, true>(a, blockIdx.x, sh);
+    else skinny_body<OT, false>(a, blockIdx.x, sh);
 }
 
 // Grouped launch: block b serves problem p with
@@ -324,6 +381,7 @@ __global__ __launch_bounds__(256) void k_skinny(LinArgs a)
 template <typename OT>
 __global__ __launch_bounds__(256) void k_skinny_grouped(const LinArgs* __restrict__ table, int count)
 {
+    __shared__ DecodeShared sh;
     const int b = blockIdx.x;
     int lo = 0, hi = count - 1;
     while (lo < hi) {  // last p with block_begin <= b
@@ -332,7 +390,8 @@ __global__ __launch_bounds__(256) void k_skinny_grouped(const LinArgs* __restric
         else hi = mid - 1;
     }
     const LinArgs a = table[lo];
-    skinny_body<OT>(a, b - a.block_begin);
+    if (decode_x_in_lds(a)) skinny_body<OT, true>(a, b - a.block_begin, sh);
+    else skinny_body<OT, false>(a, b - a.block_begin, sh);
 }
 
 // ---------------------------------------------------------------------------
@@ -485,6 +544,323 @@ __global__ __launch_bounds__(256) void k_gemm(LinArgs a)
 }
 
 // ---------------------------------------------------------------------------
+// k_gemm2: fp16 activations, M > 16, K % 64 == 0.
+// Block tile 128(m) x 128(n) x 64(k), 256 threads = 4 waves arranged WM x WN
+// (wave tile (128/WM) x (128/WN), built from 32x32x16 MFMAs).  Both operands
+// are staged through a ring of D LDS stages filled by direct global->LDS
+// loads (global_load_lds_dwordx4: no VGPRs, no ds_write), so D-1 stages of
+// loads are in flight while one is multiplied.  A is stored as fp16, B as the
+// raw int8 codes; each wave converts the B fragments it reads.
+//
+// LDS layout (1 KB per 64-lane load instruction, lane i -> bytes 16i..16i+15;
+// the swizzles make the 16 rows read by 16 lanes of a 16-byte fragment load
+// fall into 16 distinct 16-byte bank groups of the 64-bank LDS):
+//   A stage: 128 rows x 128 B; row r keeps 16-byte chunk c at slot c ^ ((r >> 1) & 7)
+//   B stage: 128 rows x  64 B; row r keeps 16-byte chunk c at slot c ^ ((r >> 2) & 3)
+// k order inside an MFMA: the B fragment (kk2, tj) of lane l holds codes
+// k = 32*kk2 + 16*(l/32) + [0, 16); bytes 0-7 feed MFMA h = 0 and 8-15 h = 1,
+// and the A fragment (kk2, h) of lane l holds x[i][32*kk2 + 16*(l/32) + 8*h + [0, 8)].
+//
+// Synchronisation: one s_barrier per stage.  Before it each thread waits
+// until its own loads of the stage to be read have landed (vmcnt counts the
+// loads issued after them) and its LDS reads of the previous stage are done
+// (lgkmcnt(0)); after it the stage read in the previous step is refilled.
+// The stage buffers are separate __shared__ objects indexed only with
+// constants, and the fill / multiply helpers take them as __restrict__
+// parameters: that is what lets the compiler tell the in-flight
+// direct-to-LDS writes of one stage from the reads of another (otherwise it
+// drains every outstanding load before each LDS read).
+//
+// Epilogue: acc * scale + bias in fp32 is transposed through LDS (the 32-row
+// quarter q of the tile in stage buffer q) and written row-major with 16-byte
+// stores, the residual added in fp32 before the single rounding to OT.
+// ---------------------------------------------------------------------------
+struct Gemm2Stage {
+    __attribute__((aligned(16))) f16 a[kGemmBM * kGemmBK];
+    __attribute__((aligned(16))) int8_t b[kGemmBN * kGemmBK];
+};
+// per thread and stage: 16/NW A loads + 8/NW B loads of 16 bytes (NW waves)
+template <int NW>
+constexpr int gemm2_loads_per_stage() { return 24 / NW; }
+constexpr int kEpiStride = kGemmBN + 4;  // fp32 row stride of an epilogue quarter
+static_assert(32 * kEpiStride * 4 <= (int)sizeof(Gemm2Stage), "epilogue quarter fits a stage buffer");
+
+// s_waitcnt with vmcnt <= v (expcnt, lgkmcnt not waited on); gfx9 encoding.
+template <int V>
+__device__ __forceinline__ void wait_vmcnt()
+{
+    static_assert(V >= 0 && V < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((V & 15) | ((V >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+__device__ __forceinline__ int swz_a(int r, int c) { return c ^ ((r >> 1) & 7); }
+__device__ __forceinline__ int swz_b(int r, int c) { return c ^ ((r >> 2) & 3); }
+
+template <int NW>
+__device__ __forceinline__ void gemm2_fill(f16* __restrict__ sa, int8_t* __restrict__ sb,
+                                           const f16* const* a_src, const int8_t* const* b_src,
+                                           int wave, int64_t k0)
+{
+#pragma unroll
+    for (int i = 0; i < 16 / NW; i++)
+        __builtin_amdgcn_global_load_lds(a_src[i] + k0, sa + (wave * (16 / NW) + i) * 512, 16, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 8 / NW; i++)
+        __builtin_amdgcn_global_load_lds(b_src[i] + k0, sb + (wave * (8 / NW) + i) * 1024, 16, 0, 0);
+}
+
+// Fragments of one stage held in registers: the B codes (int8, converted
+// just before use) and the fp16 A fragments.
+template <int TI, int TJ>
+struct Gemm2Frag {
+    u4 b[2][TJ];
+    h8 a[2][2][TI];
+};
+
+template <int TI, int TJ>
+__device__ __forceinline__ void gemm2_read(const f16* __restrict__ sa, const int8_t* __restrict__ sb,
+                                           Gemm2Frag<TI, TJ>& f, int row0, int col0, int fl, int fh)
+{
+#pragma unroll
+    for (int kk2 = 0; kk2 < 2; kk2++) {
+#pragma unroll
+        for (int tj = 0; tj < TJ; tj++) {
+            const int j = col0 + tj * 32 + fl;
+            f.b[kk2][tj] = *reinterpret_cast<const u4*>(sb + j * 64 + swz_b(j, kk2 * 2 + fh) * 16);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int ti = 0; ti < TI; ti++) {
+                const int i = row0 + ti * 32 + fl;
+                f.a[kk2][h][ti] = *reinterpret_cast<const h8*>(sa + i * 64 + swz_a(i, kk2 * 4 + fh * 2 + h) * 8);
+            }
+    }
+}
+
+template <int TI, int TJ>
+__device__ __forceinline__ void gemm2_mfma(const Gemm2Frag<TI, TJ>& f, f16v (&acc)[TI][TJ])
+{
+#pragma unroll
+    for (int kk2 = 0; kk2 < 2; kk2++) {
+        h8 fb[TJ][2];
+#pragma unroll
+        for (int tj = 0; tj < TJ; tj++) i8x16_to_h8x2(f.b[kk2][tj], fb[tj][0], fb[tj][1]);
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int ti = 0; ti < TI; ti++)
+#pragma unroll
+                for (int tj = 0; tj < TJ; tj++)
+                    acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[kk2][h][ti], fb[tj][h], acc[ti][tj], 0, 0, 0);
+    }
+}
+
+template <typename OT, int D, int NW, int WM>
+__global__ __launch_bounds__(64 * NW, 1) void k_gemm2(LinArgs a)
+{
+    static_assert(D == 4 || D == 6, "even stage count (2-way fragment double buffer), >= 4 for the epilogue");
+    static_assert(NW == 4 || NW == 8, "waves per block");
+    constexpr int NT = 64 * NW;
+    constexpr int LPS = gemm2_loads_per_stage<NW>();
+    constexpr int WN = NW / WM;
+    constexpr int TI = kGemmBM / WM / 32, TJ = kGemmBN / WN / 32;
+    using Frag = Gemm2Frag<TI, TJ>;
+    __shared__ Gemm2Stage st0, st1, st2, st3, st4, st5;
+
+    const int64_t nbm = (a.M + kGemmBM - 1) / kGemmBM;
+    const int64_t nbn = (a.N + kGemmBN - 1) / kGemmBN;
+    const int64_t logical = xcd_remap(blockIdx.x, nbm * nbn);
+    const int64_t m0 = (logical % nbm) * kGemmBM;
+    const int64_t n0 = (logical / nbm) * kGemmBN;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave % WM, wn = wave / WM;
+    const int row0 = wm * (kGemmBM / WM), col0 = wn * (kGemmBN / WN);
+    const int fl = lane & 31, fh = lane >> 5;
+    const f16* X = static_cast<const f16*>(a.inp);
+
+    // epilogue constants, loaded first (their loads are the oldest in the
+    // vmcnt queue, so the stage waits below still count correctly)
+    float sc[TJ], bi[TJ];
+#pragma unroll
+    for (int tj = 0; tj < TJ; tj++) {
+        const int64_t n = n0 + col0 + tj * 32 + fl;
+        sc[tj] = n < a.N ? a.scales[n] : 0.0f;
+        bi[tj] = (a.bias && n < a.N) ? a.bias[n] : 0.0f;
+    }
+
+    // per-lane global sources of this thread's direct-to-LDS loads (k0 added per stage)
+    const f16* a_src[16 / NW];
+#pragma unroll
+    for (int i = 0; i < 16 / NW; i++) {
+        const int r = (wave * (16 / NW) + i) * 8 + (lane >> 3);  // A stage row written by this lane
+        const int64_t gr = m0 + r < a.M ? m0 + r : a.M - 1;      // rows past M: any valid row
+        a_src[i] = X + gr * a.K + swz_a(r, lane & 7) * 8;
+    }
+    const int8_t* b_src[8 / NW];
+#pragma unroll
+    for (int i = 0; i < 8 / NW; i++) {
+        const int r = (wave * (8 / NW) + i) * 16 + (lane >> 2);
+        const int64_t gn = n0 + r < a.N ? n0 + r : a.N - 1;
+        b_src[i] = a.w + gn * a.K + swz_b(r, lane & 3) * 16;
+    }
+
+    auto stage = [&](auto S) -> Gemm2Stage& {
+        constexpr int s = decltype(S)::value % D;
+        if constexpr (s == 0) return st0;
+        else if constexpr (s == 1) return st1;
+        else if constexpr (s == 2) return st2;
+        else if constexpr (s == 3) return st3;
+        else if constexpr (s == 4) return st4;
+        else return st5;
+    };
+    auto issue = [&](Gemm2Stage& g, int64_t kt) { gemm2_fill<NW>(g.a, g.b, a_src, b_src, wave, kt * kGemmBK); };
+
+    f16v acc[TI][TJ];
+#pragma unroll
+    for (int i = 0; i < TI; i++)
+#pragma unroll
+        for (int j = 0; j < TJ; j++) acc[i][j] = f16v{};
+    Frag f0, f1;
+    auto frag = [&](auto P) -> Frag& {
+        if constexpr (decltype(P)::value % 2 == 0) return f0;
+        else return f1;
+    };
+    auto read = [&](auto S, auto P) { gemm2_read<TI, TJ>(stage(S).a, stage(S).b, frag(P), row0, col0, fl, fh); };
+    auto sync = [&]() { lds_barrier(); };
+
+    // Schedule (all straight-line, stage indices and vmcnt thresholds are
+    // compile-time constants):
+    //   prologue: issue stages 0..P-1 (P = min(D, nk)); wait stage 0; read its fragments
+    //   step j:   wait until stage j+1 has landed; barrier (stage j's buffer
+    //             is free, its fragments are in registers); refill that buffer
+    //             with stage j+D; read stage j+1's fragments; MFMAs of stage j
+    //             -- the LDS reads of j+1 overlap the MFMAs of j.
+    // For R steps from kt0 (kt0 % D == 0, so buffer and fragment parity are
+    // static), with the stage count n of the problem known to be kt0 + R:
+    auto steps = [&]<int R, bool FIRST_PASS>(int64_t kt0) {
+        [&]<int... J>(std::integer_sequence<int, J...>) {
+            ([&] {
+                constexpr int j = J;
+                if constexpr (j + 1 < R) {
+                    // later stages possibly in flight after stage j+1: j+2 .. min(j+D-1, R-1)
+                    constexpr int later = (R - 2 - j < D - 2) ? R - 2 - j : D - 2;
+                    wait_vmcnt<later * LPS>();
+                }
+                sync();
+                if constexpr (j + D < R) issue(stage(std::integral_constant<int, j>{}), kt0 + j + D);
+                if constexpr (j + 1 < R) read(std::integral_constant<int, j + 1>{}, std::integral_constant<int, j + 1>{});
+                gemm2_mfma<TI, TJ>(frag(std::integral_constant<int, j>{}), acc);
+            }(), ...);
+        }(std::make_integer_sequence<int, R>{});
+    };
+    auto prologue = [&]<int P>() {
+        [&]<int... S>(std::integer_sequence<int, S...>) {
+            (issue(stage(std::integral_constant<int, S>{}), S), ...);
+        }(std::make_integer_sequence<int, P>{});
+        wait_vmcnt<(P - 1) * LPS>();
+        sync();
+        read(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+    };
+
+    const int64_t nk = a.K / kGemmBK;
+    if (nk >= D) {
+        prologue.template operator()<D>();
+        int64_t kt0 = 0;
+        for (; kt0 + 2 * D <= nk; kt0 += D) {
+            // a full group: every step refills, every wait is at the steady-state depth
+            [&]<int... J>(std::integer_sequence<int, J...>) {
+                ([&] {
+                    constexpr int j = J;
+                    wait_vmcnt<(D - 2) * LPS>();
+                    sync();
+                    issue(stage(std::integral_constant<int, j>{}), kt0 + j + D);
+                    read(std::integral_constant<int, j + 1>{}, std::integral_constant<int, j + 1>{});
+                    gemm2_mfma<TI, TJ>(frag(std::integral_constant<int, j>{}), acc);
+                }(), ...);
+            }(std::make_integer_sequence<int, D>{});
+        }
+        const int64_t r = nk - kt0;  // D .. 2D-1
+        [&]<int... R>(std::integer_sequence<int, R...>) {
+            ((r == R + D ? steps.template operator()<R + D, false>(kt0) : void()), ...);
+        }(std::make_integer_sequence<int, D>{});
+    } else {
+        [&]<int... R>(std::integer_sequence<int, R...>) {
+            ((nk == R + 1 ? [&] {
+                prologue.template operator()<R + 1>();
+                steps.template operator()<R + 1, true>(0);
+            }() : void()), ...);
+        }(std::make_integer_sequence<int, D - 1>{});
+    }
+
+    // ---- epilogue ----
+    __builtin_amdgcn_s_waitcnt(0);  // everything, including in-flight stage loads
+    lds_barrier();
+    auto quarter = [&](int q) -> float* {
+        return reinterpret_cast<float*>(q == 0 ? &st0 : q == 1 ? &st1 : q == 2 ? &st2 : &st3);
+    };
+#pragma unroll
+    for (int tj = 0; tj < TJ; tj++) {
+        const int col = col0 + tj * 32 + fl;
+#pragma unroll
+        for (int ti = 0; ti < TI; ti++) {
+            float* q = quarter((row0 >> 5) + ti);
+#pragma unroll
+            for (int r = 0; r < 16; r++)
+                q[(8 * (r >> 2) + 4 * fh + (r & 3)) * kEpiStride + col] = acc[ti][tj][r] * sc[tj] + bi[tj];
+        }
+    }
+    lds_barrier();
+    const bool vec_ok = (a.N % 8) == 0;
+#pragma unroll 2
+    for (int it = 0; it < 2048 / NT; it++) {  // 128 rows x 16 chunks of 8 outputs
+        const int idx = tid + NT * it;
+        const int row = idx >> 4, ch = idx & 15;
+        const int64_t mm = m0 + row, nn = n0 + ch * 8;
+        if (mm >= a.M || nn >= a.N) continue;
+        const float* tq = quarter(row >> 5) + (row & 31) * kEpiStride + ch * 8;
+        const f4 v0 = *reinterpret_cast<const f4*>(tq);
+        const f4 v1 = *reinterpret_cast<const f4*>(tq + 4);
+        float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+        const int64_t o = mm * a.N + nn;
+        if (vec_ok && nn + 8 <= a.N) {
+            if constexpr (sizeof(OT) == 2) {
+                if (a.res) {
+                    const h8 r8 = *reinterpret_cast<const h8*>(static_cast<const f16*>(a.res) + o);
+#pragma unroll
+                    for (int e = 0; e < 8; e++) v[e] += (float)r8[e];
+                }
+                h8 o8;
+#pragma unroll
+                for (int e = 0; e < 8; e++) o8[e] = (f16)v[e];
+                *reinterpret_cast<h8*>(static_cast<f16*>(a.out) + o) = o8;
+            } else {
+                if (a.res) {
+                    const f4 r0 = *reinterpret_cast<const f4*>(static_cast<const float*>(a.res) + o);
+                    const f4 r1 = *reinterpret_cast<const f4*>(static_cast<const float*>(a.res) + o + 4);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        v[e] += r0[e];
+                        v[e + 4] += r1[e];
+                    }
+                }
+                *reinterpret_cast<f4*>(static_cast<float*>(a.out) + o) = f4{v[0], v[1], v[2], v[3]};
+                *reinterpret_cast<f4*>(static_cast<float*>(a.out) + o + 4) = f4{v[4], v[5], v[6], v[7]};
+            }
+        } else {
+            for (int e = 0; e < 8 && nn + e < a.N; e++) {
+                float x = v[e];
+                if (a.res) x += ld_f(static_cast<const OT*>(a.res) + o + e);
+                st_f(static_cast<OT*>(a.out) + o + e, x);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
 static inline hipStream_t S(void* s) { return static_cast<hipStream_t>(s); }
@@ -537,8 +913,56 @@ int launch_skinny_grouped(const LinArgs* dev_table, int count, int64_t total_blo
     return (int)hipGetLastError();
 }
 
+static int g_gemm2_stages = 0;
+static int g_gemm2_layout = -1;
+
+// Tuning knobs read once: VVH_GEMM_STAGES (4 or 6, default 4) and
+// VVH_GEMM_WM (block layout: 1, 2, 4 = 4 waves with that many wave rows;
+// 12, 14 = 8 waves with 2 or 4 wave rows; default 12).
+static void gemm2_config()
+{
+    if (g_gemm2_stages == 0) {
+        const char* e = getenv("VVH_GEMM_STAGES");
+        const int v = e ? atoi(e) : 4;
+        g_gemm2_stages = v == 6 ? 6 : 4;
+        const char* l = getenv("VVH_GEMM_WM");
+        const int w = l ? atoi(l) : 12;
+        g_gemm2_layout = (w == 1 || w == 2 || w == 4 || w == 12 || w == 14) ? w : 12;
+    }
+}
+
+template <int D, int NW, int WM>
+static void gemm2_launch(const LinArgs& a, bool f32, dim3 grid, hipStream_t s)
+{
+    if (f32) hipLaunchKernelGGL((k_gemm2<float, D, NW, WM>), grid, dim3(64 * NW), 0, s, a);
+    else hipLaunchKernelGGL((k_gemm2<f16, D, NW, WM>), grid, dim3(64 * NW), 0, s, a);
+}
+
+// layout code: 1, 2, 4 = 4 waves with that many wave rows; 12, 14 = 8 waves with 2 or 4 wave rows
+template <int D>
+static void gemm2_launch_wm(const LinArgs& a, bool f32, dim3 grid, hipStream_t s, int wm)
+{
+    switch (wm) {
+        case 1: gemm2_launch<D, 4, 1>(a, f32, grid, s); break;
+        case 4: gemm2_launch<D, 4, 4>(a, f32, grid, s); break;
+        case 12: gemm2_launch<D, 8, 2>(a, f32, grid, s); break;
+        case 14: gemm2_launch<D, 8, 4>(a, f32, grid, s); break;
+        default: gemm2_launch<D, 4, 2>(a, f32, grid, s); break;
+    }
+}
+
 int launch_gemm(const LinArgs& a, int out, void* stream)
 {
+    if (a.K % kGemmBK == 0) {
+        gemm2_config();
+        const int64_t nbm = (a.M + kGemmBM - 1) / kGemmBM;
+        const int64_t nbn = (a.N + kGemmBN - 1) / kGemmBN;
+        const dim3 grid((unsigned)(nbm * nbn));
+        const bool f32 = out == VVH_F32;
+        if (g_gemm2_stages == 6) gemm2_launch_wm<6>(a, f32, grid, S(stream), g_gemm2_layout);
+        else gemm2_launch_wm<4>(a, f32, grid, S(stream), g_gemm2_layout);
+        return (int)hipGetLastError();
+    }
     const int64_t nbm = (a.M + kGemmBM - 1) / kGemmBM;
     const int64_t nbn = (a.N + kGemmBN - 1) / kGemmBN;
     const dim3 grid((unsigned)(nbm * nbn));
