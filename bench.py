@@ -160,11 +160,18 @@ class Linear:
                   self.y if self.has_res else None, self.M, self.N, self.K, self.act, self.outd, None)
 
 
-def make_plan(linears, act=F16, outd=F16):
+def make_plan(linears, act=F16, outd=F16, kernel=capi.KERNEL_AUTO):
     arr = (capi.Q8Problem * len(linears))(*[l.problem() for l in linears])
     h = ctypes.c_uint64()
-    capi.call("vvh_plan_create", arr, len(linears), act, outd, ctypes.byref(h))
+    capi.set_kernel(kernel)
+    try:
+        capi.call("vvh_plan_create", arr, len(linears), act, outd, ctypes.byref(h))
+    finally:
+        capi.set_kernel(capi.KERNEL_AUTO)
     return h.value
+
+
+KERNEL_SYMBOL = {"dot": "k_dot_grouped<f16>", "stream": "k_stream<f16>", "skinny": "k_skinny_grouped<f16>"}
 
 
 def build_decode_set(replicas, layers, projs, tmp_w, M=1):
@@ -277,13 +284,15 @@ def main():
     value = step_bytes / (ms * 1e-3) / 1e9
     launches = ctypes.c_int()
     capi.call("vvh_plan_launches", plans[0], ctypes.byref(launches))
-    print(f"[bench] grouped step {ms * 1e3:.1f} us, {value:.0f} GB/s", file=sys.stderr, flush=True)
+    kern = capi.plan_kernel(plans[0])
+    print(f"[bench] {kern} step {ms * 1e3:.1f} us, {value:.0f} GB/s", file=sys.stderr, flush=True)
 
     traffic = None
     tfile = os.path.join(ROOT, "profiles", "traffic_decode_set.json")
     if os.path.exists(tfile):
         t = json.load(open(tfile))
-        traffic = t.get("hbm_bytes_per_launch")
+        if t.get("kernel") == KERNEL_SYMBOL.get(kern):  # measured on the kernel this run uses
+            traffic = t.get("hbm_bytes_per_launch")
 
     result = {
         "metric": "linear_q8 GEMV µs + HBM GB/s at Qwen2.5-0.5B shapes; prefill GEMM TFLOPS",
@@ -303,7 +312,7 @@ def main():
                    "M": 1, "layers": L, "projections_per_step": len(sets[0][1]),
                    "algorithmic_bytes_per_step": step_bytes, "weight_replicas_rotated": args.replicas,
                    "launches_per_step": launches.value, "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "kernel": "k_skinny_grouped<f16>", "achieved": round(value, 2),
+        "roofline": {"bound": "hbm", "kernel": KERNEL_SYMBOL.get(kern, kern), "achieved": round(value, 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(value / HBM_PEAK_GBS, 4),
                      "traffic": traffic},
     }
@@ -321,6 +330,17 @@ def main():
 def extras(ev, sets, projs, tmp_w, args):
     out = {}
     L = QWEN05["layers"]
+    step_bytes = sum(l.bytes for l in sets[0][1])
+    # (0) the same grouped step with the other decode kernel families
+    for fam, kern in (("skinny", capi.KERNEL_SKINNY), ("stream", capi.KERNEL_STREAM)):
+        alt = [make_plan(lins, kernel=kern) for _, lins in sets]
+        for i in range(5):
+            capi.call("vvh_plan_run", alt[i % len(alt)], None)
+        ms = timed(ev, lambda i: capi.call("vvh_plan_run", alt[i % len(alt)], None), max(args.steps // 2, 20))
+        out[f"decode_set_{fam}"] = {"kernel": KERNEL_SYMBOL[capi.plan_kernel(alt[0])], "ms_per_step": round(ms, 5),
+                                    "GBps": round(step_bytes / (ms * 1e-3) / 1e9, 2)}
+        for h in alt:
+            capi.call("vvh_plan_destroy", h)
     # (1) model order: q/k/v grouped, o, gate+up grouped, down -> 4 launches/layer
     order_plans = []
     for _, lins in sets:
@@ -341,7 +361,6 @@ def extras(ev, sets, projs, tmp_w, args):
         model_step(i)
     reps = max(args.steps // 4, 20)
     ms = timed(ev, model_step, reps)
-    step_bytes = sum(l.bytes for l in sets[0][1])
     out["model_order"] = {"launches_per_step": 4 * L, "ms_per_step": round(ms, 5),
                           "GBps": round(step_bytes / (ms * 1e-3) / 1e9, 2)}
     print(f"[bench] model order {ms * 1e3:.1f} us", file=sys.stderr, flush=True)

@@ -206,6 +206,10 @@ VVH_API int vvh_plan_run(vvh_plan plan, void* stream);
 VVH_API int vvh_plan_destroy(vvh_plan plan);
 /* Number of kernel launches one vvh_plan_run makes. */
 VVH_API int vvh_plan_launches(vvh_plan plan, int* launches);
+/* Kernel family of a single-launch plan (VVH_KERNEL_DOT, VVH_KERNEL_STREAM
+ * or VVH_KERNEL_SKINNY), or VVH_KERNEL_AUTO for a plan run as one launch per
+ * problem. */
+VVH_API int vvh_plan_kernel(vvh_plan plan, int* kernel);
 
 /* ---- quantizer and data movement ----------------------------------------- */
 /* Device restatement of quantize_per_channel (src/quantize/quantize.cc:9-48):
@@ -235,6 +239,10 @@ typedef enum vvh_kernel {
     VVH_KERNEL_GEMV_F32 = 2,  /* fp32 activations, VALU dot products */
     VVH_KERNEL_SKINNY = 3,    /* fp16 activations, M <= 16, MFMA 16x16x32 */
     VVH_KERNEL_GEMM = 4,      /* fp16 activations, LDS-tiled MFMA 32x32x16 */
+    VVH_KERNEL_STREAM = 5,    /* fp16 activations, M <= 16, K > 448: persistent
+                                 streaming decode (large N, or grouped plans) */
+    VVH_KERNEL_DOT = 6,       /* fp16 activations, M <= 2: VALU dot products over
+                                 whole cache lines of 8 weight rows */
 } vvh_kernel;
 /* Which kernel family vvh_linear_q8 would use for this call (after the
  * override below); returns a vvh_kernel value, or a negative status. */

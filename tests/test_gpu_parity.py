@@ -155,6 +155,35 @@ def test_gemm_kernel(gpu, oracle, M, N, K, outd):
              kernel=capi.KERNEL_GEMM, seed=5 * M + N)
 
 
+@pytest.mark.parametrize("outd", [F16, F32])
+@pytest.mark.parametrize("M", [1, 2, 4, 5, 16])
+@pytest.mark.parametrize("N,K", [(1, 512), (17, 592), (130, 896), (896, 4864), (300, 1040), (4099, 768)])
+def test_stream_kernel(gpu, oracle, M, N, K, outd):
+    """Persistent streaming decode forced on shapes with K tails (592, 1040),
+    N % 16 != 0, a single tile, and the 8- and 12-deep pipelines."""
+    run_case(oracle, M, N, K, F16, outd, bias=bool(M % 2), res=["sep", "inplace", None][(M + N) % 3],
+             kernel=capi.KERNEL_STREAM, seed=11 * M + K)
+
+
+@pytest.mark.parametrize("outd", [F16, F32])
+@pytest.mark.parametrize("N,K", [(1, 16), (17, 48), (128, 896), (896, 4864), (300, 1040), (4099, 592),
+                                 (64, 20480), (33, 8960)])
+def test_dot_kernel(gpu, oracle, N, K, outd):
+    """VALU dot-product decode (M = 1): K tails (48, 592, 1040), a single
+    16-code step, N % 16 != 0, activations too large for LDS (K = 20480) and
+    the ksplit reduction (few tiles)."""
+    run_case(oracle, 1, N, K, F16, outd, bias=bool(N % 2), res=["sep", "inplace", None][(N + K) % 3],
+             kernel=capi.KERNEL_DOT, seed=13 * N + K)
+
+
+def test_decode_dispatch_on_device(gpu):
+    assert capi.kernel_choice(1, 151936, 896, F16, F32) == "dot"
+    assert capi.kernel_choice(1, 896, 896, F16, F16) == "dot"
+    assert capi.kernel_choice(4, 151936, 896, F16, F16) == "stream"
+    assert capi.kernel_choice(4, 896, 896, F16, F16) == "skinny"
+    assert capi.kernel_choice(4, 4864, 448, F16, F16) == "skinny"  # 7 k steps: too short to stream
+
+
 def test_misaligned_activations_fall_back(gpu, oracle):
     """A 2-byte-offset fp16 activation base cannot take 16-byte loads: the
     dispatcher must route it to the generic kernel and stay correct."""
@@ -254,6 +283,7 @@ def test_grouped_plan_matches_single_calls(gpu, oracle):
     n = ctypes.c_int()
     capi.call("vvh_plan_launches", plan.value, ctypes.byref(n))
     assert n.value == 1
+    assert capi.plan_kernel(plan.value) == "dot"  # every problem has M = 1
     print("[case] grouped plan run", flush=True)
     capi.call("vvh_plan_run", plan.value, None)
     capi.sync()
@@ -262,6 +292,92 @@ def test_grouped_plan_matches_single_calls(gpu, oracle):
         ref = oracle.linear_q8(x.astype(np.float32), q, s, b, None if r is None else r.astype(np.float32))
         assert np.abs(y - ref).max() / np.abs(ref).max() <= TOL_F16
     capi.call("vvh_plan_destroy", plan.value)
+
+
+def _plan_case(oracle, specs, outd, kernel, seed, expect=None):
+    """specs: list of (M, N, K, bias, res) with res in {None, "sep", "inplace"}.
+    Builds one plan under the forced kernel family, runs it twice (the second
+    run must give the same result: a plan is reusable) and checks every
+    problem against the oracle.  Returns the plan's launch count."""
+    rng = np.random.default_rng(seed)
+    probs, checks, keep = [], [], []
+    for i, (M, N, K, bias, res) in enumerate(specs):
+        q, s, b = weights(N, K, seed + i, oracle)
+        x = rng.normal(0, 1, (M, K)).astype(np.float16)
+        r = rng.normal(0, 1, (M, N)).astype(npd(outd)) if res else None
+        d = dict(q=capi.DevBuf.from_array(q), s=capi.DevBuf.from_array(s),
+                 b=capi.DevBuf.from_array(b) if bias else None, x=capi.DevBuf.from_array(x),
+                 r=capi.DevBuf.from_array(r) if res == "sep" else None)
+        d["y"] = capi.DevBuf.from_array(r) if res == "inplace" else capi.DevBuf(M * N * np.dtype(npd(outd)).itemsize)
+        keep.append(d)
+        resid = d["y"].ptr if res == "inplace" else (d["r"].ptr if res == "sep" else None)
+        probs.append(capi.Q8Problem(out=d["y"].ptr, inp=d["x"].ptr, residual=resid, weight=d["q"].ptr,
+                                    scales=d["s"].ptr, bias=d["b"].ptr if bias else None, M=M, N=N, K=K))
+        checks.append((d, x, q, s, b if bias else None, r, M, N, res))
+    arr = (capi.Q8Problem * len(probs))(*probs)
+    plan = ctypes.c_uint64()
+    capi.set_kernel(kernel)
+    try:
+        capi.call("vvh_plan_create", arr, len(probs), F16, outd, ctypes.byref(plan))
+    finally:
+        capi.set_kernel(capi.KERNEL_AUTO)
+    n = ctypes.c_int()
+    capi.call("vvh_plan_launches", plan.value, ctypes.byref(n))
+    assert capi.plan_kernel(plan.value) == (expect or capi.KERNEL_NAMES[kernel])
+    for rep in range(2):
+        for d, x, q, s, b, r, M, N, res in checks:
+            if res == "inplace":  # restore the residual the previous run overwrote
+                capi.call("vvh_memcpy_h2d", d["y"].ptr, r.ctypes.data, r.nbytes)
+        print(f"[case] plan run {rep} kernel={capi.KERNEL_NAMES[kernel]} problems={len(specs)}", flush=True)
+        capi.call("vvh_plan_run", plan.value, None)
+        capi.sync()
+        for d, x, q, s, b, r, M, N, res in checks:
+            y = d["y"].to_array(npd(outd), (M, N)).astype(np.float32)
+            ref = oracle.linear_q8(x.astype(np.float32), q, s, b, None if r is None else r.astype(np.float32))
+            err = np.abs(y - ref).max() / np.abs(ref).max()
+            assert err <= TOL_F16, (M, N, res, err)
+    capi.call("vvh_plan_destroy", plan.value)
+    return n.value
+
+
+MIXED_PLAN = [(1, 896, 896, True, None), (1, 128, 896, True, None), (3, 130, 592, False, "sep"),
+              (16, 300, 1040, True, "inplace"), (1, 896, 4864, False, "inplace"), (5, 17, 768, False, None),
+              (1, 4864, 896, False, None), (2, 1, 512, True, "sep")]
+
+
+@pytest.mark.parametrize("outd", [F16, F32])
+@pytest.mark.parametrize("kernel", [capi.KERNEL_STREAM, capi.KERNEL_SKINNY], ids=["stream", "skinny_grouped"])
+def test_mixed_plan_single_launch(gpu, oracle, kernel, outd):
+    """Problems of different M, N, K, bias and residual forms in one launch of
+    either decode kernel family."""
+    assert _plan_case(oracle, MIXED_PLAN, outd, kernel, seed=300) == 1
+
+
+DOT_PLAN = [(1, 896, 896, True, None), (1, 128, 896, True, None), (1, 130, 592, False, "sep"),
+            (1, 300, 1040, True, "inplace"), (1, 896, 4864, False, "inplace"), (1, 17, 48, False, None),
+            (1, 4864, 896, False, None), (1, 1, 512, True, "sep")]
+
+
+@pytest.mark.parametrize("outd", [F16, F32])
+def test_dot_plan_single_launch(gpu, oracle, outd):
+    assert _plan_case(oracle, DOT_PLAN, outd, capi.KERNEL_AUTO, seed=500, expect="dot") == 1
+
+
+def test_dot_plan_without_lds_activations(gpu, oracle):
+    """One problem's activations do not fit the block's LDS: the whole plan
+    reads activations through the caches."""
+    specs = DOT_PLAN[:4] + [(1, 64, 20480, True, "inplace")]
+    assert _plan_case(oracle, specs, F16, capi.KERNEL_AUTO, seed=600, expect="dot") == 1
+
+
+def test_plan_with_short_rows_is_not_streamed(gpu, oracle):
+    """K = 256 (4 k steps) cannot fill the streaming pipeline.  Automatic
+    dispatch runs such a plan as one k_skinny_grouped launch; with the
+    streaming family forced, the short problem falls back to the generic
+    kernel and the plan runs one launch per problem."""
+    specs = [(2, 896, 256, True, None), (1, 4864, 896, False, None)]
+    assert _plan_case(oracle, specs, F16, capi.KERNEL_AUTO, seed=400, expect="skinny") == 1
+    assert _plan_case(oracle, specs, F16, capi.KERNEL_STREAM, seed=400, expect="auto") == 2
 
 
 def test_plan_with_prefill_problem_runs_per_call(gpu, oracle):

@@ -16,8 +16,8 @@ import numpy as np
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libvvllm_hip.so")
 
 F32, F16 = 0, 1
-KERNEL_AUTO, KERNEL_GENERIC, KERNEL_GEMV_F32, KERNEL_SKINNY, KERNEL_GEMM = range(5)
-KERNEL_NAMES = {0: "auto", 1: "generic", 2: "gemv_f32", 3: "skinny", 4: "gemm"}
+KERNEL_AUTO, KERNEL_GENERIC, KERNEL_GEMV_F32, KERNEL_SKINNY, KERNEL_GEMM, KERNEL_STREAM, KERNEL_DOT = range(7)
+KERNEL_NAMES = {0: "auto", 1: "generic", 2: "gemv_f32", 3: "skinny", 4: "gemm", 5: "stream", 6: "dot"}
 STATUS = {0: "VVH_OK", 1: "VVH_ERR_INVALID_ARG", 2: "VVH_ERR_NO_DEVICE", 3: "VVH_ERR_OUT_OF_MEMORY",
           4: "VVH_ERR_HIP", 5: "VVH_ERR_NOT_INITIALIZED", 6: "VVH_ERR_UNKNOWN_HANDLE",
           7: "VVH_ERR_UNSUPPORTED"}
@@ -67,6 +67,7 @@ SIGNATURES = {
     "vvh_plan_run": (c_int, [c_uint64, c_void_p]),
     "vvh_plan_destroy": (c_int, [c_uint64]),
     "vvh_plan_launches": (c_int, [c_uint64, POINTER(c_int)]),
+    "vvh_plan_kernel": (c_int, [c_uint64, POINTER(c_int)]),
     "vvh_quantize_per_channel": (c_int, [c_void_p, c_size_t, c_size_t, c_void_p, c_void_p, c_void_p]),
     "vvh_convert": (c_int, [c_void_p, c_int, c_void_p, c_int, c_size_t, c_void_p]),
     "vvh_fill_normal": (c_int, [c_void_p, c_int, c_size_t, c_uint64, c_float, c_float, c_void_p]),
@@ -190,3 +191,9 @@ def kernel_choice(M, N, K, act, outd) -> str:
 
 def sync() -> None:
     call("vvh_sync")
+
+
+def plan_kernel(plan: int) -> str:
+    k = c_int()
+    call("vvh_plan_kernel", plan, ctypes.byref(k))
+    return KERNEL_NAMES.get(k.value, "?")

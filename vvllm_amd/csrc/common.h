@@ -24,7 +24,30 @@ struct LinArgs {
     int64_t M, N, K;
     int32_t ksplit;           // decode kernels: waves cooperating on one 16-row tile (1, 2, 4)
     int32_t block_begin;      // grouped launch: first block of this problem
+    int64_t tile_begin;       // streaming plan: first global 16-row tile of this problem
 };
+
+// Persistent streaming decode launch (k_stream).  Work is a sequence of
+// 16-row tiles (one tile = 16 output channels x the full K).  Every wave
+// walks its own tiles, keeping a fixed number of weight loads in flight
+// across tile boundaries.
+//   mode kStreamRange: one problem (`one`); wave w takes the contiguous
+//                      tiles [T*w/W, T*(w+1)/W).
+//   mode kStreamList:  a plan; wave w takes the global tiles
+//                      list[list_off[w] .. list_off[w+1]), and
+//                      tile_prob[g] is the problem of global tile g.
+struct StreamArgs {
+    LinArgs one;
+    const LinArgs* table;
+    const int32_t* tile_prob;
+    const int32_t* list;
+    const int32_t* list_off;
+    int64_t total_tiles;
+    int32_t waves;
+    int32_t mode;
+};
+constexpr int kStreamRange = 0;
+constexpr int kStreamList = 1;
 
 // Kernel families (values match vvh_kernel).
 enum Kernel : int {
@@ -33,6 +56,8 @@ enum Kernel : int {
     K_GEMV_F32 = VVH_KERNEL_GEMV_F32,
     K_SKINNY = VVH_KERNEL_SKINNY,
     K_GEMM = VVH_KERNEL_GEMM,
+    K_STREAM = VVH_KERNEL_STREAM,
+    K_DOT = VVH_KERNEL_DOT,
 };
 
 // Largest M served by the decode kernels.
@@ -50,6 +75,28 @@ inline int64_t decode_blocks(const LinArgs& a)
     return (tiles + tiles_per_block - 1) / tiles_per_block;
 }
 
+// k_dot (M <= 2): 16-row tiles, 128-wide k steps, ksplit waves per tile.
+constexpr int64_t kDotMaxM = 1;
+constexpr int kDotStep = 128;   // k codes per row per step
+constexpr int64_t kDotLdsMax = 40 * 1024;   // dynamic LDS of one block at most
+constexpr int64_t kDotRedBytes = 4 * 2 * 16 * 4;
+inline int64_t dot_blocks(const LinArgs& a)
+{
+    const int64_t tiles = (a.N + kDecodeTileN - 1) / kDecodeTileN;
+    const int64_t tiles_per_block = 4 / a.ksplit;
+    return (tiles + tiles_per_block - 1) / tiles_per_block;
+}
+// Activations are staged in LDS when M rows of K + 8 halves fit beside the
+// reduction scratch; the launcher and the kernel both use this rule.
+inline __host__ __device__ bool dot_x_in_lds(int64_t M, int64_t K)
+{
+    return kDotRedBytes + M * (K + 8) * 2 <= kDotLdsMax;
+}
+inline __host__ __device__ int64_t dot_lds_bytes(int64_t M, int64_t K)
+{
+    return kDotRedBytes + (dot_x_in_lds(M, K) ? M * (K + 8) * 2 : 0);
+}
+
 // GEMM tile shape.
 constexpr int kGemmBM = 128;
 constexpr int kGemmBN = 128;
@@ -61,7 +108,15 @@ int launch_gemv_f32(const LinArgs& a, int out, void* stream);
 int launch_skinny(const LinArgs& a, int out, void* stream);
 int launch_skinny_grouped(const LinArgs* dev_table, int count, int64_t total_blocks, int out,
                           void* stream);
+int launch_dot(const LinArgs& a, int out, void* stream);
+// dev_block_prob[b] = problem of block b; x_in_lds: dot_x_in_lds holds for
+// every problem; lds_bytes = the largest dot_lds_bytes of the problems
+int launch_dot_grouped(const LinArgs* dev_table, const int32_t* dev_block_prob, int64_t total_blocks, int max_m,
+                       bool x_in_lds, size_t lds_bytes, int out, void* stream);
 int launch_gemm(const LinArgs& a, int out, void* stream);
+// depth = weight loads in flight per lane (8 or 12); every problem must have
+// at least `depth` 64-wide k steps.  max_m = largest M of the launch.
+int launch_stream(const StreamArgs& s, int depth, int max_m, int out, int64_t blocks, void* stream);
 
 // Auxiliary kernels (aux_kernels.hip).
 int launch_quantize(const float* w, int64_t N, int64_t K, int8_t* q, float* scales, void* stream);

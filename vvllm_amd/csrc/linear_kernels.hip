@@ -106,6 +106,38 @@ __device__ __forceinline__ u4 ld_stream(const int8_t* p)
     return __builtin_nontemporal_load(reinterpret_cast<const u4*>(p));
 }
 
+// Pointers read from memory (plan tables) are generic to the compiler, which
+// then emits flat loads; those count in lgkmcnt as well as vmcnt, so every
+// wait on a scalar load would also drain the weight stream.  Kernels that
+// take their pointers from tables cast them to the global address space.
+#define VVH_GLOBAL __attribute__((address_space(1)))
+template <typename T>
+__device__ __forceinline__ const VVH_GLOBAL T* gbl(const T* p)
+{
+    return (const VVH_GLOBAL T*)p;
+}
+template <typename T>
+__device__ __forceinline__ VVH_GLOBAL T* gbl(T* p)
+{
+    return (VVH_GLOBAL T*)p;
+}
+__device__ __forceinline__ u4 ld_stream_g(const int8_t* p)
+{
+    return __builtin_nontemporal_load(gbl(reinterpret_cast<const u4*>(p)));
+}
+
+// Plan tables are read-only for the whole launch.  Reading them through the
+// constant address space lets the compiler use scalar loads (lgkmcnt) even
+// though the kernel stores to global memory; otherwise it cannot rule out
+// aliasing and reads them with vector loads that join the weight stream's
+// vmcnt queue.
+#define VVH_CONST __attribute__((address_space(4)))
+template <typename T>
+__device__ __forceinline__ const VVH_CONST T* cst(const T* p)
+{
+    return (const VVH_CONST T*)p;
+}
+
 // ---------------------------------------------------------------------------
 // generic: any M, N, K, alignment, dtypes.  One thread per output element.
 // ---------------------------------------------------------------------------
@@ -141,7 +173,7 @@ __device__ __forceinline__ DecodeCoord decode_coord(const LinArgs& a, int64_t bl
 {
     DecodeCoord c;
     c.lane = threadIdx.x & 63;
-    c.wave = threadIdx.x >> 6;
+    c.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: keeps the loops scalar
     c.ksplit = a.ksplit;
     c.ks = c.wave % c.ksplit;
     c.tile = block * (4 / c.ksplit) + c.wave / c.ksplit;
@@ -392,6 +424,476 @@ __global__ __launch_bounds__(256) void k_skinny_grouped(const LinArgs* __restric
     const LinArgs a = table[lo];
     if (decode_x_in_lds(a)) skinny_body<OT, true>(a, b - a.block_begin, sh);
     else skinny_body<OT, false>(a, b - a.block_begin, sh);
+}
+
+// ---------------------------------------------------------------------------
+// k_dot: fp16 activations, M <= 2, VALU dot products.
+//
+// The weight stream decides the speed of a decode GEMV, and it runs fastest
+// when every load instruction covers whole 128-byte cache lines: 8 rows x
+// 128 B per instruction streams about 7 TB/s on MI355X, the 16 rows x 64 B
+// that a 16x16 MFMA operand needs about 5.5 TB/s.  So at M <= 2, where the
+// MFMA's M side would be mostly empty anyway, each wave owns a 16-row tile
+// and lane l reads the 16-byte chunk c = l%8 of the 128-byte k step of rows
+// r = l/8 and r + 8 (two loads per step), converts the codes exactly to fp16
+// and accumulates v_dot2_f32_f16 products in fp32.  The 8 lanes of a row are
+// summed with a butterfly at the end.  Activations are staged once per
+// block in LDS (a broadcast read: the 8 rows of a wave read the same 8
+// chunks), or read through the caches when they do not fit.
+//
+// Tiles and k steps are shared out as for k_skinny (decode_coord with
+// 128-wide steps).  Every weight load is issued unconditionally (steps past
+// the wave's range re-read its last step, chunks past K read inside the row)
+// and masked when consumed, so the wait counts of the pipeline are fixed.
+// ---------------------------------------------------------------------------
+constexpr int kDotDepth = 8;    // k steps (2 loads each) in flight per wave
+
+__device__ __forceinline__ DecodeCoord dot_coord(const LinArgs& a, int64_t block)
+{
+    DecodeCoord c;
+    c.lane = threadIdx.x & 63;
+    c.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: keeps the loops scalar
+    c.ksplit = a.ksplit;
+    c.ks = c.wave % c.ksplit;
+    c.tile = block * (4 / c.ksplit) + c.wave / c.ksplit;
+    const int64_t steps = (a.K + kDotStep - 1) / kDotStep;
+    const int64_t per = (steps + c.ksplit - 1) / c.ksplit;
+    c.s0 = c.ks * per < steps ? c.ks * per : steps;
+    c.s1 = c.s0 + per < steps ? c.s0 + per : steps;
+    return c;
+}
+
+// LDS of one k_dot block: the ksplit partial sums of the 16 rows of each
+// wave, then (when they fit) the staged activations, M rows with a row
+// stride of K + 8 halves.  The launcher sizes the dynamic LDS with the same
+// rule (dot_lds_bytes), so kernel and launcher agree on where x lives.
+struct DotRed {
+    float v[4][2][16];  // [wave][m][row]
+};
+
+// 16 fp16 activations times 16 exact fp16 codes, accumulated in fp32.
+__device__ __forceinline__ float dot16(const h8 w0, const h8 w1, const h8 x0, const h8 x1, float acc)
+{
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+        acc = __builtin_amdgcn_fdot2(h2{w0[2 * j], w0[2 * j + 1]}, h2{x0[2 * j], x0[2 * j + 1]}, acc, false);
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+        acc = __builtin_amdgcn_fdot2(h2{w1[2 * j], w1[2 * j + 1]}, h2{x1[2 * j], x1[2 * j + 1]}, acc, false);
+    return acc;
+}
+
+// Epilogue of one element through global-address-space pointers (the
+// problem descriptor may come from a plan table, whose pointers the compiler
+// would otherwise treat as generic and access with flat instructions).
+template <typename OT>
+__device__ __forceinline__ void store_out_g(const LinArgs& a, int64_t m, int64_t n, float acc)
+{
+    float v = acc * *gbl(a.scales + n);
+    if (a.bias) v += *gbl(a.bias + n);
+    const int64_t o = m * a.N + n;
+    if (a.res) v += (float)*gbl(static_cast<const OT*>(a.res) + o);
+    *gbl(static_cast<OT*>(a.out) + o) = (OT)v;
+}
+
+template <typename OT, int MT, bool XLDS>
+__device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* smem)
+{
+    constexpr int D = kDotDepth;
+    DotRed& red = *reinterpret_cast<DotRed*>(smem);
+    f16* xs = reinterpret_cast<f16*>(smem + kDotRedBytes);
+    const DecodeCoord c = dot_coord(a, block);
+    const int r = c.lane >> 3, ch = c.lane & 7;
+    const int64_t n0 = c.tile * kDecodeTileN;
+    const bool active = n0 < a.N && c.s0 < c.s1;
+    const int64_t rowA = n0 + r < a.N ? n0 + r : a.N - 1;
+    const int64_t rowB = n0 + 8 + r < a.N ? n0 + 8 + r : a.N - 1;
+    const int8_t* wpA = a.w + rowA * a.K;
+    const int8_t* wpB = a.w + rowB * a.K;
+    const int32_t kmax = (int32_t)a.K - 16;  // last valid chunk start of a row
+    const int32_t s1 = (int32_t)c.s1;
+    const int64_t ldx = a.K + 8;
+    const f16* xg = static_cast<const f16*>(a.inp);
+
+    // Ring of D slots, one k step each: the two weight chunks of the step
+    // and, when the activations are not in LDS, their activation chunks
+    // (loaded with the weights, so consuming a slot never waits on a younger
+    // load).  Slot u is consumed, then refilled with the step D ahead.
+    struct Slot {
+        u4 w[2];
+        h8 x[XLDS ? 1 : MT][2];
+    };
+    Slot ring[D];
+    auto issue = [&](int u, int32_t st) {
+        st = st < s1 ? st : s1 - 1;  // past the range: re-read the last step
+        int32_t k = st * kDotStep + ch * 16;
+        k = k < kmax ? k : kmax;
+        ring[u].w[0] = ld_stream_g(wpA + k);
+        ring[u].w[1] = ld_stream_g(wpB + k);
+        if (!XLDS) {
+#pragma unroll
+            for (int m = 0; m < MT; m++) {
+                const f16* xp = xg + (m < a.M ? m : 0) * a.K + k;
+                ring[u].x[m][0] = *gbl(reinterpret_cast<const h8*>(xp));
+                ring[u].x[m][1] = *gbl(reinterpret_cast<const h8*>(xp + 8));
+            }
+        }
+    };
+    float accA[MT], accB[MT];
+#pragma unroll
+    for (int m = 0; m < MT; m++) accA[m] = accB[m] = 0.0f;
+    // No branches in here: a conditional read would split the slot into
+    // basic blocks, the dot products would sink below the refills and the
+    // ring would need a second register copy.  The activation read is
+    // clamped into the row and masked instead.
+    const h8 zero8 = {};
+    auto consume = [&](int u, int32_t st) {
+        int32_t k = st * kDotStep + ch * 16;
+        const bool kv = k < a.K;
+        k = k < kmax ? k : kmax;
+        h8 a0, a1, b0, b1;
+        i8x16_to_h8x2(ring[u].w[0], a0, a1);
+        i8x16_to_h8x2(ring[u].w[1], b0, b1);
+#pragma unroll
+        for (int m = 0; m < MT; m++) {
+            h8 x0, x1;
+            if (XLDS) {
+                const int mr = m < a.M ? m : 0;
+                x0 = *reinterpret_cast<const h8*>(xs + mr * ldx + k);
+                x1 = *reinterpret_cast<const h8*>(xs + mr * ldx + k + 8);
+            } else {
+                x0 = ring[u].x[m][0];
+                x1 = ring[u].x[m][1];
+            }
+            const bool xv = kv && m < a.M;
+            x0 = xv ? x0 : zero8;
+            x1 = xv ? x1 : zero8;
+            accA[m] = dot16(a0, a1, x0, x1, accA[m]);
+            accB[m] = dot16(b0, b1, x0, x1, accB[m]);
+        }
+    };
+
+    if (XLDS) {
+        // activations to LDS, 4 chunks of 16 bytes per thread per round
+        const int64_t xchunks = a.M * a.K / 8;
+        constexpr int XL = 4;
+        int64_t base = 0;
+        for (; base + 256 * XL <= xchunks; base += 256 * XL) {
+            u4 xr[XL];
+#pragma unroll
+            for (int i = 0; i < XL; i++) xr[i] = *gbl(reinterpret_cast<const u4*>(xg + (base + threadIdx.x + 256 * i) * 8));
+#pragma unroll
+            for (int i = 0; i < XL; i++) {
+                const int64_t e = (base + threadIdx.x + 256 * i) * 8, row = e / a.K, col = e - row * a.K;
+                *reinterpret_cast<u4*>(xs + row * ldx + col) = xr[i];
+            }
+        }
+        for (int64_t idx = base + threadIdx.x; idx < xchunks; idx += 256) {
+            const int64_t e = idx * 8, row = e / a.K, col = e - row * a.K;
+            *reinterpret_cast<u4*>(xs + row * ldx + col) = *gbl(reinterpret_cast<const u4*>(xg + e));
+        }
+        __syncthreads();
+    }
+
+    if (active) {
+        int32_t s = (int32_t)c.s0;
+#pragma unroll
+        for (int u = 0; u < D; u++) issue(u, s + u);
+        // while steps remain beyond the ring: consume slot u, refill it with
+        // the step D ahead (a refill past the range re-reads the last step,
+        // so every wait in the loop counts the same D - 1 steps of loads)
+        // (the scheduling barrier keeps each refill below the last read of
+        // its slot: hoisted above it, the refill would land in other
+        // registers that must be copied back at the loop edge, and those
+        // copies wait for every outstanding load)
+        for (; s + D < s1; s += D) {
+#pragma unroll
+            for (int u = 0; u < D; u++) {
+                consume(u, s + u);
+                __builtin_amdgcn_sched_barrier(0);
+                issue(u, s + u + D);
+            }
+        }
+        // the ring holds the last steps s .. s1 - 1 (at most D)
+#pragma unroll
+        for (int u = 0; u < D; u++) {
+            if (s + u < s1) consume(u, s + u);
+        }
+    }
+    // sum the 8 chunk lanes of each row
+#pragma unroll
+    for (int m = 0; m < MT; m++) {
+#pragma unroll
+        for (int off = 1; off < 8; off <<= 1) {
+            accA[m] += __shfl_xor(accA[m], off);
+            accB[m] += __shfl_xor(accB[m], off);
+        }
+    }
+    if (c.ksplit > 1) {
+        if (ch == 0) {
+#pragma unroll
+            for (int m = 0; m < MT; m++) {
+                red.v[c.wave][m][r] = accA[m];
+                red.v[c.wave][m][8 + r] = accB[m];
+            }
+        }
+        __syncthreads();
+        if (c.ks == 0) {
+            for (int j = 1; j < c.ksplit; j++) {
+#pragma unroll
+                for (int m = 0; m < MT; m++) {
+                    accA[m] += red.v[c.wave + j][m][r];
+                    accB[m] += red.v[c.wave + j][m][8 + r];
+                }
+            }
+        }
+    }
+    if (c.ks == 0 && ch == 0 && n0 < a.N) {
+#pragma unroll
+        for (int m = 0; m < MT; m++) {
+            if (m < a.M) {
+                if (n0 + r < a.N) store_out_g<OT>(a, m, n0 + r, accA[m]);
+                if (n0 + 8 + r < a.N) store_out_g<OT>(a, m, n0 + 8 + r, accB[m]);
+            }
+        }
+    }
+}
+
+// XLDS = the activations are staged in LDS (dot_x_in_lds, decided on the
+// host for the launch: for a grouped launch it must hold for every problem).
+template <typename OT, int MT, bool XLDS>
+__global__ __launch_bounds__(256) void k_dot(LinArgs a)
+{
+    extern __shared__ __attribute__((aligned(16))) char dot_smem[];
+    dot_body<OT, MT, XLDS>(a, blockIdx.x, dot_smem);
+}
+
+// Grouped launch: block b serves problem block_prob[b].
+template <typename OT, int MT, bool XLDS>
+__global__ __launch_bounds__(256) void k_dot_grouped(const LinArgs* __restrict__ table,
+                                                     const int32_t* __restrict__ block_prob)
+{
+    extern __shared__ __attribute__((aligned(16))) char dot_smem[];
+    const int b = blockIdx.x;
+    const int p = *cst(block_prob + b);
+    const LinArgs a = table[p];
+    dot_body<OT, MT, XLDS>(a, b - a.block_begin, dot_smem);
+}
+
+// ---------------------------------------------------------------------------
+// k_stream: persistent streaming decode, fp16 activations, M <= 16.
+//
+// Same per-step arithmetic as k_skinny (a 16-row tile, lane l streams 16
+// codes of row n0 + l%16 at k = 64s + 16(l/16), two v_mfma_f32_16x16x32_f16
+// per 64-wide step), but the work is organised for the HBM stream:
+//   - each wave is independent (no LDS, no barriers) and walks a list of
+//     tiles (StreamArgs), so a launch is about 8 resident waves per CU that
+//     each stream a long run of weights;
+//   - a ring of D register slots keeps D 16-byte weight loads per lane in
+//     flight at all times, across tile boundaries: slot u is consumed, then
+//     refilled with the step D positions ahead, which may belong to the
+//     next tile;
+//   - the activation fragment of a step is loaded into the same slot as its
+//     weights (lanes whose row m >= M load nothing), and the epilogue
+//     operands of a tile (scale, bias, residual) are loaded when the issue
+//     side enters the tile, so no load is ever waited on before the loads
+//     issued ahead of it have landed anyway.
+// Every problem has nsteps = ceil(K/64) >= D, so the issue side is at most
+// one tile ahead of the consume side: two tile descriptors suffice.
+// ---------------------------------------------------------------------------
+struct StreamTile {
+    const int8_t* w;
+    const f16* x;
+    const float* sc;
+    const float* bi;
+    const void* res;
+    void* out;
+    int64_t M, N, K, n0;
+    int32_t nsteps;
+};
+
+template <bool ONE>
+__device__ __forceinline__ void stream_tile(const StreamArgs& sa, int64_t g, StreamTile& t)
+{
+    LinArgs A;
+    int64_t lt;
+    if (ONE) {
+        A = sa.one;
+        lt = g;
+    } else {
+        const int p = *cst(sa.tile_prob + g);
+        const VVH_CONST LinArgs* ap = cst(sa.table) + p;
+        A.w = ap->w;
+        A.inp = ap->inp;
+        A.scales = ap->scales;
+        A.bias = ap->bias;
+        A.res = ap->res;
+        A.out = ap->out;
+        A.M = ap->M;
+        A.N = ap->N;
+        A.K = ap->K;
+        lt = g - ap->tile_begin;
+    }
+    t.w = A.w;
+    t.x = static_cast<const f16*>(A.inp);
+    t.sc = A.scales;
+    t.bi = A.bias;
+    t.res = A.res;
+    t.out = A.out;
+    t.M = A.M;
+    t.N = A.N;
+    t.K = A.K;
+    t.n0 = lt * kDecodeTileN;
+    t.nsteps = (int32_t)((A.K + 63) / 64);
+}
+
+// Epilogue operands of one step for this lane (channel n0 + l%16, rows
+// 4(l/16) + r, r < MR), loaded in the same ring slot as the step's weights
+// and kept as loaded (converting a residual right after its load would wait
+// on it).  Only the last step of a tile uses them, but loading them for every
+// step keeps the number of vector memory operations per slot fixed: every
+// static s_waitcnt in the loop then counts about D slots of loads, whatever
+// path the wave takes at tile boundaries.  Every load reads an in-bounds
+// address (channel clamped to N-1, row to 0, absent bias or residual read
+// from the scales) and is masked in the epilogue.
+template <typename OT, int MR>
+struct StreamEpi {
+    float sc, bi;
+    OT res[MR];
+};
+
+template <typename OT, int MR>
+__device__ __forceinline__ void stream_epi_store(const StreamTile& t, int lane, const StreamEpi<OT, MR>& e, f4 acc)
+{
+    const int64_t n = t.n0 + (lane & 15);
+    if (n >= t.N) return;
+    const float bi = t.bi ? e.bi : 0.0f;
+#pragma unroll
+    for (int r = 0; r < MR; r++) {
+        const int64_t m = 4 * (lane >> 4) + r;
+        if (m < t.M) {
+            const float rv = t.res ? (float)e.res[r] : 0.0f;
+            *gbl(static_cast<OT*>(t.out) + m * t.N + n) = (OT)(acc[r] * e.sc + bi + rv);
+        }
+    }
+}
+
+// MR = residual rows per lane: 1 when every problem has M == 1 (only lanes
+// 0-15 hold a valid row), else 4.
+template <typename OT, int D, bool ONE, int MR>
+__global__ __launch_bounds__(256, 2) void k_stream(const StreamArgs sa)
+{
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)((blockIdx.x * 256u + threadIdx.x) >> 6));
+    if (wave >= sa.waves) return;
+    const int r16 = lane & 15, chunk = lane >> 4;
+
+    int64_t pos, end;
+    if (sa.mode == kStreamRange) {
+        pos = sa.total_tiles * wave / sa.waves;
+        end = sa.total_tiles * (wave + 1) / sa.waves;
+    } else {
+        pos = *cst(sa.list_off + wave);
+        end = *cst(sa.list_off + wave + 1);
+    }
+    auto next_tile = [&]() -> int64_t {
+        if (pos >= end) return -1;
+        const int64_t g = sa.mode == kStreamRange ? pos : (int64_t)*cst(sa.list + pos);
+        pos++;
+        return g;
+    };
+
+    u4 sw[D];
+    h8 sxa[D], sxb[D];
+    StreamEpi<OT, MR> se[D];
+    // per-lane issue pointers of the issue tile; the chunk offset is clamped
+    // so that the k tail of a K % 64 != 0 row still reads inside the row
+    const int8_t* iwp;
+    const f16* ixp;
+    const float *iscp, *ibip;
+    const OT* irp[MR];
+    int64_t ikmax;  // last valid 16-element chunk start of a row
+    auto issue_setup = [&](const StreamTile& t) {
+        const int64_t nc = t.n0 + r16 < t.N ? t.n0 + r16 : t.N - 1;
+        iwp = t.w + nc * t.K;
+        ixp = t.x + (r16 < t.M ? r16 : 0) * t.K;
+        ikmax = t.K - 16;
+        iscp = t.sc + nc;
+        ibip = (t.bi ? t.bi : t.sc) + nc;
+#pragma unroll
+        for (int r = 0; r < MR; r++) {
+            const int64_t m = 4 * chunk + r;
+            irp[r] = t.res ? static_cast<const OT*>(t.res) + (m < t.M ? m : 0) * t.N + nc
+                           : reinterpret_cast<const OT*>(t.sc);
+        }
+    };
+    auto issue = [&](int u, int64_t s) {
+        int64_t k = s * 64 + chunk * 16;
+        k = k < ikmax ? k : ikmax;
+        sw[u] = ld_stream_g(iwp + k);
+        sxa[u] = *gbl(reinterpret_cast<const h8*>(ixp + k));
+        sxb[u] = *gbl(reinterpret_cast<const h8*>(ixp + k + 8));
+        se[u].sc = *gbl(iscp);
+        se[u].bi = *gbl(ibip);
+#pragma unroll
+        for (int r = 0; r < MR; r++) se[u].res[r] = *gbl(irp[r]);
+    };
+
+    StreamTile cT, iT;
+    bool has_n = false;   // the issue side is in the tile after cT
+    bool idone = false;   // no tile left: the issue side re-reads its last step
+    int32_t cs = 0, is = 0;
+
+    const int64_t g0 = next_tile();
+    if (g0 < 0) return;
+    stream_tile<ONE>(sa, g0, cT);
+    iT = cT;
+    issue_setup(iT);
+
+    auto advance_issue = [&]() {
+        const int64_t g = next_tile();
+        if (g < 0) {
+            idone = true;
+            is = iT.nsteps - 1;
+            return;
+        }
+        stream_tile<ONE>(sa, g, iT);
+        issue_setup(iT);
+        has_n = true;
+        is = 0;
+    };
+
+#pragma unroll
+    for (int u = 0; u < D; u++) issue(u, is++);
+    if (is == iT.nsteps) advance_issue();
+
+    f4 acc0 = {0.f, 0.f, 0.f, 0.f};
+    f4 acc1 = {0.f, 0.f, 0.f, 0.f};
+    const h8 zero8 = {};
+    for (;;) {
+#pragma unroll
+        for (int u = 0; u < D; u++) {
+            {
+                // rows m >= M and the k tail beyond K contribute zero
+                const bool xv = r16 < cT.M && (int64_t)cs * 64 + chunk * 16 < cT.K;
+                h8 b0, b1;
+                i8x16_to_h8x2(sw[u], b0, b1);
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv ? sxa[u] : zero8, b0, acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv ? sxb[u] : zero8, b1, acc1, 0, 0, 0);
+            }
+            if (++cs == cT.nsteps) {
+                stream_epi_store<OT, MR>(cT, lane, se[u], acc0 + acc1);
+                if (!has_n) return;
+                cT = iT;
+                has_n = false;
+                cs = 0;
+                acc0 = f4{0.f, 0.f, 0.f, 0.f};
+                acc1 = f4{0.f, 0.f, 0.f, 0.f};
+            }
+            issue(u, is);
+            if (!idone && ++is == iT.nsteps) advance_issue();
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -910,6 +1412,77 @@ int launch_skinny_grouped(const LinArgs* dev_table, int count, int64_t total_blo
     const dim3 grid((unsigned)total_blocks);
     if (out == VVH_F32) hipLaunchKernelGGL((k_skinny_grouped<float>), grid, dim3(256), 0, S(stream), dev_table, count);
     else hipLaunchKernelGGL((k_skinny_grouped<f16>), grid, dim3(256), 0, S(stream), dev_table, count);
+    return (int)hipGetLastError();
+}
+
+template <int MT, bool XLDS>
+static void dot_launch(const LinArgs& a, int out, dim3 grid, size_t lds, hipStream_t s)
+{
+    if (out == VVH_F32) hipLaunchKernelGGL((k_dot<float, MT, XLDS>), grid, dim3(256), lds, s, a);
+    else hipLaunchKernelGGL((k_dot<f16, MT, XLDS>), grid, dim3(256), lds, s, a);
+}
+
+int launch_dot(const LinArgs& a, int out, void* stream)
+{
+    const dim3 grid((unsigned)dot_blocks(a));
+    const size_t lds = dot_lds_bytes(a.M, a.K);
+    const bool xl = dot_x_in_lds(a.M, a.K);
+    if (a.M <= 1) {
+        if (xl) dot_launch<1, true>(a, out, grid, lds, S(stream));
+        else dot_launch<1, false>(a, out, grid, lds, S(stream));
+    } else {
+        if (xl) dot_launch<2, true>(a, out, grid, lds, S(stream));
+        else dot_launch<2, false>(a, out, grid, lds, S(stream));
+    }
+    return (int)hipGetLastError();
+}
+
+template <int MT, bool XLDS>
+static void dot_grouped_launch(const LinArgs* table, const int32_t* block_prob, int out, dim3 grid, size_t lds,
+                               hipStream_t s)
+{
+    if (out == VVH_F32) hipLaunchKernelGGL((k_dot_grouped<float, MT, XLDS>), grid, dim3(256), lds, s, table, block_prob);
+    else hipLaunchKernelGGL((k_dot_grouped<f16, MT, XLDS>), grid, dim3(256), lds, s, table, block_prob);
+}
+
+int launch_dot_grouped(const LinArgs* dev_table, const int32_t* dev_block_prob, int64_t total_blocks, int max_m,
+                       bool x_in_lds, size_t lds_bytes, int out, void* stream)
+{
+    const dim3 grid((unsigned)total_blocks);
+    if (max_m <= 1) {
+        if (x_in_lds) dot_grouped_launch<1, true>(dev_table, dev_block_prob, out, grid, lds_bytes, S(stream));
+        else dot_grouped_launch<1, false>(dev_table, dev_block_prob, out, grid, lds_bytes, S(stream));
+    } else {
+        if (x_in_lds) dot_grouped_launch<2, true>(dev_table, dev_block_prob, out, grid, lds_bytes, S(stream));
+        else dot_grouped_launch<2, false>(dev_table, dev_block_prob, out, grid, lds_bytes, S(stream));
+    }
+    return (int)hipGetLastError();
+}
+
+template <typename OT, int D, int MR>
+static void stream_launch(const StreamArgs& s, dim3 grid, hipStream_t st)
+{
+    if (s.mode == kStreamRange) hipLaunchKernelGGL((k_stream<OT, D, true, MR>), grid, dim3(256), 0, st, s);
+    else hipLaunchKernelGGL((k_stream<OT, D, false, MR>), grid, dim3(256), 0, st, s);
+}
+
+template <int D, int MR>
+static void stream_launch_out(const StreamArgs& s, int out, dim3 grid, hipStream_t st)
+{
+    if (out == VVH_F32) stream_launch<float, D, MR>(s, grid, st);
+    else stream_launch<f16, D, MR>(s, grid, st);
+}
+
+int launch_stream(const StreamArgs& s, int depth, int max_m, int out, int64_t blocks, void* stream)
+{
+    const dim3 grid((unsigned)blocks);
+    if (max_m <= 1) {
+        if (depth >= 12) stream_launch_out<12, 1>(s, out, grid, S(stream));
+        else stream_launch_out<8, 1>(s, out, grid, S(stream));
+    } else {
+        if (depth >= 12) stream_launch_out<12, 4>(s, out, grid, S(stream));
+        else stream_launch_out<8, 4>(s, out, grid, S(stream));
+    }
     return (int)hipGetLastError();
 }
 

@@ -89,8 +89,17 @@ struct Plan {
     std::vector<LinArgs> args;   // host copy, launch order
     LinArgs* dev_table = nullptr;
     int act = 0, out = 0;
-    bool grouped = false;
+    bool grouped = false;        // one k_skinny_grouped launch
     int64_t total_blocks = 0;
+    bool stream = false;         // one k_stream launch (kStreamList)
+    bool dot = false;            // one k_dot_grouped launch
+    int32_t* dev_block_prob = nullptr;
+    bool x_in_lds = false;       // every problem's activations fit the block's LDS
+    size_t lds_bytes = 0;
+    StreamArgs sargs{};
+    int depth = 0;
+    int max_m = 0;
+    void* dev_stream = nullptr;  // tile_prob, list, list_off
 };
 std::mutex g_pmu;
 std::unordered_map<vvh_plan, Plan> g_plans;
@@ -110,34 +119,86 @@ bool mul_ok(uint64_t a, uint64_t b, uint64_t* r)
     return true;
 }
 
-int natural_kernel(std::size_t M, int act)
+// ---- persistent streaming decode (k_stream) --------------------------------
+// Knobs, read once: VVH_STREAM=0 disables the streaming kernel,
+// VVH_STREAM_WPC = resident waves per CU (default 8), VVH_STREAM_DEPTH = 8 or
+// 12 weight loads in flight per lane (default: the largest every problem
+// allows), VVH_STREAM_MIN_TILES = smallest tile count worth a persistent
+// launch (default 4 per CU).
+struct StreamCfg {
+    bool enabled = true;
+    int wpc = 8;
+    int depth = 0;
+    int64_t min_tiles = -1;
+};
+const StreamCfg& stream_cfg()
 {
-    if (act == VVH_F32) return K_GEMV_F32;
-    return M <= (std::size_t)kSkinnyMaxM ? K_SKINNY : K_GEMM;
+    static StreamCfg c = [] {
+        StreamCfg r;
+        if (const char* e = getenv("VVH_STREAM")) r.enabled = atoi(e) != 0;
+        if (const char* e = getenv("VVH_STREAM_WPC")) r.wpc = std::max(1, std::min(32, atoi(e)));
+        if (const char* e = getenv("VVH_STREAM_DEPTH")) r.depth = atoi(e) >= 12 ? 12 : 8;
+        if (const char* e = getenv("VVH_STREAM_MIN_TILES")) r.min_tiles = atoll(e);
+        return r;
+    }();
+    return c;
 }
 
-// Kernel family for a call; `aligned` = K % 16 == 0 and 16-byte aligned
-// weight and activation bases.
-int choose_kernel(std::size_t M, std::size_t K, int act, bool aligned)
+int64_t stream_max_waves() { return (int64_t)(g_cu_count > 0 ? g_cu_count : 256) * stream_cfg().wpc; }
+
+// Pipeline depth the streaming kernel can use for problems whose smallest k
+// step count is min_steps (0 = not eligible).
+int stream_depth(int64_t min_steps)
+{
+    const StreamCfg& c = stream_cfg();
+    if (!c.enabled || min_steps < 8) return 0;
+    const int d = min_steps >= 12 ? 12 : 8;
+    return c.depth ? std::min(c.depth, d) : d;
+}
+
+bool stream_worth(int64_t tiles)
+{
+    const StreamCfg& c = stream_cfg();
+    const int64_t min_tiles = c.min_tiles >= 0 ? c.min_tiles : (int64_t)(g_cu_count > 0 ? g_cu_count : 256) * 4;
+    return tiles >= min_tiles;
+}
+
+int natural_kernel(std::size_t M, std::size_t N, std::size_t K, int act)
+{
+    if (act == VVH_F32) return K_GEMV_F32;
+    if (M <= (std::size_t)kDotMaxM) return K_DOT;
+    if (M > (std::size_t)kSkinnyMaxM) return K_GEMM;
+    const int64_t tiles = ((int64_t)N + kDecodeTileN - 1) / kDecodeTileN;
+    return (stream_depth(((int64_t)K + 63) / 64) > 0 && stream_worth(tiles)) ? K_STREAM : K_SKINNY;
+}
+
+// Kernel family for one call; `aligned` = K % 16 == 0 and 16-byte aligned
+// weight and activation bases.  A family forced by vvh_set_kernel_override
+// that cannot serve the call gives K_GENERIC.
+int choose_kernel(std::size_t M, std::size_t N, std::size_t K, int act, bool aligned)
 {
     if (K == 0 || !aligned) return K_GENERIC;
     const int ov = g_override.load();
-    const int k = ov == K_AUTO ? natural_kernel(M, act) : ov;
+    const int k = ov == K_AUTO ? natural_kernel(M, N, K, act) : ov;
+    const bool decode = act == VVH_F16 && M <= (std::size_t)kSkinnyMaxM;
     switch (k) {
         case K_GEMV_F32: return act == VVH_F32 ? K_GEMV_F32 : K_GENERIC;
-        case K_SKINNY: return (act == VVH_F16 && M <= (std::size_t)kSkinnyMaxM) ? K_SKINNY : K_GENERIC;
+        case K_SKINNY: return decode ? K_SKINNY : K_GENERIC;
+        case K_STREAM: return (decode && stream_depth(((int64_t)K + 63) / 64) > 0) ? K_STREAM : K_GENERIC;
+        case K_DOT: return (act == VVH_F16 && M <= (std::size_t)kDotMaxM) ? K_DOT : K_GENERIC;
         case K_GEMM: return act == VVH_F16 ? K_GEMM : K_GENERIC;
         default: return K_GENERIC;
     }
 }
 
 // Waves of a block that split one tile's k range: enough waves in flight to
-// cover every CU several times, never more than the k steps available.
-int choose_ksplit(int64_t tiles, int64_t K)
+// cover every CU several times, never more than the k steps (of `step`
+// codes) available.
+int choose_ksplit(int64_t tiles, int64_t K, int64_t step = 64)
 {
     const int64_t target = (int64_t)(g_cu_count > 0 ? g_cu_count : 256) * 8;
     int ks = tiles >= target ? 1 : (tiles * 2 >= target ? 2 : 4);
-    const int64_t steps = (K + 63) / 64;
+    const int64_t steps = (K + step - 1) / step;
     while (ks > 1 && ks > steps) ks >>= 1;
     return ks;
 }
@@ -170,8 +231,31 @@ int run_call(const LinArgs& base, int kernel, int act, int outd, void* stream)
             e = launch_gemv_f32(a, outd, stream);
             break;
         }
+        case K_STREAM: {
+            const int64_t tiles = (a.N + kDecodeTileN - 1) / kDecodeTileN;
+            const int depth = stream_depth((a.K + 63) / 64);
+            {
+                StreamArgs sa{};
+                sa.one = a;
+                sa.total_tiles = tiles;
+                sa.mode = kStreamRange;
+                const int64_t per = (tiles + stream_max_waves() - 1) / stream_max_waves();
+                const int64_t waves = (tiles + per - 1) / per;  // equal tile counts per wave
+                sa.waves = (int32_t)waves;
+                e = launch_stream(sa, depth, (int)a.M, outd, (waves + 3) / 4, stream);
+            }
+            break;
+        }
+        case K_DOT: {
+            const int64_t tiles = (a.N + kDecodeTileN - 1) / kDecodeTileN;
+            a.ksplit = choose_ksplit(tiles, a.K, kDotStep);
+            if (dot_blocks(a) > INT32_MAX) return fail(VVH_ERR_UNSUPPORTED, "problem too large for the decode grid");
+            e = launch_dot(a, outd, stream);
+            break;
+        }
         case K_SKINNY: {
-            a.ksplit = choose_ksplit((a.N + kDecodeTileN - 1) / kDecodeTileN, a.K);
+            const int64_t tiles = (a.N + kDecodeTileN - 1) / kDecodeTileN;
+            a.ksplit = choose_ksplit(tiles, a.K);
             if (decode_blocks(a) > INT32_MAX)
                 return fail(VVH_ERR_UNSUPPORTED, "problem too large for the decode grid");
             e = launch_skinny(a, outd, stream);
@@ -213,7 +297,138 @@ int linear_dev(void* out, const void* inp, const int8_t* w, const float* scales,
     a.K = (int64_t)K;
     a.ksplit = 1;
     const bool aligned = K % 16 == 0 && aligned16(w) && aligned16(inp);
-    return run_call(a, choose_kernel(M, K, act, aligned), act, outd, stream);
+    return run_call(a, choose_kernel(M, N, K, act, aligned), act, outd, stream);
+}
+
+// k_dot plan: problems ordered by K (longest rows first, so the last blocks
+// dispatched are the short ones), each given its ksplit for the plan's total
+// tile count and a contiguous range of blocks; a block -> problem map and
+// the problem table go to the device in one allocation.
+int build_dot_plan(Plan& p, int64_t total_tiles)
+{
+    std::stable_sort(p.args.begin(), p.args.end(), [](const LinArgs& x, const LinArgs& y) { return x.K > y.K; });
+    int64_t blk = 0;
+    int max_m = 0;
+    size_t lds = 0;
+    bool x_in_lds = true;
+    for (const LinArgs& a : p.args) x_in_lds = x_in_lds && dot_x_in_lds(a.M, a.K);
+    for (LinArgs& a : p.args) {
+        a.ksplit = choose_ksplit(total_tiles, a.K, kDotStep);
+        if (blk > INT32_MAX) return fail(VVH_ERR_UNSUPPORTED, "plan too large");
+        a.block_begin = (int32_t)blk;
+        blk += dot_blocks(a);
+        max_m = std::max(max_m, (int)a.M);
+        lds = std::max(lds, (size_t)(x_in_lds ? dot_lds_bytes(a.M, a.K) : kDotRedBytes));
+    }
+    if (blk > INT32_MAX) return fail(VVH_ERR_UNSUPPORTED, "plan too large");
+    std::vector<int32_t> block_prob((size_t)blk);
+    for (size_t i = 0; i < p.args.size(); i++) {
+        const int64_t b0 = p.args[i].block_begin, b1 = b0 + dot_blocks(p.args[i]);
+        for (int64_t b = b0; b < b1; b++) block_prob[(size_t)b] = (int32_t)i;
+    }
+    const size_t b_table = align_up(p.args.size() * sizeof(LinArgs));
+    const size_t bytes = b_table + align_up((size_t)blk * 4);
+    void* base = nullptr;
+    hipError_t e = hipMalloc(&base, bytes);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return fail_hip(e, "dot plan hipMalloc");
+    }
+    char* c = static_cast<char*>(base);
+    if ((e = hipMemcpy(c, p.args.data(), p.args.size() * sizeof(LinArgs), hipMemcpyHostToDevice)) != hipSuccess ||
+        (e = hipMemcpy(c + b_table, block_prob.data(), (size_t)blk * 4, hipMemcpyHostToDevice)) != hipSuccess) {
+        (void)hipFree(base);
+        return fail_hip(e, "dot plan upload");
+    }
+    p.dot = true;
+    p.dev_stream = base;  // owns table + map
+    p.dev_table = nullptr;
+    p.total_blocks = blk;
+    p.max_m = max_m;
+    p.x_in_lds = x_in_lds;
+    p.lds_bytes = lds;
+    p.sargs = StreamArgs{};
+    p.sargs.table = reinterpret_cast<const LinArgs*>(c);
+    p.dev_block_prob = reinterpret_cast<int32_t*>(c + b_table);
+    return VVH_OK;
+}
+
+// Streaming plan: problems ordered by K (longest rows first), their 16-row
+// tiles numbered globally in that order, and each wave given a list of tiles
+// by longest-processing-time-first assignment on weight bytes (each tile goes
+// to the wave with the fewest bytes so far), so every wave streams about the
+// same number of bytes.  One device allocation holds the problem table,
+// the tile -> problem map, the per-wave lists and their offsets.
+int build_stream_plan(Plan& p, int64_t total_tiles, int depth)
+{
+    if (total_tiles > INT32_MAX) return fail(VVH_ERR_UNSUPPORTED, "plan too large for a streaming launch");
+    std::stable_sort(p.args.begin(), p.args.end(), [](const LinArgs& x, const LinArgs& y) { return x.K > y.K; });
+    const int64_t T = total_tiles;
+    std::vector<int32_t> tile_prob((size_t)T);
+    int64_t g = 0;
+    for (size_t i = 0; i < p.args.size(); i++) {
+        LinArgs& a = p.args[i];
+        a.ksplit = 1;
+        a.tile_begin = g;
+        const int64_t n = (a.N + kDecodeTileN - 1) / kDecodeTileN;
+        for (int64_t t = 0; t < n; t++) tile_prob[(size_t)(g + t)] = (int32_t)i;
+        g += n;
+    }
+    const int64_t W = std::min<int64_t>(stream_max_waves(), T);
+    // min-heap of (bytes, wave); tiles arrive in non-increasing size order
+    std::vector<std::pair<int64_t, int32_t>> heap;
+    heap.reserve((size_t)W);
+    for (int64_t w = 0; w < W; w++) heap.emplace_back(0, (int32_t)w);
+    std::vector<std::vector<int32_t>> lists((size_t)W);
+    auto cmp = [](const std::pair<int64_t, int32_t>& x, const std::pair<int64_t, int32_t>& y) { return x > y; };
+    for (int64_t t = 0; t < T; t++) {
+        std::pop_heap(heap.begin(), heap.end(), cmp);
+        auto& top = heap.back();
+        lists[(size_t)top.second].push_back((int32_t)t);
+        top.first += kDecodeTileN * p.args[(size_t)tile_prob[(size_t)t]].K;
+        std::push_heap(heap.begin(), heap.end(), cmp);
+    }
+    std::vector<int32_t> list, off;
+    list.reserve((size_t)T);
+    off.reserve((size_t)W + 1);
+    for (auto& l : lists) {
+        off.push_back((int32_t)list.size());
+        list.insert(list.end(), l.begin(), l.end());
+    }
+    off.push_back((int32_t)list.size());
+
+    const size_t b_table = align_up(p.args.size() * sizeof(LinArgs));
+    const size_t b_prob = align_up((size_t)T * 4), b_list = align_up((size_t)T * 4);
+    const size_t bytes = b_table + b_prob + b_list + align_up(off.size() * 4);
+    void* base = nullptr;
+    hipError_t e = hipMalloc(&base, bytes);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return fail_hip(e, "stream plan hipMalloc");
+    }
+    char* c = static_cast<char*>(base);
+    if ((e = hipMemcpy(c, p.args.data(), p.args.size() * sizeof(LinArgs), hipMemcpyHostToDevice)) != hipSuccess ||
+        (e = hipMemcpy(c + b_table, tile_prob.data(), (size_t)T * 4, hipMemcpyHostToDevice)) != hipSuccess ||
+        (e = hipMemcpy(c + b_table + b_prob, list.data(), (size_t)T * 4, hipMemcpyHostToDevice)) != hipSuccess ||
+        (e = hipMemcpy(c + b_table + b_prob + b_list, off.data(), off.size() * 4, hipMemcpyHostToDevice)) != hipSuccess) {
+        (void)hipFree(base);
+        return fail_hip(e, "stream plan upload");
+    }
+    p.stream = true;
+    p.depth = depth;
+    p.max_m = 0;
+    for (const LinArgs& a : p.args) p.max_m = std::max(p.max_m, (int)a.M);
+    p.dev_stream = base;
+    StreamArgs& sa = p.sargs;
+    sa = StreamArgs{};
+    sa.table = reinterpret_cast<const LinArgs*>(c);
+    sa.tile_prob = reinterpret_cast<const int32_t*>(c + b_table);
+    sa.list = reinterpret_cast<const int32_t*>(c + b_table + b_prob);
+    sa.list_off = reinterpret_cast<const int32_t*>(c + b_table + b_prob + b_list);
+    sa.total_tiles = T;
+    sa.waves = (int32_t)W;
+    sa.mode = kStreamList;
+    return VVH_OK;
 }
 
 }  // namespace
@@ -552,7 +767,8 @@ VVH_API int vvh_plan_create(const vvh_q8_problem* problems, size_t count, int ac
     Plan p;
     p.act = act_dtype;
     p.out = out_dtype;
-    bool all_skinny = true;
+    bool all_skinny = true;  // every problem takes a decode kernel (M <= 16)
+    bool all_dot = true;     // every problem takes k_dot (M <= 2)
     int64_t total_tiles = 0;
     for (size_t i = 0; i < count; i++) {
         const vvh_q8_problem& q = problems[i];
@@ -571,14 +787,29 @@ VVH_API int vvh_plan_create(const vvh_q8_problem* problems, size_t count, int ac
         a.K = (int64_t)q.K;
         a.ksplit = 1;
         const bool aligned = q.K % 16 == 0 && aligned16(q.weight) && aligned16(q.inp);
-        if (choose_kernel(q.M, q.K, act_dtype, aligned) != K_SKINNY) all_skinny = false;
+        const int kf = choose_kernel(q.M, q.N, q.K, act_dtype, aligned);
+        if (kf != K_SKINNY && kf != K_STREAM && kf != K_DOT) all_skinny = false;
+        if (kf != K_DOT) all_dot = false;
         total_tiles += (a.N + kDecodeTileN - 1) / kDecodeTileN;
         p.args.push_back(a);
     }
     if (p.args.empty()) return fail(VVH_ERR_INVALID_ARG, "every problem is empty");
     REQUIRE_INIT();
-    p.grouped = all_skinny;
-    if (p.grouped) {
+    int64_t min_steps = INT64_MAX;
+    for (const LinArgs& a : p.args) min_steps = std::min(min_steps, (a.K + 63) / 64);
+    // every problem takes a decode kernel: one streaming launch when the
+    // plan is big enough (or the streaming family is forced), else one
+    // k_skinny_grouped launch (or that family is forced)
+    const int ov = g_override.load();
+    const int depth = all_skinny && ov != K_SKINNY ? stream_depth(min_steps) : 0;
+    if (all_dot && (ov == K_AUTO || ov == K_DOT)) {
+        const int st = build_dot_plan(p, total_tiles);
+        if (st != VVH_OK) return st;
+    } else if (depth > 0 && (ov == K_STREAM || stream_worth(total_tiles))) {
+        const int st = build_stream_plan(p, total_tiles, depth);
+        if (st != VVH_OK) return st;
+    } else if (all_skinny) {
+        p.grouped = true;
         // longest rows first, so the last blocks dispatched are the short ones
         std::stable_sort(p.args.begin(), p.args.end(),
                          [](const LinArgs& x, const LinArgs& y) { return x.K > y.K; });
@@ -619,13 +850,22 @@ VVH_API int vvh_plan_run(vvh_plan plan, void* stream)
         if (it == g_plans.end()) return fail(VVH_ERR_UNKNOWN_HANDLE, "unknown plan %llu", (unsigned long long)plan);
         p = &it->second;
     }
+    if (p->dot) {
+        const int e = launch_dot_grouped(p->sargs.table, p->dev_block_prob, p->total_blocks, p->max_m, p->x_in_lds,
+                                         p->lds_bytes, p->out, stream);
+        return e == 0 ? VVH_OK : fail_hip((hipError_t)e, "grouped dot launch");
+    }
+    if (p->stream) {
+        const int e = launch_stream(p->sargs, p->depth, p->max_m, p->out, ((int64_t)p->sargs.waves + 3) / 4, stream);
+        return e == 0 ? VVH_OK : fail_hip((hipError_t)e, "streaming launch");
+    }
     if (p->grouped) {
         const int e = launch_skinny_grouped(p->dev_table, (int)p->args.size(), p->total_blocks, p->out, stream);
         return e == 0 ? VVH_OK : fail_hip((hipError_t)e, "grouped launch");
     }
     for (const LinArgs& a : p->args) {
         const bool aligned = a.K % 16 == 0 && aligned16(a.w) && aligned16(a.inp);
-        const int st = run_call(a, choose_kernel(a.M, a.K, p->act, aligned), p->act, p->out, stream);
+        const int st = run_call(a, choose_kernel(a.M, a.N, a.K, p->act, aligned), p->act, p->out, stream);
         if (st != VVH_OK) return st;
     }
     return VVH_OK;
@@ -637,6 +877,7 @@ VVH_API int vvh_plan_destroy(vvh_plan plan)
     auto it = g_plans.find(plan);
     if (it == g_plans.end()) return fail(VVH_ERR_UNKNOWN_HANDLE, "unknown plan %llu", (unsigned long long)plan);
     if (it->second.dev_table) (void)hipFree(it->second.dev_table);
+    if (it->second.dev_stream) (void)hipFree(it->second.dev_stream);
     g_plans.erase(it);
     return VVH_OK;
 }
@@ -647,7 +888,17 @@ VVH_API int vvh_plan_launches(vvh_plan plan, int* launches)
     std::lock_guard<std::mutex> lock(g_pmu);
     auto it = g_plans.find(plan);
     if (it == g_plans.end()) return fail(VVH_ERR_UNKNOWN_HANDLE, "unknown plan %llu", (unsigned long long)plan);
-    *launches = it->second.grouped ? 1 : (int)it->second.args.size();
+    *launches = (it->second.grouped || it->second.stream || it->second.dot) ? 1 : (int)it->second.args.size();
+    return VVH_OK;
+}
+
+VVH_API int vvh_plan_kernel(vvh_plan plan, int* kernel)
+{
+    if (!kernel) return fail(VVH_ERR_INVALID_ARG, "kernel is null");
+    std::lock_guard<std::mutex> lock(g_pmu);
+    auto it = g_plans.find(plan);
+    if (it == g_plans.end()) return fail(VVH_ERR_UNKNOWN_HANDLE, "unknown plan %llu", (unsigned long long)plan);
+    *kernel = it->second.dot ? K_DOT : it->second.stream ? K_STREAM : it->second.grouped ? K_SKINNY : K_AUTO;
     return VVH_OK;
 }
 
@@ -690,14 +941,13 @@ VVH_API int vvh_fill_normal(void* dst, int dtype, size_t n, uint64_t seed, float
 // ---- dispatch introspection --------------------------------------------------------------------
 VVH_API int vvh_linear_q8_choice(size_t M, size_t N, size_t K, int act_dtype, int out_dtype)
 {
-    (void)N;
     if (!valid_dtype(act_dtype) || !valid_dtype(out_dtype)) return -fail(VVH_ERR_INVALID_ARG, "bad dtype");
-    return choose_kernel(M, K, act_dtype, K % 16 == 0);
+    return choose_kernel(M, N, K, act_dtype, K % 16 == 0);
 }
 
 VVH_API int vvh_set_kernel_override(int kernel)
 {
-    if (kernel < K_AUTO || kernel > K_GEMM) return fail(VVH_ERR_INVALID_ARG, "bad kernel %d", kernel);
+    if (kernel < K_AUTO || kernel > K_DOT) return fail(VVH_ERR_INVALID_ARG, "bad kernel %d", kernel);
     g_override.store(kernel);
     return VVH_OK;
 }
