@@ -25,6 +25,12 @@ struct LinArgs {
     int32_t ksplit;           // decode kernels: waves cooperating on one 16-row tile (1, 2, 4)
     int32_t block_begin;      // grouped launch: first block of this problem
     int64_t tile_begin;       // streaming plan: first global 16-row tile of this problem
+    // GEMM split-K: nsplit blocks share each output tile, each running
+    // kstages 64-wide k stages; their raw fp32 sums go to ws[split][M][N]
+    // and k_splitk_reduce applies the epilogue.  nsplit <= 1: no split.
+    float* ws;
+    int32_t nsplit;
+    int32_t kstages;
 };
 
 // Persistent streaming decode launch (k_stream).  Work is a sequence of
@@ -114,6 +120,8 @@ int launch_dot(const LinArgs& a, int out, void* stream);
 int launch_dot_grouped(const LinArgs* dev_table, const int32_t* dev_block_prob, int64_t total_blocks, int max_m,
                        bool x_in_lds, size_t lds_bytes, int out, void* stream);
 int launch_gemm(const LinArgs& a, int out, void* stream);
+// sum of the a.nsplit partials in a.ws + epilogue (scale, bias, residual)
+int launch_splitk_reduce(const LinArgs& a, int out, void* stream);
 // depth = weight loads in flight per lane (8 or 12); every problem must have
 // at least `depth` 64-wide k steps.  max_m = largest M of the launch.
 int launch_stream(const StreamArgs& s, int depth, int max_m, int out, int64_t blocks, void* stream);

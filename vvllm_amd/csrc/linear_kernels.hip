@@ -1140,21 +1140,39 @@ __device__ __forceinline__ void gemm2_read(const f16* __restrict__ sa, const int
     }
 }
 
+// MFMAs of one stage.  The codes of the second 32-wide k slice are converted
+// while the first slice's MFMAs run, and the scheduling-group barriers
+// interleave conversion VALU with the MFMAs (each MFMA occupies the matrix
+// unit for 32 cycles, during which the wave can issue about 8 VALU ops), so
+// the conversion hides behind the matrix work instead of sitting between it.
 template <int TI, int TJ>
 __device__ __forceinline__ void gemm2_mfma(const Gemm2Frag<TI, TJ>& f, f16v (&acc)[TI][TJ])
 {
+    h8 fb[2][TJ][2];
+#pragma unroll
+    for (int tj = 0; tj < TJ; tj++) i8x16_to_h8x2(f.b[0][tj], fb[0][tj][0], fb[0][tj][1]);
 #pragma unroll
     for (int kk2 = 0; kk2 < 2; kk2++) {
-        h8 fb[TJ][2];
+        if (kk2 == 0) {
 #pragma unroll
-        for (int tj = 0; tj < TJ; tj++) i8x16_to_h8x2(f.b[kk2][tj], fb[tj][0], fb[tj][1]);
+            for (int tj = 0; tj < TJ; tj++) i8x16_to_h8x2(f.b[1][tj], fb[1][tj][0], fb[1][tj][1]);
+        }
 #pragma unroll
         for (int h = 0; h < 2; h++)
 #pragma unroll
             for (int ti = 0; ti < TI; ti++)
 #pragma unroll
                 for (int tj = 0; tj < TJ; tj++)
-                    acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[kk2][h][ti], fb[tj][h], acc[ti][tj], 0, 0, 0);
+                    acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[kk2][h][ti], fb[kk2][tj][h], acc[ti][tj], 0, 0, 0);
+    }
+    // 2*2*TI*TJ MFMAs; the 20*TJ conversion ops of slice 1 go between the
+    // MFMAs of slice 0
+    constexpr int NM = 2 * TI * TJ;        // MFMAs per slice
+    constexpr int NV = (20 * TJ + NM - 1) / NM;
+#pragma unroll
+    for (int i = 0; i < NM; i++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, NV, 0); // then conversion VALU
     }
 }
 
@@ -1172,9 +1190,14 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemm2(LinArgs a)
 
     const int64_t nbm = (a.M + kGemmBM - 1) / kGemmBM;
     const int64_t nbn = (a.N + kGemmBN - 1) / kGemmBN;
-    const int64_t logical = xcd_remap(blockIdx.x, nbm * nbn);
-    const int64_t m0 = (logical % nbm) * kGemmBM;
-    const int64_t n0 = (logical / nbm) * kGemmBN;
+    // blocks enumerate (split, tile), tiles fastest, dealt XCD by XCD
+    const int64_t tiles = nbm * nbn;
+    const bool split = a.nsplit > 1;
+    const int64_t logical = xcd_remap(blockIdx.x, tiles * (split ? a.nsplit : 1));
+    const int64_t ks = logical / tiles, tile = logical - ks * tiles;
+    const int64_t m0 = (tile % nbm) * kGemmBM;
+    const int64_t n0 = (tile / nbm) * kGemmBN;
+    const int64_t kbase = split ? ks * a.kstages * kGemmBK : 0;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1190,8 +1213,8 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemm2(LinArgs a)
 #pragma unroll
     for (int tj = 0; tj < TJ; tj++) {
         const int64_t n = n0 + col0 + tj * 32 + fl;
-        sc[tj] = n < a.N ? a.scales[n] : 0.0f;
-        bi[tj] = (a.bias && n < a.N) ? a.bias[n] : 0.0f;
+        sc[tj] = split ? 1.0f : (n < a.N ? a.scales[n] : 0.0f);  // split partials stay raw
+        bi[tj] = (!split && a.bias && n < a.N) ? a.bias[n] : 0.0f;
     }
 
     // per-lane global sources of this thread's direct-to-LDS loads (k0 added per stage)
@@ -1200,14 +1223,14 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemm2(LinArgs a)
     for (int i = 0; i < 16 / NW; i++) {
         const int r = (wave * (16 / NW) + i) * 8 + (lane >> 3);  // A stage row written by this lane
         const int64_t gr = m0 + r < a.M ? m0 + r : a.M - 1;      // rows past M: any valid row
-        a_src[i] = X + gr * a.K + swz_a(r, lane & 7) * 8;
+        a_src[i] = X + gr * a.K + kbase + swz_a(r, lane & 7) * 8;
     }
     const int8_t* b_src[8 / NW];
 #pragma unroll
     for (int i = 0; i < 8 / NW; i++) {
         const int r = (wave * (8 / NW) + i) * 16 + (lane >> 2);
         const int64_t gn = n0 + r < a.N ? n0 + r : a.N - 1;
-        b_src[i] = a.w + gn * a.K + swz_b(r, lane & 3) * 16;
+        b_src[i] = a.w + gn * a.K + kbase + swz_b(r, lane & 3) * 16;
     }
 
     auto stage = [&](auto S) -> Gemm2Stage& {
@@ -1268,7 +1291,8 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemm2(LinArgs a)
         read(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
     };
 
-    const int64_t nk = a.K / kGemmBK;
+    const int64_t nk_all = a.K / kGemmBK;
+    const int64_t nk = split ? (nk_all - kbase / kGemmBK < a.kstages ? nk_all - kbase / kGemmBK : a.kstages) : nk_all;
     if (nk >= D) {
         prologue.template operator()<D>();
         int64_t kt0 = 0;
@@ -1328,6 +1352,16 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemm2(LinArgs a)
         const f4 v1 = *reinterpret_cast<const f4*>(tq + 4);
         float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
         const int64_t o = mm * a.N + nn;
+        if (split) {  // raw partial sums of this split
+            float* wp = a.ws + ks * a.M * a.N + o;
+            if (vec_ok && nn + 8 <= a.N) {
+                *reinterpret_cast<f4*>(wp) = v0;
+                *reinterpret_cast<f4*>(wp + 4) = v1;
+            } else {
+                for (int e = 0; e < 8 && nn + e < a.N; e++) wp[e] = v[e];
+            }
+            continue;
+        }
         if (vec_ok && nn + 8 <= a.N) {
             if constexpr (sizeof(OT) == 2) {
                 if (a.res) {
@@ -1360,6 +1394,54 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemm2(LinArgs a)
             }
         }
     }
+}
+
+// ---------------------------------------------------------------------------
+// k_splitk_reduce: out = (sum over splits of ws[s][m][n]) * scale[n] + bias[n]
+// (+ res[m][n]), in fp32 with one rounding; 4 consecutive outputs per thread
+// (16-byte partial loads when N % 4 == 0).  The partials are summed in split
+// order, so the result does not depend on the launch.
+// ---------------------------------------------------------------------------
+template <typename OT>
+__global__ __launch_bounds__(256) void k_splitk_reduce(LinArgs a)
+{
+    const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t per_row = (a.N + 3) / 4;
+    if (q >= a.M * per_row) return;
+    const int64_t m = q / per_row, n = (q - m * per_row) * 4;
+    const int64_t o = m * a.N + n, plane = a.M * a.N;
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    if (a.N % 4 == 0) {
+        // four splits' loads in flight before their sums
+        int32_t s = 0;
+        for (; s + 4 <= a.nsplit; s += 4) {
+            f4 p[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) p[j] = *reinterpret_cast<const f4*>(a.ws + (s + j) * plane + o);
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) v[e] += p[j][e];
+        }
+        for (; s < a.nsplit; s++) {
+            const f4 p = *reinterpret_cast<const f4*>(a.ws + s * plane + o);
+#pragma unroll
+            for (int e = 0; e < 4; e++) v[e] += p[e];
+        }
+    } else {
+        for (int32_t s = 0; s < a.nsplit; s++)
+            for (int e = 0; e < 4 && n + e < a.N; e++) v[e] += a.ws[s * plane + o + e];
+    }
+    for (int e = 0; e < 4 && n + e < a.N; e++) store_out<OT>(a, m, n + e, v[e]);
+}
+
+int launch_splitk_reduce(const LinArgs& a, int out, void* stream)
+{
+    const int64_t threads = a.M * ((a.N + 3) / 4);
+    const dim3 grid((unsigned)((threads + 255) / 256));
+    if (out == VVH_F32) hipLaunchKernelGGL((k_splitk_reduce<float>), grid, dim3(256), 0, static_cast<hipStream_t>(stream), a);
+    else hipLaunchKernelGGL((k_splitk_reduce<f16>), grid, dim3(256), 0, static_cast<hipStream_t>(stream), a);
+    return (int)hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
@@ -1530,7 +1612,7 @@ int launch_gemm(const LinArgs& a, int out, void* stream)
         gemm2_config();
         const int64_t nbm = (a.M + kGemmBM - 1) / kGemmBM;
         const int64_t nbn = (a.N + kGemmBN - 1) / kGemmBN;
-        const dim3 grid((unsigned)(nbm * nbn));
+        const dim3 grid((unsigned)(nbm * nbn * (a.nsplit > 1 ? a.nsplit : 1)));
         const bool f32 = out == VVH_F32;
         if (g_gemm2_stages == 6) gemm2_launch_wm<6>(a, f32, grid, S(stream), g_gemm2_layout);
         else gemm2_launch_wm<4>(a, f32, grid, S(stream), g_gemm2_layout);

@@ -105,6 +105,66 @@ std::mutex g_pmu;
 std::unordered_map<vvh_plan, Plan> g_plans;
 vvh_plan g_next_plan = 1;
 
+// ---- split-K workspace ------------------------------------------------------
+// fp32 partial sums of split GEMMs, one buffer per stream (calls on one stream
+// run in order, so they can share it; calls on different streams never do).
+// Grown on demand: the old buffer is released only after its stream has
+// drained.  Kept until the process ends.
+struct Workspace {
+    void* p = nullptr;
+    std::size_t bytes = 0;
+};
+std::mutex g_wsmu;
+std::unordered_map<void*, Workspace> g_ws;
+
+int workspace_for(void* stream, std::size_t bytes, float** out)
+{
+    std::lock_guard<std::mutex> lock(g_wsmu);
+    Workspace& w = g_ws[stream];
+    if (w.bytes < bytes) {
+        if (w.p) {
+            hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+            if (e != hipSuccess) return fail_hip(e, "split-K workspace: stream synchronize");
+            (void)hipFree(w.p);
+            w.p = nullptr;
+            w.bytes = 0;
+        }
+        const std::size_t nb = std::max<std::size_t>(bytes, std::size_t(16) << 20);
+        hipError_t e = hipMalloc(&w.p, nb);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            w.p = nullptr;
+            return fail_hip(e, "split-K workspace hipMalloc");
+        }
+        w.bytes = nb;
+    }
+    *out = static_cast<float*>(w.p);
+    return VVH_OK;
+}
+
+// Number of k splits for a GEMM of `tiles` 128x128 output tiles and `stages`
+// 64-wide k stages.  A split GEMM pays a second launch and an fp32 partial
+// round trip through memory (measured: ~2.5 us launch floor, ~3 TB/s for the
+// reduction), so it only pays for long reductions over few tiles: split when
+// the tiles would leave three quarters of the CUs idle and K has at least 32
+// stages, into at most one block per CU and at least 4 stages per split
+// (Qwen2.5-0.5B down projection at M=512: 37 us -> 23 us).
+// VVH_GEMM_SPLIT=0 disables splitting, =s forces s.
+int gemm_splits(int64_t tiles, int64_t stages)
+{
+    static const int forced = [] {
+        const char* e = getenv("VVH_GEMM_SPLIT");
+        return e ? atoi(e) : -1;
+    }();
+    const int64_t cus = g_cu_count > 0 ? g_cu_count : 256;
+    int64_t s;
+    if (forced >= 0) s = forced;
+    else if (tiles * 4 > cus || stages < 32) s = 1;
+    else s = std::min<int64_t>(cus / tiles, stages / 4);
+    s = std::max<int64_t>(1, std::min<int64_t>(s, stages));
+    return (int)s;
+}
+
 constexpr std::size_t kAlign = 256;
 inline std::size_t align_up(std::size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -264,7 +324,28 @@ int run_call(const LinArgs& base, int kernel, int act, int outd, void* stream)
         case K_GEMM: {
             const int64_t nb = ((a.M + kGemmBM - 1) / kGemmBM) * ((a.N + kGemmBN - 1) / kGemmBN);
             if (nb > INT32_MAX) return fail(VVH_ERR_UNSUPPORTED, "problem too large for the GEMM grid");
+            a.nsplit = 1;
+            a.kstages = 0;
+            a.ws = nullptr;
+            if (a.K % kGemmBK == 0) {
+                const int64_t stages = a.K / kGemmBK;
+                int s = gemm_splits(nb, stages);
+                if (s > 1) {
+                    const int64_t kst = (stages + s - 1) / s;
+                    s = (int)((stages + kst - 1) / kst);  // no empty split
+                    uint64_t plane;
+                    if (s > 1 && mul_ok((uint64_t)a.M * (uint64_t)a.N, (uint64_t)s * 4, &plane) && nb * s <= INT32_MAX) {
+                        float* ws = nullptr;
+                        const int st = workspace_for(stream, plane, &ws);
+                        if (st != VVH_OK) return st;
+                        a.ws = ws;
+                        a.nsplit = s;
+                        a.kstages = (int32_t)kst;
+                    }
+                }
+            }
             e = launch_gemm(a, outd, stream);
+            if (e == 0 && a.nsplit > 1) e = launch_splitk_reduce(a, outd, stream);
             break;
         }
         default: {
