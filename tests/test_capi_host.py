@@ -105,9 +105,10 @@ def test_dispatch_choice():
         assert ch(1, 896, 896, capi.F32, capi.F32) == "gemv_f32"      # config 1
         assert ch(1, 151936, 896, capi.F16, capi.F32) == "dot"        # config 3 (M = 1)
         assert ch(1, 896, 896, capi.F16, capi.F16) == "dot"           # config 2 (M = 1)
-        assert ch(4, 151936, 896, capi.F16, capi.F32) == "stream"     # 9496 tiles
+        assert ch(4, 896, 896, capi.F16, capi.F16) == "dot"           # M <= 4
+        assert ch(5, 151936, 896, capi.F16, capi.F32) == "stream"     # 9496 tiles
         assert ch(16, 4864, 896, capi.F16, capi.F16) == "skinny"      # 304 tiles: too few to stream
-        assert ch(4, 151936, 448, capi.F16, capi.F16) == "skinny"     # 7 k steps: too short to stream
+        assert ch(5, 151936, 448, capi.F16, capi.F16) == "skinny"     # 7 k steps: too short to stream
         assert ch(17, 4864, 896, capi.F16, capi.F16) == "gemm"
         assert ch(512, 4864, 896, capi.F16, capi.F16) == "gemm"       # config 4
         assert ch(1, 2, 2, capi.F32, capi.F32) == "generic"           # K % 16 != 0
@@ -119,7 +120,7 @@ def test_dispatch_choice():
         assert ch(64, 896, 896, capi.F16, capi.F16) == "generic"      # M > 16
         capi.set_kernel(capi.KERNEL_DOT)
         assert ch(1, 16, 16, capi.F16, capi.F16) == "dot"
-        assert ch(2, 16, 16, capi.F16, capi.F16) == "generic"         # M > 1
+        assert ch(5, 16, 16, capi.F16, capi.F16) == "generic"         # M > 4
         assert ch(1, 16, 16, capi.F32, capi.F32) == "generic"         # fp32 activations
         capi.set_kernel(capi.KERNEL_STREAM)
         assert ch(1, 16, 512, capi.F16, capi.F16) == "stream"

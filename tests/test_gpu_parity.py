@@ -165,23 +165,24 @@ def test_stream_kernel(gpu, oracle, M, N, K, outd):
              kernel=capi.KERNEL_STREAM, seed=11 * M + K)
 
 
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
 @pytest.mark.parametrize("outd", [F16, F32])
 @pytest.mark.parametrize("N,K", [(1, 16), (17, 48), (128, 896), (896, 4864), (300, 1040), (4099, 592),
                                  (64, 20480), (33, 8960)])
-def test_dot_kernel(gpu, oracle, N, K, outd):
-    """VALU dot-product decode (M = 1): K tails (48, 592, 1040), a single
-    16-code step, N % 16 != 0, activations too large for LDS (K = 20480) and
-    the ksplit reduction (few tiles)."""
-    run_case(oracle, 1, N, K, F16, outd, bias=bool(N % 2), res=["sep", "inplace", None][(N + K) % 3],
-             kernel=capi.KERNEL_DOT, seed=13 * N + K)
+def test_dot_kernel(gpu, oracle, M, N, K, outd):
+    """VALU dot-product decode (M <= 4): K tails (48, 592, 1040), a single
+    16-code step, N % 16 != 0, activations too large for LDS (K = 20480,
+    and K = 8960 at M = 4) and the ksplit reduction (few tiles)."""
+    run_case(oracle, M, N, K, F16, outd, bias=bool(N % 2), res=["sep", "inplace", None][(N + K + M) % 3],
+             kernel=capi.KERNEL_DOT, seed=13 * N + K + M)
 
 
 def test_decode_dispatch_on_device(gpu):
     assert capi.kernel_choice(1, 151936, 896, F16, F32) == "dot"
-    assert capi.kernel_choice(1, 896, 896, F16, F16) == "dot"
-    assert capi.kernel_choice(4, 151936, 896, F16, F16) == "stream"
-    assert capi.kernel_choice(4, 896, 896, F16, F16) == "skinny"
-    assert capi.kernel_choice(4, 4864, 448, F16, F16) == "skinny"  # 7 k steps: too short to stream
+    assert capi.kernel_choice(4, 896, 896, F16, F16) == "dot"
+    assert capi.kernel_choice(5, 151936, 896, F16, F16) == "stream"
+    assert capi.kernel_choice(5, 896, 896, F16, F16) == "skinny"
+    assert capi.kernel_choice(5, 4864, 448, F16, F16) == "skinny"  # 7 k steps: too short to stream
 
 
 def test_misaligned_activations_fall_back(gpu, oracle):
@@ -356,11 +357,17 @@ def test_mixed_plan_single_launch(gpu, oracle, kernel, outd):
 DOT_PLAN = [(1, 896, 896, True, None), (1, 128, 896, True, None), (1, 130, 592, False, "sep"),
             (1, 300, 1040, True, "inplace"), (1, 896, 4864, False, "inplace"), (1, 17, 48, False, None),
             (1, 4864, 896, False, None), (1, 1, 512, True, "sep")]
+DOT_PLAN_M4 = [(4, 896, 896, True, None), (2, 128, 896, True, "sep"), (3, 300, 1040, False, "inplace"),
+               (1, 896, 4864, False, "inplace"), (4, 17, 48, True, None)]
 
 
 @pytest.mark.parametrize("outd", [F16, F32])
 def test_dot_plan_single_launch(gpu, oracle, outd):
     assert _plan_case(oracle, DOT_PLAN, outd, capi.KERNEL_AUTO, seed=500, expect="dot") == 1
+
+
+def test_dot_plan_several_rows(gpu, oracle):
+    assert _plan_case(oracle, DOT_PLAN_M4, F16, capi.KERNEL_AUTO, seed=550, expect="dot") == 1
 
 
 def test_dot_plan_without_lds_activations(gpu, oracle):
@@ -375,7 +382,7 @@ def test_plan_with_short_rows_is_not_streamed(gpu, oracle):
     dispatch runs such a plan as one k_skinny_grouped launch; with the
     streaming family forced, the short problem falls back to the generic
     kernel and the plan runs one launch per problem."""
-    specs = [(2, 896, 256, True, None), (1, 4864, 896, False, None)]
+    specs = [(5, 896, 256, True, None), (1, 4864, 896, False, None)]
     assert _plan_case(oracle, specs, F16, capi.KERNEL_AUTO, seed=400, expect="skinny") == 1
     assert _plan_case(oracle, specs, F16, capi.KERNEL_STREAM, seed=400, expect="auto") == 2
 

@@ -81,11 +81,11 @@ inline int64_t decode_blocks(const LinArgs& a)
     return (tiles + tiles_per_block - 1) / tiles_per_block;
 }
 
-// k_dot (M <= 2): 16-row tiles, 128-wide k steps, ksplit waves per tile.
-constexpr int64_t kDotMaxM = 1;
-constexpr int kDotStep = 128;   // k codes per row per step
-constexpr int64_t kDotLdsMax = 40 * 1024;   // dynamic LDS of one block at most
-constexpr int64_t kDotRedBytes = 4 * 2 * 16 * 4;
+// k_dot (M <= 4): 16-row tiles, 128-wide k steps, ksplit waves per tile.
+constexpr int64_t kDotMaxM = 4;
+constexpr int kDotStep = 128;               // k codes per row per step
+constexpr int64_t kDotLdsMax = 80 * 1024;   // dynamic LDS of one block at most
+constexpr int64_t kDotRedBytes = 4 * 4 * 16 * 4;
 inline int64_t dot_blocks(const LinArgs& a)
 {
     const int64_t tiles = (a.N + kDecodeTileN - 1) / kDecodeTileN;

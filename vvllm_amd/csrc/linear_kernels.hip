@@ -427,12 +427,12 @@ __global__ __launch_bounds__(256) void k_skinny_grouped(const LinArgs* __restric
 }
 
 // ---------------------------------------------------------------------------
-// k_dot: fp16 activations, M <= 2, VALU dot products.
+// k_dot: fp16 activations, M <= 4, VALU dot products.
 //
 // The weight stream decides the speed of a decode GEMV, and it runs fastest
 // when every load instruction covers whole 128-byte cache lines: 8 rows x
 // 128 B per instruction streams about 7 TB/s on MI355X, the 16 rows x 64 B
-// that a 16x16 MFMA operand needs about 5.5 TB/s.  So at M <= 2, where the
+// that a 16x16 MFMA operand needs about 5.5 TB/s.  So at M <= 4, where the
 // MFMA's M side would be mostly empty anyway, each wave owns a 16-row tile
 // and lane l reads the 16-byte chunk c = l%8 of the 128-byte k step of rows
 // r = l/8 and r + 8 (two loads per step), converts the codes exactly to fp16
@@ -468,8 +468,9 @@ __device__ __forceinline__ DecodeCoord dot_coord(const LinArgs& a, int64_t block
 // stride of K + 8 halves.  The launcher sizes the dynamic LDS with the same
 // rule (dot_lds_bytes), so kernel and launcher agree on where x lives.
 struct DotRed {
-    float v[4][2][16];  // [wave][m][row]
+    float v[4][4][16];  // [wave][m][row]
 };
+static_assert(sizeof(DotRed) == kDotRedBytes, "reduction scratch size");
 
 // 16 fp16 activations times 16 exact fp16 codes, accumulated in fp32.
 __device__ __forceinline__ float dot16(const h8 w0, const h8 w1, const h8 x0, const h8 x1, float acc)
@@ -499,7 +500,9 @@ __device__ __forceinline__ void store_out_g(const LinArgs& a, int64_t m, int64_t
 template <typename OT, int MT, bool XLDS>
 __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* smem)
 {
-    constexpr int D = kDotDepth;
+    // activations in the ring take 8 VGPRs per row and slot: halve the ring
+    // for several rows so the wave keeps two waves per SIMD's worth of VGPRs
+    constexpr int D = (XLDS || MT == 1) ? kDotDepth : kDotDepth / 2;
     DotRed& red = *reinterpret_cast<DotRed*>(smem);
     f16* xs = reinterpret_cast<f16*>(smem + kDotRedBytes);
     const DecodeCoord c = dot_coord(a, block);
@@ -1512,9 +1515,12 @@ int launch_dot(const LinArgs& a, int out, void* stream)
     if (a.M <= 1) {
         if (xl) dot_launch<1, true>(a, out, grid, lds, S(stream));
         else dot_launch<1, false>(a, out, grid, lds, S(stream));
-    } else {
+    } else if (a.M <= 2) {
         if (xl) dot_launch<2, true>(a, out, grid, lds, S(stream));
         else dot_launch<2, false>(a, out, grid, lds, S(stream));
+    } else {
+        if (xl) dot_launch<4, true>(a, out, grid, lds, S(stream));
+        else dot_launch<4, false>(a, out, grid, lds, S(stream));
     }
     return (int)hipGetLastError();
 }
@@ -1534,9 +1540,12 @@ int launch_dot_grouped(const LinArgs* dev_table, const int32_t* dev_block_prob, 
     if (max_m <= 1) {
         if (x_in_lds) dot_grouped_launch<1, true>(dev_table, dev_block_prob, out, grid, lds_bytes, S(stream));
         else dot_grouped_launch<1, false>(dev_table, dev_block_prob, out, grid, lds_bytes, S(stream));
-    } else {
+    } else if (max_m <= 2) {
         if (x_in_lds) dot_grouped_launch<2, true>(dev_table, dev_block_prob, out, grid, lds_bytes, S(stream));
         else dot_grouped_launch<2, false>(dev_table, dev_block_prob, out, grid, lds_bytes, S(stream));
+    } else {
+        if (x_in_lds) dot_grouped_launch<4, true>(dev_table, dev_block_prob, out, grid, lds_bytes, S(stream));
+        else dot_grouped_launch<4, false>(dev_table, dev_block_prob, out, grid, lds_bytes, S(stream));
     }
     return (int)hipGetLastError();
 }
