@@ -1,0 +1,107 @@
+"""HIP graph capture of the int8 linear path (launch-overhead
+removal by graph capture of the decode step).
+
+A decode plan, a several-row decode call, a GEMM and a split-K GEMM are
+issued on one stream, captured into a graph and replayed several times, with
+eager work and synchronisation between the replays.  Every replay must give
+exactly the eager results: the kernels are deterministic and the captured
+calls allocate nothing (the split-K workspace of the stream is grown by an
+eager call before capture).
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from vvllm_amd import capi
+
+pytestmark = pytest.mark.gpu
+
+F16, F32 = capi.F16, capi.F32
+
+
+def _hip():
+    for name in ("libamdhip64.so.7", "libamdhip64.so", "/opt/rocm/lib/libamdhip64.so"):
+        try:
+            return ctypes.CDLL(name)
+        except OSError:
+            continue
+    raise OSError("libamdhip64 not found")
+
+
+def _check(st, what):
+    assert st == 0, f"{what} failed with hipError {st}"
+
+
+def test_graph_replay_matches_eager(gpu, oracle):
+    hip = _hip()
+    V = ctypes.c_void_p
+    hip.hipStreamCreate.argtypes = [ctypes.POINTER(V)]
+    hip.hipStreamSynchronize.argtypes = [V]
+    hip.hipStreamBeginCapture.argtypes = [V, ctypes.c_int]
+    hip.hipStreamEndCapture.argtypes = [V, ctypes.POINTER(V)]
+    hip.hipGraphInstantiate.argtypes = [ctypes.POINTER(V), V, V, V, ctypes.c_size_t]
+    hip.hipGraphLaunch.argtypes = [V, V]
+    hip.hipGraphExecDestroy.argtypes = [V]
+    hip.hipGraphDestroy.argtypes = [V]
+    hip.hipStreamDestroy.argtypes = [V]
+    stream = V()
+    _check(hip.hipStreamCreate(ctypes.byref(stream)), "hipStreamCreate")
+
+    rng = np.random.default_rng(99)
+    keep, outs = [], []
+
+    def problem(M, N, K, bias):
+        w = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+        q, s = oracle.quantize_per_channel(w)
+        x = rng.normal(0, 1, (M, K)).astype(np.float16)
+        b = rng.normal(0, 0.01, N).astype(np.float32) if bias else None
+        d = dict(q=capi.DevBuf.from_array(q), s=capi.DevBuf.from_array(s), x=capi.DevBuf.from_array(x),
+                 b=capi.DevBuf.from_array(b) if bias else None, y=capi.DevBuf(M * N * 2), M=M, N=N, K=K)
+        keep.append(d)
+        outs.append(d)
+        return d
+
+    # a decode plan (M = 1, q/k/v-like), a 4-row decode call, a GEMM, a split-K GEMM
+    plan_ds = [problem(1, 896, 896, True), problem(1, 128, 896, True), problem(1, 4864, 896, False)]
+    probs = [capi.Q8Problem(out=d["y"].ptr, inp=d["x"].ptr, residual=None, weight=d["q"].ptr, scales=d["s"].ptr,
+                            bias=d["b"].ptr if d["b"] else None, M=1, N=d["N"], K=d["K"]) for d in plan_ds]
+    arr = (capi.Q8Problem * len(probs))(*probs)
+    plan = ctypes.c_uint64()
+    capi.call("vvh_plan_create", arr, len(probs), F16, F16, ctypes.byref(plan))
+    singles = [problem(4, 896, 896, True), problem(64, 512, 896, False), problem(64, 896, 4864, False)]
+
+    def issue():
+        capi.call("vvh_plan_run", plan.value, stream)
+        for d in singles:
+            capi.call("vvh_linear_q8_dev", d["y"].ptr, d["x"].ptr, d["q"].ptr, d["s"].ptr,
+                      d["b"].ptr if d["b"] else None, None, d["M"], d["N"], d["K"], F16, F16, stream)
+
+    def results():
+        return [d["y"].to_array(np.uint16, (d["M"], d["N"])) for d in outs]
+
+    issue()  # eager (also grows the split-K workspace of this stream)
+    _check(hip.hipStreamSynchronize(stream), "sync")
+    eager = results()
+    zero = np.zeros(max(d["M"] * d["N"] for d in outs), np.uint16)
+
+    graph, gexec = V(), V()
+    _check(hip.hipStreamBeginCapture(stream, 0), "hipStreamBeginCapture")
+    issue()
+    _check(hip.hipStreamEndCapture(stream, ctypes.byref(graph)), "hipStreamEndCapture")
+    _check(hip.hipGraphInstantiate(ctypes.byref(gexec), graph, None, None, 0), "hipGraphInstantiate")
+    scratch = capi.DevBuf(4096 * 4)
+    for rep in range(3):
+        for d in outs:  # clear the outputs, so each replay must write them again
+            capi.call("vvh_memcpy_h2d", d["y"].ptr, zero.ctypes.data, d["M"] * d["N"] * 2)
+        capi.call("vvh_fill_normal", scratch.ptr, F32, 4096, rep, 0.0, 1.0, None)  # eager work between replays
+        capi.sync()
+        print(f"[case] graph replay {rep}", flush=True)
+        _check(hip.hipGraphLaunch(gexec, stream), "hipGraphLaunch")
+        _check(hip.hipStreamSynchronize(stream), "sync")
+        for i, (a, b) in enumerate(zip(eager, results())):
+            np.testing.assert_array_equal(a, b, err_msg=f"replay {rep}, output {i}")
+    hip.hipGraphExecDestroy(gexec)
+    hip.hipGraphDestroy(graph)
+    capi.call("vvh_plan_destroy", plan.value)
+    hip.hipStreamDestroy(stream)
