@@ -16,9 +16,11 @@ N*K (codes) + 4N (scales) + 4N (bias) + 2K (activation row) + 2N (output)
 bracketed by device synchronisation and HIP events on the stream the kernels
 run on.
 
-Also reported (same JSON line, key "extras"): the same set in model order
-(q/k/v grouped, o, gate+up grouped, down: 96 launches per step), per-call
-times of single launches, the LM-head GEMV, prefill GEMM TFLOPS
+Also reported (same JSON line, key "extras"): the same set with the other
+decode kernel families; in model order (q/k/v grouped, o, gate+up grouped,
+down: 96 launches per step), launched from Python and captured in a HIP
+graph; per-call times of each projection (24 single calls captured in a
+graph, replayed); the LM-head GEMV, prefill GEMM TFLOPS
 (configs[3]) and the Qwen2.5-1.5B M sweep; and the reference CPU
 path (BackendCPU::linear_q8 compiled from the reference's sources,
 oracle/_ref) timed single-threaded on a bounded sample of the same workload.
@@ -62,6 +64,8 @@ def algo_bytes(M, N, K, bias, residual, act_bytes=2, out_bytes=2):
 # HIP events on the null stream (the stream every launch below uses)
 # ---------------------------------------------------------------------------
 class HipEvents:
+    """HIP events, streams and graphs through ctypes (timing plumbing only)."""
+
     def __init__(self):
         for name in ("libamdhip64.so.7", "libamdhip64.so", "/opt/rocm/lib/libamdhip64.so"):
             try:
@@ -69,20 +73,26 @@ class HipEvents:
                 break
             except OSError:
                 continue
-        h = self.hip
-        h.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
-        h.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
-        h.hipEventSynchronize.argtypes = [ctypes.c_void_p]
-        h.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
-        h.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        h, V = self.hip, ctypes.c_void_p
+        h.hipEventCreate.argtypes = [ctypes.POINTER(V)]
+        h.hipEventRecord.argtypes = [V, V]
+        h.hipEventSynchronize.argtypes = [V]
+        h.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), V, V]
+        h.hipEventDestroy.argtypes = [V]
+        h.hipStreamCreate.argtypes = [ctypes.POINTER(V)]
+        h.hipStreamSynchronize.argtypes = [V]
+        h.hipStreamBeginCapture.argtypes = [V, ctypes.c_int]
+        h.hipStreamEndCapture.argtypes = [V, ctypes.POINTER(V)]
+        h.hipGraphInstantiate.argtypes = [ctypes.POINTER(V), V, V, V, ctypes.c_size_t]
+        h.hipGraphLaunch.argtypes = [V, V]
 
     def create(self):
         e = ctypes.c_void_p()
         assert self.hip.hipEventCreate(ctypes.byref(e)) == 0
         return e
 
-    def record(self, e):
-        assert self.hip.hipEventRecord(e, None) == 0
+    def record(self, e, stream=None):
+        assert self.hip.hipEventRecord(e, stream) == 0
 
     def elapsed_ms(self, a, b):
         assert self.hip.hipEventSynchronize(b) == 0
@@ -90,15 +100,33 @@ class HipEvents:
         assert self.hip.hipEventElapsedTime(ctypes.byref(ms), a, b) == 0
         return ms.value
 
+    def stream(self):
+        s = ctypes.c_void_p()
+        assert self.hip.hipStreamCreate(ctypes.byref(s)) == 0
+        return s
 
-def timed(ev, fn, reps):
-    """Average ms per call of fn() over reps calls, HIP events around the loop."""
+    def graph(self, stream, fn):
+        """Captures fn(stream) into an instantiated graph."""
+        g, ge = ctypes.c_void_p(), ctypes.c_void_p()
+        assert self.hip.hipStreamBeginCapture(stream, 0) == 0
+        fn(stream)
+        assert self.hip.hipStreamEndCapture(stream, ctypes.byref(g)) == 0
+        assert self.hip.hipGraphInstantiate(ctypes.byref(ge), g, None, None, 0) == 0
+        return ge
+
+    def launch(self, ge, stream):
+        assert self.hip.hipGraphLaunch(ge, stream) == 0
+
+
+def timed(ev, fn, reps, stream=None):
+    """Average ms per call of fn(i) over reps calls, HIP events around the loop
+    on the stream the work runs on."""
     capi.sync()
     a, b = ev.create(), ev.create()
-    ev.record(a)
+    ev.record(a, stream)
     for i in range(reps):
         fn(i)
-    ev.record(b)
+    ev.record(b, stream)
     ms = ev.elapsed_ms(a, b)
     capi.sync()
     return ms / reps
@@ -155,9 +183,9 @@ class Linear:
         return capi.Q8Problem(out=self.y, inp=self.x, residual=self.y if self.has_res else None, weight=self.w,
                               scales=self.s, bias=self.b, M=self.M, N=self.N, K=self.K)
 
-    def run(self):
+    def run(self, stream=None):
         capi.call("vvh_linear_q8_dev", self.y, self.x, self.w, self.s, self.b,
-                  self.y if self.has_res else None, self.M, self.N, self.K, self.act, self.outd, None)
+                  self.y if self.has_res else None, self.M, self.N, self.K, self.act, self.outd, stream)
 
 
 def make_plan(linears, act=F16, outd=F16, kernel=capi.KERNEL_AUTO):
@@ -350,44 +378,51 @@ def extras(ev, sets, projs, tmp_w, args):
             seq += [("plan", make_plan([q, k, v])), ("lin", o), ("plan", make_plan([g, u])), ("lin", d)]
         order_plans.append(seq)
 
-    def model_step(i):
-        for kind, item in order_plans[i % len(order_plans)]:
+    def model_step_on(seq, stream):
+        for kind, item in seq:
             if kind == "plan":
-                capi.call("vvh_plan_run", item, None)
+                capi.call("vvh_plan_run", item, stream)
             else:
-                item.run()
+                item.run(stream)
+
+    def model_step(i):
+        model_step_on(order_plans[i % len(order_plans)], None)
 
     for i in range(5):
         model_step(i)
     reps = max(args.steps // 4, 20)
     ms = timed(ev, model_step, reps)
     out["model_order"] = {"launches_per_step": 4 * L, "ms_per_step": round(ms, 5),
-                          "GBps": round(step_bytes / (ms * 1e-3) / 1e9, 2)}
+                          "GBps": round(step_bytes / (ms * 1e-3) / 1e9, 2),
+                          "note": "launched one by one from Python: the host launch rate bounds it"}
     print(f"[bench] model order {ms * 1e3:.1f} us", file=sys.stderr, flush=True)
 
-    # (2) single launches per projection, events between consecutive calls
+    # the same 96 launches captured in a HIP graph per replica (GPU-side time,
+    # with the per-kernel launch floor of a graph replay)
+    stream = ev.stream()
+    graphs = [ev.graph(stream, lambda st, seq=seq: model_step_on(seq, st)) for seq in order_plans]
+    for i in range(5):
+        ev.launch(graphs[i % len(graphs)], stream)
+    ms = timed(ev, lambda i: ev.launch(graphs[i % len(graphs)], stream), reps, stream)
+    out["model_order_graph"] = {"launches_per_step": 4 * L, "ms_per_step": round(ms, 5),
+                                "GBps": round(step_bytes / (ms * 1e-3) / 1e9, 2)}
+    print(f"[bench] model order (graph) {ms * 1e3:.1f} us", file=sys.stderr, flush=True)
+
+    # (2) per-call time of each projection: its 24 single calls (one per layer)
+    # captured in a graph per replica, replayed; us per call = replay / 24
     nproj = len(projs)
-    events = [ev.create() for _ in range(nproj * L + 1)]
-    per = {p[0]: [] for p in projs}
-    for rep in range(6):
-        lins = sets[rep % len(sets)][1]
-        capi.sync()
-        ev.record(events[0])
-        for i, l in enumerate(lins):
-            l.run()
-            ev.record(events[i + 1])
-        capi.sync()
-        if rep < 2:
-            continue  # warm-up passes
-        for i in range(len(lins)):
-            per[projs[i % nproj][0]].append(ev.elapsed_ms(events[i], events[i + 1]) * 1e3)
     calls = {}
-    for (name, N, K, bias, res) in projs:
-        us = float(np.median(per[name]))
+    for pi, (name, N, K, bias, res) in enumerate(projs):
+        pg = [ev.graph(stream, lambda st, lins=lins: [lins[7 * l + pi].run(st) for l in range(L)])
+              for _, lins in sets]
+        for i in range(3):
+            ev.launch(pg[i % len(pg)], stream)
+        ms = timed(ev, lambda i: ev.launch(pg[i % len(pg)], stream), 30, stream)
+        us = ms * 1e3 / L
         b = algo_bytes(1, N, K, bias, res)
         calls[name] = {"N": N, "K": K, "us": round(us, 2), "GBps": round(b / (us * 1e-6) / 1e9, 1),
                        "kernel": capi.kernel_choice(1, N, K, F16, F16)}
-    out["per_call_in_sequence"] = calls
+    out["per_call_graph"] = calls
 
     # (3) LM head GEMV, configs[2]: K=896, N=151936, fp16 act, fp32 logits
     N, K = 151936, 896

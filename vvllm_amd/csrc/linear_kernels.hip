@@ -529,6 +529,7 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
     Slot ring[D];
     auto issue = [&](int u, int32_t st) {
         st = st < s1 ? st : s1 - 1;  // past the range: re-read the last step
+        st = st > 0 ? st : 0;        // (never below step 0)
         int32_t k = st * kDotStep + ch * 16;
         k = k < kmax ? k : kmax;
         ring[u].w[0] = ld_stream_g(wpA + k);
