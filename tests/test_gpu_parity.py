@@ -447,3 +447,42 @@ def test_convert_and_fill(gpu):
     capi.call("vvh_fill_normal", d.ptr, F32, n, 1234, 0.5, 0.02, None)
     capi.sync()
     np.testing.assert_array_equal(d.to_array(np.float32, n), a)
+
+
+# ---------------------------------------------------------------------------
+# weights beyond 2^31 codes (64-bit row offsets)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("M,kernel", [(1, capi.KERNEL_DOT), (8, capi.KERNEL_SKINNY), (32, capi.KERNEL_GEMM)],
+                         ids=["dot", "skinny", "gemm"])
+def test_weight_beyond_2g_codes(gpu, oracle, M, kernel):
+    """N = 2,400,000 rows of K = 896 codes (2.15 GB): weights filled and
+    quantized on the device; rows at both ends (offsets past 2^31) are checked
+    against the oracle on the same codes, copied back."""
+    N, K = 2_400_000, 896
+    print(f"[case] beyond 2^31 codes M={M} kernel={capi.KERNEL_NAMES[kernel]}", flush=True)
+    d_wf = capi.DevBuf(64 * 1024 * K * 4)         # fp32 staging, 64K rows at a time
+    d_q, d_s = capi.DevBuf(N * K), capi.DevBuf(N * 4)
+    for r0 in range(0, N, 64 * 1024):
+        rows = min(64 * 1024, N - r0)
+        capi.call("vvh_fill_normal", d_wf.ptr, F32, rows * K, 4242 + r0, 0.0, 0.02, None)
+        capi.call("vvh_quantize_per_channel", d_wf.ptr, rows, K, d_q.ptr + r0 * K, d_s.ptr + r0 * 4, None)
+    del d_wf
+    x = np.random.default_rng(5).normal(0, 1, (M, K)).astype(np.float16)
+    d_x, d_y = capi.DevBuf.from_array(x), capi.DevBuf(M * N * 2)
+    capi.set_kernel(kernel)
+    try:
+        capi.linear_q8_dev(d_y, d_x, d_q, d_s, None, None, M, N, K, F16, F16)
+        capi.sync()
+    finally:
+        capi.set_kernel(capi.KERNEL_AUTO)
+    check = list(range(0, 40)) + list(range(N - 2_000, N))
+    assert (N - 2_000) * K > 2 ** 31
+    q = np.empty((len(check), K), np.int8)
+    s = np.empty(len(check), np.float32)
+    for i, n in enumerate(check):
+        capi.call("vvh_memcpy_d2h", q[i].ctypes.data, d_q.ptr + n * K, K)
+        capi.call("vvh_memcpy_d2h", s[i:i + 1].ctypes.data, d_s.ptr + n * 4, 4)
+    y = d_y.to_array(np.float16, (M, N)).astype(np.float32)[:, check]
+    ref = oracle.linear_q8(x.astype(np.float32), q, s)
+    err = float(np.abs(y - ref).max() / np.abs(ref).max())
+    assert err <= TOL_F16, err
