@@ -284,6 +284,9 @@ def main():
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--workload", choices=("decode", "prefill"), default="decode",
+                    help="decode: configs[1] (the headline line); prefill: configs[3] gate/up GEMM only")
+    ap.add_argument("--prefill-m", type=int, default=512)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build targets one MI355X; the int8 linear path is measured on one GPU "
@@ -292,6 +295,8 @@ def main():
 
     name = capi.init(0)
     ev = HipEvents()
+    if args.workload == "prefill":
+        return prefill_main(args, ev, name)
     h, kv, inter, L = QWEN05["hidden"], QWEN05["kv"], QWEN05["inter"], QWEN05["layers"]
     projs = layer_projs(h, kv, inter)
     tmp_w = capi.DevBuf(max(inter * h, 151936 * 896, 8960 * 1536) * 4)
@@ -353,6 +358,39 @@ def main():
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)
+
+
+def prefill_main(args, ev, name):
+    """configs[3] gate/up GEMM alone (M = --prefill-m, N = 4864, K = 896, fp16
+    in and out): one JSON line in TFLOP/s against the fp16 MFMA peak.  Two
+    weight replicas alternate; the kernel runs on the null stream, where the
+    HIP events are recorded."""
+    M, N, K = args.prefill_m, QWEN05["inter"], QWEN05["hidden"]
+    tmp_w = capi.DevBuf(N * K * 4)
+    reps = []
+    for r in range(2):
+        ar = Arena(arena_size(Linear.sizes(M, N, K, False)))
+        reps.append((ar, Linear(ar, tmp_w.ptr, M, N, K, False, False, 900 + r)))
+    for i in range(args.warmup):
+        reps[i % 2][1].run()
+    ms = timed(ev, lambda i: reps[i % 2][1].run(), args.steps)
+    tf = reps[0][1].flops / (ms * 1e-3) / 1e12
+    kern = capi.kernel_choice(M, N, K, F16, F16)
+    if kern == "gemm" and K % 64 == 0:
+        kern = "k_gemm2<f16>"
+    print(f"[bench] {name}: prefill gate/up M={M} {ms * 1e3:.2f} us, {tf:.0f} TFLOP/s ({kern})",
+          file=sys.stderr, flush=True)
+    print(json.dumps({
+        "metric": "linear_q8 GEMV µs + HBM GB/s at Qwen2.5-0.5B shapes; prefill GEMM TFLOPS",
+        "value": round(tf, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8 weights x f16 activations, f32 accumulate",
+        "data": "synthetic (seeded N(0,0.02) fp32 weights quantized per channel on device; N(0,1) fp16 activations)",
+        "config": {"workload": f"configs[3]: prefill gate/up GEMM, M={M}, N={N}, K={K}, fp16 out",
+                   "M": M, "N": N, "K": K, "flops_per_step": reps[0][1].flops, "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "kernel": kern, "achieved": round(tf, 2), "peak": MFMA_F16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None},
+        "cpu_baseline": None}), flush=True)
 
 
 def extras(ev, sets, projs, tmp_w, args):

@@ -28,50 +28,9 @@
 #include <utility>
 
 #include "common.h"
+#include "device.h"
 
 namespace vvh {
-
-typedef _Float16 f16;
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef float f4 __attribute__((ext_vector_type(4)));
-typedef float f16v __attribute__((ext_vector_type(16)));
-typedef uint32_t u4 __attribute__((ext_vector_type(4)));
-
-// ---------------------------------------------------------------------------
-// element helpers
-// ---------------------------------------------------------------------------
-template <typename T>
-__device__ __forceinline__ float ld_f(const T* p) { return (float)*p; }
-
-template <typename T>
-__device__ __forceinline__ void st_f(T* p, float v) { *p = (T)v; }
-
-// Four int8 codes (one dword, little-endian k order) -> four exact fp16
-// values in two dwords.  The code is biased to u = q + 128 in [0, 255] and
-// placed in the low mantissa byte of an fp16 with exponent 2^10
-// (0x6400 | u == 1024 + u exactly); subtracting 1152 = 1024 + 128 returns q.
-__device__ __forceinline__ void i8x4_to_f16x4(uint32_t d, uint32_t& lo, uint32_t& hi)
-{
-    const uint32_t u = d ^ 0x80808080u;
-    const uint32_t a = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);  // bytes 0,1
-    const uint32_t b = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);  // bytes 2,3
-    const h2 off = {(f16)1152.0f, (f16)1152.0f};
-    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, a) - off);
-    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, b) - off);
-}
-
-// 16 codes -> two 8-wide fp16 MFMA operands (codes 0-7 and 8-15).
-__device__ __forceinline__ void i8x16_to_h8x2(const u4 w, h8& b0, h8& b1)
-{
-    uint32_t c[8];
-    i8x4_to_f16x4(w[0], c[0], c[1]);
-    i8x4_to_f16x4(w[1], c[2], c[3]);
-    i8x4_to_f16x4(w[2], c[4], c[5]);
-    i8x4_to_f16x4(w[3], c[6], c[7]);
-    b0 = __builtin_bit_cast(h8, u4{c[0], c[1], c[2], c[3]});
-    b1 = __builtin_bit_cast(h8, u4{c[4], c[5], c[6], c[7]});
-}
 
 // Epilogue for one output element, in fp32, one rounding to OT.
 template <typename OT>
@@ -84,21 +43,6 @@ __device__ __forceinline__ void store_out(const LinArgs& a, int64_t m, int64_t n
     st_f(static_cast<OT*>(a.out) + o, v);
 }
 
-// LDS reads done (lgkmcnt(0)), then s_barrier, without waiting on vector
-// memory loads.  Written with builtins so the compiler's wait-count tracking
-// sees the lgkmcnt(0); the empty asm with a memory clobber keeps the
-// compiler from moving memory accesses across the barrier.
-// The scheduling barriers keep the instruction scheduler from hoisting work
-// of the next pipeline step (which only depends on registers) above it.
-__device__ __forceinline__ void lds_barrier()
-{
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // vmcnt 63, expcnt 7: no wait; lgkmcnt 0
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-}
-
 // Weight rows are streamed exactly once: load them non-temporally so they do
 // not evict the activations from the caches.
 __device__ __forceinline__ u4 ld_stream(const int8_t* p)
@@ -106,36 +50,9 @@ __device__ __forceinline__ u4 ld_stream(const int8_t* p)
     return __builtin_nontemporal_load(reinterpret_cast<const u4*>(p));
 }
 
-// Pointers read from memory (plan tables) are generic to the compiler, which
-// then emits flat loads; those count in lgkmcnt as well as vmcnt, so every
-// wait on a scalar load would also drain the weight stream.  Kernels that
-// take their pointers from tables cast them to the global address space.
-#define VVH_GLOBAL __attribute__((address_space(1)))
-template <typename T>
-__device__ __forceinline__ const VVH_GLOBAL T* gbl(const T* p)
-{
-    return (const VVH_GLOBAL T*)p;
-}
-template <typename T>
-__device__ __forceinline__ VVH_GLOBAL T* gbl(T* p)
-{
-    return (VVH_GLOBAL T*)p;
-}
 __device__ __forceinline__ u4 ld_stream_g(const int8_t* p)
 {
     return __builtin_nontemporal_load(gbl(reinterpret_cast<const u4*>(p)));
-}
-
-// Plan tables are read-only for the whole launch.  Reading them through the
-// constant address space lets the compiler use scalar loads (lgkmcnt) even
-// though the kernel stores to global memory; otherwise it cannot rule out
-// aliasing and reads them with vector loads that join the weight stream's
-// vmcnt queue.
-#define VVH_CONST __attribute__((address_space(4)))
-template <typename T>
-__device__ __forceinline__ const VVH_CONST T* cst(const T* p)
-{
-    return (const VVH_CONST T*)p;
 }
 
 // ---------------------------------------------------------------------------
@@ -916,14 +833,6 @@ __global__ __launch_bounds__(256, 2) void k_stream(const StreamArgs sa)
 // ---------------------------------------------------------------------------
 constexpr int kLdsStride = kGemmBK + 8;
 
-__device__ __forceinline__ int64_t xcd_remap(int64_t b, int64_t total)
-{
-    constexpr int64_t X = 8;
-    const int64_t per = total / X, rem = total % X;
-    const int64_t xcd = b % X, idx = b / X;
-    return (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + idx;
-}
-
 template <typename OT>
 __global__ __launch_bounds__(256) void k_gemm(LinArgs a)
 {
@@ -1091,17 +1000,6 @@ constexpr int gemm2_loads_per_stage() { return 24 / NW; }
 constexpr int kEpiStride = kGemmBN + 4;  // fp32 row stride of an epilogue quarter
 static_assert(32 * kEpiStride * 4 <= (int)sizeof(Gemm2Stage), "epilogue quarter fits a stage buffer");
 
-// s_waitcnt with vmcnt <= v (expcnt, lgkmcnt not waited on); gfx9 encoding.
-template <int V>
-__device__ __forceinline__ void wait_vmcnt()
-{
-    static_assert(V >= 0 && V < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((V & 15) | ((V >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-__device__ __forceinline__ int swz_a(int r, int c) { return c ^ ((r >> 1) & 7); }
-__device__ __forceinline__ int swz_b(int r, int c) { return c ^ ((r >> 2) & 3); }
-
 template <int NW>
 __device__ __forceinline__ void gemm2_fill(f16* __restrict__ sa, int8_t* __restrict__ sb,
                                            const f16* const* a_src, const int8_t* const* b_src,
@@ -1113,71 +1011,6 @@ __device__ __forceinline__ void gemm2_fill(f16* __restrict__ sa, int8_t* __restr
 #pragma unroll
     for (int i = 0; i < 8 / NW; i++)
         __builtin_amdgcn_global_load_lds(b_src[i] + k0, sb + (wave * (8 / NW) + i) * 1024, 16, 0, 0);
-}
-
-// Fragments of one stage held in registers: the B codes (int8, converted
-// just before use) and the fp16 A fragments.
-template <int TI, int TJ>
-struct Gemm2Frag {
-    u4 b[2][TJ];
-    h8 a[2][2][TI];
-};
-
-template <int TI, int TJ>
-__device__ __forceinline__ void gemm2_read(const f16* __restrict__ sa, const int8_t* __restrict__ sb,
-                                           Gemm2Frag<TI, TJ>& f, int row0, int col0, int fl, int fh)
-{
-#pragma unroll
-    for (int kk2 = 0; kk2 < 2; kk2++) {
-#pragma unroll
-        for (int tj = 0; tj < TJ; tj++) {
-            const int j = col0 + tj * 32 + fl;
-            f.b[kk2][tj] = *reinterpret_cast<const u4*>(sb + j * 64 + swz_b(j, kk2 * 2 + fh) * 16);
-        }
-#pragma unroll
-        for (int h = 0; h < 2; h++)
-#pragma unroll
-            for (int ti = 0; ti < TI; ti++) {
-                const int i = row0 + ti * 32 + fl;
-                f.a[kk2][h][ti] = *reinterpret_cast<const h8*>(sa + i * 64 + swz_a(i, kk2 * 4 + fh * 2 + h) * 8);
-            }
-    }
-}
-
-// MFMAs of one stage.  The codes of the second 32-wide k slice are converted
-// while the first slice's MFMAs run, and the scheduling-group barriers
-// interleave conversion VALU with the MFMAs (each MFMA occupies the matrix
-// unit for 32 cycles, during which the wave can issue about 8 VALU ops), so
-// the conversion hides behind the matrix work instead of sitting between it.
-template <int TI, int TJ>
-__device__ __forceinline__ void gemm2_mfma(const Gemm2Frag<TI, TJ>& f, f16v (&acc)[TI][TJ])
-{
-    h8 fb[2][TJ][2];
-#pragma unroll
-    for (int tj = 0; tj < TJ; tj++) i8x16_to_h8x2(f.b[0][tj], fb[0][tj][0], fb[0][tj][1]);
-#pragma unroll
-    for (int kk2 = 0; kk2 < 2; kk2++) {
-        if (kk2 == 0) {
-#pragma unroll
-            for (int tj = 0; tj < TJ; tj++) i8x16_to_h8x2(f.b[1][tj], fb[1][tj][0], fb[1][tj][1]);
-        }
-#pragma unroll
-        for (int h = 0; h < 2; h++)
-#pragma unroll
-            for (int ti = 0; ti < TI; ti++)
-#pragma unroll
-                for (int tj = 0; tj < TJ; tj++)
-                    acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[kk2][h][ti], fb[kk2][tj][h], acc[ti][tj], 0, 0, 0);
-    }
-    // 2*2*TI*TJ MFMAs; the 20*TJ conversion ops of slice 1 go between the
-    // MFMAs of slice 0
-    constexpr int NM = 2 * TI * TJ;        // MFMAs per slice
-    constexpr int NV = (20 * TJ + NM - 1) / NM;
-#pragma unroll
-    for (int i = 0; i < NM; i++) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, NV, 0); // then conversion VALU
-    }
 }
 
 template <typename OT, int D, int NW, int WM>
