@@ -223,6 +223,33 @@ def build_decode_set(replicas, layers, projs, tmp_w, M=1):
 # ---------------------------------------------------------------------------
 # CPU baseline: reference BackendCPU::linear_q8 on the host, one thread
 # ---------------------------------------------------------------------------
+def bf16_layer_rows(projs, seed):
+    """Host BF16 bit patterns of one layer's projection weights, N(0, 0.02)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for name, N, K, bias, res in projs:
+        w = rng.standard_normal((N, K), dtype=np.float32) * np.float32(0.02)
+        out.append((name, N, K, (w.view(np.uint32) >> 16).astype(np.uint16)))
+    return out
+
+
+def cpu_ingest(projs):
+    """Host path a BF16 checkpoint takes in the reference (widen to fp32, then
+    quantize_per_channel) on one layer's weights, one thread: GB/s of BF16
+    input."""
+    from oracle import oracle as O
+    if not O.available("port"):
+        O.build(ref=False)
+    rows = bf16_layer_rows(projs, 5)
+    t0 = time.perf_counter()
+    for _, N, K, bits in rows:
+        O.ingest_bf16(bits)
+    el = time.perf_counter() - t0
+    nbytes = sum(b.nbytes for *_, b in rows)
+    return {"GBps": round(nbytes / el / 1e9, 3), "seconds": round(el, 3), "bf16_bytes": nbytes,
+            "sample": "one Qwen2.5-0.5B layer (q,k,v,o,gate,up,down), oracle restatement, one thread"}
+
+
 def cpu_baseline(lins, budget_s):
     from oracle import oracle as O
 
@@ -268,7 +295,7 @@ def cpu_baseline(lins, budget_s):
         if el >= budget_s:
             break
     return dict(value=round(per_pass * passes / el / 1e9, 3), unit="GB/s", cores=1, kind=kind,
-                ms_per_step=round(el / passes * 1e3, 3),
+                ms_per_step=round(el / passes * 1e3, 3), ingest_host_path=cpu_ingest(layer_projs(896, 128, 4864)),
                 sample=(f"{passes} full passes of the 24-layer decode projection set (168 linear_q8 calls, "
                         f"same int8 weights as the GPU run, fp32 activations) in {el:.1f} s, one thread; "
                         f"{'reference BackendCPU::linear_q8 compiled from its sources -O2 -mavx2 -mfma' if kind == 'reference' else 'oracle restatement of BackendCPU::linear_q8'}"))
@@ -513,6 +540,26 @@ def extras(ev, sets, projs, tmp_w, args):
                                      "TFLOPS": round(l.flops / (us * 1e-6) / 1e12, 2),
                                      "kernel": capi.kernel_choice(M, N, K, F16, F16)}
     out["qwen15_sweep"] = sweep
+
+    # (6) weight ingestion: host BF16 rows of 4 layers quantized into device mirrors
+    layers = [bf16_layer_rows(projs, 100 + l) for l in range(4)]
+    nbytes = sum(b.nbytes for rows in layers for *_, b in rows)
+    scales = [[np.empty(N, np.float32) for _, N, K, _b in rows] for rows in layers]
+    h = ctypes.c_uint64()
+    handles = []
+    t0 = time.perf_counter()
+    for rows, sc in zip(layers, scales):
+        for (_, N, K, bits), s_ in zip(rows, sc):
+            capi.call("vvh_weight_ingest", bits.ctypes.data, capi.BF16, None, N, K, s_.ctypes.data, ctypes.byref(h))
+            handles.append(h.value)
+    el = time.perf_counter() - t0
+    for hv in handles:
+        capi.call("vvh_weight_release", hv)
+    out["weight_ingest"] = {"layers": 4, "bf16_bytes": nbytes, "seconds": round(el, 4),
+                            "GBps": round(nbytes / el / 1e9, 2),
+                            "note": "host BF16 rows (pageable numpy memory) -> pinned staging -> device quantizer; "
+                                    "wall time including the host copies"}
+    print(f"[bench] weight ingest {nbytes / el / 1e9:.1f} GB/s", file=sys.stderr, flush=True)
     return out
 
 

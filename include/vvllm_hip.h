@@ -52,10 +52,12 @@ typedef enum vvh_status {
     VVH_ERR_UNSUPPORTED = 7,      /* valid call the library cannot serve */
 } vvh_status;
 
-/* Element types of activations / outputs / residuals. */
+/* Element types: activations, outputs and residuals are F32 or F16;
+ * weights handed to vvh_weight_ingest are F32 or BF16. */
 typedef enum vvh_dtype {
     VVH_F32 = 0,
     VVH_F16 = 1,
+    VVH_BF16 = 2,
 } vvh_dtype;
 
 /* Human-readable name of a status code (static storage). */
@@ -142,6 +144,26 @@ VVH_API int vvh_weight_register(const int8_t* host_weight, const float* host_sca
 VVH_API int vvh_weight_register_device(const int8_t* dev_weight, const float* dev_scales,
                                        const float* dev_bias, size_t N, size_t K,
                                        vvh_weight* handle);
+/* Weight ingestion: quantizes the host weight rows `host_weight` (N x K
+ * elements of src_dtype, VVH_F32 or VVH_BF16, row-major: e.g. a tensor of an
+ * mmap'ed safetensors file) straight into a new device mirror.  The rows go
+ * to the device in their stored width (2 bytes per BF16 weight), are widened
+ * to fp32 in registers (exact: BF16 bits are the high half of the fp32, as in
+ * the reference loader, src/safetensors/safetensors.cc:112-119, :135-141) and
+ * quantized by the device quantizer, so codes and scales are bit-identical to
+ * the host path it replaces: widen to fp32 on the host, then
+ * quantize_per_channel (src/model/qwen2/model.cc:27-33,
+ * src/quantize/quantize.cc:9-48).  The N scales are also written to
+ * host_scales.  host_bias (F32, optional) is mirrored as with
+ * vvh_weight_register.
+ * The mirror is keyed by the tuple (host_weight, host_scales, host_bias, N, K):
+ * a later vvh_weight_register / vvh_linear_q8 with host_weight reinterpreted
+ * as the int8 pointer and the same scales/bias pointers finds it, so
+ * Backend::linear_q8 callers can pass the ingested rows' address as the
+ * weight.  Synchronous.  Uses two 32 MB pinned host staging buffers and two
+ * device ones, allocated on the first call and kept until the process ends. */
+VVH_API int vvh_weight_ingest(const void* host_weight, int src_dtype, const float* host_bias, size_t N,
+                              size_t K, float* host_scales, vvh_weight* handle);
 /* Finds the mirror of a host weight pointer; VVH_ERR_UNKNOWN_HANDLE if none. */
 VVH_API int vvh_weight_find(const int8_t* host_weight, vvh_weight* handle);
 VVH_API int vvh_weight_release(vvh_weight handle);

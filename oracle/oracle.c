@@ -43,6 +43,26 @@ void orc_quantize_per_channel(const float* weight, size_t N, size_t K, int8_t* q
     }
 }
 
+/* src/safetensors/safetensors.cc:135-141: the BF16 bits become the high half
+ * of the fp32 word (exact). */
+void orc_bf16_to_f32(const uint16_t* src, size_t n, float* dst)
+{
+    for (size_t i = 0; i < n; i++) {
+        uint32_t bits = (uint32_t)src[i] << 16;
+        memcpy(&dst[i], &bits, sizeof(float));
+    }
+}
+
+/* load_tensor's BF16 branch (safetensors.cc:112-119) then quantize_per_channel
+ * (src/model/qwen2/model.cc:27-33). */
+void orc_ingest_bf16(const uint16_t* src, size_t N, size_t K, int8_t* q, float* scales)
+{
+    float* w = (float*)malloc(N * K * sizeof(float) + 1);
+    orc_bf16_to_f32(src, N * K, w);
+    orc_quantize_per_channel(w, N, K, q, scales);
+    free(w);
+}
+
 /* One output element of BackendCPU::linear_q8, AVX2+FMA branch,
  * src/backend/backend_naive.cc:216-274. */
 static float dot_avx2(const float* in_row, const int8_t* w_row, size_t K)

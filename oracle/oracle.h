@@ -22,6 +22,11 @@
  *   orc_linear_q8_f64         pinned: exact on integer-valued inputs (closed
  *                             form), agreement with orc_linear_q8 within the
  *                             fp32 error bound
+ *   orc_bf16_to_f32           pinned: the closed-form BF16 decoding
+ *                             (-1)^s 2^(e-127) (1 + m/128), subnormals, +-0,
+ *                             +-Inf and NaN, for all 65536 bit patterns
+ *   orc_ingest_bf16           composition of the two above (the host path
+ *                             vvh_weight_ingest replaces); pinned through them
  */
 #ifndef VVLLM_ORACLE_H
 #define VVLLM_ORACLE_H
@@ -32,6 +37,14 @@
 #ifdef __cplusplus
 extern "C" {
 #endif
+
+/* SafeTensorsLoader::bf16_to_f32, src/safetensors/safetensors.cc:135-141,
+ * applied elementwise as load_tensor does for BF16 tensors (:112-119). */
+void orc_bf16_to_f32(const uint16_t* src, size_t n, float* dst);
+
+/* The host path of a BF16 weight: widen (above), then quantize_per_channel
+ * (src/model/qwen2/model.cc:27-33 on a tensor from load_tensor). */
+void orc_ingest_bf16(const uint16_t* src, size_t N, size_t K, int8_t* q, float* scales);
 
 /* quantize_per_channel, src/quantize/quantize.cc:9-48.
  * q: [N*K] int8 codes, scales: [N]. */

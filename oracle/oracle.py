@@ -52,6 +52,8 @@ def _lib(kind: str) -> ctypes.CDLL:
         getattr(lib, pre + "linear_q8_add").argtypes = [_P, _P, _P, _P, _P, _P, _S, _S, _S]
         if kind == "port":
             lib.orc_linear_q8_f64.argtypes = [_P, _P, _P, _P, _P, _P, _S, _S, _S]
+            lib.orc_bf16_to_f32.argtypes = [_P, _S, _P]
+            lib.orc_ingest_bf16.argtypes = [_P, _S, _S, _P, _P]
         _libs[kind] = lib
     return _libs[kind]
 
@@ -72,6 +74,25 @@ def quantize_per_channel(w: np.ndarray, kind: str = "port"):
     s = np.empty((N,), np.float32)
     pre = "orc_" if kind == "port" else "ref_"
     getattr(_lib(kind), pre + "quantize_per_channel")(_ptr(w), N, K, _ptr(q), _ptr(s))
+    return q, s
+
+
+def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
+    """uint16 BF16 bit patterns -> float32 (safetensors.cc:135-141)."""
+    bits = np.ascontiguousarray(bits, dtype=np.uint16)
+    out = np.empty(bits.shape, np.float32)
+    _lib("port").orc_bf16_to_f32(_ptr(bits), bits.size, _ptr(out))
+    return out
+
+
+def ingest_bf16(bits: np.ndarray):
+    """[N, K] uint16 BF16 bit patterns -> (codes, scales) of the host path:
+    widen to fp32, then quantize_per_channel."""
+    bits = np.ascontiguousarray(bits, dtype=np.uint16)
+    N, K = bits.shape
+    q = np.empty((N, K), np.int8)
+    s = np.empty((N,), np.float32)
+    _lib("port").orc_ingest_bf16(_ptr(bits), N, K, _ptr(q), _ptr(s))
     return q, s
 
 

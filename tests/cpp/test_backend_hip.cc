@@ -200,6 +200,30 @@ void mirror_refresh()
     EXPECT_NEAR(out.download()[0], 128.0, 0.0, "mirror after forget_weight");
 }
 
+// BF16 rows ingested straight into the mirror, then used through linear_q8
+// with the rows' address as the weight (what Qwen2Model would pass).
+// Row 0 = [1, -1, 0.5, 0, ...]: scale 1/127, codes 127, -127, 64 (63.5 ties
+// away from zero), 0; x = e0 + e2 gives 127/127 + 64/127.
+void ingest_bf16()
+{
+    BackendHIP backend(false);
+    const std::size_t N = 8, K = 64;
+    std::vector<std::uint16_t> rows(N * K, 0);
+    auto bf = [](float f) { std::uint32_t u; std::memcpy(&u, &f, 4); return (std::uint16_t)(u >> 16); };
+    rows[0] = bf(1.0f); rows[1] = bf(-1.0f); rows[2] = bf(0.5f);
+    for (std::size_t j = 1; j < N; j++)
+        for (std::size_t k = 0; k < K; k++) rows[j * K + k] = bf(0.01f * (float)((int)((j * 31 + k * 7) % 21) - 10));
+    std::vector<float> scales(N), bias(N, 0.5f);
+    const int8_t* w = backend.ingest_weight(rows.data(), true, bias.data(), N, K, scales.data());
+    EXPECT_NEAR(scales[0], 1.0f / 127.0f, 0.0, "ingested scale");
+    std::vector<float> x(K, 0.0f);
+    x[0] = 1.0f; x[2] = 1.0f;
+    Act in(false, K), out(false, N);
+    in.upload(x);
+    backend.linear_q8(out.f(), in.f(), w, scales.data(), bias.data(), 1, N, K);
+    EXPECT_NEAR(out.download()[0], (127.0 + 64.0) * (1.0f / 127.0f) + 0.5, 1e-5, "ingested row 0");
+}
+
 void outside_path_throws()
 {
     BackendHIP backend(false);
@@ -228,6 +252,8 @@ int main()
     }
     std::printf("[case] mirror refresh\n"); std::fflush(stdout);
     mirror_refresh();
+    std::printf("[case] ingest bf16\n"); std::fflush(stdout);
+    ingest_bf16();
     outside_path_throws();
     if (g_failures) {
         std::fprintf(stderr, "test_backend_hip: %d failure(s)\n", g_failures);

@@ -87,6 +87,15 @@ def test_validation_before_device_use():
     assert st("vvh_fill_normal", None, 0, 10, 1, 0.0, 1.0, None) == 1
     assert st("vvh_quantize_per_channel", None, 4, 4, P, P, None) == 1
     assert st("vvh_set_kernel_override", 9) == 1
+    # weight ingestion: source dtype must be F32 or BF16, pointers and shape valid
+    sc = (ctypes.c_float * 4)()
+    assert st("vvh_weight_ingest", P, capi.F16, None, 4, 4, sc, ctypes.byref(h)) == 1
+    assert st("vvh_weight_ingest", None, capi.BF16, None, 4, 4, sc, ctypes.byref(h)) == 1
+    assert st("vvh_weight_ingest", P, capi.BF16, None, 4, 4, None, ctypes.byref(h)) == 1
+    assert st("vvh_weight_ingest", P, capi.BF16, None, 0, 4, sc, ctypes.byref(h)) == 1
+    assert st("vvh_weight_ingest", P, capi.BF16, None, 1 << 40, 1 << 40, sc, ctypes.byref(h)) == 1
+    assert st("vvh_weight_ingest", P, capi.BF16, None, 4, 4, sc, None) == 1
+    assert st("vvh_weight_ingest", P, capi.BF16, None, 4, 4, sc, ctypes.byref(h)) == 5  # before vvh_init
     stats = capi.PoolStats()
     assert st("vvh_pool_get_stats", ctypes.byref(stats)) == 0 and stats.bytes_in_use == 0
 

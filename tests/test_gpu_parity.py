@@ -486,3 +486,67 @@ def test_weight_beyond_2g_codes(gpu, oracle, M, kernel):
     ref = oracle.linear_q8(x.astype(np.float32), q, s)
     err = float(np.abs(y - ref).max() / np.abs(ref).max())
     assert err <= TOL_F16, err
+
+
+# ---------------------------------------------------------------------------
+# weight ingestion: host BF16 / F32 rows quantized straight into the mirror
+# ---------------------------------------------------------------------------
+def _bf16_rows(N, K, seed, std=0.02):
+    w = np.random.default_rng(seed).normal(0, std, (N, K)).astype(np.float32)
+    return (w.view(np.uint32) >> 16).astype(np.uint16)  # truncated to BF16 bit patterns
+
+
+@pytest.mark.parametrize("N,K", [(1, 1), (3, 1000), (896, 896), (4864, 896), (20000, 1000), (2, 9_000_000)],
+                         ids=["1x1", "3x1000", "896x896", "4864x896", "20000x1000_two_chunks", "2x9M_row_chunks"])
+def test_weight_ingest_bf16_bit_exact(gpu, oracle, N, K):
+    print(f"[case] ingest bf16 N={N} K={K}", flush=True)
+    bits = _bf16_rows(N, K, N + K)
+    if N >= 3:  # special rows: zero, NaN/Inf, exact ties
+        bits[0] = 0
+        bits[1, : min(K, 4)] = [0x7FC0, 0x7F80, 0xFF80, 0x3F80][: min(K, 4)]
+        bits[2, : min(K, 3)] = np.array([1.0, 0.5, -0.5], np.float32)[: min(K, 3)].view(np.uint32) >> 16
+    scales = np.empty(N, np.float32)
+    h = ctypes.c_uint64()
+    capi.call("vvh_weight_ingest", bits.ctypes.data, capi.BF16, None, N, K, scales.ctypes.data, ctypes.byref(h))
+    q_ref, s_ref = oracle.ingest_bf16(bits)
+    dq, ds, db = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+    n_, k_ = ctypes.c_size_t(), ctypes.c_size_t()
+    capi.call("vvh_weight_device_ptrs", h.value, ctypes.byref(dq), ctypes.byref(ds), ctypes.byref(db),
+              ctypes.byref(n_), ctypes.byref(k_))
+    assert (n_.value, k_.value, db.value) == (N, K, None)
+    q = np.empty((N, K), np.int8)
+    s = np.empty(N, np.float32)
+    capi.call("vvh_memcpy_d2h", q.ctypes.data, dq.value, N * K)
+    capi.call("vvh_memcpy_d2h", s.ctypes.data, ds.value, N * 4)
+    np.testing.assert_array_equal(s.view(np.uint32), s_ref.view(np.uint32))
+    np.testing.assert_array_equal(scales.view(np.uint32), s_ref.view(np.uint32))
+    np.testing.assert_array_equal(q, q_ref)
+    capi.call("vvh_weight_release", h.value)
+
+
+def test_weight_ingest_f32_and_linear(gpu, oracle):
+    """F32 rows ingest to the same codes as the host quantizer; the mirror
+    serves vvh_linear_q8; re-ingesting the same tuple returns the same handle,
+    and vvh_weight_register with the rows' address as the weight (what
+    Backend::linear_q8 passes) finds the ingested mirror."""
+    N, K = 896, 4864
+    w = np.random.default_rng(3).normal(0, 0.02, (N, K)).astype(np.float32)
+    b = np.random.default_rng(4).normal(0, 0.01, N).astype(np.float32)
+    scales = np.empty(N, np.float32)
+    h = ctypes.c_uint64()
+    capi.call("vvh_weight_ingest", w.ctypes.data, capi.F32, b.ctypes.data, N, K, scales.ctypes.data, ctypes.byref(h))
+    q_ref, s_ref = oracle.quantize_per_channel(w)
+    np.testing.assert_array_equal(scales, s_ref)
+    h2, h3 = ctypes.c_uint64(), ctypes.c_uint64()
+    capi.call("vvh_weight_ingest", w.ctypes.data, capi.F32, b.ctypes.data, N, K, scales.ctypes.data, ctypes.byref(h2))
+    capi.call("vvh_weight_register", w.ctypes.data, scales.ctypes.data, b.ctypes.data, N, K, ctypes.byref(h3))
+    assert h.value == h2.value == h3.value
+    for M in (1, 64):
+        x = np.random.default_rng(M).normal(0, 1, (M, K)).astype(np.float16)
+        d_x, d_y = capi.DevBuf.from_array(x), capi.DevBuf(M * N * 4)
+        capi.call("vvh_linear_q8", d_y.ptr, d_x.ptr, h.value, None, M, N, K, F16, F32, None)
+        capi.sync()
+        ref = oracle.linear_q8(x.astype(np.float32), q_ref, s_ref, b)
+        y = d_y.to_array(np.float32, (M, N))
+        assert np.abs(y - ref).max() / np.abs(ref).max() <= TOL_F16
+    capi.call("vvh_weight_release", h.value)

@@ -213,3 +213,42 @@ def test_planted_mistakes_are_caught(oracle):
     w = dq["q_ties_w"]
     rint_codes = np.clip(np.rint(w / dq["q_ties_scales"][:, None]), -128, 127).astype(np.int8)
     assert not np.array_equal(rint_codes, dq["q_ties_codes"])
+
+
+def test_bf16_widening_closed_form(oracle):
+    """orc_bf16_to_f32 (safetensors.cc:135-141) against the BF16 decoding
+    (-1)^s * 2^(e-127) * (1 + m/128), subnormals 2^-126 * m/128, +-0, +-Inf and
+    NaN, for every one of the 65536 bit patterns."""
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = oracle.bf16_to_f32(bits)
+    s = (bits >> 15).astype(np.int64)
+    e = ((bits >> 7) & 0xFF).astype(np.int64)
+    m = (bits & 0x7F).astype(np.float64)
+    sign = np.where(s == 1, -1.0, 1.0)
+    with np.errstate(over="ignore"):
+        normal = sign * np.ldexp(1.0 + m / 128.0, e - 127)
+    sub = sign * np.ldexp(m / 128.0, -126)
+    want = np.where(e == 0, sub, normal)
+    want = np.where((e == 255) & (m == 0), sign * np.inf, want)
+    nan = (e == 255) & (m != 0)
+    assert np.isnan(got[nan]).all()
+    ok = ~nan
+    np.testing.assert_array_equal(got[ok], want[ok].astype(np.float32))
+    np.testing.assert_array_equal(np.signbit(got[ok]), s[ok] == 1)  # -0 stays -0
+
+
+def test_ingest_bf16_known_answers(oracle):
+    """Host path of a BF16 weight (widen, then quantize): hand-computed rows.
+    [1, -1, 0.5, 0]: scale = 1/127, 0.5 * 127 = 63.5 ties away from zero -> 64.
+    [0, -0]: zero row -> scale 0, codes 0.  [2, 0.5, -0.25]: scale 2/127,
+    codes 127, 31.75 -> 32, -15.875 -> -16."""
+    def bf(x):  # exact BF16 patterns of values that have one
+        return (np.asarray(x, np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    q, s = oracle.ingest_bf16(bf([[1.0, -1.0, 0.5, 0.0]]))
+    assert s[0] == np.float32(1.0) / np.float32(127.0)
+    assert q.tolist() == [[127, -127, 64, 0]]
+    q, s = oracle.ingest_bf16(bf([[0.0, -0.0, 0.0]]))
+    assert s[0] == 0.0 and q.tolist() == [[0, 0, 0]]
+    q, s = oracle.ingest_bf16(bf([[2.0, 0.5, -0.25]]))
+    assert s[0] == np.float32(2.0) / np.float32(127.0)
+    assert q.tolist() == [[127, 32, -16]]

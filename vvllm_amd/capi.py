@@ -15,7 +15,7 @@ import numpy as np
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libvvllm_hip.so")
 
-F32, F16 = 0, 1
+F32, F16, BF16 = 0, 1, 2
 KERNEL_AUTO, KERNEL_GENERIC, KERNEL_GEMV_F32, KERNEL_SKINNY, KERNEL_GEMM, KERNEL_STREAM, KERNEL_DOT = range(7)
 KERNEL_NAMES = {0: "auto", 1: "generic", 2: "gemv_f32", 3: "skinny", 4: "gemm", 5: "stream", 6: "dot"}
 STATUS = {0: "VVH_OK", 1: "VVH_ERR_INVALID_ARG", 2: "VVH_ERR_NO_DEVICE", 3: "VVH_ERR_OUT_OF_MEMORY",
@@ -54,6 +54,7 @@ SIGNATURES = {
     "vvh_pool_release_cached": (c_int, []),
     "vvh_pool_get_stats": (c_int, [POINTER(PoolStats)]),
     "vvh_weight_register": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_size_t, POINTER(c_uint64)]),
+    "vvh_weight_ingest": (c_int, [c_void_p, c_int, c_void_p, c_size_t, c_size_t, c_void_p, POINTER(c_uint64)]),
     "vvh_weight_register_device": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_size_t, POINTER(c_uint64)]),
     "vvh_weight_find": (c_int, [c_void_p, POINTER(c_uint64)]),
     "vvh_weight_release": (c_int, [c_uint64]),

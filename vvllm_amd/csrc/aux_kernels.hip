@@ -21,15 +21,25 @@ typedef _Float16 f16;
 __device__ __forceinline__ float ref_max(float a, float b) { return (a < b) ? b : a; }
 __device__ __forceinline__ float ref_min(float a, float b) { return (b < a) ? b : a; }
 
-__global__ __launch_bounds__(256) void k_quantize(const float* __restrict__ w, int64_t N, int64_t K,
+// Source elements: fp32, or BF16 bits widened exactly to fp32 (the bits
+// become the high half of the fp32 word, as the reference's loader does,
+// src/safetensors/safetensors.cc:135-141).
+__device__ __forceinline__ float src_f32(const float* w, int64_t i) { return w[i]; }
+__device__ __forceinline__ float src_f32(const uint16_t* w, int64_t i)
+{
+    return __builtin_bit_cast(float, (uint32_t)w[i] << 16);
+}
+
+template <typename ST>
+__global__ __launch_bounds__(256) void k_quantize(const ST* __restrict__ w, int64_t N, int64_t K,
                                                   int8_t* __restrict__ q, float* __restrict__ scales)
 {
     __shared__ float part[4];
     __shared__ float row_scale;
     for (int64_t row = blockIdx.x; row < N; row += gridDim.x) {
-        const float* wr = w + row * K;
+        const ST* wr = w + row * K;
         float mx = 0.0f;
-        for (int64_t k = threadIdx.x; k < K; k += 256) mx = ref_max(mx, __builtin_fabsf(wr[k]));
+        for (int64_t k = threadIdx.x; k < K; k += 256) mx = ref_max(mx, __builtin_fabsf(src_f32(wr, k)));
         for (int off = 32; off > 0; off >>= 1) mx = ref_max(mx, __shfl_xor(mx, off));
         if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = mx;
         __syncthreads();
@@ -47,7 +57,7 @@ __global__ __launch_bounds__(256) void k_quantize(const float* __restrict__ w, i
         } else {
             const float inv_scale = 1.0f / scale;
             for (int64_t k = threadIdx.x; k < K; k += 256) {
-                float val = wr[k] * inv_scale;
+                float val = src_f32(wr, k) * inv_scale;
                 val = ref_max(-128.0f, ref_min(127.0f, roundf(val)));
                 qr[k] = (int8_t)val;
             }
@@ -56,11 +66,16 @@ __global__ __launch_bounds__(256) void k_quantize(const float* __restrict__ w, i
     }
 }
 
-int launch_quantize(const float* w, int64_t N, int64_t K, int8_t* q, float* scales, void* stream)
+int launch_quantize(const void* w, int src_dtype, int64_t N, int64_t K, int8_t* q, float* scales, void* stream)
 {
     const int64_t grid = N < 65536 ? N : 65536;
-    hipLaunchKernelGGL(k_quantize, dim3((unsigned)grid), dim3(256), 0, static_cast<hipStream_t>(stream),
-                       w, N, K, q, scales);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (src_dtype == VVH_BF16)
+        hipLaunchKernelGGL(k_quantize<uint16_t>, dim3((unsigned)grid), dim3(256), 0, s,
+                           static_cast<const uint16_t*>(w), N, K, q, scales);
+    else
+        hipLaunchKernelGGL(k_quantize<float>, dim3((unsigned)grid), dim3(256), 0, s,
+                           static_cast<const float*>(w), N, K, q, scales);
     return (int)hipGetLastError();
 }
 

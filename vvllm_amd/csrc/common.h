@@ -127,7 +127,8 @@ int launch_splitk_reduce(const LinArgs& a, int out, void* stream);
 int launch_stream(const StreamArgs& s, int depth, int max_m, int out, int64_t blocks, void* stream);
 
 // Auxiliary kernels (aux_kernels.hip).
-int launch_quantize(const float* w, int64_t N, int64_t K, int8_t* q, float* scales, void* stream);
+// w: N x K elements of src_dtype (VVH_F32 or VVH_BF16)
+int launch_quantize(const void* w, int src_dtype, int64_t N, int64_t K, int8_t* q, float* scales, void* stream);
 int launch_convert(void* dst, int dst_dtype, const void* src, int src_dtype, int64_t n,
                    void* stream);
 int launch_fill_normal(void* dst, int dtype, int64_t n, uint64_t seed, float mean, float std,

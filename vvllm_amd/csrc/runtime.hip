@@ -78,6 +78,7 @@ struct WeightEntry {
     const int8_t* w = nullptr;
     const float* scales = nullptr;
     const float* bias = nullptr;
+    int src_dtype = -1;                // vvh_weight_ingest: dtype of the host rows
 };
 std::mutex g_wmu;
 std::unordered_map<vvh_weight, WeightEntry> g_weights;
@@ -699,7 +700,7 @@ VVH_API int vvh_weight_register(const int8_t* host_weight, const float* host_sca
     if (hb != g_weight_by_host.end()) {
         const WeightEntry& e = g_weights.at(hb->second);
         if (e.host_scales == host_scales && e.host_bias == host_bias && e.N == N && e.K == K) {
-            *handle = hb->second;
+            *handle = hb->second;  // also an ingested mirror: its codes came from these rows
             return VVH_OK;
         }
         drop_weight_locked(hb->second);  // same host buffer, new contents/shape
@@ -735,6 +736,147 @@ VVH_API int vvh_weight_register(const int8_t* host_weight, const float* host_sca
     w.bytes = bytes;
     w.w = reinterpret_cast<const int8_t*>(b);
     w.scales = reinterpret_cast<const float*>(b + off_s);
+    w.bias = host_bias ? reinterpret_cast<const float*>(b + off_b) : nullptr;
+    const vvh_weight h = g_next_weight++;
+    g_weights.emplace(h, w);
+    g_weight_by_host[host_weight] = h;
+    *handle = h;
+    return VVH_OK;
+}
+
+// Weight ingestion: host rows of F32 or BF16 go to the device in their stored
+// width through two pinned staging buffers (the CPU fills one while the DMA
+// engine drains the other), are widened in registers and quantized into the
+// new mirror.  The reference widens BF16 to fp32 on the host
+// (src/safetensors/safetensors.cc:112-119) and quantizes on the host
+// (src/model/qwen2/model.cc:27-33, src/quantize/quantize.cc:9-48).
+namespace {
+constexpr std::size_t kIngestChunk = std::size_t(32) << 20;  // bytes of source rows per chunk
+
+// Staging of vvh_weight_ingest, allocated on first use and kept (pinning
+// host memory costs milliseconds); used under g_wmu.  A row longer than the
+// chunk grows it.
+struct IngestStaging {
+    void* host[2] = {nullptr, nullptr};
+    void* dev[2] = {nullptr, nullptr};
+    hipEvent_t copied[2] = {nullptr, nullptr};
+    hipStream_t stream = nullptr;
+    std::size_t bytes = 0;
+
+    void release()
+    {
+        if (stream) (void)hipStreamSynchronize(stream);
+        for (int i = 0; i < 2; i++) {
+            if (host[i]) (void)hipHostFree(host[i]);
+            if (dev[i]) (void)hipFree(dev[i]);
+            host[i] = dev[i] = nullptr;
+        }
+        bytes = 0;
+    }
+    hipError_t ensure(std::size_t need)
+    {
+        hipError_t e = hipSuccess;
+        if (!stream && (e = hipStreamCreate(&stream)) != hipSuccess) return e;
+        for (int i = 0; i < 2; i++)
+            if (!copied[i] && (e = hipEventCreateWithFlags(&copied[i], hipEventDisableTiming)) != hipSuccess) return e;
+        if (bytes >= need) return hipSuccess;
+        release();
+        for (int i = 0; i < 2; i++) {
+            if ((e = hipHostMalloc(&host[i], need, hipHostMallocDefault)) != hipSuccess ||
+                (e = hipMalloc(&dev[i], need)) != hipSuccess) {
+                release();
+                return e;
+            }
+        }
+        bytes = need;
+        return hipSuccess;
+    }
+};
+IngestStaging g_ingest;
+}  // namespace
+
+VVH_API int vvh_weight_ingest(const void* host_weight, int src_dtype, const float* host_bias, size_t N, size_t K,
+                              float* host_scales, vvh_weight* handle)
+{
+    if (!handle) return fail(VVH_ERR_INVALID_ARG, "handle is null");
+    *handle = 0;
+    if (src_dtype != VVH_F32 && src_dtype != VVH_BF16) return fail(VVH_ERR_INVALID_ARG, "bad source dtype %d", src_dtype);
+    if (!host_weight || !host_scales) return fail(VVH_ERR_INVALID_ARG, "weight or scales is null");
+    const std::size_t es = src_dtype == VVH_BF16 ? 2 : 4;
+    uint64_t nk, src_bytes;
+    if (N == 0 || K == 0 || !mul_ok(N, K, &nk) || !mul_ok(nk, es, &src_bytes))
+        return fail(VVH_ERR_INVALID_ARG, "bad shape N %zu K %zu", N, K);
+    REQUIRE_INIT();
+    std::lock_guard<std::mutex> lock(g_wmu);
+    auto hb = g_weight_by_host.find(host_weight);
+    if (hb != g_weight_by_host.end()) {
+        const WeightEntry& e = g_weights.at(hb->second);
+        if (e.host_scales == host_scales && e.host_bias == host_bias && e.N == N && e.K == K &&
+            e.src_dtype == src_dtype) {
+            *handle = hb->second;
+            return VVH_OK;
+        }
+        drop_weight_locked(hb->second);
+    }
+    const std::size_t off_s = align_up(nk);
+    const std::size_t off_b = off_s + align_up(N * sizeof(float));
+    const std::size_t bytes = off_b + (host_bias ? align_up(N * sizeof(float)) : 0);
+    void* base = nullptr;
+    hipError_t e = hipMalloc(&base, bytes);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        if (g_pool.release_cached() == 0 && hipMalloc(&base, bytes) == hipSuccess) {
+            e = hipSuccess;
+        } else {
+            (void)hipGetLastError();
+            return fail_hip(e, "weight mirror hipMalloc");
+        }
+    }
+    char* b = static_cast<char*>(base);
+    int8_t* codes = reinterpret_cast<int8_t*>(b);
+    float* scales = reinterpret_cast<float*>(b + off_s);
+    const std::size_t row_bytes = K * es;
+    const std::size_t rows_per = std::max<std::size_t>(1, std::min<std::size_t>(N, kIngestChunk / row_bytes));
+    const std::size_t chunk = rows_per * row_bytes;
+    {
+        IngestStaging& st = g_ingest;
+        auto bail = [&](hipError_t err, const char* what) {
+            (void)hipGetLastError();
+            (void)hipFree(base);
+            return fail_hip(err, what);
+        };
+        if ((e = st.ensure(std::max(chunk, kIngestChunk))) != hipSuccess) return bail(e, "ingest: staging");
+        const char* src = static_cast<const char*>(host_weight);
+        int c = 0;
+        for (std::size_t r0 = 0; r0 < N; r0 += rows_per, c ^= 1) {
+            const std::size_t rows = std::min(rows_per, N - r0);
+            // the copy that last read this pinned buffer must be done
+            if ((e = hipEventSynchronize(st.copied[c])) != hipSuccess) return bail(e, "ingest: wait");
+            std::memcpy(st.host[c], src + r0 * row_bytes, rows * row_bytes);
+            int k = 0;
+            if ((e = hipMemcpyAsync(st.dev[c], st.host[c], rows * row_bytes, hipMemcpyHostToDevice, st.stream)) !=
+                    hipSuccess ||
+                (e = hipEventRecord(st.copied[c], st.stream)) != hipSuccess ||
+                (k = launch_quantize(st.dev[c], src_dtype, (int64_t)rows, (int64_t)K, codes + r0 * K, scales + r0,
+                                     st.stream)) != 0)
+                return bail(k ? (hipError_t)k : e, "ingest: copy / quantize");
+        }
+        if ((e = hipStreamSynchronize(st.stream)) != hipSuccess ||
+            (e = hipMemcpy(host_scales, scales, N * sizeof(float), hipMemcpyDeviceToHost)) != hipSuccess ||
+            (host_bias && (e = hipMemcpy(b + off_b, host_bias, N * sizeof(float), hipMemcpyHostToDevice)) != hipSuccess))
+            return bail(e, "ingest: finish");
+    }
+    WeightEntry w;
+    w.host_w = host_weight;
+    w.host_scales = host_scales;
+    w.host_bias = host_bias;
+    w.N = N;
+    w.K = K;
+    w.src_dtype = src_dtype;
+    w.base = base;
+    w.bytes = bytes;
+    w.w = codes;
+    w.scales = scales;
     w.bias = host_bias ? reinterpret_cast<const float*>(b + off_b) : nullptr;
     const vvh_weight h = g_next_weight++;
     g_weights.emplace(h, w);
@@ -993,7 +1135,7 @@ VVH_API int vvh_quantize_per_channel(const float* dev_weight, size_t N, size_t K
     if (!dev_scales || (K > 0 && (!dev_weight || !dev_codes)))
         return fail(VVH_ERR_INVALID_ARG, "null pointer");
     REQUIRE_INIT();
-    const int e = launch_quantize(dev_weight, (int64_t)N, (int64_t)K, dev_codes, dev_scales, stream);
+    const int e = launch_quantize(dev_weight, VVH_F32, (int64_t)N, (int64_t)K, dev_codes, dev_scales, stream);
     return e == 0 ? VVH_OK : fail_hip((hipError_t)e, "quantize launch");
 }
 

@@ -92,6 +92,14 @@ void BackendHIP::fp16_to_fp32(float* dst, const void* src, std::size_t n)
     check(vvh_convert(dst, VVH_F32, src, VVH_F16, n, nullptr), "fp16_to_fp32");
 }
 
+const int8_t* BackendHIP::ingest_weight(const void* host_rows, bool bf16, const float* bias, std::size_t N,
+                                        std::size_t K, float* scales)
+{
+    vvh_weight h = 0;
+    check(vvh_weight_ingest(host_rows, bf16 ? VVH_BF16 : VVH_F32, bias, N, K, scales, &h), "ingest_weight");
+    return static_cast<const int8_t*>(host_rows);
+}
+
 void BackendHIP::forget_weight(const int8_t* host_weight)
 {
     vvh_weight h = 0;

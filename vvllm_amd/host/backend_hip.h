@@ -49,6 +49,17 @@ public:
     void fp32_to_fp16(void* dst, const float* src, std::size_t n) override;
     void fp16_to_fp32(float* dst, const void* src, std::size_t n) override;
 
+    // Quantizes host weight rows (BF16 when bf16, else F32; N x K, e.g. an
+    // mmap'ed safetensors tensor) straight into the HBM mirror and writes the
+    // N scales to `scales`.  Returns the pointer to pass as `weight` (with
+    // the same scales and bias pointers) to linear_q8 / linear_q8_add: the
+    // call then finds this mirror, with codes bit-identical to
+    // quantize_per_channel of the widened rows.  Replaces, for this backend,
+    // the host widening and quantization of Qwen2Model::load_weights
+    // (src/model/qwen2/model.cc:27-33).
+    const int8_t* ingest_weight(const void* host_rows, bool bf16, const float* bias, std::size_t N,
+                                std::size_t K, float* scales);
+
     // Drops the HBM mirror of a host weight (e.g. before its buffer is freed
     // and reused); the next linear_q8 on that pointer uploads again.
     void forget_weight(const int8_t* host_weight);
