@@ -255,6 +255,62 @@ VVH_API int vvh_fill_normal(void* dst, int dtype, size_t n, uint64_t seed, float
 
 /* ---- dispatch introspection ---------------------------------------------- */
 /* Kernel families of the linear path. */
+/* ---- the other operators of a decode step ----------------------------------
+ * Device restatements of the Backend operators transformer_forward
+ * (include/vvllm/model/transformer.h:126-189) calls besides linear_q8, as
+ * BackendCPU computes them (src/backend/backend_naive.cc; cited per entry).
+ * Activations / outputs are device arrays of `dtype` (VVH_F32 or VVH_F16);
+ * all arithmetic is fp32 with one rounding on store.  Weight-like inputs
+ * (norm weights, biases, tables) are device fp32 arrays, e.g. from
+ * vvh_mirror_f32.  Replaces BackendCUDA's versions
+ * (src/backend/backend_cuda.cc:101-356) and their kernels. */
+typedef enum vvh_op {
+    VVH_OP_ADD = 0,       /* out = x + y          (backend_naive.cc:44-50) */
+    VVH_OP_MUL = 1,       /* out = x * y          (:52-58) */
+    VVH_OP_SILU = 2,      /* out = x / (1 + e^-x)  (:60-66) */
+    VVH_OP_SILU_MUL = 3,  /* out = silu(x) * y    (:293-300) */
+} vvh_op;
+VVH_API int vvh_eltwise(int op, void* out, const void* x, const void* y, size_t n, int dtype, void* stream);
+/* `rows` rows of RMSNorm: out = x / sqrt(mean(x^2) + eps) * weight (:68-76). */
+VVH_API int vvh_rms_norm(void* out, const void* x, const float* dev_weight, size_t rows, size_t n, float eps,
+                         int dtype, void* stream);
+/* `rows` rows of softmax (:78-91). */
+VVH_API int vvh_softmax(void* out, const void* x, size_t rows, size_t n, int dtype, void* stream);
+/* Split-half RoPE in place on q [seq_len, num_heads, head_dim] and
+ * k [seq_len, num_kv_heads, head_dim], positions pos.. (:93-137). */
+VVH_API int vvh_rope(void* q, void* k, size_t seq_len, size_t num_heads, size_t num_kv_heads, size_t head_dim,
+                     size_t pos, float theta, int dtype, void* stream);
+/* out[0..hidden) = table[token_id] (fp32 table [vocab, hidden]) (:338-342). */
+VVH_API int vvh_embedding(void* out, const float* dev_table, size_t token_id, size_t hidden, size_t vocab, int dtype,
+                          void* stream);
+/* Causal attention for n_q consecutive queries (:344-378): query s of
+ * q [n_q, num_heads, head_dim] attends to positions 0 .. len0 + s - 1 of
+ * k, v [*, num_kv_heads, head_dim] (head h reads kv head
+ * h / (num_heads / num_kv_heads)); out [n_q, num_heads * head_dim].  One call
+ * replaces the model's per-query loop (transformer.h:168-173).  head_dim <= 256,
+ * len0 + n_q - 1 <= 16000. */
+VVH_API int vvh_attention(void* out, const void* q, const void* k, const void* v, size_t n_q, size_t len0,
+                          size_t num_heads, size_t num_kv_heads, size_t head_dim, float scale, int dtype,
+                          void* stream);
+/* Dense linear with fp32 or fp16 weights (wdtype): out[M,N] = x[M,K] . W[N,K]^T
+ * + bias[N] (+ residual[M,N], may alias out) -- Backend::linear / linear_add
+ * (:139-156, :302-320); the fp32 model path and the tied LM head. */
+VVH_API int vvh_dense(void* out, const void* x, const void* dev_weight, int wdtype, const float* dev_bias,
+                      const void* residual, size_t M, size_t N, size_t K, int dtype, void* stream);
+/* out[M,N] = A[M,K] . B[K,N], B fp32 row-major (:25-42). */
+VVH_API int vvh_matmul(void* out, const void* A, const float* dev_B, size_t M, size_t N, size_t K, int dtype,
+                       void* stream);
+/* Greedy sampling: *dev_index = the first index of the maximum of n fp32
+ * logits, as std::max_element (src/sampler/sampler.cc:21-25). */
+VVH_API int vvh_argmax(const float* logits, size_t n, int32_t* dev_index, void* stream);
+/* Device copy of a host fp32 array of n elements, as fp32 or converted to
+ * fp16 (as_dtype), made on first use and kept (BackendCUDA::cache_weight /
+ * cache_weight_as_fp16, backend_cuda.cc:51-95).  Keyed by (host, as_dtype):
+ * the same host pointer with a different n is re-uploaded. */
+VVH_API int vvh_mirror_f32(const float* host, size_t n, int as_dtype, const void** dev);
+/* Drops the mirrors of a host array (both dtypes). */
+VVH_API int vvh_mirror_release(const float* host);
+
 typedef enum vvh_kernel {
     VVH_KERNEL_AUTO = 0,      /* size-based choice (default) */
     VVH_KERNEL_GENERIC = 1,   /* any shape / alignment, one thread per output */

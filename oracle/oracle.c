@@ -142,3 +142,143 @@ void orc_linear_q8_f64(double* out, const float* inp, const int8_t* weight, cons
 }
 
 int orc_threads(void) { return 1; }
+
+/* ---- the other BackendCPU operators (src/backend/backend_naive.cc) ---- */
+
+/* :44-50, :52-58 */
+void orc_add(float* out, const float* x, const float* y, size_t n)
+{
+    for (size_t i = 0; i < n; i++) out[i] = x[i] + y[i];
+}
+void orc_mul(float* out, const float* x, const float* y, size_t n)
+{
+    for (size_t i = 0; i < n; i++) out[i] = x[i] * y[i];
+}
+
+/* :60-66: x * (1 / (1 + exp(-x))) */
+void orc_silu(float* out, const float* x, size_t n)
+{
+    for (size_t i = 0; i < n; i++) out[i] = x[i] * (1 / (1.0f + expf(-x[i])));
+}
+
+/* :293-300: (v / (1 + exp(-v))) * up */
+void orc_silu_mul(float* out, const float* gate, const float* up, size_t n)
+{
+    for (size_t i = 0; i < n; i++) {
+        float v = gate[i];
+        out[i] = (v / (1.0f + expf(-v))) * up[i];
+    }
+}
+
+/* :68-76: sequential sum of squares (std::accumulate), sqrt(sum / n + eps),
+ * x / rms * w */
+void orc_rms_norm(float* out, const float* x, const float* weight, size_t n, float eps)
+{
+    float sum = 0.0f;
+    for (size_t i = 0; i < n; i++) sum = sum + x[i] * x[i];
+    float rms = sqrtf(sum / (float)n + eps);
+    for (size_t i = 0; i < n; i++) out[i] = x[i] / rms * weight[i];
+}
+
+/* :78-91 */
+void orc_softmax(float* out, const float* x, size_t n)
+{
+    float max_val = x[0];
+    for (size_t i = 1; i < n; i++)
+        if (max_val < x[i]) max_val = x[i];
+    float sum = 0.0f;
+    for (size_t i = 0; i < n; i++) {
+        out[i] = expf(x[i] - max_val);
+        sum += out[i];
+    }
+    for (size_t i = 0; i < n; i++) out[i] /= sum;
+}
+
+/* :93-137: split-half pairs (i, i + half) of every q and k head */
+static void rope_heads(float* base, size_t heads, size_t head_dim, size_t position, float theta)
+{
+    size_t half = head_dim / 2;
+    for (size_t h = 0; h < heads; h++) {
+        float* head = base + h * head_dim;
+        for (size_t i = 0; i < half; i++) {
+            float freq = 1.0f / powf(theta, (float)(2 * i) / (float)head_dim);
+            float angle = (float)position * freq;
+            float cos_a = cosf(angle);
+            float sin_a = sinf(angle);
+            float x0 = head[i];
+            float x1 = head[i + half];
+            head[i] = x0 * cos_a - x1 * sin_a;
+            head[i + half] = x0 * sin_a + x1 * cos_a;
+        }
+    }
+}
+void orc_rope(float* q, float* k, size_t seq_len, size_t num_heads, size_t num_kv_heads, size_t head_dim,
+              size_t pos, float theta)
+{
+    for (size_t s = 0; s < seq_len; s++) {
+        rope_heads(q + s * num_heads * head_dim, num_heads, head_dim, pos + s, theta);
+        rope_heads(k + s * num_kv_heads * head_dim, num_kv_heads, head_dim, pos + s, theta);
+    }
+}
+
+/* :139-156: sum starts at the bias, k in order */
+void orc_linear(float* out, const float* inp, const float* weight, const float* bias, size_t M, size_t N, size_t K)
+{
+    for (size_t i = 0; i < M; i++)
+        for (size_t j = 0; j < N; j++) {
+            float sum = bias ? bias[j] : 0.0f;
+            for (size_t k = 0; k < K; k++) sum += inp[i * K + k] * weight[j * K + k];
+            out[i * N + j] = sum;
+        }
+}
+
+/* :302-320: sum starts at the residual, then the bias, k in order */
+void orc_linear_add(float* out, const float* inp, const float* weight, const float* bias, const float* residual,
+                    size_t M, size_t N, size_t K)
+{
+    for (size_t i = 0; i < M; i++)
+        for (size_t j = 0; j < N; j++) {
+            float sum = residual[i * N + j];
+            if (bias) sum += bias[j];
+            for (size_t k = 0; k < K; k++) sum += inp[i * K + k] * weight[j * K + k];
+            out[i * N + j] = sum;
+        }
+}
+
+/* :25-42 */
+void orc_matmul(float* out, const float* A, const float* B, size_t M, size_t N, size_t K)
+{
+    for (size_t i = 0; i < M; i++)
+        for (size_t j = 0; j < N; j++) {
+            float sum = 0.0f;
+            for (size_t k = 0; k < K; k++) sum += A[i * K + k] * B[k * N + j];
+            out[i * N + j] = sum;
+        }
+}
+
+/* :344-378: per head, scores = (q . k) * scale, softmax, then
+ * out[d] += p_t * v_t[d] in t order */
+void orc_causal_attention(float* out, const float* q, size_t q_idx, const float* k, const float* v, size_t attend_len,
+                          size_t num_heads, size_t num_kv_heads, size_t head_dim, float scale)
+{
+    size_t groups = num_heads / num_kv_heads;
+    float* scores = (float*)malloc(attend_len * sizeof(float) + 4);
+    for (size_t h = 0; h < num_heads; h++) {
+        size_t kv_h = h / groups;
+        const float* q_head = q + q_idx * num_heads * head_dim + h * head_dim;
+        for (size_t t = 0; t < attend_len; t++) {
+            const float* k_head = k + t * num_kv_heads * head_dim + kv_h * head_dim;
+            float dot = 0.0f;
+            for (size_t d = 0; d < head_dim; d++) dot += q_head[d] * k_head[d];
+            scores[t] = dot * scale;
+        }
+        orc_softmax(scores, scores, attend_len);
+        float* head_out = out + h * head_dim;
+        memset(head_out, 0, head_dim * sizeof(float));
+        for (size_t t = 0; t < attend_len; t++) {
+            const float* v_head = v + t * num_kv_heads * head_dim + kv_h * head_dim;
+            for (size_t d = 0; d < head_dim; d++) head_out[d] += scores[t] * v_head[d];
+        }
+    }
+    free(scores);
+}

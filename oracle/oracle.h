@@ -27,6 +27,11 @@
  *                             +-Inf and NaN, for all 65536 bit patterns
  *   orc_ingest_bf16           composition of the two above (the host path
  *                             vvh_weight_ingest replaces); pinned through them
+ *   orc_add/mul/silu/silu_mul, orc_rms_norm, orc_softmax, orc_rope,
+ *   orc_linear, orc_linear_add, orc_matmul, orc_causal_attention
+ *                             pinned: bit-exact vs the reference's BackendCPU
+ *                             compiled in place (_ref), plus closed forms
+ *                             (tests/test_oracle.py)
  */
 #ifndef VVLLM_ORACLE_H
 #define VVLLM_ORACLE_H
@@ -71,6 +76,23 @@ void orc_linear_q8_f64(double* out, const float* inp, const int8_t* weight, cons
 /* Number of threads the oracle uses: always 1 (the reference is
  * single-threaded, README.md:282). */
 int orc_threads(void);
+
+/* The other BackendCPU operators, src/backend/backend_naive.cc (line ranges
+ * in oracle.c). */
+void orc_add(float* out, const float* x, const float* y, size_t n);
+void orc_mul(float* out, const float* x, const float* y, size_t n);
+void orc_silu(float* out, const float* x, size_t n);
+void orc_silu_mul(float* out, const float* gate, const float* up, size_t n);
+void orc_rms_norm(float* out, const float* x, const float* weight, size_t n, float eps);
+void orc_softmax(float* out, const float* x, size_t n);
+void orc_rope(float* q, float* k, size_t seq_len, size_t num_heads, size_t num_kv_heads, size_t head_dim,
+              size_t pos, float theta);
+void orc_linear(float* out, const float* inp, const float* weight, const float* bias, size_t M, size_t N, size_t K);
+void orc_linear_add(float* out, const float* inp, const float* weight, const float* bias, const float* residual,
+                    size_t M, size_t N, size_t K);
+void orc_matmul(float* out, const float* A, const float* B, size_t M, size_t N, size_t K);
+void orc_causal_attention(float* out, const float* q, size_t q_idx, const float* k, const float* v, size_t attend_len,
+                          size_t num_heads, size_t num_kv_heads, size_t head_dim, float scale);
 
 #ifdef __cplusplus
 }

@@ -50,6 +50,13 @@ def _lib(kind: str) -> ctypes.CDLL:
         getattr(lib, pre + "quantize_per_channel").argtypes = [_P, _S, _S, _P, _P]
         getattr(lib, pre + "linear_q8").argtypes = [_P, _P, _P, _P, _P, _S, _S, _S]
         getattr(lib, pre + "linear_q8_add").argtypes = [_P, _P, _P, _P, _P, _P, _S, _S, _S]
+        F = ctypes.c_float
+        for nm, at in (("add", [_P, _P, _P, _S]), ("mul", [_P, _P, _P, _S]), ("silu", [_P, _P, _S]),
+                       ("silu_mul", [_P, _P, _P, _S]), ("rms_norm", [_P, _P, _P, _S, F]), ("softmax", [_P, _P, _S]),
+                       ("rope", [_P, _P, _S, _S, _S, _S, _S, F]), ("linear", [_P, _P, _P, _P, _S, _S, _S]),
+                       ("linear_add", [_P, _P, _P, _P, _P, _S, _S, _S]), ("matmul", [_P, _P, _P, _S, _S, _S]),
+                       ("causal_attention", [_P, _P, _S, _P, _P, _S, _S, _S, _S, F])):
+            getattr(lib, pre + nm).argtypes = at
         if kind == "port":
             lib.orc_linear_q8_f64.argtypes = [_P, _P, _P, _P, _P, _P, _S, _S, _S]
             lib.orc_bf16_to_f32.argtypes = [_P, _S, _P]
@@ -128,4 +135,81 @@ def linear_q8_f64(x, q, scales, bias=None, residual=None):
     out = np.empty((M, N), np.float64)
     _lib("port").orc_linear_q8_f64(_ptr(out), _ptr(x), _ptr(q), _ptr(_f32(scales)), _ptr(_f32(bias)),
                                    _ptr(_f32(residual)), M, N, K)
+    return out
+
+
+# ---- the other BackendCPU operators (src/backend/backend_naive.cc) ----
+def _fn(kind, name):
+    return getattr(_lib(kind), ("orc_" if kind == "port" else "ref_") + name)
+
+
+def eltwise(op: str, x, y=None, kind: str = "port"):
+    """op in add / mul / silu / silu_mul (y = up for silu_mul)."""
+    x = _f32(x).ravel()
+    out = np.empty_like(x)
+    if op == "silu":
+        _fn(kind, op)(_ptr(out), _ptr(x), x.size)
+    else:
+        y = _f32(y).ravel()
+        _fn(kind, op)(_ptr(out), _ptr(x), _ptr(y), x.size)
+    return out
+
+
+def rms_norm(x, w, eps, kind: str = "port"):
+    """Row by row over the last axis."""
+    x = _f32(x)
+    rows = x.reshape(-1, x.shape[-1])
+    w = _f32(w)
+    out = np.empty_like(rows)
+    for r in range(rows.shape[0]):
+        _fn(kind, "rms_norm")(_ptr(out[r]), _ptr(np.ascontiguousarray(rows[r])), _ptr(w), rows.shape[1], eps)
+    return out.reshape(x.shape)
+
+
+def softmax(x, kind: str = "port"):
+    x = _f32(x)
+    rows = x.reshape(-1, x.shape[-1])
+    out = np.empty_like(rows)
+    for r in range(rows.shape[0]):
+        _fn(kind, "softmax")(_ptr(out[r]), _ptr(np.ascontiguousarray(rows[r])), rows.shape[1])
+    return out.reshape(x.shape)
+
+
+def rope(q, k, pos, theta, kind: str = "port"):
+    """q [S, H, D], k [S, KVH, D] -> rotated copies."""
+    q, k = _f32(q).copy(), _f32(k).copy()
+    S, H, D = q.shape
+    _fn(kind, "rope")(_ptr(q), _ptr(k), S, H, k.shape[1], D, pos, theta)
+    return q, k
+
+
+def linear(x, w, bias=None, residual=None, kind: str = "port"):
+    """out = x @ w.T + bias (+ residual): Backend::linear / linear_add."""
+    x, w = _f32(x), _f32(w)
+    M, K = x.shape
+    N = w.shape[0]
+    out = np.empty((M, N), np.float32)
+    if residual is None:
+        _fn(kind, "linear")(_ptr(out), _ptr(x), _ptr(w), _ptr(_f32(bias)), M, N, K)
+    else:
+        _fn(kind, "linear_add")(_ptr(out), _ptr(x), _ptr(w), _ptr(_f32(bias)), _ptr(_f32(residual)), M, N, K)
+    return out
+
+
+def matmul(a, b, kind: str = "port"):
+    a, b = _f32(a), _f32(b)
+    M, K = a.shape
+    N = b.shape[1]
+    out = np.empty((M, N), np.float32)
+    _fn(kind, "matmul")(_ptr(out), _ptr(a), _ptr(b), M, N, K)
+    return out
+
+
+def causal_attention(q, k, v, q_idx, attend_len, scale, kind: str = "port"):
+    """q [S, H, D], k/v [T, KVH, D] -> out [H * D] for query q_idx over the
+    first attend_len positions."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    S, H, D = q.shape
+    out = np.empty(H * D, np.float32)
+    _fn(kind, "causal_attention")(_ptr(out), _ptr(q), q_idx, _ptr(k), _ptr(v), attend_len, H, k.shape[1], D, scale)
     return out

@@ -1,0 +1,229 @@
+"""GPU parity of the decode-step operators besides linear_q8 (vvh_eltwise,
+vvh_rms_norm, vvh_softmax, vvh_rope, vvh_embedding, vvh_attention, vvh_dense,
+vvh_matmul, vvh_argmax, vvh_mirror_f32) against the CPU oracle, which restates
+BackendCPU (src/backend/backend_naive.cc) and is pinned bit-for-bit to the
+reference's own build (tests/test_oracle.py).
+
+Tolerances: normalized max error max|y - r| / max|r| <= 1e-4 with fp32
+activations, <= 2e-3 with fp16 activations (inputs are rounded to fp16 first
+and the oracle gets the rounded values).  Argmax and the mirrors are exact.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from vvllm_amd import capi
+
+pytestmark = pytest.mark.gpu
+
+F16, F32 = capi.F16, capi.F32
+TOL = {F32: 1e-4, F16: 2e-3}
+
+
+def npd(d):
+    return np.float16 if d == F16 else np.float32
+
+
+def up(a, d):
+    """Device copy of `a` in activation dtype d; returns (buffer, the values the device holds)."""
+    a = np.ascontiguousarray(a, dtype=npd(d))
+    return capi.DevBuf.from_array(a), a.astype(np.float32)
+
+
+def down(buf, d, shape):
+    return buf.to_array(npd(d), shape).astype(np.float32)
+
+
+def nerr(got, ref):
+    return float(np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+def mirror(a, as_dtype=F32):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    dev = ctypes.c_void_p()
+    capi.call("vvh_mirror_f32", a.ctypes.data, a.size, as_dtype, ctypes.byref(dev))
+    return a, dev.value
+
+
+@pytest.mark.parametrize("d", [F32, F16])
+@pytest.mark.parametrize("n", [1, 1000, (1 << 20) + 3])
+@pytest.mark.parametrize("op", ["add", "mul", "silu", "silu_mul"])
+def test_eltwise(gpu, oracle, op, n, d):
+    print(f"[case] eltwise {op} n={n} dtype={d}", flush=True)
+    rng = np.random.default_rng(n)
+    dx, x = up(rng.normal(0, 2, n), d)
+    dy, y = up(rng.normal(0, 2, n), d)
+    do = capi.DevBuf(n * np.dtype(npd(d)).itemsize)
+    code = {"add": capi.OP_ADD, "mul": capi.OP_MUL, "silu": capi.OP_SILU, "silu_mul": capi.OP_SILU_MUL}[op]
+    capi.call("vvh_eltwise", code, do.ptr, dx.ptr, dy.ptr, n, d, None)
+    capi.sync()
+    assert nerr(down(do, d, (n,)), oracle.eltwise(op, x, y)) <= TOL[d]
+
+
+@pytest.mark.parametrize("d", [F32, F16])
+@pytest.mark.parametrize("rows,n", [(1, 896), (3, 1536), (128, 1000), (2, 5)])
+def test_rms_norm(gpu, oracle, rows, n, d):
+    print(f"[case] rms_norm rows={rows} n={n} dtype={d}", flush=True)
+    rng = np.random.default_rng(rows * n)
+    dx, x = up(rng.normal(0, 1, (rows, n)), d)
+    w, dw = mirror(rng.normal(1, 0.1, n))
+    do = capi.DevBuf(rows * n * np.dtype(npd(d)).itemsize)
+    capi.call("vvh_rms_norm", do.ptr, dx.ptr, dw, rows, n, 1e-6, d, None)
+    capi.sync()
+    assert nerr(down(do, d, (rows, n)), oracle.rms_norm(x, w, 1e-6)) <= TOL[d]
+    capi.call("vvh_mirror_release", w.ctypes.data)
+
+
+@pytest.mark.parametrize("d", [F32, F16])
+@pytest.mark.parametrize("rows,n", [(1, 7), (4, 1000), (1, 151936)])
+def test_softmax(gpu, oracle, rows, n, d):
+    print(f"[case] softmax rows={rows} n={n} dtype={d}", flush=True)
+    dx, x = up(np.random.default_rng(n).normal(0, 3, (rows, n)), d)
+    do = capi.DevBuf(rows * n * np.dtype(npd(d)).itemsize)
+    capi.call("vvh_softmax", do.ptr, dx.ptr, rows, n, d, None)
+    capi.sync()
+    got, ref = down(do, d, (rows, n)), oracle.softmax(x)
+    # The reference sums n exponentials one after another in fp32; over long
+    # rows its own rounding exceeds the bound, so the GPU result must then be
+    # at least as close as the reference to the exact (fp64) softmax.
+    x64 = x.astype(np.float64)
+    e = np.exp(x64 - x64.max(axis=1, keepdims=True))
+    exact = e / e.sum(axis=1, keepdims=True)
+    assert nerr(got, ref) <= TOL[d] or nerr(got, exact) <= max(TOL[d], nerr(ref, exact))
+
+
+ROPE = [(1, 14, 2, 64, 0, 1e6), (1, 14, 2, 64, 4095, 1e6), (5, 12, 2, 128, 30000, 1e6), (3, 4, 4, 32, 7, 1e4)]
+
+
+@pytest.mark.parametrize("d", [F32, F16])
+@pytest.mark.parametrize("S,H,KVH,D,pos,theta", ROPE)
+def test_rope(gpu, oracle, S, H, KVH, D, pos, theta, d):
+    print(f"[case] rope S={S} H={H} KVH={KVH} D={D} pos={pos} dtype={d}", flush=True)
+    rng = np.random.default_rng(pos + S)
+    dq, q = up(rng.normal(0, 1, (S, H, D)), d)
+    dk, k = up(rng.normal(0, 1, (S, KVH, D)), d)
+    capi.call("vvh_rope", dq.ptr, dk.ptr, S, H, KVH, D, pos, theta, d, None)
+    capi.sync()
+    rq, rk = oracle.rope(q, k, pos, theta)
+    assert nerr(down(dq, d, (S, H, D)), rq) <= TOL[d]
+    assert nerr(down(dk, d, (S, KVH, D)), rk) <= TOL[d]
+
+
+@pytest.mark.parametrize("d", [F32, F16])
+def test_embedding(gpu, d):
+    V, Hd = 1000, 896
+    table, dt = mirror(np.random.default_rng(1).normal(0, 1, (V, Hd)))
+    do = capi.DevBuf(Hd * 4)
+    for tok in (0, 37, V - 1):
+        capi.call("vvh_embedding", do.ptr, dt, tok, Hd, V, d, None)
+        capi.sync()
+        np.testing.assert_array_equal(down(do, d, (Hd,)), table[tok].astype(npd(d)).astype(np.float32))
+    assert capi.status_of("vvh_embedding", do.ptr, dt, V, Hd, V, d, None) == 1  # token out of range
+    capi.call("vvh_mirror_release", table.ctypes.data)
+
+
+ATT = [(1, 1, 14, 2, 64), (1, 100, 14, 2, 64), (1, 4096, 14, 2, 64), (4, 10, 12, 2, 128), (3, 5, 4, 4, 32),
+       (1, 16000, 2, 1, 64), (2, 7, 16, 2, 256)]
+
+
+@pytest.mark.parametrize("d", [F32, F16])
+@pytest.mark.parametrize("n_q,len0,H,KVH,D", ATT)
+def test_attention(gpu, oracle, n_q, len0, H, KVH, D, d):
+    print(f"[case] attention n_q={n_q} len0={len0} H={H} KVH={KVH} D={D} dtype={d}", flush=True)
+    T = len0 + n_q - 1
+    rng = np.random.default_rng(T + H)
+    dq, q = up(rng.normal(0, 1, (n_q, H, D)), d)
+    dk, k = up(rng.normal(0, 1, (T, KVH, D)), d)
+    dv, v = up(rng.normal(0, 1, (T, KVH, D)), d)
+    do = capi.DevBuf(n_q * H * D * np.dtype(npd(d)).itemsize)
+    scale = float(1.0 / np.sqrt(np.float32(D)))
+    capi.call("vvh_attention", do.ptr, dq.ptr, dk.ptr, dv.ptr, n_q, len0, H, KVH, D, scale, d, None)
+    capi.sync()
+    got = down(do, d, (n_q, H * D))
+    assert capi.status_of("vvh_attention", do.ptr, dq.ptr, dk.ptr, dv.ptr, 1, 16001, H, KVH, D, scale, d, None) == 7
+    for s in range(n_q):
+        ref = oracle.causal_attention(q, k, v, s, len0 + s, scale)
+        assert nerr(got[s], ref) <= TOL[d], f"query {s}"
+
+
+DENSE = [(1, 896, 896), (3, 1000, 130), (7, 40, 4864), (1, 151936, 896)]
+
+
+@pytest.mark.parametrize("d,wd", [(F32, F32), (F16, F16), (F16, F32)])
+@pytest.mark.parametrize("M,N,K", DENSE)
+def test_dense(gpu, oracle, M, N, K, d, wd):
+    print(f"[case] dense M={M} N={N} K={K} dtype={d} wdtype={wd}", flush=True)
+    rng = np.random.default_rng(N + K + M)
+    w = rng.normal(0, 0.05, (N, K)).astype(np.float32)
+    wmir, dw = mirror(w, wd)
+    weff = w.astype(np.float16).astype(np.float32) if wd == F16 else w  # what the device holds
+    b, db = mirror(rng.normal(0, 0.1, N))
+    dx, x = up(rng.normal(0, 1, (M, K)), d)
+    res = M % 2 == 1
+    dr, r = up(rng.normal(0, 1, (M, N)), d)
+    do = capi.DevBuf(M * N * np.dtype(npd(d)).itemsize)
+    capi.call("vvh_dense", do.ptr, dx.ptr, dw, wd, db, dr.ptr if res else None, M, N, K, d, None)
+    capi.sync()
+    ref = oracle.linear(x, weff, b, r if res else None)
+    assert nerr(down(do, d, (M, N)), ref) <= TOL[d]
+    for a in (wmir, b):
+        capi.call("vvh_mirror_release", a.ctypes.data)
+
+
+def test_dense_in_place_residual(gpu, oracle):
+    """linear_add with out == residual (transformer.h:165-166 calls it so)."""
+    M, N, K = 2, 64, 96
+    rng = np.random.default_rng(9)
+    w, dw = mirror(rng.normal(0, 0.1, (N, K)))
+    dx, x = up(rng.normal(0, 1, (M, K)), F32)
+    dr, r = up(rng.normal(0, 1, (M, N)), F32)
+    capi.call("vvh_dense", dr.ptr, dx.ptr, dw, F32, None, dr.ptr, M, N, K, F32, None)
+    capi.sync()
+    assert nerr(down(dr, F32, (M, N)), oracle.linear(x, w, None, r)) <= TOL[F32]
+    capi.call("vvh_mirror_release", w.ctypes.data)
+
+
+@pytest.mark.parametrize("d", [F32, F16])
+def test_matmul(gpu, oracle, d):
+    rng = np.random.default_rng(4)
+    dA, A = up(rng.normal(0, 1, (5, 70)), d)
+    B, dB = mirror(rng.normal(0, 1, (70, 33)))
+    do = capi.DevBuf(5 * 33 * 4)
+    capi.call("vvh_matmul", do.ptr, dA.ptr, dB, 5, 33, 70, d, None)
+    capi.sync()
+    assert nerr(down(do, d, (5, 33)), oracle.matmul(A, B)) <= TOL[d]
+    capi.call("vvh_mirror_release", B.ctypes.data)
+
+
+def test_argmax(gpu):
+    rng = np.random.default_rng(5)
+    di = capi.DevBuf(4)
+    for n in (1, 1000, 151936):
+        x = rng.normal(0, 1, n).astype(np.float32)
+        cases = [x]
+        if n > 10:
+            t = x.copy()
+            t[[3, n - 2, n // 2]] = 50.0  # ties: the first index wins, as std::max_element
+            cases.append(t)
+        for a in cases:
+            dx = capi.DevBuf.from_array(a)
+            capi.call("vvh_argmax", dx.ptr, n, di.ptr, None)
+            capi.sync()
+            assert int(di.to_array(np.int32, (1,))[0]) == int(np.argmax(a))
+
+
+def test_mirror_f32_and_f16(gpu):
+    a = np.random.default_rng(6).normal(0, 1, 1001).astype(np.float32)
+    _, d32 = mirror(a, F32)
+    _, d16 = mirror(a, F16)
+    b32 = np.empty(1001, np.float32)
+    b16 = np.empty(1001, np.float16)
+    capi.call("vvh_memcpy_d2h", b32.ctypes.data, d32, 1001 * 4)
+    capi.call("vvh_memcpy_d2h", b16.ctypes.data, d16, 1001 * 2)
+    np.testing.assert_array_equal(b32, a)
+    np.testing.assert_array_equal(b16, a.astype(np.float16))
+    _, again = mirror(a, F32)
+    assert again == d32  # same host array, same length: the cached copy
+    capi.call("vvh_mirror_release", a.ctypes.data)
+    assert capi.status_of("vvh_mirror_release", a.ctypes.data) == 6

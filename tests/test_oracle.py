@@ -252,3 +252,93 @@ def test_ingest_bf16_known_answers(oracle):
     q, s = oracle.ingest_bf16(bf([[2.0, 0.5, -0.25]]))
     assert s[0] == np.float32(2.0) / np.float32(127.0)
     assert q.tolist() == [[127, 32, -16]]
+
+
+# ---------------------------------------------------------------------------
+# the other BackendCPU operators (src/backend/backend_naive.cc)
+# ---------------------------------------------------------------------------
+def _need_ref(oracle):
+    if not oracle.available("reference"):
+        pytest.skip("oracle/_ref (the reference compiled in place) is not built here")
+
+
+def test_ops_bit_exact_vs_reference(oracle):
+    """Every restated operator agrees bit for bit with the reference's own
+    BackendCPU compiled from its sources (same compiler, flags and libm)."""
+    _need_ref(oracle)
+    rng = np.random.default_rng(11)
+    x = rng.normal(0, 2, 1000).astype(np.float32)
+    y = rng.normal(0, 2, 1000).astype(np.float32)
+    for op in ("add", "mul", "silu", "silu_mul"):
+        a = oracle.eltwise(op, x, y)
+        b = oracle.eltwise(op, x, y, kind="reference")
+        np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32), err_msg=op)
+    rows = rng.normal(0, 1, (3, 896)).astype(np.float32)
+    w = rng.normal(1, 0.1, 896).astype(np.float32)
+    np.testing.assert_array_equal(oracle.rms_norm(rows, w, 1e-6), oracle.rms_norm(rows, w, 1e-6, kind="reference"))
+    np.testing.assert_array_equal(oracle.softmax(rows), oracle.softmax(rows, kind="reference"))
+    q = rng.normal(0, 1, (3, 14, 64)).astype(np.float32)
+    k = rng.normal(0, 1, (3, 2, 64)).astype(np.float32)
+    for pos in (0, 7, 4000):
+        a, b = oracle.rope(q, k, pos, 1e6), oracle.rope(q, k, pos, 1e6, kind="reference")
+        np.testing.assert_array_equal(a[0], b[0])
+        np.testing.assert_array_equal(a[1], b[1])
+    X = rng.normal(0, 1, (3, 96)).astype(np.float32)
+    W = rng.normal(0, 0.1, (40, 96)).astype(np.float32)
+    bias = rng.normal(0, 0.1, 40).astype(np.float32)
+    res = rng.normal(0, 1, (3, 40)).astype(np.float32)
+    np.testing.assert_array_equal(oracle.linear(X, W, bias), oracle.linear(X, W, bias, kind="reference"))
+    np.testing.assert_array_equal(oracle.linear(X, W, None, res), oracle.linear(X, W, None, res, kind="reference"))
+    np.testing.assert_array_equal(oracle.matmul(X, W.T.copy()), oracle.matmul(X, W.T.copy(), kind="reference"))
+    kc = rng.normal(0, 1, (50, 2, 64)).astype(np.float32)
+    vc = rng.normal(0, 1, (50, 2, 64)).astype(np.float32)
+    for q_idx, ln in ((0, 1), (1, 17), (2, 50)):
+        np.testing.assert_array_equal(oracle.causal_attention(q, kc, vc, q_idx, ln, 0.125),
+                                      oracle.causal_attention(q, kc, vc, q_idx, ln, 0.125, kind="reference"))
+
+
+def test_ops_closed_forms(oracle):
+    """What the mathematics fixes, independent of the restatement."""
+    # RMSNorm of c*1 with unit weight and eps 0 is sign(c) exactly (c a power of 2)
+    for c in (4.0, -0.25):
+        np.testing.assert_array_equal(oracle.rms_norm(np.full((1, 64), c), np.ones(64), 0.0), np.sign(c))
+    # softmax of a constant row of 2^k elements is 2^-k exactly
+    np.testing.assert_array_equal(oracle.softmax(np.full((1, 256), 3.0)), np.float32(1 / 256))
+    # RoPE at position 0 is the identity; at head_dim 2 the pair rotates by `pos` radians
+    rng = np.random.default_rng(2)
+    q = rng.normal(0, 1, (1, 3, 8)).astype(np.float32)
+    k = rng.normal(0, 1, (1, 1, 8)).astype(np.float32)
+    q0, k0 = oracle.rope(q, k, 0, 10000.0)
+    np.testing.assert_array_equal(q0, q)
+    np.testing.assert_array_equal(k0, k)
+    q2 = np.array([[[1.0, 0.0]]], np.float32)
+    r, _ = oracle.rope(q2, np.zeros((1, 1, 2), np.float32), 5, 10000.0)
+    np.testing.assert_allclose(r[0, 0], [np.cos(5.0), np.sin(5.0)], atol=1e-6)
+    # RoPE preserves the norm of every (i, i + D/2) pair
+    qq, _ = oracle.rope(q, k, 123, 10000.0)
+    n0 = q[..., :4] ** 2 + q[..., 4:] ** 2
+    n1 = qq[..., :4] ** 2 + qq[..., 4:] ** 2
+    np.testing.assert_allclose(n1, n0, rtol=1e-5)
+    # attention over one position returns that position's value row (GQA: heads 0-6 -> kv 0)
+    qa = rng.normal(0, 1, (1, 14, 64)).astype(np.float32)
+    kv = rng.normal(0, 1, (1, 2, 64)).astype(np.float32)
+    va = rng.normal(0, 1, (1, 2, 64)).astype(np.float32)
+    out = oracle.causal_attention(qa, kv, va, 0, 1, 0.125).reshape(14, 64)
+    np.testing.assert_array_equal(out[:7], np.broadcast_to(va[0, 0], (7, 64)))
+    np.testing.assert_array_equal(out[7:], np.broadcast_to(va[0, 1], (7, 64)))
+    # equal keys give uniform weights: the output is the mean of the values
+    ke = np.broadcast_to(kv[:1], (8, 2, 64)).copy()
+    ve = rng.normal(0, 1, (8, 2, 64)).astype(np.float32)
+    out = oracle.causal_attention(qa, ke, ve, 0, 8, 0.125).reshape(14, 64)
+    np.testing.assert_allclose(out[0], ve[:, 0].mean(axis=0), atol=1e-6)
+    # integer-valued linear / matmul are exact (an index or transpose mistake fails)
+    X = rng.integers(-8, 8, (3, 20)).astype(np.float32)
+    W = rng.integers(-8, 8, (5, 20)).astype(np.float32)
+    b = rng.integers(-8, 8, 5).astype(np.float32)
+    want = X.astype(np.int64) @ W.astype(np.int64).T + b.astype(np.int64)
+    np.testing.assert_array_equal(oracle.linear(X, W, b), want)
+    np.testing.assert_array_equal(oracle.matmul(X, W.T.copy()), X.astype(np.int64) @ W.astype(np.int64).T)
+    # silu(0) = 0, silu_mul(0, y) = 0, silu of a large x is x
+    np.testing.assert_array_equal(oracle.eltwise("silu", np.zeros(4)), 0.0)
+    np.testing.assert_array_equal(oracle.eltwise("silu_mul", np.zeros(4), np.ones(4)), 0.0)
+    np.testing.assert_array_equal(oracle.eltwise("silu", np.array([40.0])), 40.0)

@@ -16,6 +16,7 @@ import numpy as np
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libvvllm_hip.so")
 
 F32, F16, BF16 = 0, 1, 2
+OP_ADD, OP_MUL, OP_SILU, OP_SILU_MUL = 0, 1, 2, 3
 KERNEL_AUTO, KERNEL_GENERIC, KERNEL_GEMV_F32, KERNEL_SKINNY, KERNEL_GEMM, KERNEL_STREAM, KERNEL_DOT = range(7)
 KERNEL_NAMES = {0: "auto", 1: "generic", 2: "gemv_f32", 3: "skinny", 4: "gemm", 5: "stream", 6: "dot"}
 STATUS = {0: "VVH_OK", 1: "VVH_ERR_INVALID_ARG", 2: "VVH_ERR_NO_DEVICE", 3: "VVH_ERR_OUT_OF_MEMORY",
@@ -74,6 +75,20 @@ SIGNATURES = {
     "vvh_fill_normal": (c_int, [c_void_p, c_int, c_size_t, c_uint64, c_float, c_float, c_void_p]),
     "vvh_linear_q8_choice": (c_int, [c_size_t, c_size_t, c_size_t, c_int, c_int]),
     "vvh_set_kernel_override": (c_int, [c_int]),
+    "vvh_eltwise": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_size_t, c_int, c_void_p]),
+    "vvh_rms_norm": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_size_t, c_float, c_int, c_void_p]),
+    "vvh_softmax": (c_int, [c_void_p, c_void_p, c_size_t, c_size_t, c_int, c_void_p]),
+    "vvh_rope": (c_int, [c_void_p, c_void_p, c_size_t, c_size_t, c_size_t, c_size_t, c_size_t, c_float, c_int,
+                         c_void_p]),
+    "vvh_embedding": (c_int, [c_void_p, c_void_p, c_size_t, c_size_t, c_size_t, c_int, c_void_p]),
+    "vvh_attention": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_size_t, c_size_t, c_size_t,
+                              c_size_t, c_float, c_int, c_void_p]),
+    "vvh_dense": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_size_t, c_size_t, c_size_t,
+                          c_int, c_void_p]),
+    "vvh_matmul": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_size_t, c_size_t, c_int, c_void_p]),
+    "vvh_argmax": (c_int, [c_void_p, c_size_t, c_void_p, c_void_p]),
+    "vvh_mirror_f32": (c_int, [c_void_p, c_size_t, c_int, POINTER(c_void_p)]),
+    "vvh_mirror_release": (c_int, [c_void_p]),
 }
 # entries that return a value rather than a vvh_status
 _NOT_STATUS = {"vvh_status_string", "vvh_last_error", "vvh_version", "vvh_device_cu_count",

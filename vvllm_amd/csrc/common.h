@@ -126,6 +126,23 @@ int launch_splitk_reduce(const LinArgs& a, int out, void* stream);
 // at least `depth` 64-wide k steps.  max_m = largest M of the launch.
 int launch_stream(const StreamArgs& s, int depth, int max_m, int out, int64_t blocks, void* stream);
 
+// Model-step operators (model_kernels.hip); dtype = activation type
+// (VVH_F32 / VVH_F16), computation in fp32.
+int launch_eltwise(int op, void* out, const void* x, const void* y, int64_t n, int dtype, void* stream);
+int launch_rms_norm(void* out, const void* x, const float* w, int64_t rows, int64_t n, float eps, int dtype,
+                    void* stream);
+int launch_softmax(void* out, const void* x, int64_t rows, int64_t n, int dtype, void* stream);
+int launch_rope(void* q, void* k, int64_t S, int64_t H, int64_t KVH, int64_t D, int64_t pos, float theta, int dtype,
+                void* stream);
+int launch_embedding(void* out, const float* table, int64_t token, int64_t hidden, int dtype, void* stream);
+int64_t attention_max_len();
+int launch_attention(void* out, const void* q, const void* k, const void* v, int64_t n_q, int64_t len0, int64_t H,
+                     int64_t KVH, int64_t D, float scale, int dtype, void* stream);
+int launch_dense(void* out, const void* x, const void* w, int wdtype, const float* bias, const void* res, int64_t M,
+                 int64_t N, int64_t K, int dtype, void* stream);
+int launch_matmul(void* out, const void* A, const float* B, int64_t M, int64_t N, int64_t K, int dtype, void* stream);
+int launch_argmax(const float* x, int64_t n, int32_t* idx, void* stream);
+
 // Auxiliary kernels (aux_kernels.hip).
 // w: N x K elements of src_dtype (VVH_F32 or VVH_BF16)
 int launch_quantize(const void* w, int src_dtype, int64_t N, int64_t K, int8_t* q, float* scales, void* stream);

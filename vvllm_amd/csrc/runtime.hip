@@ -1175,4 +1175,191 @@ VVH_API int vvh_set_kernel_override(int kernel)
     return VVH_OK;
 }
 
+
+// ---- the other operators of a decode step --------------------------------------------------
+namespace {
+struct ArrayMirror {
+    void* dev = nullptr;
+    std::size_t n = 0;
+};
+std::mutex g_amu;
+std::unordered_map<const float*, ArrayMirror> g_arr[2];  // [0]: fp32 copies, [1]: fp16 copies
+
+inline int act_ok(int dtype) { return dtype == VVH_F32 || dtype == VVH_F16; }
+inline int ret_launch(int e, const char* what) { return e == 0 ? VVH_OK : fail_hip((hipError_t)e, what); }
+}  // namespace
+
+VVH_API int vvh_eltwise(int op, void* out, const void* x, const void* y, size_t n, int dtype, void* stream)
+{
+    if (op < VVH_OP_ADD || op > VVH_OP_SILU_MUL || !act_ok(dtype)) return fail(VVH_ERR_INVALID_ARG, "bad op or dtype");
+    if (n == 0) return VVH_OK;
+    if (!out || !x || (op != VVH_OP_SILU && !y)) return fail(VVH_ERR_INVALID_ARG, "null pointer");
+    REQUIRE_INIT();
+    return ret_launch(launch_eltwise(op, out, x, y, (int64_t)n, dtype, stream), "eltwise launch");
+}
+
+VVH_API int vvh_rms_norm(void* out, const void* x, const float* dev_weight, size_t rows, size_t n, float eps,
+                         int dtype, void* stream)
+{
+    if (!act_ok(dtype)) return fail(VVH_ERR_INVALID_ARG, "bad dtype");
+    if (rows == 0 || n == 0) return VVH_OK;
+    if (!out || !x || !dev_weight) return fail(VVH_ERR_INVALID_ARG, "null pointer");
+    if (rows > INT32_MAX) return fail(VVH_ERR_UNSUPPORTED, "too many rows");
+    REQUIRE_INIT();
+    return ret_launch(launch_rms_norm(out, x, dev_weight, (int64_t)rows, (int64_t)n, eps, dtype, stream), "rms_norm launch");
+}
+
+VVH_API int vvh_softmax(void* out, const void* x, size_t rows, size_t n, int dtype, void* stream)
+{
+    if (!act_ok(dtype)) return fail(VVH_ERR_INVALID_ARG, "bad dtype");
+    if (rows == 0 || n == 0) return VVH_OK;
+    if (!out || !x) return fail(VVH_ERR_INVALID_ARG, "null pointer");
+    if (rows > INT32_MAX) return fail(VVH_ERR_UNSUPPORTED, "too many rows");
+    REQUIRE_INIT();
+    return ret_launch(launch_softmax(out, x, (int64_t)rows, (int64_t)n, dtype, stream), "softmax launch");
+}
+
+VVH_API int vvh_rope(void* q, void* k, size_t seq_len, size_t num_heads, size_t num_kv_heads, size_t head_dim,
+                     size_t pos, float theta, int dtype, void* stream)
+{
+    if (!act_ok(dtype)) return fail(VVH_ERR_INVALID_ARG, "bad dtype");
+    if (head_dim % 2 != 0) return fail(VVH_ERR_INVALID_ARG, "odd head_dim %zu", head_dim);
+    if (seq_len == 0 || head_dim == 0 || (num_heads == 0 && num_kv_heads == 0)) return VVH_OK;
+    if ((num_heads && !q) || (num_kv_heads && !k)) return fail(VVH_ERR_INVALID_ARG, "null pointer");
+    REQUIRE_INIT();
+    return ret_launch(launch_rope(q, k, (int64_t)seq_len, (int64_t)num_heads, (int64_t)num_kv_heads, (int64_t)head_dim,
+                                  (int64_t)pos, theta, dtype, stream),
+                      "rope launch");
+}
+
+VVH_API int vvh_embedding(void* out, const float* dev_table, size_t token_id, size_t hidden, size_t vocab, int dtype,
+                          void* stream)
+{
+    if (!act_ok(dtype)) return fail(VVH_ERR_INVALID_ARG, "bad dtype");
+    if (token_id >= vocab) return fail(VVH_ERR_INVALID_ARG, "token %zu out of range (vocab %zu)", token_id, vocab);
+    if (hidden == 0) return VVH_OK;
+    if (!out || !dev_table) return fail(VVH_ERR_INVALID_ARG, "null pointer");
+    REQUIRE_INIT();
+    return ret_launch(launch_embedding(out, dev_table, (int64_t)token_id, (int64_t)hidden, dtype, stream),
+                      "embedding launch");
+}
+
+VVH_API int vvh_attention(void* out, const void* q, const void* k, const void* v, size_t n_q, size_t len0,
+                          size_t num_heads, size_t num_kv_heads, size_t head_dim, float scale, int dtype, void* stream)
+{
+    if (!act_ok(dtype)) return fail(VVH_ERR_INVALID_ARG, "bad dtype");
+    if (n_q == 0 || num_heads == 0) return VVH_OK;
+    if (!out || !q || !k || !v) return fail(VVH_ERR_INVALID_ARG, "null pointer");
+    if (num_kv_heads == 0 || num_heads % num_kv_heads != 0)
+        return fail(VVH_ERR_INVALID_ARG, "num_heads %zu not a multiple of num_kv_heads %zu", num_heads, num_kv_heads);
+    if (head_dim == 0 || head_dim > 256) return fail(VVH_ERR_INVALID_ARG, "head_dim %zu outside 1..256", head_dim);
+    if (len0 == 0) return fail(VVH_ERR_INVALID_ARG, "a query attends to at least one position");
+    if (len0 + n_q - 1 > (size_t)attention_max_len())
+        return fail(VVH_ERR_UNSUPPORTED, "attention span %zu > %lld", len0 + n_q - 1, (long long)attention_max_len());
+    if (num_heads > 65535 || n_q > 65535) return fail(VVH_ERR_UNSUPPORTED, "grid too large");
+    REQUIRE_INIT();
+    return ret_launch(launch_attention(out, q, k, v, (int64_t)n_q, (int64_t)len0, (int64_t)num_heads,
+                                       (int64_t)num_kv_heads, (int64_t)head_dim, scale, dtype, stream),
+                      "attention launch");
+}
+
+VVH_API int vvh_dense(void* out, const void* x, const void* dev_weight, int wdtype, const float* dev_bias,
+                      const void* residual, size_t M, size_t N, size_t K, int dtype, void* stream)
+{
+    if (!act_ok(dtype) || !act_ok(wdtype)) return fail(VVH_ERR_INVALID_ARG, "bad dtype");
+    uint64_t t;
+    if (!mul_ok(M, N, &t) || !mul_ok(N, K, &t) || !mul_ok(M, K, &t)) return fail(VVH_ERR_INVALID_ARG, "size overflow");
+    if (M == 0 || N == 0) return VVH_OK;
+    if (!out || (K > 0 && (!x || !dev_weight))) return fail(VVH_ERR_INVALID_ARG, "null pointer");
+    if ((N + 3) / 4 > INT32_MAX) return fail(VVH_ERR_UNSUPPORTED, "N too large");
+    REQUIRE_INIT();
+    return ret_launch(launch_dense(out, x, dev_weight, wdtype, dev_bias, residual, (int64_t)M, (int64_t)N, (int64_t)K,
+                                   dtype, stream),
+                      "dense launch");
+}
+
+VVH_API int vvh_matmul(void* out, const void* A, const float* dev_B, size_t M, size_t N, size_t K, int dtype,
+                       void* stream)
+{
+    if (!act_ok(dtype)) return fail(VVH_ERR_INVALID_ARG, "bad dtype");
+    uint64_t t;
+    if (!mul_ok(M, N, &t) || !mul_ok(K, N, &t) || !mul_ok(M, K, &t)) return fail(VVH_ERR_INVALID_ARG, "size overflow");
+    if (M == 0 || N == 0) return VVH_OK;
+    if (!out || (K > 0 && (!A || !dev_B))) return fail(VVH_ERR_INVALID_ARG, "null pointer");
+    REQUIRE_INIT();
+    return ret_launch(launch_matmul(out, A, dev_B, (int64_t)M, (int64_t)N, (int64_t)K, dtype, stream), "matmul launch");
+}
+
+VVH_API int vvh_argmax(const float* logits, size_t n, int32_t* dev_index, void* stream)
+{
+    if (!logits || !dev_index) return fail(VVH_ERR_INVALID_ARG, "null pointer");
+    if (n == 0 || n > INT32_MAX) return fail(VVH_ERR_INVALID_ARG, "bad length %zu", n);
+    REQUIRE_INIT();
+    return ret_launch(launch_argmax(logits, (int64_t)n, dev_index, stream), "argmax launch");
+}
+
+VVH_API int vvh_mirror_f32(const float* host, size_t n, int as_dtype, const void** dev)
+{
+    if (!dev) return fail(VVH_ERR_INVALID_ARG, "dev is null");
+    *dev = nullptr;
+    if (!host || n == 0) return fail(VVH_ERR_INVALID_ARG, "empty host array");
+    if (!act_ok(as_dtype)) return fail(VVH_ERR_INVALID_ARG, "bad dtype");
+    uint64_t bytes;
+    if (!mul_ok(n, 4, &bytes)) return fail(VVH_ERR_INVALID_ARG, "size overflow");
+    REQUIRE_INIT();
+    std::lock_guard<std::mutex> lock(g_amu);
+    auto& map = g_arr[as_dtype == VVH_F16 ? 1 : 0];
+    auto it = map.find(host);
+    if (it != map.end()) {
+        if (it->second.n == n) {
+            *dev = it->second.dev;
+            return VVH_OK;
+        }
+        (void)hipDeviceSynchronize();  // the old copy may still be read by queued work
+        (void)hipFree(it->second.dev);
+        map.erase(it);
+    }
+    void* d = nullptr;
+    hipError_t e = hipMalloc(&d, as_dtype == VVH_F16 ? n * 2 : n * 4);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return fail_hip(e, "mirror hipMalloc");
+    }
+    if (as_dtype == VVH_F32) {
+        e = hipMemcpy(d, host, n * 4, hipMemcpyHostToDevice);
+    } else {  // upload fp32, convert on the device
+        void* tmp = nullptr;
+        e = hipMalloc(&tmp, n * 4);
+        if (e == hipSuccess) e = hipMemcpy(tmp, host, n * 4, hipMemcpyHostToDevice);
+        if (e == hipSuccess) {
+            const int k = launch_convert(d, VVH_F16, tmp, VVH_F32, (int64_t)n, nullptr);
+            e = k ? (hipError_t)k : hipDeviceSynchronize();
+        }
+        if (tmp) (void)hipFree(tmp);
+    }
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        (void)hipFree(d);
+        return fail_hip(e, "mirror upload");
+    }
+    map[host] = ArrayMirror{d, n};
+    *dev = d;
+    return VVH_OK;
+}
+
+VVH_API int vvh_mirror_release(const float* host)
+{
+    std::lock_guard<std::mutex> lock(g_amu);
+    bool found = false;
+    for (auto& map : g_arr) {
+        auto it = map.find(host);
+        if (it == map.end()) continue;
+        if (!found) (void)hipDeviceSynchronize();
+        (void)hipFree(it->second.dev);
+        map.erase(it);
+        found = true;
+    }
+    return found ? VVH_OK : fail(VVH_ERR_UNKNOWN_HANDLE, "no mirror of %p", (const void*)host);
+}
+
 }  // extern "C"
