@@ -91,6 +91,10 @@ VVH_API int vvh_free_host(void* ptr);
 VVH_API int vvh_memcpy_h2d(void* dst, const void* src, size_t bytes);
 VVH_API int vvh_memcpy_d2h(void* dst, const void* src, size_t bytes);
 VVH_API int vvh_memcpy_d2d(void* dst, const void* src, size_t bytes);
+/* Device-to-device copy queued on `stream` (not synchronous): the KV-cache
+ * append of a decode step (KVCacheCUDA::append copies synchronously,
+ * src/kv_cache/kv_cache_cuda.cc:74-79). */
+VVH_API int vvh_memcpy_d2d_async(void* dst, const void* src, size_t bytes, void* stream);
 
 /* ---- caching allocator -------------------------------------------------- */
 /* Stream-ordered-free caching allocator behind device_allocate /

@@ -1,6 +1,6 @@
 // GPU test of BackendHIP through the vvllm Backend interface.
 //
-// The first two cases restate the reference's own tests of the path,
+// The first cases restate the reference's own tests of the int8 path,
 // src/backend/backend_naive_test.cc:355-405 (LinearQ8MatchesFp32) and
 // :407-425 (LinearQ8WithBias), run on the MI355X backend in fp32 and in fp16
 // mode.  The others cover what the model relies on and the reference never
@@ -18,6 +18,7 @@
 #include "vvllm_hip.h"
 
 using vvllm::BackendHIP;
+using vvllm::KVCacheHIP;
 
 namespace
 {
@@ -224,16 +225,117 @@ void ingest_bf16()
     EXPECT_NEAR(out.download()[0], (127.0 + 64.0) * (1.0f / 127.0f) + 0.5, 1e-5, "ingested row 0");
 }
 
-void outside_path_throws()
+// The other operators through the Backend interface, against double-precision
+// restatements of backend_naive.cc, one decode-step's worth of shapes.
+void decode_ops(bool fp16)
 {
-    BackendHIP backend(false);
-    bool threw = false;
-    try {
-        backend.rms_norm(nullptr, nullptr, nullptr, 0, 0.0f);
-    } catch (const std::logic_error&) {
-        threw = true;
+    BackendHIP backend(fp16);
+    const std::size_t H = 4, KVH = 2, D = 16, hidden = H * D, vocab = 50;
+    unsigned st = 7u;
+    auto rnd = [&]() { st = st * 1664525u + 1013904223u; return ((st >> 9) % 2001) / 1000.0f - 1.0f; };
+    auto q16 = [&](float v) { return fp16 ? from_half(to_half(v)) : v; };
+    double tol = fp16 ? 2e-3 : 1e-4;
+
+    // embedding (always fp32 out) + rms_norm
+    std::vector<float> table(vocab * hidden), w(hidden);
+    for (auto& v : table) v = rnd();
+    for (auto& v : w) v = 1.0f + 0.1f * rnd();
+    Act e32(false, hidden), x(fp16, hidden), y(fp16, hidden);
+    backend.embedding(e32.f(), table.data(), 17, hidden, vocab);
+    std::vector<float> e = e32.download();
+    for (std::size_t i = 0; i < hidden; i++) EXPECT_NEAR(e[i], table[17 * hidden + i], 0.0, "embedding");
+    std::vector<float> xv(e);
+    for (auto& v : xv) v = q16(v);
+    x.upload(xv);
+    backend.rms_norm(y.f(), x.f(), w.data(), hidden, 1e-6f);
+    double ss = 0;
+    for (float v : xv) ss += (double)v * v;
+    const double rms = std::sqrt(ss / hidden + 1e-6);
+    std::vector<float> got = y.download();
+    for (std::size_t i = 0; i < hidden; i++) EXPECT_NEAR(got[i], xv[i] / rms * w[i], tol * 3, "rms_norm");
+
+    // silu_mul
+    std::vector<float> g(hidden), u(hidden);
+    for (std::size_t i = 0; i < hidden; i++) { g[i] = q16(2 * rnd()); u[i] = q16(rnd()); }
+    Act dg(fp16, hidden), du(fp16, hidden);
+    dg.upload(g);
+    du.upload(u);
+    backend.silu_mul(y.f(), dg.f(), du.f(), hidden);
+    got = y.download();
+    for (std::size_t i = 0; i < hidden; i++)
+        EXPECT_NEAR(got[i], g[i] / (1.0 + std::exp(-(double)g[i])) * u[i], tol * 2, "silu_mul");
+
+    // rope at position 5 then attention over a KVCacheHIP of 3 positions
+    KVCacheHIP cache(fp16);
+    cache.init(1, KVH * D);
+    std::vector<std::vector<float>> ks, vs;
+    for (std::size_t pos = 0; pos < 3; pos++) {
+        std::vector<float> qv(H * D), kv(KVH * D), vv(KVH * D);
+        for (auto& v : qv) v = q16(rnd());
+        for (auto& v : kv) v = q16(rnd());
+        for (auto& v : vv) v = q16(rnd());
+        Act dq(fp16, H * D), dk(fp16, KVH * D), dv(fp16, KVH * D), out(fp16, H * D);
+        dq.upload(qv);
+        dk.upload(kv);
+        dv.upload(vv);
+        backend.rope(dq.f(), dk.f(), 1, H, KVH, D, pos, 10000.0f);
+        // expected rotation (split-half pairs)
+        auto rot = [&](std::vector<float>& hv, std::size_t heads) {
+            for (std::size_t h = 0; h < heads; h++)
+                for (std::size_t i = 0; i < D / 2; i++) {
+                    const double f = 1.0 / std::pow(10000.0, (double)(2 * i) / D), a = pos * f;
+                    const double x0 = hv[h * D + i], x1 = hv[h * D + i + D / 2];
+                    hv[h * D + i] = (float)(x0 * std::cos(a) - x1 * std::sin(a));
+                    hv[h * D + i + D / 2] = (float)(x0 * std::sin(a) + x1 * std::cos(a));
+                }
+        };
+        rot(qv, H);
+        rot(kv, KVH);
+        got = dk.download();
+        for (std::size_t i = 0; i < KVH * D; i++) EXPECT_NEAR(got[i], kv[i], tol * 4, "rope k");
+        ks.push_back(dk.download());
+        vs.push_back(vv);
+        const std::vector<float> qr = dq.download();
+        cache.append(0, dk.f(), dv.f(), 1);
+        cache.advance(1);
+        const float scale = 1.0f / std::sqrt((float)D);
+        backend.causal_attention(out.f(), dq.f(), 0, cache.k(0), cache.v(0), pos + 1, H, KVH, D, scale);
+        got = out.download();
+        for (std::size_t h = 0; h < H; h++) {
+            const std::size_t kh = h / (H / KVH);
+            std::vector<double> p(pos + 1);
+            double mx = -1e30, sum = 0;
+            for (std::size_t t = 0; t <= pos; t++) {
+                double dot = 0;
+                for (std::size_t d = 0; d < D; d++) dot += (double)qr[h * D + d] * ks[t][kh * D + d];
+                p[t] = dot * scale;
+                mx = std::max(mx, p[t]);
+            }
+            for (auto& v : p) { v = std::exp(v - mx); sum += v; }
+            for (std::size_t d = 0; d < D; d++) {
+                double o = 0;
+                for (std::size_t t = 0; t <= pos; t++) o += p[t] / sum * vs[t][kh * D + d];
+                EXPECT_NEAR(got[h * D + d], o, tol * 4, "causal_attention over KVCacheHIP");
+            }
+        }
     }
-    if (!threw) { std::fprintf(stderr, "rms_norm did not throw\n"); g_failures++; }
+    if (cache.seq_len() != 3) { std::fprintf(stderr, "kv cache length %zu\n", cache.seq_len()); g_failures++; }
+
+    // dense linear_add (fp32 weights on the host, fp16 on the device in fp16 mode)
+    const std::size_t N = 24;
+    std::vector<float> W(N * hidden), bias(N), res(N);
+    for (auto& v : W) v = 0.1f * rnd();
+    for (auto& v : bias) v = rnd();
+    for (auto& v : res) v = q16(rnd());
+    Act dr(fp16, N);
+    dr.upload(res);
+    backend.linear_add(dr.f(), x.f(), W.data(), bias.data(), dr.f(), 1, N, hidden);
+    got = dr.download();
+    for (std::size_t j = 0; j < N; j++) {
+        double acc = res[j] + bias[j];
+        for (std::size_t k = 0; k < hidden; k++) acc += (double)xv[k] * (fp16 ? from_half(to_half(W[j * hidden + k])) : W[j * hidden + k]);
+        EXPECT_NEAR(got[j], acc, tol * 8, "linear_add");
+    }
 }
 
 }  // namespace
@@ -254,7 +356,10 @@ int main()
     mirror_refresh();
     std::printf("[case] ingest bf16\n"); std::fflush(stdout);
     ingest_bf16();
-    outside_path_throws();
+    for (bool fp16 : {false, true}) {
+        std::printf("[case] decode ops fp16=%d\n", fp16); std::fflush(stdout);
+        decode_ops(fp16);
+    }
     if (g_failures) {
         std::fprintf(stderr, "test_backend_hip: %d failure(s)\n", g_failures);
         return 1;

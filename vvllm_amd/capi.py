@@ -89,6 +89,7 @@ SIGNATURES = {
     "vvh_argmax": (c_int, [c_void_p, c_size_t, c_void_p, c_void_p]),
     "vvh_mirror_f32": (c_int, [c_void_p, c_size_t, c_int, POINTER(c_void_p)]),
     "vvh_mirror_release": (c_int, [c_void_p]),
+    "vvh_memcpy_d2d_async": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
 }
 # entries that return a value rather than a vvh_status
 _NOT_STATUS = {"vvh_status_string", "vvh_last_error", "vvh_version", "vvh_device_cu_count",

@@ -629,6 +629,15 @@ VVH_API int vvh_memcpy_h2d(void* d, const void* s, size_t n) { return copy(d, s,
 VVH_API int vvh_memcpy_d2h(void* d, const void* s, size_t n) { return copy(d, s, n, hipMemcpyDeviceToHost, "memcpy d2h"); }
 VVH_API int vvh_memcpy_d2d(void* d, const void* s, size_t n) { return copy(d, s, n, hipMemcpyDeviceToDevice, "memcpy d2d"); }
 
+VVH_API int vvh_memcpy_d2d_async(void* d, const void* s, size_t n, void* stream)
+{
+    if (n == 0) return VVH_OK;
+    if (!d || !s) return fail(VVH_ERR_INVALID_ARG, "null pointer");
+    REQUIRE_INIT();
+    const hipError_t e = hipMemcpyAsync(d, s, n, hipMemcpyDeviceToDevice, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? VVH_OK : fail_hip(e, "memcpy d2d async");
+}
+
 // ---- caching allocator -------------------------------------------------------------
 VVH_API int vvh_pool_alloc(void** ptr, size_t bytes)
 {

@@ -2,6 +2,7 @@
 // libvvllm_hip.so.  See backend_hip.h.
 #include "backend_hip.h"
 
+#include <algorithm>
 #include <stdexcept>
 #include <string>
 
@@ -20,12 +21,6 @@ void check(int status, const char* what)
         throw std::runtime_error(std::string("BackendHIP: ") + what + ": " +
                                  vvh_status_string(status) + ": " + vvh_last_error());
     }
-}
-
-[[noreturn]] void outside_path(const char* op)
-{
-    throw std::logic_error(std::string("BackendHIP::") + op +
-                           " is outside the int8 linear path this backend implements");
 }
 
 }  // namespace
@@ -106,18 +101,169 @@ void BackendHIP::forget_weight(const int8_t* host_weight)
     if (vvh_weight_find(host_weight, &h) == VVH_OK) check(vvh_weight_release(h), "forget_weight");
 }
 
-void BackendHIP::matmul(float*, const float*, const float*, std::size_t, std::size_t, std::size_t) { outside_path("matmul"); }
-void BackendHIP::add(float*, const float*, const float*, std::size_t) { outside_path("add"); }
-void BackendHIP::mul(float*, const float*, const float*, std::size_t) { outside_path("mul"); }
-void BackendHIP::silu(float*, const float*, std::size_t) { outside_path("silu"); }
-void BackendHIP::rms_norm(float*, const float*, const float*, std::size_t, float) { outside_path("rms_norm"); }
-void BackendHIP::softmax(float*, const float*, std::size_t) { outside_path("softmax"); }
-void BackendHIP::rope(float*, float*, std::size_t, std::size_t, std::size_t, std::size_t, std::size_t, float) { outside_path("rope"); }
-void BackendHIP::linear(float*, const float*, const float*, const float*, std::size_t, std::size_t, std::size_t) { outside_path("linear"); }
-void BackendHIP::silu_mul(float*, const float*, const float*, std::size_t) { outside_path("silu_mul"); }
-void BackendHIP::linear_add(float*, const float*, const float*, const float*, const float*, std::size_t, std::size_t, std::size_t) { outside_path("linear_add"); }
-void BackendHIP::embedding(float*, const float*, std::size_t, std::size_t, std::size_t) { outside_path("embedding"); }
-void BackendHIP::causal_attention(float*, const float*, std::size_t, const float*, const float*, std::size_t, std::size_t, std::size_t, std::size_t, float) { outside_path("causal_attention"); }
+// ---- the other operators of a decode step (C ABI: vvh_eltwise & co.) ----
+// Weights, norm weights, biases and tables are host fp32 pointers, mirrored
+// on first use (vvh_mirror_f32); dense weights are mirrored as fp16 in fp16
+// mode (as BackendCUDA::linear does, backend_cuda.cc:171-181).
+const void* BackendHIP::host_mirror(const float* host, std::size_t n, int as_dtype)
+{
+    const void* dev = nullptr;
+    check(vvh_mirror_f32(host, n, as_dtype, &dev), "mirror");
+    return dev;
+}
+
+std::size_t BackendHIP::elem() const { return fp16_ ? 2 : 4; }
+
+void BackendHIP::matmul(float* out, const float* A, const float* B, std::size_t M, std::size_t N, std::size_t K)
+{
+    const float* dB = static_cast<const float*>(host_mirror(B, K * N, VVH_F32));
+    check(vvh_matmul(out, A, dB, M, N, K, act_dtype(), nullptr), "matmul");
+}
+
+void BackendHIP::add(float* out, const float* x, const float* y, std::size_t n)
+{
+    check(vvh_eltwise(VVH_OP_ADD, out, x, y, n, act_dtype(), nullptr), "add");
+}
+
+void BackendHIP::mul(float* out, const float* x, const float* y, std::size_t n)
+{
+    check(vvh_eltwise(VVH_OP_MUL, out, x, y, n, act_dtype(), nullptr), "mul");
+}
+
+void BackendHIP::silu(float* out, const float* x, std::size_t n)
+{
+    check(vvh_eltwise(VVH_OP_SILU, out, x, nullptr, n, act_dtype(), nullptr), "silu");
+}
+
+void BackendHIP::silu_mul(float* out, const float* gate, const float* up, std::size_t n)
+{
+    check(vvh_eltwise(VVH_OP_SILU_MUL, out, gate, up, n, act_dtype(), nullptr), "silu_mul");
+}
+
+void BackendHIP::rms_norm(float* out, const float* x, const float* weight, std::size_t n, float eps)
+{
+    const float* dw = static_cast<const float*>(host_mirror(weight, n, VVH_F32));
+    check(vvh_rms_norm(out, x, dw, 1, n, eps, act_dtype(), nullptr), "rms_norm");
+}
+
+void BackendHIP::softmax(float* out, const float* x, std::size_t n)
+{
+    check(vvh_softmax(out, x, 1, n, act_dtype(), nullptr), "softmax");
+}
+
+void BackendHIP::rope(float* q, float* k, std::size_t seq_len, std::size_t num_heads, std::size_t num_kv_heads,
+                      std::size_t head_dim, std::size_t pos, float theta)
+{
+    check(vvh_rope(q, k, seq_len, num_heads, num_kv_heads, head_dim, pos, theta, act_dtype(), nullptr), "rope");
+}
+
+void BackendHIP::linear(float* out, const float* inp, const float* weight, const float* bias, std::size_t M,
+                        std::size_t N, std::size_t K)
+{
+    const int wd = act_dtype();
+    const void* dw = host_mirror(weight, N * K, wd);
+    const float* db = bias ? static_cast<const float*>(host_mirror(bias, N, VVH_F32)) : nullptr;
+    check(vvh_dense(out, inp, dw, wd, db, nullptr, M, N, K, act_dtype(), nullptr), "linear");
+}
+
+void BackendHIP::linear_add(float* out, const float* inp, const float* weight, const float* bias,
+                            const float* residual, std::size_t M, std::size_t N, std::size_t K)
+{
+    const int wd = act_dtype();
+    const void* dw = host_mirror(weight, N * K, wd);
+    const float* db = bias ? static_cast<const float*>(host_mirror(bias, N, VVH_F32)) : nullptr;
+    check(vvh_dense(out, inp, dw, wd, db, residual, M, N, K, act_dtype(), nullptr), "linear_add");
+}
+
+// Always fp32 out: transformer_forward embeds into an fp32 tensor and converts
+// it itself in fp16 mode (include/vvllm/model/transformer.h:93-108).
+void BackendHIP::embedding(float* out, const float* table, std::size_t token_id, std::size_t hidden_size,
+                           std::size_t vocab_size)
+{
+    const float* dt = static_cast<const float*>(host_mirror(table, vocab_size * hidden_size, VVH_F32));
+    check(vvh_embedding(out, dt, token_id, hidden_size, vocab_size, VVH_F32, nullptr), "embedding");
+}
+
+// q is the whole [seq_len, num_heads, head_dim] buffer and q_idx its row; k and
+// v are device pointers (a KVCacheHIP's rows).
+void BackendHIP::causal_attention(float* out, const float* q, std::size_t q_idx, const float* k, const float* v,
+                                  std::size_t attend_len, std::size_t num_heads, std::size_t num_kv_heads,
+                                  std::size_t head_dim, float scale)
+{
+    const char* qrow = reinterpret_cast<const char*>(q) + q_idx * num_heads * head_dim * elem();
+    check(vvh_attention(out, qrow, k, v, 1, attend_len, num_heads, num_kv_heads, head_dim, scale, act_dtype(),
+                        nullptr),
+          "causal_attention");
+}
+
+// ---- KVCacheHIP ----
+KVCacheHIP::KVCacheHIP(bool fp16) : fp16_(fp16) {}
+
+KVCacheHIP::~KVCacheHIP()
+{
+    for (auto& l : layers_) {
+        if (l.k) vvh_free(l.k);
+        if (l.v) vvh_free(l.v);
+    }
+}
+
+void KVCacheHIP::init(std::size_t num_layers, std::size_t kv_dim)
+{
+    if (!layers_.empty()) return;  // idempotent, as transformer_forward calls it every step
+    kv_dim_ = kv_dim;
+    seq_len_ = 0;
+    layers_.resize(num_layers);
+    reserve(reserve_tokens_);
+}
+
+void KVCacheHIP::grow(Layer& l, std::size_t tokens)
+{
+    const std::size_t bytes = tokens * kv_dim_ * elem();
+    void* nk = nullptr;
+    void* nv = nullptr;
+    check(vvh_malloc(&nk, bytes), "kv cache");
+    check(vvh_malloc(&nv, bytes), "kv cache");
+    if (l.k && seq_len_) {
+        check(vvh_memcpy_d2d(nk, l.k, seq_len_ * kv_dim_ * elem()), "kv cache grow");
+        check(vvh_memcpy_d2d(nv, l.v, seq_len_ * kv_dim_ * elem()), "kv cache grow");
+    }
+    if (l.k) vvh_free(l.k);
+    if (l.v) vvh_free(l.v);
+    l.k = nk;
+    l.v = nv;
+    l.cap = tokens;
+}
+
+void KVCacheHIP::reserve(std::size_t tokens)
+{
+    reserve_tokens_ = tokens;
+    for (auto& l : layers_)
+        if (l.cap < tokens) grow(l, tokens);
+}
+
+void KVCacheHIP::append(std::size_t layer, const float* k, const float* v, std::size_t num_tokens)
+{
+    Layer& l = layers_.at(layer);
+    if (seq_len_ + num_tokens > l.cap) grow(l, std::max(seq_len_ + num_tokens, 2 * l.cap));
+    const std::size_t off = seq_len_ * kv_dim_ * elem(), n = num_tokens * kv_dim_ * elem();
+    check(vvh_memcpy_d2d_async(static_cast<char*>(l.k) + off, k, n, nullptr), "kv append");
+    check(vvh_memcpy_d2d_async(static_cast<char*>(l.v) + off, v, n, nullptr), "kv append");
+}
+
+const float* KVCacheHIP::k(std::size_t layer) const
+{
+    return layer < layers_.size() ? static_cast<const float*>(layers_[layer].k) : nullptr;
+}
+
+const float* KVCacheHIP::v(std::size_t layer) const
+{
+    return layer < layers_.size() ? static_cast<const float*>(layers_[layer].v) : nullptr;
+}
+
+void KVCacheHIP::truncate(std::size_t new_seq_len)
+{
+    if (new_seq_len < seq_len_) seq_len_ = new_seq_len;
+}
 
 void* hip_device_allocate(std::size_t bytes)
 {

@@ -1,14 +1,15 @@
 // BackendHIP: the MI355X backend of the INT8 per-channel linear path.
 //
-// A drop-in for the int8 linears of BackendCUDA (src/backend/backend_cuda.h:
-// 14-84): linear_q8 / linear_q8_add run hand-written gfx950 kernels through
-// the C ABI of libvvllm_hip.so (include/vvllm_hip.h); weights, scales and
-// biases are host pointers mirrored to HBM on first use; activations are
-// device pointers (fp32, or fp16 when constructed with fp16 = true, like
-// BackendCUDA(bool fp16), backend_cuda.cc:13-26).
+// A drop-in for BackendCUDA (src/backend/backend_cuda.h:14-84):
+// linear_q8 / linear_q8_add run hand-written gfx950 kernels through the C
+// ABI of libvvllm_hip.so (include/vvllm_hip.h), and so do the other
+// operators of a decode step (norm, RoPE, attention, SiLU-mul, embedding,
+// dense linear, ...).  Weights, scales, biases, norm weights and tables are
+// host pointers mirrored to HBM on first use; activations are device
+// pointers (fp32, or fp16 when constructed with fp16 = true, like
+// BackendCUDA(bool fp16), backend_cuda.cc:13-26).  KVCacheHIP keeps the
+// per-layer K/V rows in HBM.
 //
-// Operators outside the int8 linear path (norms, RoPE, attention, fp32
-// linear, ...) are not part of this backend and throw std::logic_error.
 // Failures of the C ABI are raised as std::runtime_error carrying the
 // library's message (the reference exits the process instead).
 #pragma once
@@ -17,7 +18,10 @@
 #include <cstdint>
 #include <string>
 
+#include <vector>
+
 #include "vvllm/backend/backend.h"
+#include "vvllm/kv_cache/kv_cache.h"
 
 namespace vvllm
 {
@@ -64,7 +68,7 @@ public:
     // and reused); the next linear_q8 on that pointer uploads again.
     void forget_weight(const int8_t* host_weight);
 
-    // ---- outside the int8 path ----
+    // ---- the other operators of a decode step ----
     void matmul(float*, const float*, const float*, std::size_t, std::size_t, std::size_t) override;
     void add(float*, const float*, const float*, std::size_t) override;
     void mul(float*, const float*, const float*, std::size_t) override;
@@ -86,9 +90,49 @@ private:
     std::uint64_t mirror(const int8_t* weight, const float* scales, const float* bias,
                          std::size_t N, std::size_t K);
     int act_dtype() const;
+    std::size_t elem() const;
+    const void* host_mirror(const float* host, std::size_t n, int as_dtype);
 
     bool fp16_;
     std::string name_;
+};
+
+// Key/value cache in HBM (KVCacheCUDA, src/kv_cache/kv_cache_cuda.cc:22-95):
+// per layer, rows of kv_dim values in the backend's activation dtype.
+// append() queues device-to-device copies on the null stream (the rows come
+// from device tensors).  reserve() sizes every layer for a whole context up
+// front (one allocation per layer; 288 GB of HBM holds long contexts), so
+// appends never reallocate.
+class KVCacheHIP : public KVCache
+{
+public:
+    explicit KVCacheHIP(bool fp16 = false);
+    ~KVCacheHIP() override;
+    KVCacheHIP(const KVCacheHIP&) = delete;
+    KVCacheHIP& operator=(const KVCacheHIP&) = delete;
+
+    void init(std::size_t num_layers, std::size_t kv_dim) override;
+    void append(std::size_t layer, const float* k, const float* v, std::size_t num_tokens) override;
+    const float* k(std::size_t layer) const override;
+    const float* v(std::size_t layer) const override;
+    void reset() override { seq_len_ = 0; }
+    void truncate(std::size_t new_seq_len) override;
+
+    void reserve(std::size_t tokens);
+    std::size_t seq_len() const { return seq_len_; }
+
+private:
+    struct Layer {
+        void* k = nullptr;
+        void* v = nullptr;
+        std::size_t cap = 0;  // tokens
+    };
+    void grow(Layer& l, std::size_t tokens);
+    std::size_t elem() const { return fp16_ ? 2 : 4; }
+
+    bool fp16_;
+    std::size_t reserve_tokens_ = 128;
+    std::vector<Layer> layers_;
 };
 
 // Tensor-layer hooks for Device::HIP: the bodies of device_allocate /
