@@ -560,6 +560,36 @@ def extras(ev, sets, projs, tmp_w, args):
                             "note": "host BF16 rows (pageable numpy memory) -> pinned staging -> device quantizer; "
                                     "wall time including the host copies"}
     print(f"[bench] weight ingest {nbytes / el / 1e9:.1f} GB/s", file=sys.stderr, flush=True)
+
+    # (7) a whole decode step at Qwen2.5-0.5B shapes: every operator of
+    # transformer_forward on the device (vvllm_amd.qwen2_decode), at position
+    # 511 of a filled KV cache, launched from Python and replayed from a graph
+    from vvllm_amd import qwen2_decode as qd
+    e2e = {}
+    for head in ("dense", "int8"):
+        m = qd.Model(qd.QWEN25_05B, act=F16, lm_head=head, max_ctx=1024, seed=3)
+        m.fill_kv(5)
+        P = 511
+        for i in range(3):
+            m.step(1, P)
+        ms_eager = timed(ev, lambda i: m.step(1, P), 10)
+        m.step(1, P, stream)  # sizes the capture stream's workspace before capture
+        capi.sync()
+        g = ev.graph(stream, lambda st: m.step(1, P, st))
+        for i in range(3):
+            ev.launch(g, stream)
+        ms_graph = timed(ev, lambda i: ev.launch(g, stream), 50, stream)
+        e2e[f"{head}_lm_head"] = {"launches_per_step": m.launches_per_step(), "position": P,
+                                  "us_per_token_graph": round(ms_graph * 1e3, 1),
+                                  "tok_per_s_graph": round(1e3 / ms_graph, 1),
+                                  "us_per_token_python_launches": round(ms_eager * 1e3, 1)}
+        m.close()
+        del m
+        print(f"[bench] decode step ({head} LM head) {ms_graph * 1e3:.0f} us graph, {ms_eager * 1e3:.0f} us eager",
+              file=sys.stderr, flush=True)
+    e2e["note"] = ("synthetic Qwen2.5-0.5B-shaped model (seeded weights), fp16 activations, int8 linears, greedy "
+                   "argmax on the device; GPU time per token, no host sampling or tokenizer")
+    out["decode_step"] = e2e
     return out
 
 

@@ -20,6 +20,12 @@
  *     Launches are asynchronous on it; errors of the launch itself are
  *     reported, errors of the kernel's execution surface at the next
  *     synchronising call.
+ *   - Split-K GEMMs and multi-chunk decode attention use a per-stream
+ *     workspace that grows on demand (hipMalloc).  Under HIP graph capture
+ *     it cannot grow: run the same calls once on that stream before
+ *     capturing (the workspace is at least 16 MiB; decode attention needs
+ *     at most 512 * (num_heads / num_kv_heads) * (head_dim + 2) * 4 bytes,
+ *     4.3 MB, at any span).
  *   - All calls may be made from one host thread at a time per device
  *     (as the reference, which is single-threaded, README.md:282); the
  *     allocator and registries are internally locked.
@@ -292,7 +298,9 @@ VVH_API int vvh_embedding(void* out, const float* dev_table, size_t token_id, si
  * k, v [*, num_kv_heads, head_dim] (head h reads kv head
  * h / (num_heads / num_kv_heads)); out [n_q, num_heads * head_dim].  One call
  * replaces the model's per-query loop (transformer.h:168-173).  head_dim <= 256,
- * len0 + n_q - 1 <= 16000. */
+ * len0 + n_q - 1 <= 16000; a single query (n_q = 1, the decode step) with
+ * head_dim a multiple of 8 up to 128, num_heads / num_kv_heads <= 16 and k, v
+ * 16-byte aligned attends to up to 2^30 positions. */
 VVH_API int vvh_attention(void* out, const void* q, const void* k, const void* v, size_t n_q, size_t len0,
                           size_t num_heads, size_t num_kv_heads, size_t head_dim, float scale, int dtype,
                           void* stream);

@@ -138,6 +138,13 @@ int launch_embedding(void* out, const float* table, int64_t token, int64_t hidde
 int64_t attention_max_len();
 int launch_attention(void* out, const void* q, const void* k, const void* v, int64_t n_q, int64_t len0, int64_t H,
                      int64_t KVH, int64_t D, float scale, int dtype, void* stream);
+// n_q = 1 fast path: grouped heads, split over the sequence; ws holds
+// attention_decode_ws_floats() floats when the span has more than one chunk
+bool attention_decode_ok(const void* k, const void* v, int64_t len, int64_t H, int64_t KVH, int64_t D);
+int64_t attention_decode_max_len();
+int64_t attention_decode_ws_floats(int64_t len, int64_t H, int64_t KVH, int64_t D);
+int launch_attention_decode(void* out, const void* q, const void* k, const void* v, int64_t len, int64_t H,
+                            int64_t KVH, int64_t D, float scale, float* ws, int dtype, void* stream);
 int launch_dense(void* out, const void* x, const void* w, int wdtype, const float* bias, const void* res, int64_t M,
                  int64_t N, int64_t K, int dtype, void* stream);
 int launch_matmul(void* out, const void* A, const float* B, int64_t M, int64_t N, int64_t K, int dtype, void* stream);

@@ -286,6 +286,263 @@ __global__ __launch_bounds__(256) void k_attention(T* __restrict__ out, const T*
     }
 }
 
+// ---------------------------------------------------------------------------
+// Decode attention (one query per head, n_q = 1).  At decode positions the
+// work is small (a few hundred K/V rows per layer) and latency-bound, so it
+// is spread over many short blocks.  Block (g, c) takes kv head g and the
+// keys [c * per_block, (c + 1) * per_block) for all G = H / KVH query heads
+// that read kv head g, so each K and V row is loaded once for G heads.
+//
+// A key row is split over L lanes of 8 consecutive dims (L = D / 8 rounded
+// up to a power of two), so a 256-thread block covers C = 256 / L keys per
+// sub-chunk with one 16-byte load of K and of V per lane (two for fp32).
+// Per sub-chunk:
+//   scores   lane-partial dots for the G heads, xor-reduced over the L lanes,
+//            into LDS (scores [G][C]); the V rows go to LDS as fp32;
+//   softmax  per head (wave w takes heads w, w + 4, ...): running max m,
+//            p = exp(s - m), running sum l = l * exp(m_old - m) + sum p;
+//   P.V      thread (h, d) pairs: acc = acc * exp(m_old - m) + sum_j p_j v_j[d].
+// One block per kv head writes out = acc / l; otherwise the block writes
+// (m, l, acc[0..D)) to ws and k_attention_combine rescales the blocks to
+// their common max.  D a multiple of 8 up to 128, G <= 16, k and v rows
+// 16-byte aligned.
+// ---------------------------------------------------------------------------
+constexpr int kAttnMaxD = 128;
+constexpr int kAttnMaxG = 16;
+constexpr int kAttnOutPerThread = kAttnMaxG * kAttnMaxD / 256;
+
+__host__ __device__ inline int attn_lanes(int D)
+{
+    int L = 1;
+    while (L * 8 < D) L <<= 1;
+    return L;
+}
+
+// 8 consecutive elements at p (16-byte aligned) as fp32
+__device__ __forceinline__ void load8(const f16* p, float f[8])
+{
+    const h8 v = *reinterpret_cast<const h8*>(p);
+#pragma unroll
+    for (int e = 0; e < 8; e++) f[e] = (float)v[e];
+}
+__device__ __forceinline__ void load8(const float* p, float f[8])
+{
+    const f4 a = *reinterpret_cast<const f4*>(p), b = *reinterpret_cast<const f4*>(p + 4);
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        f[e] = a[e];
+        f[4 + e] = b[e];
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_attention_decode(T* __restrict__ out, const T* __restrict__ q,
+                                                          const T* __restrict__ k, const T* __restrict__ v,
+                                                          int64_t len, int32_t H, int32_t KVH, int32_t D, float scale,
+                                                          int64_t per_block, float* __restrict__ ws)
+{
+    __shared__ float ps[kAttnMaxG * 256];  // [h][j]: scores, then probabilities (G * C <= 16 * 256)
+    __shared__ __align__(16) float vs[256 * 8];  // [j][d]: the sub-chunk's V rows (C * D <= 256 * 8)
+    __shared__ __align__(16) float qs[kAttnMaxG * kAttnMaxD];  // [h][d]: the G query rows
+    __shared__ float m_s[kAttnMaxG], l_s[kAttnMaxG], corr_s[kAttnMaxG];
+    const int g = blockIdx.x, tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
+    const int G = H / KVH;
+    const int L = attn_lanes(D), C = 256 / L;
+    const int j = tid / L, d0 = (tid % L) * 8;
+    const bool dims_on = d0 < D;
+    const int64_t kb = (int64_t)blockIdx.y * per_block;
+    const int64_t ke = kb + per_block < len ? kb + per_block : len;
+    const int64_t kvs = (int64_t)KVH * D;
+    const int GD = G * D;
+
+    for (int i = tid; i < GD; i += 256) qs[i] = ldf(q, (int64_t)g * GD + i);
+    float acc[kAttnOutPerThread];
+#pragma unroll
+    for (int i = 0; i < kAttnOutPerThread; i++) acc[i] = 0.0f;
+    if (tid < G) {
+        m_s[tid] = -INFINITY;
+        l_s[tid] = 0.0f;
+    }
+    __syncthreads();
+
+    for (int64_t t0 = kb; t0 < ke; t0 += C) {
+        const int64_t t = t0 + j;
+        const bool key_on = t < ke;
+        float kf[8], vf[8];
+        if (key_on && dims_on) {
+            load8(k + t * kvs + (int64_t)g * D + d0, kf);
+            load8(v + t * kvs + (int64_t)g * D + d0, vf);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) kf[e] = vf[e] = 0.0f;
+        }
+        float sc[kAttnMaxG];
+#pragma unroll
+        for (int h = 0; h < kAttnMaxG; h++) {
+            float a = 0.0f;
+            if (h < G) {
+                if (dims_on) {
+                    const f4 q0 = *reinterpret_cast<const f4*>(qs + h * D + d0);
+                    const f4 q1 = *reinterpret_cast<const f4*>(qs + h * D + d0 + 4);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) a += q0[e] * kf[e] + q1[e] * kf[4 + e];
+                }
+                for (int off = L >> 1; off > 0; off >>= 1) a += __shfl_xor(a, off);
+            }
+            sc[h] = a;
+        }
+        __syncthreads();  // the previous sub-chunk's P.V has read ps and vs
+        if (tid % L == 0) {
+#pragma unroll
+            for (int h = 0; h < kAttnMaxG; h++)
+                if (h < G) ps[h * C + j] = key_on ? sc[h] * scale : -INFINITY;
+        }
+        if (dims_on) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) vs[j * D + d0 + e] = vf[e];
+        }
+        __syncthreads();
+        for (int h = wv; h < G; h += 4) {
+            float mc = -INFINITY;
+            for (int i = lane; i < C; i += 64) mc = fmaxf(mc, ps[h * C + i]);
+            for (int off = 32; off > 0; off >>= 1) mc = fmaxf(mc, __shfl_xor(mc, off));
+            const float mo = m_s[h], mn = fmaxf(mo, mc);  // mc is finite: the sub-chunk has a key
+            float sum = 0.0f;
+            for (int i = lane; i < C; i += 64) {
+                const float e = expf(ps[h * C + i] - mn);
+                ps[h * C + i] = e;
+                sum += e;
+            }
+            for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+            if (lane == 0) {
+                const float cr = expf(mo - mn);  // 0 on the first sub-chunk
+                corr_s[h] = cr;
+                l_s[h] = l_s[h] * cr + sum;
+                m_s[h] = mn;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < kAttnOutPerThread; i++) {
+            const int o = tid + 256 * i;
+            if (o < GD) {
+                const int h = o / D, d = o - h * D;
+                float a = acc[i] * corr_s[h];
+                for (int jj = 0; jj < C; jj++) a += ps[h * C + jj] * vs[jj * D + d];
+                acc[i] = a;
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < kAttnOutPerThread; i++) {
+        const int o = tid + 256 * i;
+        if (o < GD) {
+            const int h = o / D, d = o - h * D, head = g * G + h;
+            if (gridDim.y == 1) {
+                stf(out, (int64_t)head * D + d, acc[i] / l_s[h]);
+            } else {
+                float* w = ws + ((int64_t)blockIdx.y * H + head) * (D + 2);
+                w[2 + d] = acc[i];
+                if (d == 0) {
+                    w[0] = m_s[h];
+                    w[1] = l_s[h];
+                }
+            }
+        }
+    }
+}
+
+// out[h][d] = sum_c e^(m_c - M) o_c[d] / sum_c e^(m_c - M) l_c, M = max_c m_c.
+// Block per head; thread (s, d) sums the blocks c = s, s + S, ... (S = 256 / D).
+template <typename T>
+__global__ __launch_bounds__(256) void k_attention_combine(T* __restrict__ out, const float* __restrict__ ws,
+                                                           int32_t blocks, int32_t H, int32_t D)
+{
+    __shared__ float red[256], den[256];
+    const int h = blockIdx.x, tid = threadIdx.x;
+    const int S = 256 / D, s = tid / D, d = tid - s * D;
+    float M = -INFINITY;
+    for (int c = tid; c < blocks; c += 256) M = fmaxf(M, ws[((int64_t)c * H + h) * (D + 2)]);
+    red[tid] = M;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if (tid < w) red[tid] = fmaxf(red[tid], red[tid + w]);
+        __syncthreads();
+    }
+    M = red[0];
+    __syncthreads();
+    float num = 0.0f, dn = 0.0f;
+    if (s < S) {
+        for (int c = s; c < blocks; c += S) {
+            const float* w = ws + ((int64_t)c * H + h) * (D + 2);
+            const float f = expf(w[0] - M);
+            num += f * w[2 + d];
+            dn += f * w[1];
+        }
+    }
+    red[tid] = num;
+    den[tid] = dn;
+    __syncthreads();
+    if (tid < D) {
+        float a = 0.0f, b = 0.0f;
+        for (int ss = 0; ss < S; ss++) {
+            a += red[ss * D + tid];
+            b += den[ss * D + tid];
+        }
+        stf(out, (int64_t)h * D + tid, a / b);
+    }
+}
+
+bool attention_decode_ok(const void* k, const void* v, int64_t len, int64_t H, int64_t KVH, int64_t D)
+{
+    return D % 8 == 0 && D <= kAttnMaxD && H / KVH <= kAttnMaxG && reinterpret_cast<uintptr_t>(k) % 16 == 0 &&
+           reinterpret_cast<uintptr_t>(v) % 16 == 0 && len <= attention_decode_max_len();
+}
+
+int64_t attention_decode_max_len() { return (int64_t)1 << 30; }
+
+// Keys per block: whole sub-chunks, as few as keep at most ~512 blocks in
+// the grid (two per CU), so short spans get one sub-chunk per block.
+static int64_t attn_per_block(int64_t len, int64_t KVH, int64_t D)
+{
+    const int64_t C = 256 / attn_lanes((int)D);
+    const int64_t chunks = (len + C - 1) / C;
+    const int64_t nb_max = std::max<int64_t>(1, 512 / KVH);
+    const int64_t per = (chunks + nb_max - 1) / nb_max;
+    return per * C;
+}
+
+int64_t attention_decode_ws_floats(int64_t len, int64_t H, int64_t KVH, int64_t D)
+{
+    const int64_t per = attn_per_block(len, KVH, D);
+    const int64_t nb = (len + per - 1) / per;
+    return nb > 1 ? nb * H * (D + 2) : 0;
+}
+
+int launch_attention_decode(void* out, const void* q, const void* k, const void* v, int64_t len, int64_t H,
+                            int64_t KVH, int64_t D, float scale, float* ws, int dtype, void* stream)
+{
+    const int64_t per = attn_per_block(len, KVH, D);
+    const int64_t nb = (len + per - 1) / per;
+    const dim3 grid((unsigned)KVH, (unsigned)nb);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (dtype == VVH_F16) {
+        hipLaunchKernelGGL(k_attention_decode<f16>, grid, dim3(256), 0, s, (f16*)out, (const f16*)q, (const f16*)k,
+                           (const f16*)v, len, (int32_t)H, (int32_t)KVH, (int32_t)D, scale, per, ws);
+        if (nb > 1)
+            hipLaunchKernelGGL(k_attention_combine<f16>, dim3((unsigned)H), dim3(256), 0, s, (f16*)out, ws,
+                               (int32_t)nb, (int32_t)H, (int32_t)D);
+    } else {
+        hipLaunchKernelGGL(k_attention_decode<float>, grid, dim3(256), 0, s, (float*)out, (const float*)q,
+                           (const float*)k, (const float*)v, len, (int32_t)H, (int32_t)KVH, (int32_t)D, scale, per,
+                           ws);
+        if (nb > 1)
+            hipLaunchKernelGGL(k_attention_combine<float>, dim3((unsigned)H), dim3(256), 0, s, (float*)out, ws,
+                               (int32_t)nb, (int32_t)H, (int32_t)D);
+    }
+    return (int)hipGetLastError();
+}
+
 int attention_lds_bytes(int64_t max_len) { return (int)(max_len * 4 > 256 * 4 ? max_len * 4 : 256 * 4); }
 // longest attention span served: its scores plus the kernel's static LDS stay
 // within 64 KB

@@ -1263,10 +1263,24 @@ VVH_API int vvh_attention(void* out, const void* q, const void* k, const void* v
         return fail(VVH_ERR_INVALID_ARG, "num_heads %zu not a multiple of num_kv_heads %zu", num_heads, num_kv_heads);
     if (head_dim == 0 || head_dim > 256) return fail(VVH_ERR_INVALID_ARG, "head_dim %zu outside 1..256", head_dim);
     if (len0 == 0) return fail(VVH_ERR_INVALID_ARG, "a query attends to at least one position");
-    if (len0 + n_q - 1 > (size_t)attention_max_len())
-        return fail(VVH_ERR_UNSUPPORTED, "attention span %zu > %lld", len0 + n_q - 1, (long long)attention_max_len());
     if (num_heads > 65535 || n_q > 65535) return fail(VVH_ERR_UNSUPPORTED, "grid too large");
+    const bool decode = n_q == 1 && attention_decode_ok(k, v, (int64_t)len0, (int64_t)num_heads,
+                                                        (int64_t)num_kv_heads, (int64_t)head_dim);
+    if (!decode && len0 + n_q - 1 > (size_t)attention_max_len())
+        return fail(VVH_ERR_UNSUPPORTED, "attention span %zu > %lld", len0 + n_q - 1, (long long)attention_max_len());
     REQUIRE_INIT();
+    if (decode) {
+        float* ws = nullptr;
+        const int64_t wsf = attention_decode_ws_floats((int64_t)len0, (int64_t)num_heads, (int64_t)num_kv_heads,
+                                                       (int64_t)head_dim);
+        if (wsf > 0) {
+            const int st = workspace_for(stream, (std::size_t)wsf * 4, &ws);
+            if (st != VVH_OK) return st;
+        }
+        return ret_launch(launch_attention_decode(out, q, k, v, (int64_t)len0, (int64_t)num_heads,
+                                                  (int64_t)num_kv_heads, (int64_t)head_dim, scale, ws, dtype, stream),
+                          "attention launch");
+    }
     return ret_launch(launch_attention(out, q, k, v, (int64_t)n_q, (int64_t)len0, (int64_t)num_heads,
                                        (int64_t)num_kv_heads, (int64_t)head_dim, scale, dtype, stream),
                       "attention launch");
