@@ -175,7 +175,9 @@ def test_attention_unaligned_cache(gpu, oracle, d):
     assert nerr(down(do, d, (H * D,)), ref) <= TOL[d]
 
 
-DENSE = [(1, 896, 896), (3, 1000, 130), (7, 40, 4864), (1, 151936, 896)]
+# K % 8 == 0 takes the 16-byte-load kernel (K = 8, K past one 2048-wide
+# round of loads), K = 130 the element-wise one
+DENSE = [(1, 896, 896), (3, 1000, 130), (7, 40, 4864), (1, 151936, 896), (2, 64, 8), (5, 300, 2056)]
 
 
 @pytest.mark.parametrize("d,wd", [(F32, F32), (F16, F16), (F16, F32)])
@@ -227,13 +229,19 @@ def test_matmul(gpu, oracle, d):
 def test_argmax(gpu):
     rng = np.random.default_rng(5)
     di = capi.DevBuf(4)
-    for n in (1, 1000, 151936):
+    # one block (n <= 2048), a second block of one element, many blocks, and
+    # more than 1024 blocks' worth (blocks then take more than 2048 each)
+    for n in (1, 1000, 2048, 2049, 151936, 5_000_001):
         x = rng.normal(0, 1, n).astype(np.float32)
         cases = [x]
         if n > 10:
             t = x.copy()
-            t[[3, n - 2, n // 2]] = 50.0  # ties: the first index wins, as std::max_element
+            t[[3, n - 2, n // 2]] = 50.0  # ties across blocks: the first index wins, as std::max_element
             cases.append(t)
+            t = x.copy()
+            t[-1] = 60.0  # the maximum in the last element
+            cases.append(t)
+            cases.append(np.full(n, -np.inf, np.float32))  # all equal: index 0
         for a in cases:
             dx = capi.DevBuf.from_array(a)
             capi.call("vvh_argmax", dx.ptr, n, di.ptr, None)

@@ -148,7 +148,9 @@ int launch_attention_decode(void* out, const void* q, const void* k, const void*
 int launch_dense(void* out, const void* x, const void* w, int wdtype, const float* bias, const void* res, int64_t M,
                  int64_t N, int64_t K, int dtype, void* stream);
 int launch_matmul(void* out, const void* A, const float* B, int64_t M, int64_t N, int64_t K, int dtype, void* stream);
-int launch_argmax(const float* x, int64_t n, int32_t* idx, void* stream);
+// ws: argmax_ws_bytes(n) bytes (none for n <= 2048)
+int64_t argmax_ws_bytes(int64_t n);
+int launch_argmax(const float* x, int64_t n, int32_t* idx, float* ws, void* stream);
 
 // Auxiliary kernels (aux_kernels.hip).
 // w: N x K elements of src_dtype (VVH_F32 or VVH_BF16)

@@ -606,26 +606,85 @@ __global__ __launch_bounds__(256) void k_dense(T* __restrict__ out, const T* __r
     }
 }
 
+// Same product with 16-byte loads (K a multiple of 8, x and w 16-byte
+// aligned): lane l takes elements [8 l, 8 l + 8) of each 512-wide k step,
+// four steps' weight loads in flight before their FMAs.
+template <typename T, typename WT>
+__global__ __launch_bounds__(256) void k_dense_vec(T* __restrict__ out, const T* __restrict__ x,
+                                                   const WT* __restrict__ w, const float* __restrict__ bias,
+                                                   const T* res, int64_t M, int64_t N, int64_t K)
+{
+    const int64_t n = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (n >= N) return;
+    const WT* wr = w + n * K;
+    for (int64_t m0 = 0; m0 < M; m0 += 4) {
+        const int mr = (int)(M - m0 < 4 ? M - m0 : 4);
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int64_t k0 = (int64_t)lane * 8; k0 < K; k0 += 4 * 512) {
+            float wf[4][8];
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                if (k0 + u * 512 < K) load8(wr + k0 + u * 512, wf[u]);
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                if (k0 + u * 512 < K) {
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        if (r < mr) {
+                            float xf[8];
+                            load8(x + (m0 + r) * K + k0 + u * 512, xf);
+#pragma unroll
+                            for (int e = 0; e < 8; e++) acc[r] += xf[e] * wf[u][e];
+                        }
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            float a = acc[r];
+            for (int off = 32; off > 0; off >>= 1) a += __shfl_xor(a, off);
+            acc[r] = a;
+        }
+        if (lane == 0) {
+            for (int r = 0; r < mr; r++) {
+                const int64_t o = (m0 + r) * N + n;
+                float y = acc[r] + (bias ? bias[n] : 0.0f);
+                if (res) y += ldf(res, o);
+                stf(out, o, y);
+            }
+        }
+    }
+}
+
 int launch_dense(void* out, const void* x, const void* w, int wdtype, const float* bias, const void* res, int64_t M,
                  int64_t N, int64_t K, int dtype, void* stream)
 {
     const dim3 grid((unsigned)((N + 3) / 4));
     hipStream_t s = static_cast<hipStream_t>(stream);
+    const bool vec = K % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0;
+#define VVH_DENSE(T, WT)                                                                                              \
+    if (vec)                                                                                                          \
+        hipLaunchKernelGGL((k_dense_vec<T, WT>), grid, dim3(256), 0, s, (T*)out, (const T*)x, (const WT*)w, bias,   \
+                           (const T*)res, M, N, K);                                                                   \
+    else                                                                                                              \
+        hipLaunchKernelGGL((k_dense<T, WT>), grid, dim3(256), 0, s, (T*)out, (const T*)x, (const WT*)w, bias,       \
+                           (const T*)res, M, N, K);
     if (dtype == VVH_F16) {
-        if (wdtype == VVH_F16)
-            hipLaunchKernelGGL((k_dense<f16, f16>), grid, dim3(256), 0, s, (f16*)out, (const f16*)x, (const f16*)w, bias,
-                               (const f16*)res, M, N, K);
-        else
-            hipLaunchKernelGGL((k_dense<f16, float>), grid, dim3(256), 0, s, (f16*)out, (const f16*)x, (const float*)w,
-                               bias, (const f16*)res, M, N, K);
+        if (wdtype == VVH_F16) {
+            VVH_DENSE(f16, f16)
+        } else {
+            VVH_DENSE(f16, float)
+        }
     } else {
-        if (wdtype == VVH_F16)
-            hipLaunchKernelGGL((k_dense<float, f16>), grid, dim3(256), 0, s, (float*)out, (const float*)x, (const f16*)w,
-                               bias, (const float*)res, M, N, K);
-        else
-            hipLaunchKernelGGL((k_dense<float, float>), grid, dim3(256), 0, s, (float*)out, (const float*)x,
-                               (const float*)w, bias, (const float*)res, M, N, K);
+        if (wdtype == VVH_F16) {
+            VVH_DENSE(float, f16)
+        } else {
+            VVH_DENSE(float, float)
+        }
     }
+#undef VVH_DENSE
     return (int)hipGetLastError();
 }
 
@@ -656,49 +715,90 @@ int launch_matmul(void* out, const void* A, const float* B, int64_t M, int64_t N
 
 // ---------------------------------------------------------------------------
 // argmax over n fp32 values: the first index of the maximum, as
-// std::max_element (src/sampler/sampler.cc:21-25).  One block.
+// std::max_element (src/sampler/sampler.cc:21-25).  Block b takes the span
+// [b * per, (b + 1) * per) and writes its (max, first index) to the
+// workspace; one block then reduces the partials in block order.  A single
+// block writes the index directly.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, int64_t n, int32_t* __restrict__ idx)
+// (v, i) = the better of (v, i) and (ov, oi): larger value, then lower index
+__device__ __forceinline__ void argmax_merge(float& v, int64_t& i, float ov, int64_t oi)
 {
-    __shared__ float bv[16];
-    __shared__ int64_t bi[16];
-    float best = -INFINITY;
-    int64_t besti = n;  // n: none seen yet
-    for (int64_t i = threadIdx.x; i < n; i += 1024) {  // increasing i: strictly greater keeps the first
-        const float v = x[i];
-        if (besti == n || v > best) {
-            best = v;
-            besti = i;
-        }
+    if (ov > v || (ov == v && oi < i)) {
+        v = ov;
+        i = oi;
     }
-    for (int off = 32; off > 0; off >>= 1) {
-        const float ov = __shfl_xor(best, off);
-        const int64_t oi = __shfl_xor(besti, off);
-        if (ov > best || (ov == best && oi < besti)) {
-            best = ov;
-            besti = oi;
-        }
-    }
+}
+
+__device__ __forceinline__ void argmax_block(float& best, int64_t& besti)
+{
+    __shared__ float bv[4];
+    __shared__ int64_t bi[4];
+    for (int off = 32; off > 0; off >>= 1) argmax_merge(best, besti, __shfl_xor(best, off), __shfl_xor(besti, off));
     if ((threadIdx.x & 63) == 0) {
         bv[threadIdx.x >> 6] = best;
         bi[threadIdx.x >> 6] = besti;
     }
     __syncthreads();
+    best = bv[0];
+    besti = bi[0];
+    for (int w = 1; w < 4; w++) argmax_merge(best, besti, bv[w], bi[w]);
+}
+
+__global__ __launch_bounds__(256) void k_argmax_part(const float* __restrict__ x, int64_t n, int64_t per,
+                                                     float* __restrict__ pv, int64_t* __restrict__ pi,
+                                                     int32_t* __restrict__ idx)
+{
+    const int64_t b0 = (int64_t)blockIdx.x * per;
+    const int64_t e = b0 + per < n ? b0 + per : n;
+    float best = -INFINITY;
+    int64_t besti = e;  // e: none seen yet (the block's span is never empty)
+    for (int64_t i = b0 + threadIdx.x; i < e; i += 256) {  // increasing i: strictly greater keeps the first
+        const float v = x[i];
+        if (besti == e || v > best) {
+            best = v;
+            besti = i;
+        }
+    }
+    argmax_block(best, besti);
     if (threadIdx.x == 0) {
-        float b = bv[0];
-        int64_t ix = bi[0];
-        for (int w = 1; w < 16; w++)
-            if (bv[w] > b || (bv[w] == b && bi[w] < ix)) {
-                b = bv[w];
-                ix = bi[w];
-            }
-        idx[0] = (int32_t)ix;
+        if (gridDim.x == 1) {
+            idx[0] = (int32_t)besti;
+        } else {
+            pv[blockIdx.x] = best;
+            pi[blockIdx.x] = besti;
+        }
     }
 }
 
-int launch_argmax(const float* x, int64_t n, int32_t* idx, void* stream)
+__global__ __launch_bounds__(256) void k_argmax_final(const float* __restrict__ pv, const int64_t* __restrict__ pi,
+                                                      int32_t nb, int32_t* __restrict__ idx)
 {
-    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, static_cast<hipStream_t>(stream), x, n, idx);
+    float best = -INFINITY;
+    int64_t besti = INT64_MAX;
+    for (int b = threadIdx.x; b < nb; b += 256) argmax_merge(best, besti, pv[b], pi[b]);
+    argmax_block(best, besti);
+    if (threadIdx.x == 0) idx[0] = (int32_t)besti;
+}
+
+constexpr int64_t kArgmaxPer = 2048;  // elements per block
+constexpr int64_t kArgmaxMaxBlocks = 1024;
+
+int64_t argmax_ws_bytes(int64_t n)
+{
+    const int64_t per = std::max(kArgmaxPer, (n + kArgmaxMaxBlocks - 1) / kArgmaxMaxBlocks);
+    const int64_t nb = (n + per - 1) / per;
+    return nb > 1 ? nb * 12 : 0;
+}
+
+int launch_argmax(const float* x, int64_t n, int32_t* idx, float* ws, void* stream)
+{
+    const int64_t per = std::max(kArgmaxPer, (n + kArgmaxMaxBlocks - 1) / kArgmaxMaxBlocks);
+    const int64_t nb = (n + per - 1) / per;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    int64_t* pi = reinterpret_cast<int64_t*>(ws);  // nb int64 indices, then nb fp32 values
+    float* pv = ws ? reinterpret_cast<float*>(pi + nb) : nullptr;
+    hipLaunchKernelGGL(k_argmax_part, dim3((unsigned)nb), dim3(256), 0, s, x, n, per, pv, pi, idx);
+    if (nb > 1) hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(256), 0, s, pv, pi, (int32_t)nb, idx);
     return (int)hipGetLastError();
 }
 

@@ -1318,7 +1318,13 @@ VVH_API int vvh_argmax(const float* logits, size_t n, int32_t* dev_index, void* 
     if (!logits || !dev_index) return fail(VVH_ERR_INVALID_ARG, "null pointer");
     if (n == 0 || n > INT32_MAX) return fail(VVH_ERR_INVALID_ARG, "bad length %zu", n);
     REQUIRE_INIT();
-    return ret_launch(launch_argmax(logits, (int64_t)n, dev_index, stream), "argmax launch");
+    float* ws = nullptr;
+    const int64_t wsb = argmax_ws_bytes((int64_t)n);
+    if (wsb > 0) {
+        const int st = workspace_for(stream, (std::size_t)wsb, &ws);
+        if (st != VVH_OK) return st;
+    }
+    return ret_launch(launch_argmax(logits, (int64_t)n, dev_index, ws, stream), "argmax launch");
 }
 
 VVH_API int vvh_mirror_f32(const float* host, size_t n, int as_dtype, const void** dev)
