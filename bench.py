@@ -579,7 +579,7 @@ def extras(ev, sets, projs, tmp_w, args):
         for i in range(3):
             ev.launch(g, stream)
         ms_graph = timed(ev, lambda i: ev.launch(g, stream), 50, stream)
-        e2e[f"{head}_lm_head"] = {"launches_per_step": m.launches_per_step(), "position": P,
+        e2e[f"{head}_lm_head"] = {"calls_per_step": m.calls_per_step(), "position": P,
                                   "us_per_token_graph": round(ms_graph * 1e3, 1),
                                   "tok_per_s_graph": round(1e3 / ms_graph, 1),
                                   "us_per_token_python_launches": round(ms_eager * 1e3, 1)}

@@ -144,7 +144,9 @@ class Model:
             capi.call("vvh_fill_normal", L["kc"].ptr, self.act, n, seed + 2 * l, 0.0, 1.0, None)
             capi.call("vvh_fill_normal", L["vc"].ptr, self.act, n, seed + 2 * l + 1, 0.0, 1.0, None)
 
-    def launches_per_step(self) -> int:
+    def calls_per_step(self) -> int:
+        """C-ABI calls per step (attention over more than one block and the
+        argmax over the vocabulary launch two kernels each)."""
         c = self.cfg
         head = 1 if self.lm_head == "int8" or self.act == F32 else 2
         return (2 if self.act == F16 else 1) + 11 * c.layers + 1 + head + 1
@@ -229,3 +231,38 @@ class Model:
         for L, (ln1, ln2) in zip(self.layers, self.norms_host):
             out["layers"].append(dict(ln1=ln1, ln2=ln2, **{k: q8(L[k]) for k in ("q", "k", "v", "o", "gu", "down")}))
         return out
+
+
+def main(argv=None) -> int:
+    """Runs decode steps of the synthetic Qwen2.5-0.5B-shaped model at one
+    position of a filled KV cache (e.g. under rocprofv3 --kernel-trace):
+
+        python -m vvllm_amd.qwen2_decode --lm-head int8 --position 511 --steps 5
+    """
+    import argparse
+    import time
+
+    ap = argparse.ArgumentParser(description=main.__doc__)
+    ap.add_argument("--lm-head", choices=("dense", "int8"), default="int8")
+    ap.add_argument("--act", choices=("f16", "f32"), default="f16")
+    ap.add_argument("--position", type=int, default=511)
+    ap.add_argument("--steps", type=int, default=5)
+    a = ap.parse_args(argv)
+    capi.init(0)
+    m = Model(QWEN25_05B, act=F16 if a.act == "f16" else F32, lm_head=a.lm_head, max_ctx=a.position + 1, seed=3)
+    m.fill_kv(5)
+    m.step(1, a.position)
+    capi.sync()
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        m.step(1, a.position)
+    tok = m.next_token()
+    el = (time.perf_counter() - t0) / a.steps
+    print(f"{a.steps} steps at position {a.position} ({a.lm_head} LM head, {a.act}): {el * 1e6:.0f} us/step "
+          f"launched from Python, next token {tok}", flush=True)
+    m.close()
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())
