@@ -26,7 +26,7 @@ TEST_BIN = os.path.join(ROOT, "tests", "cpp", "bin")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 CXX = os.environ.get("CXX", "g++")
 
-HIP_SOURCES = ["runtime.hip", "linear_kernels.hip", "model_kernels.hip", "aux_kernels.hip"]
+HIP_SOURCES = ["runtime.hip", "linear_kernels.hip", "gemm_kernels.hip", "model_kernels.hip", "aux_kernels.hip"]
 HIP_FLAGS = [
     "--offload-arch=gfx950",
     "-O3",

@@ -1,0 +1,411 @@
+// k_gemm3: the prefill / batched int8 linear (fp16 activations, M > 16,
+// K % 64 == 0), one output tile per block, no split-K.
+//
+// out[M, N] = (x[M, K] . codes[N, K]^T) * scale[N] + bias[N] (+ res[M, N]),
+// the Backend::linear_q8 / linear_q8_add contract
+// (include/vvllm/backend/backend.h:62-65, 75-78) on MFMA.
+//
+// Block tile 128(m) x BN(n) x 64(k), BN = 32 * TJ * WN; 2 x WN waves, each a
+// 64 x (32 * TJ) wave tile built from 2 x TJ v_mfma_f32_32x32x16_f16 tiles.
+// The wave tile is chosen for the LDS read rate: per MFMA a wave reads
+// (8 KB of A + TJ * 2 KB of B) / (8 TJ) from LDS, 0.58 KB at TJ = 3 against
+// 1.25 KB for the 64 x 32 tile of k_gemm2, whose 8 waves read more bytes per
+// stage than the LDS delivers in the stage's MFMA time.
+//
+// Operands are staged through a ring of D LDS stages filled by direct
+// global -> LDS loads (global_load_lds_dwordx4), A as fp16 and B as the raw
+// int8 codes, in the same swizzled layout as k_gemm2 (swz_a / swz_b).  The
+// codes are converted to fp16 exactly (two v_perm and one packed subtract
+// per 4 codes) half a stage ahead of their MFMAs: the second k slice of a
+// stage is converted during the first slice's MFMAs, and the first k slice
+// of the next stage during the second slice's MFMAs, so no MFMA waits on a
+// conversion once the loop runs.
+//
+// Step j (stage j in registers, its first slice converted):
+//   wait for stage j+1's loads; barrier;
+//   refill stage j's buffer with k stage j + D; read stage j+1's fragments;
+//   MFMAs of (j, slice 0) || convert (j, slice 1);
+//   MFMAs of (j, slice 1) || convert (j+1, slice 0).
+// Stage indices, fragment parity and wait thresholds are compile-time
+// constants (the loop is unrolled by D, D even).
+//
+// The MFMAs compute the transposed tile (codes as the A operand, activations
+// as B): lane l then holds, for each group g of its 16 accumulator values,
+// four consecutive outputs n of row m = l % 32, which go to LDS as one
+// 16-byte write.
+//
+// Epilogue: the raw fp32 sums go through LDS (32-row quarter q of the tile
+// in stage buffer q); each thread then owns one 8-wide column chunk (its 8
+// scales and biases loaded at kernel start), applies acc * scale + bias
+// (+ residual) in fp32 with one rounding, and stores rows with 16-byte
+// stores, four rows' LDS reads in flight at a time.
+#include "common.h"
+#include "device.h"
+
+namespace vvh
+{
+
+template <int BN>
+struct Gemm3Stage {
+    static constexpr int kOps = kGemmBM * kGemmBK * 2 + BN * kGemmBK;  // A fp16 + B codes
+    static constexpr int kEpi = 32 * (BN + 4) * 4;                        // one epilogue quarter, fp32
+    __attribute__((aligned(16))) f16 a[kGemmBM * kGemmBK];
+    __attribute__((aligned(16))) int8_t b[BN * kGemmBK];
+    __attribute__((aligned(16))) char pad[kEpi > kOps ? kEpi - kOps : 16];
+};
+
+template <int TJ>
+struct Gemm3Frag {
+    u4 b[2][TJ];     // raw codes: slice kk2, column tile tj
+    h8 a[2][2][2];   // fp16 A: slice kk2, half h, row tile ti
+};
+
+template <int TJ>
+__device__ __forceinline__ void gemm3_read(const f16* __restrict__ sa, const int8_t* __restrict__ sb,
+                                           Gemm3Frag<TJ>& f, int row0, int col0, int fl, int fh)
+{
+#pragma unroll
+    for (int kk2 = 0; kk2 < 2; kk2++) {
+#pragma unroll
+        for (int tj = 0; tj < TJ; tj++) {
+            const int j = col0 + tj * 32 + fl;
+            f.b[kk2][tj] = *reinterpret_cast<const u4*>(sb + j * 64 + swz_b(j, kk2 * 2 + fh) * 16);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int ti = 0; ti < 2; ti++) {
+                const int i = row0 + ti * 32 + fl;
+                f.a[kk2][h][ti] = *reinterpret_cast<const h8*>(sa + i * 64 + swz_a(i, kk2 * 4 + fh * 2 + h) * 8);
+            }
+    }
+}
+
+template <int TJ>
+__device__ __forceinline__ void gemm3_convert(const u4 (&b)[TJ], h8 (&fb)[TJ][2])
+{
+#pragma unroll
+    for (int tj = 0; tj < TJ; tj++) i8x16_to_h8x2(b[tj], fb[tj][0], fb[tj][1]);
+}
+
+// MFMAs of one 32-wide k slice (2 x 2 x TJ of them) with the conversion of
+// another slice's codes (20 * TJ VALU) spread between them.
+template <int TJ>
+__device__ __forceinline__ void gemm3_slice(const h8 (&a)[2][2], const h8 (&fb)[TJ][2], f16v (&acc)[2][TJ],
+                                            const u4 (&nb)[TJ], h8 (&nfb)[TJ][2])
+{
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int ti = 0; ti < 2; ti++)
+#pragma unroll
+            for (int tj = 0; tj < TJ; tj++)
+                acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[tj][h], a[h][ti], acc[ti][tj], 0, 0, 0);
+    gemm3_convert<TJ>(nb, nfb);
+    constexpr int NM = 4 * TJ;
+    constexpr int NV = (20 * TJ + NM - 1) / NM;
+#pragma unroll
+    for (int i = 0; i < NM; i++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, NV, 0);  // then conversion VALU
+    }
+}
+
+template <int TJ>
+__device__ __forceinline__ void gemm3_slice_last(const h8 (&a)[2][2], const h8 (&fb)[TJ][2], f16v (&acc)[2][TJ])
+{
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int ti = 0; ti < 2; ti++)
+#pragma unroll
+            for (int tj = 0; tj < TJ; tj++)
+                acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[tj][h], a[h][ti], acc[ti][tj], 0, 0, 0);
+}
+
+// One stage's direct-to-LDS loads of this wave: buffer loads whose per-lane
+// offsets are fixed for the whole k loop and whose stage offset k0 goes in
+// the scalar offset, so a stage costs no address arithmetic.
+template <int NW, int BN>
+__device__ __forceinline__ void gemm3_fill(f16* __restrict__ sa, int8_t* __restrict__ sb, __amdgpu_buffer_rsrc_t ra,
+                                           __amdgpu_buffer_rsrc_t rb, const uint32_t* a_off, const uint32_t* b_off,
+                                           int wave, uint32_t k0)
+{
+    constexpr int LA = 16 / NW, LB = BN / 16 / NW;
+#pragma unroll
+    for (int i = 0; i < LA; i++)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, sa + (wave * LA + i) * 512, 16, a_off[i], k0 * 2, 0, 0);
+#pragma unroll
+    for (int i = 0; i < LB; i++)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, sb + (wave * LB + i) * 1024, 16, b_off[i], k0, 0, 0);
+}
+
+template <typename OT, int D, int WN, int TJ>
+__global__ __launch_bounds__(128 * WN, 1) void k_gemm3(LinArgs a)
+{
+    static_assert(D == 4, "four stages: even (static fragment parity) and one epilogue quarter per stage");
+    constexpr int NW = 2 * WN;
+    constexpr int NT = 64 * NW;
+    constexpr int BN = 32 * TJ * WN;
+    static_assert(16 % NW == 0 && (BN / 16) % NW == 0, "whole 1 KB loads per wave");
+    constexpr int LA = 16 / NW, LB = BN / 16 / NW;
+    constexpr int LPS = LA + LB;  // loads per stage per thread
+    using Stage = Gemm3Stage<BN>;
+    using Frag = Gemm3Frag<TJ>;
+    __shared__ Stage st0, st1, st2, st3;
+
+    const int64_t nbm = (a.M + kGemmBM - 1) / kGemmBM;
+    const int64_t nbn = (a.N + BN - 1) / BN;
+    const int64_t tile = xcd_remap(blockIdx.x, nbm * nbn);  // consecutive tiles (same n0) on one XCD
+    const int64_t m0 = (tile % nbm) * kGemmBM;
+    const int64_t n0 = (tile / nbm) * BN;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave & 1, wn = wave >> 1;
+    const int row0 = wm * 64, col0 = wn * (32 * TJ);
+    const int fl = lane & 31, fh = lane >> 5;
+    const f16* X = static_cast<const f16*>(a.inp);
+
+    // epilogue: thread t < RG * CH owns column chunk t % CH (8 outputs) of
+    // rows t / CH, t / CH + RG, ...; its scales and biases are loaded first
+    // (the oldest loads in the vmcnt queue)
+    constexpr int CH = BN / 8;
+    constexpr int RG = NT / CH;
+    const int ech = tid % CH, erg = tid / CH;
+    const int64_t en = n0 + ech * 8;
+    float sc[8], bi[8];
+    if (a.N % 8 == 0) {  // 16-byte loads at a clamped (always valid) chunk
+        const int64_t ec = en < a.N ? en : a.N - 8;
+        const f4 s0 = *reinterpret_cast<const f4*>(a.scales + ec), s1 = *reinterpret_cast<const f4*>(a.scales + ec + 4);
+        f4 b0 = f4{}, b1 = f4{};
+        if (a.bias) {
+            b0 = *reinterpret_cast<const f4*>(a.bias + ec);
+            b1 = *reinterpret_cast<const f4*>(a.bias + ec + 4);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            sc[e] = s0[e];
+            sc[4 + e] = s1[e];
+            bi[e] = b0[e];
+            bi[4 + e] = b1[e];
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            sc[e] = en + e < a.N ? a.scales[en + e] : 0.0f;
+            bi[e] = (a.bias && en + e < a.N) ? a.bias[en + e] : 0.0f;
+        }
+    }
+
+    // buffer resources based at the tile's first row (rows past M or N read
+    // the last valid row), per-lane byte offsets within them
+    const uint64_t a_bytes = (uint64_t)(a.M - m0) * a.K * 2, b_bytes = (uint64_t)(a.N - n0) * a.K;
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<f16*>(X + m0 * a.K), 0, (int)(a_bytes < 0xFFFFFFFFull ? a_bytes : 0xFFFFFFFFull), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int8_t*>(a.w + n0 * a.K), 0, (int)(b_bytes < 0xFFFFFFFFull ? b_bytes : 0xFFFFFFFFull), 0x00020000);
+    uint32_t a_off[LA];
+#pragma unroll
+    for (int i = 0; i < LA; i++) {
+        const int r = (wave * LA + i) * 8 + (lane >> 3);
+        const int64_t gr = m0 + r < a.M ? r : a.M - 1 - m0;
+        a_off[i] = (uint32_t)(gr * a.K * 2 + swz_a(r, lane & 7) * 16);
+    }
+    uint32_t b_off[LB];
+#pragma unroll
+    for (int i = 0; i < LB; i++) {
+        const int r = (wave * LB + i) * 16 + (lane >> 2);
+        const int64_t gn = n0 + r < a.N ? r : a.N - 1 - n0;
+        b_off[i] = (uint32_t)(gn * a.K + swz_b(r, lane & 3) * 16);
+    }
+
+    auto stage = [&](auto S) -> Stage& {
+        constexpr int s = decltype(S)::value % D;
+        if constexpr (s == 0) return st0;
+        else if constexpr (s == 1) return st1;
+        else if constexpr (s == 2) return st2;
+        else return st3;
+    };
+    auto issue = [&](Stage& g, int64_t kt) {
+        gemm3_fill<NW, BN>(g.a, g.b, ra, rb, a_off, b_off, wave, (uint32_t)(kt * kGemmBK));
+    };
+
+    f16v acc[2][TJ];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < TJ; j++) acc[i][j] = f16v{};
+    Frag f0, f1;
+    h8 fb[2][TJ][2];  // converted codes: slice, column tile, half
+    auto frag = [&](auto P) -> Frag& {
+        if constexpr (decltype(P)::value % 2 == 0) return f0;
+        else return f1;
+    };
+    auto read = [&](auto S) { gemm3_read<TJ>(stage(S).a, stage(S).b, frag(S), row0, col0, fl, fh); };
+
+    // one step of the schedule; NEXT: stage j+1 exists, REFILL: refill
+    // stage j's buffer with k stage kt0 + j + D, VM: loads still allowed in
+    // flight once stage j+1 has landed
+    auto step = [&]<int J, bool NEXT, bool REFILL, int VM>(int64_t kt0) {
+        constexpr auto j = std::integral_constant<int, J>{};
+        constexpr auto jn = std::integral_constant<int, J + 1>{};
+        if constexpr (NEXT) wait_vmcnt<VM>();
+        lds_barrier();
+        if constexpr (REFILL) issue(stage(j), kt0 + J + D);
+        if constexpr (NEXT) read(jn);
+        Frag& f = frag(j);
+        gemm3_slice<TJ>(f.a[0], fb[0], acc, f.b[1], fb[1]);
+        if constexpr (NEXT) gemm3_slice<TJ>(f.a[1], fb[1], acc, frag(jn).b[0], fb[0]);
+        else gemm3_slice_last<TJ>(f.a[1], fb[1], acc);
+    };
+    // R steps from kt0 (kt0 % D == 0) with the problem's stage count kt0 + R
+    auto steps = [&]<int R>(int64_t kt0) {
+        [&]<int... J>(std::integer_sequence<int, J...>) {
+            (step.template operator()<J, (J + 1 < R), (J + D < R),
+                                      ((R - 2 - J < D - 2) ? R - 2 - J : D - 2) * LPS>(kt0),
+             ...);
+        }(std::make_integer_sequence<int, R>{});
+    };
+    auto prologue = [&]<int P>() {
+        [&]<int... S>(std::integer_sequence<int, S...>) {
+            (issue(stage(std::integral_constant<int, S>{}), S), ...);
+        }(std::make_integer_sequence<int, P>{});
+        wait_vmcnt<(P - 1) * LPS>();
+        lds_barrier();
+        read(std::integral_constant<int, 0>{});
+        gemm3_convert<TJ>(f0.b[0], fb[0]);
+    };
+
+    const int64_t nk = a.K / kGemmBK;
+    if (nk >= D) {
+        prologue.template operator()<D>();
+        int64_t kt0 = 0;
+        for (; kt0 + 2 * D <= nk; kt0 += D) {
+            // a full group: every step refills and waits at the steady-state depth
+            [&]<int... J>(std::integer_sequence<int, J...>) {
+                (step.template operator()<J, true, true, (D - 2) * LPS>(kt0), ...);
+            }(std::make_integer_sequence<int, D>{});
+        }
+        const int64_t r = nk - kt0;  // D .. 2D-1
+        [&]<int... R>(std::integer_sequence<int, R...>) {
+            ((r == R + D ? steps.template operator()<R + D>(kt0) : void()), ...);
+        }(std::make_integer_sequence<int, D>{});
+    } else {
+        [&]<int... R>(std::integer_sequence<int, R...>) {
+            ((nk == R + 1 ? [&] {
+                prologue.template operator()<R + 1>();
+                steps.template operator()<R + 1>(0);
+            }() : void()), ...);
+        }(std::make_integer_sequence<int, D - 1>{});
+    }
+
+    // ---- epilogue ----
+    __builtin_amdgcn_s_waitcnt(0);
+    lds_barrier();
+    constexpr int ES = BN + 4;  // fp32 row stride of an epilogue quarter
+    auto quarter = [&](int q) -> float* {
+        return reinterpret_cast<float*>(q == 0 ? &st0 : q == 1 ? &st1 : q == 2 ? &st2 : &st3);
+    };
+#pragma unroll
+    for (int ti = 0; ti < 2; ti++) {
+        float* q = quarter((row0 >> 5) + ti) + fl * ES + col0 + 4 * fh;
+#pragma unroll
+        for (int tj = 0; tj < TJ; tj++)
+#pragma unroll
+            for (int g = 0; g < 4; g++)
+                *reinterpret_cast<f4*>(q + tj * 32 + 8 * g) =
+                    f4{acc[ti][tj][4 * g], acc[ti][tj][4 * g + 1], acc[ti][tj][4 * g + 2], acc[ti][tj][4 * g + 3]};
+    }
+    lds_barrier();
+    if (erg >= RG || en >= a.N) return;
+    const bool vec = (a.N % 8) == 0 && en + 8 <= a.N;
+    constexpr int RI = (kGemmBM + RG - 1) / RG;  // rows per thread
+    constexpr int U = 4;                         // rows whose LDS reads are in flight together
+#pragma unroll
+    for (int i0 = 0; i0 < RI; i0 += U) {
+        f4 v0[U], v1[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int row = erg + (i0 + u) * RG;
+            if (i0 + u < RI && row < kGemmBM) {
+                // lanes 8-15 of a 16-lane read group take the other half
+                // first, so the group covers distinct banks
+                const int sw = (ech >> 3) & 1;
+                const float* tq = quarter(row >> 5) + (row & 31) * ES + ech * 8;
+                const f4 p = *reinterpret_cast<const f4*>(tq + 4 * sw);
+                const f4 q = *reinterpret_cast<const f4*>(tq + 4 - 4 * sw);
+                v0[u] = sw ? q : p;
+                v1[u] = sw ? p : q;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int row = erg + (i0 + u) * RG;
+            const int64_t mm = m0 + row;
+            if (!(i0 + u < RI && row < kGemmBM) || mm >= a.M) continue;
+            float v[8] = {v0[u][0], v0[u][1], v0[u][2], v0[u][3], v1[u][0], v1[u][1], v1[u][2], v1[u][3]};
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[e] = v[e] * sc[e] + bi[e];
+            const int64_t o = mm * a.N + en;
+            if (vec) {
+                if constexpr (sizeof(OT) == 2) {
+                    if (a.res) {
+                        const h8 r8 = *reinterpret_cast<const h8*>(static_cast<const f16*>(a.res) + o);
+#pragma unroll
+                        for (int e = 0; e < 8; e++) v[e] += (float)r8[e];
+                    }
+                    h8 o8;
+#pragma unroll
+                    for (int e = 0; e < 8; e++) o8[e] = (f16)v[e];
+                    *reinterpret_cast<h8*>(static_cast<f16*>(a.out) + o) = o8;
+                } else {
+                    if (a.res) {
+                        const f4 r0 = *reinterpret_cast<const f4*>(static_cast<const float*>(a.res) + o);
+                        const f4 r1 = *reinterpret_cast<const f4*>(static_cast<const float*>(a.res) + o + 4);
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            v[e] += r0[e];
+                            v[e + 4] += r1[e];
+                        }
+                    }
+                    *reinterpret_cast<f4*>(static_cast<float*>(a.out) + o) = f4{v[0], v[1], v[2], v[3]};
+                    *reinterpret_cast<f4*>(static_cast<float*>(a.out) + o + 4) = f4{v[4], v[5], v[6], v[7]};
+                }
+            } else {
+                for (int e = 0; e < 8 && en + e < a.N; e++) {
+                    float x = v[e];
+                    if (a.res) x += ld_f(static_cast<const OT*>(a.res) + o + e);
+                    st_f(static_cast<OT*>(a.out) + o + e, x);
+                }
+            }
+        }
+    }
+}
+
+// Tile shapes (layout code -> WN, TJ): 1 = 128 x 192 (4 waves of 64 x 96),
+// 2 = 128 x 256 (8 waves of 64 x 64), 3 = 128 x 128 (4 waves of 64 x 64).
+int gemm3_tile_n(int layout) { return layout == 2 ? 256 : layout == 3 ? 128 : 192; }
+
+template <int WN, int TJ>
+static void gemm3_go(const LinArgs& a, bool f32, hipStream_t s)
+{
+    constexpr int BN = 32 * TJ * WN;
+    const int64_t tiles = ((a.M + kGemmBM - 1) / kGemmBM) * ((a.N + BN - 1) / BN);
+    const dim3 grid((unsigned)tiles);
+    if (f32) hipLaunchKernelGGL((k_gemm3<float, 4, WN, TJ>), grid, dim3(128 * WN), 0, s, a);
+    else hipLaunchKernelGGL((k_gemm3<f16, 4, WN, TJ>), grid, dim3(128 * WN), 0, s, a);
+}
+
+int launch_gemm3(const LinArgs& a, int out, int layout, void* stream)
+{
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const bool f32 = out == VVH_F32;
+    if (layout == 2) gemm3_go<4, 2>(a, f32, s);
+    else if (layout == 3) gemm3_go<2, 2>(a, f32, s);
+    else gemm3_go<2, 3>(a, f32, s);
+    return (int)hipGetLastError();
+}
+
+}  // namespace vvh

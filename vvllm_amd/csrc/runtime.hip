@@ -166,6 +166,27 @@ int gemm_splits(int64_t tiles, int64_t stages)
     return (int)s;
 }
 
+// k_gemm3 tile shape for an unsplit GEMM (0 = use k_gemm2): 128 x 192 when
+// it takes fewer rounds of blocks over the CUs than 128 x 128 by a margin
+// that pays for its longer tiles (a 128 x 192 tile takes 1.33x as long as a
+// 128 x 128 one on MI355X), else 128 x 128.  Split-K problems
+// (few tiles, long K) stay on k_gemm2.  VVH_GEMM3=0 disables k_gemm3,
+// =1/2/3 forces a layout for unsplit problems.
+int gemm3_layout(int64_t M, int64_t N, int splits)
+{
+    static const int forced = [] {
+        const char* e = getenv("VVH_GEMM3");
+        return e ? atoi(e) : -1;
+    }();
+    if (forced == 0 || splits > 1) return 0;
+    if (forced >= 1 && forced <= 3) return forced;
+    const int64_t cus = g_cu_count > 0 ? g_cu_count : 256;
+    const int64_t nbm = (M + kGemmBM - 1) / kGemmBM;
+    const int64_t r128 = (nbm * ((N + 127) / 128) + cus - 1) / cus;
+    const int64_t r192 = (nbm * ((N + 191) / 192) + cus - 1) / cus;
+    return 4 * r192 < 3 * r128 ? 1 : 3;
+}
+
 constexpr std::size_t kAlign = 256;
 inline std::size_t align_up(std::size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -331,6 +352,11 @@ int run_call(const LinArgs& base, int kernel, int act, int outd, void* stream)
             if (a.K % kGemmBK == 0) {
                 const int64_t stages = a.K / kGemmBK;
                 int s = gemm_splits(nb, stages);
+                const int g3 = gemm3_layout(a.M, a.N, s);
+                if (g3 > 0) {
+                    e = launch_gemm3(a, outd, g3, stream);
+                    break;
+                }
                 if (s > 1) {
                     const int64_t kst = (stages + s - 1) / s;
                     s = (int)((stages + kst - 1) / kst);  // no empty split
