@@ -311,8 +311,9 @@ def main():
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--workload", choices=("decode", "prefill"), default="decode",
-                    help="decode: configs[1] (the headline line); prefill: configs[3] gate/up GEMM only")
+    ap.add_argument("--workload", choices=("decode", "prefill", "vendor-gemm"), default="decode",
+                    help="decode: configs[1] (the headline line); prefill: configs[3] gate/up GEMM only; "
+                         "vendor-gemm: the int8 GEMM beside the vendor fp16 GEMM on the prefill shapes")
     ap.add_argument("--prefill-m", type=int, default=512)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -320,10 +321,15 @@ def main():
               "(multi-GPU sharding is design-only). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
+    if args.workload == "vendor-gemm":
+        import torch  # torch's own HIP runtime must start before this library's (else it sees no GPU)
+        torch.cuda.init()
     name = capi.init(0)
     ev = HipEvents()
     if args.workload == "prefill":
         return prefill_main(args, ev, name)
+    if args.workload == "vendor-gemm":
+        return vendor_gemm_main(args, ev)
     h, kv, inter, L = QWEN05["hidden"], QWEN05["kv"], QWEN05["inter"], QWEN05["layers"]
     projs = layer_projs(h, kv, inter)
     tmp_w = capi.DevBuf(max(inter * h, 151936 * 896, 8960 * 1536) * 4)
@@ -387,6 +393,12 @@ def main():
     print(json.dumps(result), flush=True)
 
 
+def kernel_name(M, N, K, outd=F16):
+    """Kernel family of an fp16 linear_q8 call, with the GEMM variant spelled out."""
+    k = capi.kernel_choice(M, N, K, F16, outd)
+    return capi.gemm_variant(M, N, K) if k == "gemm" else k
+
+
 def prefill_main(args, ev, name):
     """configs[3] gate/up GEMM alone (M = --prefill-m, N = 4864, K = 896, fp16
     in and out): one JSON line in TFLOP/s against the fp16 MFMA peak.  Two
@@ -402,9 +414,7 @@ def prefill_main(args, ev, name):
         reps[i % 2][1].run()
     ms = timed(ev, lambda i: reps[i % 2][1].run(), args.steps)
     tf = reps[0][1].flops / (ms * 1e-3) / 1e12
-    kern = capi.kernel_choice(M, N, K, F16, F16)
-    if kern == "gemm" and K % 64 == 0:
-        kern = "k_gemm2<f16>"
+    kern = kernel_name(M, N, K)
     print(f"[bench] {name}: prefill gate/up M={M} {ms * 1e3:.2f} us, {tf:.0f} TFLOP/s ({kern})",
           file=sys.stderr, flush=True)
     print(json.dumps({
@@ -418,6 +428,54 @@ def prefill_main(args, ev, name):
         "roofline": {"bound": "mfma", "kernel": kern, "achieved": round(tf, 2), "peak": MFMA_F16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None},
         "cpu_baseline": None}), flush=True)
+
+
+VENDOR_SHAPES = [("gate_up", 128, 4864, 896), ("gate_up", 512, 4864, 896), ("gate_up", 2048, 4864, 896),
+                 ("down", 512, 896, 4864), ("down", 2048, 896, 4864), ("gate_up_1.5b", 256, 8960, 1536)]
+
+
+def vendor_gemm_main(args, ev):
+    """Calibration: for each prefill shape, this library's int8 GEMM
+    (linear_q8, fp16 activations and output) and the vendor fp16 GEMM
+    (torch.matmul on fp16 weights, hipBLASLt) on the same M, N, K, one after
+    the other.  The vendor GEMM streams 2 bytes per weight and converts
+    nothing; it is the library speed of the same problem on this GPU.  The
+    kernel durations come from rocprofv3 --kernel-trace run over this
+    workload; the HIP-event times printed here include Python launch gaps
+    for the vendor calls (one torch call per launch)."""
+    import torch
+    out = {}
+    tmp_w = capi.DevBuf(8960 * 1536 * 4)
+    for name, M, N, K in VENDOR_SHAPES:
+        reps = []
+        for r in range(2):
+            ar = Arena(arena_size(Linear.sizes(M, N, K, False)))
+            reps.append((ar, Linear(ar, tmp_w.ptr, M, N, K, False, name.startswith("down"), 900 + r)))
+        for i in range(args.warmup):
+            reps[i % 2][1].run()
+        ms = timed(ev, lambda i: reps[i % 2][1].run(), args.steps)
+        del reps
+        As = [torch.randn(M, K, device="cuda", dtype=torch.float16) for _ in range(2)]
+        Ws = [torch.randn(N, K, device="cuda", dtype=torch.float16) for _ in range(8)]  # 8 x N x K x 2 bytes
+        for i in range(args.warmup):
+            torch.matmul(As[i % 2], Ws[i % 8].t())
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for i in range(args.steps):
+            torch.matmul(As[i % 2], Ws[i % 8].t())
+        b.record()
+        torch.cuda.synchronize()
+        vms = a.elapsed_time(b) / args.steps
+        del As, Ws
+        fl = 2 * M * N * K
+        out[f"{name}_M{M}"] = {"M": M, "N": N, "K": K, "kernel": kernel_name(M, N, K),
+                               "int8_us_events": round(ms * 1e3, 2),
+                               "int8_TFLOPS": round(fl / (ms * 1e-3) / 1e12, 1),
+                               "vendor_fp16_us_events_incl_launch_gaps": round(vms * 1e3, 2)}
+        print(f"[bench] {name} M={M}: int8 {ms * 1e3:.2f} us, vendor fp16 {vms * 1e3:.2f} us (events)",
+              file=sys.stderr, flush=True)
+    print(json.dumps({"workload": "vendor-gemm calibration", "shapes": out}), flush=True)
 
 
 def extras(ev, sets, projs, tmp_w, args):
@@ -520,7 +578,7 @@ def extras(ev, sets, projs, tmp_w, args):
             tf = reps[0][1].flops / (us * 1e-6) / 1e12
             gemm[f"{name}_M{M}"] = {"M": M, "N": N, "K": K, "us": round(us, 2), "TFLOPS": round(tf, 1),
                                     "mfma_frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
-                                    "kernel": capi.kernel_choice(M, N, K, F16, F16)}
+                                    "kernel": kernel_name(M, N, K)}
     out["prefill_gemm"] = gemm
     print(f"[bench] gemm M512 gate_up {gemm['gate_up_M512']['us']} us", file=sys.stderr, flush=True)
 
@@ -538,7 +596,7 @@ def extras(ev, sets, projs, tmp_w, args):
             l = reps[0][1]
             sweep[f"{name}_M{M}"] = {"us": round(us, 2), "GBps": round(l.bytes / (us * 1e-6) / 1e9, 1),
                                      "TFLOPS": round(l.flops / (us * 1e-6) / 1e12, 2),
-                                     "kernel": capi.kernel_choice(M, N, K, F16, F16)}
+                                     "kernel": kernel_name(M, N, K)}
     out["qwen15_sweep"] = sweep
 
     # (6) weight ingestion: host BF16 rows of 4 layers quantized into device mirrors

@@ -90,10 +90,11 @@ SIGNATURES = {
     "vvh_mirror_f32": (c_int, [c_void_p, c_size_t, c_int, POINTER(c_void_p)]),
     "vvh_mirror_release": (c_int, [c_void_p]),
     "vvh_memcpy_d2d_async": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
+    "vvh_gemm_variant": (c_int, [c_size_t, c_size_t, c_size_t, POINTER(c_int), POINTER(c_int)]),
 }
 # entries that return a value rather than a vvh_status
 _NOT_STATUS = {"vvh_status_string", "vvh_last_error", "vvh_version", "vvh_device_cu_count",
-               "vvh_linear_q8_choice"}
+               "vvh_linear_q8_choice", "vvh_gemm_variant"}
 
 
 class VVHError(RuntimeError):
@@ -204,6 +205,17 @@ def set_kernel(kernel: int) -> None:
 
 def kernel_choice(M, N, K, act, outd) -> str:
     return KERNEL_NAMES.get(load().vvh_linear_q8_choice(M, N, K, act, outd), "?")
+
+
+def gemm_variant(M, N, K) -> str:
+    """Name of the GEMM kernel an fp16 call of this shape dispatches to."""
+    tn, sp = c_int(), c_int()
+    v = load().vvh_gemm_variant(M, N, K, ctypes.byref(tn), ctypes.byref(sp))
+    if v == 3:
+        return f"k_gemm3 128x{tn.value}"
+    if v == 2:
+        return f"k_gemm2 split {sp.value}" if sp.value > 1 else "k_gemm2"
+    return "k_gemm" if v == 1 else "?"
 
 
 def sync() -> None:

@@ -1203,6 +1203,32 @@ VVH_API int vvh_linear_q8_choice(size_t M, size_t N, size_t K, int act_dtype, in
     return choose_kernel(M, N, K, act_dtype, K % 16 == 0);
 }
 
+VVH_API int vvh_gemm_variant(size_t M, size_t N, size_t K, int* tile_n, int* splits)
+{
+    if (M == 0 || N == 0) return -fail(VVH_ERR_INVALID_ARG, "empty problem");
+    int tn = kGemmBN, s = 1, v = 1;
+    if (K % kGemmBK == 0) {
+        const int64_t nb = (((int64_t)M + kGemmBM - 1) / kGemmBM) * (((int64_t)N + kGemmBN - 1) / kGemmBN);
+        const int64_t stages = (int64_t)K / kGemmBK;
+        s = gemm_splits(nb, stages);
+        if (s > 1) {  // as the dispatch: no empty split
+            const int64_t kst = (stages + s - 1) / s;
+            s = (int)((stages + kst - 1) / kst);
+        }
+        const int g3 = gemm3_layout((int64_t)M, (int64_t)N, s);
+        if (g3 > 0) {
+            v = 3;
+            tn = gemm3_tile_n(g3);
+            s = 1;
+        } else {
+            v = 2;
+        }
+    }
+    if (tile_n) *tile_n = tn;
+    if (splits) *splits = s;
+    return v;
+}
+
 VVH_API int vvh_set_kernel_override(int kernel)
 {
     if (kernel < K_AUTO || kernel > K_DOT) return fail(VVH_ERR_INVALID_ARG, "bad kernel %d", kernel);
