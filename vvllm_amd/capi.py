@@ -212,7 +212,7 @@ def gemm_variant(M, N, K) -> str:
     tn, sp = c_int(), c_int()
     v = load().vvh_gemm_variant(M, N, K, ctypes.byref(tn), ctypes.byref(sp))
     if v == 3:
-        return f"k_gemm3 128x{tn.value}"
+        return f"k_gemm3 128x{tn.value}" + (f" split {sp.value}" if sp.value > 1 else "")
     if v == 2:
         return f"k_gemm2 split {sp.value}" if sp.value > 1 else "k_gemm2"
     return "k_gemm" if v == 1 else "?"

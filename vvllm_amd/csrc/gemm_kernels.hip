@@ -1,5 +1,5 @@
 // k_gemm3: the prefill / batched int8 linear (fp16 activations, M > 16,
-// K % 64 == 0), one output tile per block, no split-K.
+// K % 64 == 0), one output tile (or one k split of it) per block.
 //
 // out[M, N] = (x[M, K] . codes[N, K]^T) * scale[N] + bias[N] (+ res[M, N]),
 // the Backend::linear_q8 / linear_q8_add contract
@@ -39,6 +39,11 @@
 // scales and biases loaded at kernel start), applies acc * scale + bias
 // (+ residual) in fp32 with one rounding, and stores rows with 16-byte
 // stores, four rows' LDS reads in flight at a time.
+//
+// Split-K (a.nsplit > 1, for few tiles over a long K): blocks enumerate
+// (split, tile), tiles fastest; split ks runs k stages [ks * kstages,
+// (ks + 1) * kstages) and writes its raw fp32 sums to ws[ks][M][N]; the
+// reduction kernel then adds the splits in order and applies the epilogue.
 #include "common.h"
 #include "device.h"
 
@@ -156,9 +161,14 @@ __global__ __launch_bounds__(128 * WN, 1) void k_gemm3(LinArgs a)
 
     const int64_t nbm = (a.M + kGemmBM - 1) / kGemmBM;
     const int64_t nbn = (a.N + BN - 1) / BN;
-    const int64_t tile = xcd_remap(blockIdx.x, nbm * nbn);  // consecutive tiles (same n0) on one XCD
+    const int64_t tiles = nbm * nbn;
+    const bool split = a.nsplit > 1;
+    // consecutive tiles (same n0) on one XCD
+    const int64_t logical = xcd_remap(blockIdx.x, tiles * (split ? a.nsplit : 1));
+    const int64_t ks = logical / tiles, tile = logical - ks * tiles;
     const int64_t m0 = (tile % nbm) * kGemmBM;
     const int64_t n0 = (tile / nbm) * BN;
+    const int64_t kbase = split ? ks * a.kstages : 0;  // first k stage of this block
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -176,7 +186,13 @@ __global__ __launch_bounds__(128 * WN, 1) void k_gemm3(LinArgs a)
     const int ech = tid % CH, erg = tid / CH;
     const int64_t en = n0 + ech * 8;
     float sc[8], bi[8];
-    if (a.N % 8 == 0) {  // 16-byte loads at a clamped (always valid) chunk
+    if (split) {  // raw partial sums: the reduction applies the epilogue
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            sc[e] = 1.0f;
+            bi[e] = 0.0f;
+        }
+    } else if (a.N % 8 == 0) {  // 16-byte loads at a clamped (always valid) chunk
         const int64_t ec = en < a.N ? en : a.N - 8;
         const f4 s0 = *reinterpret_cast<const f4*>(a.scales + ec), s1 = *reinterpret_cast<const f4*>(a.scales + ec + 4);
         f4 b0 = f4{}, b1 = f4{};
@@ -229,7 +245,7 @@ __global__ __launch_bounds__(128 * WN, 1) void k_gemm3(LinArgs a)
         else return st3;
     };
     auto issue = [&](Stage& g, int64_t kt) {
-        gemm3_fill<NW, BN>(g.a, g.b, ra, rb, a_off, b_off, wave, (uint32_t)(kt * kGemmBK));
+        gemm3_fill<NW, BN>(g.a, g.b, ra, rb, a_off, b_off, wave, (uint32_t)((kbase + kt) * kGemmBK));
     };
 
     f16v acc[2][TJ];
@@ -278,7 +294,8 @@ __global__ __launch_bounds__(128 * WN, 1) void k_gemm3(LinArgs a)
         gemm3_convert<TJ>(f0.b[0], fb[0]);
     };
 
-    const int64_t nk = a.K / kGemmBK;
+    const int64_t nk_all = a.K / kGemmBK;
+    const int64_t nk = split ? (nk_all - kbase < a.kstages ? nk_all - kbase : a.kstages) : nk_all;
     if (nk >= D) {
         prologue.template operator()<D>();
         int64_t kt0 = 0;
@@ -346,9 +363,19 @@ __global__ __launch_bounds__(128 * WN, 1) void k_gemm3(LinArgs a)
             const int64_t mm = m0 + row;
             if (!(i0 + u < RI && row < kGemmBM) || mm >= a.M) continue;
             float v[8] = {v0[u][0], v0[u][1], v0[u][2], v0[u][3], v1[u][0], v1[u][1], v1[u][2], v1[u][3]};
+            const int64_t o = mm * a.N + en;
+            if (split) {  // raw partial sums of this split
+                float* wp = a.ws + ks * a.M * a.N + o;
+                if (vec) {
+                    *reinterpret_cast<f4*>(wp) = v0[u];
+                    *reinterpret_cast<f4*>(wp + 4) = v1[u];
+                } else {
+                    for (int e = 0; e < 8 && en + e < a.N; e++) wp[e] = v[e];
+                }
+                continue;
+            }
 #pragma unroll
             for (int e = 0; e < 8; e++) v[e] = v[e] * sc[e] + bi[e];
-            const int64_t o = mm * a.N + en;
             if (vec) {
                 if constexpr (sizeof(OT) == 2) {
                     if (a.res) {
@@ -393,7 +420,7 @@ static void gemm3_go(const LinArgs& a, bool f32, hipStream_t s)
 {
     constexpr int BN = 32 * TJ * WN;
     const int64_t tiles = ((a.M + kGemmBM - 1) / kGemmBM) * ((a.N + BN - 1) / BN);
-    const dim3 grid((unsigned)tiles);
+    const dim3 grid((unsigned)(tiles * (a.nsplit > 1 ? a.nsplit : 1)));
     if (f32) hipLaunchKernelGGL((k_gemm3<float, 4, WN, TJ>), grid, dim3(128 * WN), 0, s, a);
     else hipLaunchKernelGGL((k_gemm3<f16, 4, WN, TJ>), grid, dim3(128 * WN), 0, s, a);
 }

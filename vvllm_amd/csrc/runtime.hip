@@ -145,11 +145,11 @@ int workspace_for(void* stream, std::size_t bytes, float** out)
 
 // Number of k splits for a GEMM of `tiles` 128x128 output tiles and `stages`
 // 64-wide k stages.  A split GEMM pays a second launch and an fp32 partial
-// round trip through memory (measured: ~2.5 us launch floor, ~3 TB/s for the
-// reduction), so it only pays for long reductions over few tiles: split when
-// the tiles would leave three quarters of the CUs idle and K has at least 32
-// stages, into at most one block per CU and at least 4 stages per split
-// (Qwen2.5-0.5B down projection at M=512: 37 us -> 23 us).
+// round trip through memory, so it only pays for long reductions over few
+// tiles: split when the tiles would leave half of the CUs idle and K has at
+// least 32 stages, into at most one block per CU and at least 4 stages per
+// split (Qwen2.5-0.5B down projection: M=512 37 -> 22 us, 9 splits; M=2048
+// 2 splits).
 // VVH_GEMM_SPLIT=0 disables splitting, =s forces s.
 int gemm_splits(int64_t tiles, int64_t stages)
 {
@@ -160,26 +160,27 @@ int gemm_splits(int64_t tiles, int64_t stages)
     const int64_t cus = g_cu_count > 0 ? g_cu_count : 256;
     int64_t s;
     if (forced >= 0) s = forced;
-    else if (tiles * 4 > cus || stages < 32) s = 1;
+    else if (tiles * 2 > cus || stages < 32) s = 1;
     else s = std::min<int64_t>(cus / tiles, stages / 4);
     s = std::max<int64_t>(1, std::min<int64_t>(s, stages));
     return (int)s;
 }
 
-// k_gemm3 tile shape for an unsplit GEMM (0 = use k_gemm2): 128 x 192 when
-// it takes fewer rounds of blocks over the CUs than 128 x 128 by a margin
-// that pays for its longer tiles (a 128 x 192 tile takes 1.33x as long as a
-// 128 x 128 one on MI355X), else 128 x 128.  Split-K problems
-// (few tiles, long K) stay on k_gemm2.  VVH_GEMM3=0 disables k_gemm3,
-// =1/2/3 forces a layout for unsplit problems.
+// k_gemm3 tile shape (0 = use k_gemm2): split-K problems (few tiles, long
+// K) take 128 x 128; unsplit ones 128 x 192 when it takes fewer rounds of
+// blocks over the CUs than 128 x 128 by a margin that pays for its longer
+// tiles (a 128 x 192 tile takes 1.33x as long as a 128 x 128 one on
+// MI355X), else 128 x 128.  VVH_GEMM3=0 falls back to k_gemm2, =1/2/3
+// forces a layout.
 int gemm3_layout(int64_t M, int64_t N, int splits)
 {
     static const int forced = [] {
         const char* e = getenv("VVH_GEMM3");
         return e ? atoi(e) : -1;
     }();
-    if (forced == 0 || splits > 1) return 0;
+    if (forced == 0) return 0;
     if (forced >= 1 && forced <= 3) return forced;
+    if (splits > 1) return 3;
     const int64_t cus = g_cu_count > 0 ? g_cu_count : 256;
     const int64_t nbm = (M + kGemmBM - 1) / kGemmBM;
     const int64_t r128 = (nbm * ((N + 127) / 128) + cus - 1) / cus;
@@ -352,11 +353,6 @@ int run_call(const LinArgs& base, int kernel, int act, int outd, void* stream)
             if (a.K % kGemmBK == 0) {
                 const int64_t stages = a.K / kGemmBK;
                 int s = gemm_splits(nb, stages);
-                const int g3 = gemm3_layout(a.M, a.N, s);
-                if (g3 > 0) {
-                    e = launch_gemm3(a, outd, g3, stream);
-                    break;
-                }
                 if (s > 1) {
                     const int64_t kst = (stages + s - 1) / s;
                     s = (int)((stages + kst - 1) / kst);  // no empty split
@@ -369,6 +365,12 @@ int run_call(const LinArgs& base, int kernel, int act, int outd, void* stream)
                         a.nsplit = s;
                         a.kstages = (int32_t)kst;
                     }
+                }
+                const int g3 = gemm3_layout(a.M, a.N, a.nsplit);
+                if (g3 > 0) {
+                    e = launch_gemm3(a, outd, g3, stream);
+                    if (e == 0 && a.nsplit > 1) e = launch_splitk_reduce(a, outd, stream);
+                    break;
                 }
             }
             e = launch_gemm(a, outd, stream);
@@ -1219,7 +1221,6 @@ VVH_API int vvh_gemm_variant(size_t M, size_t N, size_t K, int* tile_n, int* spl
         if (g3 > 0) {
             v = 3;
             tn = gemm3_tile_n(g3);
-            s = 1;
         } else {
             v = 2;
         }
