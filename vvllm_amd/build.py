@@ -4,6 +4,9 @@
 * ``lib/libvvllm_backend_hip.so``  -- BackendHIP, C++20 host code (g++) over the C ABI
 * ``tests/cpp/bin/test_pool``      -- CPU test of the caching allocator logic
 * ``tests/cpp/bin/test_backend_hip`` -- GPU test of BackendHIP
+* ``tests/cpp/bin/test_forward_hip`` -- GPU test: whole forward passes through
+  Backend/KVCache, checked against the CPU oracle (oracle/oracle.c, linked
+  into the test binary only)
 
 Everything is built in-tree so the artefacts travel with the source tree.
 Run ``python -m vvllm_amd.build`` or call :func:`build_all`.
@@ -85,6 +88,19 @@ def build_test_backend() -> str:
     return out
 
 
+def build_test_forward() -> str:
+    os.makedirs(TEST_BIN, exist_ok=True)
+    out = os.path.join(TEST_BIN, "test_forward_hip")
+    obj = os.path.join(TEST_BIN, "oracle.o")
+    # the oracle with the reference's CPU flags (-mavx2 -mfma, oracle/Makefile)
+    _run(["gcc", "-std=gnu11", "-O2", "-DNDEBUG", "-mavx2", "-mfma", "-c",
+          os.path.join(ROOT, "oracle", "oracle.c")], obj)
+    _run([CXX, "-std=c++20", "-O2", "-Wall", "-I" + INCLUDE, "-I" + HOST, "-I" + os.path.join(ROOT, "oracle"),
+          os.path.join(ROOT, "tests", "cpp", "test_forward_hip.cc"), obj, "-L" + LIB,
+          "-lvvllm_backend_hip", "-lvvllm_hip", "-lm", "-Wl,-rpath,$ORIGIN/../../../vvllm_amd/lib"], out)
+    return out
+
+
 def build_all(verbose: bool = True) -> None:
     with ThreadPoolExecutor(max_workers=2) as ex:
         f_hip = ex.submit(build_hip_lib)
@@ -92,6 +108,7 @@ def build_all(verbose: bool = True) -> None:
         f_hip.result()
         build_backend_lib()
         build_test_backend()
+        build_test_forward()
         f_pool.result()
     if verbose:
         print(f"built {HIP_LIB}, {BACKEND_LIB}, tests in {TEST_BIN}")
