@@ -5,8 +5,8 @@
 // :407-425 (LinearQ8WithBias), run on the MI355X backend in fp32 and in fp16
 // mode.  The others cover what the model relies on and the reference never
 // tests: linear_q8_add with out == residual (include/vvllm/model/
-// transformer.h:165-166), M > 1, and the weight mirror refreshing after
-// forget_weight.
+// transformer.h:165-166), M > 1, the weight mirror refreshing after
+// forget_weight, and mirrors released with their backend.
 #include <cmath>
 #include <cstdio>
 #include <algorithm>
@@ -170,6 +170,28 @@ void mirror_refresh()
     EXPECT_NEAR(out.download()[0], 128.0, 0.0, "mirror after forget_weight");
 }
 
+// Mirrors belong to the backend that made them (BackendCUDA frees its weight
+// caches in its destructor, backend_cuda.cc:28-35): host buffers rewritten in
+// place after their backend is gone are uploaded again by the next backend.
+void mirror_per_backend()
+{
+    const std::size_t N = 16, K = 64;
+    std::vector<int8_t> q(N * K, 1);
+    std::vector<float> scales(N, 1.0f), norm_w(K, 1.0f);
+    std::vector<float> x(K, 1.0f);
+    for (int round = 1; round <= 2; round++) {
+        BackendHIP backend(false);
+        Act in(false, K), out(false, N), normed(false, K);
+        in.upload(x);
+        backend.linear_q8(out.f(), in.f(), q.data(), scales.data(), nullptr, 1, N, K);
+        EXPECT_NEAR(out.download()[0], 64.0 * round, 0.0, "int8 mirror of this backend");
+        backend.rms_norm(normed.f(), in.f(), norm_w.data(), K, 1e-6f);
+        EXPECT_NEAR(normed.download()[0], 1.0 * round, 1e-5, "norm weight mirror of this backend");
+        std::fill(q.begin(), q.end(), (int8_t)2);  // same addresses, new contents
+        std::fill(norm_w.begin(), norm_w.end(), 2.0f);
+    }
+}
+
 // BF16 rows ingested straight into the mirror, then used through linear_q8
 // with the rows' address as the weight (what Qwen2Model would pass).
 // Row 0 = [1, -1, 0.5, 0, ...]: scale 1/127, codes 127, -127, 64 (63.5 ties
@@ -323,6 +345,8 @@ int main()
     }
     std::printf("[case] mirror refresh\n"); std::fflush(stdout);
     mirror_refresh();
+    std::printf("[case] mirror per backend\n"); std::fflush(stdout);
+    mirror_per_backend();
     std::printf("[case] ingest bf16\n"); std::fflush(stdout);
     ingest_bf16();
     for (bool fp16 : {false, true}) {

@@ -38,7 +38,12 @@
 // in stage buffer q); each thread then owns one 8-wide column chunk (its 8
 // scales and biases loaded at kernel start), applies acc * scale + bias
 // (+ residual) in fp32 with one rounding, and stores rows with 16-byte
-// stores, four rows' LDS reads in flight at a time.
+// stores.  A tile wholly inside the problem (no split, N % 8 == 0) takes a
+// branch-free path: its residual rows are loaded before the accumulators go
+// to LDS, eight rows' LDS reads are in flight together and row addresses
+// advance by a fixed stride (measured: 1.44 -> 0.72 us for the reads and
+// stores of a 128 x 128 tile).  Edge tiles take the general path, four
+// rows' LDS reads in flight at a time.
 //
 // Split-K (a.nsplit > 1, for few tiles over a long K): blocks enumerate
 // (split, tile), tiles fastest; split ks runs k stages [ks * kstages,
@@ -325,6 +330,23 @@ __global__ __launch_bounds__(128 * WN, 1) void k_gemm3(LinArgs a)
     auto quarter = [&](int q) -> float* {
         return reinterpret_cast<float*>(q == 0 ? &st0 : q == 1 ? &st1 : q == 2 ? &st2 : &st3);
     };
+    constexpr int RI = (kGemmBM + RG - 1) / RG;  // rows per thread
+    // Interior tiles (every row and column inside the problem, whole 8-wide
+    // chunks, no split) take a branch-free path; its residual rows are
+    // loaded here, so their latency overlaps the accumulator transpose.
+    const bool interior = !split && m0 + kGemmBM <= a.M && n0 + BN <= a.N && a.N % 8 == 0;
+    const bool own = erg < RG;
+    constexpr int RW = sizeof(OT) / 2;  // 16-byte chunks per 8 outputs
+    u4 rr[RI][RW];
+    const int64_t o_first = (m0 + erg) * a.N + en, o_step = RG * a.N;
+    if (interior && own && a.res) {
+        const OT* rp = static_cast<const OT*>(a.res) + o_first;
+#pragma unroll
+        for (int i = 0; i < RI; i++)
+            if (i + 1 < RI || erg + i * RG < kGemmBM)
+#pragma unroll
+                for (int c = 0; c < RW; c++) rr[i][c] = reinterpret_cast<const u4*>(rp + i * o_step)[c];
+    }
 #pragma unroll
     for (int ti = 0; ti < 2; ti++) {
         float* q = quarter((row0 >> 5) + ti) + fl * ES + col0 + 4 * fh;
@@ -336,10 +358,62 @@ __global__ __launch_bounds__(128 * WN, 1) void k_gemm3(LinArgs a)
                     f4{acc[ti][tj][4 * g], acc[ti][tj][4 * g + 1], acc[ti][tj][4 * g + 2], acc[ti][tj][4 * g + 3]};
     }
     lds_barrier();
-    if (erg >= RG || en >= a.N) return;
+    if (!own) return;
+    // lanes 8-15 of a 16-lane read group take the other half of their chunk
+    // first, so the group covers distinct banks
+    const int sw = (ech >> 3) & 1;
+    if (interior) {
+        constexpr int UB = 8;  // rows whose LDS reads are in flight together
+#pragma unroll
+        for (int i0 = 0; i0 < RI; i0 += UB) {
+            f4 p[UB], q[UB];
+#pragma unroll
+            for (int u = 0; u < UB; u++) {
+                const int i = i0 + u, row = erg + i * RG;
+                if (i < RI && (i + 1 < RI || row < kGemmBM)) {
+                    const float* tq = quarter(row >> 5) + (row & 31) * ES + ech * 8;
+                    p[u] = *reinterpret_cast<const f4*>(tq + 4 * sw);
+                    q[u] = *reinterpret_cast<const f4*>(tq + 4 - 4 * sw);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < UB; u++) {
+                const int i = i0 + u, row = erg + i * RG;
+                if (!(i < RI && (i + 1 < RI || row < kGemmBM))) continue;
+                const f4 lo = sw ? q[u] : p[u], hi = sw ? p[u] : q[u];
+                float v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+#pragma unroll
+                for (int e = 0; e < 8; e++) v[e] = v[e] * sc[e] + bi[e];
+                OT* op = static_cast<OT*>(a.out) + o_first + i * o_step;
+                if constexpr (sizeof(OT) == 2) {
+                    if (a.res) {
+                        const h8 r8 = __builtin_bit_cast(h8, rr[i][0]);
+#pragma unroll
+                        for (int e = 0; e < 8; e++) v[e] += (float)r8[e];
+                    }
+                    h8 o8;
+#pragma unroll
+                    for (int e = 0; e < 8; e++) o8[e] = (f16)v[e];
+                    *reinterpret_cast<h8*>(op) = o8;
+                } else {
+                    if (a.res) {
+                        const f4 r0 = __builtin_bit_cast(f4, rr[i][0]), r1 = __builtin_bit_cast(f4, rr[i][1]);
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            v[e] += r0[e];
+                            v[e + 4] += r1[e];
+                        }
+                    }
+                    *reinterpret_cast<f4*>(op) = f4{v[0], v[1], v[2], v[3]};
+                    *reinterpret_cast<f4*>(op + 4) = f4{v[4], v[5], v[6], v[7]};
+                }
+            }
+        }
+        return;
+    }
+    if (en >= a.N) return;
     const bool vec = (a.N % 8) == 0 && en + 8 <= a.N;
-    constexpr int RI = (kGemmBM + RG - 1) / RG;  // rows per thread
-    constexpr int U = 4;                         // rows whose LDS reads are in flight together
+    constexpr int U = 4;  // rows whose LDS reads are in flight together
 #pragma unroll
     for (int i0 = 0; i0 < RI; i0 += U) {
         f4 v0[U], v1[U];
@@ -347,9 +421,6 @@ __global__ __launch_bounds__(128 * WN, 1) void k_gemm3(LinArgs a)
         for (int u = 0; u < U; u++) {
             const int row = erg + (i0 + u) * RG;
             if (i0 + u < RI && row < kGemmBM) {
-                // lanes 8-15 of a 16-lane read group take the other half
-                // first, so the group covers distinct banks
-                const int sw = (ech >> 3) & 1;
                 const float* tq = quarter(row >> 5) + (row & 31) * ES + ech * 8;
                 const f4 p = *reinterpret_cast<const f4*>(tq + 4 * sw);
                 const f4 q = *reinterpret_cast<const f4*>(tq + 4 - 4 * sw);

@@ -32,7 +32,13 @@ BackendHIP::BackendHIP(bool fp16, int device) : fp16_(fp16)
     name_ = name;
 }
 
-BackendHIP::~BackendHIP() = default;
+BackendHIP::~BackendHIP()
+{
+    // a mirror may already be gone (forget_weight, or another backend that
+    // shared it): those calls fail harmlessly
+    for (const std::uint64_t h : weights_) (void)vvh_weight_release(h);
+    for (const float* p : arrays_) (void)vvh_mirror_release(p);
+}
 
 void* BackendHIP::allocate(std::size_t bytes)
 {
@@ -50,6 +56,7 @@ std::uint64_t BackendHIP::mirror(const int8_t* weight, const float* scales, cons
 {
     vvh_weight h = 0;
     check(vvh_weight_register(weight, scales, bias, N, K, &h), "weight mirror");
+    weights_.insert(h);
     return h;
 }
 
@@ -92,6 +99,7 @@ const int8_t* BackendHIP::ingest_weight(const void* host_rows, bool bf16, const 
 {
     vvh_weight h = 0;
     check(vvh_weight_ingest(host_rows, bf16 ? VVH_BF16 : VVH_F32, bias, N, K, scales, &h), "ingest_weight");
+    weights_.insert(h);
     return static_cast<const int8_t*>(host_rows);
 }
 
@@ -109,6 +117,7 @@ const void* BackendHIP::host_mirror(const float* host, std::size_t n, int as_dty
 {
     const void* dev = nullptr;
     check(vvh_mirror_f32(host, n, as_dtype, &dev), "mirror");
+    arrays_.insert(host);
     return dev;
 }
 

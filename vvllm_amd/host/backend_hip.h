@@ -17,7 +17,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <string>
-
+#include <unordered_set>
 #include <vector>
 
 #include "vvllm/backend/backend.h"
@@ -95,6 +95,12 @@ private:
 
     bool fp16_;
     std::string name_;
+    // Mirrors this backend created or used, released by the destructor, as
+    // BackendCUDA frees its per-instance weight caches (backend_cuda.cc:28-35):
+    // a later backend never sees device copies keyed by host addresses that
+    // may since have been freed and reused.
+    std::unordered_set<std::uint64_t> weights_;
+    std::unordered_set<const float*> arrays_;
 };
 
 // Key/value cache in HBM (KVCacheCUDA, src/kv_cache/kv_cache_cuda.cc:22-95):
