@@ -115,7 +115,7 @@ def test_gemm_variant_choice():
     assert capi.gemm_variant(512, 4864, 896) == "k_gemm3 128x128"     # 152 tiles, one round
     assert capi.gemm_variant(128, 4864, 896) == "k_gemm3 128x128"
     assert capi.gemm_variant(2048, 4864, 896) == "k_gemm3 128x192"    # 3 rounds -> 2
-    assert capi.gemm_variant(512, 896, 4864) == "k_gemm3 128x128 split 9"   # 28 tiles, 76 k stages
+    assert capi.gemm_variant(512, 896, 4864) == "k_gemm3 128x128 split 6"   # 28 tiles, 76 k stages
     assert capi.gemm_variant(2048, 896, 4864) == "k_gemm3 128x128 split 2"  # 112 tiles: half the CUs
     assert capi.gemm_variant(300, 1000, 80) == "k_gemm"               # K % 64 != 0
     assert capi.load().vvh_gemm_variant(0, 16, 64, None, None) == -1  # -VVH_ERR_INVALID_ARG

@@ -143,25 +143,40 @@ int workspace_for(void* stream, std::size_t bytes, float** out)
     return VVH_OK;
 }
 
-// Number of k splits for a GEMM of `tiles` 128x128 output tiles and `stages`
-// 64-wide k stages.  A split GEMM pays a second launch and an fp32 partial
-// round trip through memory, so it only pays for long reductions over few
-// tiles: split when the tiles would leave half of the CUs idle and K has at
-// least 32 stages, into at most one block per CU and at least 4 stages per
-// split (Qwen2.5-0.5B down projection: M=512 37 -> 22 us, 9 splits; M=2048
-// 2 splits).
+// Number of k splits for a GEMM of `tiles` 128x128 output tiles, `stages`
+// 64-wide k stages and an M x N fp32 partial plane of `plane_bytes`.  A split
+// GEMM pays a second launch and, per split, one partial plane written by the
+// GEMM and read back by the reduction, so it only pays for long reductions
+// over few tiles: split when the tiles would leave half of the CUs idle and K
+// has at least 32 stages.  The count minimises a cost model fitted to a sweep
+// of forced counts on the Qwen2.5-0.5B down projection (M=512: 33.1, 23.9,
+// 20.6, 19.9, 19.8, 19.9, 21.8, 21.5 us for 1..7 and 9 splits; M=2048: 36.4,
+// 33.7, 42.4 us for 1..3): 0.4 us per k stage and round of blocks over the
+// CUs, 2.5 us for the reduction's launch, and each plane at 1.6 TB/s.
 // VVH_GEMM_SPLIT=0 disables splitting, =s forces s.
-int gemm_splits(int64_t tiles, int64_t stages)
+int gemm_splits(int64_t tiles, int64_t stages, uint64_t plane_bytes)
 {
     static const int forced = [] {
         const char* e = getenv("VVH_GEMM_SPLIT");
         return e ? atoi(e) : -1;
     }();
     const int64_t cus = g_cu_count > 0 ? g_cu_count : 256;
-    int64_t s;
-    if (forced >= 0) s = forced;
-    else if (tiles * 2 > cus || stages < 32) s = 1;
-    else s = std::min<int64_t>(cus / tiles, stages / 4);
+    int64_t s = 1;
+    if (forced >= 0) {
+        s = forced;
+    } else if (tiles * 2 <= cus && stages >= 32) {
+        const int64_t smax = std::min<int64_t>(cus / tiles, stages / 4);
+        double best = 0;
+        for (int64_t c = 1; c <= smax; c++) {
+            const int64_t kst = (stages + c - 1) / c, ce = (stages + kst - 1) / kst;  // no empty split
+            const int64_t rounds = (tiles * ce + cus - 1) / cus;
+            const double t = 0.4 * (double)(rounds * kst) + (ce > 1 ? 2.5 + (double)ce * (double)plane_bytes / 1.6e6 : 0.0);
+            if (c == 1 || t < best) {
+                best = t;
+                s = c;
+            }
+        }
+    }
     s = std::max<int64_t>(1, std::min<int64_t>(s, stages));
     return (int)s;
 }
@@ -352,7 +367,7 @@ int run_call(const LinArgs& base, int kernel, int act, int outd, void* stream)
             a.ws = nullptr;
             if (a.K % kGemmBK == 0) {
                 const int64_t stages = a.K / kGemmBK;
-                int s = gemm_splits(nb, stages);
+                int s = gemm_splits(nb, stages, (uint64_t)a.M * (uint64_t)a.N * 4);
                 if (s > 1) {
                     const int64_t kst = (stages + s - 1) / s;
                     s = (int)((stages + kst - 1) / kst);  // no empty split
@@ -1212,7 +1227,7 @@ VVH_API int vvh_gemm_variant(size_t M, size_t N, size_t K, int* tile_n, int* spl
     if (K % kGemmBK == 0) {
         const int64_t nb = (((int64_t)M + kGemmBM - 1) / kGemmBM) * (((int64_t)N + kGemmBN - 1) / kGemmBN);
         const int64_t stages = (int64_t)K / kGemmBK;
-        s = gemm_splits(nb, stages);
+        s = gemm_splits(nb, stages, (uint64_t)M * (uint64_t)N * 4);
         if (s > 1) {  // as the dispatch: no empty split
             const int64_t kst = (stages + s - 1) / s;
             s = (int)((stages + kst - 1) / kst);
