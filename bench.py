@@ -298,7 +298,8 @@ def cpu_baseline(lins, budget_s):
                 ms_per_step=round(el / passes * 1e3, 3), ingest_host_path=cpu_ingest(layer_projs(896, 128, 4864)),
                 sample=(f"{passes} full passes of the 24-layer decode projection set (168 linear_q8 calls, "
                         f"same int8 weights as the GPU run, fp32 activations) in {el:.1f} s, one thread; "
-                        f"{'reference BackendCPU::linear_q8 compiled from its sources -O2 -mavx2 -mfma' if kind == 'reference' else 'oracle restatement of BackendCPU::linear_q8'}"))
+                        + ("reference BackendCPU::linear_q8 compiled from its sources -O2 -mavx2 -mfma"
+                           if kind == "reference" else "oracle restatement of BackendCPU::linear_q8")))
 
 
 # ---------------------------------------------------------------------------
@@ -621,11 +622,14 @@ def extras(ev, sets, projs, tmp_w, args):
 
     # (7) a whole decode step at Qwen2.5-0.5B shapes: every operator of
     # transformer_forward on the device (vvllm_amd.qwen2_decode), at position
-    # 511 of a filled KV cache, launched from Python and replayed from a graph
+    # 511 of a filled KV cache, launched from Python and replayed from a graph;
+    # "fused": the same arithmetic with the norms and SiLU-mul in the input
+    # stage of the following linear and RoPE writing the KV cache (identical
+    # logits, fewer launches)
     from vvllm_amd import qwen2_decode as qd
     e2e = {}
-    for head in ("dense", "int8"):
-        m = qd.Model(qd.QWEN25_05B, act=F16, lm_head=head, max_ctx=1024, seed=3)
+    for head, fused in (("dense", False), ("int8", False), ("dense", True), ("int8", True)):
+        m = qd.Model(qd.QWEN25_05B, act=F16, lm_head=head, max_ctx=1024, seed=3, fused=fused)
         m.fill_kv(5)
         P = 511
         for i in range(3):
@@ -637,14 +641,14 @@ def extras(ev, sets, projs, tmp_w, args):
         for i in range(3):
             ev.launch(g, stream)
         ms_graph = timed(ev, lambda i: ev.launch(g, stream), 50, stream)
-        e2e[f"{head}_lm_head"] = {"calls_per_step": m.calls_per_step(), "position": P,
+        e2e[f"{head}_lm_head" + ("_fused" if fused else "")] = {"calls_per_step": m.calls_per_step(), "position": P,
                                   "us_per_token_graph": round(ms_graph * 1e3, 1),
                                   "tok_per_s_graph": round(1e3 / ms_graph, 1),
                                   "us_per_token_python_launches": round(ms_eager * 1e3, 1)}
         m.close()
         del m
-        print(f"[bench] decode step ({head} LM head) {ms_graph * 1e3:.0f} us graph, {ms_eager * 1e3:.0f} us eager",
-              file=sys.stderr, flush=True)
+        print(f"[bench] decode step ({head} LM head{', fused' if fused else ''}) {ms_graph * 1e3:.0f} us graph, "
+              f"{ms_eager * 1e3:.0f} us eager", file=sys.stderr, flush=True)
     e2e["note"] = ("synthetic Qwen2.5-0.5B-shaped model (seeded weights), fp16 activations, int8 linears, greedy "
                    "argmax on the device; GPU time per token, no host sampling or tokenizer")
     out["decode_step"] = e2e

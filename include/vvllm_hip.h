@@ -212,6 +212,27 @@ VVH_API int vvh_linear_q8_dev(void* out, const void* inp, const int8_t* dev_weig
                               const void* residual, size_t M, size_t N, size_t K,
                               int act_dtype, int out_dtype, void* stream);
 
+/* Input stages of a decode linear (no counterpart in the reference, whose
+ * transformer_forward runs the operator before the linear as its own call,
+ * transformer.h:133-139, 176-185).  The linear reads its activation rows
+ * through the stage, with the same arithmetic and fp16 rounding as the
+ * standalone operator, so the result equals operator-then-linear exactly. */
+enum {
+    VVH_IN_NONE = 0,
+    VVH_IN_RMS_NORM = 1,  /* rows of inp -> vvh_rms_norm(in_w, in_eps) (:68-76) */
+    VVH_IN_SILU_MUL = 2,  /* rows of inp are [gate | up] of 2K values -> silu(gate) * up (:293-300) */
+};
+/* vvh_linear_q8_dev of the staged input.  Stages other than VVH_IN_NONE need
+ * fp16 activations, M <= 4, K % 16 == 0, 16-byte aligned inp, weights and
+ * in_w (fp32 [K], RMSNorm only), and M rows of K + 8 halves within the
+ * decode kernel's 80 KB of LDS; otherwise VVH_ERR_UNSUPPORTED.  For
+ * VVH_IN_SILU_MUL, inp holds M rows of 2K values (gate, then up). */
+VVH_API int vvh_linear_q8_dev_in(void* out, const void* inp, const int8_t* dev_weight,
+                                 const float* dev_scales, const float* dev_bias,
+                                 const void* residual, size_t M, size_t N, size_t K,
+                                 int act_dtype, int out_dtype, int in_op, const float* in_w,
+                                 float in_eps, void* stream);
+
 /* ---- grouped launch ------------------------------------------------------ */
 /* A plan is a fixed list of independent linear_q8 problems of one
  * (act_dtype, out_dtype) pair, resolved once (kernel choice, tile
@@ -238,6 +259,13 @@ VVH_API int vvh_plan_run(vvh_plan plan, void* stream);
 VVH_API int vvh_plan_destroy(vvh_plan plan);
 /* Number of kernel launches one vvh_plan_run makes. */
 VVH_API int vvh_plan_launches(vvh_plan plan, int* launches);
+/* Gives every problem of a plan the input stage in_op (VVH_IN_*, with
+ * in_w / in_eps as for vvh_linear_q8_dev_in): e.g. q/k/v reading the
+ * residual stream through the layer's input RMSNorm.  The plan must run as
+ * one k_dot_grouped launch with its activations in LDS (vvh_plan_kernel
+ * gives VVH_KERNEL_DOT), else VVH_ERR_UNSUPPORTED.  Waits for the device
+ * (queued runs of the plan read its table); not for use under capture. */
+VVH_API int vvh_plan_set_input_op(vvh_plan plan, int in_op, const float* in_w, float in_eps);
 /* Kernel family of a single-launch plan (VVH_KERNEL_DOT, VVH_KERNEL_STREAM
  * or VVH_KERNEL_SKINNY), or VVH_KERNEL_AUTO for a plan run as one launch per
  * problem. */
@@ -290,6 +318,16 @@ VVH_API int vvh_softmax(void* out, const void* x, size_t rows, size_t n, int dty
  * k [seq_len, num_kv_heads, head_dim], positions pos.. (:93-137). */
 VVH_API int vvh_rope(void* q, void* k, size_t seq_len, size_t num_heads, size_t num_kv_heads, size_t head_dim,
                      size_t pos, float theta, int dtype, void* stream);
+/* vvh_rope, then the KV-cache append that follows it (transformer.h:145-160,
+ * KVCache::append) in the same kernel: the rotated rows of k and the rows of
+ * v [seq_len, num_kv_heads, head_dim] are also written to rows
+ * pos .. pos + seq_len - 1 of k_cache and v_cache ([*, num_kv_heads,
+ * head_dim], the caller's capacity).  No counterpart in the reference, which
+ * copies the rows in separate calls; this saves the two copies per layer of
+ * a decode step. */
+VVH_API int vvh_rope_append(void* q, void* k, const void* v, void* k_cache, void* v_cache, size_t seq_len,
+                            size_t num_heads, size_t num_kv_heads, size_t head_dim, size_t pos, float theta, int dtype,
+                            void* stream);
 /* out[0..hidden) = table[token_id] (fp32 table [vocab, hidden]) (:338-342). */
 VVH_API int vvh_embedding(void* out, const float* dev_table, size_t token_id, size_t hidden, size_t vocab, int dtype,
                           void* stream);

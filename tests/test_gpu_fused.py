@@ -1,0 +1,176 @@
+"""The fused decode operators against the unfused sequences they replace.
+
+vvh_linear_q8_dev_in (RMSNorm or SiLU-mul as the input stage of a decode
+linear), vvh_plan_set_input_op (the same for a grouped q/k/v plan) and
+vvh_rope_append (RoPE writing the KV-cache rows) compute exactly what the
+reference's separate calls compute (transformer.h:133-160, 176-185): rms_norm
+then linear, silu_mul then linear, rope then KVCache::append.  Each stage
+rounds as the standalone kernel, so every comparison here is bit-exact; the
+standalone kernels themselves are checked against the oracle in
+test_gpu_ops.py and test_gpu_parity.py.  Whole decode steps of the fused
+harness must reproduce the unfused step's logits exactly.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from vvllm_amd import capi
+from vvllm_amd import qwen2_decode as qd
+
+pytestmark = pytest.mark.gpu
+F16, F32 = capi.F16, capi.F32
+
+
+def q8_weight(rng, N, K):
+    q = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    s = (rng.random(N, dtype=np.float32) * 0.02 + 0.001).astype(np.float32)
+    return capi.DevBuf.from_array(q), capi.DevBuf.from_array(s)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 896, 896), (2, 130, 896), (4, 64, 1536), (1, 9728, 896), (3, 17, 4864)])
+def test_rms_norm_stage(gpu, M, N, K):
+    print(f"[case] rms_norm stage M={M} N={N} K={K}", flush=True)
+    rng = np.random.default_rng(M * 7 + N + K)
+    x = rng.normal(0, 3, (M, K)).astype(np.float16)
+    w = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    bias = rng.normal(0, 0.1, N).astype(np.float32)
+    res = rng.normal(0, 1, (M, N)).astype(np.float16)
+    dq, ds = q8_weight(rng, N, K)
+    dx, dw, db = capi.DevBuf.from_array(x), capi.DevBuf.from_array(w), capi.DevBuf.from_array(bias)
+    dn = capi.DevBuf(M * K * 2)
+    ref, got = capi.DevBuf.from_array(res), capi.DevBuf.from_array(res)
+    eps = 1e-6
+    capi.call("vvh_rms_norm", dn.ptr, dx.ptr, dw.ptr, M, K, eps, F16, None)
+    capi.call("vvh_linear_q8_dev", ref.ptr, dn.ptr, dq.ptr, ds.ptr, db.ptr, ref.ptr, M, N, K, F16, F16, None)
+    capi.call("vvh_linear_q8_dev_in", got.ptr, dx.ptr, dq.ptr, ds.ptr, db.ptr, got.ptr, M, N, K, F16, F16,
+              capi.IN_RMS_NORM, dw.ptr, eps, None)
+    a, b = ref.to_array(np.float16, (M, N)), got.to_array(np.float16, (M, N))
+    assert np.array_equal(a.view(np.uint16), b.view(np.uint16)), float(np.abs(a.astype(np.float32) - b).max())
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 896, 4864), (2, 100, 4864), (3, 64, 896), (4, 48, 2048)])
+@pytest.mark.parametrize("outd", [F16, F32])
+def test_silu_mul_stage(gpu, M, N, K, outd):
+    print(f"[case] silu_mul stage M={M} N={N} K={K} out={outd}", flush=True)
+    rng = np.random.default_rng(M + N + K + outd)
+    gu = rng.normal(0, 2, (M, 2 * K)).astype(np.float16)
+    dq, ds = q8_weight(rng, N, K)
+    dgu = capi.DevBuf.from_array(gu)
+    ob = 2 if outd == F16 else 4
+    dg = capi.DevBuf(M * K * 2)
+    ref, got = capi.DevBuf(M * N * ob), capi.DevBuf(M * N * ob)
+    for m in range(M):  # the standalone operator, row by row as the model calls it
+        capi.call("vvh_eltwise", capi.OP_SILU_MUL, dg.addr(m * K * 2), dgu.addr(m * 4 * K), dgu.addr(m * 4 * K + 2 * K),
+                  K, F16, None)
+    capi.call("vvh_linear_q8_dev", ref.ptr, dg.ptr, dq.ptr, ds.ptr, None, None, M, N, K, F16, outd, None)
+    capi.call("vvh_linear_q8_dev_in", got.ptr, dgu.ptr, dq.ptr, ds.ptr, None, None, M, N, K, F16, outd,
+              capi.IN_SILU_MUL, None, 0.0, None)
+    u = np.uint16 if outd == F16 else np.uint32
+    assert np.array_equal(ref.to_array(u, (M, N)), got.to_array(u, (M, N)))
+
+
+def test_input_stage_limits(gpu):
+    """Shapes the stage cannot serve are refused, never computed another way."""
+    rng = np.random.default_rng(5)
+    dq, ds = q8_weight(rng, 64, 896)
+    dx, dw, out = capi.DevBuf(8 * 896 * 4), capi.DevBuf(896 * 4 + 16), capi.DevBuf(8 * 64 * 4)
+    unsupported, invalid = 7, 1
+
+    def st(M, act, in_op, w, K=896):
+        return capi.status_of("vvh_linear_q8_dev_in", out.ptr, dx.ptr, dq.ptr, ds.ptr, None, None, M, 64, K, act,
+                              act, in_op, w, 1e-6, None)
+    assert st(5, F16, capi.IN_RMS_NORM, dw.ptr) == unsupported       # M > 4
+    assert st(1, F32, capi.IN_RMS_NORM, dw.ptr) == unsupported       # fp32 activations
+    assert st(1, F16, capi.IN_RMS_NORM, dw.ptr + 4) == invalid       # misaligned norm weights
+    assert st(1, F16, capi.IN_RMS_NORM, None) == invalid             # no norm weights
+    assert st(1, F16, 3, dw.ptr) == invalid                          # unknown stage
+    assert st(1, F16, capi.IN_RMS_NORM, dw.ptr, K=888) == unsupported  # K % 16 != 0
+
+
+@pytest.mark.parametrize("S,pos", [(1, 0), (1, 37), (3, 5)])
+@pytest.mark.parametrize("act", [F16, F32], ids=["f16", "f32"])
+def test_rope_append(gpu, S, pos, act):
+    print(f"[case] rope_append S={S} pos={pos} act={act}", flush=True)
+    H, KVH, D, cap = 14, 2, 64, 48
+    dt = np.float16 if act == F16 else np.float32
+    rng = np.random.default_rng(S * 100 + pos + act)
+    q = rng.normal(0, 1, (S, H, D)).astype(dt)
+    k = rng.normal(0, 1, (S, KVH, D)).astype(dt)
+    v = rng.normal(0, 1, (S, KVH, D)).astype(dt)
+    cache = rng.normal(0, 1, (cap, KVH, D)).astype(dt)
+    es = np.dtype(dt).itemsize
+    row = KVH * D * es
+    # unfused: rope in place, then copy the rows into the caches
+    q1, k1, v1 = (capi.DevBuf.from_array(a) for a in (q, k, v))
+    kc1, vc1 = capi.DevBuf.from_array(cache), capi.DevBuf.from_array(cache)
+    capi.call("vvh_rope", q1.ptr, k1.ptr, S, H, KVH, D, pos, 1e6, act, None)
+    capi.call("vvh_memcpy_d2d_async", kc1.addr(pos * row), k1.ptr, S * row, None)
+    capi.call("vvh_memcpy_d2d_async", vc1.addr(pos * row), v1.ptr, S * row, None)
+    # fused
+    q2, k2, v2 = (capi.DevBuf.from_array(a) for a in (q, k, v))
+    kc2, vc2 = capi.DevBuf.from_array(cache), capi.DevBuf.from_array(cache)
+    capi.call("vvh_rope_append", q2.ptr, k2.ptr, v2.ptr, kc2.ptr, vc2.ptr, S, H, KVH, D, pos, 1e6, act, None)
+    u = np.uint16 if act == F16 else np.uint32
+    for a, b, shape in ((q1, q2, q.shape), (k1, k2, k.shape), (kc1, kc2, cache.shape), (vc1, vc2, cache.shape)):
+        assert np.array_equal(a.to_array(u, shape), b.to_array(u, shape))
+
+
+def test_plan_input_stage(gpu):
+    """q/k/v as one grouped launch reading rms_norm(x) through the plan's
+    input stage: equal to the plan over the normed rows."""
+    rng = np.random.default_rng(9)
+    K = 896
+    x = rng.normal(0, 2, (1, K)).astype(np.float16)
+    w = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    dx, dw, dn = capi.DevBuf.from_array(x), capi.DevBuf.from_array(w), capi.DevBuf(K * 2)
+    capi.call("vvh_rms_norm", dn.ptr, dx.ptr, dw.ptr, 1, K, 1e-6, F16, None)
+    shapes = [896, 128, 128]
+    ws = [q8_weight(rng, N, K) for N in shapes]
+    outs = {}
+    for name, src in (("ref", dn), ("fused", dx)):
+        bufs = [capi.DevBuf(N * 2) for N in shapes]
+        probs = [capi.Q8Problem(out=b.ptr, inp=src.ptr, residual=None, weight=q.ptr, scales=s.ptr, bias=None,
+                                M=1, N=N, K=K) for b, (q, s), N in zip(bufs, ws, shapes)]
+        h = ctypes.c_uint64()
+        capi.call("vvh_plan_create", (capi.Q8Problem * 3)(*probs), 3, F16, F16, ctypes.byref(h))
+        try:
+            if name == "fused":
+                capi.call("vvh_plan_set_input_op", h.value, capi.IN_RMS_NORM, dw.ptr, 1e-6)
+            capi.call("vvh_plan_run", h.value, None)
+            outs[name] = [b.to_array(np.uint16, (N,)) for b, N in zip(bufs, shapes)]
+        finally:
+            capi.call("vvh_plan_destroy", h.value)
+    for a, b in zip(outs["ref"], outs["fused"]):
+        assert np.array_equal(a, b)
+
+
+def fused_vs_unfused(cfg, head, steps, max_ctx):
+    models = [qd.Model(cfg, act=F16, lm_head=head, max_ctx=max_ctx, seed=11, fused=f) for f in (False, True)]
+    try:
+        assert models[1].calls_per_step() < models[0].calls_per_step()
+        tok = 3
+        for pos in range(steps):
+            print(f"[case] fused step {cfg.hidden}x{cfg.layers} head={head} pos={pos}", flush=True)
+            logits = []
+            for m in models:
+                m.step(tok, pos)
+                logits.append(m.logits_host())
+            assert np.array_equal(logits[0].view(np.uint32), logits[1].view(np.uint32)), \
+                f"pos {pos}: max difference {float(np.abs(logits[0] - logits[1]).max()):.3e}"
+            toks = [m.next_token() for m in models]
+            assert toks[0] == toks[1]
+            tok = toks[0]
+    finally:
+        for m in models:
+            m.close()
+
+
+@pytest.mark.parametrize("head", ["dense", "int8"])
+def test_fused_step_small(gpu, head):
+    fused_vs_unfused(qd.Config(hidden=128, heads=4, kv_heads=2, inter=256, layers=2, vocab=512), head, 10, 16)
+
+
+@pytest.mark.parametrize("head", ["dense", "int8"])
+def test_fused_step_qwen25_05b_shapes(gpu, head):
+    fused_vs_unfused(qd.QWEN25_05B, head, 2, 8)

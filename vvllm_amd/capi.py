@@ -17,6 +17,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libv
 
 F32, F16, BF16 = 0, 1, 2
 OP_ADD, OP_MUL, OP_SILU, OP_SILU_MUL = 0, 1, 2, 3
+IN_NONE, IN_RMS_NORM, IN_SILU_MUL = 0, 1, 2
 KERNEL_AUTO, KERNEL_GENERIC, KERNEL_GEMV_F32, KERNEL_SKINNY, KERNEL_GEMM, KERNEL_STREAM, KERNEL_DOT = range(7)
 KERNEL_NAMES = {0: "auto", 1: "generic", 2: "gemv_f32", 3: "skinny", 4: "gemm", 5: "stream", 6: "dot"}
 STATUS = {0: "VVH_OK", 1: "VVH_ERR_INVALID_ARG", 2: "VVH_ERR_NO_DEVICE", 3: "VVH_ERR_OUT_OF_MEMORY",
@@ -67,6 +68,11 @@ SIGNATURES = {
                                   c_size_t, c_size_t, c_int, c_int, c_void_p]),
     "vvh_plan_create": (c_int, [POINTER(Q8Problem), c_size_t, c_int, c_int, POINTER(c_uint64)]),
     "vvh_plan_run": (c_int, [c_uint64, c_void_p]),
+    "vvh_plan_set_input_op": (c_int, [c_uint64, c_int, c_void_p, c_float]),
+    "vvh_linear_q8_dev_in": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t,
+                                     c_size_t, c_size_t, c_int, c_int, c_int, c_void_p, c_float, c_void_p]),
+    "vvh_rope_append": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_size_t, c_size_t,
+                                c_size_t, c_size_t, c_float, c_int, c_void_p]),
     "vvh_plan_destroy": (c_int, [c_uint64]),
     "vvh_plan_launches": (c_int, [c_uint64, POINTER(c_int)]),
     "vvh_plan_kernel": (c_int, [c_uint64, POINTER(c_int)]),

@@ -31,6 +31,13 @@ struct LinArgs {
     float* ws;
     int32_t nsplit;
     int32_t kstages;
+    // k_dot input stage (activations staged in LDS only): xop 0 = inp as is,
+    // 1 = RMSNorm of each row of inp with weights xw and epsilon xeps (the
+    // arithmetic of k_rms_norm), 2 = silu(gate) * up of rows [gate | up] of
+    // 2K values (the arithmetic of k_eltwise's SiLU-mul).
+    const float* xw;
+    float xeps;
+    int32_t xop;
 };
 
 // Persistent streaming decode launch (k_stream).  Work is a sequence of
@@ -138,6 +145,8 @@ int launch_rms_norm(void* out, const void* x, const float* w, int64_t rows, int6
 int launch_softmax(void* out, const void* x, int64_t rows, int64_t n, int dtype, void* stream);
 int launch_rope(void* q, void* k, int64_t S, int64_t H, int64_t KVH, int64_t D, int64_t pos, float theta, int dtype,
                 void* stream);
+int launch_rope_append(void* q, void* k, const void* v, void* kc, void* vc, int64_t S, int64_t H, int64_t KVH,
+                       int64_t D, int64_t pos, float theta, int dtype, void* stream);
 int launch_embedding(void* out, const float* table, int64_t token, int64_t hidden, int dtype, void* stream);
 int64_t attention_max_len();
 int launch_attention(void* out, const void* q, const void* k, const void* v, int64_t n_q, int64_t len0, int64_t H,

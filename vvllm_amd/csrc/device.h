@@ -68,6 +68,39 @@ __device__ __forceinline__ void lds_barrier()
     __builtin_amdgcn_sched_barrier(0);
 }
 
+// Block-wide sum over 256 threads (4 waves); `red` holds 4 floats.  Shared by
+// k_rms_norm and the RMSNorm input stage of k_dot, which must round alike.
+__device__ __forceinline__ float block_sum256(float v, float* red)
+{
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// RMSNorm's divisor and output, and the SiLU-gated product, in the
+// reference's fp32 operation order (backend_naive.cc:68-76, :297-298); used by
+// the standalone kernels and by the fused input stage of k_dot alike.  The
+// products are materialised as fp32 (the empty asm) before any conversion to
+// fp16: otherwise the compiler may fold multiply and conversion into one
+// v_fma_mixlo_f16, which rounds once to fp16, in one kernel and not in
+// another, and the two then disagree by one fp16 ulp wherever rounding to
+// fp32 first changes the result.
+__device__ __forceinline__ float rms_of(float sum_sq, int64_t n, float eps) { return sqrtf(sum_sq / (float)n + eps); }
+__device__ __forceinline__ float rms_apply(float x, float rms, float w)
+{
+    float r = x / rms * w;
+    __asm__("" : "+v"(r));
+    return r;
+}
+__device__ __forceinline__ float silu_mul_ref(float g, float u)
+{
+    float r = (g / (1.0f + expf(-g))) * u;
+    __asm__("" : "+v"(r));
+    return r;
+}
+
 // Pointers read from memory (plan tables) are generic to the compiler, which
 // then emits flat loads; those count in lgkmcnt as well as vmcnt, so every
 // wait on a scalar load would also drain the weight stream.  Kernels that

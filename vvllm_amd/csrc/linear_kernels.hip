@@ -494,30 +494,78 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
         }
     };
 
+    // (the weight ring is issued after the staging: issued before it, the
+    // ring's 64 VGPRs stay live through the staging and occupancy drops from
+    // 5 to 3 waves per SIMD, measured 5.9 -> 5.3 TB/s on the decode set)
     if (XLDS) {
-        // activations to LDS, 4 chunks of 16 bytes per thread per round
-        const int64_t xchunks = a.M * a.K / 8;
-        constexpr int XL = 4;
-        int64_t base = 0;
-        for (; base + 256 * XL <= xchunks; base += 256 * XL) {
-            u4 xr[XL];
+        // activations to LDS (through the input stage a.xop), 4 chunks of 8
+        // values per thread per round; a round's loads are clamped into the
+        // input and its stores masked, so all of them are in flight at once
+        const int xop = a.xop;
+        const int32_t K32 = (int32_t)a.K, xchunks = (int32_t)(a.M * a.K / 8);
+        const int64_t ldin = xop == 2 ? 2 * a.K : a.K;  // [gate | up] rows for SiLU-mul
+        float rinv[MT];                                 // RMSNorm divisor of each row
 #pragma unroll
-            for (int i = 0; i < XL; i++) xr[i] = *gbl(reinterpret_cast<const u4*>(xg + (base + threadIdx.x + 256 * i) * 8));
+        for (int m = 0; m < MT; m++) rinv[m] = 1.0f;
+        if (xop == 1) {
+            // per row as k_rms_norm: thread t sums x[t], x[t + 256], ... in
+            // order, then the same block reduction
+            float* red4 = &red.v[0][0][0];
 #pragma unroll
-            for (int i = 0; i < XL; i++) {
-                const int64_t e = (base + threadIdx.x + 256 * i) * 8, row = e / a.K, col = e - row * a.K;
-                *reinterpret_cast<u4*>(xs + row * ldx + col) = xr[i];
+            for (int m = 0; m < MT; m++) {
+                if (m < a.M) {
+                    const f16* xr = xg + m * a.K;
+                    float ss = 0.0f;
+                    for (int32_t i = threadIdx.x; i < K32; i += 256) {
+                        const float v = (float)*gbl(xr + i);
+                        ss += v * v;
+                    }
+                    ss = block_sum256(ss, red4);
+                    rinv[m] = rms_of(ss, a.K, a.xeps);
+                }
             }
         }
-        for (int64_t idx = base + threadIdx.x; idx < xchunks; idx += 256) {
-            const int64_t e = idx * 8, row = e / a.K, col = e - row * a.K;
-            *reinterpret_cast<u4*>(xs + row * ldx + col) = *gbl(reinterpret_cast<const u4*>(xg + e));
+        constexpr int XL = 4;
+        for (int32_t base = 0; base < xchunks; base += 256 * XL) {
+            h8 xr[XL], yr[XL];
+#pragma unroll
+            for (int i = 0; i < XL; i++) {
+                int32_t idx = base + (int32_t)threadIdx.x + 256 * i;
+                idx = idx < xchunks ? idx : xchunks - 1;
+                const int32_t row = idx * 8 / K32, col = idx * 8 - row * K32;
+                const f16* p = xg + row * ldin + col;
+                xr[i] = *gbl(reinterpret_cast<const h8*>(p));
+                if (xop == 2) yr[i] = *gbl(reinterpret_cast<const h8*>(p + a.K));
+            }
+#pragma unroll
+            for (int i = 0; i < XL; i++) {
+                const int32_t idx = base + (int32_t)threadIdx.x + 256 * i;
+                if (idx >= xchunks) continue;
+                const int32_t row = idx * 8 / K32, col = idx * 8 - row * K32;
+                h8 v = xr[i];
+                if (xop == 1) {
+                    float rv = rinv[0];
+#pragma unroll
+                    for (int m = 1; m < MT; m++) rv = row == m ? rinv[m] : rv;
+                    const f4 w0 = *gbl(reinterpret_cast<const f4*>(a.xw + col));
+                    const f4 w1 = *gbl(reinterpret_cast<const f4*>(a.xw + col + 4));
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        v[j] = (f16)rms_apply((float)xr[i][j], rv, w0[j]);
+                        v[4 + j] = (f16)rms_apply((float)xr[i][4 + j], rv, w1[j]);
+                    }
+                } else if (xop == 2) {
+#pragma unroll
+                    for (int j = 0; j < 8; j++) v[j] = (f16)silu_mul_ref((float)xr[i][j], (float)yr[i][j]);
+                }
+                *reinterpret_cast<h8*>(xs + row * ldx + col) = v;
+            }
         }
         __syncthreads();
     }
 
+    int32_t s = (int32_t)c.s0;
     if (active) {
-        int32_t s = (int32_t)c.s0;
 #pragma unroll
         for (int u = 0; u < D; u++) issue(u, s + u);
         // while steps remain beyond the ring: consume slot u, refill it with

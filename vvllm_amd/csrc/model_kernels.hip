@@ -34,14 +34,7 @@ __device__ __forceinline__ void stf(T* p, int64_t i, float v) { p[i] = (T)v; }
 __device__ __forceinline__ float silu_ref(float v) { return v * (1.0f / (1.0f + expf(-v))); }
 
 // Block-wide sum / max over 256 threads (4 waves); `red` holds 4 floats.
-__device__ __forceinline__ float block_sum(float v, float* red)
-{
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    return (red[0] + red[1]) + (red[2] + red[3]);
-}
+__device__ __forceinline__ float block_sum(float v, float* red) { return block_sum256(v, red); }
 __device__ __forceinline__ float block_max(float v, float* red)
 {
     for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
@@ -66,7 +59,7 @@ __global__ __launch_bounds__(256) void k_eltwise(T* __restrict__ out, const T* _
         if constexpr (OP == VVH_OP_ADD) r = a + ldf(y, i);
         else if constexpr (OP == VVH_OP_MUL) r = a * ldf(y, i);
         else if constexpr (OP == VVH_OP_SILU) r = silu_ref(a);
-        else r = (a / (1.0f + expf(-a))) * ldf(y, i);  // silu_mul, backend_naive.cc:297-298
+        else r = silu_mul_ref(a, ldf(y, i));  // silu_mul, backend_naive.cc:297-298
         stf(out, i, r);
     }
 }
@@ -105,8 +98,8 @@ __global__ __launch_bounds__(256) void k_rms_norm(T* __restrict__ out, const T* 
         ss += v * v;
     }
     ss = block_sum(ss, red);
-    const float rms = sqrtf(ss / (float)n + eps);
-    for (int64_t i = threadIdx.x; i < n; i += 256) stf(orow, i, ldf(xr, i) / rms * w[i]);
+    const float rms = rms_of(ss, n, eps);
+    for (int64_t i = threadIdx.x; i < n; i += 256) stf(orow, i, rms_apply(ldf(xr, i), rms, w[i]));
 }
 
 int launch_rms_norm(void* out, const void* x, const float* w, int64_t rows, int64_t n, float eps, int dtype,
@@ -159,24 +152,31 @@ int launch_softmax(void* out, const void* x, int64_t rows, int64_t n, int dtype,
 // libm's powf / cosf / sinf return.  The exponent, reciprocal, angle and
 // rotation stay in the reference's fp32 operation order.
 // ---------------------------------------------------------------------------
-template <typename T>
+//
+// APPEND (vvh_rope_append): the threads of the k pairs also store the rotated
+// pair in the key cache row pos + s and copy the matching pair of v into the
+// value cache row, the KVCache::append that follows rope in transformer_forward
+// (transformer.h:145-160), without separate copies.
+template <typename T, bool APPEND>
 __global__ __launch_bounds__(256) void k_rope(T* __restrict__ q, T* __restrict__ k, int64_t S, int64_t H, int64_t KVH,
-                                              int64_t D, int64_t pos, float theta)
+                                              int64_t D, int64_t pos, float theta, const T* __restrict__ v,
+                                              T* __restrict__ kc, T* __restrict__ vc)
 {
     const int64_t half = D / 2;
     const int64_t nq = S * H * half, total = nq + S * KVH * half;
     for (int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x; g < total; g += (int64_t)gridDim.x * 256) {
         T* base;
-        int64_t s, i;
-        if (g < nq) {
+        int64_t s, i, hs;
+        const bool is_q = g < nq;
+        if (is_q) {
             i = g % half;
-            const int64_t hs = g / half;  // s * H + h
+            hs = g / half;  // s * H + h
             s = hs / H;
             base = q + hs * D;
         } else {
             const int64_t g2 = g - nq;
             i = g2 % half;
-            const int64_t hs = g2 / half;
+            hs = g2 / half;  // s * KVH + kvh
             s = hs / KVH;
             base = k + hs * D;
         }
@@ -185,8 +185,19 @@ __global__ __launch_bounds__(256) void k_rope(T* __restrict__ q, T* __restrict__
         const float angle = (float)(pos + s) * freq;
         const float c = (float)cos((double)angle), sn = (float)sin((double)angle);
         const float x0 = ldf(base, i), x1 = ldf(base, i + half);
-        stf(base, i, x0 * c - x1 * sn);
-        stf(base, i + half, x0 * sn + x1 * c);
+        const T r0 = (T)(x0 * c - x1 * sn), r1 = (T)(x0 * sn + x1 * c);
+        base[i] = r0;
+        base[i + half] = r1;
+        if constexpr (APPEND) {
+            if (!is_q) {
+                // row pos + s of the caches: hs * D - s * KVH * D = kvh * D
+                const int64_t dst = (pos * KVH + hs) * D;
+                kc[dst + i] = r0;
+                kc[dst + i + half] = r1;
+                vc[dst + i] = v[hs * D + i];
+                vc[dst + i + half] = v[hs * D + i + half];
+            }
+        }
     }
 }
 
@@ -198,9 +209,27 @@ int launch_rope(void* q, void* k, int64_t S, int64_t H, int64_t KVH, int64_t D, 
     const dim3 grid((unsigned)(want < 4096 ? (want > 0 ? want : 1) : 4096));
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (dtype == VVH_F16)
-        hipLaunchKernelGGL(k_rope<f16>, grid, dim3(256), 0, s, (f16*)q, (f16*)k, S, H, KVH, D, pos, theta);
+        hipLaunchKernelGGL((k_rope<f16, false>), grid, dim3(256), 0, s, (f16*)q, (f16*)k, S, H, KVH, D, pos, theta,
+                           nullptr, nullptr, nullptr);
     else
-        hipLaunchKernelGGL(k_rope<float>, grid, dim3(256), 0, s, (float*)q, (float*)k, S, H, KVH, D, pos, theta);
+        hipLaunchKernelGGL((k_rope<float, false>), grid, dim3(256), 0, s, (float*)q, (float*)k, S, H, KVH, D, pos,
+                           theta, nullptr, nullptr, nullptr);
+    return (int)hipGetLastError();
+}
+
+int launch_rope_append(void* q, void* k, const void* v, void* kc, void* vc, int64_t S, int64_t H, int64_t KVH,
+                       int64_t D, int64_t pos, float theta, int dtype, void* stream)
+{
+    const int64_t total = S * (H + KVH) * (D / 2);
+    const int64_t want = (total + 255) / 256;
+    const dim3 grid((unsigned)(want < 4096 ? (want > 0 ? want : 1) : 4096));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (dtype == VVH_F16)
+        hipLaunchKernelGGL((k_rope<f16, true>), grid, dim3(256), 0, s, (f16*)q, (f16*)k, S, H, KVH, D, pos, theta,
+                           (const f16*)v, (f16*)kc, (f16*)vc);
+    else
+        hipLaunchKernelGGL((k_rope<float, true>), grid, dim3(256), 0, s, (float*)q, (float*)k, S, H, KVH, D, pos,
+                           theta, (const float*)v, (float*)kc, (float*)vc);
     return (int)hipGetLastError();
 }
 

@@ -1010,6 +1010,51 @@ VVH_API int vvh_linear_q8_dev(void* out, const void* inp, const int8_t* dev_weig
     return linear_dev(out, inp, dev_weight, dev_scales, dev_bias, residual, M, N, K, act_dtype, out_dtype, stream);
 }
 
+// The input stage runs in k_dot's activation staging only: fp16 activations,
+// M <= kDotMaxM, K % 16 == 0, aligned operands and the rows in LDS.
+static int input_op_ok(int in_op, const float* in_w, std::size_t M, std::size_t K, int act)
+{
+    if (in_op < VVH_IN_NONE || in_op > VVH_IN_SILU_MUL) return fail(VVH_ERR_INVALID_ARG, "bad input op %d", in_op);
+    if (in_op == VVH_IN_NONE) return VVH_OK;
+    if (in_op == VVH_IN_RMS_NORM && (!in_w || !aligned16(in_w)))
+        return fail(VVH_ERR_INVALID_ARG, "RMSNorm input stage needs 16-byte aligned weights");
+    if (act != VVH_F16 || M == 0 || M > (std::size_t)kDotMaxM || K % 16 != 0 || !dot_x_in_lds((int64_t)M, (int64_t)K))
+        return fail(VVH_ERR_UNSUPPORTED, "input stage needs fp16 activations, M <= %d, K %% 16 == 0 and "
+                    "rows that fit the block's LDS (M=%zu, K=%zu)", kDotMaxM, M, K);
+    return VVH_OK;
+}
+
+VVH_API int vvh_linear_q8_dev_in(void* out, const void* inp, const int8_t* dev_weight, const float* dev_scales,
+                                 const float* dev_bias, const void* residual, size_t M, size_t N, size_t K,
+                                 int act_dtype, int out_dtype, int in_op, const float* in_w, float in_eps,
+                                 void* stream)
+{
+    if (in_op == VVH_IN_NONE)
+        return linear_dev(out, inp, dev_weight, dev_scales, dev_bias, residual, M, N, K, act_dtype, out_dtype, stream);
+    int st = validate_call(out, inp, dev_weight, dev_scales, M, N, K, act_dtype, out_dtype);
+    if (st != VVH_OK) return st;
+    if ((st = input_op_ok(in_op, in_w, M, K, act_dtype)) != VVH_OK) return st;
+    if (N == 0) return VVH_OK;
+    REQUIRE_INIT();
+    if (!aligned16(dev_weight) || !aligned16(inp))
+        return fail(VVH_ERR_UNSUPPORTED, "input stage needs 16-byte aligned weights and activations");
+    LinArgs a{};
+    a.out = out;
+    a.inp = inp;
+    a.res = residual;
+    a.w = dev_weight;
+    a.scales = dev_scales;
+    a.bias = dev_bias;
+    a.M = (int64_t)M;
+    a.N = (int64_t)N;
+    a.K = (int64_t)K;
+    a.ksplit = 1;
+    a.xop = in_op;
+    a.xw = in_w;
+    a.xeps = in_eps;
+    return run_call(a, K_DOT, act_dtype, out_dtype, stream);
+}
+
 VVH_API int vvh_linear_q8(void* out, const void* inp, vvh_weight weight, const void* residual, size_t M,
                           size_t N, size_t K, int act_dtype, int out_dtype, void* stream)
 {
@@ -1144,6 +1189,32 @@ VVH_API int vvh_plan_run(vvh_plan plan, void* stream)
         if (st != VVH_OK) return st;
     }
     return VVH_OK;
+}
+
+VVH_API int vvh_plan_set_input_op(vvh_plan plan, int in_op, const float* in_w, float in_eps)
+{
+    REQUIRE_INIT();
+    std::lock_guard<std::mutex> lock(g_pmu);
+    auto it = g_plans.find(plan);
+    if (it == g_plans.end()) return fail(VVH_ERR_UNKNOWN_HANDLE, "unknown plan %llu", (unsigned long long)plan);
+    Plan& p = it->second;
+    if (!p.dot || !p.x_in_lds)
+        return fail(VVH_ERR_UNSUPPORTED, "input stage needs a plan that runs as one k_dot_grouped launch "
+                    "with its activations in LDS");
+    for (const LinArgs& a : p.args) {
+        const int st = input_op_ok(in_op, in_w, (std::size_t)a.M, (std::size_t)a.K, p.act);
+        if (st != VVH_OK) return st;
+    }
+    for (LinArgs& a : p.args) {
+        a.xop = in_op;
+        a.xw = in_w;
+        a.xeps = in_eps;
+    }
+    // the table is read by launches already queued: replace it once they are done
+    (void)hipDeviceSynchronize();
+    const hipError_t e = hipMemcpy(const_cast<LinArgs*>(p.sargs.table), p.args.data(), p.args.size() * sizeof(LinArgs),
+                                   hipMemcpyHostToDevice);
+    return e == hipSuccess ? VVH_OK : fail_hip(e, "plan table upload");
 }
 
 VVH_API int vvh_plan_destroy(vvh_plan plan)
@@ -1307,6 +1378,21 @@ VVH_API int vvh_rope(void* q, void* k, size_t seq_len, size_t num_heads, size_t 
     return ret_launch(launch_rope(q, k, (int64_t)seq_len, (int64_t)num_heads, (int64_t)num_kv_heads, (int64_t)head_dim,
                                   (int64_t)pos, theta, dtype, stream),
                       "rope launch");
+}
+
+VVH_API int vvh_rope_append(void* q, void* k, const void* v, void* k_cache, void* v_cache, size_t seq_len,
+                            size_t num_heads, size_t num_kv_heads, size_t head_dim, size_t pos, float theta, int dtype,
+                            void* stream)
+{
+    if (!act_ok(dtype)) return fail(VVH_ERR_INVALID_ARG, "bad dtype");
+    if (head_dim % 2 != 0) return fail(VVH_ERR_INVALID_ARG, "odd head_dim %zu", head_dim);
+    if (seq_len == 0 || head_dim == 0 || (num_heads == 0 && num_kv_heads == 0)) return VVH_OK;
+    if ((num_heads && !q) || (num_kv_heads && (!k || !v || !k_cache || !v_cache)))
+        return fail(VVH_ERR_INVALID_ARG, "null pointer");
+    REQUIRE_INIT();
+    return ret_launch(launch_rope_append(q, k, v, k_cache, v_cache, (int64_t)seq_len, (int64_t)num_heads,
+                                         (int64_t)num_kv_heads, (int64_t)head_dim, (int64_t)pos, theta, dtype, stream),
+                      "rope append launch");
 }
 
 VVH_API int vvh_embedding(void* out, const float* dev_table, size_t token_id, size_t hidden, size_t vocab, int dtype,

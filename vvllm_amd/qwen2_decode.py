@@ -15,6 +15,13 @@ graph).  The LM head is the tied embedding either as a dense linear (fp16
 copy of the table in fp16 mode, like BackendCUDA) or as int8 per-channel
 codes through linear_q8 (the int8 LM head).
 
+fused=True (fp16 only) issues the same arithmetic in fewer launches: the
+RMSNorms before q/k/v, gate_up and the int8 LM head and the SiLU-mul before
+down run in the input stage of the following linear (vvh_plan_set_input_op,
+vvh_linear_q8_dev_in), and RoPE writes the K/V cache rows itself
+(vvh_rope_append).  Each stage rounds exactly as the standalone operator, so
+the logits equal the unfused step's.
+
 The model is synthetic (seeded N(0, 0.02) weights, no checkpoint); it is the
 measurement and end-to-end parity harness of this library's operators.  The
 drop-in boundary for the reference's own model code is BackendHIP.
@@ -75,9 +82,12 @@ class _Q8:
 
 
 class Model:
-    def __init__(self, cfg: Config, act: int = F16, lm_head: str = "dense", max_ctx: int = 2048, seed: int = 0):
+    def __init__(self, cfg: Config, act: int = F16, lm_head: str = "dense", max_ctx: int = 2048, seed: int = 0,
+                 fused: bool = False):
         assert lm_head in ("dense", "int8")
-        self.cfg, self.act, self.lm_head, self.max_ctx = cfg, act, lm_head, max_ctx
+        if fused and act != F16:
+            raise ValueError("the fused step needs fp16 activations")
+        self.cfg, self.act, self.lm_head, self.max_ctx, self.fused = cfg, act, lm_head, max_ctx, fused
         c = cfg
         es = 2 if act == F16 else 4
         self.es = es
@@ -125,16 +135,21 @@ class Model:
         self.logits = capi.DevBuf(c.vocab * es)
         self.logits32 = capi.DevBuf(c.vocab * 4)
         self.token = capi.DevBuf(4)
-        # one grouped launch per layer for q/k/v (they share the input)
+        # one grouped launch per layer for q/k/v (they share the input: the
+        # normed rows, or in the fused step the residual stream through the
+        # plan's RMSNorm input stage)
         self.plans = []
+        src = self.x if fused else self.norm_out
         for L in self.layers:
-            probs = [capi.Q8Problem(out=o.ptr, inp=self.norm_out.ptr, residual=None, weight=p.q.ptr,
+            probs = [capi.Q8Problem(out=o.ptr, inp=src.ptr, residual=None, weight=p.q.ptr,
                                     scales=p.s.ptr, bias=p.b.ptr, M=1, N=p.N, K=p.K)
                      for o, p in ((self.q, L["q"]), (self.k_new, L["k"]), (self.v_new, L["v"]))]
             arr = (capi.Q8Problem * 3)(*probs)
             h = ctypes.c_uint64()
             capi.call("vvh_plan_create", arr, 3, act, act, ctypes.byref(h))
             self.plans.append(h.value)
+            if fused:
+                capi.call("vvh_plan_set_input_op", h.value, capi.IN_RMS_NORM, L["ln1"].ptr, c.eps)
 
     def fill_kv(self, seed: int = 0) -> None:
         """Seeded N(0, 1) rows in every layer's whole KV cache (a stand-in
@@ -149,6 +164,9 @@ class Model:
         argmax over the vocabulary launch two kernels each)."""
         c = self.cfg
         head = 1 if self.lm_head == "int8" or self.act == F32 else 2
+        if self.fused:
+            final_norm = 0 if self.lm_head == "int8" else 1
+            return 2 + 6 * c.layers + final_norm + head + 1
         return (2 if self.act == F16 else 1) + 11 * c.layers + 1 + head + 1
 
     def close(self):
@@ -171,26 +189,36 @@ class Model:
             call("vvh_embedding", self.x.ptr, self.table.ptr, token, c.hidden, c.vocab, F32, stream)
         scale = float(1.0 / np.sqrt(np.float32(c.head_dim)))
         kvb = c.kv_dim * self.es
-        for L, plan in zip(self.layers, self.plans):
-            call("vvh_rms_norm", self.norm_out.ptr, self.x.ptr, L["ln1"].ptr, 1, c.hidden, c.eps, a, stream)
-            call("vvh_plan_run", plan, stream)
-            call("vvh_rope", self.q.ptr, self.k_new.ptr, 1, c.heads, c.kv_heads, c.head_dim, pos, c.theta, a, stream)
-            call("vvh_memcpy_d2d_async", L["kc"].ptr + pos * kvb, self.k_new.ptr, kvb, stream)
-            call("vvh_memcpy_d2d_async", L["vc"].ptr + pos * kvb, self.v_new.ptr, kvb, stream)
-            call("vvh_attention", self.attn.ptr, self.q.ptr, L["kc"].ptr, L["vc"].ptr, 1, pos + 1, c.heads,
-                 c.kv_heads, c.head_dim, scale, a, stream)
-            o = L["o"]
-            call("vvh_linear_q8_dev", self.x.ptr, self.attn.ptr, o.q.ptr, o.s.ptr, None, self.x.ptr, 1, c.hidden,
-                 c.hidden, a, a, stream)
-            call("vvh_rms_norm", self.norm_out.ptr, self.x.ptr, L["ln2"].ptr, 1, c.hidden, c.eps, a, stream)
-            g = L["gu"]
-            call("vvh_linear_q8_dev", self.gu.ptr, self.norm_out.ptr, g.q.ptr, g.s.ptr, None, None, 1, 2 * c.inter,
-                 c.hidden, a, a, stream)
-            call("vvh_eltwise", capi.OP_SILU_MUL, self.gate.ptr, self.gu.ptr, self.gu.ptr + c.inter * self.es,
-                 c.inter, a, stream)
-            d = L["down"]
-            call("vvh_linear_q8_dev", self.x.ptr, self.gate.ptr, d.q.ptr, d.s.ptr, None, self.x.ptr, 1, c.hidden,
-                 c.inter, a, a, stream)
+        if self.fused:
+            self._fused_layers(pos, scale, stream)
+        else:
+            for L, plan in zip(self.layers, self.plans):
+                call("vvh_rms_norm", self.norm_out.ptr, self.x.ptr, L["ln1"].ptr, 1, c.hidden, c.eps, a, stream)
+                call("vvh_plan_run", plan, stream)
+                call("vvh_rope", self.q.ptr, self.k_new.ptr, 1, c.heads, c.kv_heads, c.head_dim, pos, c.theta, a,
+                     stream)
+                call("vvh_memcpy_d2d_async", L["kc"].ptr + pos * kvb, self.k_new.ptr, kvb, stream)
+                call("vvh_memcpy_d2d_async", L["vc"].ptr + pos * kvb, self.v_new.ptr, kvb, stream)
+                call("vvh_attention", self.attn.ptr, self.q.ptr, L["kc"].ptr, L["vc"].ptr, 1, pos + 1, c.heads,
+                     c.kv_heads, c.head_dim, scale, a, stream)
+                o = L["o"]
+                call("vvh_linear_q8_dev", self.x.ptr, self.attn.ptr, o.q.ptr, o.s.ptr, None, self.x.ptr, 1,
+                     c.hidden, c.hidden, a, a, stream)
+                call("vvh_rms_norm", self.norm_out.ptr, self.x.ptr, L["ln2"].ptr, 1, c.hidden, c.eps, a, stream)
+                g = L["gu"]
+                call("vvh_linear_q8_dev", self.gu.ptr, self.norm_out.ptr, g.q.ptr, g.s.ptr, None, None, 1,
+                     2 * c.inter, c.hidden, a, a, stream)
+                call("vvh_eltwise", capi.OP_SILU_MUL, self.gate.ptr, self.gu.ptr, self.gu.ptr + c.inter * self.es,
+                     c.inter, a, stream)
+                d = L["down"]
+                call("vvh_linear_q8_dev", self.x.ptr, self.gate.ptr, d.q.ptr, d.s.ptr, None, self.x.ptr, 1,
+                     c.hidden, c.inter, a, a, stream)
+        if self.fused and self.lm_head == "int8":
+            h = self.head
+            call("vvh_linear_q8_dev_in", self.logits32.ptr, self.x.ptr, h.q.ptr, h.s.ptr, None, None, 1, c.vocab,
+                 c.hidden, a, F32, capi.IN_RMS_NORM, self.final_norm.ptr, c.eps, stream)
+            call("vvh_argmax", self.logits32.ptr, c.vocab, self.token.ptr, stream)
+            return
         call("vvh_rms_norm", self.final.ptr, self.x.ptr, self.final_norm.ptr, 1, c.hidden, c.eps, a, stream)
         if self.lm_head == "int8":
             h = self.head
@@ -204,6 +232,26 @@ class Model:
             call("vvh_dense", self.logits32.ptr, self.final.ptr, self.table.ptr, F32, None, None, 1, c.vocab,
                  c.hidden, F32, stream)
         call("vvh_argmax", self.logits32.ptr, c.vocab, self.token.ptr, stream)
+
+    def _fused_layers(self, pos: int, scale: float, stream) -> None:
+        """The layers of the fused step: 6 launches per layer instead of 10
+        and two copies."""
+        c, a, call = self.cfg, self.act, capi.call
+        for L, plan in zip(self.layers, self.plans):
+            call("vvh_plan_run", plan, stream)  # q/k/v of rms_norm(x, ln1)
+            call("vvh_rope_append", self.q.ptr, self.k_new.ptr, self.v_new.ptr, L["kc"].ptr, L["vc"].ptr, 1, c.heads,
+                 c.kv_heads, c.head_dim, pos, c.theta, a, stream)
+            call("vvh_attention", self.attn.ptr, self.q.ptr, L["kc"].ptr, L["vc"].ptr, 1, pos + 1, c.heads,
+                 c.kv_heads, c.head_dim, scale, a, stream)
+            o = L["o"]
+            call("vvh_linear_q8_dev", self.x.ptr, self.attn.ptr, o.q.ptr, o.s.ptr, None, self.x.ptr, 1, c.hidden,
+                 c.hidden, a, a, stream)
+            g = L["gu"]
+            call("vvh_linear_q8_dev_in", self.gu.ptr, self.x.ptr, g.q.ptr, g.s.ptr, None, None, 1, 2 * c.inter,
+                 c.hidden, a, a, capi.IN_RMS_NORM, L["ln2"].ptr, c.eps, stream)
+            d = L["down"]
+            call("vvh_linear_q8_dev_in", self.x.ptr, self.gu.ptr, d.q.ptr, d.s.ptr, None, self.x.ptr, 1, c.hidden,
+                 c.inter, a, a, capi.IN_SILU_MUL, None, 0.0, stream)
 
     def next_token(self) -> int:
         capi.sync()
@@ -247,9 +295,11 @@ def main(argv=None) -> int:
     ap.add_argument("--act", choices=("f16", "f32"), default="f16")
     ap.add_argument("--position", type=int, default=511)
     ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--fused", action="store_true", help="input stages and RoPE + KV append (fp16)")
     a = ap.parse_args(argv)
     capi.init(0)
-    m = Model(QWEN25_05B, act=F16 if a.act == "f16" else F32, lm_head=a.lm_head, max_ctx=a.position + 1, seed=3)
+    m = Model(QWEN25_05B, act=F16 if a.act == "f16" else F32, lm_head=a.lm_head, max_ctx=a.position + 1, seed=3,
+              fused=a.fused)
     m.fill_kv(5)
     m.step(1, a.position)
     capi.sync()
@@ -258,7 +308,8 @@ def main(argv=None) -> int:
         m.step(1, a.position)
     tok = m.next_token()
     el = (time.perf_counter() - t0) / a.steps
-    print(f"{a.steps} steps at position {a.position} ({a.lm_head} LM head, {a.act}): {el * 1e6:.0f} us/step "
+    print(f"{a.steps} steps at position {a.position} ({a.lm_head} LM head, {a.act}{', fused' if a.fused else ''}): "
+          f"{el * 1e6:.0f} us/step "
           f"launched from Python, next token {tok}", flush=True)
     m.close()
     return 0
