@@ -514,11 +514,21 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
 #pragma unroll
             for (int m = 0; m < MT; m++) {
                 if (m < a.M) {
+                    // 8 loads in flight per batch; masked slots read a valid
+                    // element and add an exact 0, so the sum is the same
+                    // in-order sum as k_rms_norm's
                     const f16* xr = xg + m * a.K;
                     float ss = 0.0f;
-                    for (int32_t i = threadIdx.x; i < K32; i += 256) {
-                        const float v = (float)*gbl(xr + i);
-                        ss += v * v;
+                    for (int32_t i0 = threadIdx.x; i0 < K32; i0 += 256 * 8) {
+                        float v[8];
+#pragma unroll
+                        for (int j = 0; j < 8; j++) {
+                            const int32_t i = i0 + 256 * j;
+                            const float e = (float)*gbl(xr + (i < K32 ? i : K32 - 1));
+                            v[j] = i < K32 ? e : 0.0f;
+                        }
+#pragma unroll
+                        for (int j = 0; j < 8; j++) ss += v[j] * v[j];
                     }
                     ss = block_sum256(ss, red4);
                     rinv[m] = rms_of(ss, a.K, a.xeps);
