@@ -312,9 +312,10 @@ def main():
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--workload", choices=("decode", "prefill", "vendor-gemm"), default="decode",
+    ap.add_argument("--workload", choices=("decode", "prefill", "vendor-gemm", "copy"), default="decode",
                     help="decode: configs[1] (the headline line); prefill: configs[3] gate/up GEMM only; "
-                         "vendor-gemm: the int8 GEMM beside the vendor fp16 GEMM on the prefill shapes")
+                         "vendor-gemm: the int8 GEMM beside the vendor fp16 GEMM on the prefill shapes; "
+                         "copy: a 256 MiB device-to-device copy, the calibration of the HBM traffic counters")
     ap.add_argument("--prefill-m", type=int, default=512)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -331,6 +332,8 @@ def main():
         return prefill_main(args, ev, name)
     if args.workload == "vendor-gemm":
         return vendor_gemm_main(args, ev)
+    if args.workload == "copy":
+        return copy_main(args, ev)
     h, kv, inter, L = QWEN05["hidden"], QWEN05["kv"], QWEN05["inter"], QWEN05["layers"]
     projs = layer_projs(h, kv, inter)
     tmp_w = capi.DevBuf(max(inter * h, 151936 * 896, 8960 * 1536) * 4)
@@ -429,6 +432,23 @@ def prefill_main(args, ev, name):
         "roofline": {"bound": "mfma", "kernel": kern, "achieved": round(tf, 2), "peak": MFMA_F16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None},
         "cpu_baseline": None}), flush=True)
+
+
+def copy_main(args, ev):
+    """Calibration of rocprofv3's FETCH_SIZE / WRITE_SIZE: one 256 MiB
+    device-to-device copy per step (hipMemcpyAsync, __amd_rocclr_copyBuffer),
+    which reads and writes exactly 256 MiB.  Run under rocprofv3 --pmc, the
+    counters per copy dispatch against 262144 KiB give the scale factors that
+    turn the decode kernel's counters into HBM bytes."""
+    nbytes = 256 << 20
+    src, dst = capi.DevBuf(nbytes), capi.DevBuf(nbytes)
+    capi.call("vvh_fill_normal", src.ptr, F32, nbytes // 4, 1, 0.0, 1.0, None)
+    for _ in range(args.warmup):
+        capi.call("vvh_memcpy_d2d_async", dst.ptr, src.ptr, nbytes, None)
+    ms = timed(ev, lambda i: capi.call("vvh_memcpy_d2d_async", dst.ptr, src.ptr, nbytes, None), args.steps)
+    rate = 2 * nbytes / (ms * 1e-3) / 1e9
+    print(json.dumps({"workload": "copy calibration", "bytes_read": nbytes, "bytes_written": nbytes,
+                      "ms_per_copy": round(ms, 4), "GB_per_s_read_plus_write": round(rate, 1)}), flush=True)
 
 
 VENDOR_SHAPES = [("gate_up", 128, 4864, 896), ("gate_up", 512, 4864, 896), ("gate_up", 2048, 4864, 896),
