@@ -153,24 +153,57 @@ def arena_size(items):
     return sum((n + 255) // 256 * 256 for n in items)
 
 
+ROTATE_BYTES = 1 << 30  # more than the 256 MB MALL: every timed call reads its weights from HBM
+
+
+def rotation(tmp_w, M, N, K, bias, res, seed, act=F16, outd=F16, max_reps=4096):
+    """Replicas of one projection's weights (codes, scales, bias), enough that
+    cycling through them moves >= ROTATE_BYTES of weights, in one arena; the
+    activation and output rows are shared, as in a model step, where the
+    previous operator has just written them.  Returns (arena, linears)."""
+    ab, ob = (2 if act == F16 else 4), (2 if outd == F16 else 4)
+    wsz = [N * K, 4 * N] + ([4 * N] if bias else [])
+    per = arena_size(wsz)
+    n = max(2, min(max_reps, -(-ROTATE_BYTES // per)))
+    ar = Arena(per * n + arena_size([M * K * ab, M * N * ob]))
+    x, y = ar.take(M * K * ab), ar.take(M * N * ob)
+    capi.call("vvh_fill_normal", x, act, M * K, seed + 2, 0.0, 1.0, None)
+    capi.call("vvh_fill_normal", y, outd, M * N, seed + 3, 0.0, 1.0, None)
+    return ar, [Linear(ar, tmp_w, M, N, K, bias, res, seed + 5 * r, act, outd, xy=(x, y)) for r in range(n)]
+
+
+def timed_rotation(ev, lins, steps, stream=None):
+    """ms per call over `steps` calls that rotate through `lins`, after one
+    warm-up pass over all of them (so no timed call finds its operands in
+    the MALL from the set-up writes)."""
+    for l in lins:
+        l.run(stream)
+    n = len(lins)
+    return timed(ev, lambda i: lins[(i + 1) % n].run(stream), steps, stream)
+
+
 class Linear:
     """One quantized projection resident in HBM with its input/output rows."""
 
-    def __init__(self, arena, tmp_w, M, N, K, bias, residual, seed, act=F16, outd=F16):
+    def __init__(self, arena, tmp_w, M, N, K, bias, residual, seed, act=F16, outd=F16, xy=None):
+        """xy: (x, y) device pointers to share instead of rows of its own."""
         self.M, self.N, self.K, self.has_bias, self.has_res = M, N, K, bias, residual
         self.act, self.outd = act, outd
         ab, ob = (2 if act == F16 else 4), (2 if outd == F16 else 4)
         self.w = arena.take(N * K)
         self.s = arena.take(4 * N)
         self.b = arena.take(4 * N) if bias else None
-        self.x = arena.take(M * K * ab)
-        self.y = arena.take(M * N * ob)
         capi.call("vvh_fill_normal", tmp_w, F32, N * K, seed, 0.0, 0.02, None)
         capi.call("vvh_quantize_per_channel", tmp_w, N, K, self.w, self.s, None)
         if bias:
             capi.call("vvh_fill_normal", self.b, F32, N, seed + 1, 0.0, 0.01, None)
-        capi.call("vvh_fill_normal", self.x, act, M * K, seed + 2, 0.0, 1.0, None)
-        capi.call("vvh_fill_normal", self.y, outd, M * N, seed + 3, 0.0, 1.0, None)
+        if xy is None:
+            self.x = arena.take(M * K * ab)
+            self.y = arena.take(M * N * ob)
+            capi.call("vvh_fill_normal", self.x, act, M * K, seed + 2, 0.0, 1.0, None)
+            capi.call("vvh_fill_normal", self.y, outd, M * N, seed + 3, 0.0, 1.0, None)
+        else:
+            self.x, self.y = xy
         self.bytes = algo_bytes(M, N, K, bias, residual, ab, ob)
         self.flops = 2 * M * N * K
 
@@ -405,19 +438,16 @@ def kernel_name(M, N, K, outd=F16):
 
 def prefill_main(args, ev, name):
     """configs[3] gate/up GEMM alone (M = --prefill-m, N = 4864, K = 896, fp16
-    in and out): one JSON line in TFLOP/s against the fp16 MFMA peak.  Two
-    weight replicas alternate; the kernel runs on the null stream, where the
-    HIP events are recorded."""
+    in and out): one JSON line in TFLOP/s against the fp16 MFMA peak.
+    Replicas of the weights rotate (>= 1 GiB, see rotation()); the kernel
+    runs on the null stream, where the HIP events are recorded."""
     M, N, K = args.prefill_m, QWEN05["inter"], QWEN05["hidden"]
     tmp_w = capi.DevBuf(N * K * 4)
-    reps = []
-    for r in range(2):
-        ar = Arena(arena_size(Linear.sizes(M, N, K, False)))
-        reps.append((ar, Linear(ar, tmp_w.ptr, M, N, K, False, False, 900 + r)))
+    _ar, lins = rotation(tmp_w.ptr, M, N, K, False, False, 900)
     for i in range(args.warmup):
-        reps[i % 2][1].run()
-    ms = timed(ev, lambda i: reps[i % 2][1].run(), args.steps)
-    tf = reps[0][1].flops / (ms * 1e-3) / 1e12
+        lins[i % len(lins)].run()
+    ms = timed_rotation(ev, lins, args.steps)
+    tf = lins[0].flops / (ms * 1e-3) / 1e12
     kern = kernel_name(M, N, K)
     print(f"[bench] {name}: prefill gate/up M={M} {ms * 1e3:.2f} us, {tf:.0f} TFLOP/s ({kern})",
           file=sys.stderr, flush=True)
@@ -428,7 +458,8 @@ def prefill_main(args, ev, name):
         "dtype": "int8 weights x f16 activations, f32 accumulate",
         "data": "synthetic (seeded N(0,0.02) fp32 weights quantized per channel on device; N(0,1) fp16 activations)",
         "config": {"workload": f"configs[3]: prefill gate/up GEMM, M={M}, N={N}, K={K}, fp16 out",
-                   "M": M, "N": N, "K": K, "flops_per_step": reps[0][1].flops, "parallelism": "single GPU"},
+                   "M": M, "N": N, "K": K, "flops_per_step": lins[0].flops, "replicas_rotated": len(lins),
+                   "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "kernel": kern, "achieved": round(tf, 2), "peak": MFMA_F16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None},
         "cpu_baseline": None}), flush=True)
@@ -570,18 +601,14 @@ def extras(ev, sets, projs, tmp_w, args):
 
     # (3) LM head GEMV, configs[2]: K=896, N=151936, fp16 act, fp32 logits
     N, K = 151936, 896
-    heads = []
-    for r in range(3):
-        ar = Arena(arena_size(Linear.sizes(1, N, K, False, F16, F32)))
-        heads.append((ar, Linear(ar, tmp_w, 1, N, K, False, False, 777 + r, F16, F32)))
-    for i in range(6):
-        heads[i % 3][1].run()
-    us = timed(ev, lambda i: heads[i % 3][1].run(), 60) * 1e3
-    b = heads[0][1].bytes
-    out["lm_head"] = {"N": N, "K": K, "us": round(us, 2), "GBps": round(b / (us * 1e-6) / 1e9, 1),
+    _ar, heads = rotation(tmp_w, 1, N, K, False, False, 777, F16, F32)
+    us = timed_rotation(ev, heads, 60) * 1e3
+    b = heads[0].bytes
+    out["lm_head"] = {"N": N, "K": K, "replicas_rotated": len(heads), "us": round(us, 2),
+                      "GBps": round(b / (us * 1e-6) / 1e9, 1),
                       "hbm_frac": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                       "kernel": capi.kernel_choice(1, N, K, F16, F32)}
-    del heads
+    del heads, _ar
     print(f"[bench] lm head {us:.1f} us", file=sys.stderr, flush=True)
 
     # (4) prefill GEMM, configs[3]
@@ -589,14 +616,10 @@ def extras(ev, sets, projs, tmp_w, args):
     for M in (128, 512, 2048):
         for name, N, K, res in (("gate_up", QWEN05["inter"], QWEN05["hidden"], False),
                                 ("down", QWEN05["hidden"], QWEN05["inter"], True)):
-            reps = []
-            for r in range(2):
-                ar = Arena(arena_size(Linear.sizes(M, N, K, False)))
-                reps.append((ar, Linear(ar, tmp_w, M, N, K, False, res, 900 + r)))
-            for i in range(4):
-                reps[i % 2][1].run()
-            us = timed(ev, lambda i: reps[i % 2][1].run(), 40) * 1e3
-            tf = reps[0][1].flops / (us * 1e-6) / 1e12
+            _ar, reps = rotation(tmp_w, M, N, K, False, res, 900)
+            us = timed_rotation(ev, reps, 40) * 1e3
+            tf = reps[0].flops / (us * 1e-6) / 1e12
+            del reps, _ar
             gemm[f"{name}_M{M}"] = {"M": M, "N": N, "K": K, "us": round(us, 2), "TFLOPS": round(tf, 1),
                                     "mfma_frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
                                     "kernel": kernel_name(M, N, K)}
@@ -607,14 +630,10 @@ def extras(ev, sets, projs, tmp_w, args):
     sweep = {}
     for M in (1, 4, 16, 64, 256):
         for name, N, K in (("qo", 1536, 1536), ("kv", 256, 1536), ("gate_up", 8960, 1536), ("down", 1536, 8960)):
-            reps = []
-            for r in range(2):
-                ar = Arena(arena_size(Linear.sizes(M, N, K, False)))
-                reps.append((ar, Linear(ar, tmp_w, M, N, K, False, False, 1300 + r)))
-            for i in range(4):
-                reps[i % 2][1].run()
-            us = timed(ev, lambda i: reps[i % 2][1].run(), 30) * 1e3
-            l = reps[0][1]
+            _ar, reps = rotation(tmp_w, M, N, K, False, False, 1300)
+            us = timed_rotation(ev, reps, 30) * 1e3
+            l = reps[0]
+            del reps, _ar
             sweep[f"{name}_M{M}"] = {"us": round(us, 2), "GBps": round(l.bytes / (us * 1e-6) / 1e9, 1),
                                      "TFLOPS": round(l.flops / (us * 1e-6) / 1e12, 2),
                                      "kernel": kernel_name(M, N, K)}
