@@ -96,6 +96,24 @@ def test_validation_before_device_use():
     assert st("vvh_weight_ingest", P, capi.BF16, None, 1 << 40, 1 << 40, sc, ctypes.byref(h)) == 1
     assert st("vvh_weight_ingest", P, capi.BF16, None, 4, 4, sc, None) == 1
     assert st("vvh_weight_ingest", P, capi.BF16, None, 4, 4, sc, ctypes.byref(h)) == 5  # before vvh_init
+    # input stages of a decode linear: refused shapes and arguments, before any device use
+    def lin_in(M, K, act, op, w):
+        return st("vvh_linear_q8_dev_in", P, P, P, P, None, None, M, 16, K, act, act, op, w, 1e-6, None)
+    assert lin_in(1, 896, capi.F16, 3, P) == 1                    # unknown stage
+    assert lin_in(1, 896, capi.F16, capi.IN_RMS_NORM, None) == 1  # RMSNorm without weights
+    assert lin_in(1, 896, capi.F16, capi.IN_RMS_NORM, P + 4) == 1  # misaligned weights
+    assert lin_in(5, 896, capi.F16, capi.IN_RMS_NORM, P) == 7     # M > 4
+    assert lin_in(1, 896, capi.F32, capi.IN_SILU_MUL, None) == 7  # fp32 activations
+    assert lin_in(1, 888, capi.F16, capi.IN_SILU_MUL, None) == 7  # K % 16 != 0
+    assert lin_in(4, 20000, capi.F16, capi.IN_SILU_MUL, None) == 7  # rows beyond the LDS
+    assert lin_in(1, 896, capi.F16, capi.IN_RMS_NORM, P) == 5     # valid, before vvh_init
+    assert lin_in(1, 896, capi.F16, capi.IN_NONE, None) == 5      # no stage: vvh_linear_q8_dev
+    # RoPE + KV append
+    assert st("vvh_rope_append", P, P, P, P, P, 1, 14, 2, 63, 0, 1e4, capi.F16, None) == 1  # odd head_dim
+    assert st("vvh_rope_append", P, P, P, None, P, 1, 14, 2, 64, 0, 1e4, capi.F16, None) == 1  # no key cache
+    assert st("vvh_rope_append", P, P, P, P, P, 1, 14, 2, 64, 0, 1e4, 9, None) == 1  # bad dtype
+    assert st("vvh_rope_append", P, P, P, P, P, 1, 14, 2, 64, 0, 1e4, capi.F16, None) == 5
+    assert st("vvh_plan_set_input_op", 999, capi.IN_RMS_NORM, P, 1e-6) == 5
     stats = capi.PoolStats()
     assert st("vvh_pool_get_stats", ctypes.byref(stats)) == 0 and stats.bytes_in_use == 0
 
