@@ -181,11 +181,11 @@ def test_stream_kernel(gpu, oracle, M, N, K, outd):
 @pytest.mark.parametrize("M", [1, 2, 3, 4])
 @pytest.mark.parametrize("outd", [F16, F32])
 @pytest.mark.parametrize("N,K", [(1, 16), (17, 48), (128, 896), (896, 4864), (300, 1040), (4099, 592),
-                                 (64, 20480), (33, 8960)])
+                                 (64, 20480), (33, 8960), (48, 2048)])
 def test_dot_kernel(gpu, oracle, M, N, K, outd):
     """VALU dot-product decode (M <= 4): K tails (48, 592, 1040), a single
-    16-code step, N % 16 != 0, activations too large for LDS (K = 20480,
-    and K = 8960 at M = 4) and the ksplit reduction (few tiles)."""
+    16-code step, N % 16 != 0, activations too large for LDS (K = 20480 at
+    M >= 2) and the ksplit reduction (few tiles)."""
     run_case(oracle, M, N, K, F16, outd, bias=bool(N % 2), res=["sep", "inplace", None][(N + K + M) % 3],
              kernel=capi.KERNEL_DOT, seed=13 * N + K + M)
 
