@@ -101,6 +101,47 @@ __device__ __forceinline__ float silu_mul_ref(float g, float u)
     return r;
 }
 
+// Butterfly steps within rows of 16 lanes as DPP moves (one VALU op, no
+// LDS-pipeline round trip like __shfl_xor): quad_perm [1,0,3,2] and
+// [2,3,0,1] exchange with lanes l^1 and l^2; row_half_mirror (lane i <-> 7-i
+// of each 8) and row_mirror (i <-> 15-i of each 16) reach the other half
+// once the smaller groups already hold equal values.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+// Sum over aligned groups of L lanes (L = 1, 2, 4, 8 or 16, wave-uniform);
+// every lane of a group gets the group's sum.  All lanes must be active.
+__device__ __forceinline__ float group_sum(float v, int L)
+{
+    if (L >= 2) v += dpp_mov<0xB1>(v);
+    if (L >= 4) v += dpp_mov<0x4E>(v);
+    if (L >= 8) v += dpp_mov<0x141>(v);
+    if (L >= 16) v += dpp_mov<0x140>(v);
+    return v;
+}
+// Whole-wave max / sum (all 64 lanes active): the DPP steps within rows of
+// 16, then two shuffles across rows.
+__device__ __forceinline__ float wave_max(float v)
+{
+    v = fmaxf(v, dpp_mov<0xB1>(v));
+    v = fmaxf(v, dpp_mov<0x4E>(v));
+    v = fmaxf(v, dpp_mov<0x141>(v));
+    v = fmaxf(v, dpp_mov<0x140>(v));
+    v = fmaxf(v, __shfl_xor(v, 16));
+    return fmaxf(v, __shfl_xor(v, 32));
+}
+__device__ __forceinline__ float wave_sum(float v)
+{
+    v += dpp_mov<0xB1>(v);
+    v += dpp_mov<0x4E>(v);
+    v += dpp_mov<0x141>(v);
+    v += dpp_mov<0x140>(v);
+    v += __shfl_xor(v, 16);
+    return v + __shfl_xor(v, 32);
+}
+
 // Pointers read from memory (plan tables) are generic to the compiler, which
 // then emits flat loads; those count in lgkmcnt as well as vmcnt, so every
 // wait on a scalar load would also drain the weight stream.  Kernels that

@@ -364,7 +364,9 @@ __device__ __forceinline__ void load8(const float* p, float f[8])
     }
 }
 
-template <typename T>
+// ONE: the block's span is a single sub-chunk (per_block <= C), so there is
+// nothing to prefetch.
+template <typename T, bool ONE>
 __global__ __launch_bounds__(256) void k_attention_decode(T* __restrict__ out, const T* __restrict__ q,
                                                           const T* __restrict__ k, const T* __restrict__ v,
                                                           int64_t len, int32_t H, int32_t KVH, int32_t D, float scale,
@@ -383,6 +385,20 @@ __global__ __launch_bounds__(256) void k_attention_decode(T* __restrict__ out, c
     const int64_t ke = kb + per_block < len ? kb + per_block : len;
     const int64_t kvs = (int64_t)KVH * D;
     const int GD = G * D;
+    // this thread's K/V rows (key t0 + j, dims d0 .. d0 + 7) of a sub-chunk,
+    // loaded unconditionally from a clamped row; keys past the span and dims
+    // past D are zeroed where the values are used, so the loads in flight
+    // never depend on the key and the waits stay static
+    const int dc = dims_on ? d0 : D - 8;
+    auto load_kv = [&](int64_t t0, float (&kf)[8], float (&vf)[8]) {
+        const int64_t t = t0 + j < ke ? t0 + j : ke - 1;
+        load8(k + t * kvs + (int64_t)g * D + dc, kf);
+        load8(v + t * kvs + (int64_t)g * D + dc, vf);
+    };
+    // the first sub-chunk's rows are requested before q is staged, so the
+    // two round trips overlap
+    float kf[8], vf[8];
+    load_kv(kb, kf, vf);
 
     for (int i = tid; i < GD; i += 256) qs[i] = ldf(q, (int64_t)g * GD + i);
     float acc[kAttnOutPerThread];
@@ -397,13 +413,14 @@ __global__ __launch_bounds__(256) void k_attention_decode(T* __restrict__ out, c
     for (int64_t t0 = kb; t0 < ke; t0 += C) {
         const int64_t t = t0 + j;
         const bool key_on = t < ke;
-        float kf[8], vf[8];
-        if (key_on && dims_on) {
-            load8(k + t * kvs + (int64_t)g * D + d0, kf);
-            load8(v + t * kvs + (int64_t)g * D + d0, vf);
-        } else {
+        // the next sub-chunk's rows, one sub-chunk ahead
+        float kn[8], vn[8];
+        if constexpr (!ONE) load_kv(t0 + C, kn, vn);
+        const bool on = key_on && dims_on;
 #pragma unroll
-            for (int e = 0; e < 8; e++) kf[e] = vf[e] = 0.0f;
+        for (int e = 0; e < 8; e++) {
+            kf[e] = on ? kf[e] : 0.0f;
+            vf[e] = on ? vf[e] : 0.0f;
         }
         float sc[kAttnMaxG];
 #pragma unroll
@@ -416,7 +433,7 @@ __global__ __launch_bounds__(256) void k_attention_decode(T* __restrict__ out, c
 #pragma unroll
                     for (int e = 0; e < 4; e++) a += q0[e] * kf[e] + q1[e] * kf[4 + e];
                 }
-                for (int off = L >> 1; off > 0; off >>= 1) a += __shfl_xor(a, off);
+                a = group_sum(a, L);
             }
             sc[h] = a;
         }
@@ -434,7 +451,7 @@ __global__ __launch_bounds__(256) void k_attention_decode(T* __restrict__ out, c
         for (int h = wv; h < G; h += 4) {
             float mc = -INFINITY;
             for (int i = lane; i < C; i += 64) mc = fmaxf(mc, ps[h * C + i]);
-            for (int off = 32; off > 0; off >>= 1) mc = fmaxf(mc, __shfl_xor(mc, off));
+            mc = wave_max(mc);
             const float mo = m_s[h], mn = fmaxf(mo, mc);  // mc is finite: the sub-chunk has a key
             float sum = 0.0f;
             for (int i = lane; i < C; i += 64) {
@@ -442,7 +459,7 @@ __global__ __launch_bounds__(256) void k_attention_decode(T* __restrict__ out, c
                 ps[h * C + i] = e;
                 sum += e;
             }
-            for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+            sum = wave_sum(sum);
             if (lane == 0) {
                 const float cr = expf(mo - mn);  // 0 on the first sub-chunk
                 corr_s[h] = cr;
@@ -459,6 +476,13 @@ __global__ __launch_bounds__(256) void k_attention_decode(T* __restrict__ out, c
                 float a = acc[i] * corr_s[h];
                 for (int jj = 0; jj < C; jj++) a += ps[h * C + jj] * vs[jj * D + d];
                 acc[i] = a;
+            }
+        }
+        if constexpr (!ONE) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                kf[e] = kn[e];
+                vf[e] = vn[e];
             }
         }
     }
@@ -482,41 +506,42 @@ __global__ __launch_bounds__(256) void k_attention_decode(T* __restrict__ out, c
 }
 
 // out[h][d] = sum_c e^(m_c - M) o_c[d] / sum_c e^(m_c - M) l_c, M = max_c m_c.
-// Block per head; thread (s, d) sums the blocks c = s, s + S, ... (S = 256 / D).
+// Block per head, one pass over the partials: thread (s, d) merges the
+// blocks c = s, s + S, ... (S = 256 / D) into a running maximum and sums
+// rescaled to it (the online-softmax merge); the S groups then merge the
+// same way through LDS.
 template <typename T>
 __global__ __launch_bounds__(256) void k_attention_combine(T* __restrict__ out, const float* __restrict__ ws,
                                                            int32_t blocks, int32_t H, int32_t D)
 {
-    __shared__ float red[256], den[256];
+    __shared__ float sm[256], sn[256], sd[256];
     const int h = blockIdx.x, tid = threadIdx.x;
     const int S = 256 / D, s = tid / D, d = tid - s * D;
-    float M = -INFINITY;
-    for (int c = tid; c < blocks; c += 256) M = fmaxf(M, ws[((int64_t)c * H + h) * (D + 2)]);
-    red[tid] = M;
-    __syncthreads();
-    for (int w = 128; w > 0; w >>= 1) {
-        if (tid < w) red[tid] = fmaxf(red[tid], red[tid + w]);
-        __syncthreads();
-    }
-    M = red[0];
-    __syncthreads();
-    float num = 0.0f, dn = 0.0f;
+    float M = -INFINITY, num = 0.0f, den = 0.0f;
     if (s < S) {
+#pragma unroll 4
         for (int c = s; c < blocks; c += S) {
             const float* w = ws + ((int64_t)c * H + h) * (D + 2);
-            const float f = expf(w[0] - M);
-            num += f * w[2 + d];
-            dn += f * w[1];
+            const float m = w[0], l = w[1], o = w[2 + d];
+            const float mn = fmaxf(M, m);          // m is finite: every block has a key
+            const float a = expf(M - mn), b = expf(m - mn);  // a = 0 on the first block
+            num = num * a + o * b;
+            den = den * a + l * b;
+            M = mn;
         }
     }
-    red[tid] = num;
-    den[tid] = dn;
+    sm[tid] = M;
+    sn[tid] = num;
+    sd[tid] = den;
     __syncthreads();
     if (tid < D) {
+        float mt = -INFINITY;
+        for (int g = 0; g < S; g++) mt = fmaxf(mt, sm[g * D + tid]);
         float a = 0.0f, b = 0.0f;
-        for (int ss = 0; ss < S; ss++) {
-            a += red[ss * D + tid];
-            b += den[ss * D + tid];
+        for (int g = 0; g < S; g++) {
+            const float f = expf(sm[g * D + tid] - mt);  // 0 for a group without blocks
+            a += sn[g * D + tid] * f;
+            b += sd[g * D + tid] * f;
         }
         stf(out, (int64_t)h * D + tid, a / b);
     }
@@ -554,17 +579,27 @@ int launch_attention_decode(void* out, const void* q, const void* k, const void*
     const int64_t per = attn_per_block(len, KVH, D);
     const int64_t nb = (len + per - 1) / per;
     const dim3 grid((unsigned)KVH, (unsigned)nb);
+    const bool one = per <= 256 / attn_lanes((int)D);  // one sub-chunk per block
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (dtype == VVH_F16) {
-        hipLaunchKernelGGL(k_attention_decode<f16>, grid, dim3(256), 0, s, (f16*)out, (const f16*)q, (const f16*)k,
-                           (const f16*)v, len, (int32_t)H, (int32_t)KVH, (int32_t)D, scale, per, ws);
+        if (one)
+            hipLaunchKernelGGL((k_attention_decode<f16, true>), grid, dim3(256), 0, s, (f16*)out, (const f16*)q,
+                               (const f16*)k, (const f16*)v, len, (int32_t)H, (int32_t)KVH, (int32_t)D, scale, per, ws);
+        else
+            hipLaunchKernelGGL((k_attention_decode<f16, false>), grid, dim3(256), 0, s, (f16*)out, (const f16*)q,
+                               (const f16*)k, (const f16*)v, len, (int32_t)H, (int32_t)KVH, (int32_t)D, scale, per, ws);
         if (nb > 1)
             hipLaunchKernelGGL(k_attention_combine<f16>, dim3((unsigned)H), dim3(256), 0, s, (f16*)out, ws,
                                (int32_t)nb, (int32_t)H, (int32_t)D);
     } else {
-        hipLaunchKernelGGL(k_attention_decode<float>, grid, dim3(256), 0, s, (float*)out, (const float*)q,
-                           (const float*)k, (const float*)v, len, (int32_t)H, (int32_t)KVH, (int32_t)D, scale, per,
-                           ws);
+        if (one)
+            hipLaunchKernelGGL((k_attention_decode<float, true>), grid, dim3(256), 0, s, (float*)out,
+                               (const float*)q, (const float*)k, (const float*)v, len, (int32_t)H, (int32_t)KVH,
+                               (int32_t)D, scale, per, ws);
+        else
+            hipLaunchKernelGGL((k_attention_decode<float, false>), grid, dim3(256), 0, s, (float*)out,
+                               (const float*)q, (const float*)k, (const float*)v, len, (int32_t)H, (int32_t)KVH,
+                               (int32_t)D, scale, per, ws);
         if (nb > 1)
             hipLaunchKernelGGL(k_attention_combine<float>, dim3((unsigned)H), dim3(256), 0, s, (float*)out, ws,
                                (int32_t)nb, (int32_t)H, (int32_t)D);
