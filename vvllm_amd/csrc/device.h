@@ -111,35 +111,28 @@ __device__ __forceinline__ float dpp_mov(float v)
 {
     return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
-// Sum over aligned groups of L lanes (L = 1, 2, 4, 8 or 16, wave-uniform);
-// every lane of a group gets the group's sum.  All lanes must be active.
+// Sum / max over aligned groups of L lanes (L = 1, 2, 4, ..., 64,
+// wave-uniform); every lane of a group gets the group's result.  DPP steps
+// within rows of 16, shuffles across rows.  All lanes must be active.
 __device__ __forceinline__ float group_sum(float v, int L)
 {
     if (L >= 2) v += dpp_mov<0xB1>(v);
     if (L >= 4) v += dpp_mov<0x4E>(v);
     if (L >= 8) v += dpp_mov<0x141>(v);
     if (L >= 16) v += dpp_mov<0x140>(v);
+    if (L >= 32) v += __shfl_xor(v, 16);
+    if (L >= 64) v += __shfl_xor(v, 32);
     return v;
 }
-// Whole-wave max / sum (all 64 lanes active): the DPP steps within rows of
-// 16, then two shuffles across rows.
-__device__ __forceinline__ float wave_max(float v)
+__device__ __forceinline__ float group_max(float v, int L)
 {
-    v = fmaxf(v, dpp_mov<0xB1>(v));
-    v = fmaxf(v, dpp_mov<0x4E>(v));
-    v = fmaxf(v, dpp_mov<0x141>(v));
-    v = fmaxf(v, dpp_mov<0x140>(v));
-    v = fmaxf(v, __shfl_xor(v, 16));
-    return fmaxf(v, __shfl_xor(v, 32));
-}
-__device__ __forceinline__ float wave_sum(float v)
-{
-    v += dpp_mov<0xB1>(v);
-    v += dpp_mov<0x4E>(v);
-    v += dpp_mov<0x141>(v);
-    v += dpp_mov<0x140>(v);
-    v += __shfl_xor(v, 16);
-    return v + __shfl_xor(v, 32);
+    if (L >= 2) v = fmaxf(v, dpp_mov<0xB1>(v));
+    if (L >= 4) v = fmaxf(v, dpp_mov<0x4E>(v));
+    if (L >= 8) v = fmaxf(v, dpp_mov<0x141>(v));
+    if (L >= 16) v = fmaxf(v, dpp_mov<0x140>(v));
+    if (L >= 32) v = fmaxf(v, __shfl_xor(v, 16));
+    if (L >= 64) v = fmaxf(v, __shfl_xor(v, 32));
+    return v;
 }
 
 // Pointers read from memory (plan tables) are generic to the compiler, which

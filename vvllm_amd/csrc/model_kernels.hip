@@ -328,7 +328,8 @@ __global__ __launch_bounds__(256) void k_attention(T* __restrict__ out, const T*
 // Per sub-chunk:
 //   scores   lane-partial dots for the G heads, xor-reduced over the L lanes,
 //            into LDS (scores [G][C]); the V rows go to LDS as fp32;
-//   softmax  per head (wave w takes heads w, w + 4, ...): running max m,
+//   softmax  per head (min(C, 64) lanes per head, so a wave serves 64 / C
+//            heads at once when C < 64): running max m,
 //            p = exp(s - m), running sum l = l * exp(m_old - m) + sum p;
 //   P.V      thread (h, d) pairs: acc = acc * exp(m_old - m) + sum_j p_j v_j[d].
 // One block per kv head writes out = acc / l; otherwise the block writes
@@ -372,7 +373,7 @@ __global__ __launch_bounds__(256) void k_attention_decode(T* __restrict__ out, c
                                                           int64_t len, int32_t H, int32_t KVH, int32_t D, float scale,
                                                           int64_t per_block, float* __restrict__ ws)
 {
-    __shared__ float ps[kAttnMaxG * 256];  // [h][j]: scores, then probabilities (G * C <= 16 * 256)
+    __shared__ __align__(16) float ps[kAttnMaxG * 256];  // [h][j]: scores, then probabilities (G * C <= 16 * 256)
     __shared__ __align__(16) float vs[256 * 8];  // [j][d]: the sub-chunk's V rows (C * D <= 256 * 8)
     __shared__ __align__(16) float qs[kAttnMaxG * kAttnMaxD];  // [h][d]: the G query rows
     __shared__ float m_s[kAttnMaxG], l_s[kAttnMaxG], corr_s[kAttnMaxG];
@@ -381,6 +382,7 @@ __global__ __launch_bounds__(256) void k_attention_decode(T* __restrict__ out, c
     const int L = attn_lanes(D), C = 256 / L;
     const int j = tid / L, d0 = (tid % L) * 8;
     const bool dims_on = d0 < D;
+    const int CL = C < 64 ? C : 64, R = 64 / CL, hl = lane / CL, il = lane - hl * CL;
     const int64_t kb = (int64_t)blockIdx.y * per_block;
     const int64_t ke = kb + per_block < len ? kb + per_block : len;
     const int64_t kvs = (int64_t)KVH * D;
@@ -448,19 +450,24 @@ __global__ __launch_bounds__(256) void k_attention_decode(T* __restrict__ out, c
             for (int e = 0; e < 8; e++) vs[j * D + d0 + e] = vf[e];
         }
         __syncthreads();
-        for (int h = wv; h < G; h += 4) {
+        // R heads per wave at once, CL lanes per head
+        for (int h0 = wv * R; h0 < G; h0 += 4 * R) {
+            const int h = h0 + hl;
+            const bool hon = h < G;
             float mc = -INFINITY;
-            for (int i = lane; i < C; i += 64) mc = fmaxf(mc, ps[h * C + i]);
-            mc = wave_max(mc);
-            const float mo = m_s[h], mn = fmaxf(mo, mc);  // mc is finite: the sub-chunk has a key
+            if (hon)
+                for (int i = il; i < C; i += CL) mc = fmaxf(mc, ps[h * C + i]);
+            mc = group_max(mc, CL);
+            const float mo = hon ? m_s[h] : 0.0f, mn = fmaxf(mo, mc);  // mc is finite: the sub-chunk has a key
             float sum = 0.0f;
-            for (int i = lane; i < C; i += 64) {
-                const float e = expf(ps[h * C + i] - mn);
-                ps[h * C + i] = e;
-                sum += e;
-            }
-            sum = wave_sum(sum);
-            if (lane == 0) {
+            if (hon)
+                for (int i = il; i < C; i += CL) {
+                    const float e = expf(ps[h * C + i] - mn);
+                    ps[h * C + i] = e;
+                    sum += e;
+                }
+            sum = group_sum(sum, CL);
+            if (hon && il == 0) {
                 const float cr = expf(mo - mn);  // 0 on the first sub-chunk
                 corr_s[h] = cr;
                 l_s[h] = l_s[h] * cr + sum;
