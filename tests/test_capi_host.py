@@ -3,7 +3,7 @@
 * libvvllm_hip.so loads and exports every VVH_API function that
   include/vvllm_hip.h declares, and the ctypes table binds exactly those;
 * argument validation happens on the host and returns status codes (the
-  reference has none, SURVEY: "The hot path validates nothing");
+  reference's linear_q8 path checks no arguments);
 * the kernel-family choice of the dispatcher;
 * the caching allocator logic (tests/cpp/test_pool.cc, with a fake backing
   allocator, built with ASan/UBSan);

@@ -1,5 +1,5 @@
-"""HIP graph capture of the int8 linear path (launch-overhead
-removal by graph capture of the decode step).
+"""HIP graph capture of the int8 linear path (launch-overhead removal by
+graph capture of the decode step).
 
 A decode plan, a several-row decode call, a GEMM and a split-K GEMM are
 issued on one stream, captured into a graph and replayed several times, with
