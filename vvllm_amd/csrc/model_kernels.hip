@@ -514,16 +514,16 @@ __global__ __launch_bounds__(256) void k_attention_decode(T* __restrict__ out, c
 
 // out[h][d] = sum_c e^(m_c - M) o_c[d] / sum_c e^(m_c - M) l_c, M = max_c m_c.
 // Block per head, one pass over the partials: thread (s, d) merges the
-// blocks c = s, s + S, ... (S = 256 / D) into a running maximum and sums
+// blocks c = s, s + S, ... (S = blockDim.x / D) into a running maximum and sums
 // rescaled to it (the online-softmax merge); the S groups then merge the
 // same way through LDS.
 template <typename T>
-__global__ __launch_bounds__(256) void k_attention_combine(T* __restrict__ out, const float* __restrict__ ws,
-                                                           int32_t blocks, int32_t H, int32_t D)
+__global__ __launch_bounds__(1024) void k_attention_combine(T* __restrict__ out, const float* __restrict__ ws,
+                                                            int32_t blocks, int32_t H, int32_t D)
 {
-    __shared__ float sm[256], sn[256], sd[256];
+    __shared__ float sm[1024], sn[1024], sd[1024];
     const int h = blockIdx.x, tid = threadIdx.x;
-    const int S = 256 / D, s = tid / D, d = tid - s * D;
+    const int S = (int)blockDim.x / D, s = tid / D, d = tid - s * D;
     float M = -INFINITY, num = 0.0f, den = 0.0f;
     if (s < S) {
 #pragma unroll 4
@@ -580,6 +580,16 @@ int64_t attention_decode_ws_floats(int64_t len, int64_t H, int64_t KVH, int64_t 
     return nb > 1 ? nb * H * (D + 2) : 0;
 }
 
+// Combine block: D x S threads, S (a power of two, 1 <= S <= 1024 / D) the
+// smallest that leaves each thread at most 4 partials, so long spans fold in
+// parallel instead of in one long chain per thread.
+static unsigned combine_threads(int64_t nb, int64_t D)
+{
+    int64_t S = 1;
+    while (S * 4 < nb && S * 2 * D <= 1024) S *= 2;
+    return (unsigned)(S * D);
+}
+
 int launch_attention_decode(void* out, const void* q, const void* k, const void* v, int64_t len, int64_t H,
                             int64_t KVH, int64_t D, float scale, float* ws, int dtype, void* stream)
 {
@@ -596,7 +606,7 @@ int launch_attention_decode(void* out, const void* q, const void* k, const void*
             hipLaunchKernelGGL((k_attention_decode<f16, false>), grid, dim3(256), 0, s, (f16*)out, (const f16*)q,
                                (const f16*)k, (const f16*)v, len, (int32_t)H, (int32_t)KVH, (int32_t)D, scale, per, ws);
         if (nb > 1)
-            hipLaunchKernelGGL(k_attention_combine<f16>, dim3((unsigned)H), dim3(256), 0, s, (f16*)out, ws,
+            hipLaunchKernelGGL(k_attention_combine<f16>, dim3((unsigned)H), dim3(combine_threads(nb, D)), 0, s, (f16*)out, ws,
                                (int32_t)nb, (int32_t)H, (int32_t)D);
     } else {
         if (one)
@@ -608,7 +618,7 @@ int launch_attention_decode(void* out, const void* q, const void* k, const void*
                                (const float*)q, (const float*)k, (const float*)v, len, (int32_t)H, (int32_t)KVH,
                                (int32_t)D, scale, per, ws);
         if (nb > 1)
-            hipLaunchKernelGGL(k_attention_combine<float>, dim3((unsigned)H), dim3(256), 0, s, (float*)out, ws,
+            hipLaunchKernelGGL(k_attention_combine<float>, dim3((unsigned)H), dim3(combine_threads(nb, D)), 0, s, (float*)out, ws,
                                (int32_t)nb, (int32_t)H, (int32_t)D);
     }
     return (int)hipGetLastError();
