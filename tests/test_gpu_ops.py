@@ -126,12 +126,13 @@ def test_embedding(gpu, d):
 # n_q = 1 rows with head_dim % 8 == 0, head_dim <= 128 and <= 16 query heads
 # per kv head take the split decode kernel (one chunk, two chunks with one key
 # in the second, many chunks, a span beyond the general kernel's limit,
-# blocks of several sub-chunks with a one-key tail);
+# blocks of several sub-chunks with a one-key tail, and head dims 8 to 32,
+# whose merge blocks fold up to 64 groups of partials);
 # the rest take the general kernel.
 ATT = [(1, 1, 14, 2, 64), (1, 100, 14, 2, 64), (1, 256, 14, 2, 64), (1, 257, 14, 2, 64), (1, 4096, 14, 2, 64),
        (1, 1000, 32, 8, 128), (1, 700, 16, 1, 64), (1, 513, 12, 12, 40), (1, 40000, 2, 1, 64), (1, 20001, 4, 1, 64),
        (4, 10, 12, 2, 128), (3, 5, 4, 4, 32), (1, 16000, 2, 1, 64), (2, 7, 16, 2, 256), (1, 300, 4, 2, 256),
-       (1, 300, 4, 2, 36)]
+       (1, 300, 4, 2, 36), (1, 3000, 8, 2, 16), (1, 30000, 4, 1, 8), (1, 1200, 16, 4, 32)]
 
 
 @pytest.mark.parametrize("d", [F32, F16])
