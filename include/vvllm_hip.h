@@ -20,12 +20,14 @@
  *     Launches are asynchronous on it; errors of the launch itself are
  *     reported, errors of the kernel's execution surface at the next
  *     synchronising call.
- *   - Split-K GEMMs and multi-chunk decode attention use a per-stream
- *     workspace that grows on demand (hipMalloc).  Under HIP graph capture
- *     it cannot grow: run the same calls once on that stream before
- *     capturing (the workspace is at least 16 MiB; decode attention needs
- *     at most 512 * (num_heads / num_kv_heads) * (head_dim + 2) * 4 bytes,
- *     4.3 MB, at any span).
+ *   - Split-K GEMMs, multi-chunk decode attention and multi-block sampling
+ *     use a per-stream workspace that grows on demand (hipMalloc, to at
+ *     least twice its size, never below 1 MiB).  Under HIP graph capture it
+ *     cannot grow: run the same calls once on that stream before capturing
+ *     (decode attention needs at most 512 * (num_heads / num_kv_heads) *
+ *     (head_dim + 2) * 4 bytes, 4.3 MB, at any span).  A buffer the
+ *     workspace outgrows is kept, not freed, so graphs captured before the
+ *     growth stay valid; vvh_workspace_release frees them all.
  *   - All calls may be made from one host thread at a time per device
  *     (as the reference, which is single-threaded, README.md:282); the
  *     allocator and registries are internally locked.
@@ -101,6 +103,12 @@ VVH_API int vvh_memcpy_d2d(void* dst, const void* src, size_t bytes);
  * append of a decode step (KVCacheCUDA::append copies synchronously,
  * src/kv_cache/kv_cache_cuda.cc:74-79). */
 VVH_API int vvh_memcpy_d2d_async(void* dst, const void* src, size_t bytes, void* stream);
+
+/* Frees the workspace of `stream` and every buffer it outgrew, after waiting
+ * for the device.  Graphs captured on that stream that use the workspace
+ * must not be replayed afterwards (the next call that needs it allocates a
+ * new one).  No reference counterpart (the reference has no workspace). */
+VVH_API int vvh_workspace_release(void* stream);
 
 /* ---- caching allocator -------------------------------------------------- */
 /* Stream-ordered-free caching allocator behind device_allocate /
@@ -353,6 +361,26 @@ VVH_API int vvh_matmul(void* out, const void* A, const float* dev_B, size_t M, s
 /* Greedy sampling: *dev_index = the first index of the maximum of n fp32
  * logits, as std::max_element (src/sampler/sampler.cc:21-25). */
 VVH_API int vvh_argmax(const float* logits, size_t n, int32_t* dev_index, void* stream);
+/* Samples one index from n logits (dtype VVH_F32 or VVH_F16) into
+ * *dev_index (device memory; nothing is copied to the host).  Replaces
+ * cuda_sample (src/backend/cuda_kernels.h:107-111,
+ * src/backend/cuda_kernels.cu:1322-1349) as SamplerCUDA::sample calls it
+ * (src/sampler/sampler_cuda.cc:13-18), the reference's default decode
+ * sampler (--temperature 0.7, bin/qwen/main.cc:29, :125-126).
+ *   temperature == 0: vvh_argmax (the first index of the maximum).
+ *   temperature  > 0: the Gumbel-max trick of sample_kernel (:1240-1317):
+ *     argmax_i logit_i / temperature - log(-log(u_i)), with u_i the hash
+ *     uniform of gpu_rand(seed, step, i) (:1228-1237), so a given (logits,
+ *     temperature, seed, step) always gives the same index and successive
+ *     steps draw independent samples of softmax(logit / temperature).  As
+ *     there, only noisy values > -1e30 count (NaN never does) and the index
+ *     is 0 if none does; equal noisy values resolve to the lower index.
+ *   top_p is accepted and ignored, as cuda_sample does (:1325).
+ * Unlike the reference (which exits the process on error and returns the
+ * index through a blocking copy), a negative, NaN or infinite temperature is
+ * VVH_ERR_INVALID_ARG and the call is asynchronous on `stream`. */
+VVH_API int vvh_sample(const void* logits, int dtype, size_t n, float temperature, float top_p, uint64_t seed,
+                       int32_t step, int32_t* dev_index, void* stream);
 /* Device copy of a host fp32 array of n elements, as fp32 or converted to
  * fp16 (as_dtype), made on first use and kept (BackendCUDA::cache_weight /
  * cache_weight_as_fp16, backend_cuda.cc:51-95).  Keyed by (host, as_dtype):
@@ -377,10 +405,9 @@ typedef enum vvh_kernel {
 VVH_API int vvh_linear_q8_choice(size_t M, size_t N, size_t K, int act_dtype, int out_dtype);
 /* The GEMM kernel behind VVH_KERNEL_GEMM for an fp16 call of this shape
  * (measurement and reporting; no reference counterpart): returns 3 for
- * k_gemm3 (*tile_n = 128 or 192), 2 for k_gemm2 (only when k_gemm3 is
- * switched off), 1 for k_gemm (K % 64 != 0), or a negative status; *splits
- * > 1 is a split-K launch followed by a reduction kernel.  tile_n and
- * splits may be NULL. */
+ * k_gemm3 (*tile_n = 128 or 192), 1 for k_gemm (K % 64 != 0), or a negative
+ * status; *splits > 1 is a split-K launch followed by a reduction kernel.
+ * tile_n and splits may be NULL. */
 VVH_API int vvh_gemm_variant(size_t M, size_t N, size_t K, int* tile_n, int* splits);
 /* Forces one kernel family for subsequent calls on this process (testing and
  * measurement); VVH_KERNEL_AUTO restores the size-based choice.  A forced

@@ -282,3 +282,61 @@ void orc_causal_attention(float* out, const float* q, size_t q_idx, const float*
     }
     free(scores);
 }
+
+/* ---- sampling ----------------------------------------------------------
+ * SamplerCPU::sample's greedy branch (src/sampler/sampler.cc:21-25) and the
+ * device sampler SamplerCUDA::sample -> cuda_sample
+ * (src/sampler/sampler_cuda.cc:13-18, src/backend/cuda_kernels.cu:1228-1349). */
+
+/* gpu_rand's hash (cuda_kernels.cu:1230-1235): the seed xor a Weyl step of
+ * (step, idx), then the splitmix64 finaliser. */
+uint64_t orc_sample_hash(uint64_t seed, int32_t step, int32_t idx)
+{
+    uint64_t h = seed ^ ((uint64_t)(int64_t)step * 0x9E3779B97F4A7C15ull + (uint64_t)(int64_t)idx * 0x517CC1B727220A95ull);
+    h = (h ^ (h >> 30)) * 0xBF58476D1CE4E5B9ull;
+    h = (h ^ (h >> 27)) * 0x94D049BB133111EBull;
+    return h ^ (h >> 31);
+}
+
+/* gpu_rand (:1228-1237): the top 53 bits to fp32, times 2^-53, plus 1e-10. */
+float orc_sample_uniform(uint64_t seed, int32_t step, int32_t idx)
+{
+    const uint64_t h = orc_sample_hash(seed, step, idx);
+    return (float)(h >> 11) * (1.0f / (float)(1ULL << 53)) + 1e-10f;
+}
+
+/* temperature == 0: the first index of the maximum (std::max_element,
+ * sampler.cc:21-25).  temperature > 0: sample_kernel's Gumbel-max branch
+ * (:1287-1316) in index order: noisy_i = logit_i / T - log(-log(u_i)); a
+ * candidate replaces the best only when strictly greater, from a start of
+ * -1e30 at index 0.  best / second (optional) receive the two largest noisy
+ * values, so a caller can tell a near-tie. */
+int32_t orc_sample(const float* logits, size_t n, float temperature, uint64_t seed, int32_t step, float* best,
+                   float* second)
+{
+    if (temperature == 0.0f) {
+        size_t bi = 0;
+        for (size_t i = 1; i < n; i++)
+            if (logits[bi] < logits[i]) bi = i;
+        if (best) *best = n ? logits[bi] : 0.0f;
+        if (second) *second = -INFINITY;
+        return (int32_t)bi;
+    }
+    float bv = -1e30f, sv = -INFINITY;
+    int32_t bi = 0;
+    for (size_t i = 0; i < n; i++) {
+        const float u = orc_sample_uniform(seed, step, (int32_t)i);
+        const float g = -logf(-logf(u));
+        const float v = logits[i] / temperature + g;
+        if (v > bv) {
+            sv = bv;
+            bv = v;
+            bi = (int32_t)i;
+        } else if (v > sv) {
+            sv = v;
+        }
+    }
+    if (best) *best = bv;
+    if (second) *second = sv;
+    return bi;
+}

@@ -32,6 +32,16 @@
  *                             pinned: bit-exact vs the reference's BackendCPU
  *                             compiled in place (_ref), plus closed forms
  *                             (tests/test_oracle.py)
+ *   orc_sample_hash           pinned: splitmix64's published outputs for seed
+ *                             0 (the step term is its Weyl sequence), bit
+ *                             mixing of the index term (avalanche)
+ *   orc_sample_uniform        pinned: closed form of the top-53-bit scaling,
+ *                             uniformity (Kolmogorov-Smirnov) over indices
+ *   orc_sample                pinned: temperature 0 = std::max_element,
+ *                             one-hot and dominant logits, chi-square of the
+ *                             sampled frequencies against softmax(logit / T),
+ *                             and a planted sign error in the Gumbel term
+ *                             rejected by the same test
  */
 #ifndef VVLLM_ORACLE_H
 #define VVLLM_ORACLE_H
@@ -93,6 +103,14 @@ void orc_linear_add(float* out, const float* inp, const float* weight, const flo
 void orc_matmul(float* out, const float* A, const float* B, size_t M, size_t N, size_t K);
 void orc_causal_attention(float* out, const float* q, size_t q_idx, const float* k, const float* v, size_t attend_len,
                           size_t num_heads, size_t num_kv_heads, size_t head_dim, float scale);
+
+/* Sampling: SamplerCPU's greedy branch (src/sampler/sampler.cc:21-25) at
+ * temperature 0 and the device sampler's Gumbel-max trick above it
+ * (src/backend/cuda_kernels.cu:1228-1317; cuda_sample :1322-1349). */
+uint64_t orc_sample_hash(uint64_t seed, int32_t step, int32_t idx);
+float orc_sample_uniform(uint64_t seed, int32_t step, int32_t idx);
+int32_t orc_sample(const float* logits, size_t n, float temperature, uint64_t seed, int32_t step, float* best,
+                   float* second);
 
 #ifdef __cplusplus
 }

@@ -61,6 +61,12 @@ def _lib(kind: str) -> ctypes.CDLL:
             lib.orc_linear_q8_f64.argtypes = [_P, _P, _P, _P, _P, _P, _S, _S, _S]
             lib.orc_bf16_to_f32.argtypes = [_P, _S, _P]
             lib.orc_ingest_bf16.argtypes = [_P, _S, _S, _P, _P]
+            lib.orc_sample_hash.argtypes = [ctypes.c_uint64, ctypes.c_int32, ctypes.c_int32]
+            lib.orc_sample_hash.restype = ctypes.c_uint64
+            lib.orc_sample_uniform.argtypes = [ctypes.c_uint64, ctypes.c_int32, ctypes.c_int32]
+            lib.orc_sample_uniform.restype = ctypes.c_float
+            lib.orc_sample.argtypes = [_P, _S, ctypes.c_float, ctypes.c_uint64, ctypes.c_int32, _P, _P]
+            lib.orc_sample.restype = ctypes.c_int32
         _libs[kind] = lib
     return _libs[kind]
 
@@ -213,3 +219,23 @@ def causal_attention(q, k, v, q_idx, attend_len, scale, kind: str = "port"):
     out = np.empty(H * D, np.float32)
     _fn(kind, "causal_attention")(_ptr(out), _ptr(q), q_idx, _ptr(k), _ptr(v), attend_len, H, k.shape[1], D, scale)
     return out
+
+
+def sample_hash(seed: int, step: int, idx: int) -> int:
+    """gpu_rand's 64-bit hash (src/backend/cuda_kernels.cu:1230-1235)."""
+    return int(_lib("port").orc_sample_hash(seed, step, idx))
+
+
+def sample_uniform(seed: int, step: int, idx: int) -> float:
+    """gpu_rand (src/backend/cuda_kernels.cu:1228-1237)."""
+    return float(_lib("port").orc_sample_uniform(seed, step, idx))
+
+
+def sample(logits, temperature: float, seed: int, step: int):
+    """(index, best noisy value, second best) of the device sampler's
+    Gumbel-max trick (temperature > 0) or the greedy argmax (temperature 0)."""
+    x = _f32(np.ravel(logits))
+    best, second = ctypes.c_float(), ctypes.c_float()
+    i = _lib("port").orc_sample(x.ctypes.data, x.size, temperature, seed, step, ctypes.byref(best),
+                               ctypes.byref(second))
+    return int(i), best.value, second.value

@@ -114,6 +114,14 @@ def test_validation_before_device_use():
     assert st("vvh_rope_append", P, P, P, P, P, 1, 14, 2, 64, 0, 1e4, 9, None) == 1  # bad dtype
     assert st("vvh_rope_append", P, P, P, P, P, 1, 14, 2, 64, 0, 1e4, capi.F16, None) == 5
     assert st("vvh_plan_set_input_op", 999, capi.IN_RMS_NORM, P, 1e-6) == 5
+    # sampler: temperature must be finite and >= 0, logits F32 / F16, n >= 1
+    for T in (-0.5, float("nan"), float("inf")):
+        assert st("vvh_sample", P, capi.F32, 16, T, 1.0, 1, 0, P, None) == 1
+    assert st("vvh_sample", P, 5, 16, 1.0, 1.0, 1, 0, P, None) == 1
+    assert st("vvh_sample", P, capi.F32, 0, 1.0, 1.0, 1, 0, P, None) == 1
+    assert st("vvh_sample", None, capi.F32, 16, 1.0, 1.0, 1, 0, P, None) == 1
+    assert st("vvh_sample", P, capi.F32, 16, 0.7, 0.9, 1, 0, None, None) == 1
+    assert st("vvh_sample", P, capi.F16, 16, 0.7, 0.9, 1, 0, P, None) == 5
     stats = capi.PoolStats()
     assert st("vvh_pool_get_stats", ctypes.byref(stats)) == 0 and stats.bytes_in_use == 0
 

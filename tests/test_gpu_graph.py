@@ -105,3 +105,67 @@ def test_graph_replay_matches_eager(gpu, oracle):
     hip.hipGraphDestroy(graph)
     capi.call("vvh_plan_destroy", plan.value)
     hip.hipStreamDestroy(stream)
+
+
+def test_graph_survives_workspace_growth(gpu, oracle):
+    """A graph captured with a split-K GEMM keeps working after a larger
+    split-K call on the same stream has grown the stream's workspace: the
+    outgrown buffer, whose address the graph holds, is kept, not freed."""
+    hip = _hip()
+    V = ctypes.c_void_p
+    hip.hipStreamCreate.argtypes = [ctypes.POINTER(V)]
+    hip.hipStreamSynchronize.argtypes = [V]
+    hip.hipStreamBeginCapture.argtypes = [V, ctypes.c_int]
+    hip.hipStreamEndCapture.argtypes = [V, ctypes.POINTER(V)]
+    hip.hipGraphInstantiate.argtypes = [ctypes.POINTER(V), V, V, V, ctypes.c_size_t]
+    hip.hipGraphLaunch.argtypes = [V, V]
+    hip.hipGraphExecDestroy.argtypes = [V]
+    hip.hipGraphDestroy.argtypes = [V]
+    hip.hipStreamDestroy.argtypes = [V]
+    stream = V()
+    _check(hip.hipStreamCreate(ctypes.byref(stream)), "hipStreamCreate")
+    rng = np.random.default_rng(7)
+
+    def problem(M, N, K):
+        w = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+        q, s = oracle.quantize_per_channel(w)
+        x = rng.normal(0, 1, (M, K)).astype(np.float16)
+        return dict(q=capi.DevBuf.from_array(q), s=capi.DevBuf.from_array(s), x=capi.DevBuf.from_array(x),
+                    y=capi.DevBuf(M * N * 2), M=M, N=N, K=K)
+
+    def run(d):
+        capi.call("vvh_linear_q8_dev", d["y"].ptr, d["x"].ptr, d["q"].ptr, d["s"].ptr, None, None,
+                  d["M"], d["N"], d["K"], F16, F16, stream)
+
+    def out(d):
+        return d["y"].to_array(np.uint16, (d["M"], d["N"]))
+
+    small = problem(64, 896, 4864)   # split-K, a few MB of partial planes
+    large = problem(512, 896, 4864)  # split-K, about 11 MB: grows the workspace
+    assert "split" in capi.gemm_variant(64, 896, 4864) and "split" in capi.gemm_variant(512, 896, 4864)
+    capi.call("vvh_workspace_release", stream)  # start from no workspace on this stream
+    run(small)
+    _check(hip.hipStreamSynchronize(stream), "sync")
+    eager_small = out(small)
+    graph, gexec = V(), V()
+    _check(hip.hipStreamBeginCapture(stream, 0), "hipStreamBeginCapture")
+    run(small)
+    _check(hip.hipStreamEndCapture(stream, ctypes.byref(graph)), "hipStreamEndCapture")
+    _check(hip.hipGraphInstantiate(ctypes.byref(gexec), graph, None, None, 0), "hipGraphInstantiate")
+    run(large)  # eager: grows the workspace past the captured buffer
+    _check(hip.hipStreamSynchronize(stream), "sync")
+    eager_large = out(large)
+    zero = np.zeros(64 * 896, np.uint16)
+    for rep in range(3):
+        capi.call("vvh_memcpy_h2d", small["y"].ptr, zero.ctypes.data, zero.nbytes)
+        print(f"[case] replay after workspace growth {rep}", flush=True)
+        _check(hip.hipGraphLaunch(gexec, stream), "hipGraphLaunch")
+        _check(hip.hipStreamSynchronize(stream), "sync")
+        np.testing.assert_array_equal(out(small), eager_small, err_msg=f"replay {rep}")
+        run(large)  # eager work on the grown workspace between replays
+        _check(hip.hipStreamSynchronize(stream), "sync")
+        np.testing.assert_array_equal(out(large), eager_large, err_msg=f"large after replay {rep}")
+    hip.hipGraphExecDestroy(gexec)
+    hip.hipGraphDestroy(graph)
+    capi.call("vvh_workspace_release", stream)
+    hip.hipStreamDestroy(stream)

@@ -51,6 +51,7 @@ SIGNATURES = {
     "vvh_memcpy_h2d": (c_int, [c_void_p, c_void_p, c_size_t]),
     "vvh_memcpy_d2h": (c_int, [c_void_p, c_void_p, c_size_t]),
     "vvh_memcpy_d2d": (c_int, [c_void_p, c_void_p, c_size_t]),
+    "vvh_workspace_release": (c_int, [c_void_p]),
     "vvh_pool_alloc": (c_int, [_PP, c_size_t]),
     "vvh_pool_free": (c_int, [c_void_p]),
     "vvh_pool_release_cached": (c_int, []),
@@ -93,6 +94,8 @@ SIGNATURES = {
                           c_int, c_void_p]),
     "vvh_matmul": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_size_t, c_size_t, c_int, c_void_p]),
     "vvh_argmax": (c_int, [c_void_p, c_size_t, c_void_p, c_void_p]),
+    "vvh_sample": (c_int, [c_void_p, c_int, c_size_t, ctypes.c_float, ctypes.c_float, ctypes.c_uint64, ctypes.c_int32,
+                           c_void_p, c_void_p]),
     "vvh_mirror_f32": (c_int, [c_void_p, c_size_t, c_int, POINTER(c_void_p)]),
     "vvh_mirror_release": (c_int, [c_void_p]),
     "vvh_memcpy_d2d_async": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
@@ -219,8 +222,6 @@ def gemm_variant(M, N, K) -> str:
     v = load().vvh_gemm_variant(M, N, K, ctypes.byref(tn), ctypes.byref(sp))
     if v == 3:
         return f"k_gemm3 128x{tn.value}" + (f" split {sp.value}" if sp.value > 1 else "")
-    if v == 2:
-        return f"k_gemm2 split {sp.value}" if sp.value > 1 else "k_gemm2"
     return "k_gemm" if v == 1 else "?"
 
 

@@ -115,6 +115,19 @@ constexpr int kGemmBM = 128;
 constexpr int kGemmBN = 128;
 constexpr int kGemmBK = 64;
 
+// Runtime services shared by the C ABI's source files (runtime.hip).
+// Records a message for vvh_last_error() and returns `status`.
+int fail(int status, const char* fmt, ...);
+// A fixed device buffer used as a call's workspace (split-K partial planes)
+// in place of the per-stream workspace, which grows with hipMalloc.
+struct WsSource {
+    void* fixed = nullptr;
+    std::size_t bytes = 0;
+};
+// vvh_linear_q8_dev with the workspace from wsrc (null: the stream's).
+int linear_dev(void* out, const void* inp, const int8_t* w, const float* scales, const float* bias, const void* res,
+               std::size_t M, std::size_t N, std::size_t K, int act, int outd, void* stream, const WsSource* wsrc);
+
 // Launchers (linear_kernels.hip).  Return a hipError_t value as int.
 int launch_generic(const LinArgs& a, int act, int out, void* stream);
 int launch_gemv_f32(const LinArgs& a, int out, void* stream);
@@ -164,6 +177,10 @@ int launch_matmul(void* out, const void* A, const float* B, int64_t M, int64_t N
 // ws: argmax_ws_bytes(n) bytes (none for n <= 2048)
 int64_t argmax_ws_bytes(int64_t n);
 int launch_argmax(const float* x, int64_t n, int32_t* idx, float* ws, void* stream);
+// temperature 0: argmax; > 0: Gumbel-max with the hash uniforms of (seed, step, i);
+// x holds n values of dtype (VVH_F32 / VVH_F16); ws as for launch_argmax
+int launch_sample(const void* x, int dtype, int64_t n, float temperature, uint64_t seed, int32_t step, int32_t* idx,
+                  float* ws, void* stream);
 
 // Auxiliary kernels (aux_kernels.hip).
 // w: N x K elements of src_dtype (VVH_F32 or VVH_BF16)

@@ -179,72 +179,12 @@ __device__ __forceinline__ void wait_vmcnt()
     __builtin_amdgcn_s_waitcnt((V & 15) | ((V >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// LDS layout of a GEMM stage (1 KB per 64-lane load instruction, lane i ->
+// bytes 16i..16i+15; the swizzles put the 16 rows read by 16 lanes of one
+// 16-byte fragment load in 16 distinct 16-byte bank groups of the LDS):
+//   A: 128 rows x 128 B; row r keeps 16-byte chunk c at slot c ^ ((r >> 1) & 7)
+//   B: rows of 64 B;     row r keeps 16-byte chunk c at slot c ^ ((r >> 2) & 3)
 __device__ __forceinline__ int swz_a(int r, int c) { return c ^ ((r >> 1) & 7); }
 __device__ __forceinline__ int swz_b(int r, int c) { return c ^ ((r >> 2) & 3); }
-
-// Fragments of one stage held in registers: the B codes (int8, converted
-// just before use) and the fp16 A fragments.
-template <int TI, int TJ>
-struct Gemm2Frag {
-    u4 b[2][TJ];
-    h8 a[2][2][TI];
-};
-
-template <int TI, int TJ>
-__device__ __forceinline__ void gemm2_read(const f16* __restrict__ sa, const int8_t* __restrict__ sb,
-                                           Gemm2Frag<TI, TJ>& f, int row0, int col0, int fl, int fh)
-{
-#pragma unroll
-    for (int kk2 = 0; kk2 < 2; kk2++) {
-#pragma unroll
-        for (int tj = 0; tj < TJ; tj++) {
-            const int j = col0 + tj * 32 + fl;
-            f.b[kk2][tj] = *reinterpret_cast<const u4*>(sb + j * 64 + swz_b(j, kk2 * 2 + fh) * 16);
-        }
-#pragma unroll
-        for (int h = 0; h < 2; h++)
-#pragma unroll
-            for (int ti = 0; ti < TI; ti++) {
-                const int i = row0 + ti * 32 + fl;
-                f.a[kk2][h][ti] = *reinterpret_cast<const h8*>(sa + i * 64 + swz_a(i, kk2 * 4 + fh * 2 + h) * 8);
-            }
-    }
-}
-
-// MFMAs of one stage.  The codes of the second 32-wide k slice are converted
-// while the first slice's MFMAs run, and the scheduling-group barriers
-// interleave conversion VALU with the MFMAs (each MFMA occupies the matrix
-// unit for 32 cycles, during which the wave can issue about 8 VALU ops), so
-// the conversion hides behind the matrix work instead of sitting between it.
-template <int TI, int TJ>
-__device__ __forceinline__ void gemm2_mfma(const Gemm2Frag<TI, TJ>& f, f16v (&acc)[TI][TJ])
-{
-    h8 fb[2][TJ][2];
-#pragma unroll
-    for (int tj = 0; tj < TJ; tj++) i8x16_to_h8x2(f.b[0][tj], fb[0][tj][0], fb[0][tj][1]);
-#pragma unroll
-    for (int kk2 = 0; kk2 < 2; kk2++) {
-        if (kk2 == 0) {
-#pragma unroll
-            for (int tj = 0; tj < TJ; tj++) i8x16_to_h8x2(f.b[1][tj], fb[1][tj][0], fb[1][tj][1]);
-        }
-#pragma unroll
-        for (int h = 0; h < 2; h++)
-#pragma unroll
-            for (int ti = 0; ti < TI; ti++)
-#pragma unroll
-                for (int tj = 0; tj < TJ; tj++)
-                    acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[kk2][h][ti], fb[kk2][tj][h], acc[ti][tj], 0, 0, 0);
-    }
-    // 2*2*TI*TJ MFMAs; the 20*TJ conversion ops of slice 1 go between the
-    // MFMAs of slice 0
-    constexpr int NM = 2 * TI * TJ;        // MFMAs per slice
-    constexpr int NV = (20 * TJ + NM - 1) / NM;
-#pragma unroll
-    for (int i = 0; i < NM; i++) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, NV, 0); // then conversion VALU
-    }
-}
 
 }  // namespace vvh

@@ -9,12 +9,12 @@
 // 64 x (32 * TJ) wave tile built from 2 x TJ v_mfma_f32_32x32x16_f16 tiles.
 // The wave tile is chosen for the LDS read rate: per MFMA a wave reads
 // (8 KB of A + TJ * 2 KB of B) / (8 TJ) from LDS, 0.58 KB at TJ = 3 against
-// 1.25 KB for the 64 x 32 tile of k_gemm2, whose 8 waves read more bytes per
+// 1.25 KB for a 64 x 32 wave tile, with which 8 waves read more bytes per
 // stage than the LDS delivers in the stage's MFMA time.
 //
 // Operands are staged through a ring of D LDS stages filled by direct
 // global -> LDS loads (global_load_lds_dwordx4), A as fp16 and B as the raw
-// int8 codes, in the same swizzled layout as k_gemm2 (swz_a / swz_b).  The
+// int8 codes, in the swizzled layout of swz_a / swz_b (device.h).  The
 // codes are converted to fp16 exactly (two v_perm and one packed subtract
 // per 4 codes) half a stage ahead of their MFMAs: the second k slice of a
 // stage is converted during the first slice's MFMAs, and the first k slice

@@ -1017,281 +1017,6 @@ __global__ __launch_bounds__(256) void k_gemm(LinArgs a)
 }
 
 // ---------------------------------------------------------------------------
-// k_gemm2: fp16 activations, M > 16, K % 64 == 0.
-// Block tile 128(m) x 128(n) x 64(k), 256 threads = 4 waves arranged WM x WN
-// (wave tile (128/WM) x (128/WN), built from 32x32x16 MFMAs).  Both operands
-// are staged through a ring of D LDS stages filled by direct global->LDS
-// loads (global_load_lds_dwordx4: no VGPRs, no ds_write), so D-1 stages of
-// loads are in flight while one is multiplied.  A is stored as fp16, B as the
-// raw int8 codes; each wave converts the B fragments it reads.
-//
-// LDS layout (1 KB per 64-lane load instruction, lane i -> bytes 16i..16i+15;
-// the swizzles make the 16 rows read by 16 lanes of a 16-byte fragment load
-// fall into 16 distinct 16-byte bank groups of the 64-bank LDS):
-//   A stage: 128 rows x 128 B; row r keeps 16-byte chunk c at slot c ^ ((r >> 1) & 7)
-//   B stage: 128 rows x  64 B; row r keeps 16-byte chunk c at slot c ^ ((r >> 2) & 3)
-// k order inside an MFMA: the B fragment (kk2, tj) of lane l holds codes
-// k = 32*kk2 + 16*(l/32) + [0, 16); bytes 0-7 feed MFMA h = 0 and 8-15 h = 1,
-// and the A fragment (kk2, h) of lane l holds x[i][32*kk2 + 16*(l/32) + 8*h + [0, 8)].
-//
-// Synchronisation: one s_barrier per stage.  Before it each thread waits
-// until its own loads of the stage to be read have landed (vmcnt counts the
-// loads issued after them) and its LDS reads of the previous stage are done
-// (lgkmcnt(0)); after it the stage read in the previous step is refilled.
-// The stage buffers are separate __shared__ objects indexed only with
-// constants, and the fill / multiply helpers take them as __restrict__
-// parameters: that is what lets the compiler tell the in-flight
-// direct-to-LDS writes of one stage from the reads of another (otherwise it
-// drains every outstanding load before each LDS read).
-//
-// Epilogue: acc * scale + bias in fp32 is transposed through LDS (the 32-row
-// quarter q of the tile in stage buffer q) and written row-major with 16-byte
-// stores, the residual added in fp32 before the single rounding to OT.
-// ---------------------------------------------------------------------------
-struct Gemm2Stage {
-    __attribute__((aligned(16))) f16 a[kGemmBM * kGemmBK];
-    __attribute__((aligned(16))) int8_t b[kGemmBN * kGemmBK];
-};
-// per thread and stage: 16/NW A loads + 8/NW B loads of 16 bytes (NW waves)
-template <int NW>
-constexpr int gemm2_loads_per_stage() { return 24 / NW; }
-constexpr int kEpiStride = kGemmBN + 4;  // fp32 row stride of an epilogue quarter
-static_assert(32 * kEpiStride * 4 <= (int)sizeof(Gemm2Stage), "epilogue quarter fits a stage buffer");
-
-template <int NW>
-__device__ __forceinline__ void gemm2_fill(f16* __restrict__ sa, int8_t* __restrict__ sb,
-                                           const f16* const* a_src, const int8_t* const* b_src,
-                                           int wave, int64_t k0)
-{
-#pragma unroll
-    for (int i = 0; i < 16 / NW; i++)
-        __builtin_amdgcn_global_load_lds(a_src[i] + k0, sa + (wave * (16 / NW) + i) * 512, 16, 0, 0);
-#pragma unroll
-    for (int i = 0; i < 8 / NW; i++)
-        __builtin_amdgcn_global_load_lds(b_src[i] + k0, sb + (wave * (8 / NW) + i) * 1024, 16, 0, 0);
-}
-
-template <typename OT, int D, int NW, int WM>
-__global__ __launch_bounds__(64 * NW, 1) void k_gemm2(LinArgs a)
-{
-    static_assert(D == 4 || D == 6, "even stage count (2-way fragment double buffer), >= 4 for the epilogue");
-    static_assert(NW == 4 || NW == 8, "waves per block");
-    constexpr int NT = 64 * NW;
-    constexpr int LPS = gemm2_loads_per_stage<NW>();
-    constexpr int WN = NW / WM;
-    constexpr int TI = kGemmBM / WM / 32, TJ = kGemmBN / WN / 32;
-    using Frag = Gemm2Frag<TI, TJ>;
-    __shared__ Gemm2Stage st0, st1, st2, st3, st4, st5;
-
-    const int64_t nbm = (a.M + kGemmBM - 1) / kGemmBM;
-    const int64_t nbn = (a.N + kGemmBN - 1) / kGemmBN;
-    // blocks enumerate (split, tile), tiles fastest, dealt XCD by XCD
-    const int64_t tiles = nbm * nbn;
-    const bool split = a.nsplit > 1;
-    const int64_t logical = xcd_remap(blockIdx.x, tiles * (split ? a.nsplit : 1));
-    const int64_t ks = logical / tiles, tile = logical - ks * tiles;
-    const int64_t m0 = (tile % nbm) * kGemmBM;
-    const int64_t n0 = (tile / nbm) * kGemmBN;
-    const int64_t kbase = split ? ks * a.kstages * kGemmBK : 0;
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wm = wave % WM, wn = wave / WM;
-    const int row0 = wm * (kGemmBM / WM), col0 = wn * (kGemmBN / WN);
-    const int fl = lane & 31, fh = lane >> 5;
-    const f16* X = static_cast<const f16*>(a.inp);
-
-    // epilogue constants, loaded first (their loads are the oldest in the
-    // vmcnt queue, so the stage waits below still count correctly)
-    float sc[TJ], bi[TJ];
-#pragma unroll
-    for (int tj = 0; tj < TJ; tj++) {
-        const int64_t n = n0 + col0 + tj * 32 + fl;
-        sc[tj] = split ? 1.0f : (n < a.N ? a.scales[n] : 0.0f);  // split partials stay raw
-        bi[tj] = (!split && a.bias && n < a.N) ? a.bias[n] : 0.0f;
-    }
-
-    // per-lane global sources of this thread's direct-to-LDS loads (k0 added per stage)
-    const f16* a_src[16 / NW];
-#pragma unroll
-    for (int i = 0; i < 16 / NW; i++) {
-        const int r = (wave * (16 / NW) + i) * 8 + (lane >> 3);  // A stage row written by this lane
-        const int64_t gr = m0 + r < a.M ? m0 + r : a.M - 1;      // rows past M: any valid row
-        a_src[i] = X + gr * a.K + kbase + swz_a(r, lane & 7) * 8;
-    }
-    const int8_t* b_src[8 / NW];
-#pragma unroll
-    for (int i = 0; i < 8 / NW; i++) {
-        const int r = (wave * (8 / NW) + i) * 16 + (lane >> 2);
-        const int64_t gn = n0 + r < a.N ? n0 + r : a.N - 1;
-        b_src[i] = a.w + gn * a.K + kbase + swz_b(r, lane & 3) * 16;
-    }
-
-    auto stage = [&](auto S) -> Gemm2Stage& {
-        constexpr int s = decltype(S)::value % D;
-        if constexpr (s == 0) return st0;
-        else if constexpr (s == 1) return st1;
-        else if constexpr (s == 2) return st2;
-        else if constexpr (s == 3) return st3;
-        else if constexpr (s == 4) return st4;
-        else return st5;
-    };
-    auto issue = [&](Gemm2Stage& g, int64_t kt) { gemm2_fill<NW>(g.a, g.b, a_src, b_src, wave, kt * kGemmBK); };
-
-    f16v acc[TI][TJ];
-#pragma unroll
-    for (int i = 0; i < TI; i++)
-#pragma unroll
-        for (int j = 0; j < TJ; j++) acc[i][j] = f16v{};
-    Frag f0, f1;
-    auto frag = [&](auto P) -> Frag& {
-        if constexpr (decltype(P)::value % 2 == 0) return f0;
-        else return f1;
-    };
-    auto read = [&](auto S, auto P) { gemm2_read<TI, TJ>(stage(S).a, stage(S).b, frag(P), row0, col0, fl, fh); };
-    auto sync = [&]() { lds_barrier(); };
-
-    // Schedule (all straight-line, stage indices and vmcnt thresholds are
-    // compile-time constants):
-    //   prologue: issue stages 0..P-1 (P = min(D, nk)); wait stage 0; read its fragments
-    //   step j:   wait until stage j+1 has landed; barrier (stage j's buffer
-    //             is free, its fragments are in registers); refill that buffer
-    //             with stage j+D; read stage j+1's fragments; MFMAs of stage j
-    //             -- the LDS reads of j+1 overlap the MFMAs of j.
-    // For R steps from kt0 (kt0 % D == 0, so buffer and fragment parity are
-    // static), with the stage count n of the problem known to be kt0 + R:
-    auto steps = [&]<int R, bool FIRST_PASS>(int64_t kt0) {
-        [&]<int... J>(std::integer_sequence<int, J...>) {
-            ([&] {
-                constexpr int j = J;
-                if constexpr (j + 1 < R) {
-                    // later stages possibly in flight after stage j+1: j+2 .. min(j+D-1, R-1)
-                    constexpr int later = (R - 2 - j < D - 2) ? R - 2 - j : D - 2;
-                    wait_vmcnt<later * LPS>();
-                }
-                sync();
-                if constexpr (j + D < R) issue(stage(std::integral_constant<int, j>{}), kt0 + j + D);
-                if constexpr (j + 1 < R) read(std::integral_constant<int, j + 1>{}, std::integral_constant<int, j + 1>{});
-                gemm2_mfma<TI, TJ>(frag(std::integral_constant<int, j>{}), acc);
-            }(), ...);
-        }(std::make_integer_sequence<int, R>{});
-    };
-    auto prologue = [&]<int P>() {
-        [&]<int... S>(std::integer_sequence<int, S...>) {
-            (issue(stage(std::integral_constant<int, S>{}), S), ...);
-        }(std::make_integer_sequence<int, P>{});
-        wait_vmcnt<(P - 1) * LPS>();
-        sync();
-        read(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
-    };
-
-    const int64_t nk_all = a.K / kGemmBK;
-    const int64_t nk = split ? (nk_all - kbase / kGemmBK < a.kstages ? nk_all - kbase / kGemmBK : a.kstages) : nk_all;
-    if (nk >= D) {
-        prologue.template operator()<D>();
-        int64_t kt0 = 0;
-        for (; kt0 + 2 * D <= nk; kt0 += D) {
-            // a full group: every step refills, every wait is at the steady-state depth
-            [&]<int... J>(std::integer_sequence<int, J...>) {
-                ([&] {
-                    constexpr int j = J;
-                    wait_vmcnt<(D - 2) * LPS>();
-                    sync();
-                    issue(stage(std::integral_constant<int, j>{}), kt0 + j + D);
-                    read(std::integral_constant<int, j + 1>{}, std::integral_constant<int, j + 1>{});
-                    gemm2_mfma<TI, TJ>(frag(std::integral_constant<int, j>{}), acc);
-                }(), ...);
-            }(std::make_integer_sequence<int, D>{});
-        }
-        const int64_t r = nk - kt0;  // D .. 2D-1
-        [&]<int... R>(std::integer_sequence<int, R...>) {
-            ((r == R + D ? steps.template operator()<R + D, false>(kt0) : void()), ...);
-        }(std::make_integer_sequence<int, D>{});
-    } else {
-        [&]<int... R>(std::integer_sequence<int, R...>) {
-            ((nk == R + 1 ? [&] {
-                prologue.template operator()<R + 1>();
-                steps.template operator()<R + 1, true>(0);
-            }() : void()), ...);
-        }(std::make_integer_sequence<int, D - 1>{});
-    }
-
-    // ---- epilogue ----
-    __builtin_amdgcn_s_waitcnt(0);  // everything, including in-flight stage loads
-    lds_barrier();
-    auto quarter = [&](int q) -> float* {
-        return reinterpret_cast<float*>(q == 0 ? &st0 : q == 1 ? &st1 : q == 2 ? &st2 : &st3);
-    };
-#pragma unroll
-    for (int tj = 0; tj < TJ; tj++) {
-        const int col = col0 + tj * 32 + fl;
-#pragma unroll
-        for (int ti = 0; ti < TI; ti++) {
-            float* q = quarter((row0 >> 5) + ti);
-#pragma unroll
-            for (int r = 0; r < 16; r++)
-                q[(8 * (r >> 2) + 4 * fh + (r & 3)) * kEpiStride + col] = acc[ti][tj][r] * sc[tj] + bi[tj];
-        }
-    }
-    lds_barrier();
-    const bool vec_ok = (a.N % 8) == 0;
-#pragma unroll 2
-    for (int it = 0; it < 2048 / NT; it++) {  // 128 rows x 16 chunks of 8 outputs
-        const int idx = tid + NT * it;
-        const int row = idx >> 4, ch = idx & 15;
-        const int64_t mm = m0 + row, nn = n0 + ch * 8;
-        if (mm >= a.M || nn >= a.N) continue;
-        const float* tq = quarter(row >> 5) + (row & 31) * kEpiStride + ch * 8;
-        const f4 v0 = *reinterpret_cast<const f4*>(tq);
-        const f4 v1 = *reinterpret_cast<const f4*>(tq + 4);
-        float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-        const int64_t o = mm * a.N + nn;
-        if (split) {  // raw partial sums of this split
-            float* wp = a.ws + ks * a.M * a.N + o;
-            if (vec_ok && nn + 8 <= a.N) {
-                *reinterpret_cast<f4*>(wp) = v0;
-                *reinterpret_cast<f4*>(wp + 4) = v1;
-            } else {
-                for (int e = 0; e < 8 && nn + e < a.N; e++) wp[e] = v[e];
-            }
-            continue;
-        }
-        if (vec_ok && nn + 8 <= a.N) {
-            if constexpr (sizeof(OT) == 2) {
-                if (a.res) {
-                    const h8 r8 = *reinterpret_cast<const h8*>(static_cast<const f16*>(a.res) + o);
-#pragma unroll
-                    for (int e = 0; e < 8; e++) v[e] += (float)r8[e];
-                }
-                h8 o8;
-#pragma unroll
-                for (int e = 0; e < 8; e++) o8[e] = (f16)v[e];
-                *reinterpret_cast<h8*>(static_cast<f16*>(a.out) + o) = o8;
-            } else {
-                if (a.res) {
-                    const f4 r0 = *reinterpret_cast<const f4*>(static_cast<const float*>(a.res) + o);
-                    const f4 r1 = *reinterpret_cast<const f4*>(static_cast<const float*>(a.res) + o + 4);
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        v[e] += r0[e];
-                        v[e + 4] += r1[e];
-                    }
-                }
-                *reinterpret_cast<f4*>(static_cast<float*>(a.out) + o) = f4{v[0], v[1], v[2], v[3]};
-                *reinterpret_cast<f4*>(static_cast<float*>(a.out) + o + 4) = f4{v[4], v[5], v[6], v[7]};
-            }
-        } else {
-            for (int e = 0; e < 8 && nn + e < a.N; e++) {
-                float x = v[e];
-                if (a.res) x += ld_f(static_cast<const OT*>(a.res) + o + e);
-                st_f(static_cast<OT*>(a.out) + o + e, x);
-            }
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------
 // k_splitk_reduce: out = (sum over splits of ws[s][m][n]) * scale[n] + bias[n]
 // (+ res[m][n]), in fp32 with one rounding; 4 consecutive outputs per thread
 // (16-byte partial loads when N % 4 == 0).  The partials are summed in split
@@ -1551,56 +1276,8 @@ int launch_stream(const StreamArgs& s, int depth, int max_m, int out, int64_t bl
     return (int)hipGetLastError();
 }
 
-static int g_gemm2_stages = 0;
-static int g_gemm2_layout = -1;
-
-// Tuning knobs read once: VVH_GEMM_STAGES (4 or 6, default 4) and
-// VVH_GEMM_WM (block layout: 1, 2, 4 = 4 waves with that many wave rows;
-// 12, 14 = 8 waves with 2 or 4 wave rows; default 12).
-static void gemm2_config()
-{
-    if (g_gemm2_stages == 0) {
-        const char* e = getenv("VVH_GEMM_STAGES");
-        const int v = e ? atoi(e) : 4;
-        g_gemm2_stages = v == 6 ? 6 : 4;
-        const char* l = getenv("VVH_GEMM_WM");
-        const int w = l ? atoi(l) : 12;
-        g_gemm2_layout = (w == 1 || w == 2 || w == 4 || w == 12 || w == 14) ? w : 12;
-    }
-}
-
-template <int D, int NW, int WM>
-static void gemm2_launch(const LinArgs& a, bool f32, dim3 grid, hipStream_t s)
-{
-    if (f32) hipLaunchKernelGGL((k_gemm2<float, D, NW, WM>), grid, dim3(64 * NW), 0, s, a);
-    else hipLaunchKernelGGL((k_gemm2<f16, D, NW, WM>), grid, dim3(64 * NW), 0, s, a);
-}
-
-// layout code: 1, 2, 4 = 4 waves with that many wave rows; 12, 14 = 8 waves with 2 or 4 wave rows
-template <int D>
-static void gemm2_launch_wm(const LinArgs& a, bool f32, dim3 grid, hipStream_t s, int wm)
-{
-    switch (wm) {
-        case 1: gemm2_launch<D, 4, 1>(a, f32, grid, s); break;
-        case 4: gemm2_launch<D, 4, 4>(a, f32, grid, s); break;
-        case 12: gemm2_launch<D, 8, 2>(a, f32, grid, s); break;
-        case 14: gemm2_launch<D, 8, 4>(a, f32, grid, s); break;
-        default: gemm2_launch<D, 4, 2>(a, f32, grid, s); break;
-    }
-}
-
 int launch_gemm(const LinArgs& a, int out, void* stream)
 {
-    if (a.K % kGemmBK == 0) {
-        gemm2_config();
-        const int64_t nbm = (a.M + kGemmBM - 1) / kGemmBM;
-        const int64_t nbn = (a.N + kGemmBN - 1) / kGemmBN;
-        const dim3 grid((unsigned)(nbm * nbn * (a.nsplit > 1 ? a.nsplit : 1)));
-        const bool f32 = out == VVH_F32;
-        if (g_gemm2_stages == 6) gemm2_launch_wm<6>(a, f32, grid, S(stream), g_gemm2_layout);
-        else gemm2_launch_wm<4>(a, f32, grid, S(stream), g_gemm2_layout);
-        return (int)hipGetLastError();
-    }
     const int64_t nbm = (a.M + kGemmBM - 1) / kGemmBM;
     const int64_t nbn = (a.N + kGemmBN - 1) / kGemmBN;
     const dim3 grid((unsigned)(nbm * nbn));

@@ -12,7 +12,8 @@
 //   k_attention  causal attention, one block per (head, query)  (:344-378)
 //   k_dense      out = x @ W^T + bias (+ res), fp32 or fp16 W    (:139-156, :302-320)
 //   k_matmul     out = A @ B, B [K, N]                  (:25-42)
-//   k_argmax     greedy sampling: first index of the max (src/sampler/sampler.cc:21-25)
+//   k_sample     greedy sampling, first index of the max (src/sampler/sampler.cc:21-25),
+//                and Gumbel-max temperature sampling (src/backend/cuda_kernels.cu:1228-1349)
 //
 // All are bandwidth- or latency-bound: per decode step they move kilobytes,
 // except the dense LM head (the tied embedding, vocab x hidden weights) and
@@ -795,11 +796,22 @@ int launch_matmul(void* out, const void* A, const float* B, int64_t M, int64_t N
 }
 
 // ---------------------------------------------------------------------------
-// argmax over n fp32 values: the first index of the maximum, as
-// std::max_element (src/sampler/sampler.cc:21-25).  Block b takes the span
-// [b * per, (b + 1) * per) and writes its (max, first index) to the
-// workspace; one block then reduces the partials in block order.  A single
-// block writes the index directly.
+// Sampling over n logits (fp32, or fp16 widened exactly).
+//
+// Greedy (argmax): the first index of the maximum, as std::max_element
+// (src/sampler/sampler.cc:21-25).
+//
+// Gumbel-max (temperature > 0), the device sampler of the reference
+// (src/backend/cuda_kernels.cu:1240-1317 via cuda_sample :1322-1349): index
+// argmax_i of logit_i / T + g_i with g_i = -log(-log(u_i)) and u_i the hash
+// uniform of (seed, step, i) (:1228-1237).  As there, a candidate counts
+// only when its noisy value is > -1e30 (NaN never counts) and the index is 0
+// when none does.  Equal noisy values resolve to the lower index (the
+// reference's single block keeps the lower thread's, a measure-zero event).
+//
+// Block b takes the span [b * per, (b + 1) * per) and writes its (best
+// value, index) to the workspace; one block then merges the partials in block
+// order.  A single block writes the index directly.
 // ---------------------------------------------------------------------------
 // (v, i) = the better of (v, i) and (ov, oi): larger value, then lower index
 __device__ __forceinline__ void argmax_merge(float& v, int64_t& i, float ov, int64_t oi)
@@ -825,17 +837,39 @@ __device__ __forceinline__ void argmax_block(float& best, int64_t& besti)
     for (int w = 1; w < 4; w++) argmax_merge(best, besti, bv[w], bi[w]);
 }
 
-__global__ __launch_bounds__(256) void k_argmax_part(const float* __restrict__ x, int64_t n, int64_t per,
-                                                     float* __restrict__ pv, int64_t* __restrict__ pi,
-                                                     int32_t* __restrict__ idx)
+// The reference's hash uniform in (0, 1] (cuda_kernels.cu:1228-1237): the
+// seed xor a Weyl sequence of step and index, through the splitmix64
+// finaliser, top 53 bits scaled to [0, 1) in fp32, plus 1e-10.
+__device__ __forceinline__ float sample_uniform(uint64_t seed, int32_t step, int32_t idx)
+{
+    uint64_t h = seed ^ ((uint64_t)(int64_t)step * 0x9E3779B97F4A7C15ull + (uint64_t)(int64_t)idx * 0x517CC1B727220A95ull);
+    h = (h ^ (h >> 30)) * 0xBF58476D1CE4E5B9ull;
+    h = (h ^ (h >> 27)) * 0x94D049BB133111EBull;
+    h ^= h >> 31;
+    return (float)(h >> 11) * (1.0f / 9007199254740992.0f) + 1e-10f;
+}
+
+constexpr int64_t kNone = INT64_MAX;  // partial of a block in which no candidate counted
+
+template <typename T, bool GUMBEL>
+__global__ __launch_bounds__(256) void k_sample_part(const T* __restrict__ x, int64_t n, int64_t per, float temperature,
+                                                     uint64_t seed, int32_t step, float* __restrict__ pv,
+                                                     int64_t* __restrict__ pi, int32_t* __restrict__ idx)
 {
     const int64_t b0 = (int64_t)blockIdx.x * per;
     const int64_t e = b0 + per < n ? b0 + per : n;
-    float best = -INFINITY;
-    int64_t besti = e;  // e: none seen yet (the block's span is never empty)
+    float best = GUMBEL ? -1e30f : -INFINITY;
+    int64_t besti = kNone;
     for (int64_t i = b0 + threadIdx.x; i < e; i += 256) {  // increasing i: strictly greater keeps the first
-        const float v = x[i];
-        if (besti == e || v > best) {
+        float v = (float)x[i];
+        if (GUMBEL) {
+            const float u = sample_uniform(seed, step, (int32_t)i);
+            v = v / temperature + -logf(-logf(u));
+            if (v > best) {
+                best = v;
+                besti = i;
+            }
+        } else if (besti == kNone || v > best) {  // the span is never empty: every block has a first element
             best = v;
             besti = i;
         }
@@ -843,7 +877,7 @@ __global__ __launch_bounds__(256) void k_argmax_part(const float* __restrict__ x
     argmax_block(best, besti);
     if (threadIdx.x == 0) {
         if (gridDim.x == 1) {
-            idx[0] = (int32_t)besti;
+            idx[0] = (int32_t)(besti == kNone ? 0 : besti);
         } else {
             pv[blockIdx.x] = best;
             pi[blockIdx.x] = besti;
@@ -851,14 +885,14 @@ __global__ __launch_bounds__(256) void k_argmax_part(const float* __restrict__ x
     }
 }
 
-__global__ __launch_bounds__(256) void k_argmax_final(const float* __restrict__ pv, const int64_t* __restrict__ pi,
+__global__ __launch_bounds__(256) void k_sample_final(const float* __restrict__ pv, const int64_t* __restrict__ pi,
                                                       int32_t nb, int32_t* __restrict__ idx)
 {
     float best = -INFINITY;
-    int64_t besti = INT64_MAX;
+    int64_t besti = kNone;
     for (int b = threadIdx.x; b < nb; b += 256) argmax_merge(best, besti, pv[b], pi[b]);
     argmax_block(best, besti);
-    if (threadIdx.x == 0) idx[0] = (int32_t)besti;
+    if (threadIdx.x == 0) idx[0] = (int32_t)(besti == kNone ? 0 : besti);
 }
 
 constexpr int64_t kArgmaxPer = 2048;  // elements per block
@@ -871,16 +905,30 @@ int64_t argmax_ws_bytes(int64_t n)
     return nb > 1 ? nb * 12 : 0;
 }
 
-int launch_argmax(const float* x, int64_t n, int32_t* idx, float* ws, void* stream)
+int launch_sample(const void* x, int dtype, int64_t n, float temperature, uint64_t seed, int32_t step, int32_t* idx,
+                  float* ws, void* stream)
 {
     const int64_t per = std::max(kArgmaxPer, (n + kArgmaxMaxBlocks - 1) / kArgmaxMaxBlocks);
     const int64_t nb = (n + per - 1) / per;
     hipStream_t s = static_cast<hipStream_t>(stream);
     int64_t* pi = reinterpret_cast<int64_t*>(ws);  // nb int64 indices, then nb fp32 values
     float* pv = ws ? reinterpret_cast<float*>(pi + nb) : nullptr;
-    hipLaunchKernelGGL(k_argmax_part, dim3((unsigned)nb), dim3(256), 0, s, x, n, per, pv, pi, idx);
-    if (nb > 1) hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(256), 0, s, pv, pi, (int32_t)nb, idx);
+    const dim3 grid((unsigned)nb);
+    const bool g = temperature != 0.0f;
+    if (dtype == VVH_F16) {
+        if (g) hipLaunchKernelGGL((k_sample_part<f16, true>), grid, dim3(256), 0, s, (const f16*)x, n, per, temperature, seed, step, pv, pi, idx);
+        else hipLaunchKernelGGL((k_sample_part<f16, false>), grid, dim3(256), 0, s, (const f16*)x, n, per, temperature, seed, step, pv, pi, idx);
+    } else {
+        if (g) hipLaunchKernelGGL((k_sample_part<float, true>), grid, dim3(256), 0, s, (const float*)x, n, per, temperature, seed, step, pv, pi, idx);
+        else hipLaunchKernelGGL((k_sample_part<float, false>), grid, dim3(256), 0, s, (const float*)x, n, per, temperature, seed, step, pv, pi, idx);
+    }
+    if (nb > 1) hipLaunchKernelGGL(k_sample_final, dim3(1), dim3(256), 0, s, pv, pi, (int32_t)nb, idx);
     return (int)hipGetLastError();
+}
+
+int launch_argmax(const float* x, int64_t n, int32_t* idx, float* ws, void* stream)
+{
+    return launch_sample(x, VVH_F32, n, 0.0f, 0, 0, idx, ws, stream);
 }
 
 }  // namespace vvh

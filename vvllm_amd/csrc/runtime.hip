@@ -21,7 +21,7 @@
 
 using namespace vvh;
 
-namespace {
+namespace vvh {
 
 thread_local std::string g_last_error;
 
@@ -42,6 +42,10 @@ int fail_hip(hipError_t e, const char* what)
         return fail(VVH_ERR_OUT_OF_MEMORY, "%s: %s", what, hipGetErrorString(e));
     return fail(VVH_ERR_HIP, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
 }
+
+}  // namespace vvh
+
+namespace {
 
 std::atomic<bool> g_init{false};
 int g_device = -1;
@@ -107,13 +111,17 @@ std::unordered_map<vvh_plan, Plan> g_plans;
 vvh_plan g_next_plan = 1;
 
 // ---- split-K workspace ------------------------------------------------------
-// fp32 partial sums of split GEMMs, one buffer per stream (calls on one stream
-// run in order, so they can share it; calls on different streams never do).
-// Grown on demand: the old buffer is released only after its stream has
-// drained.  Kept until the process ends.
+// fp32 partial sums of split GEMMs and the partials of multi-block decode
+// attention and sampling, one buffer per stream (calls on one stream run in
+// order, so they can share it; calls on different streams never do).  Grown
+// on demand to at least twice its size; a buffer it outgrows is retired, not
+// freed, because a HIP graph captured earlier on the stream still holds its
+// address in its kernel nodes (a replay must not touch freed memory).
+// Retired buffers are freed by vvh_workspace_release or at process end.
 struct Workspace {
     void* p = nullptr;
     std::size_t bytes = 0;
+    std::vector<void*> retired;
 };
 std::mutex g_wsmu;
 std::unordered_map<void*, Workspace> g_ws;
@@ -123,23 +131,30 @@ int workspace_for(void* stream, std::size_t bytes, float** out)
     std::lock_guard<std::mutex> lock(g_wsmu);
     Workspace& w = g_ws[stream];
     if (w.bytes < bytes) {
-        if (w.p) {
-            hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
-            if (e != hipSuccess) return fail_hip(e, "split-K workspace: stream synchronize");
-            (void)hipFree(w.p);
-            w.p = nullptr;
-            w.bytes = 0;
-        }
-        const std::size_t nb = std::max<std::size_t>(bytes, std::size_t(16) << 20);
-        hipError_t e = hipMalloc(&w.p, nb);
+        const std::size_t nb = std::max({bytes, 2 * w.bytes, std::size_t(1) << 20});
+        void* p = nullptr;
+        hipError_t e = hipMalloc(&p, nb);
         if (e != hipSuccess) {
             (void)hipGetLastError();
-            w.p = nullptr;
-            return fail_hip(e, "split-K workspace hipMalloc");
+            return fail_hip(e, "workspace hipMalloc");
         }
+        if (w.p) w.retired.push_back(w.p);
+        w.p = p;
         w.bytes = nb;
     }
     *out = static_cast<float*>(w.p);
+    return VVH_OK;
+}
+
+// A call's workspace: the stream workspace (grown with hipMalloc) when src is
+// null, else src's fixed buffer, which must be large enough.
+int workspace_get(const WsSource* src, void* stream, std::size_t bytes, float** out)
+{
+    if (!src) return workspace_for(stream, bytes, out);
+    if (bytes > src->bytes)
+        return fail(VVH_ERR_UNSUPPORTED, "the call needs %zu bytes of workspace, more than the %zu of the "
+                    "fixed buffer", bytes, src->bytes);
+    *out = static_cast<float*>(src->fixed);
     return VVH_OK;
 }
 
@@ -153,18 +168,11 @@ int workspace_for(void* stream, std::size_t bytes, float** out)
 // 20.6, 19.9, 19.8, 19.9, 21.8, 21.5 us for 1..7 and 9 splits; M=2048: 36.4,
 // 33.7, 42.4 us for 1..3): 0.4 us per k stage and round of blocks over the
 // CUs, 2.5 us for the reduction's launch, and each plane at 1.6 TB/s.
-// VVH_GEMM_SPLIT=0 disables splitting, =s forces s.
 int gemm_splits(int64_t tiles, int64_t stages, uint64_t plane_bytes)
 {
-    static const int forced = [] {
-        const char* e = getenv("VVH_GEMM_SPLIT");
-        return e ? atoi(e) : -1;
-    }();
     const int64_t cus = g_cu_count > 0 ? g_cu_count : 256;
     int64_t s = 1;
-    if (forced >= 0) {
-        s = forced;
-    } else if (tiles * 2 <= cus && stages >= 32) {
+    if (tiles * 2 <= cus && stages >= 32) {
         const int64_t smax = std::min<int64_t>(cus / tiles, stages / 4);
         double best = 0;
         for (int64_t c = 1; c <= smax; c++) {
@@ -181,20 +189,12 @@ int gemm_splits(int64_t tiles, int64_t stages, uint64_t plane_bytes)
     return (int)s;
 }
 
-// k_gemm3 tile shape (0 = use k_gemm2): split-K problems (few tiles, long
-// K) take 128 x 128; unsplit ones 128 x 192 when it takes fewer rounds of
-// blocks over the CUs than 128 x 128 by a margin that pays for its longer
-// tiles (a 128 x 192 tile takes 1.33x as long as a 128 x 128 one on
-// MI355X), else 128 x 128.  VVH_GEMM3=0 falls back to k_gemm2, =1/2/3
-// forces a layout.
+// k_gemm3 tile shape: split-K problems (few tiles, long K) take 128 x 128;
+// unsplit ones 128 x 192 when it takes fewer rounds of blocks over the CUs
+// than 128 x 128 by a margin that pays for its longer tiles (a 128 x 192
+// tile takes 1.33x as long as a 128 x 128 one on MI355X), else 128 x 128.
 int gemm3_layout(int64_t M, int64_t N, int splits)
 {
-    static const int forced = [] {
-        const char* e = getenv("VVH_GEMM3");
-        return e ? atoi(e) : -1;
-    }();
-    if (forced == 0) return 0;
-    if (forced >= 1 && forced <= 3) return forced;
     if (splits > 1) return 3;
     const int64_t cus = g_cu_count > 0 ? g_cu_count : 256;
     const int64_t nbm = (M + kGemmBM - 1) / kGemmBM;
@@ -218,48 +218,22 @@ bool mul_ok(uint64_t a, uint64_t b, uint64_t* r)
 }
 
 // ---- persistent streaming decode (k_stream) --------------------------------
-// Knobs, read once: VVH_STREAM=0 disables the streaming kernel,
-// VVH_STREAM_WPC = resident waves per CU (default 8), VVH_STREAM_DEPTH = 8 or
-// 12 weight loads in flight per lane (default: the largest every problem
-// allows), VVH_STREAM_MIN_TILES = smallest tile count worth a persistent
-// launch (default 4 per CU).
-struct StreamCfg {
-    bool enabled = true;
-    int wpc = 8;
-    int depth = 0;
-    int64_t min_tiles = -1;
-};
-const StreamCfg& stream_cfg()
-{
-    static StreamCfg c = [] {
-        StreamCfg r;
-        if (const char* e = getenv("VVH_STREAM")) r.enabled = atoi(e) != 0;
-        if (const char* e = getenv("VVH_STREAM_WPC")) r.wpc = std::max(1, std::min(32, atoi(e)));
-        if (const char* e = getenv("VVH_STREAM_DEPTH")) r.depth = atoi(e) >= 12 ? 12 : 8;
-        if (const char* e = getenv("VVH_STREAM_MIN_TILES")) r.min_tiles = atoll(e);
-        return r;
-    }();
-    return c;
-}
+// Resident waves per CU of a streaming launch, and the smallest tile count
+// worth a persistent launch (4 tiles per CU).
+constexpr int kStreamWavesPerCu = 8;
 
-int64_t stream_max_waves() { return (int64_t)(g_cu_count > 0 ? g_cu_count : 256) * stream_cfg().wpc; }
+int64_t stream_max_waves() { return (int64_t)(g_cu_count > 0 ? g_cu_count : 256) * kStreamWavesPerCu; }
 
 // Pipeline depth the streaming kernel can use for problems whose smallest k
-// step count is min_steps (0 = not eligible).
+// step count is min_steps (0 = not eligible): 12 loads in flight per lane
+// when every problem has 12 k steps, else 8.
 int stream_depth(int64_t min_steps)
 {
-    const StreamCfg& c = stream_cfg();
-    if (!c.enabled || min_steps < 8) return 0;
-    const int d = min_steps >= 12 ? 12 : 8;
-    return c.depth ? std::min(c.depth, d) : d;
+    if (min_steps < 8) return 0;
+    return min_steps >= 12 ? 12 : 8;
 }
 
-bool stream_worth(int64_t tiles)
-{
-    const StreamCfg& c = stream_cfg();
-    const int64_t min_tiles = c.min_tiles >= 0 ? c.min_tiles : (int64_t)(g_cu_count > 0 ? g_cu_count : 256) * 4;
-    return tiles >= min_tiles;
-}
+bool stream_worth(int64_t tiles) { return tiles >= (int64_t)(g_cu_count > 0 ? g_cu_count : 256) * 4; }
 
 int natural_kernel(std::size_t M, std::size_t N, std::size_t K, int act)
 {
@@ -316,7 +290,7 @@ int validate_call(const void* out, const void* inp, const int8_t* w, const float
     return VVH_OK;
 }
 
-int run_call(const LinArgs& base, int kernel, int act, int outd, void* stream)
+int run_call(const LinArgs& base, int kernel, int act, int outd, void* stream, const WsSource* wsrc = nullptr)
 {
     LinArgs a = base;
     int e = 0;
@@ -374,22 +348,18 @@ int run_call(const LinArgs& base, int kernel, int act, int outd, void* stream)
                     uint64_t plane;
                     if (s > 1 && mul_ok((uint64_t)a.M * (uint64_t)a.N, (uint64_t)s * 4, &plane) && nb * s <= INT32_MAX) {
                         float* ws = nullptr;
-                        const int st = workspace_for(stream, plane, &ws);
+                        const int st = workspace_get(wsrc, stream, plane, &ws);
                         if (st != VVH_OK) return st;
                         a.ws = ws;
                         a.nsplit = s;
                         a.kstages = (int32_t)kst;
                     }
                 }
-                const int g3 = gemm3_layout(a.M, a.N, a.nsplit);
-                if (g3 > 0) {
-                    e = launch_gemm3(a, outd, g3, stream);
-                    if (e == 0 && a.nsplit > 1) e = launch_splitk_reduce(a, outd, stream);
-                    break;
-                }
+                e = launch_gemm3(a, outd, gemm3_layout(a.M, a.N, a.nsplit), stream);
+                if (e == 0 && a.nsplit > 1) e = launch_splitk_reduce(a, outd, stream);
+                break;
             }
-            e = launch_gemm(a, outd, stream);
-            if (e == 0 && a.nsplit > 1) e = launch_splitk_reduce(a, outd, stream);
+            e = launch_gemm(a, outd, stream);  // K % 64 != 0: never split
             break;
         }
         default: {
@@ -401,28 +371,6 @@ int run_call(const LinArgs& base, int kernel, int act, int outd, void* stream)
     }
     if (e != 0) return fail_hip((hipError_t)e, "kernel launch");
     return VVH_OK;
-}
-
-int linear_dev(void* out, const void* inp, const int8_t* w, const float* scales, const float* bias,
-               const void* res, std::size_t M, std::size_t N, std::size_t K, int act, int outd,
-               void* stream)
-{
-    int st = validate_call(out, inp, w, scales, M, N, K, act, outd);
-    if (st != VVH_OK || M == 0 || N == 0) return st;
-    REQUIRE_INIT();
-    LinArgs a{};
-    a.out = out;
-    a.inp = inp;
-    a.res = res;
-    a.w = w;
-    a.scales = scales;
-    a.bias = bias;
-    a.M = (int64_t)M;
-    a.N = (int64_t)N;
-    a.K = (int64_t)K;
-    a.ksplit = 1;
-    const bool aligned = K % 16 == 0 && aligned16(w) && aligned16(inp);
-    return run_call(a, choose_kernel(M, N, K, act, aligned), act, outd, stream);
 }
 
 // k_dot plan: problems ordered by K (longest rows first, so the last blocks
@@ -557,6 +505,28 @@ int build_stream_plan(Plan& p, int64_t total_tiles, int depth)
 }
 
 }  // namespace
+
+int vvh::linear_dev(void* out, const void* inp, const int8_t* w, const float* scales, const float* bias,
+               const void* res, std::size_t M, std::size_t N, std::size_t K, int act, int outd,
+               void* stream, const WsSource* wsrc)
+{
+    int st = validate_call(out, inp, w, scales, M, N, K, act, outd);
+    if (st != VVH_OK || M == 0 || N == 0) return st;
+    REQUIRE_INIT();
+    LinArgs a{};
+    a.out = out;
+    a.inp = inp;
+    a.res = res;
+    a.w = w;
+    a.scales = scales;
+    a.bias = bias;
+    a.M = (int64_t)M;
+    a.N = (int64_t)N;
+    a.K = (int64_t)K;
+    a.ksplit = 1;
+    const bool aligned = K % 16 == 0 && aligned16(w) && aligned16(inp);
+    return run_call(a, choose_kernel(M, N, K, act, aligned), act, outd, stream, wsrc);
+}
 
 extern "C" {
 
@@ -1007,7 +977,22 @@ VVH_API int vvh_linear_q8_dev(void* out, const void* inp, const int8_t* dev_weig
                               const float* dev_bias, const void* residual, size_t M, size_t N, size_t K,
                               int act_dtype, int out_dtype, void* stream)
 {
-    return linear_dev(out, inp, dev_weight, dev_scales, dev_bias, residual, M, N, K, act_dtype, out_dtype, stream);
+    return linear_dev(out, inp, dev_weight, dev_scales, dev_bias, residual, M, N, K, act_dtype, out_dtype, stream,
+                      nullptr);
+}
+
+VVH_API int vvh_workspace_release(void* stream)
+{
+    REQUIRE_INIT();
+    std::lock_guard<std::mutex> lock(g_wsmu);
+    auto it = g_ws.find(stream);
+    if (it == g_ws.end()) return VVH_OK;
+    hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) return fail_hip(e, "workspace release: synchronize");
+    for (void* p : it->second.retired) (void)hipFree(p);
+    if (it->second.p) (void)hipFree(it->second.p);
+    g_ws.erase(it);
+    return VVH_OK;
 }
 
 // The input stage runs in k_dot's activation staging only: fp16 activations,
@@ -1030,7 +1015,8 @@ VVH_API int vvh_linear_q8_dev_in(void* out, const void* inp, const int8_t* dev_w
                                  void* stream)
 {
     if (in_op == VVH_IN_NONE)
-        return linear_dev(out, inp, dev_weight, dev_scales, dev_bias, residual, M, N, K, act_dtype, out_dtype, stream);
+        return linear_dev(out, inp, dev_weight, dev_scales, dev_bias, residual, M, N, K, act_dtype, out_dtype, stream,
+                          nullptr);
     int st = validate_call(out, inp, dev_weight, dev_scales, M, N, K, act_dtype, out_dtype);
     if (st != VVH_OK) return st;
     if ((st = input_op_ok(in_op, in_w, M, K, act_dtype)) != VVH_OK) return st;
@@ -1073,7 +1059,7 @@ VVH_API int vvh_linear_q8(void* out, const void* inp, vvh_weight weight, const v
         s = it->second.scales;
         b = it->second.bias;
     }
-    return linear_dev(out, inp, w, s, b, residual, M, N, K, act_dtype, out_dtype, stream);
+    return linear_dev(out, inp, w, s, b, residual, M, N, K, act_dtype, out_dtype, stream, nullptr);
 }
 
 // ---- plans --------------------------------------------------------------------------
@@ -1303,13 +1289,8 @@ VVH_API int vvh_gemm_variant(size_t M, size_t N, size_t K, int* tile_n, int* spl
             const int64_t kst = (stages + s - 1) / s;
             s = (int)((stages + kst - 1) / kst);
         }
-        const int g3 = gemm3_layout((int64_t)M, (int64_t)N, s);
-        if (g3 > 0) {
-            v = 3;
-            tn = gemm3_tile_n(g3);
-        } else {
-            v = 2;
-        }
+        v = 3;
+        tn = gemm3_tile_n(gemm3_layout((int64_t)M, (int64_t)N, s));
     }
     if (tile_n) *tile_n = tn;
     if (splits) *splits = s;
@@ -1479,6 +1460,26 @@ VVH_API int vvh_argmax(const float* logits, size_t n, int32_t* dev_index, void* 
         if (st != VVH_OK) return st;
     }
     return ret_launch(launch_argmax(logits, (int64_t)n, dev_index, ws, stream), "argmax launch");
+}
+
+VVH_API int vvh_sample(const void* logits, int dtype, size_t n, float temperature, float top_p, uint64_t seed,
+                       int32_t step, int32_t* dev_index, void* stream)
+{
+    (void)top_p;  // accepted and ignored, as cuda_sample does (src/backend/cuda_kernels.cu:1325)
+    if (!act_ok(dtype)) return fail(VVH_ERR_INVALID_ARG, "bad dtype");
+    if (!logits || !dev_index) return fail(VVH_ERR_INVALID_ARG, "null pointer");
+    if (n == 0 || n > INT32_MAX) return fail(VVH_ERR_INVALID_ARG, "bad length %zu", n);
+    if (!(temperature >= 0.0f) || temperature == INFINITY)
+        return fail(VVH_ERR_INVALID_ARG, "temperature %g is not a finite value >= 0", (double)temperature);
+    REQUIRE_INIT();
+    float* ws = nullptr;
+    const int64_t wsb = argmax_ws_bytes((int64_t)n);
+    if (wsb > 0) {
+        const int st = workspace_for(stream, (std::size_t)wsb, &ws);
+        if (st != VVH_OK) return st;
+    }
+    return ret_launch(launch_sample(logits, dtype, (int64_t)n, temperature, seed, step, dev_index, ws, stream),
+                      "sample launch");
 }
 
 VVH_API int vvh_mirror_f32(const float* host, size_t n, int as_dtype, const void** dev)
