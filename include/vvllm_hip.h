@@ -220,6 +220,29 @@ VVH_API int vvh_linear_q8_dev(void* out, const void* inp, const int8_t* dev_weig
                               const void* residual, size_t M, size_t N, size_t K,
                               int act_dtype, int out_dtype, void* stream);
 
+/* Size of the fixed device scratch of vvh_linear_q8_dev_noalloc: the split-K
+ * partial planes of one call (M * N * 4 bytes per split).  On a 256-CU
+ * device every split the dispatcher makes fits: it splits only GEMMs of at
+ * most 128 output tiles of 128 x 128, into at most 256 blocks, i.e. at most
+ * 256 fp32 tiles = 16 MiB. */
+#define VVH_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+/* vvh_linear_q8_dev that allocates nothing: same arguments, same kernels and
+ * the same result bits as vvh_linear_q8_dev, but the split-K partial planes
+ * go to a fixed VVH_NOALLOC_SCRATCH_BYTES device array that the library
+ * holds on each device from vvh_init until the process ends, instead of the
+ * stream's workspace (which grows with hipMalloc).  No hipMalloc, hipFree or
+ * allocating library routine is called.  A call whose partial planes need
+ * more than VVH_NOALLOC_SCRATCH_BYTES returns VVH_ERR_UNSUPPORTED.
+ * No counterpart in the reference; for callers that cannot allocate: code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc.  All calls on one device share the one array, so calls that
+ * overlap in time on that device (different streams, or threads) race;
+ * calls queued in order on one stream do not. */
+VVH_API int vvh_linear_q8_dev_noalloc(void* out, const void* inp, const int8_t* dev_weight,
+                                      const float* dev_scales, const float* dev_bias,
+                                      const void* residual, size_t M, size_t N, size_t K,
+                                      int act_dtype, int out_dtype, void* stream);
+
 /* Input stages of a decode linear (no counterpart in the reference, whose
  * transformer_forward runs the operator before the linear as its own call,
  * transformer.h:133-139, 176-185).  The linear reads its activation rows

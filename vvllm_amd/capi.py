@@ -67,6 +67,8 @@ SIGNATURES = {
                               c_int, c_int, c_void_p]),
     "vvh_linear_q8_dev": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t,
                                   c_size_t, c_size_t, c_int, c_int, c_void_p]),
+    "vvh_linear_q8_dev_noalloc": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t,
+                                          c_size_t, c_size_t, c_int, c_int, c_void_p]),
     "vvh_plan_create": (c_int, [POINTER(Q8Problem), c_size_t, c_int, c_int, POINTER(c_uint64)]),
     "vvh_plan_run": (c_int, [c_uint64, c_void_p]),
     "vvh_plan_set_input_op": (c_int, [c_uint64, c_int, c_void_p, c_float]),

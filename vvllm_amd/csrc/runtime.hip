@@ -146,6 +146,36 @@ int workspace_for(void* stream, std::size_t bytes, float** out)
     return VVH_OK;
 }
 
+// ---- fixed scratch of vvh_linear_q8_dev_noalloc ------------------------------
+// The split-K partial planes of the allocation-free entry point live in this
+// file-scope device array: the code object holds it on every device the
+// library runs on, until the process ends.  In host code its name is a
+// host-side stand-in, not a device address; vvh_init looks up the device
+// address once per device (hipGetSymbolAddress, with that device current)
+// and every host use goes through g_scratch_ptr.  Every call on one device
+// shares the array; the split GEMM writes every element of each partial
+// plane before the reduction reads it, so nothing needs clearing between
+// calls.
+static __device__ __align__(256) unsigned char g_noalloc_scratch[VVH_NOALLOC_SCRATCH_BYTES];
+constexpr int kMaxDevices = 64;
+void* g_scratch_ptr[kMaxDevices] = {};
+std::mutex g_scratch_mu;
+
+int scratch_setup(int device)
+{
+    if (device < 0 || device >= kMaxDevices) return VVH_OK;  // vvh_linear_q8_dev_noalloc refuses such devices
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[device]) return VVH_OK;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(g_noalloc_scratch));
+    if (e != hipSuccess || !p) {
+        (void)hipGetLastError();
+        return fail_hip(e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress(noalloc scratch)");
+    }
+    g_scratch_ptr[device] = p;
+    return VVH_OK;
+}
+
 // A call's workspace: the stream workspace (grown with hipMalloc) when src is
 // null, else src's fixed buffer, which must be large enough.
 int workspace_get(const WsSource* src, void* stream, std::size_t bytes, float** out)
@@ -563,6 +593,8 @@ VVH_API int vvh_init(int device, char* name_buf, size_t name_buf_size)
     hipDeviceProp_t prop;
     if ((e = hipGetDeviceProperties(&prop, device)) != hipSuccess)
         return fail_hip(e, "hipGetDeviceProperties");
+    const int st = scratch_setup(device);
+    if (st != VVH_OK) return st;
     g_device = device;
     g_cu_count = prop.multiProcessorCount;
     if (name_buf && name_buf_size > 0) {
@@ -979,6 +1011,20 @@ VVH_API int vvh_linear_q8_dev(void* out, const void* inp, const int8_t* dev_weig
 {
     return linear_dev(out, inp, dev_weight, dev_scales, dev_bias, residual, M, N, K, act_dtype, out_dtype, stream,
                       nullptr);
+}
+
+VVH_API int vvh_linear_q8_dev_noalloc(void* out, const void* inp, const int8_t* dev_weight,
+                                      const float* dev_scales, const float* dev_bias, const void* residual,
+                                      size_t M, size_t N, size_t K, int act_dtype, int out_dtype, void* stream)
+{
+    REQUIRE_INIT();
+    void* scratch = g_device >= 0 && g_device < kMaxDevices ? g_scratch_ptr[g_device] : nullptr;
+    if (!scratch)
+        return fail(VVH_ERR_UNSUPPORTED, "no fixed scratch on device %d (devices 0..%d have one)", g_device,
+                    kMaxDevices - 1);
+    const WsSource src{scratch, VVH_NOALLOC_SCRATCH_BYTES};
+    return linear_dev(out, inp, dev_weight, dev_scales, dev_bias, residual, M, N, K, act_dtype, out_dtype, stream,
+                      &src);
 }
 
 VVH_API int vvh_workspace_release(void* stream)
