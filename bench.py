@@ -283,6 +283,17 @@ def cpu_ingest(projs):
             "sample": "one Qwen2.5-0.5B layer (q,k,v,o,gate,up,down), oracle restatement, one thread"}
 
 
+def host_cpu():
+    """Model name of the host CPU (lscpu's "Model name"), from /proc/cpuinfo."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(lins, budget_s):
     from oracle import oracle as O
 
@@ -319,18 +330,28 @@ def cpu_baseline(lins, budget_s):
             calls.append((f_lin, (y.ctypes.data, x.ctypes.data, q.ctypes.data, s.ctypes.data, bp, 1, l.N, l.K)))
         host_keep.append(y)
     per_pass = sum(algo_bytes(1, l.N, l.K, l.has_bias, l.has_res, 4, 4) for *_, l in host)
-    passes, t0 = 0, time.perf_counter()
-    while True:
-        for f, a in calls:
-            f(*a)
-        passes += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s:
-            break
+    # one thread pinned to one core (the reference's CPU path is single-threaded),
+    # as `taskset -c <core>` would; the process's own affinity is restored after
+    allowed = sorted(os.sched_getaffinity(0))
+    core = allowed[0]
+    os.sched_setaffinity(0, {core})
+    try:
+        passes, t0 = 0, time.perf_counter()
+        while True:
+            for f, a in calls:
+                f(*a)
+            passes += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s:
+                break
+        ingest = cpu_ingest(layer_projs(896, 128, 4864))
+    finally:
+        os.sched_setaffinity(0, set(allowed))
     return dict(value=round(per_pass * passes / el / 1e9, 3), unit="GB/s", cores=1, kind=kind,
-                ms_per_step=round(el / passes * 1e3, 3), ingest_host_path=cpu_ingest(layer_projs(896, 128, 4864)),
+                host_cpu=host_cpu(), nproc=os.cpu_count(), cpus_allowed=len(allowed), pinned_core=core,
+                ms_per_step=round(el / passes * 1e3, 3), ingest_host_path=ingest,
                 sample=(f"{passes} full passes of the 24-layer decode projection set (168 linear_q8 calls, "
-                        f"same int8 weights as the GPU run, fp32 activations) in {el:.1f} s, one thread; "
+                        f"same int8 weights as the GPU run, fp32 activations) in {el:.1f} s, one thread pinned to core {core}; "
                         + ("reference BackendCPU::linear_q8 compiled from its sources -O2 -mavx2 -mfma"
                            if kind == "reference" else "oracle restatement of BackendCPU::linear_q8")))
 

@@ -420,7 +420,7 @@ typedef enum vvh_kernel {
     VVH_KERNEL_GEMM = 4,      /* fp16 activations, LDS-tiled MFMA 32x32x16 */
     VVH_KERNEL_STREAM = 5,    /* fp16 activations, M <= 16, K > 448: persistent
                                  streaming decode (large N, or grouped plans) */
-    VVH_KERNEL_DOT = 6,       /* fp16 activations, M <= 2: VALU dot products over
+    VVH_KERNEL_DOT = 6,       /* fp16 activations, M <= 4: VALU dot products over
                                  whole cache lines of 8 weight rows */
 } vvh_kernel;
 /* Which kernel family vvh_linear_q8 would use for this call (after the

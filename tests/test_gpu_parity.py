@@ -73,7 +73,28 @@ def run_case(oracle, M, N, K, act=F16, outd=F16, bias=True, res=None, kernel=cap
     tol = TOL_F32 if (act == F32 and outd == F32) else TOL_F16
     assert np.isfinite(got).all()
     assert err <= tol, f"normalized max error {err:.3e} > {tol:.0e}"
+    if outd == F32:
+        check_f32_bound(got, ref, x[sel], q, s, b if bias else None, None if r is None else r[sel], K)
     return err
+
+
+def check_f32_bound(got, ref, x, q, s, b, r, K):
+    """fp32 outputs carry no final fp16 rounding, so they are held to the
+    fp32 accumulation bound of the oracle's own tests: both sides sum K exact
+    (fp16 x int8) or once-rounded (fp32 x int8) products in fp32, so each is
+    within K * 2^-24 * sum_k |x q| * scale of the exact value, plus the
+    roundings of the epilogue (scale, bias, residual).  A lost k tail, a
+    dropped term or fp16 partial sums exceed it by orders of magnitude."""
+    mag = (np.abs(x.astype(np.float64)) @ np.abs(q.astype(np.float64)).T) * np.abs(s.astype(np.float64))
+    extra = np.abs(ref.astype(np.float64))
+    if b is not None:
+        extra = extra + np.abs(b.astype(np.float64))
+    if r is not None:
+        extra = extra + np.abs(r.astype(np.float64))
+    bound = 2.0 * K * 2.0 ** -24 * mag + 2.0 ** -22 * extra + 1e-30
+    diff = np.abs(got.astype(np.float64) - ref.astype(np.float64))
+    worst = float((diff / bound).max()) if diff.size else 0.0
+    assert worst <= 1.0, f"fp32 output off the fp32 accumulation bound by {worst:.2f}x"
 
 
 # ---------------------------------------------------------------------------
@@ -192,6 +213,7 @@ def test_dot_kernel(gpu, oracle, M, N, K, outd):
 
 def test_decode_dispatch_on_device(gpu):
     assert capi.kernel_choice(1, 151936, 896, F16, F32) == "dot"
+    assert capi.kernel_choice(1, 9728, 896, F16, F16) == "dot"
     assert capi.kernel_choice(4, 896, 896, F16, F16) == "dot"
     assert capi.kernel_choice(5, 151936, 896, F16, F16) == "stream"
     assert capi.kernel_choice(5, 896, 896, F16, F16) == "skinny"
@@ -563,3 +585,46 @@ def test_weight_ingest_f32_and_linear(gpu, oracle):
         y = d_y.to_array(np.float32, (M, N))
         assert np.abs(y - ref).max() / np.abs(ref).max() <= TOL_F16
     capi.call("vvh_weight_release", h.value)
+
+
+def test_headline_plan_every_projection(gpu, oracle):
+    """The workload bench.py times for its headline line: 24
+    layers x {q, k, v, o, gate, up, down} of device-made seeded weights, M=1,
+    fp16 in and out, o and down adding their residual in place, as one
+    grouped plan.  One run of the plan; every one of the 168 outputs is
+    checked against the oracle on the same codes, scales, biases,
+    activations and residuals (copied back from the device)."""
+    import bench
+
+    projs = bench.layer_projs(896, 128, 4864)
+    tmp = capi.DevBuf(4864 * 896 * 4)
+    (arena, lins), = bench.build_decode_set(1, 24, projs, tmp.ptr)
+    plan = bench.make_plan(lins)
+    assert capi.plan_kernel(plan) == "dot"
+    before = []
+    for l in lins:
+        y0 = np.empty((1, l.N), np.float16)
+        capi.call("vvh_memcpy_d2h", y0.ctypes.data, l.y, y0.nbytes)
+        before.append(y0)
+    print("[case] headline plan: 168 projections, one grouped launch", flush=True)
+    capi.call("vvh_plan_run", plan, None)
+    capi.sync()
+    worst = 0.0
+    for i, l in enumerate(lins):
+        q = np.empty((l.N, l.K), np.int8)
+        s = np.empty(l.N, np.float32)
+        x = np.empty((1, l.K), np.float16)
+        y = np.empty((1, l.N), np.float16)
+        for arr, ptr in ((q, l.w), (s, l.s), (x, l.x), (y, l.y)):
+            capi.call("vvh_memcpy_d2h", arr.ctypes.data, ptr, arr.nbytes)
+        b = None
+        if l.b:
+            b = np.empty(l.N, np.float32)
+            capi.call("vvh_memcpy_d2h", b.ctypes.data, l.b, b.nbytes)
+        r = before[i].astype(np.float32) if l.has_res else None
+        ref = oracle.linear_q8(x.astype(np.float32), q, s, b, r)
+        err = float(np.abs(y.astype(np.float32) - ref).max() / np.abs(ref).max())
+        worst = max(worst, err)
+        assert err <= TOL_F16, f"projection {i} ({projs[i % 7][0]}, layer {i // 7}): {err:.3e}"
+    print(f"[case] headline plan worst normalized error {worst:.2e}", flush=True)
+    capi.call("vvh_plan_destroy", plan)

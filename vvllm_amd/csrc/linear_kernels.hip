@@ -404,17 +404,30 @@ __device__ __forceinline__ float dot16(const h8 w0, const h8 w1, const h8 x0, co
 // Epilogue of one element through global-address-space pointers (the
 // problem descriptor may come from a plan table, whose pointers the compiler
 // would otherwise treat as generic and access with flat instructions).
+// The decode epilogue acc * scale (+ bias) (+ residual) with the product
+// rounded to fp32 before the additions (the empty asm keeps the compiler from
+// fusing it into an FMA in one instantiation and not in another): both k_dot
+// variants (operands loaded early or after the k loop) share it, so their
+// outputs agree bit for bit.
+__device__ __forceinline__ float dot_epi(float acc, float sc, bool has_bias, float bi, bool has_res, float res)
+{
+    float v = acc * sc;
+    __asm__("" : "+v"(v));
+    if (has_bias) v += bi;
+    if (has_res) v += res;
+    return v;
+}
+
 template <typename OT>
 __device__ __forceinline__ void store_out_g(const LinArgs& a, int64_t m, int64_t n, float acc)
 {
-    float v = acc * *gbl(a.scales + n);
-    if (a.bias) v += *gbl(a.bias + n);
     const int64_t o = m * a.N + n;
-    if (a.res) v += (float)*gbl(static_cast<const OT*>(a.res) + o);
-    *gbl(static_cast<OT*>(a.out) + o) = (OT)v;
+    const float bi = a.bias ? *gbl(a.bias + n) : 0.0f;
+    const float rv = a.res ? (float)*gbl(static_cast<const OT*>(a.res) + o) : 0.0f;
+    *gbl(static_cast<OT*>(a.out) + o) = (OT)dot_epi(acc, *gbl(a.scales + n), a.bias != nullptr, bi, a.res != nullptr, rv);
 }
 
-template <typename OT, int MT, bool XLDS>
+template <typename OT, int MT, bool XLDS, bool EARLY>
 __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* smem)
 {
     // activations in the ring take 8 VGPRs per row and slot: halve the ring
@@ -494,9 +507,32 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
         }
     };
 
-    // (the weight ring is issued after the staging: issued before it, the
-    // ring's 64 VGPRs stay live through the staging and occupancy drops from
-    // 5 to 3 waves per SIMD, measured 5.9 -> 5.3 TB/s on the decode set)
+    // EARLY (launches with few blocks, where latency and not occupancy sets
+    // the time): the epilogue operands of the lane's two rows and the weight
+    // ring are requested first, so the activation staging below waits for
+    // them together instead of one after the other, and nothing is loaded
+    // after the k loop.  Otherwise the ring is issued after the staging:
+    // issued before it, the ring's 64 VGPRs stay live through the staging
+    // and occupancy drops from 5 to 3 waves per SIMD (measured 5.9 -> 5.3
+    // TB/s on the grouped decode set).
+    float e_sc[2] = {0.0f, 0.0f}, e_bi[2] = {0.0f, 0.0f};
+    OT e_res[MT][2];
+    if constexpr (EARLY) {
+        const float* bp = a.bias ? a.bias : a.scales;  // absent bias / residual: in-bounds reads, unused
+        const OT* rp = a.res ? static_cast<const OT*>(a.res) : reinterpret_cast<const OT*>(a.scales);
+        const int64_t rows[2] = {rowA, rowB};
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            e_sc[h] = *gbl(a.scales + rows[h]);
+            e_bi[h] = *gbl(bp + rows[h]);
+#pragma unroll
+            for (int m = 0; m < MT; m++) e_res[m][h] = *gbl(rp + (a.res && m < a.M ? m * a.N : 0) + rows[h]);
+        }
+        if (active) {
+#pragma unroll
+            for (int u = 0; u < D; u++) issue(u, (int32_t)c.s0 + u);
+        }
+    }
     if (XLDS) {
         // activations to LDS (through the input stage a.xop), 4 chunks of 8
         // values per thread per round; a round's loads are clamped into the
@@ -576,8 +612,10 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
 
     int32_t s = (int32_t)c.s0;
     if (active) {
+        if constexpr (!EARLY) {
 #pragma unroll
-        for (int u = 0; u < D; u++) issue(u, s + u);
+            for (int u = 0; u < D; u++) issue(u, s + u);
+        }
         // while steps remain beyond the ring: consume slot u, refill it with
         // the step D ahead (a refill past the range re-reads the last step,
         // so every wait in the loop counts the same D - 1 steps of loads)
@@ -631,8 +669,19 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
 #pragma unroll
         for (int m = 0; m < MT; m++) {
             if (m < a.M) {
-                if (n0 + r < a.N) store_out_g<OT>(a, m, n0 + r, accA[m]);
-                if (n0 + 8 + r < a.N) store_out_g<OT>(a, m, n0 + 8 + r, accB[m]);
+                if constexpr (EARLY) {
+#pragma unroll
+                    for (int h = 0; h < 2; h++) {
+                        const int64_t n = n0 + 8 * h + r;
+                        if (n < a.N)
+                            *gbl(static_cast<OT*>(a.out) + m * a.N + n) =
+                                (OT)dot_epi(h ? accB[m] : accA[m], e_sc[h], a.bias != nullptr, e_bi[h],
+                                            a.res != nullptr, (float)e_res[m][h]);
+                    }
+                } else {
+                    if (n0 + r < a.N) store_out_g<OT>(a, m, n0 + r, accA[m]);
+                    if (n0 + 8 + r < a.N) store_out_g<OT>(a, m, n0 + 8 + r, accB[m]);
+                }
             }
         }
     }
@@ -640,15 +689,15 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
 
 // XLDS = the activations are staged in LDS (dot_x_in_lds, decided on the
 // host for the launch: for a grouped launch it must hold for every problem).
-template <typename OT, int MT, bool XLDS>
+template <typename OT, int MT, bool XLDS, bool EARLY>
 __global__ __launch_bounds__(256) void k_dot(LinArgs a)
 {
     extern __shared__ __attribute__((aligned(16))) char dot_smem[];
-    dot_body<OT, MT, XLDS>(a, blockIdx.x, dot_smem);
+    dot_body<OT, MT, XLDS, EARLY>(a, blockIdx.x, dot_smem);
 }
 
 // Grouped launch: block b serves problem block_prob[b].
-template <typename OT, int MT, bool XLDS>
+template <typename OT, int MT, bool XLDS, bool EARLY>
 __global__ __launch_bounds__(256) void k_dot_grouped(const LinArgs* __restrict__ table,
                                                      const int32_t* __restrict__ block_prob)
 {
@@ -656,7 +705,7 @@ __global__ __launch_bounds__(256) void k_dot_grouped(const LinArgs* __restrict__
     const int b = blockIdx.x;
     const int p = *cst(block_prob + b);
     const LinArgs a = table[p];
-    dot_body<OT, MT, XLDS>(a, b - a.block_begin, dot_smem);
+    dot_body<OT, MT, XLDS, EARLY>(a, b - a.block_begin, dot_smem);
 }
 
 // ---------------------------------------------------------------------------
@@ -1199,55 +1248,74 @@ int launch_skinny_grouped(const LinArgs* dev_table, int count, int64_t total_blo
     return (int)hipGetLastError();
 }
 
-template <int MT, bool XLDS>
+template <int MT, bool XLDS, bool EARLY>
 static void dot_launch(const LinArgs& a, int out, dim3 grid, size_t lds, hipStream_t s)
 {
-    if (out == VVH_F32) hipLaunchKernelGGL((k_dot<float, MT, XLDS>), grid, dim3(256), lds, s, a);
-    else hipLaunchKernelGGL((k_dot<f16, MT, XLDS>), grid, dim3(256), lds, s, a);
+    if (out == VVH_F32) hipLaunchKernelGGL((k_dot<float, MT, XLDS, EARLY>), grid, dim3(256), lds, s, a);
+    else hipLaunchKernelGGL((k_dot<f16, MT, XLDS, EARLY>), grid, dim3(256), lds, s, a);
 }
 
-int launch_dot(const LinArgs& a, int out, void* stream)
+template <int MT, bool XLDS>
+static void dot_launch_e(const LinArgs& a, int out, bool early, dim3 grid, size_t lds, hipStream_t s)
+{
+    if (early) dot_launch<MT, XLDS, true>(a, out, grid, lds, s);
+    else dot_launch<MT, XLDS, false>(a, out, grid, lds, s);
+}
+
+int launch_dot(const LinArgs& a, int out, bool early, void* stream)
 {
     const dim3 grid((unsigned)dot_blocks(a));
     const size_t lds = dot_lds_bytes(a.M, a.K);
     const bool xl = dot_x_in_lds(a.M, a.K);
     if (a.M <= 1) {
-        if (xl) dot_launch<1, true>(a, out, grid, lds, S(stream));
-        else dot_launch<1, false>(a, out, grid, lds, S(stream));
+        if (xl) dot_launch_e<1, true>(a, out, early, grid, lds, S(stream));
+        else dot_launch_e<1, false>(a, out, early, grid, lds, S(stream));
     } else if (a.M <= 2) {
-        if (xl) dot_launch<2, true>(a, out, grid, lds, S(stream));
-        else dot_launch<2, false>(a, out, grid, lds, S(stream));
+        if (xl) dot_launch_e<2, true>(a, out, early, grid, lds, S(stream));
+        else dot_launch_e<2, false>(a, out, early, grid, lds, S(stream));
     } else {
-        if (xl) dot_launch<4, true>(a, out, grid, lds, S(stream));
-        else dot_launch<4, false>(a, out, grid, lds, S(stream));
+        if (xl) dot_launch_e<4, true>(a, out, early, grid, lds, S(stream));
+        else dot_launch_e<4, false>(a, out, early, grid, lds, S(stream));
     }
     return (int)hipGetLastError();
 }
 
-template <int MT, bool XLDS>
+template <int MT, bool XLDS, bool EARLY>
 static void dot_grouped_launch(const LinArgs* table, const int32_t* block_prob, int out, dim3 grid, size_t lds,
                                hipStream_t s)
 {
-    if (out == VVH_F32) hipLaunchKernelGGL((k_dot_grouped<float, MT, XLDS>), grid, dim3(256), lds, s, table, block_prob);
-    else hipLaunchKernelGGL((k_dot_grouped<f16, MT, XLDS>), grid, dim3(256), lds, s, table, block_prob);
+    if (out == VVH_F32)
+        hipLaunchKernelGGL((k_dot_grouped<float, MT, XLDS, EARLY>), grid, dim3(256), lds, s, table, block_prob);
+    else hipLaunchKernelGGL((k_dot_grouped<f16, MT, XLDS, EARLY>), grid, dim3(256), lds, s, table, block_prob);
+}
+
+template <int MT, bool XLDS>
+static void dot_grouped_launch_e(const LinArgs* table, const int32_t* block_prob, int out, bool early, dim3 grid,
+                                 size_t lds, hipStream_t s)
+{
+    if (early) dot_grouped_launch<MT, XLDS, true>(table, block_prob, out, grid, lds, s);
+    else dot_grouped_launch<MT, XLDS, false>(table, block_prob, out, grid, lds, s);
 }
 
 int launch_dot_grouped(const LinArgs* dev_table, const int32_t* dev_block_prob, int64_t total_blocks, int max_m,
-                       bool x_in_lds, size_t lds_bytes, int out, void* stream)
+                       bool x_in_lds, size_t lds_bytes, int out, bool early, void* stream)
 {
     const dim3 grid((unsigned)total_blocks);
+    hipStream_t s = S(stream);
     if (max_m <= 1) {
-        if (x_in_lds) dot_grouped_launch<1, true>(dev_table, dev_block_prob, out, grid, lds_bytes, S(stream));
-        else dot_grouped_launch<1, false>(dev_table, dev_block_prob, out, grid, lds_bytes, S(stream));
+        if (x_in_lds) dot_grouped_launch_e<1, true>(dev_table, dev_block_prob, out, early, grid, lds_bytes, s);
+        else dot_grouped_launch_e<1, false>(dev_table, dev_block_prob, out, early, grid, lds_bytes, s);
     } else if (max_m <= 2) {
-        if (x_in_lds) dot_grouped_launch<2, true>(dev_table, dev_block_prob, out, grid, lds_bytes, S(stream));
-        else dot_grouped_launch<2, false>(dev_table, dev_block_prob, out, grid, lds_bytes, S(stream));
+        if (x_in_lds) dot_grouped_launch_e<2, true>(dev_table, dev_block_prob, out, early, grid, lds_bytes, s);
+        else dot_grouped_launch_e<2, false>(dev_table, dev_block_prob, out, early, grid, lds_bytes, s);
     } else {
-        if (x_in_lds) dot_grouped_launch<4, true>(dev_table, dev_block_prob, out, grid, lds_bytes, S(stream));
-        else dot_grouped_launch<4, false>(dev_table, dev_block_prob, out, grid, lds_bytes, S(stream));
+        if (x_in_lds) dot_grouped_launch_e<4, true>(dev_table, dev_block_prob, out, early, grid, lds_bytes, s);
+        else dot_grouped_launch_e<4, false>(dev_table, dev_block_prob, out, early, grid, lds_bytes, s);
     }
     return (int)hipGetLastError();
 }
+
+
 
 template <typename OT, int D, int MR>
 static void stream_launch(const StreamArgs& s, dim3 grid, hipStream_t st)

@@ -265,6 +265,14 @@ int stream_depth(int64_t min_steps)
 
 bool stream_worth(int64_t tiles) { return tiles >= (int64_t)(g_cu_count > 0 ? g_cu_count : 256) * 4; }
 
+// k_dot launches of at most one block per CU take the variant that requests
+// its weights and epilogue operands before staging the activations: they are
+// bounded by the latency of those loads, not by occupancy.  (Measured per
+// call in a graph, Qwen2.5-0.5B shapes: q 4.30 -> 4.16 us, o 4.76 -> 4.37 us;
+// at 304 blocks, gate 5.36 -> 5.75 us, so larger launches keep the other.)
+constexpr int64_t kDotEarlyBlocksPerCu = 1;
+bool dot_early(int64_t blocks) { return blocks <= (int64_t)(g_cu_count > 0 ? g_cu_count : 256) * kDotEarlyBlocksPerCu; }
+
 int natural_kernel(std::size_t M, std::size_t N, std::size_t K, int act)
 {
     if (act == VVH_F32) return K_GEMV_F32;
@@ -352,7 +360,7 @@ int run_call(const LinArgs& base, int kernel, int act, int outd, void* stream, c
             const int64_t tiles = (a.N + kDecodeTileN - 1) / kDecodeTileN;
             a.ksplit = choose_ksplit(tiles, a.K, kDotStep);
             if (dot_blocks(a) > INT32_MAX) return fail(VVH_ERR_UNSUPPORTED, "problem too large for the decode grid");
-            e = launch_dot(a, outd, stream);
+            e = launch_dot(a, outd, dot_early(dot_blocks(a)), stream);
             break;
         }
         case K_SKINNY: {
@@ -1204,7 +1212,7 @@ VVH_API int vvh_plan_run(vvh_plan plan, void* stream)
     }
     if (p->dot) {
         const int e = launch_dot_grouped(p->sargs.table, p->dev_block_prob, p->total_blocks, p->max_m, p->x_in_lds,
-                                         p->lds_bytes, p->out, stream);
+                                         p->lds_bytes, p->out, dot_early(p->total_blocks), stream);
         return e == 0 ? VVH_OK : fail_hip((hipError_t)e, "grouped dot launch");
     }
     if (p->stream) {
