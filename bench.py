@@ -647,6 +647,55 @@ def extras(ev, sets, projs, tmp_w, args):
     out["prefill_gemm"] = gemm
     print(f"[bench] gemm M512 gate_up {gemm['gate_up_M512']['us']} us", file=sys.stderr, flush=True)
 
+    # (4b) fp32 activations (the reference's default mode) on the prefill
+    # shapes: the dispatched kernel (the MFMA GEMM on split fp16 high/low
+    # parts from M = 32) beside the fp32 VALU kernel forced, across the
+    # crossover
+    f32 = {}
+    for M in (8, 16, 32, 64, 128, 512, 2048):
+        for name, N, K, res in (("gate_up", QWEN05["inter"], QWEN05["hidden"], False),
+                                ("down", QWEN05["hidden"], QWEN05["inter"], True)):
+            if name == "down" and M not in (32, 512, 2048):
+                continue
+            _ar, reps = rotation(tmp_w, M, N, K, False, res, 950, F32, F32)
+            row = {"M": M, "N": N, "K": K, "kernel": capi.kernel_choice(M, N, K, F32, F32)}
+            for fam, kern in (("auto", capi.KERNEL_AUTO), ("gemm", capi.KERNEL_GEMM),
+                              ("gemv_f32", capi.KERNEL_GEMV_F32)):
+                capi.set_kernel(kern)
+                try:
+                    us = timed_rotation(ev, reps, 30) * 1e3
+                finally:
+                    capi.set_kernel(capi.KERNEL_AUTO)
+                row[f"{fam}_us"] = round(us, 2)
+                row[f"{fam}_TFLOPS"] = round(reps[0].flops / (us * 1e-6) / 1e12, 1)
+            del reps, _ar
+            f32[f"{name}_M{M}"] = row
+    out["prefill_gemm_f32"] = f32
+    print(f"[bench] fp32 gemm M512 gate_up {f32['gate_up_M512']['auto_us']} us "
+          f"(fp32 VALU kernel {f32['gate_up_M512']['gemv_f32_us']} us)", file=sys.stderr, flush=True)
+
+    # (4c) the decode families side by side at small M (fp16), Qwen2.5-1.5B
+    # shapes: the measurement behind the crossovers of the dispatcher
+    fams = {}
+    for name, N, K in (("qo", 1536, 1536), ("gate_up", 8960, 1536), ("down", 1536, 8960)):
+        for M in (1, 2, 4, 8, 16, 32):
+            _ar, reps = rotation(tmp_w, M, N, K, False, False, 1300)
+            row = {"auto": kernel_name(M, N, K)}
+            for fam, kern in (("dot", capi.KERNEL_DOT), ("skinny", capi.KERNEL_SKINNY),
+                              ("stream", capi.KERNEL_STREAM), ("gemm", capi.KERNEL_GEMM)):
+                if capi.load().vvh_linear_q8_choice(M, N, K, F16, F16) < 0:
+                    continue
+                capi.set_kernel(kern)
+                try:
+                    if capi.kernel_choice(M, N, K, F16, F16) != fam:
+                        continue
+                    row[f"{fam}_us"] = round(timed_rotation(ev, reps, 30) * 1e3, 2)
+                finally:
+                    capi.set_kernel(capi.KERNEL_AUTO)
+            del reps, _ar
+            fams[f"{name}_M{M}"] = row
+    out["decode_families"] = fams
+
     # (5) Qwen2.5-1.5B shapes, M sweep
     sweep = {}
     for M in (1, 4, 16, 64, 256):

@@ -20,8 +20,9 @@
  *     Launches are asynchronous on it; errors of the launch itself are
  *     reported, errors of the kernel's execution surface at the next
  *     synchronising call.
- *   - Split-K GEMMs, multi-chunk decode attention and multi-block sampling
- *     use a per-stream workspace that grows on demand (hipMalloc, to at
+ *   - Split-K GEMMs, fp32-activation GEMMs (M * K * 4 + M * 4 bytes for the
+ *     split activations), multi-chunk decode attention and multi-block
+ *     sampling use a per-stream workspace that grows on demand (hipMalloc, to at
  *     least twice its size, never below 1 MiB).  Under HIP graph capture it
  *     cannot grow: run the same calls once on that stream before capturing
  *     (decode attention needs at most 512 * (num_heads / num_kv_heads) *
@@ -205,9 +206,13 @@ VVH_API int vvh_weight_stats(uint64_t* count, uint64_t* bytes);
  *     in-place residual connection of include/vvllm/model/transformer.h:
  *     165-166, 187-188).  Any other overlap of out with inp is undefined.
  *   - The dot product is accumulated in fp32 from the exact int8 codes;
- *     fp16 activations are used as given (no re-rounding); fp32 activations
- *     stay fp32 (the reference's CUDA fp32 mode rounds them to fp16 first,
- *     backend_cuda.cc:205-211; this library does not).
+ *     fp16 activations are used as given (no re-rounding).  fp32
+ *     activations are not rounded to fp16 as the reference's CUDA fp32 mode
+ *     does (backend_cuda.cc:205-211): the decode kernels (M < 32, or
+ *     K % 64 != 0) use them as they are; the GEMM (M >= 32) multiplies each
+ *     row, scaled by a power of two, as a pair of fp16 values (high part,
+ *     then the exact remainder rounded to fp16), about 22 significant bits
+ *     of each activation, with exact products and fp32 accumulation.
  *   - Epilogue in fp32, one rounding to out_dtype:
  *     out = acc*scale + bias + residual.
  *   - M == 0 or N == 0 is a no-op; K == 0 gives bias (+ residual). */
@@ -230,9 +235,11 @@ VVH_API int vvh_linear_q8_dev(void* out, const void* inp, const int8_t* dev_weig
  * the same result bits as vvh_linear_q8_dev, but the split-K partial planes
  * go to a fixed VVH_NOALLOC_SCRATCH_BYTES device array that the library
  * holds on each device from vvh_init until the process ends, instead of the
- * stream's workspace (which grows with hipMalloc).  No hipMalloc, hipFree or
- * allocating library routine is called.  A call whose partial planes need
- * more than VVH_NOALLOC_SCRATCH_BYTES returns VVH_ERR_UNSUPPORTED.
+ * stream's workspace (which grows with hipMalloc); so do the split
+ * activations of an fp32-activation GEMM (M >= 32: M * K * 4 + M * 4 bytes).
+ * No hipMalloc, hipFree or allocating library routine is called.  A call
+ * whose workspace needs more than VVH_NOALLOC_SCRATCH_BYTES returns
+ * VVH_ERR_UNSUPPORTED.
  * No counterpart in the reference; for callers that cannot allocate: code
  * under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc.  All calls on one device share the one array, so calls that
@@ -247,7 +254,9 @@ VVH_API int vvh_linear_q8_dev_noalloc(void* out, const void* inp, const int8_t* 
  * transformer_forward runs the operator before the linear as its own call,
  * transformer.h:133-139, 176-185).  The linear reads its activation rows
  * through the stage, with the same arithmetic and fp16 rounding as the
- * standalone operator, so the result equals operator-then-linear exactly. */
+ * standalone operator, and runs on the k_dot family (VVH_KERNEL_DOT), so the
+ * result equals the operator followed by vvh_linear_q8_dev on that family
+ * exactly (the automatic choice for M <= 2). */
 enum {
     VVH_IN_NONE = 0,
     VVH_IN_RMS_NORM = 1,  /* rows of inp -> vvh_rms_norm(in_w, in_eps) (:68-76) */
@@ -415,9 +424,11 @@ VVH_API int vvh_mirror_release(const float* host);
 typedef enum vvh_kernel {
     VVH_KERNEL_AUTO = 0,      /* size-based choice (default) */
     VVH_KERNEL_GENERIC = 1,   /* any shape / alignment, one thread per output */
-    VVH_KERNEL_GEMV_F32 = 2,  /* fp32 activations, VALU dot products */
+    VVH_KERNEL_GEMV_F32 = 2,  /* fp32 activations, M < 32: VALU dot products */
     VVH_KERNEL_SKINNY = 3,    /* fp16 activations, M <= 16, MFMA 16x16x32 */
-    VVH_KERNEL_GEMM = 4,      /* fp16 activations, LDS-tiled MFMA 32x32x16 */
+    VVH_KERNEL_GEMM = 4,      /* LDS-tiled MFMA 32x32x16: fp16 activations, or
+                                 fp32 activations (K % 64 == 0) split into
+                                 fp16 high and low parts */
     VVH_KERNEL_STREAM = 5,    /* fp16 activations, M <= 16, K > 448: persistent
                                  streaming decode (large N, or grouped plans) */
     VVH_KERNEL_DOT = 6,       /* fp16 activations, M <= 4: VALU dot products over

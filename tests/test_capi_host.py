@@ -152,9 +152,15 @@ def test_dispatch_choice():
     try:
         capi.set_kernel(capi.KERNEL_AUTO)
         assert ch(1, 896, 896, capi.F32, capi.F32) == "gemv_f32"      # config 1
+        assert ch(31, 4864, 896, capi.F32, capi.F32) == "gemv_f32"
+        assert ch(32, 4864, 896, capi.F32, capi.F32) == "gemm"        # fp32 prefill on MFMA
+        assert ch(512, 4864, 880, capi.F32, capi.F32) == "gemv_f32"   # K % 64 != 0
         assert ch(1, 151936, 896, capi.F16, capi.F32) == "dot"        # config 3 (M = 1)
         assert ch(1, 896, 896, capi.F16, capi.F16) == "dot"           # config 2 (M = 1)
-        assert ch(4, 896, 896, capi.F16, capi.F16) == "dot"           # M <= 4
+        assert ch(2, 896, 896, capi.F16, capi.F16) == "dot"           # M <= 2
+        assert ch(3, 896, 896, capi.F16, capi.F16) == "skinny"        # M = 3..16
+        assert ch(4, 1536, 8960, capi.F16, capi.F16) == "gemm"        # long rows, few tiles: split-K GEMM
+        assert ch(2, 1536, 8960, capi.F16, capi.F16) == "dot"
         assert ch(5, 151936, 896, capi.F16, capi.F32) == "stream"     # 9496 tiles
         assert ch(16, 4864, 896, capi.F16, capi.F16) == "skinny"      # 304 tiles: too few to stream
         assert ch(5, 151936, 448, capi.F16, capi.F16) == "skinny"     # 7 k steps: too short to stream
@@ -164,7 +170,8 @@ def test_dispatch_choice():
         assert ch(4, 16, 0, capi.F16, capi.F16) == "generic"          # K == 0
         capi.set_kernel(capi.KERNEL_GEMM)
         assert ch(1, 896, 896, capi.F16, capi.F16) == "gemm"
-        assert ch(1, 896, 896, capi.F32, capi.F32) == "generic"       # cannot serve fp32
+        assert ch(1, 896, 896, capi.F32, capi.F32) == "gemm"          # fp32 split into fp16 hi/lo
+        assert ch(40, 896, 880, capi.F32, capi.F32) == "generic"      # fp32 needs K % 64 == 0
         capi.set_kernel(capi.KERNEL_SKINNY)
         assert ch(64, 896, 896, capi.F16, capi.F16) == "generic"      # M > 16
         capi.set_kernel(capi.KERNEL_DOT)

@@ -10,6 +10,7 @@ standalone kernels themselves are checked against the oracle in
 test_gpu_ops.py and test_gpu_parity.py.  Whole decode steps of the fused
 harness must reproduce the unfused step's logits exactly.
 """
+import contextlib
 import ctypes
 
 import numpy as np
@@ -20,6 +21,17 @@ from vvllm_amd import qwen2_decode as qd
 
 pytestmark = pytest.mark.gpu
 F16, F32 = capi.F16, capi.F32
+
+
+@contextlib.contextmanager
+def dot_kernel():
+    """The unfused reference on k_dot, the family the input stages run on
+    (automatic dispatch takes it only up to M = 2)."""
+    capi.set_kernel(capi.KERNEL_DOT)
+    try:
+        yield
+    finally:
+        capi.set_kernel(capi.KERNEL_AUTO)
 
 
 def q8_weight(rng, N, K):
@@ -42,7 +54,8 @@ def test_rms_norm_stage(gpu, M, N, K):
     ref, got = capi.DevBuf.from_array(res), capi.DevBuf.from_array(res)
     eps = 1e-6
     capi.call("vvh_rms_norm", dn.ptr, dx.ptr, dw.ptr, M, K, eps, F16, None)
-    capi.call("vvh_linear_q8_dev", ref.ptr, dn.ptr, dq.ptr, ds.ptr, db.ptr, ref.ptr, M, N, K, F16, F16, None)
+    with dot_kernel():  # the stage runs on k_dot: compare with the same family
+        capi.call("vvh_linear_q8_dev", ref.ptr, dn.ptr, dq.ptr, ds.ptr, db.ptr, ref.ptr, M, N, K, F16, F16, None)
     capi.call("vvh_linear_q8_dev_in", got.ptr, dx.ptr, dq.ptr, ds.ptr, db.ptr, got.ptr, M, N, K, F16, F16,
               capi.IN_RMS_NORM, dw.ptr, eps, None)
     a, b = ref.to_array(np.float16, (M, N)), got.to_array(np.float16, (M, N))
@@ -63,7 +76,8 @@ def test_silu_mul_stage(gpu, M, N, K, outd):
     for m in range(M):  # the standalone operator, row by row as the model calls it
         capi.call("vvh_eltwise", capi.OP_SILU_MUL, dg.addr(m * K * 2), dgu.addr(m * 4 * K), dgu.addr(m * 4 * K + 2 * K),
                   K, F16, None)
-    capi.call("vvh_linear_q8_dev", ref.ptr, dg.ptr, dq.ptr, ds.ptr, None, None, M, N, K, F16, outd, None)
+    with dot_kernel():
+        capi.call("vvh_linear_q8_dev", ref.ptr, dg.ptr, dq.ptr, ds.ptr, None, None, M, N, K, F16, outd, None)
     capi.call("vvh_linear_q8_dev_in", got.ptr, dgu.ptr, dq.ptr, ds.ptr, None, None, M, N, K, F16, outd,
               capi.IN_SILU_MUL, None, 0.0, None)
     u = np.uint16 if outd == F16 else np.uint32

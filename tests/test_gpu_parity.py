@@ -214,7 +214,9 @@ def test_dot_kernel(gpu, oracle, M, N, K, outd):
 def test_decode_dispatch_on_device(gpu):
     assert capi.kernel_choice(1, 151936, 896, F16, F32) == "dot"
     assert capi.kernel_choice(1, 9728, 896, F16, F16) == "dot"
-    assert capi.kernel_choice(4, 896, 896, F16, F16) == "dot"
+    assert capi.kernel_choice(2, 896, 896, F16, F16) == "dot"
+    assert capi.kernel_choice(4, 896, 896, F16, F16) == "skinny"
+    assert capi.kernel_choice(4, 1536, 8960, F16, F16) == "gemm"
     assert capi.kernel_choice(5, 151936, 896, F16, F16) == "stream"
     assert capi.kernel_choice(5, 896, 896, F16, F16) == "skinny"
     assert capi.kernel_choice(5, 4864, 448, F16, F16) == "skinny"  # 7 k steps: too short to stream
@@ -402,7 +404,10 @@ def test_dot_plan_single_launch(gpu, oracle, outd):
 
 
 def test_dot_plan_several_rows(gpu, oracle):
-    assert _plan_case(oracle, DOT_PLAN_M4, F16, capi.KERNEL_AUTO, seed=550, expect="dot") == 1
+    """k_dot_grouped with up to 4 activation rows (forced: automatic dispatch
+    takes k_dot only up to M = 2, so this plan runs on k_skinny_grouped)."""
+    assert _plan_case(oracle, DOT_PLAN_M4, F16, capi.KERNEL_DOT, seed=550, expect="dot") == 1
+    assert _plan_case(oracle, DOT_PLAN_M4, F16, capi.KERNEL_AUTO, seed=551, expect="skinny") == 1
 
 
 def test_dot_plan_without_lds_activations(gpu, oracle):
@@ -628,3 +633,49 @@ def test_headline_plan_every_projection(gpu, oracle):
         assert err <= TOL_F16, f"projection {i} ({projs[i % 7][0]}, layer {i // 7}): {err:.3e}"
     print(f"[case] headline plan worst normalized error {worst:.2e}", flush=True)
     capi.call("vvh_plan_destroy", plan)
+
+
+# ---------------------------------------------------------------------------
+# fp32 activations on the MFMA GEMM (split into scaled fp16 high/low parts)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("outd", [F32, F16])
+@pytest.mark.parametrize("M,N,K,res", [(16, 4864, 896, None), (32, 896, 896, "sep"), (128, 4864, 896, None),
+                                       (512, 4864, 896, None), (512, 896, 4864, "inplace"),
+                                       (130, 250, 4864, "sep"), (300, 776, 256, "inplace")])
+def test_fp32_gemm(gpu, oracle, M, N, K, res, outd):
+    """The reference's default (fp32) mode on the prefill GEMM: fp32 in,
+    fp32 or fp16 out, against the oracle at the fp32 bar (1e-4 and, for fp32
+    outputs, the fp32 accumulation bound).  Includes split-K (K = 4864 with
+    few tiles), edge tiles (N = 250, 776; M = 130, 300) and M = 16 forced."""
+    kern = capi.KERNEL_GEMM if M < 32 else capi.KERNEL_AUTO
+    if M >= 32:
+        assert capi.kernel_choice(M, N, K, F32, outd) == "gemm"
+    run_case(oracle, M, N, K, F32, outd, bias=bool(N % 2 == 0), res=res, kernel=kern, seed=3 * M + N + K)
+
+
+def test_fp32_gemm_scaled_rows(gpu, oracle):
+    """Rows whose range needs the per-row power-of-two scaling: values far
+    beyond fp16's range (1e5 .. 3e6), a row of tiny values (1e-30), an
+    all-zero row, and a row mixing huge and tiny values; every output within
+    the fp32 accumulation bound of the oracle."""
+    M, N, K = 64, 384, 896
+    rng = np.random.default_rng(8)
+    q, s, b = weights(N, K, 8, oracle)
+    x = rng.normal(0, 1, (M, K)).astype(np.float32)
+    x[1] *= np.float32(1e5)
+    x[2] *= np.float32(3e6)
+    x[3] *= np.float32(1e-30)
+    x[4] = 0.0
+    x[5, ::2] *= np.float32(1e4)
+    x[5, 1::2] *= np.float32(1e-4)
+    d = [capi.DevBuf.from_array(a) for a in (q, s, b, x)]
+    y = capi.DevBuf(M * N * 4)
+    print("[case] fp32 gemm scaled rows", flush=True)
+    assert capi.kernel_choice(M, N, K, F32, F32) == "gemm"
+    capi.linear_q8_dev(y, d[3], d[0], d[1], d[2], None, M, N, K, F32, F32)
+    capi.sync()
+    got = y.to_array(np.float32, (M, N))
+    ref = oracle.linear_q8(x, q, s, b)
+    assert np.isfinite(got).all()
+    np.testing.assert_array_equal(got[4], b)  # zero row: the bias exactly
+    check_f32_bound(got, ref, x, q, s, b, None, K)

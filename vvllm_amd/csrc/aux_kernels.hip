@@ -131,6 +131,61 @@ __global__ __launch_bounds__(256) void k_fill_normal(T* __restrict__ d, int64_t 
     }
 }
 
+// ---------------------------------------------------------------------------
+// fp32 activations for the fp16 MFMA GEMM: row m of x [M, K] becomes row m of
+// xs [M, 2K] fp16, the high parts hi_k = fp16(x_k * s) followed by the low
+// parts lo_k = fp16(x_k * s - hi_k), with s = 2^p chosen per row so that the
+// row's largest |x| * s lies in [2^14, 2^15) (in range for fp16 with room for
+// its 11-bit significand), and rs[m] = 1/s.  x_k * s is exact (a power of
+// two), x_k * s - hi_k is exact (Sterbenz), so hi + lo carries x_k * s to
+// about 22 bits (or to the fp16 subnormal step 2^-24 of the scaled row); the
+// int8 x fp16 products of both parts are exact in the GEMM's fp32
+// accumulation.  A row without a finite nonzero maximum (all zeros, or
+// containing Inf or NaN) keeps s = 1, so Inf and NaN reach the sums as such.
+// One block per row.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_split_f32(const float* __restrict__ x, int64_t K, f16* __restrict__ xs,
+                                                   float* __restrict__ rs)
+{
+    __shared__ float part[4];
+    const int64_t m = blockIdx.x;
+    const float* xr = x + m * K;
+    float mx = 0.0f;
+    // an Inf or NaN anywhere in the row makes the row maximum Inf
+    for (int64_t k = threadIdx.x; k < K; k += 256) {
+        const float v = __builtin_fabsf(xr[k]);
+        mx = __builtin_isfinite(v) ? fmaxf(mx, v) : __builtin_inff();
+    }
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3]));
+    int p = 0;
+    if (mx > 0.0f && __builtin_isfinite(mx)) {
+        int e;
+        (void)frexpf(mx, &e);          // mx = f * 2^e, f in [0.5, 1)
+        p = 15 - e;                    // mx * 2^p in [2^14, 2^15)
+        p = p < -126 ? -126 : (p > 126 ? 126 : p);
+    }
+    const float s = ldexpf(1.0f, p);
+    if (threadIdx.x == 0) rs[m] = ldexpf(1.0f, -p);
+    f16* hr = xs + m * 2 * K;
+    for (int64_t k = threadIdx.x; k < K; k += 256) {
+        const float v = xr[k] * s;
+        const f16 hi = (f16)v;
+        hr[k] = hi;
+        hr[K + k] = __builtin_isfinite((float)hi) ? (f16)(v - (float)hi) : (f16)0.0f;
+    }
+}
+
+int launch_split_f32(const float* x, int64_t M, int64_t K, void* xs, float* rs, void* stream)
+{
+    if (M <= 0) return 0;
+    hipLaunchKernelGGL(k_split_f32, dim3((unsigned)M), dim3(256), 0, static_cast<hipStream_t>(stream), x, K,
+                       static_cast<f16*>(xs), rs);
+    return (int)hipGetLastError();
+}
+
 int launch_fill_normal(void* dst, int dtype, int64_t n, uint64_t seed, float mean, float std, void* stream)
 {
     const int64_t want = (n + 255) / 256;

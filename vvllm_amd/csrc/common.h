@@ -38,6 +38,12 @@ struct LinArgs {
     const float* xw;
     float xeps;
     int32_t xop;
+    // fp32 activations on the GEMM: inp holds M rows of 2 * bk fp16 values
+    // (K = 2 * bk), the high and low fp16 parts of each fp32 activation
+    // scaled by a power of two, and xrs[m] = that row's inverse scale; the
+    // codes have rows of bk (0: K).
+    int64_t bk;
+    const float* xrs;
 };
 
 // Persistent streaming decode launch (k_stream).  Work is a sequence of
@@ -191,5 +197,8 @@ int launch_convert(void* dst, int dst_dtype, const void* src, int src_dtype, int
                    void* stream);
 int launch_fill_normal(void* dst, int dtype, int64_t n, uint64_t seed, float mean, float std,
                        void* stream);
+// fp32 rows x [M, K] -> xs [M, 2K] fp16 (scaled high parts, then low parts)
+// and rs [M] (inverse scales), the activations of an fp32 call on the GEMM
+int launch_split_f32(const float* x, int64_t M, int64_t K, void* xs, float* rs, void* stream);
 
 }  // namespace vvh

@@ -139,15 +139,15 @@ __device__ __forceinline__ void gemm3_slice_last(const h8 (&a)[2][2], const h8 (
 template <int NW, int BN>
 __device__ __forceinline__ void gemm3_fill(f16* __restrict__ sa, int8_t* __restrict__ sb, __amdgpu_buffer_rsrc_t ra,
                                            __amdgpu_buffer_rsrc_t rb, const uint32_t* a_off, const uint32_t* b_off,
-                                           int wave, uint32_t k0)
+                                           int wave, uint32_t ka, uint32_t kb)
 {
     constexpr int LA = 16 / NW, LB = BN / 16 / NW;
 #pragma unroll
     for (int i = 0; i < LA; i++)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, sa + (wave * LA + i) * 512, 16, a_off[i], k0 * 2, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, sa + (wave * LA + i) * 512, 16, a_off[i], ka * 2, 0, 0);
 #pragma unroll
     for (int i = 0; i < LB; i++)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, sb + (wave * LB + i) * 1024, 16, b_off[i], k0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, sb + (wave * LB + i) * 1024, 16, b_off[i], kb, 0, 0);
 }
 
 template <typename OT, int D, int WN, int TJ>
@@ -222,11 +222,15 @@ __global__ __launch_bounds__(128 * WN, 1) void k_gemm3(LinArgs a)
 
     // buffer resources based at the tile's first row (rows past M or N read
     // the last valid row), per-lane byte offsets within them
-    const uint64_t a_bytes = (uint64_t)(a.M - m0) * a.K * 2, b_bytes = (uint64_t)(a.N - n0) * a.K;
+    // KB: row length of the codes; a.bk != 0 (split fp32 activations, whose
+    // rows hold K = 2 * KB values: hi parts, then lo parts) makes the code
+    // stages wrap around at KB
+    const int64_t KB = a.bk ? a.bk : a.K;
+    const uint64_t a_bytes = (uint64_t)(a.M - m0) * a.K * 2, b_bytes = (uint64_t)(a.N - n0) * KB;
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<f16*>(X + m0 * a.K), 0, (int)(a_bytes < 0xFFFFFFFFull ? a_bytes : 0xFFFFFFFFull), 0x00020000);
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<int8_t*>(a.w + n0 * a.K), 0, (int)(b_bytes < 0xFFFFFFFFull ? b_bytes : 0xFFFFFFFFull), 0x00020000);
+        const_cast<int8_t*>(a.w + n0 * KB), 0, (int)(b_bytes < 0xFFFFFFFFull ? b_bytes : 0xFFFFFFFFull), 0x00020000);
     uint32_t a_off[LA];
 #pragma unroll
     for (int i = 0; i < LA; i++) {
@@ -239,7 +243,7 @@ __global__ __launch_bounds__(128 * WN, 1) void k_gemm3(LinArgs a)
     for (int i = 0; i < LB; i++) {
         const int r = (wave * LB + i) * 16 + (lane >> 2);
         const int64_t gn = n0 + r < a.N ? r : a.N - 1 - n0;
-        b_off[i] = (uint32_t)(gn * a.K + swz_b(r, lane & 3) * 16);
+        b_off[i] = (uint32_t)(gn * KB + swz_b(r, lane & 3) * 16);
     }
 
     auto stage = [&](auto S) -> Stage& {
@@ -250,7 +254,8 @@ __global__ __launch_bounds__(128 * WN, 1) void k_gemm3(LinArgs a)
         else return st3;
     };
     auto issue = [&](Stage& g, int64_t kt) {
-        gemm3_fill<NW, BN>(g.a, g.b, ra, rb, a_off, b_off, wave, (uint32_t)((kbase + kt) * kGemmBK));
+        const int64_t k0 = (kbase + kt) * kGemmBK;
+        gemm3_fill<NW, BN>(g.a, g.b, ra, rb, a_off, b_off, wave, (uint32_t)k0, (uint32_t)(k0 < KB ? k0 : k0 - KB));
     };
 
     f16v acc[2][TJ];
@@ -346,6 +351,16 @@ __global__ __launch_bounds__(128 * WN, 1) void k_gemm3(LinArgs a)
             if (i + 1 < RI || erg + i * RG < kGemmBM)
 #pragma unroll
                 for (int c = 0; c < RW; c++) rr[i][c] = reinterpret_cast<const u4*>(rp + i * o_step)[c];
+    }
+    if (a.xrs) {
+        // split fp32 activations: each row's sums times its power-of-two scale
+#pragma unroll
+        for (int ti = 0; ti < 2; ti++) {
+            const int64_t m = m0 + row0 + ti * 32 + fl;
+            const float rs = a.xrs[m < a.M ? m : a.M - 1];
+#pragma unroll
+            for (int tj = 0; tj < TJ; tj++) acc[ti][tj] *= rs;
+        }
     }
 #pragma unroll
     for (int ti = 0; ti < 2; ti++) {

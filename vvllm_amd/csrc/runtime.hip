@@ -273,12 +273,34 @@ bool stream_worth(int64_t tiles) { return tiles >= (int64_t)(g_cu_count > 0 ? g_
 constexpr int64_t kDotEarlyBlocksPerCu = 1;
 bool dot_early(int64_t blocks) { return blocks <= (int64_t)(g_cu_count > 0 ? g_cu_count : 256) * kDotEarlyBlocksPerCu; }
 
+// fp32 activations take the GEMM (on their split fp16 form) from this many
+// rows on, when K % 64 == 0; below it k_gemv_f32, which streams the weights
+// once per 8 rows.
+constexpr std::size_t kGemmF32MinM = 32;
+
+// Small-M fp16 dispatch, from a sweep of every family forced on each shape
+// (bench.py extras "decode_families"; us per call, Qwen2.5-1.5B and -0.5B
+// shapes, M = 1 / 2 / 4):
+//   down 1536 x 8960: dot 8.4 / 11.2 / 15.5, skinny 16.1 / 16.5 / 16.9,
+//                     split-K GEMM 12.6 / 12.6 / 12.9 (13.0 at M = 8, 13.4 at 16)
+//   gate_up 8960 x 1536: dot 7.8 / 8.4 / 9.6, skinny 7.9 / 8.1 / 8.7
+//   q/o 1536 x 1536: dot 4.6 / 5.5 / 6.5, skinny 5.5 / 5.6 / 6.4
+//   down 896 x 4864: dot 6.4 / 8.2 / 10.8, skinny 9.0 / 10.1 / 10.6, GEMM 10.7
+//   gate_up 4864 x 896: dot 5.5 / 6.0 / 7.0, skinny 5.5 / 5.7 / 6.3
+// k_dot up to M = 2; from M = 3 k_skinny (or k_stream on very many tiles),
+// except rows of at least kLongK codes on few tiles, where the decode kernels
+// have too few waves for the long reduction and the split-K GEMM is faster.
+constexpr std::size_t kDotAutoMaxM = 2;
+constexpr int64_t kLongK = 8192;
+constexpr int64_t kLongKMaxTiles = 128;  // 16-row tiles: N <= 2048
+
 int natural_kernel(std::size_t M, std::size_t N, std::size_t K, int act)
 {
-    if (act == VVH_F32) return K_GEMV_F32;
-    if (M <= (std::size_t)kDotMaxM) return K_DOT;
+    if (act == VVH_F32) return (M >= kGemmF32MinM && K % kGemmBK == 0) ? K_GEMM : K_GEMV_F32;
+    if (M <= kDotAutoMaxM) return K_DOT;
     if (M > (std::size_t)kSkinnyMaxM) return K_GEMM;
     const int64_t tiles = ((int64_t)N + kDecodeTileN - 1) / kDecodeTileN;
+    if ((int64_t)K >= kLongK && K % kGemmBK == 0 && tiles <= kLongKMaxTiles) return K_GEMM;
     return (stream_depth(((int64_t)K + 63) / 64) > 0 && stream_worth(tiles)) ? K_STREAM : K_SKINNY;
 }
 
@@ -296,7 +318,7 @@ int choose_kernel(std::size_t M, std::size_t N, std::size_t K, int act, bool ali
         case K_SKINNY: return decode ? K_SKINNY : K_GENERIC;
         case K_STREAM: return (decode && stream_depth(((int64_t)K + 63) / 64) > 0) ? K_STREAM : K_GENERIC;
         case K_DOT: return (act == VVH_F16 && M <= (std::size_t)kDotMaxM) ? K_DOT : K_GENERIC;
-        case K_GEMM: return act == VVH_F16 ? K_GEMM : K_GENERIC;
+        case K_GEMM: return (act == VVH_F16 || K % kGemmBK == 0) ? K_GEMM : K_GENERIC;
         default: return K_GENERIC;
     }
 }
@@ -378,20 +400,45 @@ int run_call(const LinArgs& base, int kernel, int act, int outd, void* stream, c
             a.kstages = 0;
             a.ws = nullptr;
             if (a.K % kGemmBK == 0) {
-                const int64_t stages = a.K / kGemmBK;
+                // fp32 activations: the GEMM runs on their split fp16 form
+                // (M rows of 2K: scaled high parts, then low parts, plus one
+                // inverse scale per row), made in the workspace first
+                const bool f32 = act == VVH_F32;
+                uint64_t xs_bytes = 0, rs_bytes = 0;
+                if (f32) {
+                    if (!mul_ok((uint64_t)a.M * (uint64_t)a.K, 4, &xs_bytes))
+                        return fail(VVH_ERR_UNSUPPORTED, "problem too large for the fp32 GEMM path");
+                    xs_bytes = align_up(xs_bytes);
+                    rs_bytes = align_up((uint64_t)a.M * 4);
+                }
+                const int64_t stages = (f32 ? 2 * a.K : a.K) / kGemmBK;
                 int s = gemm_splits(nb, stages, (uint64_t)a.M * (uint64_t)a.N * 4);
+                uint64_t plane = 0;
                 if (s > 1) {
                     const int64_t kst = (stages + s - 1) / s;
                     s = (int)((stages + kst - 1) / kst);  // no empty split
-                    uint64_t plane;
                     if (s > 1 && mul_ok((uint64_t)a.M * (uint64_t)a.N, (uint64_t)s * 4, &plane) && nb * s <= INT32_MAX) {
-                        float* ws = nullptr;
-                        const int st = workspace_get(wsrc, stream, plane, &ws);
-                        if (st != VVH_OK) return st;
-                        a.ws = ws;
                         a.nsplit = s;
                         a.kstages = (int32_t)kst;
+                    } else {
+                        plane = 0;
                     }
+                }
+                if (xs_bytes + rs_bytes + plane > 0) {
+                    float* ws = nullptr;
+                    const int st = workspace_get(wsrc, stream, xs_bytes + rs_bytes + plane, &ws);
+                    if (st != VVH_OK) return st;
+                    char* wb = reinterpret_cast<char*>(ws);
+                    if (f32) {
+                        e = launch_split_f32(static_cast<const float*>(a.inp), a.M, a.K, wb,
+                                             reinterpret_cast<float*>(wb + xs_bytes), stream);
+                        if (e != 0) break;
+                        a.inp = wb;
+                        a.xrs = reinterpret_cast<const float*>(wb + xs_bytes);
+                        a.bk = a.K;
+                        a.K = 2 * a.K;
+                    }
+                    if (a.nsplit > 1) a.ws = reinterpret_cast<float*>(wb + xs_bytes + rs_bytes);
                 }
                 e = launch_gemm3(a, outd, gemm3_layout(a.M, a.N, a.nsplit), stream);
                 if (e == 0 && a.nsplit > 1) e = launch_splitk_reduce(a, outd, stream);
