@@ -303,8 +303,12 @@ VVH_API int vvh_plan_launches(vvh_plan plan, int* launches);
  * in_w / in_eps as for vvh_linear_q8_dev_in): e.g. q/k/v reading the
  * residual stream through the layer's input RMSNorm.  The plan must run as
  * one k_dot_grouped launch with its activations in LDS (vvh_plan_kernel
- * gives VVH_KERNEL_DOT), else VVH_ERR_UNSUPPORTED.  Waits for the device
- * (queued runs of the plan read its table); not for use under capture. */
+ * gives VVH_KERNEL_DOT), else VVH_ERR_UNSUPPORTED.  The stage is written
+ * into the plan's device table in place, after waiting for the device
+ * (queued runs of the plan read that table): set it before capturing any
+ * graph that runs the plan.  Graphs already captured from the plan read the
+ * same table, so every later replay of them runs the new stage too.  Calling
+ * it while a stream is being captured fails (it synchronises the device). */
 VVH_API int vvh_plan_set_input_op(vvh_plan plan, int in_op, const float* in_w, float in_eps);
 /* Kernel family of a single-launch plan (VVH_KERNEL_DOT, VVH_KERNEL_STREAM
  * or VVH_KERNEL_SKINNY), or VVH_KERNEL_AUTO for a plan run as one launch per

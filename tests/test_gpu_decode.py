@@ -84,3 +84,28 @@ def test_decode_small_model(gpu, oracle, act, head):
 def test_decode_qwen25_05b_shapes(gpu, oracle, head):
     """Two steps at the real Qwen2.5-0.5B shapes (24 layers, vocab 151936)."""
     run(oracle, qd.QWEN25_05B, capi.F16, head, steps=2, max_ctx=16)
+
+
+@pytest.mark.parametrize("fused", [False, True], ids=["unfused", "fused"])
+def test_decode_late_position(gpu, oracle, fused):
+    """One step at position 511 of a filled KV cache, Qwen2.5-0.5B shapes, as
+    bench.py times it: the span of 512 keys runs the split decode attention
+    (several blocks per kv head) and its combine launch, which the short
+    steps above never reach.  The cache rows the step reads are copied back
+    from the device, so the CPU forward attends to the same context."""
+    cfg, P, max_ctx = qd.QWEN25_05B, 511, 1024
+    m = qd.Model(cfg, act=capi.F16, lm_head="int8", max_ctx=max_ctx, seed=13, fused=fused)
+    try:
+        m.fill_kv(5)
+        capi.sync()
+        W = m.host_weights()
+        cache = [(L["kc"].to_array(np.float16, (max_ctx, cfg.kv_dim)).astype(np.float32),
+                  L["vc"].to_array(np.float16, (max_ctx, cfg.kv_dim)).astype(np.float32)) for L in m.layers]
+        print(f"[case] decode late position {P} fused={fused}", flush=True)
+        m.step(3, P)
+        got = m.logits_host()
+        ref = cpu_step(oracle, W, cfg, 3, P, cache, True, True)
+        err = float(np.abs(got - ref).max() / np.abs(ref).max())
+        assert err <= TOL[capi.F16], f"pos {P}: normalized logits error {err:.2e}"
+    finally:
+        m.close()
