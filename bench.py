@@ -172,6 +172,32 @@ def rotation(tmp_w, M, N, K, bias, res, seed, act=F16, outd=F16, max_reps=4096):
     return ar, [Linear(ar, tmp_w, M, N, K, bias, res, seed + 5 * r, act, outd, xy=(x, y)) for r in range(n)]
 
 
+GRAPH_CALLS = 64  # calls captured per HIP graph in graph_rotation
+
+
+def graph_rotation(ev, lins, stream, min_calls=60):
+    """ms per call over the replicas in `lins`, each called once per pass,
+    the calls captured in HIP graphs of at most GRAPH_CALLS calls on `stream`
+    and replayed: what a model step pays per call on the GPU, without the
+    host's launch time (a Python call costs several microseconds, more than
+    a small projection's kernel).  Every replica runs once on `stream`
+    before capture (this sizes the stream's workspace) and one replayed pass
+    precedes the timed passes."""
+    for l in lins:
+        l.run(stream)
+    capi.sync()
+    graphs = [ev.graph(stream, lambda st, c=lins[i:i + GRAPH_CALLS]: [l.run(st) for l in c])
+              for i in range(0, len(lins), GRAPH_CALLS)]
+
+    def one_pass(_i):
+        for g in graphs:
+            ev.launch(g, stream)
+
+    one_pass(0)
+    passes = max(2, -(-min_calls // len(lins)))
+    return timed(ev, one_pass, passes, stream) / len(lins)
+
+
 def timed_rotation(ev, lins, steps, stream=None):
     """ms per call over `steps` calls that rotate through `lins`, after one
     warm-up pass over all of them (so no timed call finds its operands in
@@ -623,7 +649,7 @@ def extras(ev, sets, projs, tmp_w, args):
     # (3) LM head GEMV, configs[2]: K=896, N=151936, fp16 act, fp32 logits
     N, K = 151936, 896
     _ar, heads = rotation(tmp_w, 1, N, K, False, False, 777, F16, F32)
-    us = timed_rotation(ev, heads, 60) * 1e3
+    us = graph_rotation(ev, heads, stream) * 1e3
     b = heads[0].bytes
     out["lm_head"] = {"N": N, "K": K, "replicas_rotated": len(heads), "us": round(us, 2),
                       "GBps": round(b / (us * 1e-6) / 1e9, 1),
@@ -638,7 +664,7 @@ def extras(ev, sets, projs, tmp_w, args):
         for name, N, K, res in (("gate_up", QWEN05["inter"], QWEN05["hidden"], False),
                                 ("down", QWEN05["hidden"], QWEN05["inter"], True)):
             _ar, reps = rotation(tmp_w, M, N, K, False, res, 900)
-            us = timed_rotation(ev, reps, 40) * 1e3
+            us = graph_rotation(ev, reps, stream) * 1e3
             tf = reps[0].flops / (us * 1e-6) / 1e12
             del reps, _ar
             gemm[f"{name}_M{M}"] = {"M": M, "N": N, "K": K, "us": round(us, 2), "TFLOPS": round(tf, 1),
@@ -663,7 +689,7 @@ def extras(ev, sets, projs, tmp_w, args):
                               ("gemv_f32", capi.KERNEL_GEMV_F32)):
                 capi.set_kernel(kern)
                 try:
-                    us = timed_rotation(ev, reps, 30) * 1e3
+                    us = graph_rotation(ev, reps, stream) * 1e3
                 finally:
                     capi.set_kernel(capi.KERNEL_AUTO)
                 row[f"{fam}_us"] = round(us, 2)
@@ -689,7 +715,7 @@ def extras(ev, sets, projs, tmp_w, args):
                 try:
                     if capi.kernel_choice(M, N, K, F16, F16) != fam:
                         continue
-                    row[f"{fam}_us"] = round(timed_rotation(ev, reps, 30) * 1e3, 2)
+                    row[f"{fam}_us"] = round(graph_rotation(ev, reps, stream) * 1e3, 2)
                 finally:
                     capi.set_kernel(capi.KERNEL_AUTO)
             del reps, _ar
@@ -701,7 +727,7 @@ def extras(ev, sets, projs, tmp_w, args):
     for M in (1, 4, 16, 64, 256):
         for name, N, K in (("qo", 1536, 1536), ("kv", 256, 1536), ("gate_up", 8960, 1536), ("down", 1536, 8960)):
             _ar, reps = rotation(tmp_w, M, N, K, False, False, 1300)
-            us = timed_rotation(ev, reps, 30) * 1e3
+            us = graph_rotation(ev, reps, stream) * 1e3
             l = reps[0]
             del reps, _ar
             sweep[f"{name}_M{M}"] = {"us": round(us, 2), "GBps": round(l.bytes / (us * 1e-6) / 1e9, 1),

@@ -157,7 +157,8 @@ def test_dispatch_choice():
         assert ch(512, 4864, 880, capi.F32, capi.F32) == "gemv_f32"   # K % 64 != 0
         assert ch(1, 151936, 896, capi.F16, capi.F32) == "dot"        # config 3 (M = 1)
         assert ch(1, 896, 896, capi.F16, capi.F16) == "dot"           # config 2 (M = 1)
-        assert ch(2, 896, 896, capi.F16, capi.F16) == "dot"           # M <= 2
+        assert ch(2, 896, 896, capi.F16, capi.F16) == "dot"           # M = 2, few tiles
+        assert ch(2, 4864, 896, capi.F16, capi.F16) == "skinny"       # M = 2, 304 tiles
         assert ch(3, 896, 896, capi.F16, capi.F16) == "skinny"        # M = 3..16
         assert ch(4, 1536, 8960, capi.F16, capi.F16) == "gemm"        # long rows, few tiles: split-K GEMM
         assert ch(2, 1536, 8960, capi.F16, capi.F16) == "dot"

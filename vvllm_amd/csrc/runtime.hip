@@ -193,7 +193,8 @@ int workspace_get(const WsSource* src, void* stream, std::size_t bytes, float** 
 // GEMM pays a second launch and, per split, one partial plane written by the
 // GEMM and read back by the reduction, so it only pays for long reductions
 // over few tiles: split when the tiles would leave half of the CUs idle and K
-// has at least 32 stages.  The count minimises a cost model fitted to a sweep
+// has at least 8 stages (with fewer, a block's k loop is shorter than the
+// reduction launch).  The count minimises a cost model fitted to a sweep
 // of forced counts on the Qwen2.5-0.5B down projection (M=512: 33.1, 23.9,
 // 20.6, 19.9, 19.8, 19.9, 21.8, 21.5 us for 1..7 and 9 splits; M=2048: 36.4,
 // 33.7, 42.4 us for 1..3): 0.4 us per k stage and round of blocks over the
@@ -202,7 +203,7 @@ int gemm_splits(int64_t tiles, int64_t stages, uint64_t plane_bytes)
 {
     const int64_t cus = g_cu_count > 0 ? g_cu_count : 256;
     int64_t s = 1;
-    if (tiles * 2 <= cus && stages >= 32) {
+    if (tiles * 2 <= cus && stages >= 8) {
         const int64_t smax = std::min<int64_t>(cus / tiles, stages / 4);
         double best = 0;
         for (int64_t c = 1; c <= smax; c++) {
@@ -279,27 +280,30 @@ bool dot_early(int64_t blocks) { return blocks <= (int64_t)(g_cu_count > 0 ? g_c
 constexpr std::size_t kGemmF32MinM = 32;
 
 // Small-M fp16 dispatch, from a sweep of every family forced on each shape
-// (bench.py extras "decode_families"; us per call, Qwen2.5-1.5B and -0.5B
-// shapes, M = 1 / 2 / 4):
-//   down 1536 x 8960: dot 8.4 / 11.2 / 15.5, skinny 16.1 / 16.5 / 16.9,
-//                     split-K GEMM 12.6 / 12.6 / 12.9 (13.0 at M = 8, 13.4 at 16)
-//   gate_up 8960 x 1536: dot 7.8 / 8.4 / 9.6, skinny 7.9 / 8.1 / 8.7
-//   q/o 1536 x 1536: dot 4.6 / 5.5 / 6.5, skinny 5.5 / 5.6 / 6.4
-//   down 896 x 4864: dot 6.4 / 8.2 / 10.8, skinny 9.0 / 10.1 / 10.6, GEMM 10.7
-//   gate_up 4864 x 896: dot 5.5 / 6.0 / 7.0, skinny 5.5 / 5.7 / 6.3
-// k_dot up to M = 2; from M = 3 k_skinny (or k_stream on very many tiles),
-// except rows of at least kLongK codes on few tiles, where the decode kernels
-// have too few waves for the long reduction and the split-K GEMM is faster.
+// (bench.py extras "decode_families"; us per call on the GPU, calls
+// replayed from HIP graphs; Qwen2.5-1.5B and -0.5B shapes, M = 1 / 2 / 4):
+//   q/o 1536 x 1536:    dot 4.5 / 5.2 / 6.2, skinny 5.1 / 5.3 / 6.0
+//   gate_up 8960 x 1536: dot 7.8 / 8.4 / 9.7, skinny 7.6 / 7.9 / 8.6
+//   gate_up 4864 x 896:  dot 5.3 / 5.7 / 6.8, skinny 5.1 / 5.3 / 5.8
+//   down 896 x 4864:     dot 6.1 / 8.0 / 10.5, skinny 8.7 / 9.8 / 10.3
+//   down 1536 x 8960:    dot 8.5 / 11.0 / 15.3, skinny 15.9 / 16.3 / 16.7,
+//                        split-K GEMM 13.3 / 13.3 / 13.4 (13.6 at M = 8)
+// k_dot at M = 1, and at M = 2 unless the problem has many tiles (the MFMA
+// decode kernel is then faster); k_skinny from M = 3 (or k_stream on very
+// many tiles), except rows of at least kLongK codes on few tiles, where the
+// decode kernels have too few waves for the long reduction and the split-K
+// GEMM is faster.
 constexpr std::size_t kDotAutoMaxM = 2;
+constexpr int64_t kDotM2MaxTiles = 256;  // M = 2: k_dot below this many 16-row tiles
 constexpr int64_t kLongK = 8192;
 constexpr int64_t kLongKMaxTiles = 128;  // 16-row tiles: N <= 2048
 
 int natural_kernel(std::size_t M, std::size_t N, std::size_t K, int act)
 {
     if (act == VVH_F32) return (M >= kGemmF32MinM && K % kGemmBK == 0) ? K_GEMM : K_GEMV_F32;
-    if (M <= kDotAutoMaxM) return K_DOT;
-    if (M > (std::size_t)kSkinnyMaxM) return K_GEMM;
     const int64_t tiles = ((int64_t)N + kDecodeTileN - 1) / kDecodeTileN;
+    if (M == 1 || (M <= kDotAutoMaxM && tiles < kDotM2MaxTiles)) return K_DOT;
+    if (M > (std::size_t)kSkinnyMaxM) return K_GEMM;
     if ((int64_t)K >= kLongK && K % kGemmBK == 0 && tiles <= kLongKMaxTiles) return K_GEMM;
     return (stream_depth(((int64_t)K + 63) / 64) > 0 && stream_worth(tiles)) ? K_STREAM : K_SKINNY;
 }
