@@ -392,12 +392,24 @@ def main():
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--workload", choices=("decode", "prefill", "vendor-gemm", "copy"), default="decode",
+    ap.add_argument("--workload", choices=("decode", "prefill", "lm-head", "vendor-gemm", "copy"), default="decode",
                     help="decode: configs[1] (the headline line); prefill: configs[3] gate/up GEMM only; "
+                         "lm-head: configs[2] alone; "
                          "vendor-gemm: the int8 GEMM beside the vendor fp16 GEMM on the prefill shapes; "
                          "copy: a 256 MiB device-to-device copy, the calibration of the HBM traffic counters")
     ap.add_argument("--prefill-m", type=int, default=512)
+    ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
+                    help="summarise a rocprofv3 --kernel-trace CSV of a bench run: the dispatches of the kernel "
+                         "named by --kernel after the first --skip of them (the warm-up steps); no GPU is used")
+    ap.add_argument("--kernel", default="k_dot_grouped", help="substring of the kernel name (--trace-summary)")
+    ap.add_argument("--skip", type=int, default=None, help="dispatches to skip (--trace-summary; default --warmup)")
+    ap.add_argument("--count", type=int, default=None,
+                    help="dispatches to summarise after the skipped ones (--trace-summary; default --steps)")
+    ap.add_argument("--bytes", type=float, default=360339456.0,
+                    help="algorithmic bytes per dispatch (--trace-summary; default: the headline step)")
     args = ap.parse_args()
+    if args.trace_summary:
+        return trace_summary(args)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build targets one MI355X; the int8 linear path is measured on one GPU "
               "(multi-GPU sharding is design-only). Run with --gpus 1.", file=sys.stderr)
@@ -410,6 +422,8 @@ def main():
     ev = HipEvents()
     if args.workload == "prefill":
         return prefill_main(args, ev, name)
+    if args.workload == "lm-head":
+        return lm_head_main(args, ev, name)
     if args.workload == "vendor-gemm":
         return vendor_gemm_main(args, ev)
     if args.workload == "copy":
@@ -477,6 +491,32 @@ def main():
     print(json.dumps(result), flush=True)
 
 
+def trace_summary(args):
+    """Timed dispatches of one kernel in a rocprofv3 kernel trace: count,
+    mean / median / min / max duration, and algorithmic bytes / mean
+    against the HBM peak, as one JSON line."""
+    import csv
+    import statistics
+    rows = [r for r in csv.DictReader(open(args.trace_summary)) if args.kernel in r["Kernel_Name"]]
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    skip = args.warmup if args.skip is None else args.skip
+    count = args.steps if args.count is None else args.count
+    rows_all = len(rows)
+    rows = rows[:skip + count]
+    d = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in rows[skip:]]
+    if not d:
+        print(json.dumps({"error": f"no dispatch of {args.kernel!r} after {skip}"}))
+        return
+    mean = sum(d) / len(d)
+    span = (int(rows[-1]["End_Timestamp"]) - int(rows[skip]["Start_Timestamp"])) / 1e3 / len(d)
+    print(json.dumps({"kernel": rows[0]["Kernel_Name"][:120], "dispatches": rows_all, "skipped": skip,
+                      "timed": len(d), "mean_us": round(mean, 3), "median_us": round(statistics.median(d), 3),
+                      "min_us": round(min(d), 3), "max_us": round(max(d), 3),
+                      "span_per_dispatch_us": round(span, 3),
+                      "GBps_at_mean": round(args.bytes / (mean * 1e-6) / 1e9, 1),
+                      "hbm_frac_at_mean": round(args.bytes / (mean * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}))
+
+
 def kernel_name(M, N, K, outd=F16):
     """Kernel family of an fp16 linear_q8 call, with the GEMM variant spelled out."""
     k = capi.kernel_choice(M, N, K, F16, outd)
@@ -509,6 +549,35 @@ def prefill_main(args, ev, name):
                    "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "kernel": kern, "achieved": round(tf, 2), "peak": MFMA_F16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None},
+        "cpu_baseline": None}), flush=True)
+
+
+def lm_head_main(args, ev, name):
+    """configs[2] alone: the LM-head GEMV (M=1, K=896, N=151936, fp16
+    activations, fp32 logits), 8 weight replicas rotated (>= 1 GiB), calls
+    launched back to back on the null stream (each call, about 25 us, is
+    longer than its launch) and timed with HIP events: one JSON line in GB/s
+    against the HBM peak."""
+    N, K = 151936, QWEN05["hidden"]
+    tmp_w = capi.DevBuf(N * K * 4)
+    _ar, heads = rotation(tmp_w.ptr, 1, N, K, False, False, 777, F16, F32)
+    for i in range(args.warmup):
+        heads[i % len(heads)].run()
+    ms = timed(ev, lambda i: heads[i % len(heads)].run(), args.steps)
+    b = heads[0].bytes
+    gbs = b / (ms * 1e-3) / 1e9
+    print(f"[bench] {name}: lm head {ms * 1e3:.2f} us, {gbs:.0f} GB/s", file=sys.stderr, flush=True)
+    print(json.dumps({
+        "metric": "linear_q8 GEMV µs + HBM GB/s at Qwen2.5-0.5B shapes; prefill GEMM TFLOPS",
+        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8 weights x f16 activations, f32 accumulate",
+        "data": "synthetic (seeded N(0,0.02) fp32 weights quantized per channel on device; N(0,1) fp16 activations)",
+        "config": {"workload": f"configs[2]: LM-head GEMV, M=1, N={N}, K={K}, fp32 logits",
+                   "M": 1, "N": N, "K": K, "algorithmic_bytes_per_step": b, "replicas_rotated": len(heads),
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": "k_dot<float>", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
         "cpu_baseline": None}), flush=True)
 
 
