@@ -5,12 +5,15 @@
 // the Backend::linear_q8 / linear_q8_add contract
 // (include/vvllm/backend/backend.h:62-65, 75-78) on MFMA.
 //
-// Block tile 128(m) x BN(n) x 64(k), BN = 32 * TJ * WN; 2 x WN waves, each a
-// 64 x (32 * TJ) wave tile built from 2 x TJ v_mfma_f32_32x32x16_f16 tiles.
-// The wave tile is chosen for the LDS read rate: per MFMA a wave reads
-// (8 KB of A + TJ * 2 KB of B) / (8 TJ) from LDS, 0.58 KB at TJ = 3 against
-// 1.25 KB for a 64 x 32 wave tile, with which 8 waves read more bytes per
-// stage than the LDS delivers in the stage's MFMA time.
+// Block tile 128(m) x BN(n) x 64(k), BN = 32 * TJ * WN; (4 / TI) x WN waves,
+// each a (32 * TI) x (32 * TJ) wave tile built from TI x TJ
+// v_mfma_f32_32x32x16_f16 tiles.
+// A wave tile trades LDS reads against code conversions: per MFMA a wave
+// reads (TI * 4 KB of A + TJ * 2 KB of B) / (4 TI TJ) from LDS and converts
+// 20 / TI codes' worth of VALU (5 ops per 4 codes, each converted fragment
+// feeding TI row tiles).  64 x 96 (TI = 2, TJ = 3): 0.58 KB and 5 VALU per
+// MFMA; 128 x 32 (TI = 4, TJ = 1): 1.25 KB and 2.5 VALU, which measured a
+// few percent faster at 128 x 128 blocks.
 //
 // Operands are staged through a ring of D LDS stages filled by direct
 // global -> LDS loads (global_load_lds_dwordx4), A as fp16 and B as the raw
@@ -64,15 +67,15 @@ struct Gemm3Stage {
     __attribute__((aligned(16))) char pad[kEpi > kOps ? kEpi - kOps : 16];
 };
 
-template <int TJ>
+template <int TJ, int TI>
 struct Gemm3Frag {
-    u4 b[2][TJ];     // raw codes: slice kk2, column tile tj
-    h8 a[2][2][2];   // fp16 A: slice kk2, half h, row tile ti
+    u4 b[2][TJ];      // raw codes: slice kk2, column tile tj
+    h8 a[2][2][TI];   // fp16 A: slice kk2, half h, row tile ti
 };
 
-template <int TJ>
+template <int TJ, int TI>
 __device__ __forceinline__ void gemm3_read(const f16* __restrict__ sa, const int8_t* __restrict__ sb,
-                                           Gemm3Frag<TJ>& f, int row0, int col0, int fl, int fh)
+                                           Gemm3Frag<TJ, TI>& f, int row0, int col0, int fl, int fh)
 {
 #pragma unroll
     for (int kk2 = 0; kk2 < 2; kk2++) {
@@ -84,7 +87,7 @@ __device__ __forceinline__ void gemm3_read(const f16* __restrict__ sa, const int
 #pragma unroll
         for (int h = 0; h < 2; h++)
 #pragma unroll
-            for (int ti = 0; ti < 2; ti++) {
+            for (int ti = 0; ti < TI; ti++) {
                 const int i = row0 + ti * 32 + fl;
                 f.a[kk2][h][ti] = *reinterpret_cast<const h8*>(sa + i * 64 + swz_a(i, kk2 * 4 + fh * 2 + h) * 8);
             }
@@ -98,21 +101,21 @@ __device__ __forceinline__ void gemm3_convert(const u4 (&b)[TJ], h8 (&fb)[TJ][2]
     for (int tj = 0; tj < TJ; tj++) i8x16_to_h8x2(b[tj], fb[tj][0], fb[tj][1]);
 }
 
-// MFMAs of one 32-wide k slice (2 x 2 x TJ of them) with the conversion of
+// MFMAs of one 32-wide k slice (2 x TI x TJ of them) with the conversion of
 // another slice's codes (20 * TJ VALU) spread between them.
-template <int TJ>
-__device__ __forceinline__ void gemm3_slice(const h8 (&a)[2][2], const h8 (&fb)[TJ][2], f16v (&acc)[2][TJ],
+template <int TJ, int TI>
+__device__ __forceinline__ void gemm3_slice(const h8 (&a)[2][TI], const h8 (&fb)[TJ][2], f16v (&acc)[TI][TJ],
                                             const u4 (&nb)[TJ], h8 (&nfb)[TJ][2])
 {
 #pragma unroll
     for (int h = 0; h < 2; h++)
 #pragma unroll
-        for (int ti = 0; ti < 2; ti++)
+        for (int ti = 0; ti < TI; ti++)
 #pragma unroll
             for (int tj = 0; tj < TJ; tj++)
                 acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[tj][h], a[h][ti], acc[ti][tj], 0, 0, 0);
     gemm3_convert<TJ>(nb, nfb);
-    constexpr int NM = 4 * TJ;
+    constexpr int NM = 2 * TI * TJ;
     constexpr int NV = (20 * TJ + NM - 1) / NM;
 #pragma unroll
     for (int i = 0; i < NM; i++) {
@@ -121,13 +124,13 @@ __device__ __forceinline__ void gemm3_slice(const h8 (&a)[2][2], const h8 (&fb)[
     }
 }
 
-template <int TJ>
-__device__ __forceinline__ void gemm3_slice_last(const h8 (&a)[2][2], const h8 (&fb)[TJ][2], f16v (&acc)[2][TJ])
+template <int TJ, int TI>
+__device__ __forceinline__ void gemm3_slice_last(const h8 (&a)[2][TI], const h8 (&fb)[TJ][2], f16v (&acc)[TI][TJ])
 {
 #pragma unroll
     for (int h = 0; h < 2; h++)
 #pragma unroll
-        for (int ti = 0; ti < 2; ti++)
+        for (int ti = 0; ti < TI; ti++)
 #pragma unroll
             for (int tj = 0; tj < TJ; tj++)
                 acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[tj][h], a[h][ti], acc[ti][tj], 0, 0, 0);
@@ -150,18 +153,20 @@ __device__ __forceinline__ void gemm3_fill(f16* __restrict__ sa, int8_t* __restr
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, sb + (wave * LB + i) * 1024, 16, b_off[i], kb, 0, 0);
 }
 
-template <typename OT, int D, int WN, int TJ>
-__global__ __launch_bounds__(128 * WN, 1) void k_gemm3(LinArgs a)
+template <typename OT, int D, int WN, int TJ, int TI>
+__global__ __launch_bounds__(64 * (4 / TI) * WN, 1) void k_gemm3(LinArgs a)
 {
     static_assert(D == 4, "four stages: even (static fragment parity) and one epilogue quarter per stage");
-    constexpr int NW = 2 * WN;
+    static_assert(TI == 2 || TI == 4, "wave tiles of 64 or 128 rows");
+    constexpr int WM = 4 / TI;  // waves along the 128 rows
+    constexpr int NW = WM * WN;
     constexpr int NT = 64 * NW;
     constexpr int BN = 32 * TJ * WN;
     static_assert(16 % NW == 0 && (BN / 16) % NW == 0, "whole 1 KB loads per wave");
     constexpr int LA = 16 / NW, LB = BN / 16 / NW;
     constexpr int LPS = LA + LB;  // loads per stage per thread
     using Stage = Gemm3Stage<BN>;
-    using Frag = Gemm3Frag<TJ>;
+    using Frag = Gemm3Frag<TJ, TI>;
     __shared__ Stage st0, st1, st2, st3;
 
     const int64_t nbm = (a.M + kGemmBM - 1) / kGemmBM;
@@ -178,8 +183,8 @@ __global__ __launch_bounds__(128 * WN, 1) void k_gemm3(LinArgs a)
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave & 1, wn = wave >> 1;
-    const int row0 = wm * 64, col0 = wn * (32 * TJ);
+    const int wm = wave % WM, wn = wave / WM;
+    const int row0 = wm * (32 * TI), col0 = wn * (32 * TJ);
     const int fl = lane & 31, fh = lane >> 5;
     const f16* X = static_cast<const f16*>(a.inp);
 
@@ -258,9 +263,9 @@ __global__ __launch_bounds__(128 * WN, 1) void k_gemm3(LinArgs a)
         gemm3_fill<NW, BN>(g.a, g.b, ra, rb, a_off, b_off, wave, (uint32_t)k0, (uint32_t)(k0 < KB ? k0 : k0 - KB));
     };
 
-    f16v acc[2][TJ];
+    f16v acc[TI][TJ];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < TI; i++)
 #pragma unroll
         for (int j = 0; j < TJ; j++) acc[i][j] = f16v{};
     Frag f0, f1;
@@ -269,7 +274,7 @@ __global__ __launch_bounds__(128 * WN, 1) void k_gemm3(LinArgs a)
         if constexpr (decltype(P)::value % 2 == 0) return f0;
         else return f1;
     };
-    auto read = [&](auto S) { gemm3_read<TJ>(stage(S).a, stage(S).b, frag(S), row0, col0, fl, fh); };
+    auto read = [&](auto S) { gemm3_read<TJ, TI>(stage(S).a, stage(S).b, frag(S), row0, col0, fl, fh); };
 
     // one step of the schedule; NEXT: stage j+1 exists, REFILL: refill
     // stage j's buffer with k stage kt0 + j + D, VM: loads still allowed in
@@ -282,9 +287,9 @@ __global__ __launch_bounds__(128 * WN, 1) void k_gemm3(LinArgs a)
         if constexpr (REFILL) issue(stage(j), kt0 + J + D);
         if constexpr (NEXT) read(jn);
         Frag& f = frag(j);
-        gemm3_slice<TJ>(f.a[0], fb[0], acc, f.b[1], fb[1]);
-        if constexpr (NEXT) gemm3_slice<TJ>(f.a[1], fb[1], acc, frag(jn).b[0], fb[0]);
-        else gemm3_slice_last<TJ>(f.a[1], fb[1], acc);
+        gemm3_slice<TJ, TI>(f.a[0], fb[0], acc, f.b[1], fb[1]);
+        if constexpr (NEXT) gemm3_slice<TJ, TI>(f.a[1], fb[1], acc, frag(jn).b[0], fb[0]);
+        else gemm3_slice_last<TJ, TI>(f.a[1], fb[1], acc);
     };
     // R steps from kt0 (kt0 % D == 0) with the problem's stage count kt0 + R
     auto steps = [&]<int R>(int64_t kt0) {
@@ -355,7 +360,7 @@ __global__ __launch_bounds__(128 * WN, 1) void k_gemm3(LinArgs a)
     if (a.xrs) {
         // split fp32 activations: each row's sums times its power-of-two scale
 #pragma unroll
-        for (int ti = 0; ti < 2; ti++) {
+        for (int ti = 0; ti < TI; ti++) {
             const int64_t m = m0 + row0 + ti * 32 + fl;
             const float rs = a.xrs[m < a.M ? m : a.M - 1];
 #pragma unroll
@@ -363,7 +368,7 @@ __global__ __launch_bounds__(128 * WN, 1) void k_gemm3(LinArgs a)
         }
     }
 #pragma unroll
-    for (int ti = 0; ti < 2; ti++) {
+    for (int ti = 0; ti < TI; ti++) {
         float* q = quarter((row0 >> 5) + ti) + fl * ES + col0 + 4 * fh;
 #pragma unroll
         for (int tj = 0; tj < TJ; tj++)
@@ -497,27 +502,30 @@ __global__ __launch_bounds__(128 * WN, 1) void k_gemm3(LinArgs a)
     }
 }
 
-// Tile shapes (layout code -> WN, TJ): 1 = 128 x 192 (4 waves of 64 x 96),
-// 2 = 128 x 256 (8 waves of 64 x 64), 3 = 128 x 128 (4 waves of 64 x 64).
-int gemm3_tile_n(int layout) { return layout == 2 ? 256 : layout == 3 ? 128 : 192; }
+// Tile shapes (layout code -> WN, TJ, TI): 1 = 128 x 192 (4 waves of
+// 64 x 96), 3 = 128 x 128 (4 waves of 128 x 32: each converted code
+// fragment feeds 4 row tiles, 2.5 conversion VALU per MFMA; measured against
+// 4 waves of 64 x 64 in the same runs: M=512 gate/up 11.13 -> 10.78 us,
+// M=2048 33.7 -> 33.3 us, split-K down M=2048 32.7 -> 32.0 us).
+int gemm3_tile_n(int layout) { return layout == 3 ? 128 : 192; }
 
-template <int WN, int TJ>
+template <int WN, int TJ, int TI>
 static void gemm3_go(const LinArgs& a, bool f32, hipStream_t s)
 {
     constexpr int BN = 32 * TJ * WN;
+    constexpr int NT = 64 * (4 / TI) * WN;
     const int64_t tiles = ((a.M + kGemmBM - 1) / kGemmBM) * ((a.N + BN - 1) / BN);
     const dim3 grid((unsigned)(tiles * (a.nsplit > 1 ? a.nsplit : 1)));
-    if (f32) hipLaunchKernelGGL((k_gemm3<float, 4, WN, TJ>), grid, dim3(128 * WN), 0, s, a);
-    else hipLaunchKernelGGL((k_gemm3<f16, 4, WN, TJ>), grid, dim3(128 * WN), 0, s, a);
+    if (f32) hipLaunchKernelGGL((k_gemm3<float, 4, WN, TJ, TI>), grid, dim3(NT), 0, s, a);
+    else hipLaunchKernelGGL((k_gemm3<f16, 4, WN, TJ, TI>), grid, dim3(NT), 0, s, a);
 }
 
 int launch_gemm3(const LinArgs& a, int out, int layout, void* stream)
 {
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool f32 = out == VVH_F32;
-    if (layout == 2) gemm3_go<4, 2>(a, f32, s);
-    else if (layout == 3) gemm3_go<2, 2>(a, f32, s);
-    else gemm3_go<2, 3>(a, f32, s);
+    if (layout == 3) gemm3_go<4, 1, 4>(a, f32, s);
+    else gemm3_go<2, 3, 2>(a, f32, s);
     return (int)hipGetLastError();
 }
 
