@@ -310,6 +310,25 @@ VVH_API int vvh_plan_launches(vvh_plan plan, int* launches);
  * same table, so every later replay of them runs the new stage too.  Calling
  * it while a stream is being captured fails (it synchronises the device). */
 VVH_API int vvh_plan_set_input_op(vvh_plan plan, int in_op, const float* in_w, float in_eps);
+/* RoPE and the KV-cache append as the epilogue of a q/k/v plan: problems
+ * q_index, k_index and v_index (indices into the list given to
+ * vvh_plan_create) then write what vvh_rope_append would leave after a plain
+ * run of the plan, bit for bit: q and k rotated in place (split-half RoPE of
+ * each head of head_dim, base theta, at position pos + m for activation row
+ * m), and the rotated k rows and the v rows also written to rows pos + m of
+ * k_cache and v_cache ([*, N of k] of the plan's output dtype).  Saves the
+ * RoPE launch of a decode layer (transformer.h:145-160, the reference's
+ * rope then KVCache::append).  No reference counterpart.  The plan must run
+ * as one k_dot_grouped launch (vvh_plan_kernel gives VVH_KERNEL_DOT); q's
+ * rows and k's rows must be whole heads (N % head_dim == 0), k and v alike,
+ * head_dim a multiple of 16.  Like vvh_plan_set_input_op, the plan's device
+ * table is rewritten in place after waiting for the device: set it before
+ * capturing graphs that run the plan.  The position is an argument of each
+ * run: vvh_plan_run_pos (vvh_plan_run runs at position 0). */
+VVH_API int vvh_plan_set_rope(vvh_plan plan, size_t q_index, size_t k_index, size_t v_index, size_t head_dim,
+                              float theta, void* k_cache, void* v_cache);
+/* vvh_plan_run with the position of activation row 0 for a RoPE epilogue. */
+VVH_API int vvh_plan_run_pos(vvh_plan plan, size_t pos, void* stream);
 /* Kernel family of a single-launch plan (VVH_KERNEL_DOT, VVH_KERNEL_STREAM
  * or VVH_KERNEL_SKINNY), or VVH_KERNEL_AUTO for a plan run as one launch per
  * problem. */

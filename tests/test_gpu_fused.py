@@ -159,6 +159,87 @@ def test_plan_input_stage(gpu):
         assert np.array_equal(a, b)
 
 
+def _qkv_plan(bufs, src, ws, M, K, outd):
+    probs = [capi.Q8Problem(out=b.ptr, inp=src.ptr, residual=None, weight=q.ptr, scales=s.ptr, bias=bb.ptr,
+                            M=M, N=N, K=K) for b, (q, s, bb, N) in zip(bufs, ws)]
+    h = ctypes.c_uint64()
+    capi.call("vvh_plan_create", (capi.Q8Problem * 3)(*probs), 3, F16, outd, ctypes.byref(h))
+    assert capi.plan_kernel(h.value) == "dot"
+    return h.value
+
+
+@pytest.mark.parametrize("M,H,KVH,D,pos,outd,stage", [
+    (1, 14, 2, 64, 511, F16, True),    # Qwen2.5-0.5B, as the fused decode step runs it
+    (1, 14, 2, 64, 0, F16, False),
+    (2, 4, 4, 128, 37, F16, True),     # two positions in one run, MHA, head_dim 128
+    (1, 8, 2, 32, 1000, F32, False),   # fp32 outputs and caches, head_dim 32
+    (2, 12, 2, 128, 5, F32, True),
+])
+def test_plan_rope_epilogue(gpu, M, H, KVH, D, pos, outd, stage):
+    """RoPE and the K/V cache append as the epilogue of the q/k/v plan
+    (vvh_plan_set_rope, vvh_plan_run_pos) against the plan's plain run
+    followed by vvh_rope_append, bit for bit: q, k, v and both caches."""
+    print(f"[case] plan rope M={M} H={H} KVH={KVH} D={D} pos={pos} out={outd} stage={stage}", flush=True)
+    rng = np.random.default_rng(M * 1000 + H * 10 + D + pos)
+    K, theta, eps, cap = 896, 1e6, 1e-6, pos + M + 3
+    dt = np.float16 if outd == F16 else np.float32
+    x = rng.normal(0, 2, (M, K)).astype(np.float16)
+    w = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    dx, dw = capi.DevBuf.from_array(x), capi.DevBuf.from_array(w)
+    shapes = [H * D, KVH * D, KVH * D]
+    ws = []
+    for N in shapes:
+        q, s = q8_weight(rng, N, K)
+        ws.append((q, s, capi.DevBuf.from_array(rng.normal(0, 0.1, N).astype(np.float32)), N))
+    cache = rng.normal(0, 1, (cap, KVH * D)).astype(dt)
+    results = {}
+    for mode in ("ref", "fused"):
+        bufs = [capi.DevBuf(M * N * np.dtype(dt).itemsize) for N in shapes]
+        kc, vc = capi.DevBuf.from_array(cache), capi.DevBuf.from_array(cache)
+        h = _qkv_plan(bufs, dx, ws, M, K, outd)
+        try:
+            if stage:
+                capi.call("vvh_plan_set_input_op", h, capi.IN_RMS_NORM, dw.ptr, eps)
+            if mode == "ref":
+                capi.call("vvh_plan_run", h, None)
+                capi.call("vvh_rope_append", bufs[0].ptr, bufs[1].ptr, bufs[2].ptr, kc.ptr, vc.ptr, M, H, KVH, D, pos,
+                          theta, outd, None)
+            else:
+                capi.call("vvh_plan_set_rope", h, 0, 1, 2, D, theta, kc.ptr, vc.ptr)
+                capi.call("vvh_plan_run_pos", h, pos, None)
+            capi.sync()
+        finally:
+            capi.call("vvh_plan_destroy", h)
+        u = np.uint16 if outd == F16 else np.uint32
+        results[mode] = [b.to_array(u, (M * N,)) for b, N in zip(bufs, shapes)] + \
+                        [kc.to_array(u, cache.shape), vc.to_array(u, cache.shape)]
+    for name, a, b in zip(("q", "k", "v", "k_cache", "v_cache"), results["ref"], results["fused"]):
+        assert np.array_equal(a, b), name
+
+
+def test_plan_rope_limits(gpu):
+    """The RoPE epilogue is refused where it cannot apply."""
+    rng = np.random.default_rng(3)
+    K = 256
+    dx = capi.DevBuf.from_array(rng.normal(0, 1, (1, K)).astype(np.float16))
+    ws = [(*q8_weight(rng, N, K), capi.DevBuf(N * 4), N) for N in (128, 64, 64)]
+    bufs = [capi.DevBuf(N * 2) for N in (128, 64, 64)]
+    kc, vc = capi.DevBuf(64 * 2 * 4), capi.DevBuf(64 * 2 * 4)
+    h = _qkv_plan(bufs, dx, ws, 1, K, F16)
+    try:
+        st = lambda *a: capi.status_of("vvh_plan_set_rope", h, *a)
+        invalid, unsupported = 1, 7
+        assert st(0, 1, 1, 32, 1e6, kc.ptr, vc.ptr) == invalid         # k and v the same problem
+        assert st(0, 1, 5, 32, 1e6, kc.ptr, vc.ptr) == invalid         # no problem 5
+        assert st(0, 1, 2, 24, 1e6, kc.ptr, vc.ptr) == unsupported     # head_dim % 16 != 0
+        assert st(0, 1, 2, 48, 1e6, kc.ptr, vc.ptr) == invalid         # 128 rows are not whole heads of 48
+        assert st(0, 1, 2, 32, 0.0, kc.ptr, vc.ptr) == invalid         # theta
+        assert st(0, 1, 2, 32, 1e6, None, vc.ptr) == invalid           # no cache
+        assert st(0, 1, 2, 32, 1e6, kc.ptr, vc.ptr) == 0
+    finally:
+        capi.call("vvh_plan_destroy", h)
+
+
 def fused_vs_unfused(cfg, head, steps, max_ctx):
     models = [qd.Model(cfg, act=F16, lm_head=head, max_ctx=max_ctx, seed=11, fused=f) for f in (False, True)]
     try:

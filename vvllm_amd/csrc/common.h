@@ -38,6 +38,17 @@ struct LinArgs {
     const float* xw;
     float xeps;
     int32_t xop;
+    // q/k/v plan epilogue with RoPE and the KV-cache append (k_dot plans,
+    // vvh_plan_set_rope): rope 0 = plain store; 1 = q rows, rotated; 2 = k
+    // rows, rotated and also written to row pos + m of `cache`; 3 = v rows,
+    // also written to row pos + m of `cache`.  For 1 and 2 a tile of head h
+    // holds the row pairs (h*rope_d + 8s + r, + rope_d/2), r < 8, so each lane
+    // owns the two halves of its rotation.
+    int32_t rope;
+    int32_t rope_d;
+    float rope_theta;
+    void* cache;
+    int32_t src;  // plans: index of the problem in the caller's list
     // fp32 activations on the GEMM: inp holds M rows of 2 * bk fp16 values
     // (K = 2 * bk), the high and low fp16 parts of each fp32 activation
     // scaled by a power of two, and xrs[m] = that row's inverse scale; the
@@ -145,8 +156,9 @@ int launch_skinny_grouped(const LinArgs* dev_table, int count, int64_t total_blo
 int launch_dot(const LinArgs& a, int out, bool early, void* stream);
 // dev_block_prob[b] = problem of block b; x_in_lds: dot_x_in_lds holds for
 // every problem; lds_bytes = the largest dot_lds_bytes of the problems
+// pos: position of activation row 0 for problems with a RoPE epilogue
 int launch_dot_grouped(const LinArgs* dev_table, const int32_t* dev_block_prob, int64_t total_blocks, int max_m,
-                       bool x_in_lds, size_t lds_bytes, int out, bool early, void* stream);
+                       bool x_in_lds, size_t lds_bytes, int out, bool early, int64_t pos, void* stream);
 int launch_gemm(const LinArgs& a, int out, void* stream);
 // k_gemm3 (gemm_kernels.hip): one 128 x BN tile (or one k split of it) per
 // block, K % 64 == 0; layout 1 = 128 x 192, 3 = 128 x 128

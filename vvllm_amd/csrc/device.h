@@ -101,6 +101,26 @@ __device__ __forceinline__ float silu_mul_ref(float g, float u)
     return r;
 }
 
+// Split-half RoPE of one pair (x0, x1) = (v[i], v[i + D/2]) of a head at
+// position p, in the reference's operation order (backend_naive.cc:93-137):
+// angle = p * (1 / theta^(2i/D)) with the power, cos and sin taken in fp64
+// and rounded to fp32.  The four products are rounded to fp32 before the sum
+// and the difference (the empty asm: otherwise the compiler may fuse them
+// into FMAs in one kernel and not in another), so k_rope and the RoPE
+// epilogue of a q/k/v plan rotate bit-identically.
+__device__ __forceinline__ void rope_rotate(float x0, float x1, int64_t p, int64_t i, int64_t D, float theta,
+                                            float& r0, float& r1)
+{
+    const float e = (float)(2 * i) / (float)D;
+    const float freq = 1.0f / (float)pow((double)theta, (double)e);
+    const float angle = (float)p * freq;
+    const float c = (float)cos((double)angle), sn = (float)sin((double)angle);
+    float a = x0 * c, b = x1 * sn, d = x0 * sn, f = x1 * c;
+    __asm__("" : "+v"(a), "+v"(b), "+v"(d), "+v"(f));
+    r0 = a - b;
+    r1 = d + f;
+}
+
 // Butterfly steps within rows of 16 lanes as DPP moves (one VALU op, no
 // LDS-pipeline round trip like __shfl_xor): quad_perm [1,0,3,2] and
 // [2,3,0,1] exchange with lanes l^1 and l^2; row_half_mirror (lane i <-> 7-i

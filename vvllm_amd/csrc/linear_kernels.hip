@@ -427,8 +427,54 @@ __device__ __forceinline__ void store_out_g(const LinArgs& a, int64_t m, int64_t
     *gbl(static_cast<OT*>(a.out) + o) = (OT)dot_epi(acc, *gbl(a.scales + n), a.bias != nullptr, bi, a.res != nullptr, rv);
 }
 
+// Epilogue of a q/k/v plan problem with RoPE (a.rope != 0) for the lane's
+// rows A and B of each activation row m: the linear's value rounded to OT
+// (what vvh_rope would read back), then for q/k rows the split-half rotation
+// of the pair (rows A and B are i and i + D/2 of one head) at position
+// pos + m, then the store; k and v rows also go to row pos + m of the cache.
+// Bit-identical to the plan's plain store followed by vvh_rope_append.
+template <typename OT, int MT, bool EARLY>
+__device__ __forceinline__ void dot_store_rope(const LinArgs& a, int64_t pos, int64_t rowA, int64_t rowB,
+                                               const float (&accA)[MT], const float (&accB)[MT],
+                                               const float (&e_sc)[2], const float (&e_bi)[2], const OT (&e_res)[MT][2])
+{
+    const int64_t rows[2] = {rowA, rowB};
+    float sc[2], bi[2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        sc[h] = EARLY ? e_sc[h] : *gbl(a.scales + rows[h]);
+        bi[h] = EARLY ? e_bi[h] : (a.bias ? *gbl(a.bias + rows[h]) : 0.0f);
+    }
+    OT* out = static_cast<OT*>(a.out);
+    OT* cache = static_cast<OT*>(a.cache);
+#pragma unroll
+    for (int m = 0; m < MT; m++) {
+        if (m >= a.M) continue;
+        OT v[2];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int64_t o = m * a.N + rows[h];
+            const float rv = a.res ? (EARLY ? (float)e_res[m][h] : (float)*gbl(static_cast<const OT*>(a.res) + o))
+                                   : 0.0f;
+            v[h] = (OT)dot_epi(h ? accB[m] : accA[m], sc[h], a.bias != nullptr, bi[h], a.res != nullptr, rv);
+        }
+        if (a.rope != 3) {
+            const int64_t i = rowA % a.rope_d;  // the pair's index within its head (< rope_d / 2)
+            float r0, r1;
+            rope_rotate((float)v[0], (float)v[1], pos + m, i, a.rope_d, a.rope_theta, r0, r1);
+            v[0] = (OT)r0;
+            v[1] = (OT)r1;
+        }
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            *gbl(out + m * a.N + rows[h]) = v[h];
+            if (a.rope != 1) *gbl(cache + (pos + m) * a.N + rows[h]) = v[h];
+        }
+    }
+}
+
 template <typename OT, int MT, bool XLDS, bool EARLY>
-__device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* smem)
+__device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* smem, int64_t pos)
 {
     // activations in the ring take 8 VGPRs per row and slot: halve the ring
     // for several rows so the wave keeps two waves per SIMD's worth of VGPRs
@@ -439,8 +485,20 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
     const int r = c.lane >> 3, ch = c.lane & 7;
     const int64_t n0 = c.tile * kDecodeTileN;
     const bool active = n0 < a.N && c.s0 < c.s1;
-    const int64_t rowA = n0 + r < a.N ? n0 + r : a.N - 1;
-    const int64_t rowB = n0 + 8 + r < a.N ? n0 + 8 + r : a.N - 1;
+    // rows of the lane: n0 + r and n0 + 8 + r, or for rotated q/k rows the
+    // pair (h*D + 8s + r, + D/2) of tile s of head h (rope_d % 16 == 0 and
+    // N % rope_d == 0, checked when the plan gets its RoPE epilogue)
+    const bool pair = a.rope == 1 || a.rope == 2;
+    int64_t rowA, rowB;
+    if (pair) {
+        const int64_t tph = a.rope_d / 16;
+        const int64_t hd = c.tile / tph, sd = c.tile - hd * tph;
+        rowA = hd * a.rope_d + 8 * sd + r;
+        rowB = rowA + a.rope_d / 2;
+    } else {
+        rowA = n0 + r < a.N ? n0 + r : a.N - 1;
+        rowB = n0 + 8 + r < a.N ? n0 + 8 + r : a.N - 1;
+    }
     const int8_t* wpA = a.w + rowA * a.K;
     const int8_t* wpB = a.w + rowB * a.K;
     const int32_t kmax = (int32_t)a.K - 16;  // last valid chunk start of a row
@@ -665,6 +723,11 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
             }
         }
     }
+    if (a.rope != 0) {
+        if (c.ks == 0 && ch == 0 && n0 < a.N) dot_store_rope<OT, MT, EARLY>(a, pos, rowA, rowB, accA, accB, e_sc, e_bi,
+                                                                          e_res);
+        return;
+    }
     if (c.ks == 0 && ch == 0 && n0 < a.N) {
 #pragma unroll
         for (int m = 0; m < MT; m++) {
@@ -693,19 +756,20 @@ template <typename OT, int MT, bool XLDS, bool EARLY>
 __global__ __launch_bounds__(256) void k_dot(LinArgs a)
 {
     extern __shared__ __attribute__((aligned(16))) char dot_smem[];
-    dot_body<OT, MT, XLDS, EARLY>(a, blockIdx.x, dot_smem);
+    dot_body<OT, MT, XLDS, EARLY>(a, blockIdx.x, dot_smem, 0);
 }
 
 // Grouped launch: block b serves problem block_prob[b].
 template <typename OT, int MT, bool XLDS, bool EARLY>
+// `pos`: the position of activation row 0 for problems with a RoPE epilogue.
 __global__ __launch_bounds__(256) void k_dot_grouped(const LinArgs* __restrict__ table,
-                                                     const int32_t* __restrict__ block_prob)
+                                                     const int32_t* __restrict__ block_prob, int64_t pos)
 {
     extern __shared__ __attribute__((aligned(16))) char dot_smem[];
     const int b = blockIdx.x;
     const int p = *cst(block_prob + b);
     const LinArgs a = table[p];
-    dot_body<OT, MT, XLDS, EARLY>(a, b - a.block_begin, dot_smem);
+    dot_body<OT, MT, XLDS, EARLY>(a, b - a.block_begin, dot_smem, pos);
 }
 
 // ---------------------------------------------------------------------------
@@ -1281,36 +1345,38 @@ int launch_dot(const LinArgs& a, int out, bool early, void* stream)
 }
 
 template <int MT, bool XLDS, bool EARLY>
-static void dot_grouped_launch(const LinArgs* table, const int32_t* block_prob, int out, dim3 grid, size_t lds,
-                               hipStream_t s)
+static void dot_grouped_launch(const LinArgs* table, const int32_t* block_prob, int64_t pos, int out, dim3 grid,
+                               size_t lds, hipStream_t s)
 {
     if (out == VVH_F32)
-        hipLaunchKernelGGL((k_dot_grouped<float, MT, XLDS, EARLY>), grid, dim3(256), lds, s, table, block_prob);
-    else hipLaunchKernelGGL((k_dot_grouped<f16, MT, XLDS, EARLY>), grid, dim3(256), lds, s, table, block_prob);
+        hipLaunchKernelGGL((k_dot_grouped<float, MT, XLDS, EARLY>), grid, dim3(256), lds, s, table, block_prob, pos);
+    else hipLaunchKernelGGL((k_dot_grouped<f16, MT, XLDS, EARLY>), grid, dim3(256), lds, s, table, block_prob, pos);
 }
 
 template <int MT, bool XLDS>
-static void dot_grouped_launch_e(const LinArgs* table, const int32_t* block_prob, int out, bool early, dim3 grid,
-                                 size_t lds, hipStream_t s)
+static void dot_grouped_launch_e(const LinArgs* table, const int32_t* block_prob, int64_t pos, int out, bool early,
+                                 dim3 grid, size_t lds, hipStream_t s)
 {
-    if (early) dot_grouped_launch<MT, XLDS, true>(table, block_prob, out, grid, lds, s);
-    else dot_grouped_launch<MT, XLDS, false>(table, block_prob, out, grid, lds, s);
+    if (early) dot_grouped_launch<MT, XLDS, true>(table, block_prob, pos, out, grid, lds, s);
+    else dot_grouped_launch<MT, XLDS, false>(table, block_prob, pos, out, grid, lds, s);
 }
 
 int launch_dot_grouped(const LinArgs* dev_table, const int32_t* dev_block_prob, int64_t total_blocks, int max_m,
-                       bool x_in_lds, size_t lds_bytes, int out, bool early, void* stream)
+                       bool x_in_lds, size_t lds_bytes, int out, bool early, int64_t pos, void* stream)
 {
     const dim3 grid((unsigned)total_blocks);
     hipStream_t s = S(stream);
+    const LinArgs* t = dev_table;
+    const int32_t* bp = dev_block_prob;
     if (max_m <= 1) {
-        if (x_in_lds) dot_grouped_launch_e<1, true>(dev_table, dev_block_prob, out, early, grid, lds_bytes, s);
-        else dot_grouped_launch_e<1, false>(dev_table, dev_block_prob, out, early, grid, lds_bytes, s);
+        if (x_in_lds) dot_grouped_launch_e<1, true>(t, bp, pos, out, early, grid, lds_bytes, s);
+        else dot_grouped_launch_e<1, false>(t, bp, pos, out, early, grid, lds_bytes, s);
     } else if (max_m <= 2) {
-        if (x_in_lds) dot_grouped_launch_e<2, true>(dev_table, dev_block_prob, out, early, grid, lds_bytes, s);
-        else dot_grouped_launch_e<2, false>(dev_table, dev_block_prob, out, early, grid, lds_bytes, s);
+        if (x_in_lds) dot_grouped_launch_e<2, true>(t, bp, pos, out, early, grid, lds_bytes, s);
+        else dot_grouped_launch_e<2, false>(t, bp, pos, out, early, grid, lds_bytes, s);
     } else {
-        if (x_in_lds) dot_grouped_launch_e<4, true>(dev_table, dev_block_prob, out, early, grid, lds_bytes, s);
-        else dot_grouped_launch_e<4, false>(dev_table, dev_block_prob, out, early, grid, lds_bytes, s);
+        if (x_in_lds) dot_grouped_launch_e<4, true>(t, bp, pos, out, early, grid, lds_bytes, s);
+        else dot_grouped_launch_e<4, false>(t, bp, pos, out, early, grid, lds_bytes, s);
     }
     return (int)hipGetLastError();
 }

@@ -181,12 +181,9 @@ __global__ __launch_bounds__(256) void k_rope(T* __restrict__ q, T* __restrict__
             s = hs / KVH;
             base = k + hs * D;
         }
-        const float e = (float)(2 * i) / (float)D;
-        const float freq = 1.0f / (float)pow((double)theta, (double)e);
-        const float angle = (float)(pos + s) * freq;
-        const float c = (float)cos((double)angle), sn = (float)sin((double)angle);
-        const float x0 = ldf(base, i), x1 = ldf(base, i + half);
-        const T r0 = (T)(x0 * c - x1 * sn), r1 = (T)(x0 * sn + x1 * c);
+        float f0, f1;
+        rope_rotate(ldf(base, i), ldf(base, i + half), pos + s, i, D, theta, f0, f1);
+        const T r0 = (T)f0, r1 = (T)f1;
         base[i] = r0;
         base[i + half] = r1;
         if constexpr (APPEND) {

@@ -8,6 +8,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -1197,6 +1198,7 @@ VVH_API int vvh_plan_create(const vvh_q8_problem* problems, size_t count, int ac
         a.N = (int64_t)q.N;
         a.K = (int64_t)q.K;
         a.ksplit = 1;
+        a.src = (int32_t)i;
         const bool aligned = q.K % 16 == 0 && aligned16(q.weight) && aligned16(q.inp);
         const int kf = choose_kernel(q.M, q.N, q.K, act_dtype, aligned);
         if (kf != K_SKINNY && kf != K_STREAM && kf != K_DOT) all_skinny = false;
@@ -1251,7 +1253,17 @@ VVH_API int vvh_plan_create(const vvh_q8_problem* problems, size_t count, int ac
     return VVH_OK;
 }
 
-VVH_API int vvh_plan_run(vvh_plan plan, void* stream)
+static int plan_run(vvh_plan plan, int64_t pos, void* stream);
+
+VVH_API int vvh_plan_run(vvh_plan plan, void* stream) { return plan_run(plan, 0, stream); }
+
+VVH_API int vvh_plan_run_pos(vvh_plan plan, size_t pos, void* stream)
+{
+    if (pos > (size_t)INT64_MAX / 2) return fail(VVH_ERR_INVALID_ARG, "position %zu out of range", pos);
+    return plan_run(plan, (int64_t)pos, stream);
+}
+
+static int plan_run(vvh_plan plan, int64_t pos, void* stream)
 {
     REQUIRE_INIT();
     const Plan* p;
@@ -1263,7 +1275,7 @@ VVH_API int vvh_plan_run(vvh_plan plan, void* stream)
     }
     if (p->dot) {
         const int e = launch_dot_grouped(p->sargs.table, p->dev_block_prob, p->total_blocks, p->max_m, p->x_in_lds,
-                                         p->lds_bytes, p->out, dot_early(p->total_blocks), stream);
+                                         p->lds_bytes, p->out, dot_early(p->total_blocks), pos, stream);
         return e == 0 ? VVH_OK : fail_hip((hipError_t)e, "grouped dot launch");
     }
     if (p->stream) {
@@ -1301,6 +1313,51 @@ VVH_API int vvh_plan_set_input_op(vvh_plan plan, int in_op, const float* in_w, f
         a.xw = in_w;
         a.xeps = in_eps;
     }
+    // the table is read by launches already queued: replace it once they are done
+    (void)hipDeviceSynchronize();
+    const hipError_t e = hipMemcpy(const_cast<LinArgs*>(p.sargs.table), p.args.data(), p.args.size() * sizeof(LinArgs),
+                                   hipMemcpyHostToDevice);
+    return e == hipSuccess ? VVH_OK : fail_hip(e, "plan table upload");
+}
+
+VVH_API int vvh_plan_set_rope(vvh_plan plan, size_t q_index, size_t k_index, size_t v_index, size_t head_dim,
+                              float theta, void* k_cache, void* v_cache)
+{
+    REQUIRE_INIT();
+    std::lock_guard<std::mutex> lock(g_pmu);
+    auto it = g_plans.find(plan);
+    if (it == g_plans.end()) return fail(VVH_ERR_UNKNOWN_HANDLE, "unknown plan %llu", (unsigned long long)plan);
+    Plan& p = it->second;
+    if (!p.dot) return fail(VVH_ERR_UNSUPPORTED, "RoPE epilogue needs a plan that runs as one k_dot_grouped launch");
+    if (q_index == k_index || q_index == v_index || k_index == v_index)
+        return fail(VVH_ERR_INVALID_ARG, "q, k and v must be different problems");
+    if (!k_cache || !v_cache) return fail(VVH_ERR_INVALID_ARG, "k_cache and v_cache must be device pointers");
+    if (head_dim < 16 || head_dim % 16 != 0 || head_dim > 4096)
+        return fail(VVH_ERR_UNSUPPORTED, "RoPE epilogue needs head_dim a multiple of 16 (got %zu)", head_dim);
+    if (!(theta > 0.0f) || !std::isfinite(theta)) return fail(VVH_ERR_INVALID_ARG, "theta must be positive");
+    LinArgs* q = nullptr;
+    LinArgs* k = nullptr;
+    LinArgs* v = nullptr;
+    for (LinArgs& a : p.args) {
+        if ((size_t)a.src == q_index) q = &a;
+        if ((size_t)a.src == k_index) k = &a;
+        if ((size_t)a.src == v_index) v = &a;
+    }
+    if (!q || !k || !v) return fail(VVH_ERR_INVALID_ARG, "q, k or v index names no (non-empty) problem of the plan");
+    if (q->N % (int64_t)head_dim != 0 || k->N % (int64_t)head_dim != 0 || k->N != v->N || k->M != v->M ||
+        q->M != k->M)
+        return fail(VVH_ERR_INVALID_ARG, "q rows (%lld), k and v rows (%lld, %lld) must be whole heads of %zu, with "
+                    "k and v alike and one M", (long long)q->N, (long long)k->N, (long long)v->N, head_dim);
+    q->rope = 1;
+    k->rope = 2;
+    v->rope = 3;
+    for (LinArgs* a : {q, k, v}) {
+        a->rope_d = (int32_t)head_dim;
+        a->rope_theta = theta;
+    }
+    q->cache = nullptr;
+    k->cache = k_cache;
+    v->cache = v_cache;
     // the table is read by launches already queued: replace it once they are done
     (void)hipDeviceSynchronize();
     const hipError_t e = hipMemcpy(const_cast<LinArgs*>(p.sargs.table), p.args.data(), p.args.size() * sizeof(LinArgs),

@@ -18,10 +18,11 @@ codes through linear_q8 (the int8 LM head).
 fused=True (fp16 only) issues the same arithmetic in fewer launches: the
 RMSNorms before q/k/v and gate_up and the SiLU-mul before down run in the
 input stage of the following linear (vvh_plan_set_input_op,
-vvh_linear_q8_dev_in), and RoPE writes the K/V cache rows itself
-(vvh_rope_append).  Each stage rounds exactly as the standalone operator, so
-the logits equal the unfused step's.  The final norm stays a launch of its
-own: every block of the LM head would repeat it.
+vvh_linear_q8_dev_in), RoPE and the K/V cache rows are the epilogue of the
+q/k/v plan (vvh_plan_set_rope, vvh_plan_run_pos), and the embedding row is
+gathered straight to fp16.  Each stage rounds exactly as the standalone
+operator, so the logits equal the unfused step's.  The final norm stays a
+launch of its own: every block of the LM head would repeat it.
 
 The model is synthetic (seeded N(0, 0.02) weights, no checkpoint); it is the
 measurement and end-to-end parity harness of this library's operators.  The
@@ -151,6 +152,8 @@ class Model:
             self.plans.append(h.value)
             if fused:
                 capi.call("vvh_plan_set_input_op", h.value, capi.IN_RMS_NORM, L["ln1"].ptr, c.eps)
+                # RoPE and the K/V cache rows in the plan's epilogue (problems 0, 1, 2 = q, k, v)
+                capi.call("vvh_plan_set_rope", h.value, 0, 1, 2, c.head_dim, c.theta, L["kc"].ptr, L["vc"].ptr)
 
     def fill_kv(self, seed: int = 0) -> None:
         """Seeded N(0, 1) rows in every layer's whole KV cache (a stand-in
@@ -166,7 +169,7 @@ class Model:
         c = self.cfg
         head = 1 if self.lm_head == "int8" or self.act == F32 else 2
         if self.fused:
-            return 2 + 6 * c.layers + 1 + head + 1
+            return 1 + 5 * c.layers + 1 + head + 1
         return (2 if self.act == F16 else 1) + 11 * c.layers + 1 + head + 1
 
     def close(self):
@@ -182,7 +185,9 @@ class Model:
         if pos >= self.max_ctx:
             raise ValueError(f"position {pos} beyond the KV cache ({self.max_ctx})")
         call = capi.call
-        if a == F16:
+        if a == F16 and self.fused:  # the table row rounded to fp16 once, in the gather
+            call("vvh_embedding", self.x.ptr, self.table.ptr, token, c.hidden, c.vocab, F16, stream)
+        elif a == F16:  # as BackendCUDA: the fp32 row, then the cast
             call("vvh_embedding", self.x32.ptr, self.table.ptr, token, c.hidden, c.vocab, F32, stream)
             call("vvh_convert", self.x.ptr, F16, self.x32.ptr, F32, c.hidden, stream)
         else:
@@ -228,13 +233,12 @@ class Model:
         call("vvh_argmax", self.logits32.ptr, c.vocab, self.token.ptr, stream)
 
     def _fused_layers(self, pos: int, scale: float, stream) -> None:
-        """The layers of the fused step: 6 launches per layer instead of 10
-        and two copies."""
+        """The layers of the fused step: 5 launches per layer (6 with the
+        attention merge) instead of 10 and two copies."""
         c, a, call = self.cfg, self.act, capi.call
         for L, plan in zip(self.layers, self.plans):
-            call("vvh_plan_run", plan, stream)  # q/k/v of rms_norm(x, ln1)
-            call("vvh_rope_append", self.q.ptr, self.k_new.ptr, self.v_new.ptr, L["kc"].ptr, L["vc"].ptr, 1, c.heads,
-                 c.kv_heads, c.head_dim, pos, c.theta, a, stream)
+            # q/k/v of rms_norm(x, ln1), RoPE'd, k and v rows written to the cache
+            call("vvh_plan_run_pos", plan, pos, stream)
             call("vvh_attention", self.attn.ptr, self.q.ptr, L["kc"].ptr, L["vc"].ptr, 1, pos + 1, c.heads,
                  c.kv_heads, c.head_dim, scale, a, stream)
             o = L["o"]
