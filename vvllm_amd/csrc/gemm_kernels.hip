@@ -41,7 +41,8 @@
 // in stage buffer q); each thread then owns one 8-wide column chunk (its 8
 // scales and biases loaded at kernel start), applies acc * scale + bias
 // (+ residual) in fp32 with one rounding, and stores rows with 16-byte
-// stores.  A tile wholly inside the problem (no split, N % 8 == 0) takes a
+// non-temporal stores (the output is not read again by this kernel; measured
+// M=2048 gate/up 30.8 -> 29.2 us against plain stores).  A tile wholly inside the problem (no split, N % 8 == 0) takes a
 // branch-free path: its residual rows are loaded before the accumulators go
 // to LDS, eight rows' LDS reads are in flight together and row addresses
 // advance by a fixed stride (measured: 1.44 -> 0.72 us for the reads and
@@ -414,7 +415,7 @@ __global__ __launch_bounds__(64 * (4 / TI) * WN, 1) void k_gemm3(LinArgs a)
                     h8 o8;
 #pragma unroll
                     for (int e = 0; e < 8; e++) o8[e] = (f16)v[e];
-                    *reinterpret_cast<h8*>(op) = o8;
+                    __builtin_nontemporal_store(o8, reinterpret_cast<h8*>(op));
                 } else {
                     if (a.res) {
                         const f4 r0 = __builtin_bit_cast(f4, rr[i][0]), r1 = __builtin_bit_cast(f4, rr[i][1]);
@@ -424,8 +425,8 @@ __global__ __launch_bounds__(64 * (4 / TI) * WN, 1) void k_gemm3(LinArgs a)
                             v[e + 4] += r1[e];
                         }
                     }
-                    *reinterpret_cast<f4*>(op) = f4{v[0], v[1], v[2], v[3]};
-                    *reinterpret_cast<f4*>(op + 4) = f4{v[4], v[5], v[6], v[7]};
+                    __builtin_nontemporal_store(f4{v[0], v[1], v[2], v[3]}, reinterpret_cast<f4*>(op));
+                    __builtin_nontemporal_store(f4{v[4], v[5], v[6], v[7]}, reinterpret_cast<f4*>(op + 4));
                 }
             }
         }
@@ -477,7 +478,7 @@ __global__ __launch_bounds__(64 * (4 / TI) * WN, 1) void k_gemm3(LinArgs a)
                     h8 o8;
 #pragma unroll
                     for (int e = 0; e < 8; e++) o8[e] = (f16)v[e];
-                    *reinterpret_cast<h8*>(static_cast<f16*>(a.out) + o) = o8;
+                    __builtin_nontemporal_store(o8, reinterpret_cast<h8*>(static_cast<f16*>(a.out) + o));
                 } else {
                     if (a.res) {
                         const f4 r0 = *reinterpret_cast<const f4*>(static_cast<const float*>(a.res) + o);
@@ -488,8 +489,9 @@ __global__ __launch_bounds__(64 * (4 / TI) * WN, 1) void k_gemm3(LinArgs a)
                             v[e + 4] += r1[e];
                         }
                     }
-                    *reinterpret_cast<f4*>(static_cast<float*>(a.out) + o) = f4{v[0], v[1], v[2], v[3]};
-                    *reinterpret_cast<f4*>(static_cast<float*>(a.out) + o + 4) = f4{v[4], v[5], v[6], v[7]};
+                    __builtin_nontemporal_store(f4{v[0], v[1], v[2], v[3]}, reinterpret_cast<f4*>(static_cast<float*>(a.out) + o));
+                    __builtin_nontemporal_store(f4{v[4], v[5], v[6], v[7]},
+                                                reinterpret_cast<f4*>(static_cast<float*>(a.out) + o + 4));
                 }
             } else {
                 for (int e = 0; e < 8 && en + e < a.N; e++) {
