@@ -1,5 +1,5 @@
-"""HIP graph capture of the int8 linear path (launch-overhead removal by
-graph capture of the decode step).
+"""HIP graph capture of the int8 linear path and of the split decode
+attention (launch-overhead removal by graph capture of the decode step).
 
 A decode plan, a several-row decode call, a GEMM and a split-K GEMM are
 issued on one stream, captured into a graph and replayed several times, with
@@ -165,6 +165,66 @@ def test_graph_survives_workspace_growth(gpu, oracle):
         run(large)  # eager work on the grown workspace between replays
         _check(hip.hipStreamSynchronize(stream), "sync")
         np.testing.assert_array_equal(out(large), eager_large, err_msg=f"large after replay {rep}")
+    hip.hipGraphExecDestroy(gexec)
+    hip.hipGraphDestroy(graph)
+    capi.call("vvh_workspace_release", stream)
+    hip.hipStreamDestroy(stream)
+
+
+def test_graph_split_attention(gpu, oracle):
+    """Split decode attention (blocks merged in the same launch through
+    per-kv-head arrival counters) captured into a graph and replayed, with
+    eager split calls on the same stream between the replays: every replay
+    matches the eager outputs bit for bit, so the counters are back at zero
+    after every call, captured or not."""
+    hip = _hip()
+    V = ctypes.c_void_p
+    hip.hipStreamCreate.argtypes = [ctypes.POINTER(V)]
+    hip.hipStreamSynchronize.argtypes = [V]
+    hip.hipStreamBeginCapture.argtypes = [V, ctypes.c_int]
+    hip.hipStreamEndCapture.argtypes = [V, ctypes.POINTER(V)]
+    hip.hipGraphInstantiate.argtypes = [ctypes.POINTER(V), V, V, V, ctypes.c_size_t]
+    hip.hipGraphLaunch.argtypes = [V, V]
+    hip.hipGraphExecDestroy.argtypes = [V]
+    hip.hipGraphDestroy.argtypes = [V]
+    hip.hipStreamDestroy.argtypes = [V]
+    stream = V()
+    _check(hip.hipStreamCreate(ctypes.byref(stream)), "hipStreamCreate")
+    H, KVH, D, T = 14, 2, 64, 6000
+    rng = np.random.default_rng(21)
+    q = capi.DevBuf.from_array(rng.normal(0, 1, (H, D)).astype(np.float16))
+    k = capi.DevBuf.from_array(rng.normal(0, 1, (T, KVH, D)).astype(np.float16))
+    v = capi.DevBuf.from_array(rng.normal(0, 1, (T, KVH, D)).astype(np.float16))
+    scale = float(1.0 / np.sqrt(np.float32(D)))
+    lens = (6000, 300, 2500)  # split, one block, split with fewer blocks
+    outs = [capi.DevBuf(H * D * 2) for _ in lens]
+
+    def issue(bufs):
+        for n, o in zip(lens, bufs):
+            capi.call("vvh_attention", o.ptr, q.ptr, k.ptr, v.ptr, 1, n, H, KVH, D, scale, F16, stream)
+
+    issue(outs)  # eager: sizes the stream's workspace and sets up its counters
+    _check(hip.hipStreamSynchronize(stream), "sync")
+    eager = [o.to_array(np.uint16, (H * D,)) for o in outs]
+    graph, gexec = V(), V()
+    _check(hip.hipStreamBeginCapture(stream, 0), "hipStreamBeginCapture")
+    issue(outs)
+    _check(hip.hipStreamEndCapture(stream, ctypes.byref(graph)), "hipStreamEndCapture")
+    _check(hip.hipGraphInstantiate(ctypes.byref(gexec), graph, None, None, 0), "hipGraphInstantiate")
+    others = [capi.DevBuf(H * D * 2) for _ in lens]
+    zero = np.zeros(H * D, np.uint16)
+    for rep in range(3):
+        for o in outs:
+            capi.call("vvh_memcpy_h2d", o.ptr, zero.ctypes.data, zero.nbytes)
+        print(f"[case] split attention replay {rep}", flush=True)
+        _check(hip.hipGraphLaunch(gexec, stream), "hipGraphLaunch")
+        _check(hip.hipStreamSynchronize(stream), "sync")
+        for i, (a, o) in enumerate(zip(eager, outs)):
+            np.testing.assert_array_equal(o.to_array(np.uint16, (H * D,)), a, err_msg=f"replay {rep}, len {lens[i]}")
+        issue(others)  # eager split calls between the replays
+        _check(hip.hipStreamSynchronize(stream), "sync")
+        for i, (a, o) in enumerate(zip(eager, others)):
+            np.testing.assert_array_equal(o.to_array(np.uint16, (H * D,)), a, err_msg=f"eager {rep}, len {lens[i]}")
     hip.hipGraphExecDestroy(gexec)
     hip.hipGraphDestroy(graph)
     capi.call("vvh_workspace_release", stream)

@@ -124,15 +124,19 @@ def test_embedding(gpu, d):
 
 
 # n_q = 1 rows with head_dim % 8 == 0, head_dim <= 128 and <= 16 query heads
-# per kv head take the split decode kernel (one chunk, two chunks with one key
-# in the second, many chunks, a span beyond the general kernel's limit,
-# blocks of several sub-chunks with a one-key tail, and head dims 8 to 32,
-# whose merge blocks fold up to 64 groups of partials);
-# the rest take the general kernel.
+# per kv head take a decode kernel: fp16 with head_dim 64 or 128 the
+# matrix-core one (one block of 4 waves up to 256 keys, of 8 waves up to 512,
+# split blocks merged in the same launch beyond: one key, a one-key tail,
+# 16 heads per kv head, spans of several chunks per wave), everything else
+# the lane kernel (one chunk, two chunks with one key in the second, many
+# chunks, a span beyond the general kernel's limit, blocks of several
+# sub-chunks with a one-key tail, and head dims 8 to 40, whose merge blocks
+# fold up to 64 groups of partials); the rest take the general kernel.
 ATT = [(1, 1, 14, 2, 64), (1, 100, 14, 2, 64), (1, 256, 14, 2, 64), (1, 257, 14, 2, 64), (1, 4096, 14, 2, 64),
        (1, 1000, 32, 8, 128), (1, 700, 16, 1, 64), (1, 513, 12, 12, 40), (1, 40000, 2, 1, 64), (1, 20001, 4, 1, 64),
        (4, 10, 12, 2, 128), (3, 5, 4, 4, 32), (1, 16000, 2, 1, 64), (2, 7, 16, 2, 256), (1, 300, 4, 2, 256),
-       (1, 300, 4, 2, 36), (1, 3000, 8, 2, 16), (1, 30000, 4, 1, 8), (1, 1200, 16, 4, 32)]
+       (1, 300, 4, 2, 36), (1, 3000, 8, 2, 16), (1, 30000, 4, 1, 8), (1, 1200, 16, 4, 32), (1, 512, 14, 2, 64),
+       (1, 450, 28, 4, 128), (1, 65, 12, 2, 128), (1, 513, 16, 1, 128)]
 
 
 @pytest.mark.parametrize("d", [F32, F16])
@@ -155,6 +159,28 @@ def test_attention(gpu, oracle, n_q, len0, H, KVH, D, d):
     for s in range(n_q):
         ref = oracle.causal_attention(q, k, v, s, len0 + s, scale)
         assert nerr(got[s], ref) <= TOL[d], f"query {s}"
+
+
+def test_attention_split_calls_in_a_row(gpu, oracle):
+    """Split decode calls back to back on one stream, with different block
+    counts: each merges its own partials (the per-kv-head arrival counters
+    are back at zero after every call), the outputs match the oracle."""
+    H, KVH, D = 14, 2, 64
+    T = 9000
+    rng = np.random.default_rng(11)
+    dq, q = up(rng.normal(0, 1, (1, H, D)), F16)
+    dk, k = up(rng.normal(0, 1, (T, KVH, D)), F16)
+    dv, v = up(rng.normal(0, 1, (T, KVH, D)), F16)
+    scale = float(1.0 / np.sqrt(np.float32(D)))
+    lens = (4096, 1500, 9000, 700, 4096)
+    outs = [capi.DevBuf(H * D * 2) for _ in lens]
+    for n, do in zip(lens, outs):
+        print(f"[case] split attention len={n}", flush=True)
+        capi.call("vvh_attention", do.ptr, dq.ptr, dk.ptr, dv.ptr, 1, n, H, KVH, D, scale, F16, None)
+    capi.sync()
+    for n, do in zip(lens, outs):
+        ref = oracle.causal_attention(q, k, v, 0, n, scale)
+        assert nerr(down(do, F16, (H * D,)), ref) <= TOL[F16], f"len {n}"
 
 
 @pytest.mark.parametrize("d", [F32, F16])

@@ -184,13 +184,28 @@ int launch_embedding(void* out, const float* table, int64_t token, int64_t hidde
 int64_t attention_max_len();
 int launch_attention(void* out, const void* q, const void* k, const void* v, int64_t n_q, int64_t len0, int64_t H,
                      int64_t KVH, int64_t D, float scale, int dtype, void* stream);
-// n_q = 1 fast path: grouped heads, split over the sequence; ws holds
-// attention_decode_ws_floats() floats when the span has more than one chunk
+// n_q = 1 fast path: grouped heads, split over the sequence into nb blocks
+// per kv head.  mfma: the fp16 matrix-core kernel (head_dim 64 or 128), which
+// merges the blocks in the same launch and, with nb > 1, needs a zeroed
+// arrival counter per kv head (cnt, kAttnCounters of them per stream); else
+// the lane kernel, followed by a merge launch when nb > 1.  ws holds
+// attention_decode_ws_floats() floats (none when nb == 1).
+struct AttnDecodePlan {
+    bool mfma;
+    int waves;          // waves per block of the mfma kernel (4 or 8)
+    int64_t per_block;  // keys per block
+    int64_t nb;         // blocks per kv head
+};
+constexpr int64_t kAttnCounters = 16384;
 bool attention_decode_ok(const void* k, const void* v, int64_t len, int64_t H, int64_t KVH, int64_t D);
 int64_t attention_decode_max_len();
-int64_t attention_decode_ws_floats(int64_t len, int64_t H, int64_t KVH, int64_t D);
-int launch_attention_decode(void* out, const void* q, const void* k, const void* v, int64_t len, int64_t H,
-                            int64_t KVH, int64_t D, float scale, float* ws, int dtype, void* stream);
+AttnDecodePlan attention_decode_plan(const void* q, int64_t len, int64_t H, int64_t KVH, int64_t D, int dtype);
+int64_t attention_decode_ws_floats(const AttnDecodePlan& p, int64_t H, int64_t D);
+inline bool attention_decode_counted(const AttnDecodePlan& p) { return p.mfma && p.nb > 1; }
+int launch_attention_decode(const AttnDecodePlan& p, void* out, const void* q, const void* k, const void* v,
+                            int64_t len, int64_t H, int64_t KVH, int64_t D, float scale, float* ws, unsigned* cnt,
+                            int dtype, void* stream);
+int launch_zero_u32(unsigned* p, int64_t n, void* stream);
 int launch_dense(void* out, const void* x, const void* w, int wdtype, const float* bias, const void* res, int64_t M,
                  int64_t N, int64_t K, int dtype, void* stream);
 int launch_matmul(void* out, const void* A, const float* B, int64_t M, int64_t N, int64_t K, int dtype, void* stream);

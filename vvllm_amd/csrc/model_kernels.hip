@@ -552,6 +552,232 @@ __global__ __launch_bounds__(1024) void k_attention_combine(T* __restrict__ out,
     }
 }
 
+// ---------------------------------------------------------------------------
+// Decode attention on the matrix cores: fp16 q, K and V, head_dim 64 or 128,
+// at most 16 query heads per kv head.  Same arithmetic as above (fp32 scores,
+// softmax and sums) with no runtime-shaped loops: a span of one key and a
+// span of 256 cost the same few dependent steps.
+//
+// Grid (KVH, nb), W = kDecWaves waves per block (4 or 8).  Block (g, b) takes kv head
+// g and the keys [b * per_block, (b + 1) * per_block); its span is cut into
+// chunks of 64 keys and wave w takes chunks w, w + W, ...  Per chunk, one
+// wave:
+//   S^T = K . q^T   v_mfma_f32_16x16x32_f16 per 16-key tile and 32 dims:
+//                   A = K rows (lane: key l % 16, the 8 dims of group l / 16,
+//                   one 16-byte load), B = the G query rows of the kv head
+//                   padded with zero rows to 16 columns.  Per lane the result
+//                   is head l % 16's scores for keys 4 (l / 16) + 0..3 of each
+//                   tile;
+//   softmax         online, per head: max and sum over the lane's 16 scores and
+//                   the 4 lanes of the head (exp2 of scores pre-scaled by
+//                   log2 e);
+//   O^T += V^T P^T  A = V^T (16 dims x 32 keys), gathered from the chunk's V
+//                   rows staged in the wave's LDS region; B = the lane's own
+//                   probabilities: the 8 keys a lane supplies to a 32-key step
+//                   are its scores of two tiles, so P needs no shuffles.  P is
+//                   split into fp16 hi + lo (two products), keeping ~22 bits.
+// The K-dimension order inside an MFMA is the same for A and B, so any
+// assignment of dims (or keys) to a lane's 8 slots that A and B share gives
+// the same sums.  The W waves merge their (max, sum, O) through LDS.  With one
+// block per kv head the block writes the output; otherwise each block writes
+// its partial (max, sum, O) to ws, and the last block of the kv head to arrive
+// (a per-kv-head counter in cnt, left at zero again for the next call) merges
+// the nb partials and writes the output: one launch either way.
+// ---------------------------------------------------------------------------
+constexpr int kDecChunk = 64;  // keys per wave and chunk
+
+typedef _Float16 h4v __attribute__((ext_vector_type(4)));
+
+template <int D, int kDecWaves>
+__global__ __launch_bounds__(64 * kDecWaves) void k_attention_decode_mfma(f16* __restrict__ out, const f16* __restrict__ q,
+                                                               const f16* __restrict__ k, const f16* __restrict__ v,
+                                                               int64_t len, int32_t H, int32_t KVH, float scale_log2,
+                                                               int64_t per_block, float* __restrict__ ws,
+                                                               unsigned* __restrict__ cnt)
+{
+    constexpr int DS = D / 32;              // 32-dim steps of a score tile
+    constexpr int DE = D / 16;              // 16-dim tiles of O^T
+    constexpr int VP = D + 4;               // V row pitch in LDS (halves): 2-byte gathers conflict-free
+    constexpr int VR = kDecChunk * D / 512; // 16-byte pieces of a chunk's V rows per lane
+    constexpr int OP = D + 4;               // O row pitch in LDS (floats)
+    static_assert(kDecWaves * kDecChunk * VP * 2 >= kDecWaves * 16 * OP * 4, "O aliases the V regions");
+    __shared__ __align__(16) _Float16 vs[kDecWaves * kDecChunk * VP];
+    __shared__ float wm[kDecWaves][16], wl[kDecWaves][16];
+    __shared__ int last_s;
+    const int g = blockIdx.x, tid = threadIdx.x, w = tid >> 6, lane = tid & 63, r = lane & 15, gr = lane >> 4;
+    const int G = H / KVH;
+    const int64_t kvs = (int64_t)KVH * D;
+    const int64_t kb = (int64_t)blockIdx.y * per_block;
+    const int64_t ke = kb + per_block < len ? kb + per_block : len;
+    const f16* kh = k + (int64_t)g * D;
+    const f16* vh = v + (int64_t)g * D;
+
+    h8 qb[DS];
+#pragma unroll
+    for (int s = 0; s < DS; s++) {
+        h8 z = {};
+        qb[s] = r < G ? *reinterpret_cast<const h8*>(q + ((int64_t)g * G + r) * D + 32 * s + 8 * gr) : z;
+    }
+    float m = -INFINITY, l = 0.0f;  // head r's running max (log2 units) and sum
+    f4 o[DE];
+#pragma unroll
+    for (int e = 0; e < DE; e++) o[e] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    _Float16* vw = vs + w * kDecChunk * VP;
+
+    for (int64_t c0 = kb + (int64_t)w * kDecChunk; c0 < ke; c0 += kDecWaves * kDecChunk) {
+        // every row index clamped into the span: rows past it are loaded from
+        // key ke - 1 and weighted 0
+        h8 ka[4][DS], vr[VR];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const int64_t key = c0 + 16 * t + r < ke ? c0 + 16 * t + r : ke - 1;
+#pragma unroll
+            for (int s = 0; s < DS; s++)
+                ka[t][s] = __builtin_nontemporal_load(reinterpret_cast<const h8*>(kh + key * kvs + 32 * s + 8 * gr));
+        }
+#pragma unroll
+        for (int i = 0; i < VR; i++) {
+            const int p = i * 64 + lane, row = p / (D / 8), col = (p % (D / 8)) * 8;
+            const int64_t key = c0 + row < ke ? c0 + row : ke - 1;
+            vr[i] = __builtin_nontemporal_load(reinterpret_cast<const h8*>(vh + key * kvs + col));
+        }
+        f4 sc[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            sc[t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int s = 0; s < DS; s++) sc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[t][s], qb[s], sc[t], 0, 0, 0);
+        }
+        float cm = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float x = c0 + 16 * t + 4 * gr + i < ke ? sc[t][i] * scale_log2 : -INFINITY;
+                sc[t][i] = x;
+                cm = fmaxf(cm, x);
+            }
+        cm = fmaxf(cm, __shfl_xor(cm, 16));
+        cm = fmaxf(cm, __shfl_xor(cm, 32));  // finite: key c0 is in the span
+        const float mn = fmaxf(m, cm), corr = exp2f(m - mn);  // corr = 0 on the first chunk
+        float ps = 0.0f;
+        h8 ph[2], pl[2];
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const float p = exp2f(sc[2 * u + j / 4][j % 4] - mn);
+                ps += p;
+                const _Float16 hi = (_Float16)p;
+                ph[u][j] = hi;
+                pl[u][j] = (_Float16)(p - (float)hi);
+            }
+        ps += __shfl_xor(ps, 16);
+        ps += __shfl_xor(ps, 32);
+        l = l * corr + ps;
+        m = mn;
+#pragma unroll
+        for (int e = 0; e < DE; e++) o[e] *= corr;
+        // the chunk's V rows into the wave's region; one wave's LDS accesses
+        // complete in order, so the gathers below read these rows, and the
+        // next chunk's writes follow this chunk's gathers
+#pragma unroll
+        for (int i = 0; i < VR; i++) {
+            const int p = i * 64 + lane, row = p / (D / 8), col = (p % (D / 8)) * 8;
+            *reinterpret_cast<h4v*>(vw + row * VP + col) = h4v{vr[i][0], vr[i][1], vr[i][2], vr[i][3]};
+            *reinterpret_cast<h4v*>(vw + row * VP + col + 4) = h4v{vr[i][4], vr[i][5], vr[i][6], vr[i][7]};
+        }
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+#pragma unroll
+            for (int e = 0; e < DE; e++) {
+                h8 va;
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const int key = 32 * u + (j < 4 ? 4 * gr + j : 16 + 4 * gr + j - 4);
+                    va[j] = vw[key * VP + 16 * e + r];
+                }
+                o[e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, ph[u], o[e], 0, 0, 0);
+                o[e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl[u], o[e], 0, 0, 0);
+            }
+    }
+
+    // merge the waves: (max, sum) per head, O^T per head as rows of os
+    __syncthreads();  // every wave is done with its V region
+    float* os = reinterpret_cast<float*>(vs);
+    if (gr == 0) {
+        wm[w][r] = m;
+        wl[w][r] = l;
+    }
+#pragma unroll
+    for (int e = 0; e < DE; e++) *reinterpret_cast<f4*>(os + (w * 16 + r) * OP + 16 * e + 4 * gr) = o[e];
+    __syncthreads();
+    const bool split = gridDim.y > 1;
+    for (int idx = tid; idx < G * D; idx += 64 * kDecWaves) {
+        const int h = idx / D, d = idx - h * D;
+        float M = -INFINITY;
+#pragma unroll
+        for (int ww = 0; ww < kDecWaves; ww++) M = fmaxf(M, wm[ww][h]);  // finite: wave 0 has a key
+        float num = 0.0f, den = 0.0f;
+#pragma unroll
+        for (int ww = 0; ww < kDecWaves; ww++) {
+            const float f = exp2f(wm[ww][h] - M);  // 0 for a wave without keys
+            num += f * os[(ww * 16 + h) * OP + d];
+            den += f * wl[ww][h];
+        }
+        if (!split) {
+            out[((int64_t)g * G + h) * D + d] = (f16)(num / den);
+        } else {
+            float* pw = ws + ((int64_t)blockIdx.y * H + (int64_t)g * G + h) * (D + 2);
+            pw[2 + d] = num;
+            if (d == 0) {
+                pw[0] = M;
+                pw[1] = den;
+            }
+        }
+    }
+    if (!split) return;
+    // the partials visible device-wide before the block counts itself in
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) last_s = atomicAdd(cnt + g, 1u) == gridDim.y - 1;
+    __syncthreads();
+    if (!last_s) return;
+    __threadfence();  // the other blocks' partials, not stale cached lines
+    const int nb = (int)gridDim.y;
+    for (int idx = tid; idx < G * D; idx += 64 * kDecWaves) {
+        const int h = idx / D, d = idx - h * D;
+        const float* pw = ws + ((int64_t)g * G + h) * (D + 2);
+        const int64_t step = (int64_t)H * (D + 2);
+        float M = -INFINITY, num = 0.0f, den = 0.0f;
+#pragma unroll 4
+        for (int b = 0; b < nb; b++) {
+            const float mb = pw[b * step], lb = pw[b * step + 1], ob = pw[b * step + 2 + d];
+            const float mx = fmaxf(M, mb);  // mb is finite: every block has a key
+            const float a = exp2f(M - mx), c = exp2f(mb - mx);
+            num = num * a + ob * c;
+            den = den * a + lb * c;
+            M = mx;
+        }
+        out[((int64_t)g * G + h) * D + d] = (f16)(num / den);
+    }
+    if (tid == 0) cnt[g] = 0u;  // ready for the next call on this stream
+}
+
+__global__ void k_zero_u32(unsigned* __restrict__ p, int64_t n)
+{
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+int launch_zero_u32(unsigned* p, int64_t n, void* stream)
+{
+    if (n <= 0) return 0;
+    hipLaunchKernelGGL(k_zero_u32, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       p, n);
+    return (int)hipGetLastError();
+}
+
 bool attention_decode_ok(const void* k, const void* v, int64_t len, int64_t H, int64_t KVH, int64_t D)
 {
     return D % 8 == 0 && D <= kAttnMaxD && H / KVH <= kAttnMaxG && reinterpret_cast<uintptr_t>(k) % 16 == 0 &&
@@ -560,8 +786,9 @@ bool attention_decode_ok(const void* k, const void* v, int64_t len, int64_t H, i
 
 int64_t attention_decode_max_len() { return (int64_t)1 << 30; }
 
-// Keys per block: whole sub-chunks, as few as keep at most ~512 blocks in
-// the grid (two per CU), so short spans get one sub-chunk per block.
+// Keys per block of the lane kernel: whole sub-chunks, as few as keep at
+// most ~512 blocks in the grid (two per CU), so short spans get one
+// sub-chunk per block.
 static int64_t attn_per_block(int64_t len, int64_t KVH, int64_t D)
 {
     const int64_t C = 256 / attn_lanes((int)D);
@@ -571,11 +798,39 @@ static int64_t attn_per_block(int64_t len, int64_t KVH, int64_t D)
     return per * C;
 }
 
-int64_t attention_decode_ws_floats(int64_t len, int64_t H, int64_t KVH, int64_t D)
+// The matrix-core kernel takes spans of up to 8 chunks of 64 keys in one
+// block per kv head, one chunk per wave (4 waves up to 4 chunks, else 8), with
+// no cross-block merge.  Longer spans take 4-wave blocks, one chunk per wave
+// while that keeps at most 64 blocks per kv head and ~256 blocks in all,
+// several beyond.  (Graph-replayed, Qwen2.5-0.5B shapes: a wave's second
+// chunk costs ~2 us, the cross-block merge ~3.4 us, so 8 waves in one block
+// win at 512 keys and 4-wave blocks at 1024 and beyond.)
+AttnDecodePlan attention_decode_plan(const void* q, int64_t len, int64_t H, int64_t KVH, int64_t D, int dtype)
 {
-    const int64_t per = attn_per_block(len, KVH, D);
-    const int64_t nb = (len + per - 1) / per;
-    return nb > 1 ? nb * H * (D + 2) : 0;
+    AttnDecodePlan p{};
+    p.mfma = dtype == VVH_F16 && (D == 64 || D == 128) && H / KVH <= 16 && KVH <= kAttnCounters &&
+             reinterpret_cast<uintptr_t>(q) % 16 == 0;
+    if (p.mfma) {
+        const int64_t chunks = (len + kDecChunk - 1) / kDecChunk;
+        if (chunks <= 8) {
+            p.waves = chunks <= 4 ? 4 : 8;
+            p.per_block = p.waves * kDecChunk;
+        } else {
+            p.waves = 4;
+            const int64_t nb_cap = std::min<int64_t>(64, std::max<int64_t>(1, 256 / KVH));
+            const int64_t per_wave = (chunks + 4 * nb_cap - 1) / (4 * nb_cap);
+            p.per_block = per_wave * 4 * kDecChunk;
+        }
+    } else {
+        p.per_block = attn_per_block(len, KVH, D);
+    }
+    p.nb = (len + p.per_block - 1) / p.per_block;
+    return p;
+}
+
+int64_t attention_decode_ws_floats(const AttnDecodePlan& p, int64_t H, int64_t D)
+{
+    return p.nb > 1 ? p.nb * H * (D + 2) : 0;
 }
 
 // Combine block: D x S threads, S (a power of two, 1 <= S <= 1024 / D) the
@@ -588,14 +843,26 @@ static unsigned combine_threads(int64_t nb, int64_t D)
     return (unsigned)(S * D);
 }
 
-int launch_attention_decode(void* out, const void* q, const void* k, const void* v, int64_t len, int64_t H,
-                            int64_t KVH, int64_t D, float scale, float* ws, int dtype, void* stream)
+int launch_attention_decode(const AttnDecodePlan& p, void* out, const void* q, const void* k, const void* v,
+                            int64_t len, int64_t H, int64_t KVH, int64_t D, float scale, float* ws, unsigned* cnt,
+                            int dtype, void* stream)
 {
-    const int64_t per = attn_per_block(len, KVH, D);
-    const int64_t nb = (len + per - 1) / per;
+    const int64_t per = p.per_block, nb = p.nb;
     const dim3 grid((unsigned)KVH, (unsigned)nb);
-    const bool one = per <= 256 / attn_lanes((int)D);  // one sub-chunk per block
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (p.mfma) {
+        const float sl = (float)((double)scale * 1.4426950408889634);  // scores in log2 units
+        auto go = [&](auto kern) {
+            hipLaunchKernelGGL(kern, grid, dim3(64 * p.waves), 0, s, (f16*)out, (const f16*)q, (const f16*)k,
+                               (const f16*)v, len, (int32_t)H, (int32_t)KVH, sl, per, ws, cnt);
+        };
+        if (D == 64)
+            p.waves == 8 ? go(k_attention_decode_mfma<64, 8>) : go(k_attention_decode_mfma<64, 4>);
+        else
+            p.waves == 8 ? go(k_attention_decode_mfma<128, 8>) : go(k_attention_decode_mfma<128, 4>);
+        return (int)hipGetLastError();
+    }
+    const bool one = per <= 256 / attn_lanes((int)D);  // one sub-chunk per block
     if (dtype == VVH_F16) {
         if (one)
             hipLaunchKernelGGL((k_attention_decode<f16, true>), grid, dim3(256), 0, s, (f16*)out, (const f16*)q,

@@ -123,6 +123,7 @@ struct Workspace {
     void* p = nullptr;
     std::size_t bytes = 0;
     std::vector<void*> retired;
+    unsigned* cnt = nullptr;  // kAttnCounters arrival counters of the decode attention, zero between calls
 };
 std::mutex g_wsmu;
 std::unordered_map<void*, Workspace> g_ws;
@@ -144,6 +145,32 @@ int workspace_for(void* stream, std::size_t bytes, float** out)
         w.bytes = nb;
     }
     *out = static_cast<float*>(w.p);
+    return VVH_OK;
+}
+
+// The stream's decode-attention counters: allocated on first use and zeroed
+// by a kernel queued on the stream ahead of the call that needs them (a
+// kernel, not a memset, so that a capture of that call records it as a
+// kernel node); every call leaves them at zero again.
+int counters_for(void* stream, unsigned** out)
+{
+    std::lock_guard<std::mutex> lock(g_wsmu);
+    Workspace& w = g_ws[stream];
+    if (!w.cnt) {
+        void* p = nullptr;
+        hipError_t e = hipMalloc(&p, (std::size_t)kAttnCounters * sizeof(unsigned));
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            return fail_hip(e, "attention counters hipMalloc");
+        }
+        const int st = launch_zero_u32(static_cast<unsigned*>(p), kAttnCounters, stream);
+        if (st != 0) {
+            (void)hipFree(p);
+            return fail_hip((hipError_t)st, "attention counters zero launch");
+        }
+        w.cnt = static_cast<unsigned*>(p);
+    }
+    *out = w.cnt;
     return VVH_OK;
 }
 
@@ -1097,6 +1124,7 @@ VVH_API int vvh_workspace_release(void* stream)
     if (e != hipSuccess) return fail_hip(e, "workspace release: synchronize");
     for (void* p : it->second.retired) (void)hipFree(p);
     if (it->second.p) (void)hipFree(it->second.p);
+    if (it->second.cnt) (void)hipFree(it->second.cnt);
     g_ws.erase(it);
     return VVH_OK;
 }
@@ -1567,15 +1595,22 @@ VVH_API int vvh_attention(void* out, const void* q, const void* k, const void* v
         return fail(VVH_ERR_UNSUPPORTED, "attention span %zu > %lld", len0 + n_q - 1, (long long)attention_max_len());
     REQUIRE_INIT();
     if (decode) {
+        const AttnDecodePlan p = attention_decode_plan(q, (int64_t)len0, (int64_t)num_heads, (int64_t)num_kv_heads,
+                                                       (int64_t)head_dim, dtype);
         float* ws = nullptr;
-        const int64_t wsf = attention_decode_ws_floats((int64_t)len0, (int64_t)num_heads, (int64_t)num_kv_heads,
-                                                       (int64_t)head_dim);
+        unsigned* cnt = nullptr;
+        const int64_t wsf = attention_decode_ws_floats(p, (int64_t)num_heads, (int64_t)head_dim);
         if (wsf > 0) {
             const int st = workspace_for(stream, (std::size_t)wsf * 4, &ws);
             if (st != VVH_OK) return st;
         }
-        return ret_launch(launch_attention_decode(out, q, k, v, (int64_t)len0, (int64_t)num_heads,
-                                                  (int64_t)num_kv_heads, (int64_t)head_dim, scale, ws, dtype, stream),
+        if (attention_decode_counted(p)) {
+            const int st = counters_for(stream, &cnt);
+            if (st != VVH_OK) return st;
+        }
+        return ret_launch(launch_attention_decode(p, out, q, k, v, (int64_t)len0, (int64_t)num_heads,
+                                                  (int64_t)num_kv_heads, (int64_t)head_dim, scale, ws, cnt, dtype,
+                                                  stream),
                           "attention launch");
     }
     return ret_launch(launch_attention(out, q, k, v, (int64_t)n_q, (int64_t)len0, (int64_t)num_heads,
