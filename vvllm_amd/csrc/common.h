@@ -152,13 +152,15 @@ int launch_skinny(const LinArgs& a, int out, void* stream);
 int launch_skinny_grouped(const LinArgs* dev_table, int count, int64_t total_blocks, int out,
                           void* stream);
 // early: the variant for launches with few blocks, which requests the
-// epilogue operands and the weight ring before staging the activations
-int launch_dot(const LinArgs& a, int out, bool early, void* stream);
+// epilogue operands and the weight ring before staging the activations;
+// depth: k steps in flight per wave (2, 4 or 8)
+int launch_dot(const LinArgs& a, int out, bool early, int depth, void* stream);
 // dev_block_prob[b] = problem of block b; x_in_lds: dot_x_in_lds holds for
 // every problem; lds_bytes = the largest dot_lds_bytes of the problems
 // pos: position of activation row 0 for problems with a RoPE epilogue
 int launch_dot_grouped(const LinArgs* dev_table, const int32_t* dev_block_prob, int64_t total_blocks, int max_m,
-                       bool x_in_lds, size_t lds_bytes, int out, bool early, int64_t pos, void* stream);
+                       bool x_in_lds, size_t lds_bytes, int out, bool early, int depth, int64_t pos,
+                       void* stream);
 int launch_gemm(const LinArgs& a, int out, void* stream);
 // k_gemm3 (gemm_kernels.hip): one 128 x BN tile (or one k split of it) per
 // block, K % 64 == 0; layout 1 = 128 x 192, 3 = 128 x 128

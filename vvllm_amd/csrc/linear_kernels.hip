@@ -363,7 +363,10 @@ __global__ __launch_bounds__(256) void k_skinny_grouped(const LinArgs* __restric
 // the wave's range re-read its last step, chunks past K read inside the row)
 // and masked when consumed, so the wait counts of the pipeline are fixed.
 // ---------------------------------------------------------------------------
-constexpr int kDotDepth = 8;    // k steps (2 loads each) in flight per wave
+// The ring depth DEPTH (k steps of 2 loads each in flight per wave) is a
+// template parameter, 2, 4 or 8, chosen per launch to hold the waves' k
+// ranges (dot_depth on the host): each slot past a wave's range re-reads a
+// step and costs issue time on a short call.
 
 __device__ __forceinline__ DecodeCoord dot_coord(const LinArgs& a, int64_t block)
 {
@@ -473,12 +476,12 @@ __device__ __forceinline__ void dot_store_rope(const LinArgs& a, int64_t pos, in
     }
 }
 
-template <typename OT, int MT, bool XLDS, bool EARLY>
+template <typename OT, int MT, bool XLDS, bool EARLY, int DEPTH>
 __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* smem, int64_t pos)
 {
     // activations in the ring take 8 VGPRs per row and slot: halve the ring
     // for several rows so the wave keeps two waves per SIMD's worth of VGPRs
-    constexpr int D = (XLDS || MT == 1) ? kDotDepth : kDotDepth / 2;
+    constexpr int D = (XLDS || MT == 1 || DEPTH < 4) ? DEPTH : DEPTH / 2;
     DotRed& red = *reinterpret_cast<DotRed*>(smem);
     f16* xs = reinterpret_cast<f16*>(smem + kDotRedBytes);
     const DecodeCoord c = dot_coord(a, block);
@@ -752,16 +755,16 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
 
 // XLDS = the activations are staged in LDS (dot_x_in_lds, decided on the
 // host for the launch: for a grouped launch it must hold for every problem).
-template <typename OT, int MT, bool XLDS, bool EARLY>
+template <typename OT, int MT, bool XLDS, bool EARLY, int DEPTH>
 __global__ __launch_bounds__(256) void k_dot(LinArgs a)
 {
     extern __shared__ __attribute__((aligned(16))) char dot_smem[];
-    dot_body<OT, MT, XLDS, EARLY>(a, blockIdx.x, dot_smem, 0);
+    dot_body<OT, MT, XLDS, EARLY, DEPTH>(a, blockIdx.x, dot_smem, 0);
 }
 
 // Grouped launch: block b serves problem block_prob[b].
-template <typename OT, int MT, bool XLDS, bool EARLY>
 // `pos`: the position of activation row 0 for problems with a RoPE epilogue.
+template <typename OT, int MT, bool XLDS, bool EARLY, int DEPTH>
 __global__ __launch_bounds__(256) void k_dot_grouped(const LinArgs* __restrict__ table,
                                                      const int32_t* __restrict__ block_prob, int64_t pos)
 {
@@ -769,7 +772,7 @@ __global__ __launch_bounds__(256) void k_dot_grouped(const LinArgs* __restrict__
     const int b = blockIdx.x;
     const int p = *cst(block_prob + b);
     const LinArgs a = table[p];
-    dot_body<OT, MT, XLDS, EARLY>(a, b - a.block_begin, dot_smem, pos);
+    dot_body<OT, MT, XLDS, EARLY, DEPTH>(a, b - a.block_begin, dot_smem, pos);
 }
 
 // ---------------------------------------------------------------------------
@@ -1312,71 +1315,93 @@ int launch_skinny_grouped(const LinArgs* dev_table, int count, int64_t total_blo
     return (int)hipGetLastError();
 }
 
-template <int MT, bool XLDS, bool EARLY>
+template <int MT, bool XLDS, bool EARLY, int DEPTH>
 static void dot_launch(const LinArgs& a, int out, dim3 grid, size_t lds, hipStream_t s)
 {
-    if (out == VVH_F32) hipLaunchKernelGGL((k_dot<float, MT, XLDS, EARLY>), grid, dim3(256), lds, s, a);
-    else hipLaunchKernelGGL((k_dot<f16, MT, XLDS, EARLY>), grid, dim3(256), lds, s, a);
+    if (out == VVH_F32) hipLaunchKernelGGL((k_dot<float, MT, XLDS, EARLY, DEPTH>), grid, dim3(256), lds, s, a);
+    else hipLaunchKernelGGL((k_dot<f16, MT, XLDS, EARLY, DEPTH>), grid, dim3(256), lds, s, a);
+}
+
+template <int MT, bool XLDS, bool EARLY>
+static void dot_launch_d(const LinArgs& a, int out, int depth, dim3 grid, size_t lds, hipStream_t s)
+{
+    // activations outside LDS (rows too long for it) always take 8
+    if (XLDS && depth <= 2) dot_launch<MT, XLDS, EARLY, XLDS ? 2 : 8>(a, out, grid, lds, s);
+    else if (XLDS && depth <= 4) dot_launch<MT, XLDS, EARLY, XLDS ? 4 : 8>(a, out, grid, lds, s);
+    else dot_launch<MT, XLDS, EARLY, 8>(a, out, grid, lds, s);
 }
 
 template <int MT, bool XLDS>
-static void dot_launch_e(const LinArgs& a, int out, bool early, dim3 grid, size_t lds, hipStream_t s)
+static void dot_launch_e(const LinArgs& a, int out, bool early, int depth, dim3 grid, size_t lds, hipStream_t s)
 {
-    if (early) dot_launch<MT, XLDS, true>(a, out, grid, lds, s);
-    else dot_launch<MT, XLDS, false>(a, out, grid, lds, s);
+    if (early) dot_launch_d<MT, XLDS, true>(a, out, depth, grid, lds, s);
+    else dot_launch_d<MT, XLDS, false>(a, out, depth, grid, lds, s);
 }
 
-int launch_dot(const LinArgs& a, int out, bool early, void* stream)
+int launch_dot(const LinArgs& a, int out, bool early, int depth, void* stream)
 {
     const dim3 grid((unsigned)dot_blocks(a));
     const size_t lds = dot_lds_bytes(a.M, a.K);
     const bool xl = dot_x_in_lds(a.M, a.K);
     if (a.M <= 1) {
-        if (xl) dot_launch_e<1, true>(a, out, early, grid, lds, S(stream));
-        else dot_launch_e<1, false>(a, out, early, grid, lds, S(stream));
+        if (xl) dot_launch_e<1, true>(a, out, early, depth, grid, lds, S(stream));
+        else dot_launch_e<1, false>(a, out, early, depth, grid, lds, S(stream));
     } else if (a.M <= 2) {
-        if (xl) dot_launch_e<2, true>(a, out, early, grid, lds, S(stream));
-        else dot_launch_e<2, false>(a, out, early, grid, lds, S(stream));
+        if (xl) dot_launch_e<2, true>(a, out, early, depth, grid, lds, S(stream));
+        else dot_launch_e<2, false>(a, out, early, depth, grid, lds, S(stream));
     } else {
-        if (xl) dot_launch_e<4, true>(a, out, early, grid, lds, S(stream));
-        else dot_launch_e<4, false>(a, out, early, grid, lds, S(stream));
+        if (xl) dot_launch_e<4, true>(a, out, early, depth, grid, lds, S(stream));
+        else dot_launch_e<4, false>(a, out, early, depth, grid, lds, S(stream));
     }
     return (int)hipGetLastError();
 }
 
-template <int MT, bool XLDS, bool EARLY>
+template <int MT, bool XLDS, bool EARLY, int DEPTH>
 static void dot_grouped_launch(const LinArgs* table, const int32_t* block_prob, int64_t pos, int out, dim3 grid,
                                size_t lds, hipStream_t s)
 {
     if (out == VVH_F32)
-        hipLaunchKernelGGL((k_dot_grouped<float, MT, XLDS, EARLY>), grid, dim3(256), lds, s, table, block_prob, pos);
-    else hipLaunchKernelGGL((k_dot_grouped<f16, MT, XLDS, EARLY>), grid, dim3(256), lds, s, table, block_prob, pos);
+        hipLaunchKernelGGL((k_dot_grouped<float, MT, XLDS, EARLY, DEPTH>), grid, dim3(256), lds, s, table, block_prob,
+                           pos);
+    else
+        hipLaunchKernelGGL((k_dot_grouped<f16, MT, XLDS, EARLY, DEPTH>), grid, dim3(256), lds, s, table, block_prob,
+                           pos);
+}
+
+template <int MT, bool XLDS, bool EARLY>
+static void dot_grouped_launch_d(const LinArgs* table, const int32_t* block_prob, int64_t pos, int out, int depth,
+                                 dim3 grid, size_t lds, hipStream_t s)
+{
+    if (XLDS && depth <= 2) dot_grouped_launch<MT, XLDS, EARLY, XLDS ? 2 : 8>(table, block_prob, pos, out, grid, lds, s);
+    else if (XLDS && depth <= 4)
+        dot_grouped_launch<MT, XLDS, EARLY, XLDS ? 4 : 8>(table, block_prob, pos, out, grid, lds, s);
+    else dot_grouped_launch<MT, XLDS, EARLY, 8>(table, block_prob, pos, out, grid, lds, s);
 }
 
 template <int MT, bool XLDS>
 static void dot_grouped_launch_e(const LinArgs* table, const int32_t* block_prob, int64_t pos, int out, bool early,
-                                 dim3 grid, size_t lds, hipStream_t s)
+                                 int depth, dim3 grid, size_t lds, hipStream_t s)
 {
-    if (early) dot_grouped_launch<MT, XLDS, true>(table, block_prob, pos, out, grid, lds, s);
-    else dot_grouped_launch<MT, XLDS, false>(table, block_prob, pos, out, grid, lds, s);
+    if (early) dot_grouped_launch_d<MT, XLDS, true>(table, block_prob, pos, out, depth, grid, lds, s);
+    else dot_grouped_launch_d<MT, XLDS, false>(table, block_prob, pos, out, depth, grid, lds, s);
 }
 
 int launch_dot_grouped(const LinArgs* dev_table, const int32_t* dev_block_prob, int64_t total_blocks, int max_m,
-                       bool x_in_lds, size_t lds_bytes, int out, bool early, int64_t pos, void* stream)
+                       bool x_in_lds, size_t lds_bytes, int out, bool early, int depth, int64_t pos, void* stream)
 {
     const dim3 grid((unsigned)total_blocks);
     hipStream_t s = S(stream);
     const LinArgs* t = dev_table;
     const int32_t* bp = dev_block_prob;
     if (max_m <= 1) {
-        if (x_in_lds) dot_grouped_launch_e<1, true>(t, bp, pos, out, early, grid, lds_bytes, s);
-        else dot_grouped_launch_e<1, false>(t, bp, pos, out, early, grid, lds_bytes, s);
+        if (x_in_lds) dot_grouped_launch_e<1, true>(t, bp, pos, out, early, depth, grid, lds_bytes, s);
+        else dot_grouped_launch_e<1, false>(t, bp, pos, out, early, depth, grid, lds_bytes, s);
     } else if (max_m <= 2) {
-        if (x_in_lds) dot_grouped_launch_e<2, true>(t, bp, pos, out, early, grid, lds_bytes, s);
-        else dot_grouped_launch_e<2, false>(t, bp, pos, out, early, grid, lds_bytes, s);
+        if (x_in_lds) dot_grouped_launch_e<2, true>(t, bp, pos, out, early, depth, grid, lds_bytes, s);
+        else dot_grouped_launch_e<2, false>(t, bp, pos, out, early, depth, grid, lds_bytes, s);
     } else {
-        if (x_in_lds) dot_grouped_launch_e<4, true>(t, bp, pos, out, early, grid, lds_bytes, s);
-        else dot_grouped_launch_e<4, false>(t, bp, pos, out, early, grid, lds_bytes, s);
+        if (x_in_lds) dot_grouped_launch_e<4, true>(t, bp, pos, out, early, depth, grid, lds_bytes, s);
+        else dot_grouped_launch_e<4, false>(t, bp, pos, out, early, depth, grid, lds_bytes, s);
     }
     return (int)hipGetLastError();
 }

@@ -104,6 +104,7 @@ struct Plan {
     size_t lds_bytes = 0;
     StreamArgs sargs{};
     int depth = 0;
+    int dot_depth = 8;           // k_dot_grouped ring depth: the deepest any problem needs
     int max_m = 0;
     void* dev_stream = nullptr;  // tile_prob, list, list_off
 };
@@ -302,6 +303,20 @@ bool stream_worth(int64_t tiles) { return tiles >= (int64_t)(g_cu_count > 0 ? g_
 constexpr int64_t kDotEarlyBlocksPerCu = 1;
 bool dot_early(int64_t blocks) { return blocks <= (int64_t)(g_cu_count > 0 ? g_cu_count : 256) * kDotEarlyBlocksPerCu; }
 
+// k_dot weight-ring depth: the smallest of 2, 4 and 8 k steps that holds a
+// wave's k range; 4 for longer ranges.  Each ring slot past the range
+// re-reads a step (so that every wait in the pipeline has a fixed count),
+// which costs issue time.  Graph-replayed at M = 1: 2 steps per wave (Qwen2.5-
+// 0.5B q/k/v/o/gate/up), depth 8 -> 2: o 4.34 -> 3.93 us, gate/up 7.10 ->
+// 5.70 us; 10 steps per wave (0.5B down), depth 8 -> 4: 6.57 -> 6.08 us,
+// 18 steps (1.5B down) 8.64 -> 8.55 us.
+int dot_depth(int64_t K, int ksplit)
+{
+    const int64_t steps = (K + kDotStep - 1) / kDotStep;
+    const int64_t per_wave = (steps + ksplit - 1) / ksplit;
+    return per_wave <= 2 ? 2 : per_wave <= 4 ? 4 : per_wave <= 8 ? 8 : 4;
+}
+
 // fp32 activations take the GEMM (on their split fp16 form) from this many
 // rows on, when K % 64 == 0; below it k_gemv_f32, which streams the weights
 // once per 8 rows.
@@ -414,7 +429,7 @@ int run_call(const LinArgs& base, int kernel, int act, int outd, void* stream, c
             const int64_t tiles = (a.N + kDecodeTileN - 1) / kDecodeTileN;
             a.ksplit = choose_ksplit(tiles, a.K, kDotStep);
             if (dot_blocks(a) > INT32_MAX) return fail(VVH_ERR_UNSUPPORTED, "problem too large for the decode grid");
-            e = launch_dot(a, outd, dot_early(dot_blocks(a)), stream);
+            e = launch_dot(a, outd, dot_early(dot_blocks(a)), dot_depth(a.K, a.ksplit), stream);
             break;
         }
         case K_SKINNY: {
@@ -502,8 +517,10 @@ int build_dot_plan(Plan& p, int64_t total_tiles)
     size_t lds = 0;
     bool x_in_lds = true;
     for (const LinArgs& a : p.args) x_in_lds = x_in_lds && dot_x_in_lds(a.M, a.K);
+    int depth = 2;
     for (LinArgs& a : p.args) {
         a.ksplit = choose_ksplit(total_tiles, a.K, kDotStep);
+        depth = std::max(depth, dot_depth(a.K, a.ksplit));
         if (blk > INT32_MAX) return fail(VVH_ERR_UNSUPPORTED, "plan too large");
         a.block_begin = (int32_t)blk;
         blk += dot_blocks(a);
@@ -535,6 +552,7 @@ int build_dot_plan(Plan& p, int64_t total_tiles)
     p.dev_table = nullptr;
     p.total_blocks = blk;
     p.max_m = max_m;
+    p.dot_depth = depth;
     p.x_in_lds = x_in_lds;
     p.lds_bytes = lds;
     p.sargs = StreamArgs{};
@@ -1303,7 +1321,8 @@ static int plan_run(vvh_plan plan, int64_t pos, void* stream)
     }
     if (p->dot) {
         const int e = launch_dot_grouped(p->sargs.table, p->dev_block_prob, p->total_blocks, p->max_m, p->x_in_lds,
-                                         p->lds_bytes, p->out, dot_early(p->total_blocks), pos, stream);
+                                         p->lds_bytes, p->out, dot_early(p->total_blocks), p->dot_depth, pos,
+                                         stream);
         return e == 0 ? VVH_OK : fail_hip((hipError_t)e, "grouped dot launch");
     }
     if (p->stream) {
