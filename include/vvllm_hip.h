@@ -327,6 +327,18 @@ VVH_API int vvh_plan_set_input_op(vvh_plan plan, int in_op, const float* in_w, f
  * run: vvh_plan_run_pos (vvh_plan_run runs at position 0). */
 VVH_API int vvh_plan_set_rope(vvh_plan plan, size_t q_index, size_t k_index, size_t v_index, size_t head_dim,
                               float theta, void* k_cache, void* v_cache);
+/* SiLU-gated epilogue (no reference counterpart): problem `index` of the
+ * plan has weights [gate | up] (N = 2 * inter rows, inter % 8 == 0, no
+ * residual) and writes, instead of its N outputs per row, M rows of inter
+ * values silu(gate) * up to its out: bit for bit what a plain run of the plan
+ * followed by vvh_eltwise(VVH_OP_SILU_MUL) leaves there (each linear value
+ * rounded to the output dtype, the product rounded once).  Saves the SiLU-mul
+ * of a decode layer's MLP (transformer.h:180-183) from being repeated in
+ * every block of the down projection's input stage.  The plan must run as one
+ * k_dot_grouped launch (vvh_plan_kernel gives VVH_KERNEL_DOT).  Like
+ * vvh_plan_set_input_op, the plan's device table is rewritten in place after
+ * waiting for the device: set it before capturing graphs that run the plan. */
+VVH_API int vvh_plan_set_glu(vvh_plan plan, size_t index);
 /* vvh_plan_run with the position of activation row 0 for a RoPE epilogue. */
 VVH_API int vvh_plan_run_pos(vvh_plan plan, size_t pos, void* stream);
 /* Kernel family of a single-launch plan (VVH_KERNEL_DOT, VVH_KERNEL_STREAM

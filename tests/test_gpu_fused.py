@@ -159,6 +159,71 @@ def test_plan_input_stage(gpu):
         assert np.array_equal(a, b)
 
 
+@pytest.mark.parametrize("M,inter,K,bias,outd,stage", [(1, 4864, 896, False, F16, True), (1, 136, 256, True, F16, False),
+                                                        (3, 512, 896, True, F32, True), (4, 8, 1536, False, F16, False),
+                                                        (2, 8960, 1536, False, F16, True)])
+def test_plan_glu_epilogue(gpu, M, inter, K, bias, outd, stage):
+    """gate/up as a plan with the SiLU-gated epilogue (and the RMSNorm input
+    stage): bit for bit the plain plan's [gate | up] rows through
+    vvh_eltwise(SILU_MUL)."""
+    print(f"[case] glu epilogue M={M} inter={inter} K={K} bias={bias} outd={outd} stage={stage}", flush=True)
+    rng = np.random.default_rng(M + inter + K)
+    N = 2 * inter
+    x = rng.normal(0, 2, (M, K)).astype(np.float16)
+    w = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    q, s = q8_weight(rng, N, K)
+    b = capi.DevBuf.from_array(rng.normal(0, 0.1, N).astype(np.float32)) if bias else None
+    dx, dw = capi.DevBuf.from_array(x), capi.DevBuf.from_array(w)
+    es = 2 if outd == F16 else 4
+    full, ref, got = capi.DevBuf(M * N * es), capi.DevBuf(M * inter * es), capi.DevBuf(M * inter * es)
+
+    def plan(out, glu):
+        pr = capi.Q8Problem(out=out.ptr, inp=dx.ptr, residual=None, weight=q.ptr, scales=s.ptr,
+                            bias=b.ptr if b else None, M=M, N=N, K=K)
+        h = ctypes.c_uint64()
+        with dot_kernel():  # several rows with many tiles would take k_skinny
+            capi.call("vvh_plan_create", (capi.Q8Problem * 1)(pr), 1, F16, outd, ctypes.byref(h))
+        kern = ctypes.c_int()
+        capi.call("vvh_plan_kernel", h.value, ctypes.byref(kern))
+        assert kern.value == capi.KERNEL_DOT
+        if stage:
+            capi.call("vvh_plan_set_input_op", h.value, capi.IN_RMS_NORM, dw.ptr, 1e-6)
+        if glu:
+            capi.call("vvh_plan_set_glu", h.value, 0)
+        capi.call("vvh_plan_run", h.value, None)
+        capi.call("vvh_plan_destroy", h.value)
+
+    plan(full, False)
+    for m in range(M):  # row m of the plain plan: [gate | up] of inter each
+        capi.call("vvh_eltwise", capi.OP_SILU_MUL, ref.addr(m * inter * es), full.addr(m * N * es),
+                  full.addr((m * N + inter) * es), inter, outd, None)
+    plan(got, True)
+    capi.sync()
+    u = np.uint16 if outd == F16 else np.uint32
+    assert np.array_equal(ref.to_array(u, (M, inter)), got.to_array(u, (M, inter)))
+
+
+def test_plan_glu_limits(gpu):
+    rng = np.random.default_rng(4)
+    K = 256
+    x, y = capi.DevBuf(K * 2), capi.DevBuf(64 * 2)
+    q, s = q8_weight(rng, 40, K)
+
+    def status(N, res=False, rope=False):
+        pr = capi.Q8Problem(out=y.ptr, inp=x.ptr, residual=y.ptr if res else None, weight=q.ptr, scales=s.ptr,
+                            bias=None, M=1, N=N, K=K)
+        h = ctypes.c_uint64()
+        capi.call("vvh_plan_create", (capi.Q8Problem * 1)(pr), 1, F16, F16, ctypes.byref(h))
+        try:
+            return capi.status_of("vvh_plan_set_glu", h.value, 0), capi.status_of("vvh_plan_set_glu", h.value, 5)
+        finally:
+            capi.call("vvh_plan_destroy", h.value)
+
+    assert status(32) == (0, 1)    # index 5 names no problem
+    assert status(40)[0] == 7      # inter % 8 != 0
+    assert status(32, res=True)[0] == 1
+
+
 def _qkv_plan(bufs, src, ws, M, K, outd):
     probs = [capi.Q8Problem(out=b.ptr, inp=src.ptr, residual=None, weight=q.ptr, scales=s.ptr, bias=bb.ptr,
                             M=M, N=N, K=K) for b, (q, s, bb, N) in zip(bufs, ws)]

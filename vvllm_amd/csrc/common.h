@@ -49,6 +49,9 @@ struct LinArgs {
     float rope_theta;
     void* cache;
     int32_t src;  // plans: index of the problem in the caller's list
+    // plans: 1 = SiLU-gated epilogue: the N rows are [gate | up] of N / 2
+    // each and out gets M rows of N / 2 values silu(gate) * up
+    int32_t glu;
     // fp32 activations on the GEMM: inp holds M rows of 2 * bk fp16 values
     // (K = 2 * bk), the high and low fp16 parts of each fp32 activation
     // scaled by a power of two, and xrs[m] = that row's inverse scale; the

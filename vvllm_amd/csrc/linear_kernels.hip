@@ -476,6 +476,34 @@ __device__ __forceinline__ void dot_store_rope(const LinArgs& a, int64_t pos, in
     }
 }
 
+// SiLU-gated epilogue of a plan problem (a.glu): rows A and B of the lane
+// are gate row i and up row N/2 + i; each linear value rounded to OT (what
+// vvh_eltwise would read back), then silu(gate) * up, rounded once, to
+// element i of output row m (rows of N / 2).  Bit-identical to the plan's
+// plain store followed by vvh_eltwise(VVH_OP_SILU_MUL).
+template <typename OT, int MT, bool EARLY>
+__device__ __forceinline__ void dot_store_glu(const LinArgs& a, int64_t rowA, int64_t rowB,
+                                              const float (&accA)[MT], const float (&accB)[MT],
+                                              const float (&e_sc)[2], const float (&e_bi)[2])
+{
+    const int64_t rows[2] = {rowA, rowB};
+    float sc[2], bi[2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        sc[h] = EARLY ? e_sc[h] : *gbl(a.scales + rows[h]);
+        bi[h] = EARLY ? e_bi[h] : (a.bias ? *gbl(a.bias + rows[h]) : 0.0f);
+    }
+    OT* out = static_cast<OT*>(a.out);
+    const int64_t half = a.N / 2;
+#pragma unroll
+    for (int m = 0; m < MT; m++) {
+        if (m >= a.M) continue;
+        const OT g = (OT)dot_epi(accA[m], sc[0], a.bias != nullptr, bi[0], false, 0.0f);
+        const OT u = (OT)dot_epi(accB[m], sc[1], a.bias != nullptr, bi[1], false, 0.0f);
+        *gbl(out + m * half + rowA) = (OT)silu_mul_ref((float)g, (float)u);
+    }
+}
+
 template <typename OT, int MT, bool XLDS, bool EARLY, int DEPTH>
 __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* smem, int64_t pos)
 {
@@ -498,6 +526,10 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
         const int64_t hd = c.tile / tph, sd = c.tile - hd * tph;
         rowA = hd * a.rope_d + 8 * sd + r;
         rowB = rowA + a.rope_d / 2;
+    } else if (a.glu) {
+        // gate row 8 t + r and its up row (N % 16 == 0: every tile is whole)
+        rowA = c.tile * 8 + r;
+        rowB = a.N / 2 + rowA;
     } else {
         rowA = n0 + r < a.N ? n0 + r : a.N - 1;
         rowB = n0 + 8 + r < a.N ? n0 + 8 + r : a.N - 1;
@@ -725,6 +757,10 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
                 }
             }
         }
+    }
+    if (a.glu) {
+        if (c.ks == 0 && ch == 0 && n0 < a.N) dot_store_glu<OT, MT, EARLY>(a, rowA, rowB, accA, accB, e_sc, e_bi);
+        return;
     }
     if (a.rope != 0) {
         if (c.ks == 0 && ch == 0 && n0 < a.N) dot_store_rope<OT, MT, EARLY>(a, pos, rowA, rowB, accA, accB, e_sc, e_bi,

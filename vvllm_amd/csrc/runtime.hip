@@ -1391,6 +1391,8 @@ VVH_API int vvh_plan_set_rope(vvh_plan plan, size_t q_index, size_t k_index, siz
         if ((size_t)a.src == v_index) v = &a;
     }
     if (!q || !k || !v) return fail(VVH_ERR_INVALID_ARG, "q, k or v index names no (non-empty) problem of the plan");
+    if (q->glu || k->glu || v->glu)
+        return fail(VVH_ERR_INVALID_ARG, "a problem with the SiLU-gated epilogue cannot take RoPE");
     if (q->N % (int64_t)head_dim != 0 || k->N % (int64_t)head_dim != 0 || k->N != v->N || k->M != v->M ||
         q->M != k->M)
         return fail(VVH_ERR_INVALID_ARG, "q rows (%lld), k and v rows (%lld, %lld) must be whole heads of %zu, with "
@@ -1405,6 +1407,32 @@ VVH_API int vvh_plan_set_rope(vvh_plan plan, size_t q_index, size_t k_index, siz
     q->cache = nullptr;
     k->cache = k_cache;
     v->cache = v_cache;
+    // the table is read by launches already queued: replace it once they are done
+    (void)hipDeviceSynchronize();
+    const hipError_t e = hipMemcpy(const_cast<LinArgs*>(p.sargs.table), p.args.data(), p.args.size() * sizeof(LinArgs),
+                                   hipMemcpyHostToDevice);
+    return e == hipSuccess ? VVH_OK : fail_hip(e, "plan table upload");
+}
+
+VVH_API int vvh_plan_set_glu(vvh_plan plan, size_t index)
+{
+    REQUIRE_INIT();
+    std::lock_guard<std::mutex> lock(g_pmu);
+    auto it = g_plans.find(plan);
+    if (it == g_plans.end()) return fail(VVH_ERR_UNKNOWN_HANDLE, "unknown plan %llu", (unsigned long long)plan);
+    Plan& p = it->second;
+    if (!p.dot)
+        return fail(VVH_ERR_UNSUPPORTED, "SiLU-gated epilogue needs a plan that runs as one k_dot_grouped launch");
+    LinArgs* g = nullptr;
+    for (LinArgs& a : p.args)
+        if ((size_t)a.src == index) g = &a;
+    if (!g) return fail(VVH_ERR_INVALID_ARG, "index %zu names no (non-empty) problem of the plan", index);
+    if (g->N % 16 != 0)
+        return fail(VVH_ERR_UNSUPPORTED, "SiLU-gated epilogue needs N = 2 * inter with inter %% 8 == 0 (N %lld)",
+                    (long long)g->N);
+    if (g->res) return fail(VVH_ERR_INVALID_ARG, "SiLU-gated epilogue takes no residual");
+    if (g->rope) return fail(VVH_ERR_INVALID_ARG, "a problem with a RoPE epilogue cannot be SiLU-gated");
+    g->glu = 1;
     // the table is read by launches already queued: replace it once they are done
     (void)hipDeviceSynchronize();
     const hipError_t e = hipMemcpy(const_cast<LinArgs*>(p.sargs.table), p.args.data(), p.args.size() * sizeof(LinArgs),

@@ -16,10 +16,10 @@ copy of the table in fp16 mode, like BackendCUDA) or as int8 per-channel
 codes through linear_q8 (the int8 LM head).
 
 fused=True (fp16 only) issues the same arithmetic in fewer launches: the
-RMSNorms before q/k/v and gate_up and the SiLU-mul before down run in the
-input stage of the following linear (vvh_plan_set_input_op,
-vvh_linear_q8_dev_in), RoPE and the K/V cache rows are the epilogue of the
-q/k/v plan (vvh_plan_set_rope, vvh_plan_run_pos), and the embedding row is
+RMSNorms before q/k/v and gate_up run in the input stage of those plans
+(vvh_plan_set_input_op), RoPE and the K/V cache rows are the epilogue of the
+q/k/v plan (vvh_plan_set_rope, vvh_plan_run_pos), the SiLU-mul is the
+epilogue of the gate_up plan (vvh_plan_set_glu), and the embedding row is
 gathered straight to fp16.  Each stage rounds exactly as the standalone
 operator, so the logits equal the unfused step's.  The final norm stays a
 launch of its own: every block of the LM head would repeat it.
@@ -154,6 +154,20 @@ class Model:
                 capi.call("vvh_plan_set_input_op", h.value, capi.IN_RMS_NORM, L["ln1"].ptr, c.eps)
                 # RoPE and the K/V cache rows in the plan's epilogue (problems 0, 1, 2 = q, k, v)
                 capi.call("vvh_plan_set_rope", h.value, 0, 1, 2, c.head_dim, c.theta, L["kc"].ptr, L["vc"].ptr)
+        # fused: gate/up as a one-problem plan that reads the residual stream
+        # through the post-attention RMSNorm and writes silu(gate) * up
+        self.mlp_plans = []
+        if fused:
+            for L in self.layers:
+                g = L["gu"]
+                pr = capi.Q8Problem(out=self.gate.ptr, inp=self.x.ptr, residual=None, weight=g.q.ptr,
+                                    scales=g.s.ptr, bias=None, M=1, N=2 * c.inter, K=c.hidden)
+                arr = (capi.Q8Problem * 1)(pr)
+                h = ctypes.c_uint64()
+                capi.call("vvh_plan_create", arr, 1, act, act, ctypes.byref(h))
+                self.mlp_plans.append(h.value)
+                capi.call("vvh_plan_set_input_op", h.value, capi.IN_RMS_NORM, L["ln2"].ptr, c.eps)
+                capi.call("vvh_plan_set_glu", h.value, 0)
 
     def fill_kv(self, seed: int = 0) -> None:
         """Seeded N(0, 1) rows in every layer's whole KV cache (a stand-in
@@ -173,9 +187,9 @@ class Model:
         return (2 if self.act == F16 else 1) + 11 * c.layers + 1 + head + 1
 
     def close(self):
-        for h in self.plans:
+        for h in self.plans + self.mlp_plans:
             capi.call("vvh_plan_destroy", h)
-        self.plans = []
+        self.plans, self.mlp_plans = [], []
 
     # ---- one decode step -------------------------------------------------
     def step(self, token: int, pos: int, stream=None) -> None:
@@ -233,10 +247,11 @@ class Model:
         call("vvh_argmax", self.logits32.ptr, c.vocab, self.token.ptr, stream)
 
     def _fused_layers(self, pos: int, scale: float, stream) -> None:
-        """The layers of the fused step: 5 launches per layer (6 with the
-        attention merge) instead of 10 and two copies."""
+        """The layers of the fused step: 5 launches per layer (q/k/v with
+        RMSNorm in and RoPE + cache rows out, attention, o, gate/up with
+        RMSNorm in and SiLU-mul out, down) instead of 10 and two copies."""
         c, a, call = self.cfg, self.act, capi.call
-        for L, plan in zip(self.layers, self.plans):
+        for L, plan, mlp in zip(self.layers, self.plans, self.mlp_plans):
             # q/k/v of rms_norm(x, ln1), RoPE'd, k and v rows written to the cache
             call("vvh_plan_run_pos", plan, pos, stream)
             call("vvh_attention", self.attn.ptr, self.q.ptr, L["kc"].ptr, L["vc"].ptr, 1, pos + 1, c.heads,
@@ -244,12 +259,11 @@ class Model:
             o = L["o"]
             call("vvh_linear_q8_dev", self.x.ptr, self.attn.ptr, o.q.ptr, o.s.ptr, None, self.x.ptr, 1, c.hidden,
                  c.hidden, a, a, stream)
-            g = L["gu"]
-            call("vvh_linear_q8_dev_in", self.gu.ptr, self.x.ptr, g.q.ptr, g.s.ptr, None, None, 1, 2 * c.inter,
-                 c.hidden, a, a, capi.IN_RMS_NORM, L["ln2"].ptr, c.eps, stream)
+            # silu(gate) * up of rms_norm(x, ln2) in one launch
+            call("vvh_plan_run", mlp, stream)
             d = L["down"]
-            call("vvh_linear_q8_dev_in", self.x.ptr, self.gu.ptr, d.q.ptr, d.s.ptr, None, self.x.ptr, 1, c.hidden,
-                 c.inter, a, a, capi.IN_SILU_MUL, None, 0.0, stream)
+            call("vvh_linear_q8_dev", self.x.ptr, self.gate.ptr, d.q.ptr, d.s.ptr, None, self.x.ptr, 1, c.hidden,
+                 c.inter, a, a, stream)
 
     def next_token(self) -> int:
         capi.sync()
