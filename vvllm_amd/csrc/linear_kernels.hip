@@ -1361,9 +1361,11 @@ static void dot_launch(const LinArgs& a, int out, dim3 grid, size_t lds, hipStre
 template <int MT, bool XLDS, bool EARLY>
 static void dot_launch_d(const LinArgs& a, int out, int depth, dim3 grid, size_t lds, hipStream_t s)
 {
-    // activations outside LDS (rows too long for it) always take 8
-    if (XLDS && depth <= 2) dot_launch<MT, XLDS, EARLY, XLDS ? 2 : 8>(a, out, grid, lds, s);
-    else if (XLDS && depth <= 4) dot_launch<MT, XLDS, EARLY, XLDS ? 4 : 8>(a, out, grid, lds, s);
+    // late launches with activations outside LDS (rows too long for it)
+    // always take 8
+    constexpr bool any = XLDS || EARLY;
+    if (any && depth <= 2) dot_launch<MT, XLDS, EARLY, any ? 2 : 8>(a, out, grid, lds, s);
+    else if (any && depth <= 4) dot_launch<MT, XLDS, EARLY, any ? 4 : 8>(a, out, grid, lds, s);
     else dot_launch<MT, XLDS, EARLY, 8>(a, out, grid, lds, s);
 }
 
@@ -1377,8 +1379,10 @@ static void dot_launch_e(const LinArgs& a, int out, bool early, int depth, dim3 
 int launch_dot(const LinArgs& a, int out, bool early, int depth, void* stream)
 {
     const dim3 grid((unsigned)dot_blocks(a));
-    const size_t lds = dot_lds_bytes(a.M, a.K);
-    const bool xl = dot_x_in_lds(a.M, a.K);
+    // early launches without an input stage load the activations with the
+    // weights (see dot_early)
+    const bool xl = dot_x_in_lds(a.M, a.K) && (a.xop != 0 || !early);
+    const size_t lds = xl ? dot_lds_bytes(a.M, a.K) : (size_t)kDotRedBytes;
     if (a.M <= 1) {
         if (xl) dot_launch_e<1, true>(a, out, early, depth, grid, lds, S(stream));
         else dot_launch_e<1, false>(a, out, early, depth, grid, lds, S(stream));
@@ -1408,9 +1412,10 @@ template <int MT, bool XLDS, bool EARLY>
 static void dot_grouped_launch_d(const LinArgs* table, const int32_t* block_prob, int64_t pos, int out, int depth,
                                  dim3 grid, size_t lds, hipStream_t s)
 {
-    if (XLDS && depth <= 2) dot_grouped_launch<MT, XLDS, EARLY, XLDS ? 2 : 8>(table, block_prob, pos, out, grid, lds, s);
-    else if (XLDS && depth <= 4)
-        dot_grouped_launch<MT, XLDS, EARLY, XLDS ? 4 : 8>(table, block_prob, pos, out, grid, lds, s);
+    constexpr bool any = XLDS || EARLY;
+    if (any && depth <= 2) dot_grouped_launch<MT, XLDS, EARLY, any ? 2 : 8>(table, block_prob, pos, out, grid, lds, s);
+    else if (any && depth <= 4)
+        dot_grouped_launch<MT, XLDS, EARLY, any ? 4 : 8>(table, block_prob, pos, out, grid, lds, s);
     else dot_grouped_launch<MT, XLDS, EARLY, 8>(table, block_prob, pos, out, grid, lds, s);
 }
 

@@ -296,10 +296,14 @@ int stream_depth(int64_t min_steps)
 bool stream_worth(int64_t tiles) { return tiles >= (int64_t)(g_cu_count > 0 ? g_cu_count : 256) * 4; }
 
 // k_dot launches of at most one block per CU take the variant that requests
-// its weights and epilogue operands before staging the activations: they are
-// bounded by the latency of those loads, not by occupancy.  (Measured per
-// call in a graph, Qwen2.5-0.5B shapes: q 4.30 -> 4.16 us, o 4.76 -> 4.37 us;
-// at 304 blocks, gate 5.36 -> 5.75 us, so larger launches keep the other.)
+// its weights and epilogue operands first: they are bounded by the latency of
+// those loads, not by occupancy.  (Measured per call in a graph, Qwen2.5-0.5B
+// shapes: q 4.30 -> 4.16 us, o 4.76 -> 4.37 us; at 304 blocks, gate 5.36 ->
+// 5.75 us, so larger launches keep the other.)  Without an input stage they
+// also load the activations with the weights instead of staging them in LDS
+// behind a barrier: graph-replayed, k/v 3.46 -> 2.88 us, q 3.76 -> 3.23 us,
+// o 4.04 -> 3.49 us, down 6.04 -> 4.96 us.  Same products in the same order,
+// so the same results.
 constexpr int64_t kDotEarlyBlocksPerCu = 1;
 bool dot_early(int64_t blocks) { return blocks <= (int64_t)(g_cu_count > 0 ? g_cu_count : 256) * kDotEarlyBlocksPerCu; }
 
@@ -1320,8 +1324,13 @@ static int plan_run(vvh_plan plan, int64_t pos, void* stream)
         p = &it->second;
     }
     if (p->dot) {
-        const int e = launch_dot_grouped(p->sargs.table, p->dev_block_prob, p->total_blocks, p->max_m, p->x_in_lds,
-                                         p->lds_bytes, p->out, dot_early(p->total_blocks), p->dot_depth, pos,
+        // early launches load the activations with the weights (no LDS
+        // staging) unless an input stage needs them in LDS
+        const bool early = dot_early(p->total_blocks);
+        const bool in_op = !p->args.empty() && p->args[0].xop != VVH_IN_NONE;
+        const bool xl = p->x_in_lds && (in_op || !early);
+        const int e = launch_dot_grouped(p->sargs.table, p->dev_block_prob, p->total_blocks, p->max_m, xl,
+                                         xl ? p->lds_bytes : (size_t)kDotRedBytes, p->out, early, p->dot_depth, pos,
                                          stream);
         return e == 0 ? VVH_OK : fail_hip((hipError_t)e, "grouped dot launch");
     }
