@@ -295,16 +295,18 @@ int stream_depth(int64_t min_steps)
 
 bool stream_worth(int64_t tiles) { return tiles >= (int64_t)(g_cu_count > 0 ? g_cu_count : 256) * 4; }
 
-// k_dot launches of at most one block per CU take the variant that requests
-// its weights and epilogue operands first: they are bounded by the latency of
-// those loads, not by occupancy.  (Measured per call in a graph, Qwen2.5-0.5B
-// shapes: q 4.30 -> 4.16 us, o 4.76 -> 4.37 us; at 304 blocks, gate 5.36 ->
-// 5.75 us, so larger launches keep the other.)  Without an input stage they
-// also load the activations with the weights instead of staging them in LDS
-// behind a barrier: graph-replayed, k/v 3.46 -> 2.88 us, q 3.76 -> 3.23 us,
-// o 4.04 -> 3.49 us, down 6.04 -> 4.96 us.  Same products in the same order,
-// so the same results.
-constexpr int64_t kDotEarlyBlocksPerCu = 1;
+// k_dot launches of at most four blocks per CU take the variant that
+// requests its weights and epilogue operands first: they are bounded by the
+// latency of those loads, not by occupancy.  Without an input stage they also
+// load the activations with the weights instead of staging them in LDS
+// behind a barrier (same products in the same order, so the same results).
+// Graph-replayed, Qwen2.5-0.5B shapes at M = 1: k/v 3.46 -> 2.88 us, q 3.76
+// -> 3.23 us, o 4.04 -> 3.49 us, down 6.04 -> 4.96 us; gate/up (608 blocks)
+// 5.74 -> 4.58 us, 18992 x 896 (594 blocks) 7.11 -> 6.28 us.  (With the old
+// 8-deep ring, the early variant lost at 304 blocks, 5.36 -> 5.75 us: the ring
+// held 64 VGPRs through the staging; with the ring sized to the k range it
+// holds 16.)  Eight blocks per CU measured the same as four.
+constexpr int64_t kDotEarlyBlocksPerCu = 4;
 bool dot_early(int64_t blocks) { return blocks <= (int64_t)(g_cu_count > 0 ? g_cu_count : 256) * kDotEarlyBlocksPerCu; }
 
 // k_dot weight-ring depth: the smallest of 2, 4 and 8 k steps that holds a
