@@ -157,14 +157,18 @@ def test_dispatch_choice():
         assert ch(512, 4864, 880, capi.F32, capi.F32) == "gemv_f32"   # K % 64 != 0
         assert ch(1, 151936, 896, capi.F16, capi.F32) == "dot"        # config 3 (M = 1)
         assert ch(1, 896, 896, capi.F16, capi.F16) == "dot"           # config 2 (M = 1)
-        assert ch(2, 896, 896, capi.F16, capi.F16) == "dot"           # M = 2, few tiles
-        assert ch(2, 4864, 896, capi.F16, capi.F16) == "skinny"       # M = 2, 304 tiles
-        assert ch(3, 896, 896, capi.F16, capi.F16) == "skinny"        # M = 3..16
-        assert ch(4, 1536, 8960, capi.F16, capi.F16) == "gemm"        # long rows, few tiles: split-K GEMM
-        assert ch(2, 1536, 8960, capi.F16, capi.F16) == "dot"
-        assert ch(5, 151936, 896, capi.F16, capi.F32) == "stream"     # 9496 tiles
-        assert ch(16, 4864, 896, capi.F16, capi.F16) == "skinny"      # 304 tiles: too few to stream
-        assert ch(5, 151936, 448, capi.F16, capi.F16) == "skinny"     # 7 k steps: too short to stream
+        assert ch(2, 896, 896, capi.F16, capi.F16) == "dot"           # M = 2
+        assert ch(2, 151936, 896, capi.F16, capi.F32) == "dot"        # M = 2, 9496 tiles
+        assert ch(4, 896, 896, capi.F16, capi.F16) == "dot"           # M = 3, 4 on few tiles
+        assert ch(4, 1536, 8960, capi.F16, capi.F16) == "dot"
+        assert ch(3, 9728, 896, capi.F16, capi.F16) == "skinny"       # M = 3, 608 tiles
+        assert ch(5, 1536, 8960, capi.F16, capi.F16) == "gemm"        # long rows, few tiles: split-K GEMM
+        assert ch(8, 896, 4864, capi.F16, capi.F16) == "gemm"         # long rows, few tiles: split-K GEMM
+        assert ch(8, 4864, 896, capi.F16, capi.F16) == "skinny"       # M <= 8
+        assert ch(5, 151936, 896, capi.F16, capi.F32) == "skinny"     # streaming only when forced
+        assert ch(16, 4864, 896, capi.F16, capi.F16) == "gemm"        # M > 8 on 304 tiles
+        assert ch(16, 896, 4864, capi.F16, capi.F16) == "gemm"        # M > 8 on long rows
+        assert ch(16, 1536, 1536, capi.F16, capi.F16) == "skinny"     # M > 8, few tiles, short rows
         assert ch(17, 4864, 896, capi.F16, capi.F16) == "gemm"
         assert ch(512, 4864, 896, capi.F16, capi.F16) == "gemm"       # config 4
         assert ch(1, 2, 2, capi.F32, capi.F32) == "generic"           # K % 16 != 0

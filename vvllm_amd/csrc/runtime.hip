@@ -293,8 +293,6 @@ int stream_depth(int64_t min_steps)
     return min_steps >= 12 ? 12 : 8;
 }
 
-bool stream_worth(int64_t tiles) { return tiles >= (int64_t)(g_cu_count > 0 ? g_cu_count : 256) * 4; }
-
 // k_dot launches of at most four blocks per CU take the variant that
 // requests its weights and epilogue operands first: they are bounded by the
 // latency of those loads, not by occupancy.  Without an input stage they also
@@ -329,32 +327,44 @@ int dot_depth(int64_t K, int ksplit)
 constexpr std::size_t kGemmF32MinM = 32;
 
 // Small-M fp16 dispatch, from a sweep of every family forced on each shape
-// (bench.py extras "decode_families"; us per call on the GPU, calls
-// replayed from HIP graphs; Qwen2.5-1.5B and -0.5B shapes, M = 1 / 2 / 4):
-//   q/o 1536 x 1536:    dot 4.5 / 5.2 / 6.2, skinny 5.1 / 5.3 / 6.0
-//   gate_up 8960 x 1536: dot 7.8 / 8.4 / 9.7, skinny 7.6 / 7.9 / 8.6
-//   gate_up 4864 x 896:  dot 5.3 / 5.7 / 6.8, skinny 5.1 / 5.3 / 5.8
-//   down 896 x 4864:     dot 6.1 / 8.0 / 10.5, skinny 8.7 / 9.8 / 10.3
-//   down 1536 x 8960:    dot 8.5 / 11.0 / 15.3, skinny 15.9 / 16.3 / 16.7,
-//                        split-K GEMM 13.3 / 13.3 / 13.4 (13.6 at M = 8)
-// k_dot at M = 1, and at M = 2 unless the problem has many tiles (the MFMA
-// decode kernel is then faster); k_skinny from M = 3 (or k_stream on very
-// many tiles), except rows of at least kLongK codes on few tiles, where the
-// decode kernels have too few waves for the long reduction and the split-K
-// GEMM is faster.
+// (us per call on the GPU, calls replayed from HIP graphs; the bench.py
+// extras "decode_families" repeat part of it):
+//                         M:  1     2     3     4     8     16
+//   q 896 x 896      dot    3.22  3.73  4.59  4.66
+//                    skinny 4.37  4.62  4.95  5.16  5.46
+//                    gemm   8.59  8.57  8.74  8.83  8.91
+//   down 896 x 4864  dot    5.05  6.77  8.25  8.89
+//                    skinny 9.20  9.97 10.19 11.56 10.60 14.29
+//                    gemm  10.36 10.42 10.57 10.84 10.81 10.99
+//   gate_up 9728 x 896     dot 4.56 5.83 7.28 7.42, skinny 6.01 6.16 6.53 6.77 7.34
+//   1.5B q/o 1536 x 1536   dot 3.67 4.41 5.39 5.55, skinny 5.26 5.40 5.99 6.25 5.58 5.56 (gemm 9.9 at 16)
+//   1.5B gate_up 17920 x 1536  dot 9.39 10.86 14.85 15.31, skinny 10.88 11.59 11.93 12.23 15.14 18.33,
+//                          gemm 13.78 14.30 14.20 13.87 14.40 14.43
+//   1.5B down 1536 x 8960  dot 7.48 10.40 12.26 12.41, skinny 16.27 .. 22.82, gemm 12.8 .. 13.2
+//   151936 x 896           dot 28.3 (M = 2) 34.1 (3), skinny 33.2 35.1 38.6 (8) 63.1 (16), gemm 54-56
+// k_dot at M <= 2, and at M <= 4 below 256 tiles; k_skinny otherwise up to
+// M = 8 (and beyond on few tiles with short rows), except rows of at least
+// kLongK codes on few tiles, where the split-K GEMM wins (0.5B down at M = 6:
+// 11.1 against 11.7 us); from M = 9 the GEMM on many tiles or long rows.  k_stream lost to k_skinny by 1.7-3.5x at every
+// M and shape of the sweep (e.g. 151936 x 896: 58-78 us), so it runs only
+// when forced.
 constexpr std::size_t kDotAutoMaxM = 2;
-constexpr int64_t kDotM2MaxTiles = 256;  // M = 2: k_dot below this many 16-row tiles
-constexpr int64_t kLongK = 8192;
+constexpr int64_t kDotFewTiles = 256;    // M = 3, 4: k_dot below this many 16-row tiles
+constexpr int64_t kLongK = 4096;         // M >= 5 (k_dot takes M <= 4 on few tiles)
 constexpr int64_t kLongKMaxTiles = 128;  // 16-row tiles: N <= 2048
+constexpr std::size_t kSkinnyAutoMaxM = 8;
+constexpr int64_t kGemmLongRows = 4096;  // M > 8: the GEMM on rows of this many codes
 
 int natural_kernel(std::size_t M, std::size_t N, std::size_t K, int act)
 {
     if (act == VVH_F32) return (M >= kGemmF32MinM && K % kGemmBK == 0) ? K_GEMM : K_GEMV_F32;
     const int64_t tiles = ((int64_t)N + kDecodeTileN - 1) / kDecodeTileN;
-    if (M == 1 || (M <= kDotAutoMaxM && tiles < kDotM2MaxTiles)) return K_DOT;
+    if (M <= kDotAutoMaxM || (M <= (std::size_t)kDotMaxM && tiles < kDotFewTiles)) return K_DOT;
     if (M > (std::size_t)kSkinnyMaxM) return K_GEMM;
     if ((int64_t)K >= kLongK && K % kGemmBK == 0 && tiles <= kLongKMaxTiles) return K_GEMM;
-    return (stream_depth(((int64_t)K + 63) / 64) > 0 && stream_worth(tiles)) ? K_STREAM : K_SKINNY;
+    if (M > kSkinnyAutoMaxM && K % kGemmBK == 0 && (tiles >= kDotFewTiles || (int64_t)K >= kGemmLongRows))
+        return K_GEMM;
+    return K_SKINNY;
 }
 
 // Kernel family for one call; `aligned` = K % 16 == 0 and 16-byte aligned
@@ -1262,15 +1272,14 @@ VVH_API int vvh_plan_create(const vvh_q8_problem* problems, size_t count, int ac
     REQUIRE_INIT();
     int64_t min_steps = INT64_MAX;
     for (const LinArgs& a : p.args) min_steps = std::min(min_steps, (a.K + 63) / 64);
-    // every problem takes a decode kernel: one streaming launch when the
-    // plan is big enough (or the streaming family is forced), else one
-    // k_skinny_grouped launch (or that family is forced)
+    // every problem takes a decode kernel: one k_skinny_grouped launch, or
+    // one streaming launch when that family is forced
     const int ov = g_override.load();
     const int depth = all_skinny && ov != K_SKINNY ? stream_depth(min_steps) : 0;
     if (all_dot && (ov == K_AUTO || ov == K_DOT)) {
         const int st = build_dot_plan(p, total_tiles);
         if (st != VVH_OK) return st;
-    } else if (depth > 0 && (ov == K_STREAM || stream_worth(total_tiles))) {
+    } else if (depth > 0 && ov == K_STREAM) {
         const int st = build_stream_plan(p, total_tiles, depth);
         if (st != VVH_OK) return st;
     } else if (all_skinny) {
