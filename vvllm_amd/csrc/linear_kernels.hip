@@ -364,9 +364,9 @@ __global__ __launch_bounds__(256) void k_skinny_grouped(const LinArgs* __restric
 // and masked when consumed, so the wait counts of the pipeline are fixed.
 // ---------------------------------------------------------------------------
 // The ring depth DEPTH (k steps of 2 loads each in flight per wave) is a
-// template parameter, 2, 4 or 8, chosen per launch to hold the waves' k
-// ranges (dot_depth on the host): each slot past a wave's range re-reads a
-// step and costs issue time on a short call.
+// template parameter, 2 or 4, chosen per launch (dot_depth on the host): 2
+// when that holds the waves' k ranges, since each slot past a wave's range
+// re-reads a step and costs issue time on a short call.
 
 __device__ __forceinline__ DecodeCoord dot_coord(const LinArgs& a, int64_t block)
 {
@@ -1361,12 +1361,8 @@ static void dot_launch(const LinArgs& a, int out, dim3 grid, size_t lds, hipStre
 template <int MT, bool XLDS, bool EARLY>
 static void dot_launch_d(const LinArgs& a, int out, int depth, dim3 grid, size_t lds, hipStream_t s)
 {
-    // late launches with activations outside LDS (rows too long for it)
-    // always take 8
-    constexpr bool any = XLDS || EARLY;
-    if (any && depth <= 2) dot_launch<MT, XLDS, EARLY, any ? 2 : 8>(a, out, grid, lds, s);
-    else if (any && depth <= 4) dot_launch<MT, XLDS, EARLY, any ? 4 : 8>(a, out, grid, lds, s);
-    else dot_launch<MT, XLDS, EARLY, 8>(a, out, grid, lds, s);
+    if (depth <= 2) dot_launch<MT, XLDS, EARLY, 2>(a, out, grid, lds, s);
+    else dot_launch<MT, XLDS, EARLY, 4>(a, out, grid, lds, s);
 }
 
 template <int MT, bool XLDS>
@@ -1412,11 +1408,8 @@ template <int MT, bool XLDS, bool EARLY>
 static void dot_grouped_launch_d(const LinArgs* table, const int32_t* block_prob, int64_t pos, int out, int depth,
                                  dim3 grid, size_t lds, hipStream_t s)
 {
-    constexpr bool any = XLDS || EARLY;
-    if (any && depth <= 2) dot_grouped_launch<MT, XLDS, EARLY, any ? 2 : 8>(table, block_prob, pos, out, grid, lds, s);
-    else if (any && depth <= 4)
-        dot_grouped_launch<MT, XLDS, EARLY, any ? 4 : 8>(table, block_prob, pos, out, grid, lds, s);
-    else dot_grouped_launch<MT, XLDS, EARLY, 8>(table, block_prob, pos, out, grid, lds, s);
+    if (depth <= 2) dot_grouped_launch<MT, XLDS, EARLY, 2>(table, block_prob, pos, out, grid, lds, s);
+    else dot_grouped_launch<MT, XLDS, EARLY, 4>(table, block_prob, pos, out, grid, lds, s);
 }
 
 template <int MT, bool XLDS>

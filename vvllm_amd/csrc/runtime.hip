@@ -104,7 +104,7 @@ struct Plan {
     size_t lds_bytes = 0;
     StreamArgs sargs{};
     int depth = 0;
-    int dot_depth = 8;           // k_dot_grouped ring depth: the deepest any problem needs
+    int dot_depth = 4;           // k_dot_grouped ring depth: the deepest any problem needs
     int max_m = 0;
     void* dev_stream = nullptr;  // tile_prob, list, list_off
 };
@@ -307,18 +307,21 @@ int stream_depth(int64_t min_steps)
 constexpr int64_t kDotEarlyBlocksPerCu = 4;
 bool dot_early(int64_t blocks) { return blocks <= (int64_t)(g_cu_count > 0 ? g_cu_count : 256) * kDotEarlyBlocksPerCu; }
 
-// k_dot weight-ring depth: the smallest of 2, 4 and 8 k steps that holds a
-// wave's k range; 4 for longer ranges.  Each ring slot past the range
-// re-reads a step (so that every wait in the pipeline has a fixed count),
-// which costs issue time.  Graph-replayed at M = 1: 2 steps per wave (Qwen2.5-
-// 0.5B q/k/v/o/gate/up), depth 8 -> 2: o 4.34 -> 3.93 us, gate/up 7.10 ->
-// 5.70 us; 10 steps per wave (0.5B down), depth 8 -> 4: 6.57 -> 6.08 us,
-// 18 steps (1.5B down) 8.64 -> 8.55 us.
+// k_dot weight-ring depth: 2 k steps when that holds a wave's k range, else
+// 4.  Each ring slot past the range re-reads a step (so that every wait in
+// the pipeline has a fixed count), which costs issue time, and beyond 4
+// slots the deeper ring gained nothing.  Graph-replayed at M = 1: 2 steps
+// per wave (Qwen2.5-0.5B q/k/v/o/gate/up), depth 8 -> 2: o 4.34 -> 3.93 us,
+// gate/up 7.10 -> 5.70 us; 10 steps (0.5B down), 8 -> 4: 6.57 -> 6.08 us;
+// 7 steps (LM head, 151936 x 896), 8 -> 4: 25.5 -> 25.1 us; 12 steps (1.5B
+// gate/up), 9.5 -> 8.6 us; the headline decode set (one grouped launch),
+// 56.2 -> 55.0 us per step over 20 steps (61.8 -> 61.7 over 200).  Depth 2
+// everywhere: 56.5 us and 25.6 us.
 int dot_depth(int64_t K, int ksplit)
 {
     const int64_t steps = (K + kDotStep - 1) / kDotStep;
     const int64_t per_wave = (steps + ksplit - 1) / ksplit;
-    return per_wave <= 2 ? 2 : per_wave <= 4 ? 4 : per_wave <= 8 ? 8 : 4;
+    return per_wave <= 2 ? 2 : 4;
 }
 
 // fp32 activations take the GEMM (on their split fp16 form) from this many
