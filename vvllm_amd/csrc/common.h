@@ -156,7 +156,7 @@ int launch_skinny_grouped(const LinArgs* dev_table, int count, int64_t total_blo
                           void* stream);
 // early: the variant for launches with few blocks, which requests the
 // epilogue operands and the weight ring before staging the activations;
-// depth: k steps in flight per wave (2 or 4)
+// depth: k steps in flight per wave (2, 4 or 7)
 int launch_dot(const LinArgs& a, int out, bool early, int depth, void* stream);
 // dev_block_prob[b] = problem of block b; x_in_lds: dot_x_in_lds holds for
 // every problem; lds_bytes = the largest dot_lds_bytes of the problems

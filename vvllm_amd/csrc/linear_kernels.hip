@@ -364,9 +364,9 @@ __global__ __launch_bounds__(256) void k_skinny_grouped(const LinArgs* __restric
 // and masked when consumed, so the wait counts of the pipeline are fixed.
 // ---------------------------------------------------------------------------
 // The ring depth DEPTH (k steps of 2 loads each in flight per wave) is a
-// template parameter, 2 or 4, chosen per launch (dot_depth on the host): 2
-// when that holds the waves' k ranges, since each slot past a wave's range
-// re-reads a step and costs issue time on a short call.
+// template parameter, 2, 4 or 7, chosen per launch (dot_depth on the host)
+// to hold the waves' k ranges where it can: each slot past a wave's range
+// re-reads a step and costs issue time.
 
 __device__ __forceinline__ DecodeCoord dot_coord(const LinArgs& a, int64_t block)
 {
@@ -1362,7 +1362,8 @@ template <int MT, bool XLDS, bool EARLY>
 static void dot_launch_d(const LinArgs& a, int out, int depth, dim3 grid, size_t lds, hipStream_t s)
 {
     if (depth <= 2) dot_launch<MT, XLDS, EARLY, 2>(a, out, grid, lds, s);
-    else dot_launch<MT, XLDS, EARLY, 4>(a, out, grid, lds, s);
+    else if (depth <= 4) dot_launch<MT, XLDS, EARLY, 4>(a, out, grid, lds, s);
+    else dot_launch<MT, XLDS, EARLY, 7>(a, out, grid, lds, s);
 }
 
 template <int MT, bool XLDS>
@@ -1409,7 +1410,8 @@ static void dot_grouped_launch_d(const LinArgs* table, const int32_t* block_prob
                                  dim3 grid, size_t lds, hipStream_t s)
 {
     if (depth <= 2) dot_grouped_launch<MT, XLDS, EARLY, 2>(table, block_prob, pos, out, grid, lds, s);
-    else dot_grouped_launch<MT, XLDS, EARLY, 4>(table, block_prob, pos, out, grid, lds, s);
+    else if (depth <= 4) dot_grouped_launch<MT, XLDS, EARLY, 4>(table, block_prob, pos, out, grid, lds, s);
+    else dot_grouped_launch<MT, XLDS, EARLY, 7>(table, block_prob, pos, out, grid, lds, s);
 }
 
 template <int MT, bool XLDS>

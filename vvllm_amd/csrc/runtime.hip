@@ -104,7 +104,7 @@ struct Plan {
     size_t lds_bytes = 0;
     StreamArgs sargs{};
     int depth = 0;
-    int dot_depth = 4;           // k_dot_grouped ring depth: the deepest any problem needs
+    int dot_depth = 4;           // k_dot_grouped ring depth: the largest dot_depth of the problems
     int max_m = 0;
     void* dev_stream = nullptr;  // tile_prob, list, list_off
 };
@@ -293,35 +293,38 @@ int stream_depth(int64_t min_steps)
     return min_steps >= 12 ? 12 : 8;
 }
 
-// k_dot launches of at most four blocks per CU take the variant that
+// k_dot launches of at most ten blocks per CU take the variant that
 // requests its weights and epilogue operands first: they are bounded by the
 // latency of those loads, not by occupancy.  Without an input stage they also
 // load the activations with the weights instead of staging them in LDS
 // behind a barrier (same products in the same order, so the same results).
 // Graph-replayed, Qwen2.5-0.5B shapes at M = 1: k/v 3.46 -> 2.88 us, q 3.76
 // -> 3.23 us, o 4.04 -> 3.49 us, down 6.04 -> 4.96 us; gate/up (608 blocks)
-// 5.74 -> 4.58 us, 18992 x 896 (594 blocks) 7.11 -> 6.28 us.  (With the old
-// 8-deep ring, the early variant lost at 304 blocks, 5.36 -> 5.75 us: the ring
-// held 64 VGPRs through the staging; with the ring sized to the k range it
-// holds 16.)  Eight blocks per CU measured the same as four.
-constexpr int64_t kDotEarlyBlocksPerCu = 4;
+// 5.74 -> 4.58 us, 18992 x 896 (594 blocks) 7.11 -> 6.28 us, the LM head
+// (2374 blocks) 25.1 -> 24.7 us.  (With the old 8-deep ring, the early
+// variant lost at 304 blocks, 5.36 -> 5.75 us: the ring held 64 VGPRs through
+// the staging; with the ring sized to the k range it holds 16 or 32.)  At 20
+// blocks per CU, which takes in the headline decode set (4752 blocks), that
+// set measured the same as with staging.
+constexpr int64_t kDotEarlyBlocksPerCu = 10;
 bool dot_early(int64_t blocks) { return blocks <= (int64_t)(g_cu_count > 0 ? g_cu_count : 256) * kDotEarlyBlocksPerCu; }
 
-// k_dot weight-ring depth: 2 k steps when that holds a wave's k range, else
-// 4.  Each ring slot past the range re-reads a step (so that every wait in
-// the pipeline has a fixed count), which costs issue time, and beyond 4
-// slots the deeper ring gained nothing.  Graph-replayed at M = 1: 2 steps
-// per wave (Qwen2.5-0.5B q/k/v/o/gate/up), depth 8 -> 2: o 4.34 -> 3.93 us,
-// gate/up 7.10 -> 5.70 us; 10 steps (0.5B down), 8 -> 4: 6.57 -> 6.08 us;
-// 7 steps (LM head, 151936 x 896), 8 -> 4: 25.5 -> 25.1 us; 12 steps (1.5B
-// gate/up), 9.5 -> 8.6 us; the headline decode set (one grouped launch),
-// 56.2 -> 55.0 us per step over 20 steps (61.8 -> 61.7 over 200).  Depth 2
-// everywhere: 56.5 us and 25.6 us.
+// k_dot weight-ring depth: the wave's whole k range when it has 2 k steps
+// (depth 2) or 5 to 7 (depth 7), else 4.  Each ring slot past the range
+// re-reads a step (so that every wait in the pipeline has a fixed count),
+// which costs issue time, and a ring deeper than the range refills.
+// Graph-replayed at M = 1, against the earlier fixed 8: 2 steps per wave
+// (Qwen2.5-0.5B q/k/v/o/gate/up at ksplit 4), depth 2: o 4.34 -> 3.93 us,
+// gate/up 7.10 -> 5.70 us; 10 steps (0.5B down), depth 4: 6.57 -> 6.08 us;
+// the headline decode set (one grouped launch), 56.2 -> 54.7 us per step over
+// 20 steps.  7 steps (LM head, 151936 x 896): depth 8 25.5 us, 4 24.3 us, 7
+// 23.6 us; depth 7 on longer ranges (down 896 x 4864, 1536 x 8960) lost 10%
+// against 4.
 int dot_depth(int64_t K, int ksplit)
 {
     const int64_t steps = (K + kDotStep - 1) / kDotStep;
     const int64_t per_wave = (steps + ksplit - 1) / ksplit;
-    return per_wave <= 2 ? 2 : 4;
+    return per_wave <= 2 ? 2 : (per_wave >= 5 && per_wave <= 7) ? 7 : 4;
 }
 
 // fp32 activations take the GEMM (on their split fp16 form) from this many
