@@ -508,8 +508,11 @@ template <typename OT, int MT, bool XLDS, bool EARLY, int DEPTH>
 __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* smem, int64_t pos)
 {
     // activations in the ring take 8 VGPRs per row and slot: halve the ring
-    // for several rows so the wave keeps two waves per SIMD's worth of VGPRs
-    constexpr int D = (XLDS || MT == 1 || DEPTH < 4) ? DEPTH : DEPTH / 2;
+    // for several rows so the wave keeps two waves per SIMD's worth of VGPRs,
+    // except in early launches, whose few blocks occupancy does not bound
+    // (graph-replayed, down projections at M = 2: 0.5B 7.35 -> 6.55 us, 1.5B
+    // 10.32 -> 9.06 us with the whole ring)
+    constexpr int D = (XLDS || MT == 1 || DEPTH < 4 || EARLY) ? DEPTH : DEPTH / 2;
     DotRed& red = *reinterpret_cast<DotRed*>(smem);
     f16* xs = reinterpret_cast<f16*>(smem + kDotRedBytes);
     const DecodeCoord c = dot_coord(a, block);
