@@ -613,6 +613,13 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
     // TB/s on the grouped decode set).
     float e_sc[2] = {0.0f, 0.0f}, e_bi[2] = {0.0f, 0.0f};
     OT e_res[MT][2];
+    // RMSNorm stage of an early launch whose rows take one batch of
+    // sum-of-squares loads and one round of chunks per thread: the rows and
+    // norm weights are requested before the weight ring, so the sums, the
+    // block reduction and the normalization run while the weights are in
+    // flight (the in-order wait counter lets a wait for the rows leave the
+    // younger ring loads outstanding)
+    const bool rms_first = EARLY && XLDS && a.xop == 1 && a.K <= 256 * 8 && a.M * a.K / 8 <= 256 * 4;
     if constexpr (EARLY) {
         const float* bp = a.bias ? a.bias : a.scales;  // absent bias / residual: in-bounds reads, unused
         const OT* rp = a.res ? static_cast<const OT*>(a.res) : reinterpret_cast<const OT*>(a.scales);
@@ -624,12 +631,82 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
 #pragma unroll
             for (int m = 0; m < MT; m++) e_res[m][h] = *gbl(rp + (a.res && m < a.M ? m * a.N : 0) + rows[h]);
         }
-        if (active) {
+        if (active && !rms_first) {
 #pragma unroll
             for (int u = 0; u < D; u++) issue(u, (int32_t)c.s0 + u);
         }
     }
-    if (XLDS) {
+    if (XLDS && rms_first) {
+        const int32_t K32 = (int32_t)a.K, xchunks = (int32_t)(a.M * a.K / 8);
+        constexpr int XL = 4;
+        f16 raw[MT][8];
+        h8 xr[XL];
+        f4 w0[XL], w1[XL];
+#pragma unroll
+        for (int m = 0; m < MT; m++) {
+            const f16* xrow = xg + (m < a.M ? m : 0) * a.K;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int32_t i = (int32_t)threadIdx.x + 256 * j;
+                raw[m][j] = *gbl(xrow + (i < K32 ? i : K32 - 1));
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < XL; i++) {
+            int32_t idx = (int32_t)threadIdx.x + 256 * i;
+            idx = idx < xchunks ? idx : xchunks - 1;
+            const int32_t row = idx * 8 / K32, col = idx * 8 - row * K32;
+            xr[i] = *gbl(reinterpret_cast<const h8*>(xg + row * a.K + col));
+            w0[i] = *gbl(reinterpret_cast<const f4*>(a.xw + col));
+            w1[i] = *gbl(reinterpret_cast<const f4*>(a.xw + col + 4));
+        }
+        // keep every row load ahead of the ring in issue order, and issue the
+        // ring in every wave (an inactive wave's slots read clamped, in-bounds
+        // rows and steps, unused): a wait for a row value then always counts
+        // exactly the ring's loads as younger
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < D; u++) issue(u, (int32_t)c.s0 + u);
+        __builtin_amdgcn_sched_barrier(0);
+        // per row as k_rms_norm: thread t sums x[t], x[t + 256], ... in order
+        // (slots past the row add an exact 0), then the same block reduction
+        float* red4 = &red.v[0][0][0];
+        float rinv[MT];
+#pragma unroll
+        for (int m = 0; m < MT; m++) {
+            rinv[m] = 1.0f;
+            if (m < a.M) {
+                float v[8];
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const int32_t i = (int32_t)threadIdx.x + 256 * j;
+                    v[j] = i < K32 ? (float)raw[m][j] : 0.0f;
+                }
+                float ss = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 8; j++) ss += v[j] * v[j];
+                ss = block_sum256(ss, red4);
+                rinv[m] = rms_of(ss, a.K, a.xeps);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < XL; i++) {
+            const int32_t idx = (int32_t)threadIdx.x + 256 * i;
+            if (idx >= xchunks) continue;
+            const int32_t row = idx * 8 / K32, col = idx * 8 - row * K32;
+            float rv = rinv[0];
+#pragma unroll
+            for (int m = 1; m < MT; m++) rv = row == m ? rinv[m] : rv;
+            h8 v;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                v[j] = (f16)rms_apply((float)xr[i][j], rv, w0[i][j]);
+                v[4 + j] = (f16)rms_apply((float)xr[i][4 + j], rv, w1[i][j]);
+            }
+            *reinterpret_cast<h8*>(xs + row * ldx + col) = v;
+        }
+        __syncthreads();
+    } else if (XLDS) {
         // activations to LDS (through the input stage a.xop), 4 chunks of 8
         // values per thread per round; a round's loads are clamped into the
         // input and its stores masked, so all of them are in flight at once
