@@ -413,7 +413,12 @@ VVH_API int vvh_embedding(void* out, const float* dev_table, size_t token_id, si
  * replaces the model's per-query loop (transformer.h:168-173).  head_dim <= 256,
  * len0 + n_q - 1 <= 16000; a single query (n_q = 1, the decode step) with
  * head_dim a multiple of 8 up to 128, num_heads / num_kv_heads <= 16 and k, v
- * 16-byte aligned attends to up to 2^30 positions. */
+ * 16-byte aligned attends to up to 2^30 positions.  A single query over a
+ * span long enough to split across blocks uses the stream's workspace; in
+ * fp16 with head_dim 64 or 128 (and q 16-byte aligned) the blocks are merged
+ * in the same launch through 64 KB of arrival counters per stream, allocated
+ * by the stream's first such call: make that call before capturing graphs
+ * on the stream, as for the workspace (vvh_workspace_release frees both). */
 VVH_API int vvh_attention(void* out, const void* q, const void* k, const void* v, size_t n_q, size_t len0,
                           size_t num_heads, size_t num_kv_heads, size_t head_dim, float scale, int dtype,
                           void* stream);
