@@ -104,6 +104,11 @@ VVH_API int vvh_memcpy_d2d(void* dst, const void* src, size_t bytes);
  * append of a decode step (KVCacheCUDA::append copies synchronously,
  * src/kv_cache/kv_cache_cuda.cc:74-79). */
 VVH_API int vvh_memcpy_d2d_async(void* dst, const void* src, size_t bytes, void* stream);
+/* The KV-cache append's two device-to-device copies (k rows and v rows,
+ * `bytes` each; KVCacheCUDA::append, src/kv_cache/kv_cache_cuda.cc:40-79)
+ * as one kernel queued on `stream`.  Source and destination ranges must not
+ * overlap. */
+VVH_API int vvh_kv_append(void* k_dst, void* v_dst, const void* k_src, const void* v_src, size_t bytes, void* stream);
 
 /* Frees the workspace of `stream` and every buffer it outgrew, after waiting
  * for the device.  Graphs captured on that stream that use the workspace

@@ -161,6 +161,30 @@ def test_attention(gpu, oracle, n_q, len0, H, KVH, D, d):
         assert nerr(got[s], ref) <= TOL[d], f"query {s}"
 
 
+@pytest.mark.parametrize("nbytes,off", [(256, 0), (4096 * 2, 0), (250, 0), (256, 2), (1, 0)])
+def test_kv_append(gpu, nbytes, off):
+    """The KV append's two copies in one launch: 16-byte chunks when every
+    pointer and the size allow it, bytes otherwise; rows around the
+    destination range stay untouched."""
+    rng = np.random.default_rng(nbytes + off)
+    k = rng.integers(0, 256, nbytes + 32, dtype=np.uint8)
+    v = rng.integers(0, 256, nbytes + 32, dtype=np.uint8)
+    dk, dv = capi.DevBuf.from_array(k), capi.DevBuf.from_array(v)
+    kc0 = rng.integers(0, 256, 3 * nbytes + 64, dtype=np.uint8)
+    vc0 = rng.integers(0, 256, 3 * nbytes + 64, dtype=np.uint8)
+    kc, vc = capi.DevBuf.from_array(kc0), capi.DevBuf.from_array(vc0)
+    at = nbytes + 16 + off
+    capi.call("vvh_kv_append", kc.addr(at), vc.addr(at), dk.addr(off), dv.addr(off), nbytes, None)
+    capi.sync()
+    ek, ev = kc0.copy(), vc0.copy()
+    ek[at:at + nbytes] = k[off:off + nbytes]
+    ev[at:at + nbytes] = v[off:off + nbytes]
+    np.testing.assert_array_equal(kc.to_array(np.uint8, ek.shape), ek)
+    np.testing.assert_array_equal(vc.to_array(np.uint8, ev.shape), ev)
+    assert capi.status_of("vvh_kv_append", kc.ptr, None, dk.ptr, dv.ptr, 16, None) == 1  # null pointer
+    capi.call("vvh_kv_append", kc.ptr, vc.ptr, dk.ptr, dv.ptr, 0, None)  # nothing to copy
+
+
 def test_attention_split_calls_in_a_row(gpu, oracle):
     """Split decode calls back to back on one stream, with different block
     counts: each merges its own partials (the per-kv-head arrival counters

@@ -211,6 +211,7 @@ int launch_attention_decode(const AttnDecodePlan& p, void* out, const void* q, c
                             int64_t len, int64_t H, int64_t KVH, int64_t D, float scale, float* ws, unsigned* cnt,
                             int dtype, void* stream);
 int launch_zero_u32(unsigned* p, int64_t n, void* stream);
+int launch_copy2(void* d0, const void* s0, void* d1, const void* s1, int64_t bytes, void* stream);
 int launch_dense(void* out, const void* x, const void* w, int wdtype, const float* bias, const void* res, int64_t M,
                  int64_t N, int64_t K, int dtype, void* stream);
 int launch_matmul(void* out, const void* A, const float* B, int64_t M, int64_t N, int64_t K, int dtype, void* stream);

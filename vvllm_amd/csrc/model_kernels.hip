@@ -773,6 +773,35 @@ __global__ void k_zero_u32(unsigned* __restrict__ p, int64_t n)
     if (i < n) p[i] = 0u;
 }
 
+// Two copies of n bytes in one launch (the K and V rows of a cache append):
+// 16-byte chunks when every pointer and n allow it, else bytes.
+template <typename U>
+__global__ __launch_bounds__(256) void k_copy2(U* __restrict__ d0, const U* __restrict__ s0, U* __restrict__ d1,
+                                              const U* __restrict__ s1, int64_t n)
+{
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < 2 * n; i += (int64_t)gridDim.x * 256) {
+        if (i < n) d0[i] = s0[i];
+        else d1[i - n] = s1[i - n];
+    }
+}
+
+int launch_copy2(void* d0, const void* s0, void* d1, const void* s1, int64_t bytes, void* stream)
+{
+    if (bytes <= 0) return 0;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const bool v16 = bytes % 16 == 0 && ((reinterpret_cast<uintptr_t>(d0) | reinterpret_cast<uintptr_t>(s0) |
+                                          reinterpret_cast<uintptr_t>(d1) | reinterpret_cast<uintptr_t>(s1)) & 15) == 0;
+    const int64_t n = v16 ? bytes / 16 : bytes;
+    const unsigned blocks = (unsigned)std::min<int64_t>((2 * n + 255) / 256, 1024);
+    if (v16)
+        hipLaunchKernelGGL(k_copy2<u4>, dim3(blocks), dim3(256), 0, s, (u4*)d0, (const u4*)s0, (u4*)d1, (const u4*)s1,
+                           n);
+    else
+        hipLaunchKernelGGL(k_copy2<uint8_t>, dim3(blocks), dim3(256), 0, s, (uint8_t*)d0, (const uint8_t*)s0,
+                           (uint8_t*)d1, (const uint8_t*)s1, n);
+    return (int)hipGetLastError();
+}
+
 int launch_zero_u32(unsigned* p, int64_t n, void* stream)
 {
     if (n <= 0) return 0;

@@ -1579,6 +1579,15 @@ std::unordered_map<const float*, ArrayMirror> g_arr[2];  // [0]: fp32 copies, [1
 
 inline int act_ok(int dtype) { return dtype == VVH_F32 || dtype == VVH_F16; }
 inline int ret_launch(int e, const char* what) { return e == 0 ? VVH_OK : fail_hip((hipError_t)e, what); }
+
+VVH_API int vvh_kv_append(void* k_dst, void* v_dst, const void* k_src, const void* v_src, size_t bytes, void* stream)
+{
+    if (bytes == 0) return VVH_OK;
+    if (!k_dst || !v_dst || !k_src || !v_src) return fail(VVH_ERR_INVALID_ARG, "null pointer");
+    if (bytes > (size_t)INT64_MAX / 2) return fail(VVH_ERR_INVALID_ARG, "size overflow");
+    REQUIRE_INIT();
+    return ret_launch(launch_copy2(k_dst, k_src, v_dst, v_src, (int64_t)bytes, stream), "kv append launch");
+}
 }  // namespace
 
 VVH_API int vvh_eltwise(int op, void* out, const void* x, const void* y, size_t n, int dtype, void* stream)

@@ -255,8 +255,7 @@ void KVCacheHIP::append(std::size_t layer, const float* k, const float* v, std::
     Layer& l = layers_.at(layer);
     if (seq_len_ + num_tokens > l.cap) grow(l, std::max(seq_len_ + num_tokens, 2 * l.cap));
     const std::size_t off = seq_len_ * kv_dim_ * elem(), n = num_tokens * kv_dim_ * elem();
-    check(vvh_memcpy_d2d_async(static_cast<char*>(l.k) + off, k, n, nullptr), "kv append");
-    check(vvh_memcpy_d2d_async(static_cast<char*>(l.v) + off, v, n, nullptr), "kv append");
+    check(vvh_kv_append(static_cast<char*>(l.k) + off, static_cast<char*>(l.v) + off, k, v, n, nullptr), "kv append");
 }
 
 const float* KVCacheHIP::k(std::size_t layer) const

@@ -105,8 +105,8 @@ private:
 
 // Key/value cache in HBM (KVCacheCUDA, src/kv_cache/kv_cache_cuda.cc:22-95):
 // per layer, rows of kv_dim values in the backend's activation dtype.
-// append() queues device-to-device copies on the null stream (the rows come
-// from device tensors).  reserve() sizes every layer for a whole context up
+// append() queues one kernel on the null stream that copies the k and v
+// rows (they come from device tensors).  reserve() sizes every layer for a whole context up
 // front (one allocation per layer; 288 GB of HBM holds long contexts), so
 // appends never reallocate.
 class KVCacheHIP : public KVCache

@@ -178,13 +178,13 @@ class Model:
             capi.call("vvh_fill_normal", L["vc"].ptr, self.act, n, seed + 2 * l + 1, 0.0, 1.0, None)
 
     def calls_per_step(self) -> int:
-        """C-ABI calls per step (attention over more than one block and the
-        argmax over the vocabulary launch two kernels each)."""
+        """C-ABI calls per step (fp32 attention over more than one block and
+        the argmax over the vocabulary launch two kernels each)."""
         c = self.cfg
         head = 1 if self.lm_head == "int8" or self.act == F32 else 2
         if self.fused:
             return 1 + 5 * c.layers + 1 + head + 1
-        return (2 if self.act == F16 else 1) + 11 * c.layers + 1 + head + 1
+        return (2 if self.act == F16 else 1) + 10 * c.layers + 1 + head + 1
 
     def close(self):
         for h in self.plans + self.mlp_plans:
@@ -216,8 +216,8 @@ class Model:
                 call("vvh_plan_run", plan, stream)
                 call("vvh_rope", self.q.ptr, self.k_new.ptr, 1, c.heads, c.kv_heads, c.head_dim, pos, c.theta, a,
                      stream)
-                call("vvh_memcpy_d2d_async", L["kc"].ptr + pos * kvb, self.k_new.ptr, kvb, stream)
-                call("vvh_memcpy_d2d_async", L["vc"].ptr + pos * kvb, self.v_new.ptr, kvb, stream)
+                call("vvh_kv_append", L["kc"].ptr + pos * kvb, L["vc"].ptr + pos * kvb, self.k_new.ptr,
+                     self.v_new.ptr, kvb, stream)
                 call("vvh_attention", self.attn.ptr, self.q.ptr, L["kc"].ptr, L["vc"].ptr, 1, pos + 1, c.heads,
                      c.kv_heads, c.head_dim, scale, a, stream)
                 o = L["o"]
@@ -249,7 +249,7 @@ class Model:
     def _fused_layers(self, pos: int, scale: float, stream) -> None:
         """The layers of the fused step: 5 launches per layer (q/k/v with
         RMSNorm in and RoPE + cache rows out, attention, o, gate/up with
-        RMSNorm in and SiLU-mul out, down) instead of 10 and two copies."""
+        RMSNorm in and SiLU-mul out, down) instead of 10."""
         c, a, call = self.cfg, self.act, capi.call
         for L, plan, mlp in zip(self.layers, self.plans, self.mlp_plans):
             # q/k/v of rms_norm(x, ln1), RoPE'd, k and v rows written to the cache
