@@ -93,6 +93,35 @@ __global__ __launch_bounds__(256) void k_rms_norm(T* __restrict__ out, const T* 
     __shared__ float red[4];
     const T* xr = x + (int64_t)blockIdx.x * n;
     T* orow = out + (int64_t)blockIdx.x * n;
+    // thread t sums x[t]^2, x[t + 256]^2, ... in order, then the block sum:
+    // the order k_dot's RMSNorm input stage reproduces
+    constexpr int RC = 8;
+    if (n <= 256 * RC) {
+        // rows of up to 2048: the thread's elements and weights requested at
+        // once and kept for the output (one round trip instead of two);
+        // slots past the row add an exact 0
+        float v[RC], wv[RC];
+#pragma unroll
+        for (int j = 0; j < RC; j++) {
+            const int64_t i = threadIdx.x + 256 * j, ic = i < n ? i : n - 1;
+            v[j] = ldf(xr, ic);
+            wv[j] = w[ic];
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < RC; j++) {
+            const float e = threadIdx.x + 256 * j < n ? v[j] : 0.0f;
+            ss += e * e;
+        }
+        ss = block_sum(ss, red);
+        const float rms = rms_of(ss, n, eps);
+#pragma unroll
+        for (int j = 0; j < RC; j++) {
+            const int64_t i = threadIdx.x + 256 * j;
+            if (i < n) stf(orow, i, rms_apply(v[j], rms, wv[j]));
+        }
+        return;
+    }
     float ss = 0.0f;
     for (int64_t i = threadIdx.x; i < n; i += 256) {
         const float v = ldf(xr, i);
