@@ -40,6 +40,9 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     # IEEE fp32 division for the quantizer's scale and reciprocal
     "-fhip-fp32-correctly-rounded-divide-sqrt",
+    # the leading scalar kernel arguments (up to 16 dwords) arrive in SGPRs at
+    # dispatch instead of through a load from the kernel-argument segment
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-I" + INCLUDE,
 ]
 

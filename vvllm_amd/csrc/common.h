@@ -60,6 +60,13 @@ struct LinArgs {
     const float* xrs;
 };
 
+// k_dot_grouped: a plan of at most kDotInline problems passes its table in
+// the kernel arguments, so a block finds its problem without a memory load.
+constexpr int kDotInline = 4;
+struct DotGroup {
+    LinArgs p[kDotInline];
+};
+
 // Persistent streaming decode launch (k_stream).  Work is a sequence of
 // 16-row tiles (one tile = 16 output channels x the full K).  Every wave
 // walks its own tiles, keeping a fixed number of weight loads in flight
@@ -113,6 +120,11 @@ constexpr int64_t kDotMaxM = 4;
 constexpr int kDotStep = 128;               // k codes per row per step
 constexpr int64_t kDotLdsMax = 80 * 1024;   // dynamic LDS of one block at most
 constexpr int64_t kDotRedBytes = 4 * 4 * 16 * 4;
+// k_dot takes N, M and K as 32-bit kernel arguments and 32-bit k offsets
+inline bool dot_fits(int64_t N, int64_t K)
+{
+    return N <= INT32_MAX && K <= INT32_MAX - kDotStep;
+}
 inline int64_t dot_blocks(const LinArgs& a)
 {
     const int64_t tiles = (a.N + kDecodeTileN - 1) / kDecodeTileN;
@@ -158,12 +170,14 @@ int launch_skinny_grouped(const LinArgs* dev_table, int count, int64_t total_blo
 // epilogue operands and the weight ring before staging the activations;
 // depth: k steps in flight per wave (2, 4 or 7)
 int launch_dot(const LinArgs& a, int out, bool early, int depth, void* stream);
-// dev_block_prob[b] = problem of block b; x_in_lds: dot_x_in_lds holds for
-// every problem; lds_bytes = the largest dot_lds_bytes of the problems
-// pos: position of activation row 0 for problems with a RoPE epilogue
-int launch_dot_grouped(const LinArgs* dev_table, const int32_t* dev_block_prob, int64_t total_blocks, int max_m,
-                       bool x_in_lds, size_t lds_bytes, int out, bool early, int depth, int64_t pos,
-                       void* stream);
+// dev_block_prob[b] = problem of block b; args: the host copy of the
+// count problems of dev_table (passed in the kernel arguments when count <=
+// kDotInline); x_in_lds: dot_x_in_lds holds for every problem; lds_bytes =
+// the largest dot_lds_bytes of the problems; pos: position of activation
+// row 0 for problems with a RoPE epilogue
+int launch_dot_grouped(const LinArgs* dev_table, const int32_t* dev_block_prob, const LinArgs* args, int count,
+                       int64_t total_blocks, int max_m, bool x_in_lds, size_t lds_bytes, int out, bool early,
+                       int depth, int64_t pos, void* stream);
 int launch_gemm(const LinArgs& a, int out, void* stream);
 // k_gemm3 (gemm_kernels.hip): one 128 x BN tile (or one k split of it) per
 // block, K % 64 == 0; layout 1 = 128 x 192, 3 = 128 x 128

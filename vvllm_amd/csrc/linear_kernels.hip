@@ -373,11 +373,12 @@ __device__ __forceinline__ DecodeCoord dot_coord(const LinArgs& a, int64_t block
     DecodeCoord c;
     c.lane = threadIdx.x & 63;
     c.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: keeps the loops scalar
-    c.ksplit = a.ksplit;
-    c.ks = c.wave % c.ksplit;
-    c.tile = block * (4 / c.ksplit) + c.wave / c.ksplit;
-    const int64_t steps = (a.K + kDotStep - 1) / kDotStep;
-    const int64_t per = (steps + c.ksplit - 1) / c.ksplit;
+    c.ksplit = a.ksplit;  // 1, 2 or 4: shifts, not divisions
+    const int lg = __builtin_ctz(c.ksplit);
+    c.ks = c.wave & (c.ksplit - 1);
+    c.tile = block * (4 >> lg) + (c.wave >> lg);
+    const int32_t steps = ((int32_t)a.K + kDotStep - 1) / kDotStep;  // K <= INT32_MAX - kDotStep
+    const int32_t per = (steps + c.ksplit - 1) >> lg;
     c.s0 = c.ks * per < steps ? c.ks * per : steps;
     c.s1 = c.s0 + per < steps ? c.s0 + per : steps;
     return c;
@@ -871,23 +872,48 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
 
 // XLDS = the activations are staged in LDS (dot_x_in_lds, decided on the
 // host for the launch: for a grouped launch it must hold for every problem).
+// The fields that the first loads of a block depend on come first, as scalar
+// arguments, which arrive preloaded into registers at dispatch (up to 16
+// dwords; the struct is read from the kernel-argument segment when used).
+// A plain call has no RoPE or SiLU-gated epilogue.
 template <typename OT, int MT, bool XLDS, bool EARLY, int DEPTH>
-__global__ __launch_bounds__(256) void k_dot(LinArgs a)
+__global__ __launch_bounds__(256) void k_dot(const int8_t* w, const void* inp, const float* scales,
+                                             const float* bias, const void* res, int32_t N, int32_t M, int32_t K,
+                                             int32_t ksplit, const LinArgs a)
 {
     extern __shared__ __attribute__((aligned(16))) char dot_smem[];
-    dot_body<OT, MT, XLDS, EARLY, DEPTH>(a, blockIdx.x, dot_smem, 0);
+    LinArgs b = a;
+    b.w = w;
+    b.inp = inp;
+    b.scales = scales;
+    b.bias = bias;
+    b.res = res;
+    b.N = N;
+    b.M = M;
+    b.K = K;
+    b.ksplit = ksplit;
+    b.rope = 0;
+    b.glu = 0;
+    dot_body<OT, MT, XLDS, EARLY, DEPTH>(b, blockIdx.x, dot_smem, 0);
 }
 
-// Grouped launch: block b serves problem block_prob[b].
-// `pos`: the position of activation row 0 for problems with a RoPE epilogue.
+// Grouped launch.  count <= kDotInline: the problems are g.p[0, count) and
+// b1, b2, b3 are the first blocks of problems 1, 2, 3 (INT32_MAX where there
+// is none), all in the kernel arguments, so the block's problem is found
+// without a memory load (the leading scalar arguments are preloaded into
+// registers at dispatch); larger plans: block b serves problem
+// table[block_prob[b]].  `pos`: the position of activation row 0 for
+// problems with a RoPE epilogue.
 template <typename OT, int MT, bool XLDS, bool EARLY, int DEPTH>
-__global__ __launch_bounds__(256) void k_dot_grouped(const LinArgs* __restrict__ table,
-                                                     const int32_t* __restrict__ block_prob, int64_t pos)
+__global__ __launch_bounds__(256) void k_dot_grouped(int32_t b1, int32_t b2, int32_t b3, int32_t count, int64_t pos,
+                                                     const LinArgs* __restrict__ table,
+                                                     const int32_t* __restrict__ block_prob, const DotGroup g)
 {
     extern __shared__ __attribute__((aligned(16))) char dot_smem[];
     const int b = blockIdx.x;
-    const int p = *cst(block_prob + b);
-    const LinArgs a = table[p];
+    LinArgs a;
+    if (count <= kDotInline) a = g.p[(b >= b1) + (b >= b2) + (b >= b3)];
+    else a = table[*cst(block_prob + b)];
     dot_body<OT, MT, XLDS, EARLY, DEPTH>(a, b - a.block_begin, dot_smem, pos);
 }
 
@@ -1434,8 +1460,14 @@ int launch_skinny_grouped(const LinArgs* dev_table, int count, int64_t total_blo
 template <int MT, bool XLDS, bool EARLY, int DEPTH>
 static void dot_launch(const LinArgs& a, int out, dim3 grid, size_t lds, hipStream_t s)
 {
-    if (out == VVH_F32) hipLaunchKernelGGL((k_dot<float, MT, XLDS, EARLY, DEPTH>), grid, dim3(256), lds, s, a);
-    else hipLaunchKernelGGL((k_dot<f16, MT, XLDS, EARLY, DEPTH>), grid, dim3(256), lds, s, a);
+    // dot_fits(N, K) holds (checked by the runtime)
+    const int32_t N = (int32_t)a.N, M = (int32_t)a.M, K = (int32_t)a.K;
+    if (out == VVH_F32)
+        hipLaunchKernelGGL((k_dot<float, MT, XLDS, EARLY, DEPTH>), grid, dim3(256), lds, s, a.w, a.inp, a.scales,
+                           a.bias, a.res, N, M, K, a.ksplit, a);
+    else
+        hipLaunchKernelGGL((k_dot<f16, MT, XLDS, EARLY, DEPTH>), grid, dim3(256), lds, s, a.w, a.inp, a.scales,
+                           a.bias, a.res, N, M, K, a.ksplit, a);
 }
 
 template <int MT, bool XLDS, bool EARLY>
@@ -1473,51 +1505,69 @@ int launch_dot(const LinArgs& a, int out, bool early, int depth, void* stream)
     return (int)hipGetLastError();
 }
 
+// The kernel arguments of a grouped launch besides the launch shape.
+struct DotGroupArgs {
+    int32_t b[3];
+    int32_t count;
+    int64_t pos;
+    const LinArgs* table;
+    const int32_t* block_prob;
+    DotGroup g;
+};
+
 template <int MT, bool XLDS, bool EARLY, int DEPTH>
-static void dot_grouped_launch(const LinArgs* table, const int32_t* block_prob, int64_t pos, int out, dim3 grid,
-                               size_t lds, hipStream_t s)
+static void dot_grouped_launch(const DotGroupArgs& k, int out, dim3 grid, size_t lds, hipStream_t s)
 {
     if (out == VVH_F32)
-        hipLaunchKernelGGL((k_dot_grouped<float, MT, XLDS, EARLY, DEPTH>), grid, dim3(256), lds, s, table, block_prob,
-                           pos);
+        hipLaunchKernelGGL((k_dot_grouped<float, MT, XLDS, EARLY, DEPTH>), grid, dim3(256), lds, s, k.b[0], k.b[1],
+                           k.b[2], k.count, k.pos, k.table, k.block_prob, k.g);
     else
-        hipLaunchKernelGGL((k_dot_grouped<f16, MT, XLDS, EARLY, DEPTH>), grid, dim3(256), lds, s, table, block_prob,
-                           pos);
+        hipLaunchKernelGGL((k_dot_grouped<f16, MT, XLDS, EARLY, DEPTH>), grid, dim3(256), lds, s, k.b[0], k.b[1],
+                           k.b[2], k.count, k.pos, k.table, k.block_prob, k.g);
 }
 
 template <int MT, bool XLDS, bool EARLY>
-static void dot_grouped_launch_d(const LinArgs* table, const int32_t* block_prob, int64_t pos, int out, int depth,
-                                 dim3 grid, size_t lds, hipStream_t s)
+static void dot_grouped_launch_d(const DotGroupArgs& k, int out, int depth, dim3 grid, size_t lds, hipStream_t s)
 {
-    if (depth <= 2) dot_grouped_launch<MT, XLDS, EARLY, 2>(table, block_prob, pos, out, grid, lds, s);
-    else if (depth <= 4) dot_grouped_launch<MT, XLDS, EARLY, 4>(table, block_prob, pos, out, grid, lds, s);
-    else dot_grouped_launch<MT, XLDS, EARLY, 7>(table, block_prob, pos, out, grid, lds, s);
+    if (depth <= 2) dot_grouped_launch<MT, XLDS, EARLY, 2>(k, out, grid, lds, s);
+    else if (depth <= 4) dot_grouped_launch<MT, XLDS, EARLY, 4>(k, out, grid, lds, s);
+    else dot_grouped_launch<MT, XLDS, EARLY, 7>(k, out, grid, lds, s);
 }
 
 template <int MT, bool XLDS>
-static void dot_grouped_launch_e(const LinArgs* table, const int32_t* block_prob, int64_t pos, int out, bool early,
-                                 int depth, dim3 grid, size_t lds, hipStream_t s)
+static void dot_grouped_launch_e(const DotGroupArgs& k, int out, bool early, int depth, dim3 grid, size_t lds,
+                                 hipStream_t s)
 {
-    if (early) dot_grouped_launch_d<MT, XLDS, true>(table, block_prob, pos, out, depth, grid, lds, s);
-    else dot_grouped_launch_d<MT, XLDS, false>(table, block_prob, pos, out, depth, grid, lds, s);
+    if (early) dot_grouped_launch_d<MT, XLDS, true>(k, out, depth, grid, lds, s);
+    else dot_grouped_launch_d<MT, XLDS, false>(k, out, depth, grid, lds, s);
 }
 
-int launch_dot_grouped(const LinArgs* dev_table, const int32_t* dev_block_prob, int64_t total_blocks, int max_m,
-                       bool x_in_lds, size_t lds_bytes, int out, bool early, int depth, int64_t pos, void* stream)
+int launch_dot_grouped(const LinArgs* dev_table, const int32_t* dev_block_prob, const LinArgs* args, int count,
+                       int64_t total_blocks, int max_m, bool x_in_lds, size_t lds_bytes, int out, bool early,
+                       int depth, int64_t pos, void* stream)
 {
     const dim3 grid((unsigned)total_blocks);
     hipStream_t s = S(stream);
-    const LinArgs* t = dev_table;
-    const int32_t* bp = dev_block_prob;
+    DotGroupArgs k{};
+    k.count = count;
+    k.pos = pos;
+    k.table = dev_table;
+    k.block_prob = dev_block_prob;
+    for (int i = 0; i < 3; ++i) k.b[i] = INT32_MAX;
+    if (count <= kDotInline)
+        for (int i = 0; i < count; ++i) {
+            k.g.p[i] = args[i];
+            if (i > 0) k.b[i - 1] = args[i].block_begin;
+        }
     if (max_m <= 1) {
-        if (x_in_lds) dot_grouped_launch_e<1, true>(t, bp, pos, out, early, depth, grid, lds_bytes, s);
-        else dot_grouped_launch_e<1, false>(t, bp, pos, out, early, depth, grid, lds_bytes, s);
+        if (x_in_lds) dot_grouped_launch_e<1, true>(k, out, early, depth, grid, lds_bytes, s);
+        else dot_grouped_launch_e<1, false>(k, out, early, depth, grid, lds_bytes, s);
     } else if (max_m <= 2) {
-        if (x_in_lds) dot_grouped_launch_e<2, true>(t, bp, pos, out, early, depth, grid, lds_bytes, s);
-        else dot_grouped_launch_e<2, false>(t, bp, pos, out, early, depth, grid, lds_bytes, s);
+        if (x_in_lds) dot_grouped_launch_e<2, true>(k, out, early, depth, grid, lds_bytes, s);
+        else dot_grouped_launch_e<2, false>(k, out, early, depth, grid, lds_bytes, s);
     } else {
-        if (x_in_lds) dot_grouped_launch_e<4, true>(t, bp, pos, out, early, depth, grid, lds_bytes, s);
-        else dot_grouped_launch_e<4, false>(t, bp, pos, out, early, depth, grid, lds_bytes, s);
+        if (x_in_lds) dot_grouped_launch_e<4, true>(k, out, early, depth, grid, lds_bytes, s);
+        else dot_grouped_launch_e<4, false>(k, out, early, depth, grid, lds_bytes, s);
     }
     return (int)hipGetLastError();
 }

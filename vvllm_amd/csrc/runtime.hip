@@ -365,7 +365,9 @@ int natural_kernel(std::size_t M, std::size_t N, std::size_t K, int act)
 {
     if (act == VVH_F32) return (M >= kGemmF32MinM && K % kGemmBK == 0) ? K_GEMM : K_GEMV_F32;
     const int64_t tiles = ((int64_t)N + kDecodeTileN - 1) / kDecodeTileN;
-    if (M <= kDotAutoMaxM || (M <= (std::size_t)kDotMaxM && tiles < kDotFewTiles)) return K_DOT;
+    if ((M <= kDotAutoMaxM || (M <= (std::size_t)kDotMaxM && tiles < kDotFewTiles)) &&
+        dot_fits((int64_t)N, (int64_t)K))
+        return K_DOT;
     if (M > (std::size_t)kSkinnyMaxM) return K_GEMM;
     if ((int64_t)K >= kLongK && K % kGemmBK == 0 && tiles <= kLongKMaxTiles) return K_GEMM;
     if (M > kSkinnyAutoMaxM && K % kGemmBK == 0 && (tiles >= kDotFewTiles || (int64_t)K >= kGemmLongRows))
@@ -386,7 +388,9 @@ int choose_kernel(std::size_t M, std::size_t N, std::size_t K, int act, bool ali
         case K_GEMV_F32: return act == VVH_F32 ? K_GEMV_F32 : K_GENERIC;
         case K_SKINNY: return decode ? K_SKINNY : K_GENERIC;
         case K_STREAM: return (decode && stream_depth(((int64_t)K + 63) / 64) > 0) ? K_STREAM : K_GENERIC;
-        case K_DOT: return (act == VVH_F16 && M <= (std::size_t)kDotMaxM) ? K_DOT : K_GENERIC;
+        case K_DOT:
+            return (act == VVH_F16 && M <= (std::size_t)kDotMaxM && dot_fits((int64_t)N, (int64_t)K)) ? K_DOT
+                                                                                                        : K_GENERIC;
         case K_GEMM: return (act == VVH_F16 || K % kGemmBK == 0) ? K_GEMM : K_GENERIC;
         default: return K_GENERIC;
     }
@@ -451,6 +455,9 @@ int run_call(const LinArgs& base, int kernel, int act, int outd, void* stream, c
             const int64_t tiles = (a.N + kDecodeTileN - 1) / kDecodeTileN;
             a.ksplit = choose_ksplit(tiles, a.K, kDotStep);
             if (dot_blocks(a) > INT32_MAX) return fail(VVH_ERR_UNSUPPORTED, "problem too large for the decode grid");
+            if (!dot_fits(a.N, a.K))
+                return fail(VVH_ERR_UNSUPPORTED, "N (%lld) or K (%lld) too large for the decode kernel",
+                            (long long)a.N, (long long)a.K);
             e = launch_dot(a, outd, dot_early(dot_blocks(a)), dot_depth(a.K, a.ksplit), stream);
             break;
         }
@@ -1346,9 +1353,9 @@ static int plan_run(vvh_plan plan, int64_t pos, void* stream)
         const bool early = dot_early(p->total_blocks);
         const bool in_op = !p->args.empty() && p->args[0].xop != VVH_IN_NONE;
         const bool xl = p->x_in_lds && (in_op || !early);
-        const int e = launch_dot_grouped(p->sargs.table, p->dev_block_prob, p->total_blocks, p->max_m, xl,
-                                         xl ? p->lds_bytes : (size_t)kDotRedBytes, p->out, early, p->dot_depth, pos,
-                                         stream);
+        const int e = launch_dot_grouped(p->sargs.table, p->dev_block_prob, p->args.data(), (int)p->args.size(),
+                                         p->total_blocks, p->max_m, xl, xl ? p->lds_bytes : (size_t)kDotRedBytes,
+                                         p->out, early, p->dot_depth, pos, stream);
         return e == 0 ? VVH_OK : fail_hip((hipError_t)e, "grouped dot launch");
     }
     if (p->stream) {
