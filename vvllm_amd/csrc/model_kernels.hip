@@ -618,11 +618,13 @@ constexpr int kDecChunk = 64;  // keys per wave and chunk
 typedef _Float16 h4v __attribute__((ext_vector_type(4)));
 
 template <int D, int kDecWaves>
-__global__ __launch_bounds__(64 * kDecWaves) void k_attention_decode_mfma(f16* __restrict__ out, const f16* __restrict__ q,
+// What the first loads depend on comes first (q, k, v, the key range, the
+// head layout: 14 dwords, preloaded into registers at dispatch); G = H / KVH.
+__global__ __launch_bounds__(64 * kDecWaves) void k_attention_decode_mfma(const f16* __restrict__ q,
                                                                const f16* __restrict__ k, const f16* __restrict__ v,
-                                                               int64_t len, int32_t H, int32_t KVH, float scale_log2,
-                                                               int64_t per_block, float* __restrict__ ws,
-                                                               unsigned* __restrict__ cnt)
+                                                               int64_t len, int64_t per_block, int32_t KVH, int32_t G,
+                                                               float scale_log2, f16* __restrict__ out,
+                                                               float* __restrict__ ws, unsigned* __restrict__ cnt)
 {
     constexpr int DS = D / 32;              // 32-dim steps of a score tile
     constexpr int DE = D / 16;              // 16-dim tiles of O^T
@@ -634,7 +636,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void k_attention_decode_mfma(f16* _
     __shared__ float wm[kDecWaves][16], wl[kDecWaves][16];
     __shared__ int last_s;
     const int g = blockIdx.x, tid = threadIdx.x, w = tid >> 6, lane = tid & 63, r = lane & 15, gr = lane >> 4;
-    const int G = H / KVH;
+    const int H = G * KVH;
     const int64_t kvs = (int64_t)KVH * D;
     const int64_t kb = (int64_t)blockIdx.y * per_block;
     const int64_t ke = kb + per_block < len ? kb + per_block : len;
@@ -914,8 +916,8 @@ int launch_attention_decode(const AttnDecodePlan& p, void* out, const void* q, c
     if (p.mfma) {
         const float sl = (float)((double)scale * 1.4426950408889634);  // scores in log2 units
         auto go = [&](auto kern) {
-            hipLaunchKernelGGL(kern, grid, dim3(64 * p.waves), 0, s, (f16*)out, (const f16*)q, (const f16*)k,
-                               (const f16*)v, len, (int32_t)H, (int32_t)KVH, sl, per, ws, cnt);
+            hipLaunchKernelGGL(kern, grid, dim3(64 * p.waves), 0, s, (const f16*)q, (const f16*)k, (const f16*)v,
+                               len, per, (int32_t)KVH, (int32_t)(H / KVH), sl, (f16*)out, ws, cnt);
         };
         if (D == 64)
             p.waves == 8 ? go(k_attention_decode_mfma<64, 8>) : go(k_attention_decode_mfma<64, 4>);
