@@ -311,9 +311,10 @@ VVH_API int vvh_plan_launches(vvh_plan plan, int* launches);
  * gives VVH_KERNEL_DOT), else VVH_ERR_UNSUPPORTED.  The stage is written
  * into the plan's device table in place, after waiting for the device
  * (queued runs of the plan read that table): set it before capturing any
- * graph that runs the plan.  Graphs already captured from the plan read the
- * same table, so every later replay of them runs the new stage too.  Calling
- * it while a stream is being captured fails (it synchronises the device). */
+ * graph that runs the plan.  A graph captured before the call is not
+ * updated (a plan of up to 4 problems passes its table in each launch's
+ * kernel arguments): capture it again.  Calling it while a stream is being
+ * captured fails (it synchronises the device). */
 VVH_API int vvh_plan_set_input_op(vvh_plan plan, int in_op, const float* in_w, float in_eps);
 /* RoPE and the KV-cache append as the epilogue of a q/k/v plan: problems
  * q_index, k_index and v_index (indices into the list given to
@@ -328,8 +329,10 @@ VVH_API int vvh_plan_set_input_op(vvh_plan plan, int in_op, const float* in_w, f
  * rows and k's rows must be whole heads (N % head_dim == 0), k and v alike,
  * head_dim a multiple of 16.  Like vvh_plan_set_input_op, the plan's device
  * table is rewritten in place after waiting for the device: set it before
- * capturing graphs that run the plan.  The position is an argument of each
- * run: vvh_plan_run_pos (vvh_plan_run runs at position 0). */
+ * capturing graphs that run the plan.  The plan keeps a device table of the
+ * head_dim / 2 pair frequencies (1 / theta^(2i / head_dim), worked out once
+ * by vvh_rope's arithmetic) until it is destroyed.  The position is an
+ * argument of each run: vvh_plan_run_pos (vvh_plan_run runs at position 0). */
 VVH_API int vvh_plan_set_rope(vvh_plan plan, size_t q_index, size_t k_index, size_t v_index, size_t head_dim,
                               float theta, void* k_cache, void* v_cache);
 /* SiLU-gated epilogue (no reference counterpart): problem `index` of the

@@ -48,6 +48,7 @@ struct LinArgs {
     int32_t rope_d;
     float rope_theta;
     void* cache;
+    const float* rope_freq;  // q and k rows: rope_freq(i, rope_d, rope_theta) for i < rope_d / 2
     int32_t src;  // plans: index of the problem in the caller's list
     // plans: 1 = SiLU-gated epilogue: the N rows are [gate | up] of N / 2
     // each and out gets M rows of N / 2 values silu(gate) * up
@@ -195,6 +196,8 @@ int launch_eltwise(int op, void* out, const void* x, const void* y, int64_t n, i
 int launch_rms_norm(void* out, const void* x, const float* w, int64_t rows, int64_t n, float eps, int dtype,
                     void* stream);
 int launch_softmax(void* out, const void* x, int64_t rows, int64_t n, int dtype, void* stream);
+// out[i] = rope_freq(i, D, theta) for i < D / 2
+int launch_rope_freq(float* out, int64_t D, float theta, void* stream);
 int launch_rope(void* q, void* k, int64_t S, int64_t H, int64_t KVH, int64_t D, int64_t pos, float theta, int dtype,
                 void* stream);
 int launch_rope_append(void* q, void* k, const void* v, void* kc, void* vc, int64_t S, int64_t H, int64_t KVH,

@@ -108,17 +108,40 @@ __device__ __forceinline__ float silu_mul_ref(float g, float u)
 // and the difference (the empty asm: otherwise the compiler may fuse them
 // into FMAs in one kernel and not in another), so k_rope and the RoPE
 // epilogue of a q/k/v plan rotate bit-identically.
-__device__ __forceinline__ void rope_rotate(float x0, float x1, int64_t p, int64_t i, int64_t D, float theta,
-                                            float& r0, float& r1)
+// rope_freq gives the pair's frequency (an fp64 power: the longest part, and
+// the same at every position, so plans keep a table of it), rope_cs_freq
+// the cosine and sine at position p (one fp64 argument reduction for both),
+// rope_apply the rotation; rope_rotate is the three in turn.
+__device__ __forceinline__ float rope_freq(int64_t i, int64_t D, float theta)
 {
     const float e = (float)(2 * i) / (float)D;
-    const float freq = 1.0f / (float)pow((double)theta, (double)e);
+    return 1.0f / (float)pow((double)theta, (double)e);
+}
+__device__ __forceinline__ void rope_cs_freq(int64_t p, float freq, float& c, float& sn)
+{
     const float angle = (float)p * freq;
-    const float c = (float)cos((double)angle), sn = (float)sin((double)angle);
+    double sd, cd;
+    sincos((double)angle, &sd, &cd);
+    c = (float)cd;
+    sn = (float)sd;
+}
+__device__ __forceinline__ void rope_cs(int64_t p, int64_t i, int64_t D, float theta, float& c, float& sn)
+{
+    rope_cs_freq(p, rope_freq(i, D, theta), c, sn);
+}
+__device__ __forceinline__ void rope_apply(float x0, float x1, float c, float sn, float& r0, float& r1)
+{
     float a = x0 * c, b = x1 * sn, d = x0 * sn, f = x1 * c;
     __asm__("" : "+v"(a), "+v"(b), "+v"(d), "+v"(f));
     r0 = a - b;
     r1 = d + f;
+}
+__device__ __forceinline__ void rope_rotate(float x0, float x1, int64_t p, int64_t i, int64_t D, float theta,
+                                            float& r0, float& r1)
+{
+    float c, sn;
+    rope_cs(p, i, D, theta, c, sn);
+    rope_apply(x0, x1, c, sn, r0, r1);
 }
 
 // Butterfly steps within rows of 16 lanes as DPP moves (one VALU op, no

@@ -437,10 +437,12 @@ __device__ __forceinline__ void store_out_g(const LinArgs& a, int64_t m, int64_t
 // of the pair (rows A and B are i and i + D/2 of one head) at position
 // pos + m, then the store; k and v rows also go to row pos + m of the cache.
 // Bit-identical to the plan's plain store followed by vvh_rope_append.
+// rc, rs: rope_cs of the pair at position pos + m (q and k rows).
 template <typename OT, int MT, bool EARLY>
 __device__ __forceinline__ void dot_store_rope(const LinArgs& a, int64_t pos, int64_t rowA, int64_t rowB,
                                                const float (&accA)[MT], const float (&accB)[MT],
-                                               const float (&e_sc)[2], const float (&e_bi)[2], const OT (&e_res)[MT][2])
+                                               const float (&e_sc)[2], const float (&e_bi)[2], const OT (&e_res)[MT][2],
+                                               const float (&rc)[MT], const float (&rs)[MT])
 {
     const int64_t rows[2] = {rowA, rowB};
     float sc[2], bi[2];
@@ -463,9 +465,8 @@ __device__ __forceinline__ void dot_store_rope(const LinArgs& a, int64_t pos, in
             v[h] = (OT)dot_epi(h ? accB[m] : accA[m], sc[h], a.bias != nullptr, bi[h], a.res != nullptr, rv);
         }
         if (a.rope != 3) {
-            const int64_t i = rowA % a.rope_d;  // the pair's index within its head (< rope_d / 2)
             float r0, r1;
-            rope_rotate((float)v[0], (float)v[1], pos + m, i, a.rope_d, a.rope_theta, r0, r1);
+            rope_apply((float)v[0], (float)v[1], rc[m], rs[m], r0, r1);
             v[0] = (OT)r0;
             v[1] = (OT)r1;
         }
@@ -614,6 +615,22 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
     // TB/s on the grouped decode set).
     float e_sc[2] = {0.0f, 0.0f}, e_bi[2] = {0.0f, 0.0f};
     OT e_res[MT][2];
+    // RoPE cosine and sine of the lane's pair for each activation row (q and
+    // k rows).  Early launches work them out right after requesting the
+    // weights, while the loads are in flight: they take a long chain of fp64
+    // operations that depends only on the position and the pair.
+    // The pair's frequency comes from the plan's table (rowA % rope_d is the
+    // pair's index within its head, < rope_d / 2).
+    float rc[MT], rs[MT], rfreq = 0.0f;
+    auto rope_load = [&]() {
+        if (pair) rfreq = *gbl(a.rope_freq + rowA % a.rope_d);
+    };
+    auto rope_prep = [&]() {
+        if (pair) {
+#pragma unroll
+            for (int m = 0; m < MT; m++) rope_cs_freq(pos + m, rfreq, rc[m], rs[m]);
+        }
+    };
     // RMSNorm stage of an early launch whose rows take one batch of
     // sum-of-squares loads and one round of chunks per thread: the rows and
     // norm weights are requested before the weight ring, so the sums, the
@@ -632,10 +649,12 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
 #pragma unroll
             for (int m = 0; m < MT; m++) e_res[m][h] = *gbl(rp + (a.res && m < a.M ? m * a.N : 0) + rows[h]);
         }
+        rope_load();
         if (active && !rms_first) {
 #pragma unroll
             for (int u = 0; u < D; u++) issue(u, (int32_t)c.s0 + u);
         }
+        if (!rms_first) rope_prep();
     }
     if (XLDS && rms_first) {
         const int32_t K32 = (int32_t)a.K, xchunks = (int32_t)(a.M * a.K / 8);
@@ -669,6 +688,7 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
 #pragma unroll
         for (int u = 0; u < D; u++) issue(u, (int32_t)c.s0 + u);
         __builtin_amdgcn_sched_barrier(0);
+        rope_prep();
         // per row as k_rms_norm: thread t sums x[t], x[t + 256], ... in order
         // (slots past the row add an exact 0), then the same block reduction
         float* red4 = &red.v[0][0][0];
@@ -844,8 +864,13 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
         return;
     }
     if (a.rope != 0) {
-        if (c.ks == 0 && ch == 0 && n0 < a.N) dot_store_rope<OT, MT, EARLY>(a, pos, rowA, rowB, accA, accB, e_sc, e_bi,
-                                                                          e_res);
+        if (c.ks == 0 && ch == 0 && n0 < a.N) {
+            if constexpr (!EARLY) {
+                rope_load();
+                rope_prep();
+            }
+            dot_store_rope<OT, MT, EARLY>(a, pos, rowA, rowB, accA, accB, e_sc, e_bi, e_res, rc, rs);
+        }
         return;
     }
     if (c.ks == 0 && ch == 0 && n0 < a.N) {

@@ -228,6 +228,20 @@ __global__ __launch_bounds__(256) void k_rope(T* __restrict__ q, T* __restrict__
     }
 }
 
+__global__ __launch_bounds__(256) void k_rope_freq(float* __restrict__ out, int64_t D, float theta)
+{
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < D / 2) out[i] = rope_freq(i, D, theta);
+}
+
+int launch_rope_freq(float* out, int64_t D, float theta, void* stream)
+{
+    const int64_t n = D / 2;
+    hipLaunchKernelGGL(k_rope_freq, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       out, D, theta);
+    return (int)hipGetLastError();
+}
+
 int launch_rope(void* q, void* k, int64_t S, int64_t H, int64_t KVH, int64_t D, int64_t pos, float theta, int dtype,
                 void* stream)
 {

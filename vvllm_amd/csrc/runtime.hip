@@ -107,6 +107,10 @@ struct Plan {
     int dot_depth = 4;           // k_dot_grouped ring depth: the largest dot_depth of the problems
     int max_m = 0;
     void* dev_stream = nullptr;  // tile_prob, list, list_off
+    float* rope_freq = nullptr;  // RoPE epilogue: the pair frequencies of the q and k rows
+    // tables replaced by a later vvh_plan_set_rope: a graph captured before
+    // may still read them, so they are freed with the plan
+    std::vector<float*> rope_retired;
 };
 std::mutex g_pmu;
 std::unordered_map<vvh_plan, Plan> g_plans;
@@ -1442,6 +1446,18 @@ VVH_API int vvh_plan_set_rope(vvh_plan plan, size_t q_index, size_t k_index, siz
     v->cache = v_cache;
     // the table is read by launches already queued: replace it once they are done
     (void)hipDeviceSynchronize();
+    // the pair frequencies, worked out once on the device by the function
+    // vvh_rope uses
+    if (p.rope_freq) p.rope_retired.push_back(p.rope_freq);
+    p.rope_freq = nullptr;
+    hipError_t fe = hipMalloc(&p.rope_freq, head_dim / 2 * sizeof(float));
+    if (fe == hipSuccess) fe = (hipError_t)launch_rope_freq(p.rope_freq, (int64_t)head_dim, theta, nullptr);
+    if (fe == hipSuccess) fe = hipDeviceSynchronize();
+    if (fe != hipSuccess) {
+        q->rope = k->rope = v->rope = 0;
+        return fail_hip(fe, "RoPE frequency table");
+    }
+    q->rope_freq = k->rope_freq = p.rope_freq;
     const hipError_t e = hipMemcpy(const_cast<LinArgs*>(p.sargs.table), p.args.data(), p.args.size() * sizeof(LinArgs),
                                    hipMemcpyHostToDevice);
     return e == hipSuccess ? VVH_OK : fail_hip(e, "plan table upload");
@@ -1480,6 +1496,8 @@ VVH_API int vvh_plan_destroy(vvh_plan plan)
     if (it == g_plans.end()) return fail(VVH_ERR_UNKNOWN_HANDLE, "unknown plan %llu", (unsigned long long)plan);
     if (it->second.dev_table) (void)hipFree(it->second.dev_table);
     if (it->second.dev_stream) (void)hipFree(it->second.dev_stream);
+    if (it->second.rope_freq) (void)hipFree(it->second.rope_freq);
+    for (float* t : it->second.rope_retired) (void)hipFree(t);
     g_plans.erase(it);
     return VVH_OK;
 }
