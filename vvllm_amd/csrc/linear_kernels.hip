@@ -637,7 +637,7 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
     // block reduction and the normalization run while the weights are in
     // flight (the in-order wait counter lets a wait for the rows leave the
     // younger ring loads outstanding)
-    const bool rms_first = EARLY && XLDS && a.xop == 1 && a.K <= 256 * 8 && a.M * a.K / 8 <= 256 * 4;
+    const bool rms_first = EARLY && XLDS && a.xop == 1 && a.K <= 256 * 8;
     if constexpr (EARLY) {
         const float* bp = a.bias ? a.bias : a.scales;  // absent bias / residual: in-bounds reads, unused
         const OT* rp = a.res ? static_cast<const OT*>(a.res) : reinterpret_cast<const OT*>(a.scales);
@@ -658,7 +658,8 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
     }
     if (XLDS && rms_first) {
         const int32_t K32 = (int32_t)a.K, xchunks = (int32_t)(a.M * a.K / 8);
-        constexpr int XL = 4;
+        // M <= MT rows of K <= 2048: at most MT chunks of 8 per thread
+        constexpr int XL = MT;
         f16 raw[MT][8];
         h8 xr[XL];
         f4 w0[XL], w1[XL];
