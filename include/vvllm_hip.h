@@ -487,9 +487,10 @@ typedef enum vvh_kernel {
 VVH_API int vvh_linear_q8_choice(size_t M, size_t N, size_t K, int act_dtype, int out_dtype);
 /* The GEMM kernel behind VVH_KERNEL_GEMM for an fp16 call of this shape
  * (measurement and reporting; no reference counterpart): returns 3 for
- * k_gemm3 (*tile_n = 128 or 192), 1 for k_gemm (K % 64 != 0), or a negative
- * status; *splits > 1 is a split-K launch followed by a reduction kernel.
- * tile_n and splits may be NULL. */
+ * k_gemm3 on 128-row tiles, 4 for k_gemm3 on 64-row tiles (*tile_n = 128
+ * or 192), 1 for k_gemm (K % 64 != 0), or a negative status; *splits > 1 is
+ * a split-K launch followed by a reduction kernel.  tile_n and splits may
+ * be NULL. */
 VVH_API int vvh_gemm_variant(size_t M, size_t N, size_t K, int* tile_n, int* splits);
 /* Forces one kernel family for subsequent calls on this process (testing and
  * measurement); VVH_KERNEL_AUTO restores the size-based choice.  A forced

@@ -135,11 +135,14 @@ def test_init_without_device_reports_no_device():
 
 def test_gemm_variant_choice():
     """The GEMM kernel behind the "gemm" family (host logic, 256 CUs assumed
-    off the device): k_gemm3 with 128 x 128 tiles when one round of blocks
-    covers the problem, 128 x 192 when that saves a round, split-K for few
-    tiles over a long K, k_gemm for K % 64 != 0."""
-    assert capi.gemm_variant(512, 4864, 896) == "k_gemm3 128x128"     # 152 tiles, one round
-    assert capi.gemm_variant(128, 4864, 896) == "k_gemm3 128x128"
+    off the device): k_gemm3 with 64 x 128 tiles when those give each block
+    a CU, 128 x 128 tiles when one round of blocks covers the problem,
+    128 x 192 when that saves a round, split-K for few tiles over a long K,
+    k_gemm for K % 64 != 0."""
+    assert capi.gemm_variant(512, 4864, 896) == "k_gemm3 128x128"     # 304 64-row tiles; 152, one round
+    assert capi.gemm_variant(128, 4864, 896) == "k_gemm3 64x128"      # 76 64-row tiles
+    assert capi.gemm_variant(512, 1152, 896) == "k_gemm3 64x128"      # 72
+    assert capi.gemm_variant(256, 8960, 1536) == "k_gemm3 128x128"    # 280 64-row tiles > 256 CUs
     assert capi.gemm_variant(2048, 4864, 896) == "k_gemm3 128x192"    # 3 rounds -> 2
     assert capi.gemm_variant(512, 896, 4864) == "k_gemm3 128x128 split 6"   # 28 tiles, 76 k stages
     assert capi.gemm_variant(2048, 896, 4864) == "k_gemm3 128x128 split 2"  # 112 tiles: half the CUs

@@ -226,8 +226,8 @@ def gemm_variant(M, N, K) -> str:
     """Name of the GEMM kernel an fp16 call of this shape dispatches to."""
     tn, sp = c_int(), c_int()
     v = load().vvh_gemm_variant(M, N, K, ctypes.byref(tn), ctypes.byref(sp))
-    if v == 3:
-        return f"k_gemm3 128x{tn.value}" + (f" split {sp.value}" if sp.value > 1 else "")
+    if v in (3, 4):
+        return f"k_gemm3 {128 if v == 3 else 64}x{tn.value}" + (f" split {sp.value}" if sp.value > 1 else "")
     return "k_gemm" if v == 1 else "?"
 
 

@@ -180,9 +180,11 @@ int launch_dot_grouped(const LinArgs* dev_table, const int32_t* dev_block_prob, 
                        int64_t total_blocks, int max_m, bool x_in_lds, size_t lds_bytes, int out, bool early,
                        int depth, int64_t pos, void* stream);
 int launch_gemm(const LinArgs& a, int out, void* stream);
-// k_gemm3 (gemm_kernels.hip): one 128 x BN tile (or one k split of it) per
-// block, K % 64 == 0; layout 1 = 128 x 192, 3 = 128 x 128
+// k_gemm3 (gemm_kernels.hip): one BM x BN tile (or one k split of it) per
+// block, K % 64 == 0; layout 1 = 128 x 192, 3 = 128 x 128, 4 = 64 x 128,
+// 5 = 128 x 128 as 8 waves
 int gemm3_tile_n(int layout);
+int gemm3_tile_m(int layout);
 int launch_gemm3(const LinArgs& a, int out, int layout, void* stream);
 // sum of the a.nsplit partials in a.ws + epilogue (scale, bias, residual)
 int launch_splitk_reduce(const LinArgs& a, int out, void* stream);

@@ -59,11 +59,11 @@
 namespace vvh
 {
 
-template <int BN>
+template <int BN, int BM>
 struct Gemm3Stage {
-    static constexpr int kOps = kGemmBM * kGemmBK * 2 + BN * kGemmBK;  // A fp16 + B codes
-    static constexpr int kEpi = 32 * (BN + 4) * 4;                        // one epilogue quarter, fp32
-    __attribute__((aligned(16))) f16 a[kGemmBM * kGemmBK];
+    static constexpr int kOps = BM * kGemmBK * 2 + BN * kGemmBK;  // A fp16 + B codes
+    static constexpr int kEpi = 32 * (BN + 4) * 4;                 // one 32-row epilogue quarter, fp32
+    __attribute__((aligned(16))) f16 a[BM * kGemmBK];
     __attribute__((aligned(16))) int8_t b[BN * kGemmBK];
     __attribute__((aligned(16))) char pad[kEpi > kOps ? kEpi - kOps : 16];
 };
@@ -140,12 +140,12 @@ __device__ __forceinline__ void gemm3_slice_last(const h8 (&a)[2][TI], const h8 
 // One stage's direct-to-LDS loads of this wave: buffer loads whose per-lane
 // offsets are fixed for the whole k loop and whose stage offset k0 goes in
 // the scalar offset, so a stage costs no address arithmetic.
-template <int NW, int BN>
+template <int NW, int BN, int BM>
 __device__ __forceinline__ void gemm3_fill(f16* __restrict__ sa, int8_t* __restrict__ sb, __amdgpu_buffer_rsrc_t ra,
                                            __amdgpu_buffer_rsrc_t rb, const uint32_t* a_off, const uint32_t* b_off,
                                            int wave, uint32_t ka, uint32_t kb)
 {
-    constexpr int LA = 16 / NW, LB = BN / 16 / NW;
+    constexpr int LA = BM / 8 / NW, LB = BN / 16 / NW;
 #pragma unroll
     for (int i = 0; i < LA; i++)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, sa + (wave * LA + i) * 512, 16, a_off[i], ka * 2, 0, 0);
@@ -154,30 +154,34 @@ __device__ __forceinline__ void gemm3_fill(f16* __restrict__ sa, int8_t* __restr
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, sb + (wave * LB + i) * 1024, 16, b_off[i], kb, 0, 0);
 }
 
-template <typename OT, int D, int WN, int TJ, int TI>
-__global__ __launch_bounds__(64 * (4 / TI) * WN, 1) void k_gemm3(LinArgs a)
+// BM = 64: blocks of half the LDS and registers, two resident per CU, so one
+// block's MFMAs run while the other waits at its barrier or for its loads.
+template <typename OT, int D, int WN, int TJ, int TI, int BM>
+__global__ __launch_bounds__(64 * (BM / 32 / TI) * WN, BM == 64 ? 2 : 1) void k_gemm3(LinArgs a)
 {
     static_assert(D == 4, "four stages: even (static fragment parity) and one epilogue quarter per stage");
     static_assert(TI == 2 || TI == 4, "wave tiles of 64 or 128 rows");
-    constexpr int WM = 4 / TI;  // waves along the 128 rows
+    static_assert(BM == 64 || BM == 128, "block tiles of 64 or 128 rows");
+    constexpr int WM = BM / 32 / TI;  // waves along the BM rows
+    static_assert(WM >= 1, "a wave tile within the block");
     constexpr int NW = WM * WN;
     constexpr int NT = 64 * NW;
     constexpr int BN = 32 * TJ * WN;
-    static_assert(16 % NW == 0 && (BN / 16) % NW == 0, "whole 1 KB loads per wave");
-    constexpr int LA = 16 / NW, LB = BN / 16 / NW;
+    static_assert((BM / 8) % NW == 0 && (BN / 16) % NW == 0, "whole 1 KB loads per wave");
+    constexpr int LA = BM / 8 / NW, LB = BN / 16 / NW;
     constexpr int LPS = LA + LB;  // loads per stage per thread
-    using Stage = Gemm3Stage<BN>;
+    using Stage = Gemm3Stage<BN, BM>;
     using Frag = Gemm3Frag<TJ, TI>;
     __shared__ Stage st0, st1, st2, st3;
 
-    const int64_t nbm = (a.M + kGemmBM - 1) / kGemmBM;
+    const int64_t nbm = (a.M + BM - 1) / BM;
     const int64_t nbn = (a.N + BN - 1) / BN;
     const int64_t tiles = nbm * nbn;
     const bool split = a.nsplit > 1;
     // consecutive tiles (same n0) on one XCD
     const int64_t logical = xcd_remap(blockIdx.x, tiles * (split ? a.nsplit : 1));
     const int64_t ks = logical / tiles, tile = logical - ks * tiles;
-    const int64_t m0 = (tile % nbm) * kGemmBM;
+    const int64_t m0 = (tile % nbm) * BM;
     const int64_t n0 = (tile / nbm) * BN;
     const int64_t kbase = split ? ks * a.kstages : 0;  // first k stage of this block
 
@@ -261,7 +265,7 @@ __global__ __launch_bounds__(64 * (4 / TI) * WN, 1) void k_gemm3(LinArgs a)
     };
     auto issue = [&](Stage& g, int64_t kt) {
         const int64_t k0 = (kbase + kt) * kGemmBK;
-        gemm3_fill<NW, BN>(g.a, g.b, ra, rb, a_off, b_off, wave, (uint32_t)k0, (uint32_t)(k0 < KB ? k0 : k0 - KB));
+        gemm3_fill<NW, BN, BM>(g.a, g.b, ra, rb, a_off, b_off, wave, (uint32_t)k0, (uint32_t)(k0 < KB ? k0 : k0 - KB));
     };
 
     f16v acc[TI][TJ];
@@ -341,11 +345,11 @@ __global__ __launch_bounds__(64 * (4 / TI) * WN, 1) void k_gemm3(LinArgs a)
     auto quarter = [&](int q) -> float* {
         return reinterpret_cast<float*>(q == 0 ? &st0 : q == 1 ? &st1 : q == 2 ? &st2 : &st3);
     };
-    constexpr int RI = (kGemmBM + RG - 1) / RG;  // rows per thread
+    constexpr int RI = (BM + RG - 1) / RG;  // rows per thread
     // Interior tiles (every row and column inside the problem, whole 8-wide
     // chunks, no split) take a branch-free path; its residual rows are
     // loaded here, so their latency overlaps the accumulator transpose.
-    const bool interior = !split && m0 + kGemmBM <= a.M && n0 + BN <= a.N && a.N % 8 == 0;
+    const bool interior = !split && m0 + BM <= a.M && n0 + BN <= a.N && a.N % 8 == 0;
     const bool own = erg < RG;
     constexpr int RW = sizeof(OT) / 2;  // 16-byte chunks per 8 outputs
     u4 rr[RI][RW];
@@ -354,7 +358,7 @@ __global__ __launch_bounds__(64 * (4 / TI) * WN, 1) void k_gemm3(LinArgs a)
         const OT* rp = static_cast<const OT*>(a.res) + o_first;
 #pragma unroll
         for (int i = 0; i < RI; i++)
-            if (i + 1 < RI || erg + i * RG < kGemmBM)
+            if (i + 1 < RI || erg + i * RG < BM)
 #pragma unroll
                 for (int c = 0; c < RW; c++) rr[i][c] = reinterpret_cast<const u4*>(rp + i * o_step)[c];
     }
@@ -391,7 +395,7 @@ __global__ __launch_bounds__(64 * (4 / TI) * WN, 1) void k_gemm3(LinArgs a)
 #pragma unroll
             for (int u = 0; u < UB; u++) {
                 const int i = i0 + u, row = erg + i * RG;
-                if (i < RI && (i + 1 < RI || row < kGemmBM)) {
+                if (i < RI && (i + 1 < RI || row < BM)) {
                     const float* tq = quarter(row >> 5) + (row & 31) * ES + ech * 8;
                     p[u] = *reinterpret_cast<const f4*>(tq + 4 * sw);
                     q[u] = *reinterpret_cast<const f4*>(tq + 4 - 4 * sw);
@@ -400,7 +404,7 @@ __global__ __launch_bounds__(64 * (4 / TI) * WN, 1) void k_gemm3(LinArgs a)
 #pragma unroll
             for (int u = 0; u < UB; u++) {
                 const int i = i0 + u, row = erg + i * RG;
-                if (!(i < RI && (i + 1 < RI || row < kGemmBM))) continue;
+                if (!(i < RI && (i + 1 < RI || row < BM))) continue;
                 const f4 lo = sw ? q[u] : p[u], hi = sw ? p[u] : q[u];
                 float v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 #pragma unroll
@@ -441,7 +445,7 @@ __global__ __launch_bounds__(64 * (4 / TI) * WN, 1) void k_gemm3(LinArgs a)
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const int row = erg + (i0 + u) * RG;
-            if (i0 + u < RI && row < kGemmBM) {
+            if (i0 + u < RI && row < BM) {
                 const float* tq = quarter(row >> 5) + (row & 31) * ES + ech * 8;
                 const f4 p = *reinterpret_cast<const f4*>(tq + 4 * sw);
                 const f4 q = *reinterpret_cast<const f4*>(tq + 4 - 4 * sw);
@@ -453,7 +457,7 @@ __global__ __launch_bounds__(64 * (4 / TI) * WN, 1) void k_gemm3(LinArgs a)
         for (int u = 0; u < U; u++) {
             const int row = erg + (i0 + u) * RG;
             const int64_t mm = m0 + row;
-            if (!(i0 + u < RI && row < kGemmBM) || mm >= a.M) continue;
+            if (!(i0 + u < RI && row < BM) || mm >= a.M) continue;
             float v[8] = {v0[u][0], v0[u][1], v0[u][2], v0[u][3], v1[u][0], v1[u][1], v1[u][2], v1[u][3]};
             const int64_t o = mm * a.N + en;
             if (split) {  // raw partial sums of this split
@@ -504,30 +508,35 @@ __global__ __launch_bounds__(64 * (4 / TI) * WN, 1) void k_gemm3(LinArgs a)
     }
 }
 
-// Tile shapes (layout code -> WN, TJ, TI): 1 = 128 x 192 (4 waves of
+// Tile shapes (layout code -> WN, TJ, TI, BM): 1 = 128 x 192 (4 waves of
 // 64 x 96), 3 = 128 x 128 (4 waves of 128 x 32: each converted code
 // fragment feeds 4 row tiles, 2.5 conversion VALU per MFMA; measured against
 // 4 waves of 64 x 64 in the same runs: M=512 gate/up 11.13 -> 10.78 us,
-// M=2048 33.7 -> 33.3 us, split-K down M=2048 32.7 -> 32.0 us).
-int gemm3_tile_n(int layout) { return layout == 3 ? 128 : 192; }
+// M=2048 33.7 -> 33.3 us, split-K down M=2048 32.7 -> 32.0 us), 4 = 64 x 128
+// (4 waves of 64 x 32, two blocks per CU), 5 = 128 x 128 (8 waves of 64 x 32,
+// two per SIMD).
+int gemm3_tile_n(int layout) { return layout == 1 ? 192 : 128; }
+int gemm3_tile_m(int layout) { return layout == 4 ? 64 : 128; }
 
-template <int WN, int TJ, int TI>
+template <int WN, int TJ, int TI, int BM>
 static void gemm3_go(const LinArgs& a, bool f32, hipStream_t s)
 {
     constexpr int BN = 32 * TJ * WN;
-    constexpr int NT = 64 * (4 / TI) * WN;
-    const int64_t tiles = ((a.M + kGemmBM - 1) / kGemmBM) * ((a.N + BN - 1) / BN);
+    constexpr int NT = 64 * (BM / 32 / TI) * WN;
+    const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
     const dim3 grid((unsigned)(tiles * (a.nsplit > 1 ? a.nsplit : 1)));
-    if (f32) hipLaunchKernelGGL((k_gemm3<float, 4, WN, TJ, TI>), grid, dim3(NT), 0, s, a);
-    else hipLaunchKernelGGL((k_gemm3<f16, 4, WN, TJ, TI>), grid, dim3(NT), 0, s, a);
+    if (f32) hipLaunchKernelGGL((k_gemm3<float, 4, WN, TJ, TI, BM>), grid, dim3(NT), 0, s, a);
+    else hipLaunchKernelGGL((k_gemm3<f16, 4, WN, TJ, TI, BM>), grid, dim3(NT), 0, s, a);
 }
 
 int launch_gemm3(const LinArgs& a, int out, int layout, void* stream)
 {
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool f32 = out == VVH_F32;
-    if (layout == 3) gemm3_go<4, 1, 4>(a, f32, s);
-    else gemm3_go<2, 3, 2>(a, f32, s);
+    if (layout == 3) gemm3_go<4, 1, 4, 128>(a, f32, s);
+    else if (layout == 4) gemm3_go<4, 1, 2, 64>(a, f32, s);
+    else if (layout == 5) gemm3_go<4, 1, 2, 128>(a, f32, s);
+    else gemm3_go<2, 3, 2, 128>(a, f32, s);
     return (int)hipGetLastError();
 }
 

@@ -253,14 +253,22 @@ int gemm_splits(int64_t tiles, int64_t stages, uint64_t plane_bytes)
     return (int)s;
 }
 
-// k_gemm3 tile shape: split-K problems (few tiles, long K) take 128 x 128;
-// unsplit ones 128 x 192 when it takes fewer rounds of blocks over the CUs
-// than 128 x 128 by a margin that pays for its longer tiles (a 128 x 192
-// tile takes 1.33x as long as a 128 x 128 one on MI355X), else 128 x 128.
+// k_gemm3 tile shape: split-K problems (few tiles, long K) take 128 x 128.
+// Unsplit ones take 64 x 128 when those tiles give every block a CU of its
+// own (then more CUs work than with 128-row tiles, each on half a tile:
+// gate/up N=4864 K=896 at M=128 and 256, 10.5 -> 8.2 us; q/k/v N=1152 at
+// M=512, 10.3 -> 8.0 us; with more 64-row tiles than CUs, two share a CU
+// and the time rises: M=512 gate/up 10.7 -> 11.8 us); else 128 x 192 when
+// it takes fewer rounds of blocks over the CUs than 128 x 128 by a margin
+// that pays for its longer tiles (a 128 x 192 tile takes 1.33x as long as a
+// 128 x 128 one on MI355X), else 128 x 128.  (128 x 128 as 8 waves of
+// 64 x 32, layout 5, measured the same as 4 waves of 128 x 32 at M=512:
+// the loads into LDS, not latency within a SIMD, bound a block.)
 int gemm3_layout(int64_t M, int64_t N, int splits)
 {
     if (splits > 1) return 3;
     const int64_t cus = g_cu_count > 0 ? g_cu_count : 256;
+    if (((M + 63) / 64) * ((N + 127) / 128) <= cus) return 4;
     const int64_t nbm = (M + kGemmBM - 1) / kGemmBM;
     const int64_t r128 = (nbm * ((N + 127) / 128) + cus - 1) / cus;
     const int64_t r192 = (nbm * ((N + 191) / 192) + cus - 1) / cus;
@@ -1577,8 +1585,9 @@ VVH_API int vvh_gemm_variant(size_t M, size_t N, size_t K, int* tile_n, int* spl
             const int64_t kst = (stages + s - 1) / s;
             s = (int)((stages + kst - 1) / kst);
         }
-        v = 3;
-        tn = gemm3_tile_n(gemm3_layout((int64_t)M, (int64_t)N, s));
+        const int layout = gemm3_layout((int64_t)M, (int64_t)N, s);
+        v = gemm3_tile_m(layout) == 64 ? 4 : 3;
+        tn = gemm3_tile_n(layout);
     }
     if (tile_n) *tile_n = tn;
     if (splits) *splits = s;
