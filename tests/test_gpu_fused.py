@@ -40,7 +40,8 @@ def q8_weight(rng, N, K):
     return capi.DevBuf.from_array(q), capi.DevBuf.from_array(s)
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 896, 896), (2, 130, 896), (4, 64, 1536), (1, 9728, 896), (3, 17, 4864)])
+@pytest.mark.parametrize("M,N,K", [(1, 896, 896), (2, 130, 896), (4, 64, 1536), (1, 9728, 896), (3, 17, 4864),
+                                   (1, 640, 4864)])
 def test_rms_norm_stage(gpu, M, N, K):
     print(f"[case] rms_norm stage M={M} N={N} K={K}", flush=True)
     rng = np.random.default_rng(M * 7 + N + K)
