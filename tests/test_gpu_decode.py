@@ -86,14 +86,17 @@ def test_decode_qwen25_05b_shapes(gpu, oracle, head):
     run(oracle, qd.QWEN25_05B, capi.F16, head, steps=2, max_ctx=16)
 
 
+@pytest.mark.parametrize("P", [511, 700])
 @pytest.mark.parametrize("fused", [False, True], ids=["unfused", "fused"])
-def test_decode_late_position(gpu, oracle, fused):
-    """One step at position 511 of a filled KV cache, Qwen2.5-0.5B shapes, as
-    bench.py times it: the span of 512 keys runs the split decode attention
-    (several blocks per kv head) and its combine launch, which the short
-    steps above never reach.  The cache rows the step reads are copied back
-    from the device, so the CPU forward attends to the same context."""
-    cfg, P, max_ctx = qd.QWEN25_05B, 511, 1024
+def test_decode_late_position(gpu, oracle, fused, P):
+    """One step at a late position of a filled KV cache, Qwen2.5-0.5B shapes:
+    511 as bench.py times it (512 keys: the MFMA decode attention with one
+    8-wave block per kv head, 8 chunks of 64 keys) and 700 (11 chunks: the
+    span split over several blocks per kv head, merged in the same launch by
+    the last block to arrive), which the short steps above never reach.  The
+    cache rows the step reads are copied back from the device, so the CPU
+    forward attends to the same context."""
+    cfg, max_ctx = qd.QWEN25_05B, 1024
     m = qd.Model(cfg, act=capi.F16, lm_head="int8", max_ctx=max_ctx, seed=13, fused=fused)
     try:
         m.fill_kv(5)
