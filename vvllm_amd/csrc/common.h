@@ -181,8 +181,7 @@ int launch_dot_grouped(const LinArgs* dev_table, const int32_t* dev_block_prob, 
                        int depth, int64_t pos, void* stream);
 int launch_gemm(const LinArgs& a, int out, void* stream);
 // k_gemm3 (gemm_kernels.hip): one BM x BN tile (or one k split of it) per
-// block, K % 64 == 0; layout 1 = 128 x 192, 3 = 128 x 128, 4 = 64 x 128,
-// 5 = 128 x 128 as 8 waves
+// block, K % 64 == 0; layout 1 = 128 x 192, 3 = 128 x 128, 4 = 64 x 128
 int gemm3_tile_n(int layout);
 int gemm3_tile_m(int layout);
 int launch_gemm3(const LinArgs& a, int out, int layout, void* stream);

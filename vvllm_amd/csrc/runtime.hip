@@ -262,8 +262,8 @@ int gemm_splits(int64_t tiles, int64_t stages, uint64_t plane_bytes)
 // it takes fewer rounds of blocks over the CUs than 128 x 128 by a margin
 // that pays for its longer tiles (a 128 x 192 tile takes 1.33x as long as a
 // 128 x 128 one on MI355X), else 128 x 128.  (128 x 128 as 8 waves of
-// 64 x 32, layout 5, measured the same as 4 waves of 128 x 32 at M=512:
-// the loads into LDS, not latency within a SIMD, bound a block.)
+// 64 x 32 measured the same as 4 waves of 128 x 32 at M=512: the loads
+// into LDS, not latency within a SIMD, bound a block.)
 int gemm3_layout(int64_t M, int64_t N, int splits)
 {
     if (splits > 1) return 3;
