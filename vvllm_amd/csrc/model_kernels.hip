@@ -631,9 +631,19 @@ constexpr int kDecChunk = 64;  // keys per wave and chunk
 
 typedef _Float16 h4v __attribute__((ext_vector_type(4)));
 
-template <int D, int kDecWaves>
+// ds_read_b64_tr_b16 (gfx950): an 8-byte LDS read per lane, transposed in
+// groups of 16 lanes (lane i's element j is lane 4j + i/4's element i % 4).
+// p must point into LDS, 8-byte aligned.
+__device__ __forceinline__ h4v lds_read_tr16(const _Float16* p)
+{
+    typedef short s4v __attribute__((ext_vector_type(4)));
+    const s4v v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4v*)(p));
+    return __builtin_bit_cast(h4v, v);
+}
+
 // What the first loads depend on comes first (q, k, v, the key range, the
 // head layout: 14 dwords, preloaded into registers at dispatch); G = H / KVH.
+template <int D, int kDecWaves>
 __global__ __launch_bounds__(64 * kDecWaves) void k_attention_decode_mfma(const f16* __restrict__ q,
                                                                const f16* __restrict__ k, const f16* __restrict__ v,
                                                                int64_t len, int64_t per_block, int32_t KVH, int32_t G,
@@ -735,16 +745,19 @@ __global__ __launch_bounds__(64 * kDecWaves) void k_attention_decode_mfma(const 
             *reinterpret_cast<h4v*>(vw + row * VP + col) = h4v{vr[i][0], vr[i][1], vr[i][2], vr[i][3]};
             *reinterpret_cast<h4v*>(vw + row * VP + col + 4) = h4v{vr[i][4], vr[i][5], vr[i][6], vr[i][7]};
         }
+        // A operand of the PV MFMAs: lane (r, gr) holds V[key][16e + r] for
+        // keys 32u + 4gr + j and 32u + 16 + 4gr + j, j < 4.  Two LDS transpose
+        // reads give them: in each group of 16 lanes, lane i's element j
+        // comes from lane 4j + i/4's 8-byte piece, element i % 4, so lane s
+        // of the group points at 4 consecutive dims (16e + 4(s % 4)) of key
+        // row 32u + 4gr + s / 4 (and of the row 16 keys on).
 #pragma unroll
         for (int u = 0; u < 2; u++)
 #pragma unroll
             for (int e = 0; e < DE; e++) {
-                h8 va;
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    const int key = 32 * u + (j < 4 ? 4 * gr + j : 16 + 4 * gr + j - 4);
-                    va[j] = vw[key * VP + 16 * e + r];
-                }
+                const _Float16* src = vw + (32 * u + 4 * gr + (r >> 2)) * VP + 16 * e + 4 * (r & 3);
+                const h4v lo = lds_read_tr16(src), hi = lds_read_tr16(src + 16 * VP);
+                const h8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
                 o[e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, ph[u], o[e], 0, 0, 0);
                 o[e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl[u], o[e], 0, 0, 0);
             }
