@@ -121,6 +121,11 @@ constexpr int64_t kDotMaxM = 4;
 constexpr int kDotStep = 128;               // k codes per row per step
 constexpr int64_t kDotLdsMax = 80 * 1024;   // dynamic LDS of one block at most
 constexpr int64_t kDotRedBytes = 4 * 4 * 16 * 4;
+// k_dot with 3 or 4 activation rows (MT = 4) takes its dot products on MFMA:
+// each wave passes its step's 16 x 128 code tile through LDS (rows of
+// kDotWtPitch bytes) to gather the MFMA operand fragments
+constexpr int kDotWtPitch = 144;
+constexpr int64_t kDotWtBytes = 4 * 16 * kDotWtPitch;
 // k_dot takes N, M and K as 32-bit kernel arguments and 32-bit k offsets
 inline bool dot_fits(int64_t N, int64_t K)
 {

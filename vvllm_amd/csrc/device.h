@@ -53,6 +53,15 @@ __device__ __forceinline__ void i8x16_to_h8x2(const u4 w, h8& b0, h8& b1)
     b1 = __builtin_bit_cast(h8, u4{c[4], c[5], c[6], c[7]});
 }
 
+// 8 codes (two dwords) -> one 8-wide fp16 MFMA operand, in code order.
+__device__ __forceinline__ h8 i8x8_to_h8(const uint32_t w0, const uint32_t w1)
+{
+    uint32_t c[4];
+    i8x4_to_f16x4(w0, c[0], c[1]);
+    i8x4_to_f16x4(w1, c[2], c[3]);
+    return __builtin_bit_cast(h8, u4{c[0], c[1], c[2], c[3]});
+}
+
 // LDS reads done (lgkmcnt(0)), then s_barrier, without waiting on vector
 // memory loads.  Written with builtins so the compiler's wait-count tracking
 // sees the lgkmcnt(0); the empty asm with a memory clobber keeps the

@@ -515,6 +515,11 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
     // (graph-replayed, down projections at M = 2: 0.5B 7.35 -> 6.55 us, 1.5B
     // 10.32 -> 9.06 us with the whole ring)
     constexpr int D = (XLDS || MT == 1 || DEPTH < 4 || EARLY) ? DEPTH : DEPTH / 2;
+    // MF (3-4 activation rows): the dot products on MFMA (16 rows x 16
+    // columns, M of them used, 32 codes per instruction) instead of v_dot2:
+    // the step's weights go through the wave's LDS tile into the MFMA
+    // operand layout, the activations are loaded as MFMA operands
+    constexpr bool MF = MT == 4;
     DotRed& red = *reinterpret_cast<DotRed*>(smem);
     f16* xs = reinterpret_cast<f16*>(smem + kDotRedBytes);
     const DecodeCoord c = dot_coord(a, block);
@@ -545,6 +550,11 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
     const int32_t s1 = (int32_t)c.s1;
     const int64_t ldx = a.K + 8;
     const f16* xg = static_cast<const f16*>(a.inp);
+    // MF: lane l is MFMA row / column fi = l % 16 and k group fg = l / 16;
+    // its activation row (clamped: columns past M are computed and unused)
+    const int fi = c.lane & 15, fg = c.lane >> 4;
+    const int32_t fm = fi < a.M ? fi : 0;
+    char* wt = smem + kDotRedBytes + (XLDS ? a.M * ldx * 2 : 0) + c.wave * (16 * kDotWtPitch);
 
     // Ring of D slots, one k step each: the two weight chunks of the step
     // and, when the activations are not in LDS, their activation chunks
@@ -552,7 +562,7 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
     // load).  Slot u is consumed, then refilled with the step D ahead.
     struct Slot {
         u4 w[2];
-        h8 x[XLDS ? 1 : MT][2];
+        h8 x[XLDS ? 1 : (MF ? 4 : MT)][MF ? 1 : 2];  // MF: the step's 4 operand fragments
     };
     Slot ring[D];
     auto issue = [&](int u, int32_t st) {
@@ -562,7 +572,14 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
         k = k < kmax ? k : kmax;
         ring[u].w[0] = ld_stream_g(wpA + k);
         ring[u].w[1] = ld_stream_g(wpB + k);
-        if (!XLDS) {
+        if (!XLDS && MF) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                int32_t kx = st * kDotStep + 32 * j + 8 * fg;
+                kx = kx < (int32_t)a.K - 8 ? kx : (int32_t)a.K - 8;
+                ring[u].x[j][0] = *gbl(reinterpret_cast<const h8*>(xg + fm * a.K + kx));
+            }
+        } else if (!XLDS) {
 #pragma unroll
             for (int m = 0; m < MT; m++) {
                 const f16* xp = xg + (m < a.M ? m : 0) * a.K + k;
@@ -571,6 +588,7 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
             }
         }
     };
+    f4 facc = {0.0f, 0.0f, 0.0f, 0.0f};  // MF: rows 4 fg .. 4 fg + 3, column fi
     float accA[MT], accB[MT];
 #pragma unroll
     for (int m = 0; m < MT; m++) accA[m] = accB[m] = 0.0f;
@@ -580,6 +598,32 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
     // clamped into the row and masked instead.
     const h8 zero8 = {};
     auto consume = [&](int u, int32_t st) {
+        if constexpr (MF) {
+            // the wave's 16 rows x 128 codes: lane (r, ch) holds codes
+            // 16 ch .. 16 ch + 15 of rows r and 8 + r; one wave's LDS
+            // accesses complete in order, so the reads below see these
+            // writes and the next step's writes follow these reads
+            *reinterpret_cast<u4*>(wt + r * kDotWtPitch + 16 * ch) = ring[u].w[0];
+            *reinterpret_cast<u4*>(wt + (8 + r) * kDotWtPitch + 16 * ch) = ring[u].w[1];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                // codes 32 j + 8 fg .. + 7 of row fi against the same k of activation row fi
+                const int32_t kx = st * kDotStep + 32 * j + 8 * fg;
+                typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+                const u2v cw = *reinterpret_cast<const u2v*>(wt + fi * kDotWtPitch + 32 * j + 8 * fg);
+                const h8 af = i8x8_to_h8(cw[0], cw[1]);
+                h8 bf;
+                if (XLDS) {
+                    const int32_t kc = kx < (int32_t)a.K - 8 ? kx : (int32_t)a.K - 8;
+                    bf = *reinterpret_cast<const h8*>(xs + fm * ldx + kc);
+                } else {
+                    bf = ring[u].x[j][0];
+                }
+                bf = kx < (int32_t)a.K ? bf : zero8;  // past K: the clamped codes meet zeros
+                facc = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf, facc, 0, 0, 0);
+            }
+            return;
+        }
         int32_t k = st * kDotStep + ch * 16;
         const bool kv = k < a.K;
         k = k < kmax ? k : kmax;
@@ -832,16 +876,41 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
             if (s + u < s1) consume(u, s + u);
         }
     }
-    // sum the 8 chunk lanes of each row
+    if constexpr (MF) {
+        // the MFMA tile (rows 4 fg + q of column fi) into the reduction
+        // scratch, then every lane takes its rows r and 8 + r back, the
+        // ksplit waves of its tile added in wave order
+        if (fi < MT) {
 #pragma unroll
-    for (int m = 0; m < MT; m++) {
+            for (int q = 0; q < 4; q++) red.v[c.wave][fi][4 * fg + q] = facc[q];
+        }
+        __syncthreads();
+        const int w0 = c.ks == 0 ? c.wave : c.wave - c.ks;
 #pragma unroll
-        for (int off = 1; off < 8; off <<= 1) {
-            accA[m] += __shfl_xor(accA[m], off);
-            accB[m] += __shfl_xor(accB[m], off);
+        for (int m = 0; m < MT; m++) {
+            accA[m] = red.v[w0][m][r];
+            accB[m] = red.v[w0][m][8 + r];
+        }
+        for (int j = 1; j < c.ksplit; j++) {
+#pragma unroll
+            for (int m = 0; m < MT; m++) {
+                accA[m] += red.v[w0 + j][m][r];
+                accB[m] += red.v[w0 + j][m][8 + r];
+            }
         }
     }
-    if (c.ksplit > 1) {
+    // sum the 8 chunk lanes of each row
+    if constexpr (!MF) {
+#pragma unroll
+        for (int m = 0; m < MT; m++) {
+#pragma unroll
+            for (int off = 1; off < 8; off <<= 1) {
+                accA[m] += __shfl_xor(accA[m], off);
+                accB[m] += __shfl_xor(accB[m], off);
+            }
+        }
+    }
+    if (!MF && c.ksplit > 1) {
         if (ch == 0) {
 #pragma unroll
             for (int m = 0; m < MT; m++) {
@@ -1517,7 +1586,7 @@ int launch_dot(const LinArgs& a, int out, bool early, int depth, void* stream)
     // early launches without an input stage load the activations with the
     // weights (see dot_early)
     const bool xl = dot_x_in_lds(a.M, a.K) && (a.xop != 0 || !early);
-    const size_t lds = xl ? dot_lds_bytes(a.M, a.K) : (size_t)kDotRedBytes;
+    const size_t lds = (xl ? dot_lds_bytes(a.M, a.K) : (size_t)kDotRedBytes) + (a.M > 2 ? kDotWtBytes : 0);
     if (a.M <= 1) {
         if (xl) dot_launch_e<1, true>(a, out, early, depth, grid, lds, S(stream));
         else dot_launch_e<1, false>(a, out, early, depth, grid, lds, S(stream));
@@ -1574,6 +1643,7 @@ int launch_dot_grouped(const LinArgs* dev_table, const int32_t* dev_block_prob, 
 {
     const dim3 grid((unsigned)total_blocks);
     hipStream_t s = S(stream);
+    if (max_m > 2) lds_bytes += kDotWtBytes;  // the MFMA path's code tiles
     DotGroupArgs k{};
     k.count = count;
     k.pos = pos;
