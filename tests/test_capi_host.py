@@ -164,7 +164,8 @@ def test_dispatch_choice():
         assert ch(2, 151936, 896, capi.F16, capi.F32) == "dot"        # M = 2, 9496 tiles
         assert ch(4, 896, 896, capi.F16, capi.F16) == "dot"           # M = 3, 4 on few tiles
         assert ch(4, 1536, 8960, capi.F16, capi.F16) == "dot"
-        assert ch(3, 9728, 896, capi.F16, capi.F16) == "skinny"       # M = 3, 608 tiles
+        assert ch(3, 9728, 896, capi.F16, capi.F16) == "dot"          # M = 3, 608 tiles
+        assert ch(3, 17920, 1536, capi.F16, capi.F16) == "skinny"     # M = 3, 1120 tiles
         assert ch(5, 1536, 8960, capi.F16, capi.F16) == "gemm"        # long rows, few tiles: split-K GEMM
         assert ch(8, 896, 4864, capi.F16, capi.F16) == "gemm"         # long rows, few tiles: split-K GEMM
         assert ch(8, 4864, 896, capi.F16, capi.F16) == "skinny"       # M <= 8

@@ -219,7 +219,8 @@ def test_decode_dispatch_on_device(gpu):
     assert capi.kernel_choice(2, 896, 896, F16, F16) == "dot"
     assert capi.kernel_choice(4, 896, 896, F16, F16) == "dot"
     assert capi.kernel_choice(4, 1536, 8960, F16, F16) == "dot"
-    assert capi.kernel_choice(4, 9728, 896, F16, F16) == "skinny"
+    assert capi.kernel_choice(4, 9728, 896, F16, F16) == "dot"
+    assert capi.kernel_choice(4, 17920, 1536, F16, F16) == "skinny"
     assert capi.kernel_choice(5, 1536, 8960, F16, F16) == "gemm"
     assert capi.kernel_choice(5, 151936, 896, F16, F16) == "skinny"
     assert capi.kernel_choice(16, 4864, 896, F16, F16) == "gemm"
@@ -408,11 +409,11 @@ def test_dot_plan_single_launch(gpu, oracle, outd):
 
 def test_dot_plan_several_rows(gpu, oracle):
     """k_dot_grouped with up to 4 activation rows (automatic dispatch takes
-    k_dot for M <= 4 on few tiles); one problem of M = 3 on 304 tiles takes
-    k_skinny, and with it the whole plan runs on k_skinny_grouped."""
+    k_dot for M <= 4 below 1024 tiles); one problem of M = 3 on 1120 tiles
+    takes k_skinny, and with it the whole plan runs on k_skinny_grouped."""
     assert _plan_case(oracle, DOT_PLAN_M4, F16, capi.KERNEL_DOT, seed=550, expect="dot") == 1
     assert _plan_case(oracle, DOT_PLAN_M4, F16, capi.KERNEL_AUTO, seed=551, expect="dot") == 1
-    specs = DOT_PLAN_M4 + [(3, 4864, 896, False, None)]
+    specs = DOT_PLAN_M4 + [(3, 17920, 1536, False, None)]
     assert _plan_case(oracle, specs, F16, capi.KERNEL_AUTO, seed=552, expect="skinny") == 1
 
 

@@ -360,14 +360,21 @@ constexpr std::size_t kGemmF32MinM = 32;
 //                          gemm 13.78 14.30 14.20 13.87 14.40 14.43
 //   1.5B down 1536 x 8960  dot 7.48 10.40 12.26 12.41, skinny 16.27 .. 22.82, gemm 12.8 .. 13.2
 //   151936 x 896           dot 28.3 (M = 2) 34.1 (3), skinny 33.2 35.1 38.6 (8) 63.1 (16), gemm 54-56
-// k_dot at M <= 2, and at M <= 4 below 256 tiles; k_skinny otherwise up to
+// With k_dot's MFMA path for 3-4 rows (same graph replay), M = 3 / 4:
+//   gate 4864 x 896 (304 tiles)          dot 4.22 4.36, skinny 5.59 5.87
+//   gate_up 9728 x 896 (608 tiles)       dot 5.48 5.67, skinny 6.35 6.65
+//   1.5B q/k/v 2048 x 1536 (128 tiles)   dot 4.18 4.34, skinny 5.82 6.06
+//   1.5B gate_up 17920 x 1536 (1120)     dot 12.35 12.87, skinny 11.90 12.23
+//   151936 x 896 (9496 tiles)            dot 38.6 40.2, skinny 34.9 35.8
+// k_dot at M <= 2, and at M <= 4 below 1024 tiles; k_skinny otherwise up to
 // M = 8 (and beyond on few tiles with short rows), except rows of at least
 // kLongK codes on few tiles, where the split-K GEMM wins (0.5B down at M = 6:
 // 11.1 against 11.7 us); from M = 9 the GEMM on many tiles or long rows.  k_stream lost to k_skinny by 1.7-3.5x at every
 // M and shape of the sweep (e.g. 151936 x 896: 58-78 us), so it runs only
 // when forced.
 constexpr std::size_t kDotAutoMaxM = 2;
-constexpr int64_t kDotFewTiles = 256;    // M = 3, 4: k_dot below this many 16-row tiles
+constexpr int64_t kDotFewTiles = 256;    // M > 8: the GEMM from this many 16-row tiles
+constexpr int64_t kDotMfTiles = 1024;    // M = 3, 4: k_dot (its MFMA path) below this many tiles
 constexpr int64_t kLongK = 4096;         // M >= 5 (k_dot takes M <= 4 on few tiles)
 constexpr int64_t kLongKMaxTiles = 128;  // 16-row tiles: N <= 2048
 constexpr std::size_t kSkinnyAutoMaxM = 8;
@@ -377,7 +384,7 @@ int natural_kernel(std::size_t M, std::size_t N, std::size_t K, int act)
 {
     if (act == VVH_F32) return (M >= kGemmF32MinM && K % kGemmBK == 0) ? K_GEMM : K_GEMV_F32;
     const int64_t tiles = ((int64_t)N + kDecodeTileN - 1) / kDecodeTileN;
-    if ((M <= kDotAutoMaxM || (M <= (std::size_t)kDotMaxM && tiles < kDotFewTiles)) &&
+    if ((M <= kDotAutoMaxM || (M <= (std::size_t)kDotMaxM && tiles < kDotMfTiles)) &&
         dot_fits((int64_t)N, (int64_t)K))
         return K_DOT;
     if (M > (std::size_t)kSkinnyMaxM) return K_GEMM;
