@@ -166,9 +166,11 @@ def test_dispatch_choice():
         assert ch(4, 1536, 8960, capi.F16, capi.F16) == "dot"
         assert ch(3, 9728, 896, capi.F16, capi.F16) == "dot"          # M = 3, 608 tiles
         assert ch(3, 17920, 1536, capi.F16, capi.F16) == "skinny"     # M = 3, 1120 tiles
-        assert ch(5, 1536, 8960, capi.F16, capi.F16) == "gemm"        # long rows, few tiles: split-K GEMM
-        assert ch(8, 896, 4864, capi.F16, capi.F16) == "gemm"         # long rows, few tiles: split-K GEMM
-        assert ch(8, 4864, 896, capi.F16, capi.F16) == "skinny"       # M <= 8
+        assert ch(5, 1536, 8960, capi.F16, capi.F16) == "dot"         # M = 5..8 below 1024 tiles
+        assert ch(8, 896, 4864, capi.F16, capi.F16) == "dot"
+        assert ch(8, 4864, 896, capi.F16, capi.F16) == "dot"
+        assert ch(8, 17920, 1536, capi.F16, capi.F16) == "skinny"     # M <= 8 on 1120 tiles
+        assert ch(9, 1536, 8960, capi.F16, capi.F16) == "gemm"        # long rows, few tiles: split-K GEMM
         assert ch(5, 151936, 896, capi.F16, capi.F32) == "skinny"     # streaming only when forced
         assert ch(16, 4864, 896, capi.F16, capi.F16) == "gemm"        # M > 8 on 304 tiles
         assert ch(16, 896, 4864, capi.F16, capi.F16) == "gemm"        # M > 8 on long rows
@@ -185,7 +187,8 @@ def test_dispatch_choice():
         assert ch(64, 896, 896, capi.F16, capi.F16) == "generic"      # M > 16
         capi.set_kernel(capi.KERNEL_DOT)
         assert ch(1, 16, 16, capi.F16, capi.F16) == "dot"
-        assert ch(5, 16, 16, capi.F16, capi.F16) == "generic"         # M > 4
+        assert ch(8, 16, 16, capi.F16, capi.F16) == "dot"
+        assert ch(9, 16, 16, capi.F16, capi.F16) == "generic"         # M > 8
         assert ch(1, 16, 16, capi.F32, capi.F32) == "generic"         # fp32 activations
         capi.set_kernel(capi.KERNEL_STREAM)
         assert ch(1, 16, 512, capi.F16, capi.F16) == "stream"

@@ -201,14 +201,15 @@ def test_stream_kernel(gpu, oracle, M, N, K, outd):
              kernel=capi.KERNEL_STREAM, seed=11 * M + K)
 
 
-@pytest.mark.parametrize("M", [1, 2, 3, 4])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8])
 @pytest.mark.parametrize("outd", [F16, F32])
 @pytest.mark.parametrize("N,K", [(1, 16), (17, 48), (128, 896), (896, 4864), (300, 1040), (4099, 592),
                                  (64, 20480), (33, 8960), (48, 2048)])
 def test_dot_kernel(gpu, oracle, M, N, K, outd):
-    """VALU dot-product decode (M <= 4): K tails (48, 592, 1040), a single
-    16-code step, N % 16 != 0, activations too large for LDS (K = 20480 at
-    M >= 2) and the ksplit reduction (few tiles)."""
+    """Dot-product decode (v_dot2 for M <= 2, MFMA for 3 <= M <= 8): K tails
+    (48, 592, 1040), a single 16-code step, N % 16 != 0, activations too
+    large for LDS (K = 20480 at M >= 2) and the ksplit reduction (few
+    tiles)."""
     run_case(oracle, M, N, K, F16, outd, bias=bool(N % 2), res=["sep", "inplace", None][(N + K + M) % 3],
              kernel=capi.KERNEL_DOT, seed=13 * N + K + M)
 
@@ -221,7 +222,10 @@ def test_decode_dispatch_on_device(gpu):
     assert capi.kernel_choice(4, 1536, 8960, F16, F16) == "dot"
     assert capi.kernel_choice(4, 9728, 896, F16, F16) == "dot"
     assert capi.kernel_choice(4, 17920, 1536, F16, F16) == "skinny"
-    assert capi.kernel_choice(5, 1536, 8960, F16, F16) == "gemm"
+    assert capi.kernel_choice(5, 1536, 8960, F16, F16) == "dot"
+    assert capi.kernel_choice(8, 896, 4864, F16, F16) == "dot"
+    assert capi.kernel_choice(8, 17920, 1536, F16, F16) == "skinny"
+    assert capi.kernel_choice(9, 1536, 8960, F16, F16) == "gemm"
     assert capi.kernel_choice(5, 151936, 896, F16, F16) == "skinny"
     assert capi.kernel_choice(16, 4864, 896, F16, F16) == "gemm"
 
@@ -400,6 +404,8 @@ DOT_PLAN = [(1, 896, 896, True, None), (1, 128, 896, True, None), (1, 130, 592, 
             (1, 4864, 896, False, None), (1, 1, 512, True, "sep")]
 DOT_PLAN_M4 = [(4, 896, 896, True, None), (2, 128, 896, True, "sep"), (3, 300, 1040, False, "inplace"),
                (1, 896, 4864, False, "inplace"), (4, 17, 48, True, None)]
+DOT_PLAN_M8 = [(8, 896, 896, True, None), (5, 128, 896, True, "sep"), (7, 300, 1040, False, "inplace"),
+               (6, 896, 4864, False, "inplace"), (1, 17, 48, True, None), (3, 130, 592, True, "sep")]
 
 
 @pytest.mark.parametrize("outd", [F16, F32])
@@ -409,12 +415,20 @@ def test_dot_plan_single_launch(gpu, oracle, outd):
 
 def test_dot_plan_several_rows(gpu, oracle):
     """k_dot_grouped with up to 4 activation rows (automatic dispatch takes
-    k_dot for M <= 4 below 1024 tiles); one problem of M = 3 on 1120 tiles
+    k_dot for M <= 8 below 1024 tiles); one problem of M = 3 on 1120 tiles
     takes k_skinny, and with it the whole plan runs on k_skinny_grouped."""
     assert _plan_case(oracle, DOT_PLAN_M4, F16, capi.KERNEL_DOT, seed=550, expect="dot") == 1
     assert _plan_case(oracle, DOT_PLAN_M4, F16, capi.KERNEL_AUTO, seed=551, expect="dot") == 1
     specs = DOT_PLAN_M4 + [(3, 17920, 1536, False, None)]
     assert _plan_case(oracle, specs, F16, capi.KERNEL_AUTO, seed=552, expect="skinny") == 1
+
+
+@pytest.mark.parametrize("outd", [F16, F32])
+def test_dot_plan_up_to_eight_rows(gpu, oracle, outd):
+    """k_dot_grouped with 5-8 activation rows in one launch (the MFMA path
+    with 16 x 16 operand tiles, 8 of their rows used), mixed with plans of
+    fewer rows, K tails and a long-row problem."""
+    assert _plan_case(oracle, DOT_PLAN_M8, outd, capi.KERNEL_AUTO, seed=560, expect="dot") == 1
 
 
 def test_dot_plan_without_lds_activations(gpu, oracle):
@@ -426,11 +440,13 @@ def test_dot_plan_without_lds_activations(gpu, oracle):
 
 def test_plan_with_short_rows_is_not_streamed(gpu, oracle):
     """K = 256 (4 k steps) cannot fill the streaming pipeline.  Automatic
-    dispatch runs such a plan as one k_skinny_grouped launch; with the
-    streaming family forced, the short problem falls back to the generic
-    kernel and the plan runs one launch per problem."""
+    dispatch runs such a plan as one k_dot_grouped launch (k_skinny_grouped
+    when that family is forced); with the streaming family forced, the short
+    problem falls back to the generic kernel and the plan runs one launch per
+    problem."""
     specs = [(5, 896, 256, True, None), (1, 4864, 896, False, None)]
-    assert _plan_case(oracle, specs, F16, capi.KERNEL_AUTO, seed=400, expect="skinny") == 1
+    assert _plan_case(oracle, specs, F16, capi.KERNEL_AUTO, seed=400, expect="dot") == 1
+    assert _plan_case(oracle, specs, F16, capi.KERNEL_SKINNY, seed=400, expect="skinny") == 1
     assert _plan_case(oracle, specs, F16, capi.KERNEL_STREAM, seed=400, expect="auto") == 2
 
 

@@ -344,16 +344,18 @@ __global__ __launch_bounds__(256) void k_skinny_grouped(const LinArgs* __restric
 }
 
 // ---------------------------------------------------------------------------
-// k_dot: fp16 activations, M <= 4, VALU dot products.
+// k_dot: fp16 activations, M <= 8; dot products on VALU (M <= 2) or MFMA
+// (M = 3..8, see MF below).
 //
 // The weight stream decides the speed of a decode GEMV, and it runs fastest
 // when every load instruction covers whole 128-byte cache lines: 8 rows x
 // 128 B per instruction streams about 7 TB/s on MI355X, the 16 rows x 64 B
-// that a 16x16 MFMA operand needs about 5.5 TB/s.  So at M <= 4, where the
+// that a 16x16 MFMA operand needs about 5.5 TB/s.  So at M <= 8, where the
 // MFMA's M side would be mostly empty anyway, each wave owns a 16-row tile
 // and lane l reads the 16-byte chunk c = l%8 of the 128-byte k step of rows
 // r = l/8 and r + 8 (two loads per step), converts the codes exactly to fp16
-// and accumulates v_dot2_f32_f16 products in fp32.  The 8 lanes of a row are
+// and (M <= 2) accumulates v_dot2_f32_f16 products in fp32; with more rows
+// the loaded tile is regathered through LDS into MFMA operands instead.  The 8 lanes of a row are
 // summed with a butterfly at the end.  Activations are staged once per
 // block in LDS (a broadcast read: the 8 rows of a wave read the same 8
 // chunks), or read through the caches when they do not fit.
@@ -389,7 +391,7 @@ __device__ __forceinline__ DecodeCoord dot_coord(const LinArgs& a, int64_t block
 // stride of K + 8 halves.  The launcher sizes the dynamic LDS with the same
 // rule (dot_lds_bytes), so kernel and launcher agree on where x lives.
 struct DotRed {
-    float v[4][4][16];  // [wave][m][row]
+    float v[4][kDotMaxM][16];  // [wave][m][row]
 };
 static_assert(sizeof(DotRed) == kDotRedBytes, "reduction scratch size");
 
@@ -515,11 +517,11 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
     // (graph-replayed, down projections at M = 2: 0.5B 7.35 -> 6.55 us, 1.5B
     // 10.32 -> 9.06 us with the whole ring)
     constexpr int D = (XLDS || MT == 1 || DEPTH < 4 || EARLY) ? DEPTH : DEPTH / 2;
-    // MF (3-4 activation rows): the dot products on MFMA (16 rows x 16
+    // MF (3-8 activation rows): the dot products on MFMA (16 rows x 16
     // columns, M of them used, 32 codes per instruction) instead of v_dot2:
     // the step's weights go through the wave's LDS tile into the MFMA
     // operand layout, the activations are loaded as MFMA operands
-    constexpr bool MF = MT == 4;
+    constexpr bool MF = MT >= 4;
     DotRed& red = *reinterpret_cast<DotRed*>(smem);
     f16* xs = reinterpret_cast<f16*>(smem + kDotRedBytes);
     const DecodeCoord c = dot_coord(a, block);
@@ -681,7 +683,7 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
     // block reduction and the normalization run while the weights are in
     // flight (the in-order wait counter lets a wait for the rows leave the
     // younger ring loads outstanding)
-    const bool rms_first = EARLY && XLDS && a.xop == 1 && a.K <= 256 * 8;
+    const bool rms_first = EARLY && XLDS && MT <= 4 && a.xop == 1 && a.K <= 256 * 8;
     if constexpr (EARLY) {
         const float* bp = a.bias ? a.bias : a.scales;  // absent bias / residual: in-bounds reads, unused
         const OT* rp = a.res ? static_cast<const OT*>(a.res) : reinterpret_cast<const OT*>(a.scales);
@@ -700,79 +702,82 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
         }
         if (!rms_first) rope_prep();
     }
-    if (XLDS && rms_first) {
-        const int32_t K32 = (int32_t)a.K, xchunks = (int32_t)(a.M * a.K / 8);
-        // M <= MT rows of K <= 2048: at most MT chunks of 8 per thread
-        constexpr int XL = MT;
-        f16 raw[MT][8];
-        h8 xr[XL];
-        f4 w0[XL], w1[XL];
-#pragma unroll
-        for (int m = 0; m < MT; m++) {
-            const f16* xrow = xg + (m < a.M ? m : 0) * a.K;
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const int32_t i = (int32_t)threadIdx.x + 256 * j;
-                raw[m][j] = *gbl(xrow + (i < K32 ? i : K32 - 1));
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < XL; i++) {
-            int32_t idx = (int32_t)threadIdx.x + 256 * i;
-            idx = idx < xchunks ? idx : xchunks - 1;
-            const int32_t row = idx * 8 / K32, col = idx * 8 - row * K32;
-            xr[i] = *gbl(reinterpret_cast<const h8*>(xg + row * a.K + col));
-            w0[i] = *gbl(reinterpret_cast<const f4*>(a.xw + col));
-            w1[i] = *gbl(reinterpret_cast<const f4*>(a.xw + col + 4));
-        }
-        // keep every row load ahead of the ring in issue order, and issue the
-        // ring in every wave (an inactive wave's slots read clamped, in-bounds
-        // rows and steps, unused): a wait for a row value then always counts
-        // exactly the ring's loads as younger
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int u = 0; u < D; u++) issue(u, (int32_t)c.s0 + u);
-        __builtin_amdgcn_sched_barrier(0);
-        rope_prep();
-        // per row as k_rms_norm: thread t sums x[t], x[t + 256], ... in order
-        // (slots past the row add an exact 0), then the same block reduction
-        float* red4 = &red.v[0][0][0];
-        float rinv[MT];
-#pragma unroll
-        for (int m = 0; m < MT; m++) {
-            rinv[m] = 1.0f;
-            if (m < a.M) {
-                float v[8];
-#pragma unroll
+    if constexpr (XLDS && MT <= 4) {
+        if (rms_first) {
+            const int32_t K32 = (int32_t)a.K, xchunks = (int32_t)(a.M * a.K / 8);
+            // M <= MT rows of K <= 2048: at most MT chunks of 8 per thread
+            constexpr int XL = MT;
+            f16 raw[MT][8];
+            h8 xr[XL];
+            f4 w0[XL], w1[XL];
+    #pragma unroll
+            for (int m = 0; m < MT; m++) {
+                const f16* xrow = xg + (m < a.M ? m : 0) * a.K;
+    #pragma unroll
                 for (int j = 0; j < 8; j++) {
                     const int32_t i = (int32_t)threadIdx.x + 256 * j;
-                    v[j] = i < K32 ? (float)raw[m][j] : 0.0f;
+                    raw[m][j] = *gbl(xrow + (i < K32 ? i : K32 - 1));
                 }
-                float ss = 0.0f;
-#pragma unroll
-                for (int j = 0; j < 8; j++) ss += v[j] * v[j];
-                ss = block_sum256(ss, red4);
-                rinv[m] = rms_of(ss, a.K, a.xeps);
             }
-        }
-#pragma unroll
-        for (int i = 0; i < XL; i++) {
-            const int32_t idx = (int32_t)threadIdx.x + 256 * i;
-            if (idx >= xchunks) continue;
-            const int32_t row = idx * 8 / K32, col = idx * 8 - row * K32;
-            float rv = rinv[0];
-#pragma unroll
-            for (int m = 1; m < MT; m++) rv = row == m ? rinv[m] : rv;
-            h8 v;
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                v[j] = (f16)rms_apply((float)xr[i][j], rv, w0[i][j]);
-                v[4 + j] = (f16)rms_apply((float)xr[i][4 + j], rv, w1[i][j]);
+    #pragma unroll
+            for (int i = 0; i < XL; i++) {
+                int32_t idx = (int32_t)threadIdx.x + 256 * i;
+                idx = idx < xchunks ? idx : xchunks - 1;
+                const int32_t row = idx * 8 / K32, col = idx * 8 - row * K32;
+                xr[i] = *gbl(reinterpret_cast<const h8*>(xg + row * a.K + col));
+                w0[i] = *gbl(reinterpret_cast<const f4*>(a.xw + col));
+                w1[i] = *gbl(reinterpret_cast<const f4*>(a.xw + col + 4));
             }
-            *reinterpret_cast<h8*>(xs + row * ldx + col) = v;
+            // keep every row load ahead of the ring in issue order, and issue the
+            // ring in every wave (an inactive wave's slots read clamped, in-bounds
+            // rows and steps, unused): a wait for a row value then always counts
+            // exactly the ring's loads as younger
+            __builtin_amdgcn_sched_barrier(0);
+    #pragma unroll
+            for (int u = 0; u < D; u++) issue(u, (int32_t)c.s0 + u);
+            __builtin_amdgcn_sched_barrier(0);
+            rope_prep();
+            // per row as k_rms_norm: thread t sums x[t], x[t + 256], ... in order
+            // (slots past the row add an exact 0), then the same block reduction
+            float* red4 = &red.v[0][0][0];
+            float rinv[MT];
+    #pragma unroll
+            for (int m = 0; m < MT; m++) {
+                rinv[m] = 1.0f;
+                if (m < a.M) {
+                    float v[8];
+    #pragma unroll
+                    for (int j = 0; j < 8; j++) {
+                        const int32_t i = (int32_t)threadIdx.x + 256 * j;
+                        v[j] = i < K32 ? (float)raw[m][j] : 0.0f;
+                    }
+                    float ss = 0.0f;
+    #pragma unroll
+                    for (int j = 0; j < 8; j++) ss += v[j] * v[j];
+                    ss = block_sum256(ss, red4);
+                    rinv[m] = rms_of(ss, a.K, a.xeps);
+                }
+            }
+    #pragma unroll
+            for (int i = 0; i < XL; i++) {
+                const int32_t idx = (int32_t)threadIdx.x + 256 * i;
+                if (idx >= xchunks) continue;
+                const int32_t row = idx * 8 / K32, col = idx * 8 - row * K32;
+                float rv = rinv[0];
+    #pragma unroll
+                for (int m = 1; m < MT; m++) rv = row == m ? rinv[m] : rv;
+                h8 v;
+    #pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    v[j] = (f16)rms_apply((float)xr[i][j], rv, w0[i][j]);
+                    v[4 + j] = (f16)rms_apply((float)xr[i][4 + j], rv, w1[i][j]);
+                }
+                *reinterpret_cast<h8*>(xs + row * ldx + col) = v;
+            }
+            __syncthreads();
         }
-        __syncthreads();
-    } else if (XLDS) {
+    }
+    if (XLDS && !rms_first) {
         // activations to LDS (through the input stage a.xop), 4 chunks of 8
         // values per thread per round; a round's loads are clamped into the
         // input and its stores masked, so all of them are in flight at once
@@ -1593,9 +1598,12 @@ int launch_dot(const LinArgs& a, int out, bool early, int depth, void* stream)
     } else if (a.M <= 2) {
         if (xl) dot_launch_e<2, true>(a, out, early, depth, grid, lds, S(stream));
         else dot_launch_e<2, false>(a, out, early, depth, grid, lds, S(stream));
-    } else {
+    } else if (a.M <= 4) {
         if (xl) dot_launch_e<4, true>(a, out, early, depth, grid, lds, S(stream));
         else dot_launch_e<4, false>(a, out, early, depth, grid, lds, S(stream));
+    } else {
+        if (xl) dot_launch_e<8, true>(a, out, early, depth, grid, lds, S(stream));
+        else dot_launch_e<8, false>(a, out, early, depth, grid, lds, S(stream));
     }
     return (int)hipGetLastError();
 }
@@ -1661,9 +1669,12 @@ int launch_dot_grouped(const LinArgs* dev_table, const int32_t* dev_block_prob, 
     } else if (max_m <= 2) {
         if (x_in_lds) dot_grouped_launch_e<2, true>(k, out, early, depth, grid, lds_bytes, s);
         else dot_grouped_launch_e<2, false>(k, out, early, depth, grid, lds_bytes, s);
-    } else {
+    } else if (max_m <= 4) {
         if (x_in_lds) dot_grouped_launch_e<4, true>(k, out, early, depth, grid, lds_bytes, s);
         else dot_grouped_launch_e<4, false>(k, out, early, depth, grid, lds_bytes, s);
+    } else {
+        if (x_in_lds) dot_grouped_launch_e<8, true>(k, out, early, depth, grid, lds_bytes, s);
+        else dot_grouped_launch_e<8, false>(k, out, early, depth, grid, lds_bytes, s);
     }
     return (int)hipGetLastError();
 }

@@ -366,16 +366,23 @@ constexpr std::size_t kGemmF32MinM = 32;
 //   1.5B q/k/v 2048 x 1536 (128 tiles)   dot 4.18 4.34, skinny 5.82 6.06
 //   1.5B gate_up 17920 x 1536 (1120)     dot 12.35 12.87, skinny 11.90 12.23
 //   151936 x 896 (9496 tiles)            dot 38.6 40.2, skinny 34.9 35.8
-// k_dot at M <= 2, and at M <= 4 below 1024 tiles; k_skinny otherwise up to
+// and with that path for 5-8 rows (8-row operands), M = 5 / 6 / 8:
+//   o 896 x 896            dot 4.04 4.20 4.49, skinny 5.12 5.11 5.26, gemm 9.4-9.6
+//   gate 4864 x 896        dot 5.15 5.34 5.63, skinny 6.02 6.13 6.28, gemm 10.0
+//   gate_up 9728 x 896     dot 6.12 6.36 6.76, skinny 7.01 6.80 7.28, gemm 10.6
+//   down 896 x 4864        dot 6.91 7.14 7.54, skinny 10.3-10.4, gemm 11.2
+//   1.5B q/o 1536 x 1536   dot 4.80 5.02 5.32, skinny 5.96 5.28 5.31, gemm 9.7
+//   1.5B down 1536 x 8960  dot 9.56 9.80 10.56, skinny 16.6-16.9, gemm 13.0-13.1
+// k_dot at M <= 2, and at M <= 8 below 1024 tiles; k_skinny otherwise up to
 // M = 8 (and beyond on few tiles with short rows), except rows of at least
-// kLongK codes on few tiles, where the split-K GEMM wins (0.5B down at M = 6:
-// 11.1 against 11.7 us); from M = 9 the GEMM on many tiles or long rows.  k_stream lost to k_skinny by 1.7-3.5x at every
+// kLongK codes on few tiles, where the split-K GEMM wins; from M = 9 the
+// GEMM on many tiles or long rows.  k_stream lost to k_skinny by 1.7-3.5x at every
 // M and shape of the sweep (e.g. 151936 x 896: 58-78 us), so it runs only
 // when forced.
 constexpr std::size_t kDotAutoMaxM = 2;
 constexpr int64_t kDotFewTiles = 256;    // M > 8: the GEMM from this many 16-row tiles
-constexpr int64_t kDotMfTiles = 1024;    // M = 3, 4: k_dot (its MFMA path) below this many tiles
-constexpr int64_t kLongK = 4096;         // M >= 5 (k_dot takes M <= 4 on few tiles)
+constexpr int64_t kDotMfTiles = 1024;    // M = 3..8: k_dot (its MFMA path) below this many tiles
+constexpr int64_t kLongK = 4096;         // M >= 9 (k_dot takes M <= 8 on few tiles)
 constexpr int64_t kLongKMaxTiles = 128;  // 16-row tiles: N <= 2048
 constexpr std::size_t kSkinnyAutoMaxM = 8;
 constexpr int64_t kGemmLongRows = 4096;  // M > 8: the GEMM on rows of this many codes
@@ -1196,16 +1203,17 @@ VVH_API int vvh_workspace_release(void* stream)
 }
 
 // The input stage runs in k_dot's activation staging only: fp16 activations,
-// M <= kDotMaxM, K % 16 == 0, aligned operands and the rows in LDS.
+// M <= kStageMaxM, K % 16 == 0, aligned operands and the rows in LDS.
 static int input_op_ok(int in_op, const float* in_w, std::size_t M, std::size_t K, int act)
 {
     if (in_op < VVH_IN_NONE || in_op > VVH_IN_SILU_MUL) return fail(VVH_ERR_INVALID_ARG, "bad input op %d", in_op);
     if (in_op == VVH_IN_NONE) return VVH_OK;
     if (in_op == VVH_IN_RMS_NORM && (!in_w || !aligned16(in_w)))
         return fail(VVH_ERR_INVALID_ARG, "RMSNorm input stage needs 16-byte aligned weights");
-    if (act != VVH_F16 || M == 0 || M > (std::size_t)kDotMaxM || K % 16 != 0 || !dot_x_in_lds((int64_t)M, (int64_t)K))
+    if (act != VVH_F16 || M == 0 || M > (std::size_t)kStageMaxM || K % 16 != 0 ||
+        !dot_x_in_lds((int64_t)M, (int64_t)K))
         return fail(VVH_ERR_UNSUPPORTED, "input stage needs fp16 activations, M <= %d, K %% 16 == 0 and "
-                    "rows that fit the block's LDS (M=%zu, K=%zu)", kDotMaxM, M, K);
+                    "rows that fit the block's LDS (M=%zu, K=%zu)", kStageMaxM, M, K);
     return VVH_OK;
 }
 
