@@ -170,10 +170,15 @@ def test_dispatch_choice():
         assert ch(8, 896, 4864, capi.F16, capi.F16) == "dot"
         assert ch(8, 4864, 896, capi.F16, capi.F16) == "dot"
         assert ch(8, 17920, 1536, capi.F16, capi.F16) == "skinny"     # M <= 8 on 1120 tiles
-        assert ch(9, 1536, 8960, capi.F16, capi.F16) == "gemm"        # long rows, few tiles: split-K GEMM
+        assert ch(9, 1536, 8960, capi.F16, capi.F16) == "dot"         # long rows, few tiles, M <= 12
+        assert ch(12, 896, 4864, capi.F16, capi.F16) == "dot"
+        assert ch(13, 896, 4864, capi.F16, capi.F16) == "gemm"        # long rows, few tiles: split-K GEMM
+        assert ch(9, 8960, 1536, capi.F16, capi.F16) == "skinny"      # M > 8 below 1024 tiles
+        assert ch(16, 17920, 1536, capi.F16, capi.F16) == "gemm"      # M > 8 on 1120 tiles
+        assert ch(16, 4096, 8192, capi.F16, capi.F16) == "gemm"       # M > 8, long rows on 256 tiles
         assert ch(5, 151936, 896, capi.F16, capi.F32) == "skinny"     # streaming only when forced
-        assert ch(16, 4864, 896, capi.F16, capi.F16) == "gemm"        # M > 8 on 304 tiles
-        assert ch(16, 896, 4864, capi.F16, capi.F16) == "gemm"        # M > 8 on long rows
+        assert ch(16, 4864, 896, capi.F16, capi.F16) == "skinny"      # M > 8 on 304 tiles
+        assert ch(16, 896, 4864, capi.F16, capi.F16) == "gemm"        # M > 12 on long rows
         assert ch(16, 1536, 1536, capi.F16, capi.F16) == "skinny"     # M > 8, few tiles, short rows
         assert ch(17, 4864, 896, capi.F16, capi.F16) == "gemm"
         assert ch(512, 4864, 896, capi.F16, capi.F16) == "gemm"       # config 4
@@ -187,8 +192,8 @@ def test_dispatch_choice():
         assert ch(64, 896, 896, capi.F16, capi.F16) == "generic"      # M > 16
         capi.set_kernel(capi.KERNEL_DOT)
         assert ch(1, 16, 16, capi.F16, capi.F16) == "dot"
-        assert ch(8, 16, 16, capi.F16, capi.F16) == "dot"
-        assert ch(9, 16, 16, capi.F16, capi.F16) == "generic"         # M > 8
+        assert ch(16, 16, 16, capi.F16, capi.F16) == "dot"
+        assert ch(17, 16, 16, capi.F16, capi.F16) == "generic"        # M > 16
         assert ch(1, 16, 16, capi.F32, capi.F32) == "generic"         # fp32 activations
         capi.set_kernel(capi.KERNEL_STREAM)
         assert ch(1, 16, 512, capi.F16, capi.F16) == "stream"

@@ -201,12 +201,12 @@ def test_stream_kernel(gpu, oracle, M, N, K, outd):
              kernel=capi.KERNEL_STREAM, seed=11 * M + K)
 
 
-@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8, 12, 16])
 @pytest.mark.parametrize("outd", [F16, F32])
 @pytest.mark.parametrize("N,K", [(1, 16), (17, 48), (128, 896), (896, 4864), (300, 1040), (4099, 592),
                                  (64, 20480), (33, 8960), (48, 2048)])
 def test_dot_kernel(gpu, oracle, M, N, K, outd):
-    """Dot-product decode (v_dot2 for M <= 2, MFMA for 3 <= M <= 8): K tails
+    """Dot-product decode (v_dot2 for M <= 2, MFMA for 3 <= M <= 16): K tails
     (48, 592, 1040), a single 16-code step, N % 16 != 0, activations too
     large for LDS (K = 20480 at M >= 2) and the ksplit reduction (few
     tiles)."""
@@ -225,9 +225,11 @@ def test_decode_dispatch_on_device(gpu):
     assert capi.kernel_choice(5, 1536, 8960, F16, F16) == "dot"
     assert capi.kernel_choice(8, 896, 4864, F16, F16) == "dot"
     assert capi.kernel_choice(8, 17920, 1536, F16, F16) == "skinny"
-    assert capi.kernel_choice(9, 1536, 8960, F16, F16) == "gemm"
+    assert capi.kernel_choice(9, 1536, 8960, F16, F16) == "dot"
+    assert capi.kernel_choice(13, 1536, 8960, F16, F16) == "gemm"
     assert capi.kernel_choice(5, 151936, 896, F16, F16) == "skinny"
-    assert capi.kernel_choice(16, 4864, 896, F16, F16) == "gemm"
+    assert capi.kernel_choice(16, 4864, 896, F16, F16) == "skinny"
+    assert capi.kernel_choice(16, 17920, 1536, F16, F16) == "gemm"
 
 
 def test_misaligned_activations_fall_back(gpu, oracle):
@@ -406,6 +408,8 @@ DOT_PLAN_M4 = [(4, 896, 896, True, None), (2, 128, 896, True, "sep"), (3, 300, 1
                (1, 896, 4864, False, "inplace"), (4, 17, 48, True, None)]
 DOT_PLAN_M8 = [(8, 896, 896, True, None), (5, 128, 896, True, "sep"), (7, 300, 1040, False, "inplace"),
                (6, 896, 4864, False, "inplace"), (1, 17, 48, True, None), (3, 130, 592, True, "sep")]
+DOT_PLAN_M16 = [(16, 896, 896, True, None), (9, 128, 896, True, "sep"), (12, 300, 1040, False, "inplace"),
+                (10, 896, 4864, False, "inplace"), (2, 17, 48, True, None), (16, 64, 20480, True, "sep")]
 
 
 @pytest.mark.parametrize("outd", [F16, F32])
@@ -429,6 +433,14 @@ def test_dot_plan_up_to_eight_rows(gpu, oracle, outd):
     with 16 x 16 operand tiles, 8 of their rows used), mixed with plans of
     fewer rows, K tails and a long-row problem."""
     assert _plan_case(oracle, DOT_PLAN_M8, outd, capi.KERNEL_AUTO, seed=560, expect="dot") == 1
+
+
+@pytest.mark.parametrize("outd", [F16, F32])
+def test_dot_plan_up_to_sixteen_rows(gpu, oracle, outd):
+    """k_dot_grouped forced on problems of up to 16 activation rows (16-row
+    MFMA operands), one of them with activations read through the caches
+    (K = 20480 does not fit the block's LDS at M = 16)."""
+    assert _plan_case(oracle, DOT_PLAN_M16, outd, capi.KERNEL_DOT, seed=570, expect="dot") == 1
 
 
 def test_dot_plan_without_lds_activations(gpu, oracle):

@@ -116,13 +116,13 @@ inline int64_t decode_blocks(const LinArgs& a)
     return (tiles + tiles_per_block - 1) / tiles_per_block;
 }
 
-// k_dot (M <= 8): 16-row tiles, 128-wide k steps, ksplit waves per tile.
-constexpr int64_t kDotMaxM = 8;
+// k_dot (M <= 16): 16-row tiles, 128-wide k steps, ksplit waves per tile.
+constexpr int64_t kDotMaxM = 16;
 constexpr int kStageMaxM = 4;  // rows of a decode linear with an input stage
 constexpr int kDotStep = 128;               // k codes per row per step
 constexpr int64_t kDotLdsMax = 80 * 1024;   // dynamic LDS of one block at most
 constexpr int64_t kDotRedBytes = 4 * kDotMaxM * 16 * 4;
-// k_dot with 3 to 8 activation rows (MT = 4 or 8) takes its dot products on MFMA:
+// k_dot with 3 to 16 activation rows (MT = 4, 8 or 16) takes its dot products on MFMA:
 // each wave passes its step's 16 x 128 code tile through LDS (rows of
 // kDotWtPitch bytes) to gather the MFMA operand fragments
 constexpr int kDotWtPitch = 144;

@@ -344,13 +344,13 @@ __global__ __launch_bounds__(256) void k_skinny_grouped(const LinArgs* __restric
 }
 
 // ---------------------------------------------------------------------------
-// k_dot: fp16 activations, M <= 8; dot products on VALU (M <= 2) or MFMA
-// (M = 3..8, see MF below).
+// k_dot: fp16 activations, M <= 16; dot products on VALU (M <= 2) or MFMA
+// (M = 3..16, see MF below).
 //
 // The weight stream decides the speed of a decode GEMV, and it runs fastest
 // when every load instruction covers whole 128-byte cache lines: 8 rows x
 // 128 B per instruction streams about 7 TB/s on MI355X, the 16 rows x 64 B
-// that a 16x16 MFMA operand needs about 5.5 TB/s.  So at M <= 8, where the
+// that a 16x16 MFMA operand needs about 5.5 TB/s.  So at M <= 16, where the
 // MFMA's M side would be mostly empty anyway, each wave owns a 16-row tile
 // and lane l reads the 16-byte chunk c = l%8 of the 128-byte k step of rows
 // r = l/8 and r + 8 (two loads per step), converts the codes exactly to fp16
@@ -517,7 +517,7 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
     // (graph-replayed, down projections at M = 2: 0.5B 7.35 -> 6.55 us, 1.5B
     // 10.32 -> 9.06 us with the whole ring)
     constexpr int D = (XLDS || MT == 1 || DEPTH < 4 || EARLY) ? DEPTH : DEPTH / 2;
-    // MF (3-8 activation rows): the dot products on MFMA (16 rows x 16
+    // MF (3-16 activation rows): the dot products on MFMA (16 rows x 16
     // columns, M of them used, 32 codes per instruction) instead of v_dot2:
     // the step's weights go through the wave's LDS tile into the MFMA
     // operand layout, the activations are loaded as MFMA operands
@@ -1601,9 +1601,12 @@ int launch_dot(const LinArgs& a, int out, bool early, int depth, void* stream)
     } else if (a.M <= 4) {
         if (xl) dot_launch_e<4, true>(a, out, early, depth, grid, lds, S(stream));
         else dot_launch_e<4, false>(a, out, early, depth, grid, lds, S(stream));
-    } else {
+    } else if (a.M <= 8) {
         if (xl) dot_launch_e<8, true>(a, out, early, depth, grid, lds, S(stream));
         else dot_launch_e<8, false>(a, out, early, depth, grid, lds, S(stream));
+    } else {
+        if (xl) dot_launch_e<16, true>(a, out, early, depth, grid, lds, S(stream));
+        else dot_launch_e<16, false>(a, out, early, depth, grid, lds, S(stream));
     }
     return (int)hipGetLastError();
 }
@@ -1672,9 +1675,12 @@ int launch_dot_grouped(const LinArgs* dev_table, const int32_t* dev_block_prob, 
     } else if (max_m <= 4) {
         if (x_in_lds) dot_grouped_launch_e<4, true>(k, out, early, depth, grid, lds_bytes, s);
         else dot_grouped_launch_e<4, false>(k, out, early, depth, grid, lds_bytes, s);
-    } else {
+    } else if (max_m <= 8) {
         if (x_in_lds) dot_grouped_launch_e<8, true>(k, out, early, depth, grid, lds_bytes, s);
         else dot_grouped_launch_e<8, false>(k, out, early, depth, grid, lds_bytes, s);
+    } else {
+        if (x_in_lds) dot_grouped_launch_e<16, true>(k, out, early, depth, grid, lds_bytes, s);
+        else dot_grouped_launch_e<16, false>(k, out, early, depth, grid, lds_bytes, s);
     }
     return (int)hipGetLastError();
 }

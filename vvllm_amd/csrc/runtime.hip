@@ -373,31 +373,48 @@ constexpr std::size_t kGemmF32MinM = 32;
 //   down 896 x 4864        dot 6.91 7.14 7.54, skinny 10.3-10.4, gemm 11.2
 //   1.5B q/o 1536 x 1536   dot 4.80 5.02 5.32, skinny 5.96 5.28 5.31, gemm 9.7
 //   1.5B down 1536 x 8960  dot 9.56 9.80 10.56, skinny 16.6-16.9, gemm 13.0-13.1
-// k_dot at M <= 2, and at M <= 8 below 1024 tiles; k_skinny otherwise up to
-// M = 8 (and beyond on few tiles with short rows), except rows of at least
-// kLongK codes on few tiles, where the split-K GEMM wins; from M = 9 the
-// GEMM on many tiles or long rows.  k_stream lost to k_skinny by 1.7-3.5x at every
-// M and shape of the sweep (e.g. 151936 x 896: 58-78 us), so it runs only
-// when forced.
+// and at M = 8 / 9 / 12 / 16 (k_dot's 16-row operands from M = 9):
+//   o 896 x 896                  dot 4.53 5.83 6.29 6.94, skinny 5.25 5.33 4.57 4.67, gemm 9.6-9.8
+//   gate 4864 x 896 (304 tiles)  dot 5.69 6.98 7.55 8.37, skinny 6.22 6.34 5.91 6.23, gemm 10.1-10.2
+//   gate_up 9728 x 896 (608)     dot 6.84 8.05 8.70 9.66, skinny 7.31 7.37 7.26 7.61, gemm 10.65 10.7 10.78 8.10
+//   down 896 x 4864 (56)         dot 7.61 8.56 9.46 10.77, skinny 10.4-11.1, gemm 11.25 11.37 11.4 11.43
+//   1.5B q/o 1536 x 1536         dot 5.30 6.12 6.64 7.34, skinny 5.34 5.33 5.48 5.56, gemm 9.8-9.9
+//   1.5B k/v 256 x 1536          dot 5.14 5.94 6.50 7.17, skinny 5.20 5.21 5.34 5.46, gemm 9.4
+//   1.5B gate 8960 x 1536 (560)  dot 9.00 9.89 10.92 12.42, skinny 9.10 9.18 10.01 10.66, gemm 12.2-12.6
+//   1.5B down 1536 x 8960 (96)   dot 10.65 11.81 13.20 15.39, skinny 17.0-18.3, gemm 13.25 13.39 13.55 14.04
+//   1.5B gate_up 17920 x 1536 (1120)  dot 15.6 16.7 18.1 20.5, skinny 15.0 15.1 16.3 18.1, gemm 12.6-12.7
+// So: k_dot at M <= 2, and at M <= 8 below 1024 tiles; from M = 9, rows of
+// at least kLongK codes on few tiles take k_dot up to M = 12 and the
+// split-K GEMM above, 1024 and more tiles (or rows of kGemmLongRows codes)
+// the GEMM, the rest k_skinny; k_skinny also for M <= 8 on 1024 and more
+// tiles.  k_stream lost to k_skinny by 1.7-3.5x at every M and shape of the
+// sweep (e.g. 151936 x 896: 58-78 us), so it runs only when forced.
 constexpr std::size_t kDotAutoMaxM = 2;
-constexpr int64_t kDotFewTiles = 256;    // M > 8: the GEMM from this many 16-row tiles
-constexpr int64_t kDotMfTiles = 1024;    // M = 3..8: k_dot (its MFMA path) below this many tiles
-constexpr int64_t kLongK = 4096;         // M >= 9 (k_dot takes M <= 8 on few tiles)
-constexpr int64_t kLongKMaxTiles = 128;  // 16-row tiles: N <= 2048
+constexpr std::size_t kDotAutoMfMaxM = 8;    // k_dot's MFMA path below kDotMfTiles tiles
+constexpr std::size_t kDotLongMaxM = 12;     // M > 8: k_dot on long rows over few tiles up to this M
+constexpr int64_t kDotMfTiles = 1024;        // M = 3..16: below this many tiles k_dot / k_skinny, else
+                                             // k_skinny (M <= 8) / the GEMM (M > 8)
+constexpr int64_t kLongK = 4096;             // M > 8: long rows ...
+constexpr int64_t kLongKMaxTiles = 128;      // ... on few 16-row tiles (N <= 2048)
 constexpr std::size_t kSkinnyAutoMaxM = 8;
-constexpr int64_t kGemmLongRows = 4096;  // M > 8: the GEMM on rows of this many codes
+constexpr int64_t kGemmLongRows = 4096;      // M > 8: the GEMM on rows of this many codes over more tiles
 
 int natural_kernel(std::size_t M, std::size_t N, std::size_t K, int act)
 {
     if (act == VVH_F32) return (M >= kGemmF32MinM && K % kGemmBK == 0) ? K_GEMM : K_GEMV_F32;
     const int64_t tiles = ((int64_t)N + kDecodeTileN - 1) / kDecodeTileN;
-    if ((M <= kDotAutoMaxM || (M <= (std::size_t)kDotMaxM && tiles < kDotMfTiles)) &&
-        dot_fits((int64_t)N, (int64_t)K))
-        return K_DOT;
+    const bool dot_ok = dot_fits((int64_t)N, (int64_t)K);
+    if ((M <= kDotAutoMaxM || (M <= kDotAutoMfMaxM && tiles < kDotMfTiles)) && dot_ok) return K_DOT;
     if (M > (std::size_t)kSkinnyMaxM) return K_GEMM;
-    if ((int64_t)K >= kLongK && K % kGemmBK == 0 && tiles <= kLongKMaxTiles) return K_GEMM;
-    if (M > kSkinnyAutoMaxM && K % kGemmBK == 0 && (tiles >= kDotFewTiles || (int64_t)K >= kGemmLongRows))
-        return K_GEMM;
+    if (M > kSkinnyAutoMaxM) {
+        const bool gemm_ok = K % kGemmBK == 0;
+        if ((int64_t)K >= kLongK && tiles <= kLongKMaxTiles) {
+            if (M <= kDotLongMaxM && dot_ok) return K_DOT;
+            if (gemm_ok) return K_GEMM;
+        } else if (gemm_ok && (tiles >= kDotMfTiles || (int64_t)K >= kGemmLongRows)) {
+            return K_GEMM;
+        }
+    }
     return K_SKINNY;
 }
 
