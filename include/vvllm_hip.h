@@ -261,7 +261,8 @@ VVH_API int vvh_linear_q8_dev_noalloc(void* out, const void* inp, const int8_t* 
  * through the stage, with the same arithmetic and fp16 rounding as the
  * standalone operator, and runs on the k_dot family (VVH_KERNEL_DOT), so the
  * result equals the operator followed by vvh_linear_q8_dev on that family
- * exactly (the automatic choice for M <= 2). */
+ * exactly (the automatic choice for M <= 2, and for M <= 8 below 1024
+ * 16-row tiles). */
 enum {
     VVH_IN_NONE = 0,
     VVH_IN_RMS_NORM = 1,  /* rows of inp -> vvh_rms_norm(in_w, in_eps) (:68-76) */
@@ -479,8 +480,9 @@ typedef enum vvh_kernel {
                                  fp16 high and low parts */
     VVH_KERNEL_STREAM = 5,    /* fp16 activations, M <= 16, K > 448: persistent
                                  streaming decode (large N, or grouped plans) */
-    VVH_KERNEL_DOT = 6,       /* fp16 activations, M <= 4: VALU dot products over
-                                 whole cache lines of 8 weight rows */
+    VVH_KERNEL_DOT = 6,       /* fp16 activations, M <= 16: weights loaded as
+                                 whole cache lines of 8 rows; VALU dot products
+                                 (M <= 2) or MFMA 16x16x32 (M >= 3) */
 } vvh_kernel;
 /* Which kernel family vvh_linear_q8 would use for this call (after the
  * override below); returns a vvh_kernel value, or a negative status. */
