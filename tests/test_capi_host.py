@@ -180,7 +180,13 @@ def test_dispatch_choice():
         assert ch(16, 4864, 896, capi.F16, capi.F16) == "skinny"      # M > 8 on 304 tiles
         assert ch(16, 896, 4864, capi.F16, capi.F16) == "gemm"        # M > 12 on long rows
         assert ch(16, 1536, 1536, capi.F16, capi.F16) == "skinny"     # M > 8, few tiles, short rows
-        assert ch(17, 4864, 896, capi.F16, capi.F16) == "gemm"
+        assert ch(17, 4864, 896, capi.F16, capi.F16) == "gemm"        # M > 16 on 304 tiles
+        assert ch(17, 1152, 896, capi.F16, capi.F16) == "skinny"      # M > 16: 2-4 groups of 16 rows
+        assert ch(64, 896, 896, capi.F16, capi.F16) == "skinny"       #   on few tiles, M * K <= 64 * 896
+        assert ch(32, 1536, 1536, capi.F16, capi.F16) == "skinny"
+        assert ch(48, 1536, 1536, capi.F16, capi.F16) == "gemm"
+        assert ch(32, 896, 4864, capi.F16, capi.F16) == "gemm"
+        assert ch(65, 896, 896, capi.F16, capi.F16) == "gemm"
         assert ch(512, 4864, 896, capi.F16, capi.F16) == "gemm"       # config 4
         assert ch(1, 2, 2, capi.F32, capi.F32) == "generic"           # K % 16 != 0
         assert ch(4, 16, 0, capi.F16, capi.F16) == "generic"          # K == 0
@@ -189,7 +195,8 @@ def test_dispatch_choice():
         assert ch(1, 896, 896, capi.F32, capi.F32) == "gemm"          # fp32 split into fp16 hi/lo
         assert ch(40, 896, 880, capi.F32, capi.F32) == "generic"      # fp32 needs K % 64 == 0
         capi.set_kernel(capi.KERNEL_SKINNY)
-        assert ch(64, 896, 896, capi.F16, capi.F16) == "generic"      # M > 16
+        assert ch(64, 896, 896, capi.F16, capi.F16) == "skinny"
+        assert ch(65, 896, 896, capi.F16, capi.F16) == "generic"      # M > 64
         capi.set_kernel(capi.KERNEL_DOT)
         assert ch(1, 16, 16, capi.F16, capi.F16) == "dot"
         assert ch(16, 16, 16, capi.F16, capi.F16) == "dot"

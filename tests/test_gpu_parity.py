@@ -161,9 +161,12 @@ def test_gemv_f32_kernel(gpu, oracle, M, N, K):
 
 
 @pytest.mark.parametrize("outd", [F16, F32])
-@pytest.mark.parametrize("M", [1, 2, 4, 7, 15, 16])
+@pytest.mark.parametrize("M", [1, 2, 4, 7, 15, 16, 17, 32, 33, 64])
 @pytest.mark.parametrize("N,K", [(1, 16), (17, 48), (128, 896), (896, 4864), (300, 1040)])
 def test_skinny_kernel(gpu, oracle, M, N, K, outd):
+    """One 16-row MFMA operand of activations (M <= 16), or 2 and 4 groups of
+    16 rows against each weight chunk (M = 17..64), ragged in every
+    dimension."""
     run_case(oracle, M, N, K, F16, outd, bias=bool(M % 2), res=["sep", "inplace", None][M % 3],
              kernel=capi.KERNEL_SKINNY, seed=3 * M + K)
 
@@ -230,6 +233,8 @@ def test_decode_dispatch_on_device(gpu):
     assert capi.kernel_choice(5, 151936, 896, F16, F16) == "skinny"
     assert capi.kernel_choice(16, 4864, 896, F16, F16) == "skinny"
     assert capi.kernel_choice(16, 17920, 1536, F16, F16) == "gemm"
+    assert capi.kernel_choice(64, 1152, 896, F16, F16) == "skinny"
+    assert capi.kernel_choice(64, 1536, 1536, F16, F16) == "gemm"
 
 
 def test_misaligned_activations_fall_back(gpu, oracle):

@@ -102,7 +102,8 @@ enum Kernel : int {
 };
 
 // Largest M served by the decode kernels.
-constexpr int64_t kSkinnyMaxM = 16;   // one 16-row MFMA operand
+constexpr int64_t kSkinnyMaxM = 16;   // one 16-row MFMA operand (grouped launches, k_stream)
+constexpr int64_t kSkinnyMgMaxM = 64;  // single k_skinny calls: up to 4 groups of 16 rows
 constexpr int64_t kGemvF32MaxM = 8;   // rows of fp32 activations per pass
 
 // Rows of output channels handled by one wave of the decode kernels.

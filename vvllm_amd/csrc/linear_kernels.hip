@@ -217,7 +217,10 @@ struct DecodeShared {
 
 __device__ __forceinline__ bool decode_x_in_lds(const LinArgs& a) { return a.M * a.K * 2 <= kXLdsBytes; }
 
-template <typename OT, bool XLDS>
+// G > 1 (16 < M <= 16 G): the lane's activation rows are m, m + 16, ...,
+// m + 16 (G - 1), one MFMA accumulator pair per group, so each weight chunk
+// is loaded and converted once for all G groups.
+template <typename OT, bool XLDS, int G = 1>
 __device__ __forceinline__ void skinny_body(const LinArgs& a, int64_t block, DecodeShared& sh)
 {
     constexpr int D = kDecodeDepth;
@@ -226,13 +229,18 @@ __device__ __forceinline__ void skinny_body(const LinArgs& a, int64_t block, Dec
     const int64_t nrow = n0 + (c.lane & 15) < a.N ? n0 + (c.lane & 15) : a.N - 1;
     const int chunk = c.lane >> 4;
     const int m = c.lane & 15;
-    const bool mvalid = m < a.M;
     const bool active = n0 < a.N;
     const int8_t* wp = a.w + nrow * a.K + chunk * 16;
     const int64_t ldx = a.K + 8;  // padded LDS row stride of the staged activations
     const f16* xg = static_cast<const f16*>(a.inp);
-    const f16* xp = XLDS ? sh.xs + (mvalid ? m : 0) * ldx + chunk * 16
-                         : xg + (mvalid ? m : 0) * a.K + chunk * 16;
+    bool mvalid[G];
+    const f16* xp[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        const int mg = m + 16 * g;
+        mvalid[g] = mg < a.M;
+        xp[g] = XLDS ? sh.xs + (mvalid[g] ? mg : 0) * ldx + chunk * 16 : xg + (mvalid[g] ? mg : 0) * a.K + chunk * 16;
+    }
 
     u4 wa[D], wb[D];
     auto issue = [&](u4 (&buf)[D], int64_t s) {
@@ -243,22 +251,26 @@ __device__ __forceinline__ void skinny_body(const LinArgs& a, int64_t block, Dec
             if (active && st < c.s1 && st * 64 + chunk * 16 < a.K) buf[u] = ld_stream(wp + st * 64);
         }
     };
-    f4 acc0 = {0.f, 0.f, 0.f, 0.f};
-    f4 acc1 = {0.f, 0.f, 0.f, 0.f};
+    f4 acc0[G], acc1[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) acc0[g] = acc1[g] = f4{0.f, 0.f, 0.f, 0.f};
     auto consume = [&](const u4 (&buf)[D], int64_t s) {
 #pragma unroll
         for (int u = 0; u < D; u++) {
             const int64_t st = s + u;
             if (st < c.s1) {
-                h8 xa = {}, xb = {};
-                if (mvalid && st * 64 + chunk * 16 < a.K) {
-                    xa = *reinterpret_cast<const h8*>(xp + st * 64);
-                    xb = *reinterpret_cast<const h8*>(xp + st * 64 + 8);
-                }
                 h8 b0, b1;
                 i8x16_to_h8x2(buf[u], b0, b1);
-                acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, b0, acc0, 0, 0, 0);
-                acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(xb, b1, acc1, 0, 0, 0);
+#pragma unroll
+                for (int g = 0; g < G; g++) {
+                    h8 xa = {}, xb = {};
+                    if (mvalid[g] && st * 64 + chunk * 16 < a.K) {
+                        xa = *reinterpret_cast<const h8*>(xp[g] + st * 64);
+                        xb = *reinterpret_cast<const h8*>(xp[g] + st * 64 + 8);
+                    }
+                    acc0[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, b0, acc0[g], 0, 0, 0);
+                    acc1[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xb, b1, acc1[g], 0, 0, 0);
+                }
             }
         }
     };
@@ -297,32 +309,36 @@ __device__ __forceinline__ void skinny_body(const LinArgs& a, int64_t block, Dec
             consume(wb, s + D);
         }
     }
-    f4 acc = acc0 + acc1;
-    if (c.ksplit > 1) {
-        sh.red[c.wave][c.lane] = acc;
-        __syncthreads();
-        if (c.ks == 0) {
-            for (int j = 1; j < c.ksplit; j++) acc += sh.red[c.wave + j][c.lane];
-        }
-    }
-    if (c.ks == 0) {
-        const int64_t n = n0 + (c.lane & 15);
-        if (n < a.N) {
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int64_t mm = 4 * (c.lane >> 4) + r;
-                if (mm < a.M) store_out<OT>(a, mm, n, acc[r]);
+    for (int g = 0; g < G; g++) {
+        f4 acc = acc0[g] + acc1[g];
+        if (c.ksplit > 1) {
+            if (g > 0) __syncthreads();  // the previous group's sums are read
+            sh.red[c.wave][c.lane] = acc;
+            __syncthreads();
+            if (c.ks == 0) {
+                for (int j = 1; j < c.ksplit; j++) acc += sh.red[c.wave + j][c.lane];
+            }
+        }
+        if (c.ks == 0) {
+            const int64_t n = n0 + (c.lane & 15);
+            if (n < a.N) {
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int64_t mm = 16 * g + 4 * (c.lane >> 4) + r;
+                    if (mm < a.M) store_out<OT>(a, mm, n, acc[r]);
+                }
             }
         }
     }
 }
 
-template <typename OT>
+template <typename OT, int G>
 __global__ __launch_bounds__(256) void k_skinny(LinArgs a)
 {
     __shared__ DecodeShared sh;
-    if (decode_x_in_lds(a)) skinny_body<OT, true>(a, blockIdx.x, sh);
-    else skinny_body<OT, false>(a, blockIdx.x, sh);
+    if (decode_x_in_lds(a)) skinny_body<OT, true, G>(a, blockIdx.x, sh);
+    else skinny_body<OT, false, G>(a, blockIdx.x, sh);
 }
 
 // Grouped launch: block b serves problem p with
@@ -1540,11 +1556,19 @@ int launch_gemv_f32(const LinArgs& a, int out, void* stream)
     return (int)hipGetLastError();
 }
 
+template <int G>
+static void skinny_launch(const LinArgs& a, int out, dim3 grid, hipStream_t s)
+{
+    if (out == VVH_F32) hipLaunchKernelGGL((k_skinny<float, G>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((k_skinny<f16, G>), grid, dim3(256), 0, s, a);
+}
+
 int launch_skinny(const LinArgs& a, int out, void* stream)
 {
     const dim3 grid((unsigned)decode_blocks(a));
-    if (out == VVH_F32) hipLaunchKernelGGL((k_skinny<float>), grid, dim3(256), 0, S(stream), a);
-    else hipLaunchKernelGGL((k_skinny<f16>), grid, dim3(256), 0, S(stream), a);
+    if (a.M <= 16) skinny_launch<1>(a, out, grid, S(stream));
+    else if (a.M <= 32) skinny_launch<2>(a, out, grid, S(stream));
+    else skinny_launch<4>(a, out, grid, S(stream));
     return (int)hipGetLastError();
 }
 

@@ -398,6 +398,17 @@ constexpr int64_t kLongK = 4096;             // M > 8: long rows ...
 constexpr int64_t kLongKMaxTiles = 128;      // ... on few 16-row tiles (N <= 2048)
 constexpr std::size_t kSkinnyAutoMaxM = 8;
 constexpr int64_t kGemmLongRows = 4096;      // M > 8: the GEMM on rows of this many codes over more tiles
+// M = 17..64 (k_skinny with 2 or 4 groups of 16 rows against the GEMM, same
+// graph replay), M = 17 / 32 / 48 / 64:
+//   0.5B q/k/v 1152 x 896 (72 tiles)  skinny 5.46 6.27 8.38 9.64, gemm 9.94 9.98 10.16 10.41
+//   0.5B o 896 x 896 (56)             skinny 5.45 6.24 8.31 9.58, gemm 9.89 9.91 10.10 10.33
+//   1.5B q/o 1536 x 1536 (96)         skinny 6.79 7.68 10.31 12.05, gemm 10.01 10.09 10.57 10.90
+//   1.5B k/v 256 x 1536 (16)          skinny 6.63 7.52 10.10 11.84, gemm 9.50 9.59 9.87 10.11
+//   1.5B gate 8960 x 1536 (560)       skinny 12.06 16.0 20.95 25.49, gemm 12.68 13.53 14.88 11.89
+//   0.5B down 896 x 4864 (56)         skinny 14.15 16.1 21.85 26.07, gemm 11.57 12.0 12.78 12.41
+//   (gate/up and longer rows: the GEMM by 1.3-3.4x)
+// so k_skinny at most kLongKMaxTiles tiles with M * K <= kSkinnyMgMaxMK.
+constexpr int64_t kSkinnyMgMaxMK = 64 * 896;
 
 int natural_kernel(std::size_t M, std::size_t N, std::size_t K, int act)
 {
@@ -405,7 +416,14 @@ int natural_kernel(std::size_t M, std::size_t N, std::size_t K, int act)
     const int64_t tiles = ((int64_t)N + kDecodeTileN - 1) / kDecodeTileN;
     const bool dot_ok = dot_fits((int64_t)N, (int64_t)K);
     if ((M <= kDotAutoMaxM || (M <= kDotAutoMfMaxM && tiles < kDotMfTiles)) && dot_ok) return K_DOT;
-    if (M > (std::size_t)kSkinnyMaxM) return K_GEMM;
+    if (M > (std::size_t)kSkinnyMaxM) {
+        // k_skinny with up to 4 groups of 16 rows: one weight pass, the
+        // activations (M * K halves) read again by every wave, so few tiles
+        // and short rows only
+        if (M <= (std::size_t)kSkinnyMgMaxM && tiles <= kLongKMaxTiles && (int64_t)(M * K) <= kSkinnyMgMaxMK)
+            return K_SKINNY;
+        return K_GEMM;
+    }
     if (M > kSkinnyAutoMaxM) {
         const bool gemm_ok = K % kGemmBK == 0;
         if ((int64_t)K >= kLongK && tiles <= kLongKMaxTiles) {
@@ -429,7 +447,7 @@ int choose_kernel(std::size_t M, std::size_t N, std::size_t K, int act, bool ali
     const bool decode = act == VVH_F16 && M <= (std::size_t)kSkinnyMaxM;
     switch (k) {
         case K_GEMV_F32: return act == VVH_F32 ? K_GEMV_F32 : K_GENERIC;
-        case K_SKINNY: return decode ? K_SKINNY : K_GENERIC;
+        case K_SKINNY: return (act == VVH_F16 && M <= (std::size_t)kSkinnyMgMaxM) ? K_SKINNY : K_GENERIC;
         case K_STREAM: return (decode && stream_depth(((int64_t)K + 63) / 64) > 0) ? K_STREAM : K_GENERIC;
         case K_DOT:
             return (act == VVH_F16 && M <= (std::size_t)kDotMaxM && dot_fits((int64_t)N, (int64_t)K)) ? K_DOT
@@ -1320,7 +1338,9 @@ VVH_API int vvh_plan_create(const vvh_q8_problem* problems, size_t count, int ac
         a.src = (int32_t)i;
         const bool aligned = q.K % 16 == 0 && aligned16(q.weight) && aligned16(q.inp);
         const int kf = choose_kernel(q.M, q.N, q.K, act_dtype, aligned);
-        if (kf != K_SKINNY && kf != K_STREAM && kf != K_DOT) all_skinny = false;
+        // the grouped decode launches take one 16-row activation group
+        if ((kf != K_SKINNY && kf != K_STREAM && kf != K_DOT) || (kf == K_SKINNY && q.M > (std::size_t)kSkinnyMaxM))
+            all_skinny = false;
         if (kf != K_DOT) all_dot = false;
         total_tiles += (a.N + kDecodeTileN - 1) / kDecodeTileN;
         p.args.push_back(a);
