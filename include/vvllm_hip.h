@@ -474,7 +474,9 @@ typedef enum vvh_kernel {
     VVH_KERNEL_AUTO = 0,      /* size-based choice (default) */
     VVH_KERNEL_GENERIC = 1,   /* any shape / alignment, one thread per output */
     VVH_KERNEL_GEMV_F32 = 2,  /* fp32 activations, M < 32: VALU dot products */
-    VVH_KERNEL_SKINNY = 3,    /* fp16 activations, M <= 16, MFMA 16x16x32 */
+    VVH_KERNEL_SKINNY = 3,    /* fp16 activations, M <= 64 (1, 2 or 4 groups of
+                                 16 rows per weight chunk; plans: M <= 16),
+                                 MFMA 16x16x32 */
     VVH_KERNEL_GEMM = 4,      /* LDS-tiled MFMA 32x32x16: fp16 activations, or
                                  fp32 activations (K % 64 == 0) split into
                                  fp16 high and low parts */
