@@ -162,11 +162,12 @@ def test_gemv_f32_kernel(gpu, oracle, M, N, K):
 
 @pytest.mark.parametrize("outd", [F16, F32])
 @pytest.mark.parametrize("M", [1, 2, 4, 7, 15, 16, 17, 32, 33, 64])
-@pytest.mark.parametrize("N,K", [(1, 16), (17, 48), (128, 896), (896, 4864), (300, 1040)])
+@pytest.mark.parametrize("N,K", [(1, 16), (17, 48), (128, 896), (896, 4864), (300, 1040), (40, 128)])
 def test_skinny_kernel(gpu, oracle, M, N, K, outd):
     """One 16-row MFMA operand of activations (M <= 16), or 2 and 4 groups of
     16 rows against each weight chunk (M = 17..64), ragged in every
-    dimension."""
+    dimension; K = 128 at M = 64 is 16 KB of activations whose padded rows
+    would not fit the LDS staging area (read through the caches instead)."""
     run_case(oracle, M, N, K, F16, outd, bias=bool(M % 2), res=["sep", "inplace", None][M % 3],
              kernel=capi.KERNEL_SKINNY, seed=3 * M + K)
 

@@ -215,7 +215,12 @@ struct DecodeShared {
     __attribute__((aligned(16))) f16 xs[kXLdsHalves];
 };
 
-__device__ __forceinline__ bool decode_x_in_lds(const LinArgs& a) { return a.M * a.K * 2 <= kXLdsBytes; }
+// at most kXLdsBytes of activations (the staging loop's 4 chunks per
+// thread), in rows padded to K + 8 halves that fit xs (implied for M <= 16)
+__device__ __forceinline__ bool decode_x_in_lds(const LinArgs& a)
+{
+    return a.M * a.K * 2 <= kXLdsBytes && a.M * (a.K + 8) <= kXLdsHalves;
+}
 
 // G > 1 (16 < M <= 16 G): the lane's activation rows are m, m + 16, ...,
 // m + 16 (G - 1), one MFMA accumulator pair per group, so each weight chunk
