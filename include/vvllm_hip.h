@@ -213,8 +213,8 @@ VVH_API int vvh_weight_stats(uint64_t* count, uint64_t* bytes);
  *   - The dot product is accumulated in fp32 from the exact int8 codes;
  *     fp16 activations are used as given (no re-rounding).  fp32
  *     activations are not rounded to fp16 as the reference's CUDA fp32 mode
- *     does (backend_cuda.cc:205-211): the decode kernels (M < 32, or
- *     K % 64 != 0) use them as they are; the GEMM (M >= 32) multiplies each
+ *     does (backend_cuda.cc:205-211): the decode kernels (M < 16, or
+ *     K % 64 != 0) use them as they are; the GEMM (M >= 16) multiplies each
  *     row, scaled by a power of two, as a pair of fp16 values (high part,
  *     then the exact remainder rounded to fp16), about 22 significant bits
  *     of each activation, with exact products and fp32 accumulation.
@@ -241,7 +241,7 @@ VVH_API int vvh_linear_q8_dev(void* out, const void* inp, const int8_t* dev_weig
  * go to a fixed VVH_NOALLOC_SCRATCH_BYTES device array that the library
  * holds on each device from vvh_init until the process ends, instead of the
  * stream's workspace (which grows with hipMalloc); so do the split
- * activations of an fp32-activation GEMM (M >= 32: M * K * 4 + M * 4 bytes).
+ * activations of an fp32-activation GEMM (M >= 16: M * K * 4 + M * 4 bytes).
  * No hipMalloc, hipFree or allocating library routine is called.  A call
  * whose workspace needs more than VVH_NOALLOC_SCRATCH_BYTES returns
  * VVH_ERR_UNSUPPORTED.
@@ -473,7 +473,7 @@ VVH_API int vvh_mirror_release(const float* host);
 typedef enum vvh_kernel {
     VVH_KERNEL_AUTO = 0,      /* size-based choice (default) */
     VVH_KERNEL_GENERIC = 1,   /* any shape / alignment, one thread per output */
-    VVH_KERNEL_GEMV_F32 = 2,  /* fp32 activations, M < 32: VALU dot products */
+    VVH_KERNEL_GEMV_F32 = 2,  /* fp32 activations, M < 16: VALU dot products */
     VVH_KERNEL_SKINNY = 3,    /* fp16 activations, M <= 64 (1, 2 or 4 groups of
                                  16 rows per weight chunk; plans: M <= 16),
                                  MFMA 16x16x32 */

@@ -155,8 +155,8 @@ def test_dispatch_choice():
     try:
         capi.set_kernel(capi.KERNEL_AUTO)
         assert ch(1, 896, 896, capi.F32, capi.F32) == "gemv_f32"      # config 1
-        assert ch(31, 4864, 896, capi.F32, capi.F32) == "gemv_f32"
-        assert ch(32, 4864, 896, capi.F32, capi.F32) == "gemm"        # fp32 prefill on MFMA
+        assert ch(15, 4864, 896, capi.F32, capi.F32) == "gemv_f32"
+        assert ch(16, 4864, 896, capi.F32, capi.F32) == "gemm"        # fp32 prefill on MFMA
         assert ch(512, 4864, 880, capi.F32, capi.F32) == "gemv_f32"   # K % 64 != 0
         assert ch(1, 151936, 896, capi.F16, capi.F32) == "dot"        # config 3 (M = 1)
         assert ch(1, 896, 896, capi.F16, capi.F16) == "dot"           # config 2 (M = 1)

@@ -687,9 +687,10 @@ def test_fp32_gemm(gpu, oracle, M, N, K, res, outd):
     """The reference's default (fp32) mode on the prefill GEMM: fp32 in,
     fp32 or fp16 out, against the oracle at the fp32 bar (1e-4 and, for fp32
     outputs, the fp32 accumulation bound).  Includes split-K (K = 4864 with
-    few tiles), edge tiles (N = 250, 776; M = 130, 300) and M = 16 forced."""
-    kern = capi.KERNEL_GEMM if M < 32 else capi.KERNEL_AUTO
-    if M >= 32:
+    few tiles), edge tiles (N = 250, 776; M = 130, 300) and M = 16, the
+    smallest M the automatic choice sends to the GEMM."""
+    kern = capi.KERNEL_AUTO
+    if K % 64 == 0:
         assert capi.kernel_choice(M, N, K, F32, outd) == "gemm"
     run_case(oracle, M, N, K, F32, outd, bias=bool(N % 2 == 0), res=res, kernel=kern, seed=3 * M + N + K)
 

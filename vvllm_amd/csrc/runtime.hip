@@ -341,8 +341,9 @@ int dot_depth(int64_t K, int ksplit)
 
 // fp32 activations take the GEMM (on their split fp16 form) from this many
 // rows on, when K % 64 == 0; below it k_gemv_f32, which streams the weights
-// once per 8 rows.
-constexpr std::size_t kGemmF32MinM = 32;
+// once per 8 rows (gate/up 4864 x 896, graph replay: M = 8 13.7 against
+// 14.1 us on the GEMM, M = 16 17.0 against 14.2, M = 32 23.9 against 15.1).
+constexpr std::size_t kGemmF32MinM = 16;
 
 // Small-M fp16 dispatch, from a sweep of every family forced on each shape
 // (us per call on the GPU, calls replayed from HIP graphs; the bench.py
