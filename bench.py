@@ -455,7 +455,8 @@ def main():
     tfile = os.path.join(ROOT, "profiles", "traffic_decode_set.json")
     if os.path.exists(tfile):
         t = json.load(open(tfile))
-        if t.get("kernel") == KERNEL_SYMBOL.get(kern):  # measured on the kernel this run uses
+        # measured on the kernel family this run uses (the file names the full instantiation)
+        if t.get("kernel", "").split("<")[0] == KERNEL_SYMBOL.get(kern, "?").split("<")[0]:
             traffic = t.get("hbm_bytes_per_launch")
 
     result = {
