@@ -145,7 +145,9 @@ def test_gemm_variant_choice():
     assert capi.gemm_variant(256, 8960, 1536) == "k_gemm3 128x128"    # 280 64-row tiles > 256 CUs
     assert capi.gemm_variant(2048, 4864, 896) == "k_gemm3 128x192"    # 3 rounds -> 2
     assert capi.gemm_variant(512, 896, 4864) == "k_gemm3 128x128 split 6"   # 28 tiles, 76 k stages
-    assert capi.gemm_variant(2048, 896, 4864) == "k_gemm3 128x128 split 2"  # 112 tiles: half the CUs
+    assert capi.gemm_variant(2048, 896, 4864) == "k_gemm3 64x128"   # 224 64-row tiles beat 2 splits
+    assert capi.gemm_variant(64, 1536, 1536) == "k_gemm3 128x128 split 6"   # 12 tiles, 24 k stages
+    assert capi.gemm_variant(256, 1536, 1536) == "k_gemm3 64x128"   # 48 64-row tiles beat 3 splits
     assert capi.gemm_variant(300, 1000, 80) == "k_gemm"               # K % 64 != 0
     assert capi.load().vvh_gemm_variant(0, 16, 64, None, None) == -1  # -VVH_ERR_INVALID_ARG
 

@@ -231,10 +231,17 @@ int workspace_get(const WsSource* src, void* stream, std::size_t bytes, float** 
 // of forced counts on the Qwen2.5-0.5B down projection (M=512: 33.1, 23.9,
 // 20.6, 19.9, 19.8, 19.9, 21.8, 21.5 us for 1..7 and 9 splits; M=2048: 36.4,
 // 33.7, 42.4 us for 1..3): 0.4 us per k stage and round of blocks over the
-// CUs, 2.5 us for the reduction's launch, and each plane at 1.6 TB/s.
-int gemm_splits(int64_t tiles, int64_t stages, uint64_t plane_bytes)
+// CUs, 2.5 us for the reduction's launch, and each plane at 1.6 TB/s.  An
+// unsplit call whose 64-row tiles give every block a CU runs on 64 x 128
+// tiles (gemm3_layout), priced at 0.3 us per k stage: a sweep of forced
+// counts at M = 64..256 (1.5B q/o at M = 256: unsplit 11.38 us against
+// 13.95 for 3 splits; at M = 64: 11.48 against 10.88 for 6) puts it there.
+int gemm_splits(int64_t M, int64_t N, int64_t stages)
 {
     const int64_t cus = g_cu_count > 0 ? g_cu_count : 256;
+    const int64_t tiles = ((M + kGemmBM - 1) / kGemmBM) * ((N + kGemmBN - 1) / kGemmBN);
+    const bool tiles64 = ((M + 63) / 64) * ((N + 127) / 128) <= cus;  // unsplit layout: 64 x 128
+    const double plane_bytes = (double)M * (double)N * 4.0;
     int64_t s = 1;
     if (tiles * 2 <= cus && stages >= 8) {
         const int64_t smax = std::min<int64_t>(cus / tiles, stages / 4);
@@ -242,7 +249,9 @@ int gemm_splits(int64_t tiles, int64_t stages, uint64_t plane_bytes)
         for (int64_t c = 1; c <= smax; c++) {
             const int64_t kst = (stages + c - 1) / c, ce = (stages + kst - 1) / kst;  // no empty split
             const int64_t rounds = (tiles * ce + cus - 1) / cus;
-            const double t = 0.4 * (double)(rounds * kst) + (ce > 1 ? 2.5 + (double)ce * (double)plane_bytes / 1.6e6 : 0.0);
+            const double t = ce == 1 && tiles64 ? 0.3 * (double)stages
+                                                : 0.4 * (double)(rounds * kst) +
+                                                      (ce > 1 ? 2.5 + (double)ce * plane_bytes / 1.6e6 : 0.0);
             if (c == 1 || t < best) {
                 best = t;
                 s = c;
@@ -550,7 +559,7 @@ int run_call(const LinArgs& base, int kernel, int act, int outd, void* stream, c
                     rs_bytes = align_up((uint64_t)a.M * 4);
                 }
                 const int64_t stages = (f32 ? 2 * a.K : a.K) / kGemmBK;
-                int s = gemm_splits(nb, stages, (uint64_t)a.M * (uint64_t)a.N * 4);
+                int s = gemm_splits(a.M, a.N, stages);
                 uint64_t plane = 0;
                 if (s > 1) {
                     const int64_t kst = (stages + s - 1) / s;
@@ -1631,9 +1640,8 @@ VVH_API int vvh_gemm_variant(size_t M, size_t N, size_t K, int* tile_n, int* spl
     if (M == 0 || N == 0) return -fail(VVH_ERR_INVALID_ARG, "empty problem");
     int tn = kGemmBN, s = 1, v = 1;
     if (K % kGemmBK == 0) {
-        const int64_t nb = (((int64_t)M + kGemmBM - 1) / kGemmBM) * (((int64_t)N + kGemmBN - 1) / kGemmBN);
         const int64_t stages = (int64_t)K / kGemmBK;
-        s = gemm_splits(nb, stages, (uint64_t)M * (uint64_t)N * 4);
+        s = gemm_splits((int64_t)M, (int64_t)N, stages);
         if (s > 1) {  // as the dispatch: no empty split
             const int64_t kst = (stages + s - 1) / s;
             s = (int)((stages + kst - 1) / kst);
