@@ -228,7 +228,9 @@ def test_decode_dispatch_on_device(gpu):
     assert capi.kernel_choice(4, 17920, 1536, F16, F16) == "skinny"
     assert capi.kernel_choice(5, 1536, 8960, F16, F16) == "dot"
     assert capi.kernel_choice(8, 896, 4864, F16, F16) == "dot"
-    assert capi.kernel_choice(8, 17920, 1536, F16, F16) == "skinny"
+    assert capi.kernel_choice(8, 17920, 1536, F16, F16) == "gemm"
+    assert capi.kernel_choice(8, 151936, 896, F16, F16) == "skinny"
+    assert capi.kernel_choice(16, 896, 4864, F16, F16) == "dot"
     assert capi.kernel_choice(9, 1536, 8960, F16, F16) == "dot"
     assert capi.kernel_choice(13, 1536, 8960, F16, F16) == "gemm"
     assert capi.kernel_choice(5, 151936, 896, F16, F16) == "skinny"

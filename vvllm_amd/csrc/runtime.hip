@@ -393,15 +393,26 @@ constexpr std::size_t kGemmF32MinM = 16;
 //   1.5B gate 8960 x 1536 (560)  dot 9.00 9.89 10.92 12.42, skinny 9.10 9.18 10.01 10.66, gemm 12.2-12.6
 //   1.5B down 1536 x 8960 (96)   dot 10.65 11.81 13.20 15.39, skinny 17.0-18.3, gemm 13.25 13.39 13.55 14.04
 //   1.5B gate_up 17920 x 1536 (1120)  dot 15.6 16.7 18.1 20.5, skinny 15.0 15.1 16.3 18.1, gemm 12.6-12.7
-// So: k_dot at M <= 2, and at M <= 8 below 1024 tiles; from M = 9, rows of
-// at least kLongK codes on few tiles take k_dot up to M = 12 and the
-// split-K GEMM above, 1024 and more tiles (or rows of kGemmLongRows codes)
-// the GEMM, the rest k_skinny; k_skinny also for M <= 8 on 1024 and more
-// tiles.  k_stream lost to k_skinny by 1.7-3.5x at every M and shape of the
+// and on >= 1024 tiles or long rows, M = 4..8 / 12..16:
+//   1.5B gate_up 17920 x 1536 (1120 tiles), M = 4 5 6 7 8: skinny 11.67 12.19 13.94 14.49 15.02,
+//                                            gemm 11.87 12.40 12.59 12.57 12.62
+//   151936 x 896 (9496 tiles), M = 4 6 8 12 16: skinny 34.8 36.0 37.1 57.9 63.4, gemm 52.6 52.7 52.3 53.3 54.5
+//   0.5B down 896 x 4864, M = 12 13 14 16: dot 9.42 9.77 10.17 10.77, skinny 10.6-11.0, gemm 11.4-11.5
+//   1.5B down 1536 x 8960, M = 12 13 14 16: dot 13.21 13.72 14.44 15.30, gemm 13.31 13.35 13.35 13.42
+// So: k_dot at M <= 2, and at M <= 8 below 1024 tiles; at M = 6..8 on more
+// tiles the GEMM when its 64 x 128 tiles fit one round over the CUs (not
+// the LM head: 1187 of them); from M = 9, rows of at least kLongK codes on
+// few tiles take k_dot up to M = 12 or M * K = 16 * 4864 and the split-K
+// GEMM above, 1024 and more tiles (or rows of kGemmLongRows codes) the
+// GEMM, the rest k_skinny; k_skinny also for M <= 8 on 1024 and more tiles
+// otherwise.  k_stream lost to k_skinny by 1.7-3.5x at every M and shape of the
 // sweep (e.g. 151936 x 896: 58-78 us), so it runs only when forced.
 constexpr std::size_t kDotAutoMaxM = 2;
 constexpr std::size_t kDotAutoMfMaxM = 8;    // k_dot's MFMA path below kDotMfTiles tiles
-constexpr std::size_t kDotLongMaxM = 12;     // M > 8: k_dot on long rows over few tiles up to this M
+constexpr std::size_t kDotLongMaxM = 12;     // M > 8: k_dot on long rows over few tiles up to this M,
+constexpr int64_t kDotLongMaxMK = 16 * 4864; // or while M * K is at most this
+constexpr std::size_t kGemmWideMinM = 6;     // M = 6..8 on >= kDotMfTiles tiles: the GEMM when its
+                                             // 64 x 128 tiles fit one round over the CUs
 constexpr int64_t kDotMfTiles = 1024;        // M = 3..16: below this many tiles k_dot / k_skinny, else
                                              // k_skinny (M <= 8) / the GEMM (M > 8)
 constexpr int64_t kLongK = 4096;             // M > 8: long rows ...
@@ -426,6 +437,9 @@ int natural_kernel(std::size_t M, std::size_t N, std::size_t K, int act)
     const int64_t tiles = ((int64_t)N + kDecodeTileN - 1) / kDecodeTileN;
     const bool dot_ok = dot_fits((int64_t)N, (int64_t)K);
     if ((M <= kDotAutoMaxM || (M <= kDotAutoMfMaxM && tiles < kDotMfTiles)) && dot_ok) return K_DOT;
+    const int64_t cus = g_cu_count > 0 ? g_cu_count : 256;
+    if (M >= kGemmWideMinM && M <= kSkinnyAutoMaxM && K % kGemmBK == 0 && ((int64_t)N + 127) / 128 <= cus)
+        return K_GEMM;
     if (M > (std::size_t)kSkinnyMaxM) {
         // k_skinny with up to 4 groups of 16 rows: one weight pass, the
         // activations (M * K halves) read again by every wave, so few tiles
@@ -437,7 +451,7 @@ int natural_kernel(std::size_t M, std::size_t N, std::size_t K, int act)
     if (M > kSkinnyAutoMaxM) {
         const bool gemm_ok = K % kGemmBK == 0;
         if ((int64_t)K >= kLongK && tiles <= kLongKMaxTiles) {
-            if (M <= kDotLongMaxM && dot_ok) return K_DOT;
+            if ((M <= kDotLongMaxM || (int64_t)(M * K) <= kDotLongMaxMK) && dot_ok) return K_DOT;
             if (gemm_ok) return K_GEMM;
         } else if (gemm_ok && (tiles >= kDotMfTiles || (int64_t)K >= kGemmLongRows)) {
             return K_GEMM;
