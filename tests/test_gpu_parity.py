@@ -240,6 +240,16 @@ def test_decode_dispatch_on_device(gpu):
     assert capi.kernel_choice(64, 1536, 1536, F16, F16) == "gemm"
 
 
+@pytest.mark.parametrize("M,N,K,family", [(8, 17920, 1536, "gemm"), (6, 17920, 1536, "gemm"), (5, 17920, 1536, "skinny"),
+                                          (16, 896, 4864, "dot"), (13, 896, 4864, "dot"), (13, 1536, 8960, "gemm"),
+                                          (64, 1152, 896, "skinny"), (33, 1536, 1536, "skinny")])
+def test_dispatch_edges_parity(gpu, oracle, M, N, K, family):
+    """The automatic choice at the edges of the small-M dispatch rules, each
+    against the oracle as dispatched (bias and residual on)."""
+    assert capi.kernel_choice(M, N, K, F16, F16) == family
+    run_case(oracle, M, N, K, F16, F16, bias=True, res="sep", kernel=capi.KERNEL_AUTO, seed=17 * M + N)
+
+
 def test_misaligned_activations_fall_back(gpu, oracle):
     """A 2-byte-offset fp16 activation base cannot take 16-byte loads: the
     dispatcher must route it to the generic kernel and stay correct."""
