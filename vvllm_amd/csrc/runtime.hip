@@ -236,6 +236,8 @@ int workspace_get(const WsSource* src, void* stream, std::size_t bytes, float** 
 // tiles (gemm3_layout), priced at 0.3 us per k stage: a sweep of forced
 // counts at M = 64..256 (1.5B q/o at M = 256: unsplit 11.38 us against
 // 13.95 for 3 splits; at M = 64: 11.48 against 10.88 for 6) puts it there.
+// Splits may be as short as 2 stages (1.5B k/v at M = 64: 12 splits 9.18 us
+// against 10.12 for 6, the model's choice at the former floor of 4).
 int gemm_splits(int64_t M, int64_t N, int64_t stages)
 {
     const int64_t cus = g_cu_count > 0 ? g_cu_count : 256;
@@ -244,7 +246,7 @@ int gemm_splits(int64_t M, int64_t N, int64_t stages)
     const double plane_bytes = (double)M * (double)N * 4.0;
     int64_t s = 1;
     if (tiles * 2 <= cus && stages >= 8) {
-        const int64_t smax = std::min<int64_t>(cus / tiles, stages / 4);
+        const int64_t smax = std::min<int64_t>(cus / tiles, stages / 2);
         double best = 0;
         for (int64_t c = 1; c <= smax; c++) {
             const int64_t kst = (stages + c - 1) / c, ce = (stages + kst - 1) / kst;  // no empty split
