@@ -221,28 +221,27 @@ int workspace_get(const WsSource* src, void* stream, std::size_t bytes, float** 
     return VVH_OK;
 }
 
-// Number of k splits for a GEMM of `tiles` 128x128 output tiles, `stages`
-// 64-wide k stages and an M x N fp32 partial plane of `plane_bytes`.  A split
-// GEMM pays a second launch and, per split, one partial plane written by the
-// GEMM and read back by the reduction, so it only pays for long reductions
-// over few tiles: split when the tiles would leave half of the CUs idle and K
-// has at least 8 stages (with fewer, a block's k loop is shorter than the
-// reduction launch).  The count minimises a cost model fitted to a sweep
-// of forced counts on the Qwen2.5-0.5B down projection (M=512: 33.1, 23.9,
-// 20.6, 19.9, 19.8, 19.9, 21.8, 21.5 us for 1..7 and 9 splits; M=2048: 36.4,
-// 33.7, 42.4 us for 1..3): 0.4 us per k stage and round of blocks over the
-// CUs, 2.5 us for the reduction's launch, and each plane at 1.6 TB/s.  An
-// unsplit call whose 64-row tiles give every block a CU runs on 64 x 128
-// tiles (gemm3_layout), priced at 0.3 us per k stage: a sweep of forced
-// counts at M = 64..256 (1.5B q/o at M = 256: unsplit 11.38 us against
-// 13.95 for 3 splits; at M = 64: 11.48 against 10.88 for 6) puts it there.
-// Splits may be as short as 2 stages (1.5B k/v at M = 64: 12 splits 9.18 us
-// against 10.12 for 6, the model's choice at the former floor of 4).
+// Number of k splits for an M x N GEMM of `stages` 64-wide k stages.  A
+// split GEMM pays a second launch and, per split, one M x N fp32 partial
+// plane written by the GEMM and read back by the reduction, so it only pays
+// for long reductions over few tiles: split when the 64 x 128 tiles would
+// leave half of the CUs idle and K has at least 8 stages.  Split and
+// unsplit calls at that size run on 64 x 128 tiles (gemm3_layout).  The
+// count minimises a cost model fitted to sweeps of forced counts (graph
+// replay): 0.25 us per k stage of a split block, 2.5 us for the
+// reduction's launch, each plane at 1.6 TB/s, and 0.3 us per stage for an
+// unsplit call.  Measured on 64 x 128 against 128 x 128 split tiles:
+// 0.5B down (896 x 4864) at M = 128: 8 splits 11.77 us (128 x 128, 11
+// splits: 14.64), M = 512: 4 splits 16.81 (6 on 128 x 128: 19.51), M = 64:
+// 13 splits 11.13 (12.43); 1.5B down (1536 x 8960) at M = 16: 20 splits
+// 11.83 (12.98), M = 64: 10 splits 14.25 (15.78), M = 256: 5 splits 19.74
+// (22.0); 1.5B q/o at M = 64: 6 splits 9.73 (10.9), k/v: 12 splits 8.41
+// (9.18).  Splits may be as short as 2 stages (k/v at M = 64: 12 splits
+// against 6 at a floor of 4 stages, 9.18 against 10.12 us on 128 x 128).
 int gemm_splits(int64_t M, int64_t N, int64_t stages)
 {
     const int64_t cus = g_cu_count > 0 ? g_cu_count : 256;
-    const int64_t tiles = ((M + kGemmBM - 1) / kGemmBM) * ((N + kGemmBN - 1) / kGemmBN);
-    const bool tiles64 = ((M + 63) / 64) * ((N + 127) / 128) <= cus;  // unsplit layout: 64 x 128
+    const int64_t tiles = ((M + 63) / 64) * ((N + 127) / 128);  // 64 x 128 tiles
     const double plane_bytes = (double)M * (double)N * 4.0;
     int64_t s = 1;
     if (tiles * 2 <= cus && stages >= 8) {
@@ -251,9 +250,8 @@ int gemm_splits(int64_t M, int64_t N, int64_t stages)
         for (int64_t c = 1; c <= smax; c++) {
             const int64_t kst = (stages + c - 1) / c, ce = (stages + kst - 1) / kst;  // no empty split
             const int64_t rounds = (tiles * ce + cus - 1) / cus;
-            const double t = ce == 1 && tiles64 ? 0.3 * (double)stages
-                                                : 0.4 * (double)(rounds * kst) +
-                                                      (ce > 1 ? 2.5 + (double)ce * plane_bytes / 1.6e6 : 0.0);
+            const double t = ce == 1 ? 0.3 * (double)stages
+                                     : 0.25 * (double)(rounds * kst) + 2.5 + (double)ce * plane_bytes / 1.6e6;
             if (c == 1 || t < best) {
                 best = t;
                 s = c;
@@ -264,7 +262,7 @@ int gemm_splits(int64_t M, int64_t N, int64_t stages)
     return (int)s;
 }
 
-// k_gemm3 tile shape: split-K problems (few tiles, long K) take 128 x 128.
+// k_gemm3 tile shape: split-K problems (few tiles, long K) take 64 x 128.
 // Unsplit ones take 64 x 128 when those tiles give every block a CU of its
 // own (then more CUs work than with 128-row tiles, each on half a tile:
 // gate/up N=4864 K=896 at M=128 and 256, 10.5 -> 8.2 us; q/k/v N=1152 at
@@ -277,7 +275,7 @@ int gemm_splits(int64_t M, int64_t N, int64_t stages)
 // into LDS, not latency within a SIMD, bound a block.)
 int gemm3_layout(int64_t M, int64_t N, int splits)
 {
-    if (splits > 1) return 3;
+    if (splits > 1) return 4;
     const int64_t cus = g_cu_count > 0 ? g_cu_count : 256;
     if (((M + 63) / 64) * ((N + 127) / 128) <= cus) return 4;
     const int64_t nbm = (M + kGemmBM - 1) / kGemmBM;
