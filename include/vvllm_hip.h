@@ -233,8 +233,8 @@ VVH_API int vvh_linear_q8_dev(void* out, const void* inp, const int8_t* dev_weig
 /* Size of the fixed device scratch of vvh_linear_q8_dev_noalloc: the split-K
  * partial planes of one call (M * N * 4 bytes per split).  On a 256-CU
  * device every split the dispatcher makes fits: it splits only GEMMs of at
- * most 128 output tiles of 128 x 128, into at most 256 blocks, i.e. at most
- * 256 fp32 tiles = 16 MiB. */
+ * most 128 output tiles of 64 x 128, into at most 256 blocks, i.e. at most
+ * 256 fp32 tiles of 32 KiB = 8 MiB of planes. */
 #define VVH_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
 /* vvh_linear_q8_dev that allocates nothing: same arguments, same kernels and
  * the same result bits as vvh_linear_q8_dev, but the split-K partial planes
