@@ -85,6 +85,8 @@ class HipEvents:
         h.hipStreamEndCapture.argtypes = [V, ctypes.POINTER(V)]
         h.hipGraphInstantiate.argtypes = [ctypes.POINTER(V), V, V, V, ctypes.c_size_t]
         h.hipGraphLaunch.argtypes = [V, V]
+        h.hipGraphDestroy.argtypes = [V]
+        h.hipGraphExecDestroy.argtypes = [V]
 
     def create(self):
         e = ctypes.c_void_p()
@@ -106,16 +108,31 @@ class HipEvents:
         return s
 
     def graph(self, stream, fn):
-        """Captures fn(stream) into an instantiated graph."""
+        """Captures fn(stream) into an instantiated graph; the captured graph
+        itself is destroyed once instantiated.  The caller releases the
+        executable graph with drop()."""
         g, ge = ctypes.c_void_p(), ctypes.c_void_p()
         assert self.hip.hipStreamBeginCapture(stream, 0) == 0
         fn(stream)
         assert self.hip.hipStreamEndCapture(stream, ctypes.byref(g)) == 0
-        assert self.hip.hipGraphInstantiate(ctypes.byref(ge), g, None, None, 0) == 0
+        try:
+            assert self.hip.hipGraphInstantiate(ctypes.byref(ge), g, None, None, 0) == 0
+        finally:
+            assert self.hip.hipGraphDestroy(g) == 0
         return ge
 
     def launch(self, ge, stream):
         assert self.hip.hipGraphLaunch(ge, stream) == 0
+
+    def drop(self, *graphs):
+        """Destroys executable graphs (after the work queued from them ends)."""
+        capi.sync()
+        for ge in graphs:
+            assert self.hip.hipGraphExecDestroy(ge) == 0
+
+    def destroy(self, *events):
+        for e in events:
+            assert self.hip.hipEventDestroy(e) == 0
 
 
 def timed(ev, fn, reps, stream=None):
@@ -123,12 +140,15 @@ def timed(ev, fn, reps, stream=None):
     on the stream the work runs on."""
     capi.sync()
     a, b = ev.create(), ev.create()
-    ev.record(a, stream)
-    for i in range(reps):
-        fn(i)
-    ev.record(b, stream)
-    ms = ev.elapsed_ms(a, b)
-    capi.sync()
+    try:
+        ev.record(a, stream)
+        for i in range(reps):
+            fn(i)
+        ev.record(b, stream)
+        ms = ev.elapsed_ms(a, b)
+        capi.sync()
+    finally:
+        ev.destroy(a, b)
     return ms / reps
 
 
@@ -156,11 +176,25 @@ def arena_size(items):
 ROTATE_BYTES = 1 << 30  # more than the 256 MB MALL: every timed call reads its weights from HBM
 
 
+def check_scratch(tmp_w, N, K):
+    """Raises before any device call when the fp32 weight scratch `tmp_w`
+    (anything with .ptr and .nbytes, e.g. a capi.DevBuf) cannot hold the
+    N x K fp32 weights that vvh_fill_normal writes into it."""
+    need = N * K * 4
+    nbytes = getattr(tmp_w, "nbytes", None)
+    if nbytes is None or not getattr(tmp_w, "ptr", None):
+        raise TypeError("the weight scratch must be a device buffer with .ptr and .nbytes")
+    if need > nbytes:
+        raise ValueError(f"weight scratch of {nbytes} bytes is too small for {N} x {K} fp32 weights ({need} bytes)")
+
+
 def rotation(tmp_w, M, N, K, bias, res, seed, act=F16, outd=F16, max_reps=4096):
     """Replicas of one projection's weights (codes, scales, bias), enough that
     cycling through them moves >= ROTATE_BYTES of weights, in one arena; the
     activation and output rows are shared, as in a model step, where the
-    previous operator has just written them.  Returns (arena, linears)."""
+    previous operator has just written them.  tmp_w: the fp32 weight scratch
+    (a capi.DevBuf of at least N * K * 4 bytes).  Returns (arena, linears)."""
+    check_scratch(tmp_w, N, K)
     ab, ob = (2 if act == F16 else 4), (2 if outd == F16 else 4)
     wsz = [N * K, 4 * N] + ([4 * N] if bias else [])
     per = arena_size(wsz)
@@ -193,9 +227,12 @@ def graph_rotation(ev, lins, stream, min_calls=60):
         for g in graphs:
             ev.launch(g, stream)
 
-    one_pass(0)
-    passes = max(2, -(-min_calls // len(lins)))
-    return timed(ev, one_pass, passes, stream) / len(lins)
+    try:
+        one_pass(0)
+        passes = max(2, -(-min_calls // len(lins)))
+        return timed(ev, one_pass, passes, stream) / len(lins)
+    finally:
+        ev.drop(*graphs)
 
 
 def timed_rotation(ev, lins, steps, stream=None):
@@ -212,15 +249,18 @@ class Linear:
     """One quantized projection resident in HBM with its input/output rows."""
 
     def __init__(self, arena, tmp_w, M, N, K, bias, residual, seed, act=F16, outd=F16, xy=None):
-        """xy: (x, y) device pointers to share instead of rows of its own."""
+        """tmp_w: the device scratch (a capi.DevBuf) that holds the N x K fp32
+        weights before quantization; xy: (x, y) device pointers to share
+        instead of rows of its own."""
+        check_scratch(tmp_w, N, K)
         self.M, self.N, self.K, self.has_bias, self.has_res = M, N, K, bias, residual
         self.act, self.outd = act, outd
         ab, ob = (2 if act == F16 else 4), (2 if outd == F16 else 4)
         self.w = arena.take(N * K)
         self.s = arena.take(4 * N)
         self.b = arena.take(4 * N) if bias else None
-        capi.call("vvh_fill_normal", tmp_w, F32, N * K, seed, 0.0, 0.02, None)
-        capi.call("vvh_quantize_per_channel", tmp_w, N, K, self.w, self.s, None)
+        capi.call("vvh_fill_normal", tmp_w.ptr, F32, N * K, seed, 0.0, 0.02, None)
+        capi.call("vvh_quantize_per_channel", tmp_w.ptr, N, K, self.w, self.s, None)
         if bias:
             capi.call("vvh_fill_normal", self.b, F32, N, seed + 1, 0.0, 0.01, None)
         if xy is None:
@@ -362,22 +402,28 @@ def cpu_baseline(lins, budget_s):
     core = allowed[0]
     os.sched_setaffinity(0, {core})
     try:
-        passes, t0 = 0, time.perf_counter()
-        while True:
+        def one_pass():
+            t = time.perf_counter()
             for f, a in calls:
                 f(*a)
-            passes += 1
-            el = time.perf_counter() - t0
-            if el >= budget_s:
-                break
+            return time.perf_counter() - t
+
+        one_pass()  # warm-up: first touch of the host copies, caches, clocks
+        times, t0 = [], time.perf_counter()
+        while len(times) < 20 or time.perf_counter() - t0 < budget_s:
+            times.append(one_pass())
+        el = time.perf_counter() - t0
         ingest = cpu_ingest(layer_projs(896, 128, 4864))
     finally:
         os.sched_setaffinity(0, set(allowed))
-    return dict(value=round(per_pass * passes / el / 1e9, 3), unit="GB/s", cores=1, kind=kind,
+    med = float(np.median(times))
+    return dict(value=round(per_pass / med / 1e9, 3), unit="GB/s", cores=1, kind=kind,
                 host_cpu=host_cpu(), nproc=os.cpu_count(), cpus_allowed=len(allowed), pinned_core=core,
-                ms_per_step=round(el / passes * 1e3, 3), ingest_host_path=ingest,
-                sample=(f"{passes} full passes of the 24-layer decode projection set (168 linear_q8 calls, "
-                        f"same int8 weights as the GPU run, fp32 activations) in {el:.1f} s, one thread pinned to core {core}; "
+                ms_per_step=round(med * 1e3, 3), ms_per_step_mean=round(el / len(times) * 1e3, 3),
+                timed_passes=len(times), ingest_host_path=ingest,
+                sample=(f"one warm-up pass, then {len(times)} timed passes (the median reported) of the 24-layer "
+                        f"decode projection set (168 linear_q8 calls, same int8 weights as the GPU run, fp32 "
+                        f"activations) in {el:.1f} s, one thread pinned to core {core}; "
                         + ("reference BackendCPU::linear_q8 compiled from its sources -O2 -mavx2 -mfma"
                            if kind == "reference" else "oracle restatement of BackendCPU::linear_q8")))
 
@@ -433,7 +479,7 @@ def main():
     tmp_w = capi.DevBuf(max(inter * h, 151936 * 896, 8960 * 1536) * 4)
 
     t_setup = time.perf_counter()
-    sets = build_decode_set(args.replicas, L, projs, tmp_w.ptr)
+    sets = build_decode_set(args.replicas, L, projs, tmp_w)
     plans = [make_plan(lins) for _, lins in sets]
     step_bytes = sum(l.bytes for l in sets[0][1])
     print(f"[bench] {name}: {args.replicas} x {len(sets[0][1])} projections, "
@@ -483,7 +529,7 @@ def main():
     }
 
     if not args.no_extras:
-        result["extras"] = extras(ev, sets, projs, tmp_w.ptr, args)
+        result["extras"] = extras(ev, sets, projs, tmp_w, args)
     if not args.no_cpu:
         print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(sets[0][1], args.cpu_seconds)
@@ -531,7 +577,7 @@ def prefill_main(args, ev, name):
     runs on the null stream, where the HIP events are recorded."""
     M, N, K = args.prefill_m, QWEN05["inter"], QWEN05["hidden"]
     tmp_w = capi.DevBuf(N * K * 4)
-    _ar, lins = rotation(tmp_w.ptr, M, N, K, False, False, 900)
+    _ar, lins = rotation(tmp_w, M, N, K, False, False, 900)
     for i in range(args.warmup):
         lins[i % len(lins)].run()
     ms = timed_rotation(ev, lins, args.steps)
@@ -561,7 +607,7 @@ def lm_head_main(args, ev, name):
     against the HBM peak."""
     N, K = 151936, QWEN05["hidden"]
     tmp_w = capi.DevBuf(N * K * 4)
-    _ar, heads = rotation(tmp_w.ptr, 1, N, K, False, False, 777, F16, F32)
+    _ar, heads = rotation(tmp_w, 1, N, K, False, False, 777, F16, F32)
     for i in range(args.warmup):
         heads[i % len(heads)].run()
     ms = timed(ev, lambda i: heads[i % len(heads)].run(), args.steps)
@@ -619,7 +665,7 @@ def vendor_gemm_main(args, ev):
         reps = []
         for r in range(2):
             ar = Arena(arena_size(Linear.sizes(M, N, K, False)))
-            reps.append((ar, Linear(ar, tmp_w.ptr, M, N, K, False, name.startswith("down"), 900 + r)))
+            reps.append((ar, Linear(ar, tmp_w, M, N, K, False, name.startswith("down"), 900 + r)))
         for i in range(args.warmup):
             reps[i % 2][1].run()
         ms = timed(ev, lambda i: reps[i % 2][1].run(), args.steps)
@@ -696,6 +742,11 @@ def extras(ev, sets, projs, tmp_w, args):
     for i in range(5):
         ev.launch(graphs[i % len(graphs)], stream)
     ms = timed(ev, lambda i: ev.launch(graphs[i % len(graphs)], stream), reps, stream)
+    ev.drop(*graphs)
+    for seq in order_plans:
+        for kind, item in seq:
+            if kind == "plan":
+                capi.call("vvh_plan_destroy", item)
     out["model_order_graph"] = {"launches_per_step": 4 * L, "ms_per_step": round(ms, 5),
                                 "GBps": round(step_bytes / (ms * 1e-3) / 1e9, 2)}
     print(f"[bench] model order (graph) {ms * 1e3:.1f} us", file=sys.stderr, flush=True)
@@ -710,6 +761,7 @@ def extras(ev, sets, projs, tmp_w, args):
         for i in range(3):
             ev.launch(pg[i % len(pg)], stream)
         ms = timed(ev, lambda i: ev.launch(pg[i % len(pg)], stream), 30, stream)
+        ev.drop(*pg)
         us = ms * 1e3 / L
         b = algo_bytes(1, N, K, bias, res)
         calls[name] = {"N": N, "K": K, "us": round(us, 2), "GBps": round(b / (us * 1e-6) / 1e9, 1),
@@ -846,6 +898,7 @@ def extras(ev, sets, projs, tmp_w, args):
         for i in range(3):
             ev.launch(g, stream)
         ms_graph = timed(ev, lambda i: ev.launch(g, stream), 50, stream)
+        ev.drop(g)
         e2e[f"{head}_lm_head" + ("_fused" if fused else "")] = {"calls_per_step": m.calls_per_step(), "position": P,
                                   "us_per_token_graph": round(ms_graph * 1e3, 1),
                                   "tok_per_s_graph": round(1e3 / ms_graph, 1),

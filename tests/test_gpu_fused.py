@@ -163,7 +163,9 @@ def test_plan_input_stage(gpu):
 @pytest.mark.parametrize("M,inter,K,bias,outd,stage", [(1, 4864, 896, False, F16, True), (1, 136, 256, True, F16, False),
                                                         (3, 512, 896, True, F32, True), (4, 8, 1536, False, F16, False),
                                                         (2, 8960, 1536, False, F16, True),
-                                                        (6, 512, 896, True, F16, False), (8, 72, 2048, False, F32, False)])
+                                                        (6, 512, 896, True, F16, False), (8, 72, 2048, False, F32, False),
+                                                        # 17 tiles with the stage: the last block's idle tiles
+                                                        (1, 136, 256, True, F16, True), (2, 40, 512, True, F32, True)])
 def test_plan_glu_epilogue(gpu, M, inter, K, bias, outd, stage):
     """gate/up as a plan with the SiLU-gated epilogue (and the RMSNorm input
     stage): bit for bit the plain plan's [gate | up] rows through
@@ -243,6 +245,8 @@ def _qkv_plan(bufs, src, ws, M, K, outd):
     (2, 12, 2, 128, 5, F32, True),
     (5, 4, 2, 64, 100, F16, False),    # 5-8 rows: the MFMA dot path's 8-row operands
     (8, 8, 2, 128, 3, F32, False),
+    (1, 3, 1, 32, 9, F16, True),       # head_dim 32 and 48: tile counts that leave idle tiles in the last block
+    (1, 5, 1, 48, 3, F16, True),
 ])
 def test_plan_rope_epilogue(gpu, M, H, KVH, D, pos, outd, stage):
     """RoPE and the K/V cache append as the epilogue of the q/k/v plan

@@ -117,7 +117,8 @@ QWEN05_LAYER = [  # (name, N, K, bias, residual)
 @pytest.mark.parametrize("proj", QWEN05_LAYER, ids=[p[0] for p in QWEN05_LAYER])
 def test_config2_qwen05_decode(gpu, oracle, proj, outd):
     name, N, K, bias, res = proj
-    run_case(oracle, 1, N, K, F16, outd, bias=bias, res=res, seed=hash(name) % 1000)
+    seed = 200 + [p[0] for p in QWEN05_LAYER].index(name)  # fixed per projection: a failure replays
+    run_case(oracle, 1, N, K, F16, outd, bias=bias, res=res, seed=seed)
 
 
 def test_config3_lm_head(gpu, oracle):

@@ -553,15 +553,19 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
     // pair (h*D + 8s + r, + D/2) of tile s of head h (rope_d % 16 == 0 and
     // N % rope_d == 0, checked when the plan gets its RoPE epilogue)
     const bool pair = a.rope == 1 || a.rope == 2;
+    // an idle tile past the problem (the partly filled last block of a
+    // launch) takes tile 0's rows, so its early loads of scales, biases,
+    // residuals and weights stay inside the problem; it stores nothing
+    const int64_t tile_r = n0 < a.N ? c.tile : 0;
     int64_t rowA, rowB;
     if (pair) {
         const int64_t tph = a.rope_d / 16;
-        const int64_t hd = c.tile / tph, sd = c.tile - hd * tph;
+        const int64_t hd = tile_r / tph, sd = tile_r - hd * tph;
         rowA = hd * a.rope_d + 8 * sd + r;
         rowB = rowA + a.rope_d / 2;
     } else if (a.glu) {
         // gate row 8 t + r and its up row (N % 16 == 0: every tile is whole)
-        rowA = c.tile * 8 + r;
+        rowA = tile_r * 8 + r;
         rowB = a.N / 2 + rowA;
     } else {
         rowA = n0 + r < a.N ? n0 + r : a.N - 1;

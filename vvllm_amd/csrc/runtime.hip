@@ -154,22 +154,38 @@ int workspace_for(void* stream, std::size_t bytes, float** out)
 }
 
 // The stream's decode-attention counters: allocated on first use and zeroed
-// by a kernel queued on the stream ahead of the call that needs them (a
-// kernel, not a memset, so that a capture of that call records it as a
-// kernel node); every call leaves them at zero again.
+// before this returns, by a kernel on a private non-blocking stream that the
+// host waits for.  So they are zero for the first direct call and for the
+// first replay alike, also when the first use happens inside a capture of
+// `stream` (the private stream is not captured; no memset node is recorded);
+// every call leaves them at zero again.
+hipStream_t g_zero_stream[64] = {};
+
 int counters_for(void* stream, unsigned** out)
 {
     std::lock_guard<std::mutex> lock(g_wsmu);
     Workspace& w = g_ws[stream];
     if (!w.cnt) {
+        if (g_device < 0 || g_device >= 64) return fail(VVH_ERR_UNSUPPORTED, "device %d out of range", g_device);
+        hipStream_t& zs = g_zero_stream[g_device];
+        if (!zs) {
+            const hipError_t e = hipStreamCreateWithFlags(&zs, hipStreamNonBlocking);
+            if (e != hipSuccess) {
+                (void)hipGetLastError();
+                zs = nullptr;
+                return fail_hip(e, "attention counters: private stream");
+            }
+        }
         void* p = nullptr;
         hipError_t e = hipMalloc(&p, (std::size_t)kAttnCounters * sizeof(unsigned));
         if (e != hipSuccess) {
             (void)hipGetLastError();
             return fail_hip(e, "attention counters hipMalloc");
         }
-        const int st = launch_zero_u32(static_cast<unsigned*>(p), kAttnCounters, stream);
+        int st = launch_zero_u32(static_cast<unsigned*>(p), kAttnCounters, zs);
+        if (st == 0) st = (int)hipStreamSynchronize(zs);
         if (st != 0) {
+            (void)hipGetLastError();
             (void)hipFree(p);
             return fail_hip((hipError_t)st, "attention counters zero launch");
         }
@@ -1503,10 +1519,14 @@ VVH_API int vvh_plan_set_rope(vvh_plan plan, size_t q_index, size_t k_index, siz
     if (head_dim < 16 || head_dim % 16 != 0 || head_dim > 4096)
         return fail(VVH_ERR_UNSUPPORTED, "RoPE epilogue needs head_dim a multiple of 16 (got %zu)", head_dim);
     if (!(theta > 0.0f) || !std::isfinite(theta)) return fail(VVH_ERR_INVALID_ARG, "theta must be positive");
+    // the change is made on a copy of the plan's entries and becomes the
+    // plan's only once the device table holds it, so a failed call (a
+    // capture in progress, an allocation failure) leaves the plan as it was
+    std::vector<LinArgs> next = p.args;
     LinArgs* q = nullptr;
     LinArgs* k = nullptr;
     LinArgs* v = nullptr;
-    for (LinArgs& a : p.args) {
+    for (LinArgs& a : next) {
         if ((size_t)a.src == q_index) q = &a;
         if ((size_t)a.src == k_index) k = &a;
         if ((size_t)a.src == v_index) v = &a;
@@ -1518,6 +1538,20 @@ VVH_API int vvh_plan_set_rope(vvh_plan plan, size_t q_index, size_t k_index, siz
         q->M != k->M)
         return fail(VVH_ERR_INVALID_ARG, "q rows (%lld), k and v rows (%lld, %lld) must be whole heads of %zu, with "
                     "k and v alike and one M", (long long)q->N, (long long)k->N, (long long)v->N, head_dim);
+    // the table is read by launches already queued: replace it once they are done
+    hipError_t fe = hipDeviceSynchronize();
+    if (fe != hipSuccess) return fail_hip(fe, "plan RoPE epilogue: synchronize (no change made)");
+    // the pair frequencies, worked out once on the device by the function
+    // vvh_rope uses
+    float* freq = nullptr;
+    fe = hipMalloc(&freq, head_dim / 2 * sizeof(float));
+    if (fe == hipSuccess) fe = (hipError_t)launch_rope_freq(freq, (int64_t)head_dim, theta, nullptr);
+    if (fe == hipSuccess) fe = hipDeviceSynchronize();
+    if (fe != hipSuccess) {
+        (void)hipGetLastError();
+        if (freq) (void)hipFree(freq);
+        return fail_hip(fe, "RoPE frequency table (no change made)");
+    }
     q->rope = 1;
     k->rope = 2;
     v->rope = 3;
@@ -1528,23 +1562,21 @@ VVH_API int vvh_plan_set_rope(vvh_plan plan, size_t q_index, size_t k_index, siz
     q->cache = nullptr;
     k->cache = k_cache;
     v->cache = v_cache;
-    // the table is read by launches already queued: replace it once they are done
-    (void)hipDeviceSynchronize();
-    // the pair frequencies, worked out once on the device by the function
-    // vvh_rope uses
-    if (p.rope_freq) p.rope_retired.push_back(p.rope_freq);
-    p.rope_freq = nullptr;
-    hipError_t fe = hipMalloc(&p.rope_freq, head_dim / 2 * sizeof(float));
-    if (fe == hipSuccess) fe = (hipError_t)launch_rope_freq(p.rope_freq, (int64_t)head_dim, theta, nullptr);
-    if (fe == hipSuccess) fe = hipDeviceSynchronize();
-    if (fe != hipSuccess) {
-        q->rope = k->rope = v->rope = 0;
-        return fail_hip(fe, "RoPE frequency table");
-    }
-    q->rope_freq = k->rope_freq = p.rope_freq;
-    const hipError_t e = hipMemcpy(const_cast<LinArgs*>(p.sargs.table), p.args.data(), p.args.size() * sizeof(LinArgs),
+    q->rope_freq = k->rope_freq = freq;
+    const hipError_t e = hipMemcpy(const_cast<LinArgs*>(p.sargs.table), next.data(), next.size() * sizeof(LinArgs),
                                    hipMemcpyHostToDevice);
-    return e == hipSuccess ? VVH_OK : fail_hip(e, "plan table upload");
+    if (e != hipSuccess) {
+        // the device table may hold part of the new entries: put the old ones back
+        (void)hipGetLastError();
+        (void)hipMemcpy(const_cast<LinArgs*>(p.sargs.table), p.args.data(), p.args.size() * sizeof(LinArgs),
+                        hipMemcpyHostToDevice);
+        (void)hipFree(freq);
+        return fail_hip(e, "plan table upload (no change made)");
+    }
+    if (p.rope_freq) p.rope_retired.push_back(p.rope_freq);
+    p.rope_freq = freq;
+    p.args = std::move(next);
+    return VVH_OK;
 }
 
 VVH_API int vvh_plan_set_glu(vvh_plan plan, size_t index)
@@ -1565,12 +1597,22 @@ VVH_API int vvh_plan_set_glu(vvh_plan plan, size_t index)
                     (long long)g->N);
     if (g->res) return fail(VVH_ERR_INVALID_ARG, "SiLU-gated epilogue takes no residual");
     if (g->rope) return fail(VVH_ERR_INVALID_ARG, "a problem with a RoPE epilogue cannot be SiLU-gated");
-    g->glu = 1;
-    // the table is read by launches already queued: replace it once they are done
-    (void)hipDeviceSynchronize();
-    const hipError_t e = hipMemcpy(const_cast<LinArgs*>(p.sargs.table), p.args.data(), p.args.size() * sizeof(LinArgs),
-                                   hipMemcpyHostToDevice);
-    return e == hipSuccess ? VVH_OK : fail_hip(e, "plan table upload");
+    // the table is read by launches already queued: replace it once they
+    // are done; the plan's entries change only once the upload succeeded
+    hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) return fail_hip(e, "plan SiLU-gated epilogue: synchronize (no change made)");
+    std::vector<LinArgs> next = p.args;
+    next[(size_t)(g - p.args.data())].glu = 1;
+    e = hipMemcpy(const_cast<LinArgs*>(p.sargs.table), next.data(), next.size() * sizeof(LinArgs),
+                  hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        (void)hipMemcpy(const_cast<LinArgs*>(p.sargs.table), p.args.data(), p.args.size() * sizeof(LinArgs),
+                        hipMemcpyHostToDevice);
+        return fail_hip(e, "plan table upload (no change made)");
+    }
+    p.args = std::move(next);
+    return VVH_OK;
 }
 
 VVH_API int vvh_plan_destroy(vvh_plan plan)
