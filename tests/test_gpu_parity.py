@@ -657,7 +657,7 @@ def test_headline_plan_every_projection(gpu, oracle):
 
     projs = bench.layer_projs(896, 128, 4864)
     tmp = capi.DevBuf(4864 * 896 * 4)
-    (arena, lins), = bench.build_decode_set(1, 24, projs, tmp.ptr)
+    (arena, lins), = bench.build_decode_set(1, 24, projs, tmp)
     plan = bench.make_plan(lins)
     assert capi.plan_kernel(plan) == "dot"
     before = []

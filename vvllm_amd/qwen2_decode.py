@@ -74,6 +74,8 @@ class _Q8:
         self.q = capi.DevBuf(N * K)
         self.s = capi.DevBuf(N * 4)
         if src is None:
+            if tmp.nbytes < N * K * 4:
+                raise ValueError(f"weight scratch of {tmp.nbytes} bytes is too small for {N} x {K} fp32 weights")
             capi.call("vvh_fill_normal", tmp.ptr, F32, N * K, seed, 0.0, 0.02, None)
             src = tmp
         capi.call("vvh_quantize_per_channel", src.ptr, N, K, self.q.ptr, self.s.ptr, None)
