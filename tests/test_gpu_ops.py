@@ -228,10 +228,13 @@ def test_attention_unaligned_cache(gpu, oracle, d):
 
 # K % 8 == 0 takes the 16-byte-load kernel (K = 8, K past one 2048-wide
 # round of loads), K = 130 the element-wise one
-DENSE = [(1, 896, 896), (3, 1000, 130), (7, 40, 4864), (1, 151936, 896), (2, 64, 8), (5, 300, 2056)]
+DENSE = [(1, 896, 896), (3, 1000, 130), (7, 40, 4864), (1, 151936, 896), (2, 64, 8), (5, 300, 2056),
+         # the streaming form (M <= 4, N >= 16384): a row tail (16390 % 16), a k tail
+         # inside the last 128-byte step (904), a single step (64), M = 3 and 4
+         (2, 16390, 904), (4, 20000, 64), (3, 16384, 1000)]
 
 
-@pytest.mark.parametrize("d,wd", [(F32, F32), (F16, F16), (F16, F32)])
+@pytest.mark.parametrize("d,wd", [(F32, F32), (F16, F16), (F16, F32), (F32, F16)])
 @pytest.mark.parametrize("M,N,K", DENSE)
 def test_dense(gpu, oracle, M, N, K, d, wd):
     print(f"[case] dense M={M} N={N} K={K} dtype={d} wdtype={wd}", flush=True)

@@ -1094,11 +1094,175 @@ __global__ __launch_bounds__(256) void k_dense_vec(T* __restrict__ out, const T*
     }
 }
 
+// The same product for M <= 4 activation rows over many weight rows (the
+// tied LM head, 151936 x 896 fp16 weights), laid out like the int8 decode
+// kernel k_dot: a wave owns a tile of 16 weight rows, lane l reads the
+// 16-byte chunk l % 8 of one 128-byte line of rows n0 + l / 8 and
+// n0 + 8 + l / 8, so every load instruction covers 8 rows x one whole cache
+// line, and a ring of D k steps (one line of each row per step) is in flight;
+// each slot also carries the lane's activation chunk of that step.  While
+// steps remain beyond the ring, the slot consumed is refilled with the step D
+// ahead (past the range it re-reads the last step, never consumed), so every
+// wait counts the same D - 1 steps of loads.  fp16 x fp16 products go
+// through v_dot2_f32_f16 (exact products, fp32 sums), other types through
+// fp32 FMAs; the 8 chunk lanes of a row are summed at the end.  k_dense_vec
+// keeps one row per wave and two 16-byte loads in flight per lane, which
+// held the LM head to 4.1 TB/s.
+template <typename T, int E>
+struct alignas(sizeof(T) * E >= 16 ? 16 : sizeof(T) * E) DenseX {
+    T v[E];
+};
+
+template <typename T, typename WT, int MT, int D>
+__global__ __launch_bounds__(256) void k_dense_stream(T* __restrict__ out, const T* __restrict__ x,
+                                                      const WT* __restrict__ w, const float* __restrict__ bias,
+                                                      const T* res, int64_t M, int64_t N, int64_t K)
+{
+    constexpr int E = 16 / (int)sizeof(WT);  // weights per 16-byte chunk
+    constexpr int STEP = 8 * E;              // k per step: one 128-byte line of each row
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane >> 3, c = lane & 7;
+    const int64_t n0 = ((int64_t)blockIdx.x * 4 + wave) * 16;
+    if (n0 >= N) return;  // no block-wide synchronisation below
+    const int64_t rowA = n0 + r < N ? n0 + r : N - 1;
+    const int64_t rowB = n0 + 8 + r < N ? n0 + 8 + r : N - 1;
+    const WT* wa = w + rowA * K;
+    const WT* wb = w + rowB * K;
+    const int32_t steps = (int32_t)((K + STEP - 1) / STEP);
+    const int32_t kmax = (int32_t)K - E;  // last chunk start of a row (K % E == 0)
+    struct Slot {
+        u4 wA, wB;
+        DenseX<T, E> xv[MT];
+    };
+    Slot ring[D];
+    auto issue = [&](int u, int32_t st) {
+        st = st < steps ? st : steps - 1;  // past the range: re-read the last step (never consumed)
+        int32_t k = st * STEP + c * E;
+        k = k < kmax ? k : kmax;
+        ring[u].wA = __builtin_nontemporal_load(reinterpret_cast<const u4*>(wa + k));
+        ring[u].wB = __builtin_nontemporal_load(reinterpret_cast<const u4*>(wb + k));
+#pragma unroll
+        for (int m = 0; m < MT; m++)
+            ring[u].xv[m] = *reinterpret_cast<const DenseX<T, E>*>(x + (m < M ? m : 0) * K + k);
+    };
+    float accA[MT], accB[MT];
+#pragma unroll
+    for (int m = 0; m < MT; m++) accA[m] = accB[m] = 0.0f;
+    auto consume = [&](int u, int32_t st) {
+        const bool kv = st * STEP + c * E < K;  // chunk inside the row (a K tail reads a clamped chunk)
+        if constexpr (sizeof(WT) == 2 && sizeof(T) == 2) {
+            const h8 a = __builtin_bit_cast(h8, ring[u].wA), b = __builtin_bit_cast(h8, ring[u].wB);
+#pragma unroll
+            for (int m = 0; m < MT; m++) {
+                h8 xh = __builtin_bit_cast(h8, ring[u].xv[m]);
+                xh = (kv && m < M) ? xh : h8{};
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    accA[m] = __builtin_amdgcn_fdot2(h2{a[2 * j], a[2 * j + 1]}, h2{xh[2 * j], xh[2 * j + 1]},
+                                                     accA[m], false);
+                    accB[m] = __builtin_amdgcn_fdot2(h2{b[2 * j], b[2 * j + 1]}, h2{xh[2 * j], xh[2 * j + 1]},
+                                                     accB[m], false);
+                }
+            }
+        } else {
+            const auto a = __builtin_bit_cast(DenseX<WT, E>, ring[u].wA);
+            const auto b = __builtin_bit_cast(DenseX<WT, E>, ring[u].wB);
+#pragma unroll
+            for (int m = 0; m < MT; m++) {
+                const bool on = kv && m < M;
+#pragma unroll
+                for (int e = 0; e < E; e++) {
+                    const float xf = on ? (float)ring[u].xv[m].v[e] : 0.0f;
+                    accA[m] += xf * (float)a.v[e];
+                    accB[m] += xf * (float)b.v[e];
+                }
+            }
+        }
+    };
+    int32_t st = 0;
+#pragma unroll
+    for (int u = 0; u < D; u++) issue(u, u);
+    for (; st + D < steps; st += D) {
+#pragma unroll
+        for (int u = 0; u < D; u++) {
+            consume(u, st + u);
+            __builtin_amdgcn_sched_barrier(0);
+            issue(u, st + u + D);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < D; u++)
+        if (st + u < steps) consume(u, st + u);
+#pragma unroll
+    for (int m = 0; m < MT; m++) {
+        accA[m] = group_sum(accA[m], 8);
+        accB[m] = group_sum(accB[m], 8);
+    }
+    if (c != 0) return;
+#pragma unroll
+    for (int m = 0; m < MT; m++) {
+        if (m >= M) continue;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int64_t n = n0 + 8 * h + r;
+            if (n >= N) continue;
+            const int64_t o = m * N + n;
+            float y = (h ? accB[m] : accA[m]) + (bias ? bias[n] : 0.0f);
+            if (res) y += ldf(res, o);
+            stf(out, o, y);
+        }
+    }
+}
+
+// rows of weights from which the streaming form pays (one block of 4 wave
+// tiles of 16 rows per CU at least)
+constexpr int64_t kDenseStreamMinN = 16384;
+
+template <typename T, typename WT>
+static void dense_stream_go(void* out, const void* x, const void* w, const float* bias, const void* res, int64_t M,
+                            int64_t N, int64_t K, hipStream_t s)
+{
+    constexpr int E = 16 / (int)sizeof(WT);
+    const int64_t steps = (K + 8 * E - 1) / (8 * E);
+    const dim3 grid((unsigned)(((N + 15) / 16 + 3) / 4));
+#define VVH_DS(MT, D)                                                                                                     hipLaunchKernelGGL((k_dense_stream<T, WT, MT, D>), grid, dim3(256), 0, s, (T*)out, (const T*)x, (const WT*)w,                          bias, (const T*)res, M, N, K)
+    if (M == 1) {
+        if (steps >= 7) VVH_DS(1, 7);
+        else VVH_DS(1, 4);
+    } else if (M == 2) {
+        if (steps >= 7) VVH_DS(2, 7);
+        else VVH_DS(2, 4);
+    } else {
+        VVH_DS(4, 4);
+    }
+#undef VVH_DS
+}
+
 int launch_dense(void* out, const void* x, const void* w, int wdtype, const float* bias, const void* res, int64_t M,
                  int64_t N, int64_t K, int dtype, void* stream)
 {
     const dim3 grid((unsigned)((N + 3) / 4));
     hipStream_t s = static_cast<hipStream_t>(stream);
+    {
+        // the streaming form: M <= 4, many rows, rows of whole 16-byte chunks,
+        // 16-byte aligned weights and activations aligned for their chunks
+        const int64_t e = wdtype == VVH_F16 ? 8 : 4;
+        const uintptr_t xal = (uintptr_t)(e * (dtype == VVH_F16 ? 2 : 4));
+        const bool stream_ok = M >= 1 && M <= 4 && N >= kDenseStreamMinN && K >= e && K % e == 0 &&
+                               reinterpret_cast<uintptr_t>(w) % 16 == 0 &&
+                               reinterpret_cast<uintptr_t>(x) % (xal < 16 ? xal : 16) == 0;
+        if (stream_ok) {
+            if (dtype == VVH_F16) {
+                if (wdtype == VVH_F16) dense_stream_go<f16, f16>(out, x, w, bias, res, M, N, K, s);
+                else dense_stream_go<f16, float>(out, x, w, bias, res, M, N, K, s);
+            } else {
+                if (wdtype == VVH_F16) dense_stream_go<float, f16>(out, x, w, bias, res, M, N, K, s);
+                else dense_stream_go<float, float>(out, x, w, bias, res, M, N, K, s);
+            }
+            return (int)hipGetLastError();
+        }
+    }
     const bool vec = K % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0;
 #define VVH_DENSE(T, WT)                                                                                              \
     if (vec)                                                                                                          \
