@@ -230,12 +230,18 @@ VVH_API int vvh_linear_q8_dev(void* out, const void* inp, const int8_t* dev_weig
                               const void* residual, size_t M, size_t N, size_t K,
                               int act_dtype, int out_dtype, void* stream);
 
-/* Size of the fixed device scratch of vvh_linear_q8_dev_noalloc: the split-K
- * partial planes of one call (M * N * 4 bytes per split).  On a 256-CU
- * device every split the dispatcher makes fits: it splits only GEMMs of at
- * most 128 output tiles of 64 x 128, into at most 256 blocks, i.e. at most
- * 256 fp32 tiles of 32 KiB = 8 MiB of planes. */
-#define VVH_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+/* Size of the fixed device scratch of vvh_linear_q8_dev_noalloc.  One call
+ * needs the split-K partial planes (M * N * 4 bytes per split; on a 256-CU
+ * device the dispatcher splits only GEMMs of at most 128 output tiles of
+ * 64 x 128, into at most 256 blocks: at most 256 fp32 tiles of 32 KiB =
+ * 8 MiB) plus, for fp32 activations on the GEMM (M >= 16), their split fp16
+ * form: M * K * 4 bytes and M * 4 bytes, each rounded up to 256.  32 MiB
+ * holds every fp16-activation call and fp32-activation calls up to about
+ * 6 M activation elements (the configs[3] shapes in fp32 up to M = 1024 at
+ * K = 4864, e.g. the down projection at M = 512: 9.96 MB + 4 planes of
+ * 1.84 MB); a call that needs more returns VVH_ERR_UNSUPPORTED before any
+ * launch (vvh_linear_q8_dev runs it). */
+#define VVH_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
 /* vvh_linear_q8_dev that allocates nothing: same arguments, same kernels and
  * the same result bits as vvh_linear_q8_dev, but the split-K partial planes
  * go to a fixed VVH_NOALLOC_SCRATCH_BYTES device array that the library
@@ -243,8 +249,8 @@ VVH_API int vvh_linear_q8_dev(void* out, const void* inp, const int8_t* dev_weig
  * stream's workspace (which grows with hipMalloc); so do the split
  * activations of an fp32-activation GEMM (M >= 16: M * K * 4 + M * 4 bytes).
  * No hipMalloc, hipFree or allocating library routine is called.  A call
- * whose workspace needs more than VVH_NOALLOC_SCRATCH_BYTES returns
- * VVH_ERR_UNSUPPORTED.
+ * whose workspace needs more than VVH_NOALLOC_SCRATCH_BYTES (the bound above)
+ * returns VVH_ERR_UNSUPPORTED and launches nothing.
  * No counterpart in the reference; for callers that cannot allocate: code
  * under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc.  All calls on one device share the one array, so calls that
