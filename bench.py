@@ -438,11 +438,24 @@ def main():
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--workload", choices=("decode", "prefill", "lm-head", "vendor-gemm", "copy"), default="decode",
+    ap.add_argument("--workload", choices=("decode", "prefill", "lm-head", "vendor-gemm", "copy", "configs",
+                                           "dense-head"),
+                    default="decode",
                     help="decode: configs[1] (the headline line); prefill: configs[3] gate/up GEMM only; "
                          "lm-head: configs[2] alone; "
                          "vendor-gemm: the int8 GEMM beside the vendor fp16 GEMM on the prefill shapes; "
-                         "copy: a 256 MiB device-to-device copy, the calibration of the HBM traffic counters")
+                         "copy: a 256 MiB device-to-device copy, the calibration of the HBM traffic counters; "
+                         "configs: every configs[3] and configs[4] (M = 1, 16, 256) shape, bracketed for "
+                         "rocprofv3 (see --trace-configs); dense-head: the dense fp16 tied LM head (vvh_dense)")
+    ap.add_argument("--trace-configs", metavar="KERNEL_TRACE_CSV",
+                    help="summarise the rocprofv3 kernel trace of a --workload configs run per shape and kernel "
+                         "(needs --configs-json, the run's JSON line; --pmc adds counter CSVs); no GPU is used")
+    ap.add_argument("--configs-json", metavar="FILE", help="the JSON line printed by --workload configs")
+    ap.add_argument("--pmc", nargs="*", metavar="COUNTER_CSV", help="rocprofv3 --pmc CSVs of the same workload")
+    ap.add_argument("--markdown", action="store_true", help="--trace-configs: also print a markdown table")
+    ap.add_argument("--max-replicas", type=int, default=4096,
+                    help="--workload configs: at most this many weight replicas per shape (counter runs, where "
+                         "every set-up kernel is serialised, use few)")
     ap.add_argument("--prefill-m", type=int, default=512)
     ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
                     help="summarise a rocprofv3 --kernel-trace CSV of a bench run: the dispatches of the kernel "
@@ -456,6 +469,8 @@ def main():
     args = ap.parse_args()
     if args.trace_summary:
         return trace_summary(args)
+    if args.trace_configs:
+        return configs_summary(args)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build targets one MI355X; the int8 linear path is measured on one GPU "
               "(multi-GPU sharding is design-only). Run with --gpus 1.", file=sys.stderr)
@@ -474,6 +489,10 @@ def main():
         return vendor_gemm_main(args, ev)
     if args.workload == "copy":
         return copy_main(args, ev)
+    if args.workload == "configs":
+        return configs_main(args, ev)
+    if args.workload == "dense-head":
+        return dense_head_main(args, ev)
     h, kv, inter, L = QWEN05["hidden"], QWEN05["kv"], QWEN05["inter"], QWEN05["layers"]
     projs = layer_projs(h, kv, inter)
     tmp_w = capi.DevBuf(max(inter * h, 151936 * 896, 8960 * 1536) * 4)
@@ -626,6 +645,165 @@ def lm_head_main(args, ev, name):
         "roofline": {"bound": "hbm", "kernel": "k_dot<float>", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
         "cpu_baseline": None}), flush=True)
+
+
+# The per-shape profiling workload: BASELINE.json configs[3] (both MLP shapes at
+# M = 128, 512, 2048) and configs[4] (the Qwen2.5-1.5B shapes at M = 1, 16, 256),
+# fp16 activations and outputs; the down projections add their residual in place
+# (as the model calls them, include/vvllm/model/transformer.h:187-188).
+CONFIG_SHAPES = [(f"c3_{nm}_M{M}", M, N, K, res) for M in (128, 512, 2048)
+                 for nm, N, K, res in (("gate_up", 4864, 896, False), ("down", 896, 4864, True))] + \
+                [(f"c4_{nm}_M{M}", M, N, K, False) for M in (1, 16, 256)
+                 for nm, N, K in (("qo", 1536, 1536), ("kv", 256, 1536), ("gate_up", 8960, 1536), ("down", 1536, 8960))]
+
+
+def separator(buf):
+    """A kernel that no linear_q8 call uses (vvh_argmax over 1 value, which
+    runs k_sample_part): it brackets each shape's timed calls in a rocprofv3
+    kernel trace."""
+    capi.call("vvh_argmax", buf.ptr, 1, buf.ptr + 64, None)
+
+
+def configs_main(args, ev):
+    """Every configs[3] / configs[4] shape, one after the other: weight replicas
+    rotated (>= 1 GiB, as rotation()), one untimed pass over them, then
+    --steps calls launched one by one on the null stream between two
+    separator kernels.  Under rocprofv3 --kernel-trace (or --pmc) the calls
+    of shape i are the dispatches between separators 2i and 2i+1; run
+    bench.py --trace-configs on that trace for the per-kernel durations.  The
+    JSON line gives each shape's kernel, algorithmic bytes and flops and the
+    HIP-event time per call (launches from Python: the host's launch rate
+    bounds the small shapes; the kernel durations come from the trace)."""
+    tmp = capi.DevBuf(8960 * 1536 * 4)
+    sep = capi.DevBuf(256)
+    capi.call("vvh_fill_normal", sep.ptr, F32, 1, 1, 0.0, 1.0, None)
+    out = {}
+    for name, M, N, K, res in CONFIG_SHAPES:
+        print(f"[bench] {name}: set-up", file=sys.stderr, flush=True)
+        _ar, lins = rotation(tmp, M, N, K, False, res, 900, max_reps=args.max_replicas)
+        for l in lins:
+            l.run()
+        capi.sync()
+        separator(sep)
+        ms = timed(ev, lambda i: lins[i % len(lins)].run(), args.steps)
+        separator(sep)
+        capi.sync()
+        l = lins[0]
+        out[name] = {"M": M, "N": N, "K": K, "residual": res, "kernel": kernel_name(M, N, K),
+                     "calls": args.steps, "bytes": l.bytes, "flops": l.flops, "us_events": round(ms * 1e3, 3),
+                     "replicas_rotated": len(lins)}
+        print(f"[bench] {name}: {ms * 1e3:.2f} us/call (events) {out[name]['kernel']}", file=sys.stderr, flush=True)
+        del lins, _ar
+    print(json.dumps({"workload": "configs", "order": [s[0] for s in CONFIG_SHAPES], "shapes": out}), flush=True)
+
+
+def configs_summary(args):
+    """Per-shape kernel durations of a --workload configs run from its
+    rocprofv3 kernel trace (and counters from --pmc traces of the same
+    workload): the dispatches between separator pairs, grouped by kernel;
+    per call the algorithmic bytes and flops over the summed kernel means.
+    One JSON line; with --markdown, a table as well."""
+    import csv
+    import statistics
+    meta = json.load(open(args.configs_json))
+    order = meta["order"]
+
+    def segments(rows, key):
+        rows.sort(key=key)
+        segs, cur, open_ = [], None, False
+        prev_sep = False
+        for r in rows:
+            is_sep = "k_sample_part" in r["Kernel_Name"]  # vvh_argmax's kernel
+            if is_sep and not prev_sep:
+                if open_:
+                    segs.append(cur)
+                    open_ = False
+                else:
+                    cur, open_ = [], True
+            elif not is_sep and open_:
+                cur.append(r)
+            prev_sep = is_sep
+        return segs
+
+    rows = list(csv.DictReader(open(args.trace_configs)))
+    segs = segments(rows, lambda r: int(r["Start_Timestamp"]))
+    if len(segs) != len(order):
+        print(json.dumps({"error": f"{len(segs)} bracketed segments for {len(order)} shapes"}))
+        return
+    counters = {}
+    for path in args.pmc or []:
+        crow = list(csv.DictReader(open(path)))
+        # one row per (dispatch, counter): order dispatches by id
+        by_disp = {}
+        for r in crow:
+            d = by_disp.setdefault(int(r["Dispatch_Id"]), {"Kernel_Name": r["Kernel_Name"], "c": {}})
+            d["c"][r["Counter_Name"]] = d["c"].get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+        disp = [{"Kernel_Name": v["Kernel_Name"], "id": k, "c": v["c"]} for k, v in by_disp.items()]
+        for name, seg in zip(order, segments(disp, lambda r: r["id"])):
+            for r in seg:
+                kshort = r["Kernel_Name"].split("(")[0][:90]
+                acc = counters.setdefault(name, {}).setdefault(kshort, {})
+                for cn, cv in r["c"].items():
+                    acc.setdefault(cn, []).append(cv)
+    out = {}
+    for name, seg in zip(order, segs):
+        sh = meta["shapes"][name]
+        ks = {}
+        for r in seg:
+            kshort = r["Kernel_Name"].split("(")[0][:90]
+            ks.setdefault(kshort, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        kern = {}
+        per_call = 0.0
+        for k, d in ks.items():
+            mean = sum(d) / len(d)
+            per_call += mean * len(d) / sh["calls"]
+            kern[k] = {"dispatches": len(d), "mean_us": round(mean, 3), "median_us": round(statistics.median(d), 3),
+                       "min_us": round(min(d), 3), "max_us": round(max(d), 3)}
+            c = counters.get(name, {}).get(k)
+            if c:
+                kern[k]["counters_mean"] = {cn: round(sum(v) / len(v), 1) for cn, v in c.items()}
+        out[name] = {**sh, "kernels": kern, "kernel_us_per_call": round(per_call, 3),
+                     "GBps": round(sh["bytes"] / (per_call * 1e-6) / 1e9, 1),
+                     "hbm_frac": round(sh["bytes"] / (per_call * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                     "TFLOPS": round(sh["flops"] / (per_call * 1e-6) / 1e12, 1),
+                     "mfma_frac": round(sh["flops"] / (per_call * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}
+    print(json.dumps({"configs": out}))
+    if args.markdown:
+        print("\n| Shape | Kernel | Calls | Mean µs | Median µs | Bytes | GB/s | HBM frac | TFLOP/s | MFMA frac |")
+        print("|---|---|---|---|---|---|---|---|---|---|")
+        for name in order:
+            o = out[name]
+            for i, (k, v) in enumerate(o["kernels"].items()):
+                head = (f"| {name} | `{k}` | {v['dispatches']} | {v['mean_us']} | {v['median_us']} | ")
+                if i == 0:
+                    print(head + f"{o['bytes']} | {o['GBps']} | {o['hbm_frac']} | {o['TFLOPS']} | {o['mfma_frac']} |")
+                else:
+                    print(head + "| | | | |")
+
+
+def dense_head_main(args, ev):
+    """The tied LM head as the reference computes it (a dense linear over the
+    fp16 embedding table, transformer.h:202-203 -> backend_cuda.cc:171-179):
+    vvh_dense, M = 1, N = 151936, K = 896, fp16 weights, activations and
+    logits; 4 replicas of the 272 MB table rotated (1.09 GB), calls launched
+    one by one on the null stream (each is longer than its launch) and timed
+    with HIP events.  One JSON line in GB/s against the HBM peak."""
+    N, K, reps = 151936, QWEN05["hidden"], 4
+    tables = [capi.DevBuf(N * K * 2) for _ in range(reps)]
+    for i, t in enumerate(tables):
+        capi.call("vvh_fill_normal", t.ptr, F16, N * K, 40 + i, 0.0, 0.02, None)
+    x, y = capi.DevBuf(K * 2), capi.DevBuf(N * 2)
+    capi.call("vvh_fill_normal", x.ptr, F16, K, 7, 0.0, 1.0, None)
+    run = lambda i: capi.call("vvh_dense", y.ptr, x.ptr, tables[i % reps].ptr, F16, None, None, 1, N, K, F16, None)
+    for i in range(max(args.warmup, reps)):
+        run(i)
+    ms = timed(ev, run, args.steps)
+    b = N * K * 2 + K * 2 + N * 2
+    gbs = b / (ms * 1e-3) / 1e9
+    print(f"[bench] dense fp16 LM head {ms * 1e3:.2f} us, {gbs:.0f} GB/s", file=sys.stderr, flush=True)
+    print(json.dumps({"workload": "dense fp16 LM head (vvh_dense, M=1, N=151936, K=896)", "us": round(ms * 1e3, 3),
+                      "GBps": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": b,
+                      "steps": args.steps, "replicas_rotated": reps}), flush=True)
 
 
 def copy_main(args, ev):

@@ -31,6 +31,10 @@ struct LinArgs {
     float* ws;
     int32_t nsplit;
     int32_t kstages;
+    // GEMM tile numbering: 0 = row blocks fastest (consecutive tiles share
+    // their codes), 1 = column blocks fastest (consecutive tiles share their
+    // activation rows); each XCD runs a contiguous range of tiles
+    int32_t norder;
     // k_dot input stage (activations staged in LDS only): xop 0 = inp as is,
     // 1 = RMSNorm of each row of inp with weights xw and epsilon xeps (the
     // arithmetic of k_rms_norm), 2 = silu(gate) * up of rows [gate | up] of

@@ -178,11 +178,13 @@ __global__ __launch_bounds__(64 * (BM / 32 / TI) * WN, BM == 64 ? 2 : 1) void k_
     const int64_t nbn = (a.N + BN - 1) / BN;
     const int64_t tiles = nbm * nbn;
     const bool split = a.nsplit > 1;
-    // consecutive tiles (same n0) on one XCD
+    // consecutive tiles (same n0, or same m0 with a.norder) on one XCD
     const int64_t logical = xcd_remap(blockIdx.x, tiles * (split ? a.nsplit : 1));
     const int64_t ks = logical / tiles, tile = logical - ks * tiles;
-    const int64_t m0 = (tile % nbm) * BM;
-    const int64_t n0 = (tile / nbm) * BN;
+    const int64_t mb = a.norder ? tile / nbn : tile % nbm;
+    const int64_t nb = a.norder ? tile - mb * nbn : tile / nbm;
+    const int64_t m0 = mb * BM;
+    const int64_t n0 = nb * BN;
     const int64_t kbase = split ? ks * a.kstages : 0;  // first k stage of this block
 
     const int tid = threadIdx.x;

@@ -278,6 +278,31 @@ int gemm_splits(int64_t M, int64_t N, int64_t stages)
     return (int)s;
 }
 
+// k_gemm3 tile numbering.  Each XCD (with its own L2) runs a contiguous
+// range of about tiles * splits / 8 tiles.  Numbered row blocks fastest, the
+// range covers many row blocks of few column blocks (the activation rows of
+// all of them, the codes of few); column blocks fastest, the reverse.  The
+// order whose range touches fewer operand bytes is taken: the down
+// projection at M = 2048 (K = 4864: 32 x 7 tiles of 64 x 128) touches
+// 18.0 MB per XCD row-fastest (28 row blocks of 622 KB of activations)
+// against 6.8 MB column-fastest, and moved 155.7 MB of HBM traffic per call
+// for 31.6 MB of algorithmic bytes row-fastest (rocprofv3 FETCH_SIZE).
+// Measured (graph replay, every order forced in turn): that down projection
+// 31.3 us row-fastest, 28.0 column-fastest; gate/up at M = 2048 (128 x 192,
+// row-fastest kept) 30.5 against 31.5 us; the other configs[3] / configs[4]
+// GEMM shapes alike within 0.3 us either way.
+int gemm3_norder(int64_t M, int64_t N, int64_t act_row_halfs, int64_t krange_codes, int layout, int64_t splits)
+{
+    const int64_t bm = gemm3_tile_m(layout), bn = gemm3_tile_n(layout);
+    const int64_t nbm = (M + bm - 1) / bm, nbn = (N + bn - 1) / bn;
+    const int64_t tiles = nbm * nbn;
+    const int64_t t = std::min(tiles, (tiles * splits + 7) / 8);  // one XCD's share, within one split
+    const double a_blk = (double)bm * (double)act_row_halfs * 2.0, b_blk = (double)bn * (double)krange_codes;
+    const double fp_m = (double)std::min(t, nbm) * a_blk + (double)((t + nbm - 1) / nbm) * b_blk;
+    const double fp_n = (double)((t + nbn - 1) / nbn) * a_blk + (double)std::min(t, nbn) * b_blk;
+    return fp_n < fp_m ? 1 : 0;
+}
+
 // k_gemm3 tile shape: split-K problems (few tiles, long K) take 64 x 128.
 // Unsplit ones take 64 x 128 when those tiles give every block a CU of its
 // own (then more CUs work than with 128-row tiles, each on half a tile:
@@ -617,7 +642,13 @@ int run_call(const LinArgs& base, int kernel, int act, int outd, void* stream, c
                     }
                     if (a.nsplit > 1) a.ws = reinterpret_cast<float*>(wb + xs_bytes + rs_bytes);
                 }
-                e = launch_gemm3(a, outd, gemm3_layout(a.M, a.N, a.nsplit), stream);
+                {
+                    const int layout = gemm3_layout(a.M, a.N, a.nsplit);
+                    const int64_t krange = a.nsplit > 1 ? (int64_t)a.kstages * kGemmBK : (a.bk ? a.bk : a.K);
+                    const int64_t arow = a.nsplit > 1 ? (int64_t)a.kstages * kGemmBK : a.K;
+                    a.norder = gemm3_norder(a.M, a.N, arow, krange, layout, a.nsplit);
+                    e = launch_gemm3(a, outd, layout, stream);
+                }
                 if (e == 0 && a.nsplit > 1) e = launch_splitk_reduce(a, outd, stream);
                 break;
             }
