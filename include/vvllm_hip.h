@@ -437,6 +437,29 @@ VVH_API int vvh_embedding(void* out, const float* dev_table, size_t token_id, si
 VVH_API int vvh_attention(void* out, const void* q, const void* k, const void* v, size_t n_q, size_t len0,
                           size_t num_heads, size_t num_kv_heads, size_t head_dim, float scale, int dtype,
                           void* stream);
+/* Decode attention split for a merge in the next linear (no counterpart in the
+ * reference: its transformer_forward runs attention and the o projection as
+ * two calls, transformer.h:168-178).  For a single query (n_q = 1) in fp16,
+ * head_dim 64 or 128, num_heads / num_kv_heads <= 16 and a span of at most
+ * 512 positions, writes *nparts part rows per query head to parts: part p of
+ * head h at parts + (p * num_heads + h) * (head_dim + 4), as head_dim
+ * numerator floats, the running maximum (log2 units) and the exponential
+ * sum.  parts_floats must cover *nparts * num_heads * (head_dim + 4) floats,
+ * *nparts <= 8 (4 for spans of at most 256).  parts 16-byte aligned; other
+ * shapes VVH_ERR_UNSUPPORTED.  vvh_linear_q8_dev_attn merges the parts into
+ * exactly the fp16 row vvh_attention writes for the same call. */
+VVH_API int vvh_attention_parts(float* parts, size_t parts_floats, size_t* nparts, const void* q, const void* k,
+                                const void* v, size_t len0, size_t num_heads, size_t num_kv_heads,
+                                size_t head_dim, float scale, int dtype, void* stream);
+/* vvh_linear_q8_dev (M = 1, fp16 activations) of the attention row merged
+ * from nparts parts of vvh_attention_parts (K = num_heads * head_dim): the
+ * attention output and the o projection (+ residual, may alias out) of a
+ * decode step in one launch, on the k_dot family, equal to vvh_attention
+ * followed by vvh_linear_q8_dev on that family.  K % 16 == 0, K <= 1024,
+ * 16-byte aligned parts and weights; otherwise VVH_ERR_UNSUPPORTED. */
+VVH_API int vvh_linear_q8_dev_attn(void* out, const float* parts, size_t nparts, size_t head_dim,
+                                   const int8_t* dev_weight, const float* dev_scales, const float* dev_bias,
+                                   const void* residual, size_t N, size_t K, int out_dtype, void* stream);
 /* Dense linear with fp32 or fp16 weights (wdtype): out[M,N] = x[M,K] . W[N,K]^T
  * + bias[N] (+ residual[M,N], may alias out) -- Backend::linear / linear_add
  * (:139-156, :302-320); the fp32 model path and the tied LM head. */

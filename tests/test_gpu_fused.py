@@ -2,8 +2,9 @@
 
 vvh_linear_q8_dev_in (RMSNorm or SiLU-mul as the input stage of a decode
 linear), vvh_plan_set_input_op (the same for a grouped q/k/v plan) and
-vvh_rope_append (RoPE writing the KV-cache rows) compute exactly what the
-reference's separate calls compute (transformer.h:133-160, 176-185): rms_norm
+vvh_rope_append (RoPE writing the KV-cache rows) and vvh_attention_parts +
+vvh_linear_q8_dev_attn (attention merged in the o projection's input stage)
+compute exactly what the reference's separate calls compute (transformer.h:133-160, 176-185): rms_norm
 then linear, silu_mul then linear, rope then KVCache::append.  Each stage
 rounds as the standalone kernel, so every comparison here is bit-exact; the
 standalone kernels themselves are checked against the oracle in
@@ -313,6 +314,76 @@ def test_plan_rope_limits(gpu):
         capi.call("vvh_plan_destroy", h)
 
 
+# (len0, H, KVH, D): spans of 1 to 512 keys (4 parts up to 256, else 8),
+# grouped and plain heads, head_dim 64 and 128, K = H * D up to 1024
+ATTN_PARTS_CASES = [(1, 14, 2, 64), (2, 14, 2, 64), (63, 14, 2, 64), (64, 14, 2, 64), (65, 14, 2, 64),
+                    (200, 14, 2, 64), (256, 14, 2, 64), (257, 14, 2, 64), (511, 14, 2, 64), (512, 14, 2, 64),
+                    (100, 4, 4, 128), (384, 8, 2, 128), (512, 16, 1, 64), (300, 8, 1, 128)]
+
+
+@pytest.mark.parametrize("len0,H,KVH,D", ATTN_PARTS_CASES)
+@pytest.mark.parametrize("outd", [F16, F32], ids=["f16out", "f32out"])
+def test_attention_parts_o_projection(gpu, len0, H, KVH, D, outd):
+    """vvh_attention_parts then vvh_linear_q8_dev_attn (o + bias + residual in
+    place) against vvh_attention then vvh_linear_q8_dev on k_dot: the same
+    bits."""
+    print(f"[case] attention parts len0={len0} H={H} KVH={KVH} D={D} out={outd}", flush=True)
+    rng = np.random.default_rng(len0 * 131 + H * 7 + D)
+    K = N = H * D
+    q = rng.normal(0, 1, (H, D)).astype(np.float16)
+    kc = rng.normal(0, 1, (len0, KVH, D)).astype(np.float16)
+    vc = rng.normal(0, 1, (len0, KVH, D)).astype(np.float16)
+    dq, ds = q8_weight(rng, N, K)
+    bias = capi.DevBuf.from_array(rng.normal(0, 0.1, N).astype(np.float32))
+    res = rng.normal(0, 1, N).astype(np.float16 if outd == F16 else np.float32)
+    dqv, dk, dv = capi.DevBuf.from_array(q), capi.DevBuf.from_array(kc), capi.DevBuf.from_array(vc)
+    attn = capi.DevBuf(K * 2)
+    ref, got = capi.DevBuf.from_array(res), capi.DevBuf.from_array(res)
+    scale = float(1.0 / np.sqrt(np.float32(D)))
+    capi.call("vvh_attention", attn.ptr, dqv.ptr, dk.ptr, dv.ptr, 1, len0, H, KVH, D, scale, F16, None)
+    with dot_kernel():
+        capi.call("vvh_linear_q8_dev", ref.ptr, attn.ptr, dq.ptr, ds.ptr, bias.ptr, ref.ptr, 1, N, K, F16, outd, None)
+    nf = 8 * H * (D + 4)
+    parts = capi.DevBuf(nf * 4)
+    n = ctypes.c_size_t()
+    capi.call("vvh_attention_parts", parts.ptr, nf, ctypes.byref(n), dqv.ptr, dk.ptr, dv.ptr, len0, H, KVH, D,
+              scale, F16, None)
+    assert n.value == (4 if len0 <= 256 else 8)
+    capi.call("vvh_linear_q8_dev_attn", got.ptr, parts.ptr, n.value, D, dq.ptr, ds.ptr, bias.ptr, got.ptr, N, K,
+              outd, None)
+    u = np.uint16 if outd == F16 else np.uint32
+    a, b = ref.to_array(u, (N,)), got.to_array(u, (N,))
+    assert np.array_equal(a, b), f"{int((a != b).sum())} of {N} outputs differ"
+
+
+def test_attention_parts_limits(gpu):
+    H, KVH, D = 14, 2, 64
+    q, k, v = capi.DevBuf(H * D * 2), capi.DevBuf(600 * KVH * D * 2), capi.DevBuf(600 * KVH * D * 2)
+    nf = 8 * H * (D + 4)
+    parts = capi.DevBuf(nf * 4)
+    n = ctypes.c_size_t()
+    st = lambda *a: capi.status_of("vvh_attention_parts", *a)
+    invalid, unsupported = 1, 7
+    assert st(parts.ptr, nf, ctypes.byref(n), q.ptr, k.ptr, v.ptr, 513, H, KVH, D, 0.125, F16, None) == unsupported
+    assert st(parts.ptr, nf, ctypes.byref(n), q.ptr, k.ptr, v.ptr, 100, H, KVH, D, 0.125, F32, None) == unsupported
+    assert st(parts.ptr, nf, ctypes.byref(n), q.ptr, k.ptr, v.ptr, 100, 12, 2, 96, 0.125, F16, None) == unsupported
+    assert st(parts.ptr, nf - 1, ctypes.byref(n), q.ptr, k.ptr, v.ptr, 300, H, KVH, D, 0.125, F16, None) == invalid
+    assert st(parts.ptr, nf, None, q.ptr, k.ptr, v.ptr, 100, H, KVH, D, 0.125, F16, None) == invalid
+    assert st(parts.ptr, nf, ctypes.byref(n), q.ptr, k.ptr, v.ptr, 0, H, KVH, D, 0.125, F16, None) == invalid
+    assert st(parts.ptr, nf, ctypes.byref(n), q.ptr, k.ptr, v.ptr, 300, H, KVH, D, 0.125, F16, None) == 0
+    assert n.value == 8
+    rng = np.random.default_rng(5)
+    dq, ds = q8_weight(rng, 896, 896)
+    out = capi.DevBuf(896 * 2)
+    so = lambda *a: capi.status_of("vvh_linear_q8_dev_attn", *a)
+    assert so(out.ptr, parts.ptr, 0, D, dq.ptr, ds.ptr, None, None, 896, 896, F16, None) == invalid
+    assert so(out.ptr, parts.ptr, 9, D, dq.ptr, ds.ptr, None, None, 896, 896, F16, None) == invalid
+    assert so(out.ptr, parts.ptr, 8, 60, dq.ptr, ds.ptr, None, None, 896, 896, F16, None) == invalid
+    big_q, big_s = q8_weight(rng, 16, 1536)
+    assert so(out.ptr, parts.ptr, 8, 64, big_q.ptr, big_s.ptr, None, None, 16, 1536, F16, None) == unsupported
+    assert so(out.ptr, parts.ptr, 8, D, dq.ptr, ds.ptr, None, None, 896, 896, F16, None) == 0
+
+
 def fused_vs_unfused(cfg, head, steps, max_ctx):
     models = [qd.Model(cfg, act=F16, lm_head=head, max_ctx=max_ctx, seed=11, fused=f) for f in (False, True)]
     try:
@@ -342,3 +413,26 @@ def test_fused_step_small(gpu, head):
 @pytest.mark.parametrize("head", ["dense", "int8"])
 def test_fused_step_qwen25_05b_shapes(gpu, head):
     fused_vs_unfused(qd.QWEN25_05B, head, 2, 8)
+
+
+@pytest.mark.parametrize("P", [255, 256, 511, 600])
+def test_fused_step_late_positions(gpu, P):
+    """One step at a late position of a filled KV cache, Qwen2.5-0.5B shapes:
+    spans of 256 and 512 keys take the attention parts merged in the o
+    projection (4 and 8 parts), 257 the 8-part form with a short last chunk,
+    601 vvh_attention (the span over several blocks); the logits equal the
+    unfused step's bit for bit."""
+    cfg, max_ctx = qd.QWEN25_05B, 1024
+    models = [qd.Model(cfg, act=F16, lm_head="int8", max_ctx=max_ctx, seed=13, fused=f) for f in (False, True)]
+    try:
+        print(f"[case] fused step late position {P}", flush=True)
+        logits = []
+        for m in models:
+            m.fill_kv(5)
+            m.step(3, P)
+            logits.append(m.logits_host())
+        assert np.array_equal(logits[0].view(np.uint32), logits[1].view(np.uint32)), \
+            f"max difference {float(np.abs(logits[0] - logits[1]).max()):.3e}"
+    finally:
+        for m in models:
+            m.close()

@@ -96,6 +96,10 @@ SIGNATURES = {
     "vvh_embedding": (c_int, [c_void_p, c_void_p, c_size_t, c_size_t, c_size_t, c_int, c_void_p]),
     "vvh_attention": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_size_t, c_size_t, c_size_t,
                               c_size_t, c_float, c_int, c_void_p]),
+    "vvh_attention_parts": (c_int, [c_void_p, c_size_t, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t,
+                                    c_size_t, c_size_t, c_size_t, c_float, c_int, c_void_p]),
+    "vvh_linear_q8_dev_attn": (c_int, [c_void_p, c_void_p, c_size_t, c_size_t, c_void_p, c_void_p, c_void_p,
+                                       c_void_p, c_size_t, c_size_t, c_int, c_void_p]),
     "vvh_dense": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_size_t, c_size_t, c_size_t,
                           c_int, c_void_p]),
     "vvh_matmul": (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_size_t, c_size_t, c_int, c_void_p]),

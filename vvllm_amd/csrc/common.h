@@ -38,10 +38,16 @@ struct LinArgs {
     // k_dot input stage (activations staged in LDS only): xop 0 = inp as is,
     // 1 = RMSNorm of each row of inp with weights xw and epsilon xeps (the
     // arithmetic of k_rms_norm), 2 = silu(gate) * up of rows [gate | up] of
-    // 2K values (the arithmetic of k_eltwise's SiLU-mul).
+    // 2K values (the arithmetic of k_eltwise's SiLU-mul),
+    // 3 = the merge of decode-attention parts (one activation row): inp holds
+    // xparts blocks of K / xhd part rows of xhd + 4 floats [O, m, l, -, -]
+    // (k_attention_parts), element h xhd + d of the row is the merge of the
+    // parts of head h.
     const float* xw;
     float xeps;
     int32_t xop;
+    int32_t xparts;
+    int32_t xhd;
     // q/k/v plan epilogue with RoPE and the KV-cache append (k_dot plans,
     // vvh_plan_set_rope): rope 0 = plain store; 1 = q rows, rotated; 2 = k
     // rows, rotated and also written to row pos + m of `cache`; 3 = v rows,
@@ -124,6 +130,16 @@ inline int64_t decode_blocks(const LinArgs& a)
 // k_dot (M <= 16): 16-row tiles, 128-wide k steps, ksplit waves per tile.
 constexpr int64_t kDotMaxM = 16;
 constexpr int kStageMaxM = 4;  // rows of a decode linear with an input stage
+// attention merge stage: at most kAttnMaxParts parts, K <= kAttnMergeMaxK (4 per thread)
+constexpr int kAttnMaxParts = 8;
+constexpr int kAttnMergeMaxK = 1024;
+// k_dot first stages (requested ahead of the weight ring, a template
+// parameter of the kernel): none, RMSNorm (xop 1, M <= 4, K <= 2048), the
+// attention merge (xop 3)
+constexpr int kFirstNone = 0;
+constexpr int kFirstRms = 1;
+constexpr int kFirstAttn = 3;
+inline bool dot_first_rms_ok(int64_t M, int64_t K) { return M <= 4 && K <= 256 * 8; }
 constexpr int kDotStep = 128;               // k codes per row per step
 constexpr int64_t kDotLdsMax = 80 * 1024;   // dynamic LDS of one block at most
 constexpr int64_t kDotRedBytes = 4 * kDotMaxM * 16 * 4;
@@ -239,6 +255,11 @@ inline bool attention_decode_counted(const AttnDecodePlan& p) { return p.mfma &&
 int launch_attention_decode(const AttnDecodePlan& p, void* out, const void* q, const void* k, const void* v,
                             int64_t len, int64_t H, int64_t KVH, int64_t D, float scale, float* ws, unsigned* cnt,
                             int dtype, void* stream);
+// Per-wave parts of the decode attention (k_attention_parts) for spans the
+// matrix-core kernel takes in one block (mfma and nb == 1 in the plan);
+// nparts = that block's waves.  parts: nparts * H rows of D + 4 floats.
+int launch_attention_parts(float* parts, const void* q, const void* k, const void* v, int64_t len, int64_t H,
+                           int64_t KVH, int64_t D, float scale, int nparts, void* stream);
 int launch_zero_u32(unsigned* p, int64_t n, void* stream);
 int launch_copy2(void* d0, const void* s0, void* d1, const void* s1, int64_t bytes, void* stream);
 int launch_dense(void* out, const void* x, const void* w, int wdtype, const float* bias, const void* res, int64_t M,

@@ -62,6 +62,18 @@ __device__ __forceinline__ h8 i8x8_to_h8(const uint32_t w0, const uint32_t w1)
     return __builtin_bit_cast(h8, u4{c[0], c[1], c[2], c[3]});
 }
 
+// One step of merging decode-attention partials: a partial with running
+// maximum mi (log2 units), exponential sum li and numerator oi joins the
+// totals (num, den) under the common maximum M.  The attention kernel's merge
+// of its waves and the o-projection's merge stage (k_dot input stage 3) both
+// take it, in part order, so the two produce the same bits.
+__device__ __forceinline__ void attn_merge_add(float& num, float& den, float mi, float M, float oi, float li)
+{
+    const float f = exp2f(mi - M);
+    num = __builtin_fmaf(f, oi, num);
+    den = __builtin_fmaf(f, li, den);
+}
+
 // LDS reads done (lgkmcnt(0)), then s_barrier, without waiting on vector
 // memory loads.  Written with builtins so the compiler's wait-count tracking
 // sees the lgkmcnt(0); the empty asm with a memory clobber keeps the

@@ -529,7 +529,7 @@ __device__ __forceinline__ void dot_store_glu(const LinArgs& a, int64_t rowA, in
     }
 }
 
-template <typename OT, int MT, bool XLDS, bool EARLY, int DEPTH>
+template <typename OT, int MT, bool XLDS, bool EARLY, int DEPTH, int FS>
 __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* smem, int64_t pos)
 {
     // activations in the ring take 8 VGPRs per row and slot: halve the ring
@@ -702,13 +702,20 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
             for (int m = 0; m < MT; m++) rope_cs_freq(pos + m, rfreq, rc[m], rs[m]);
         }
     };
-    // RMSNorm stage of an early launch whose rows take one batch of
-    // sum-of-squares loads and one round of chunks per thread: the rows and
-    // norm weights are requested before the weight ring, so the sums, the
-    // block reduction and the normalization run while the weights are in
-    // flight (the in-order wait counter lets a wait for the rows leave the
-    // younger ring loads outstanding)
-    const bool rms_first = EARLY && XLDS && MT <= 4 && a.xop == 1 && a.K <= 256 * 8;
+    // First stages (FS, chosen per launch by the host): the stage's operands
+    // are requested before the weight ring and the stage runs while the
+    // weights are in flight (the in-order wait counter lets a wait for them
+    // leave the younger ring loads outstanding).
+    //   kFirstRms: the RMSNorm stage of an early launch whose rows take one
+    //     batch of sum-of-squares loads and one round of chunks per thread
+    //     (xop 1, M <= 4, K <= 2048);
+    //   kFirstAttn: the attention merge stage (xop 3, one row, K <= 1024).
+    // A compile-time choice: chosen at run time, the other path's ring issue
+    // comes before the stage's loads, and the compiler then waits for every
+    // older load before the stage's first one (a whole round trip).
+    constexpr bool rms_first = FS == kFirstRms && EARLY && XLDS && MT <= 4;
+    constexpr bool attn_first = FS == kFirstAttn && EARLY && XLDS && MT == 1;
+    constexpr bool first = rms_first || attn_first;
     if constexpr (EARLY) {
         const float* bp = a.bias ? a.bias : a.scales;  // absent bias / residual: in-bounds reads, unused
         const OT* rp = a.res ? static_cast<const OT*>(a.res) : reinterpret_cast<const OT*>(a.scales);
@@ -721,14 +728,16 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
             for (int m = 0; m < MT; m++) e_res[m][h] = *gbl(rp + (a.res && m < a.M ? m * a.N : 0) + rows[h]);
         }
         rope_load();
-        if (active && !rms_first) {
+        if constexpr (!first) {
+            if (active) {
 #pragma unroll
-            for (int u = 0; u < D; u++) issue(u, (int32_t)c.s0 + u);
+                for (int u = 0; u < D; u++) issue(u, (int32_t)c.s0 + u);
+            }
+            rope_prep();
         }
-        if (!rms_first) rope_prep();
     }
     if constexpr (XLDS && MT <= 4) {
-        if (rms_first) {
+        if constexpr (rms_first) {
             const int32_t K32 = (int32_t)a.K, xchunks = (int32_t)(a.M * a.K / 8);
             // M <= MT rows of K <= 2048: at most MT chunks of 8 per thread
             constexpr int XL = MT;
@@ -800,9 +809,55 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
                 *reinterpret_cast<h8*>(xs + row * ldx + col) = v;
             }
             __syncthreads();
+        } else if constexpr (attn_first) {
+            // element e = h hd + d of the row: the parts of head h merged in
+            // part order (what k_attention_decode_mfma does with its waves);
+            // thread t takes elements 4t .. 4t + 3 (K <= 1024).  No branch
+            // around the loads (a conditional load would make the compiler
+            // wait for every older one): slots past the part count re-read
+            // part np - 1 and threads past K / 4 the last chunk, unused
+            typedef float f2 __attribute__((ext_vector_type(2)));
+            typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+            const float* pp = static_cast<const float*>(a.inp);
+            const int32_t hd = a.xhd, np = a.xparts, pitch = hd + 4;
+            const int32_t heads = (int32_t)a.K / hd, chunks = (int32_t)a.K / 4;
+            const int32_t idx0 = (int32_t)threadIdx.x, idx = idx0 < chunks ? idx0 : chunks - 1;
+            const int32_t e0 = 4 * idx, h = e0 / hd, d0 = e0 - h * hd;
+            f4 po[kAttnMaxParts];
+            f2 pml[kAttnMaxParts];
+#pragma unroll
+            for (int pc = 0; pc < kAttnMaxParts; pc++) {
+                const int32_t pcc = pc < np ? pc : np - 1;
+                const float* pr = pp + ((int64_t)pcc * heads + h) * pitch;
+                po[pc] = *gbl(reinterpret_cast<const f4*>(pr + d0));
+                pml[pc] = *gbl(reinterpret_cast<const f2*>(pr + hd));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int u = 0; u < D; u++) issue(u, (int32_t)c.s0 + u);
+            __builtin_amdgcn_sched_barrier(0);
+            if (idx0 < chunks) {
+                float M = -INFINITY;
+#pragma unroll
+                for (int pc = 0; pc < kAttnMaxParts; pc++)
+                    if (pc < np) M = fmaxf(M, pml[pc][0]);
+                float num[4] = {0.0f, 0.0f, 0.0f, 0.0f}, den[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int pc = 0; pc < kAttnMaxParts; pc++) {
+                    if (pc < np) {
+#pragma unroll
+                        for (int j = 0; j < 4; j++)
+                            attn_merge_add(num[j], den[j], pml[pc][0], M, po[pc][j], pml[pc][1]);
+                    }
+                }
+                const h4 v = {(f16)(num[0] / den[0]), (f16)(num[1] / den[1]), (f16)(num[2] / den[2]),
+                              (f16)(num[3] / den[3])};
+                *reinterpret_cast<h4*>(xs + e0) = v;
+            }
+            __syncthreads();
         }
     }
-    if (XLDS && !rms_first) {
+    if constexpr (XLDS && !first) {
         // activations to LDS (through the input stage a.xop), 4 chunks of 8
         // values per thread per round; a round's loads are clamped into the
         // input and its stores masked, so all of them are in flight at once
@@ -1001,7 +1056,7 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
 // arguments, which arrive preloaded into registers at dispatch (up to 16
 // dwords; the struct is read from the kernel-argument segment when used).
 // A plain call has no RoPE or SiLU-gated epilogue.
-template <typename OT, int MT, bool XLDS, bool EARLY, int DEPTH>
+template <typename OT, int MT, bool XLDS, bool EARLY, int DEPTH, int FS>
 __global__ __launch_bounds__(256) void k_dot(const int8_t* w, const void* inp, const float* scales,
                                              const float* bias, const void* res, int32_t N, int32_t M, int32_t K,
                                              int32_t ksplit, const LinArgs a)
@@ -1019,7 +1074,7 @@ __global__ __launch_bounds__(256) void k_dot(const int8_t* w, const void* inp, c
     b.ksplit = ksplit;
     b.rope = 0;
     b.glu = 0;
-    dot_body<OT, MT, XLDS, EARLY, DEPTH>(b, blockIdx.x, dot_smem, 0);
+    dot_body<OT, MT, XLDS, EARLY, DEPTH, FS>(b, blockIdx.x, dot_smem, 0);
 }
 
 // Grouped launch.  count <= kDotInline: the problems are g.p[0, count) and
@@ -1029,7 +1084,7 @@ __global__ __launch_bounds__(256) void k_dot(const int8_t* w, const void* inp, c
 // registers at dispatch); larger plans: block b serves problem
 // table[block_prob[b]].  `pos`: the position of activation row 0 for
 // problems with a RoPE epilogue.
-template <typename OT, int MT, bool XLDS, bool EARLY, int DEPTH>
+template <typename OT, int MT, bool XLDS, bool EARLY, int DEPTH, int FS>
 __global__ __launch_bounds__(256) void k_dot_grouped(int32_t b1, int32_t b2, int32_t b3, int32_t count, int64_t pos,
                                                      const LinArgs* __restrict__ table,
                                                      const int32_t* __restrict__ block_prob, const DotGroup g)
@@ -1039,7 +1094,7 @@ __global__ __launch_bounds__(256) void k_dot_grouped(int32_t b1, int32_t b2, int
     LinArgs a;
     if (count <= kDotInline) a = g.p[(b >= b1) + (b >= b2) + (b >= b3)];
     else a = table[*cst(block_prob + b)];
-    dot_body<OT, MT, XLDS, EARLY, DEPTH>(a, b - a.block_begin, dot_smem, pos);
+    dot_body<OT, MT, XLDS, EARLY, DEPTH, FS>(a, b - a.block_begin, dot_smem, pos);
 }
 
 // ---------------------------------------------------------------------------
@@ -1590,32 +1645,42 @@ int launch_skinny_grouped(const LinArgs* dev_table, int count, int64_t total_blo
     return (int)hipGetLastError();
 }
 
-template <int MT, bool XLDS, bool EARLY, int DEPTH>
+template <int MT, bool XLDS, bool EARLY, int DEPTH, int FS>
 static void dot_launch(const LinArgs& a, int out, dim3 grid, size_t lds, hipStream_t s)
 {
     // dot_fits(N, K) holds (checked by the runtime)
     const int32_t N = (int32_t)a.N, M = (int32_t)a.M, K = (int32_t)a.K;
     if (out == VVH_F32)
-        hipLaunchKernelGGL((k_dot<float, MT, XLDS, EARLY, DEPTH>), grid, dim3(256), lds, s, a.w, a.inp, a.scales,
-                           a.bias, a.res, N, M, K, a.ksplit, a);
+        hipLaunchKernelGGL((k_dot<float, MT, XLDS, EARLY, DEPTH, FS>), grid, dim3(256), lds, s, a.w, a.inp,
+                           a.scales, a.bias, a.res, N, M, K, a.ksplit, a);
     else
-        hipLaunchKernelGGL((k_dot<f16, MT, XLDS, EARLY, DEPTH>), grid, dim3(256), lds, s, a.w, a.inp, a.scales,
-                           a.bias, a.res, N, M, K, a.ksplit, a);
+        hipLaunchKernelGGL((k_dot<f16, MT, XLDS, EARLY, DEPTH, FS>), grid, dim3(256), lds, s, a.w, a.inp,
+                           a.scales, a.bias, a.res, N, M, K, a.ksplit, a);
 }
 
-template <int MT, bool XLDS, bool EARLY>
+template <int MT, bool XLDS, bool EARLY, int FS>
 static void dot_launch_d(const LinArgs& a, int out, int depth, dim3 grid, size_t lds, hipStream_t s)
 {
-    if (depth <= 2) dot_launch<MT, XLDS, EARLY, 2>(a, out, grid, lds, s);
-    else if (depth <= 4) dot_launch<MT, XLDS, EARLY, 4>(a, out, grid, lds, s);
-    else dot_launch<MT, XLDS, EARLY, 7>(a, out, grid, lds, s);
+    if (depth <= 2) dot_launch<MT, XLDS, EARLY, 2, FS>(a, out, grid, lds, s);
+    else if (depth <= 4) dot_launch<MT, XLDS, EARLY, 4, FS>(a, out, grid, lds, s);
+    else dot_launch<MT, XLDS, EARLY, 7, FS>(a, out, grid, lds, s);
 }
 
+// first stages exist for early launches with staged activations only
 template <int MT, bool XLDS>
-static void dot_launch_e(const LinArgs& a, int out, bool early, int depth, dim3 grid, size_t lds, hipStream_t s)
+static void dot_launch_e(const LinArgs& a, int out, bool early, int fs, int depth, dim3 grid, size_t lds,
+                         hipStream_t s)
 {
-    if (early) dot_launch_d<MT, XLDS, true>(a, out, depth, grid, lds, s);
-    else dot_launch_d<MT, XLDS, false>(a, out, depth, grid, lds, s);
+    if (!early) {
+        dot_launch_d<MT, XLDS, false, kFirstNone>(a, out, depth, grid, lds, s);
+        return;
+    }
+    if constexpr (XLDS && MT <= 4) {
+        if (fs == kFirstRms) return dot_launch_d<MT, true, true, kFirstRms>(a, out, depth, grid, lds, s);
+        if constexpr (MT == 1)
+            if (fs == kFirstAttn) return dot_launch_d<MT, true, true, kFirstAttn>(a, out, depth, grid, lds, s);
+    }
+    dot_launch_d<MT, XLDS, true, kFirstNone>(a, out, depth, grid, lds, s);
 }
 
 int launch_dot(const LinArgs& a, int out, bool early, int depth, void* stream)
@@ -1625,21 +1690,26 @@ int launch_dot(const LinArgs& a, int out, bool early, int depth, void* stream)
     // weights (see dot_early)
     const bool xl = dot_x_in_lds(a.M, a.K) && (a.xop != 0 || !early);
     const size_t lds = (xl ? dot_lds_bytes(a.M, a.K) : (size_t)kDotRedBytes) + (a.M > 2 ? kDotWtBytes : 0);
+    // the attention merge stage exists only as a first stage (any block count)
+    if (a.xop == 3) early = true;
+    const int fs = !(early && xl) ? kFirstNone
+                   : a.xop == 3 ? kFirstAttn
+                   : (a.xop == 1 && dot_first_rms_ok(a.M, a.K)) ? kFirstRms : kFirstNone;
     if (a.M <= 1) {
-        if (xl) dot_launch_e<1, true>(a, out, early, depth, grid, lds, S(stream));
-        else dot_launch_e<1, false>(a, out, early, depth, grid, lds, S(stream));
+        if (xl) dot_launch_e<1, true>(a, out, early, fs, depth, grid, lds, S(stream));
+        else dot_launch_e<1, false>(a, out, early, fs, depth, grid, lds, S(stream));
     } else if (a.M <= 2) {
-        if (xl) dot_launch_e<2, true>(a, out, early, depth, grid, lds, S(stream));
-        else dot_launch_e<2, false>(a, out, early, depth, grid, lds, S(stream));
+        if (xl) dot_launch_e<2, true>(a, out, early, fs, depth, grid, lds, S(stream));
+        else dot_launch_e<2, false>(a, out, early, fs, depth, grid, lds, S(stream));
     } else if (a.M <= 4) {
-        if (xl) dot_launch_e<4, true>(a, out, early, depth, grid, lds, S(stream));
-        else dot_launch_e<4, false>(a, out, early, depth, grid, lds, S(stream));
+        if (xl) dot_launch_e<4, true>(a, out, early, fs, depth, grid, lds, S(stream));
+        else dot_launch_e<4, false>(a, out, early, fs, depth, grid, lds, S(stream));
     } else if (a.M <= 8) {
-        if (xl) dot_launch_e<8, true>(a, out, early, depth, grid, lds, S(stream));
-        else dot_launch_e<8, false>(a, out, early, depth, grid, lds, S(stream));
+        if (xl) dot_launch_e<8, true>(a, out, early, fs, depth, grid, lds, S(stream));
+        else dot_launch_e<8, false>(a, out, early, fs, depth, grid, lds, S(stream));
     } else {
-        if (xl) dot_launch_e<16, true>(a, out, early, depth, grid, lds, S(stream));
-        else dot_launch_e<16, false>(a, out, early, depth, grid, lds, S(stream));
+        if (xl) dot_launch_e<16, true>(a, out, early, fs, depth, grid, lds, S(stream));
+        else dot_launch_e<16, false>(a, out, early, fs, depth, grid, lds, S(stream));
     }
     return (int)hipGetLastError();
 }
@@ -1654,31 +1724,37 @@ struct DotGroupArgs {
     DotGroup g;
 };
 
-template <int MT, bool XLDS, bool EARLY, int DEPTH>
+template <int MT, bool XLDS, bool EARLY, int DEPTH, int FS>
 static void dot_grouped_launch(const DotGroupArgs& k, int out, dim3 grid, size_t lds, hipStream_t s)
 {
     if (out == VVH_F32)
-        hipLaunchKernelGGL((k_dot_grouped<float, MT, XLDS, EARLY, DEPTH>), grid, dim3(256), lds, s, k.b[0], k.b[1],
-                           k.b[2], k.count, k.pos, k.table, k.block_prob, k.g);
+        hipLaunchKernelGGL((k_dot_grouped<float, MT, XLDS, EARLY, DEPTH, FS>), grid, dim3(256), lds, s, k.b[0],
+                           k.b[1], k.b[2], k.count, k.pos, k.table, k.block_prob, k.g);
     else
-        hipLaunchKernelGGL((k_dot_grouped<f16, MT, XLDS, EARLY, DEPTH>), grid, dim3(256), lds, s, k.b[0], k.b[1],
-                           k.b[2], k.count, k.pos, k.table, k.block_prob, k.g);
+        hipLaunchKernelGGL((k_dot_grouped<f16, MT, XLDS, EARLY, DEPTH, FS>), grid, dim3(256), lds, s, k.b[0],
+                           k.b[1], k.b[2], k.count, k.pos, k.table, k.block_prob, k.g);
 }
 
-template <int MT, bool XLDS, bool EARLY>
+template <int MT, bool XLDS, bool EARLY, int FS>
 static void dot_grouped_launch_d(const DotGroupArgs& k, int out, int depth, dim3 grid, size_t lds, hipStream_t s)
 {
-    if (depth <= 2) dot_grouped_launch<MT, XLDS, EARLY, 2>(k, out, grid, lds, s);
-    else if (depth <= 4) dot_grouped_launch<MT, XLDS, EARLY, 4>(k, out, grid, lds, s);
-    else dot_grouped_launch<MT, XLDS, EARLY, 7>(k, out, grid, lds, s);
+    if (depth <= 2) dot_grouped_launch<MT, XLDS, EARLY, 2, FS>(k, out, grid, lds, s);
+    else if (depth <= 4) dot_grouped_launch<MT, XLDS, EARLY, 4, FS>(k, out, grid, lds, s);
+    else dot_grouped_launch<MT, XLDS, EARLY, 7, FS>(k, out, grid, lds, s);
 }
 
+// plans take the RMSNorm first stage only (no attention merge stage)
 template <int MT, bool XLDS>
-static void dot_grouped_launch_e(const DotGroupArgs& k, int out, bool early, int depth, dim3 grid, size_t lds,
-                                 hipStream_t s)
+static void dot_grouped_launch_e(const DotGroupArgs& k, int out, bool early, int fs, int depth, dim3 grid,
+                                 size_t lds, hipStream_t s)
 {
-    if (early) dot_grouped_launch_d<MT, XLDS, true>(k, out, depth, grid, lds, s);
-    else dot_grouped_launch_d<MT, XLDS, false>(k, out, depth, grid, lds, s);
+    if (!early) {
+        dot_grouped_launch_d<MT, XLDS, false, kFirstNone>(k, out, depth, grid, lds, s);
+        return;
+    }
+    if constexpr (XLDS && MT <= 4)
+        if (fs == kFirstRms) return dot_grouped_launch_d<MT, true, true, kFirstRms>(k, out, depth, grid, lds, s);
+    dot_grouped_launch_d<MT, XLDS, true, kFirstNone>(k, out, depth, grid, lds, s);
 }
 
 int launch_dot_grouped(const LinArgs* dev_table, const int32_t* dev_block_prob, const LinArgs* args, int count,
@@ -1699,21 +1775,25 @@ int launch_dot_grouped(const LinArgs* dev_table, const int32_t* dev_block_prob, 
             k.g.p[i] = args[i];
             if (i > 0) k.b[i - 1] = args[i].block_begin;
         }
+    // the RMSNorm first stage when every problem takes it
+    bool rms = early && x_in_lds && count > 0;
+    for (int i = 0; i < count; ++i) rms = rms && args[i].xop == 1 && dot_first_rms_ok(args[i].M, args[i].K);
+    const int fs = rms ? kFirstRms : kFirstNone;
     if (max_m <= 1) {
-        if (x_in_lds) dot_grouped_launch_e<1, true>(k, out, early, depth, grid, lds_bytes, s);
-        else dot_grouped_launch_e<1, false>(k, out, early, depth, grid, lds_bytes, s);
+        if (x_in_lds) dot_grouped_launch_e<1, true>(k, out, early, fs, depth, grid, lds_bytes, s);
+        else dot_grouped_launch_e<1, false>(k, out, early, fs, depth, grid, lds_bytes, s);
     } else if (max_m <= 2) {
-        if (x_in_lds) dot_grouped_launch_e<2, true>(k, out, early, depth, grid, lds_bytes, s);
-        else dot_grouped_launch_e<2, false>(k, out, early, depth, grid, lds_bytes, s);
+        if (x_in_lds) dot_grouped_launch_e<2, true>(k, out, early, fs, depth, grid, lds_bytes, s);
+        else dot_grouped_launch_e<2, false>(k, out, early, fs, depth, grid, lds_bytes, s);
     } else if (max_m <= 4) {
-        if (x_in_lds) dot_grouped_launch_e<4, true>(k, out, early, depth, grid, lds_bytes, s);
-        else dot_grouped_launch_e<4, false>(k, out, early, depth, grid, lds_bytes, s);
+        if (x_in_lds) dot_grouped_launch_e<4, true>(k, out, early, fs, depth, grid, lds_bytes, s);
+        else dot_grouped_launch_e<4, false>(k, out, early, fs, depth, grid, lds_bytes, s);
     } else if (max_m <= 8) {
-        if (x_in_lds) dot_grouped_launch_e<8, true>(k, out, early, depth, grid, lds_bytes, s);
-        else dot_grouped_launch_e<8, false>(k, out, early, depth, grid, lds_bytes, s);
+        if (x_in_lds) dot_grouped_launch_e<8, true>(k, out, early, fs, depth, grid, lds_bytes, s);
+        else dot_grouped_launch_e<8, false>(k, out, early, fs, depth, grid, lds_bytes, s);
     } else {
-        if (x_in_lds) dot_grouped_launch_e<16, true>(k, out, early, depth, grid, lds_bytes, s);
-        else dot_grouped_launch_e<16, false>(k, out, early, depth, grid, lds_bytes, s);
+        if (x_in_lds) dot_grouped_launch_e<16, true>(k, out, early, fs, depth, grid, lds_bytes, s);
+        else dot_grouped_launch_e<16, false>(k, out, early, fs, depth, grid, lds_bytes, s);
     }
     return (int)hipGetLastError();
 }

@@ -641,45 +641,36 @@ __device__ __forceinline__ h4v lds_read_tr16(const _Float16* p)
     return __builtin_bit_cast(h4v, v);
 }
 
-// What the first loads depend on comes first (q, k, v, the key range, the
-// head layout: 14 dwords, preloaded into registers at dispatch); G = H / KVH.
-template <int D, int kDecWaves>
-__global__ __launch_bounds__(64 * kDecWaves) void k_attention_decode_mfma(const f16* __restrict__ q,
-                                                               const f16* __restrict__ k, const f16* __restrict__ v,
-                                                               int64_t len, int64_t per_block, int32_t KVH, int32_t G,
-                                                               float scale_log2, f16* __restrict__ out,
-                                                               float* __restrict__ ws, unsigned* __restrict__ cnt)
+// The G query rows of kv head g as B operands of the score MFMAs (lane:
+// head l % 16, dims 32 s + 8 (l / 16) .. + 7; rows past G are zero).
+template <int D>
+__device__ __forceinline__ void attn_load_q(const f16* __restrict__ q, int g, int G, int lane, h8 (&qb)[D / 32])
+{
+    const int r = lane & 15, gr = lane >> 4;
+#pragma unroll
+    for (int s = 0; s < D / 32; s++) {
+        h8 z = {};
+        qb[s] = r < G ? *reinterpret_cast<const h8*>(q + ((int64_t)g * G + r) * D + 32 * s + 8 * gr) : z;
+    }
+}
+
+// One wave's share of a kv head's span: the chunks of 64 keys starting at
+// c0, c0 + cstep, ... below ke, folded into head (lane % 16)'s running max m
+// (log2 units), sum l and O^T fragments o.  vw: the wave's LDS region of
+// kDecChunk rows of D + 4 halves.  kh / vh: the kv head's column in the K / V
+// caches (row stride kvs).
+template <int D>
+__device__ __forceinline__ void attn_wave_chunks(const f16* __restrict__ kh, const f16* __restrict__ vh, int64_t kvs,
+                                                 const h8 (&qb)[D / 32], int64_t c0, int64_t cstep, int64_t ke,
+                                                 float scale_log2, _Float16* vw, int lane, float& m, float& l,
+                                                 f4 (&o)[D / 16])
 {
     constexpr int DS = D / 32;              // 32-dim steps of a score tile
     constexpr int DE = D / 16;              // 16-dim tiles of O^T
     constexpr int VP = D + 4;               // V row pitch in LDS (halves): 2-byte gathers conflict-free
     constexpr int VR = kDecChunk * D / 512; // 16-byte pieces of a chunk's V rows per lane
-    constexpr int OP = D + 4;               // O row pitch in LDS (floats)
-    static_assert(kDecWaves * kDecChunk * VP * 2 >= kDecWaves * 16 * OP * 4, "O aliases the V regions");
-    __shared__ __align__(16) _Float16 vs[kDecWaves * kDecChunk * VP];
-    __shared__ float wm[kDecWaves][16], wl[kDecWaves][16];
-    __shared__ int last_s;
-    const int g = blockIdx.x, tid = threadIdx.x, w = tid >> 6, lane = tid & 63, r = lane & 15, gr = lane >> 4;
-    const int H = G * KVH;
-    const int64_t kvs = (int64_t)KVH * D;
-    const int64_t kb = (int64_t)blockIdx.y * per_block;
-    const int64_t ke = kb + per_block < len ? kb + per_block : len;
-    const f16* kh = k + (int64_t)g * D;
-    const f16* vh = v + (int64_t)g * D;
-
-    h8 qb[DS];
-#pragma unroll
-    for (int s = 0; s < DS; s++) {
-        h8 z = {};
-        qb[s] = r < G ? *reinterpret_cast<const h8*>(q + ((int64_t)g * G + r) * D + 32 * s + 8 * gr) : z;
-    }
-    float m = -INFINITY, l = 0.0f;  // head r's running max (log2 units) and sum
-    f4 o[DE];
-#pragma unroll
-    for (int e = 0; e < DE; e++) o[e] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-    _Float16* vw = vs + w * kDecChunk * VP;
-
-    for (int64_t c0 = kb + (int64_t)w * kDecChunk; c0 < ke; c0 += kDecWaves * kDecChunk) {
+    const int r = lane & 15, gr = lane >> 4;
+    for (; c0 < ke; c0 += cstep) {
         // every row index clamped into the span: rows past it are loaded from
         // key ke - 1 and weighted 0.  Plain (cached) loads: a layer's K/V rows
         // are read again at the next token while the weights in between
@@ -762,6 +753,38 @@ __global__ __launch_bounds__(64 * kDecWaves) void k_attention_decode_mfma(const 
                 o[e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl[u], o[e], 0, 0, 0);
             }
     }
+}
+
+// What the first loads depend on comes first (q, k, v, the key range, the
+// head layout: 14 dwords, preloaded into registers at dispatch); G = H / KVH.
+template <int D, int kDecWaves>
+__global__ __launch_bounds__(64 * kDecWaves) void k_attention_decode_mfma(const f16* __restrict__ q,
+                                                               const f16* __restrict__ k, const f16* __restrict__ v,
+                                                               int64_t len, int64_t per_block, int32_t KVH, int32_t G,
+                                                               float scale_log2, f16* __restrict__ out,
+                                                               float* __restrict__ ws, unsigned* __restrict__ cnt)
+{
+    constexpr int DE = D / 16;              // 16-dim tiles of O^T
+    constexpr int VP = D + 4;               // V row pitch in LDS (halves)
+    constexpr int OP = D + 4;               // O row pitch in LDS (floats)
+    static_assert(kDecWaves * kDecChunk * VP * 2 >= kDecWaves * 16 * OP * 4, "O aliases the V regions");
+    __shared__ __align__(16) _Float16 vs[kDecWaves * kDecChunk * VP];
+    __shared__ float wm[kDecWaves][16], wl[kDecWaves][16];
+    __shared__ int last_s;
+    const int g = blockIdx.x, tid = threadIdx.x, w = tid >> 6, lane = tid & 63, r = lane & 15, gr = lane >> 4;
+    const int H = G * KVH;
+    const int64_t kvs = (int64_t)KVH * D;
+    const int64_t kb = (int64_t)blockIdx.y * per_block;
+    const int64_t ke = kb + per_block < len ? kb + per_block : len;
+
+    h8 qb[D / 32];
+    attn_load_q<D>(q, g, G, lane, qb);
+    float m = -INFINITY, l = 0.0f;  // head r's running max (log2 units) and sum
+    f4 o[DE];
+#pragma unroll
+    for (int e = 0; e < DE; e++) o[e] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    attn_wave_chunks<D>(k + (int64_t)g * D, v + (int64_t)g * D, kvs, qb, kb + (int64_t)w * kDecChunk,
+                        (int64_t)kDecWaves * kDecChunk, ke, scale_log2, vs + w * kDecChunk * VP, lane, m, l, o);
 
     // merge the waves: (max, sum) per head, O^T per head as rows of os
     __syncthreads();  // every wave is done with its V region
@@ -781,11 +804,8 @@ __global__ __launch_bounds__(64 * kDecWaves) void k_attention_decode_mfma(const 
         for (int ww = 0; ww < kDecWaves; ww++) M = fmaxf(M, wm[ww][h]);  // finite: wave 0 has a key
         float num = 0.0f, den = 0.0f;
 #pragma unroll
-        for (int ww = 0; ww < kDecWaves; ww++) {
-            const float f = exp2f(wm[ww][h] - M);  // 0 for a wave without keys
-            num += f * os[(ww * 16 + h) * OP + d];
-            den += f * wl[ww][h];
-        }
+        for (int ww = 0; ww < kDecWaves; ww++)  // a wave without keys adds exact zeros
+            attn_merge_add(num, den, wm[ww][h], M, os[(ww * 16 + h) * OP + d], wl[ww][h]);
         if (!split) {
             out[((int64_t)g * G + h) * D + d] = (f16)(num / den);
         } else {
@@ -823,6 +843,44 @@ __global__ __launch_bounds__(64 * kDecWaves) void k_attention_decode_mfma(const 
         out[((int64_t)g * G + h) * D + d] = (f16)(num / den);
     }
     if (tid == 0) cnt[g] = 0u;  // ready for the next call on this stream
+}
+
+// Decode attention as per-wave parts, for spans that k_attention_decode_mfma
+// takes in one block of W waves (nb == 1): block (g, w) is one wave doing
+// what wave w of that block does (the chunks w, w + W, ... of kv head g, the
+// same wave body) and writes, for each query head h = g G + r of the kv
+// head, its running max m, sum l and O (D values) to the part row
+// parts + (w H + h) (D + 4) as [O, m, l, -, -].  Merging the W part rows of a
+// head in part order (attn_merge_add, then num / den) repeats the block's
+// merge of its waves, so the output has the bits of the one-launch kernel;
+// the merge runs in the consumer (k_dot input stage 3).  One wave per block
+// spreads a kv head's K/V rows over W CUs instead of one.
+template <int D>
+__global__ __launch_bounds__(64) void k_attention_parts(const f16* __restrict__ q, const f16* __restrict__ k,
+                                                        const f16* __restrict__ v, int64_t len, int32_t KVH,
+                                                        int32_t G, float scale_log2, float* __restrict__ parts)
+{
+    constexpr int DE = D / 16;
+    __shared__ __align__(16) _Float16 vs[kDecChunk * (D + 4)];
+    const int g = blockIdx.x, w = blockIdx.y, lane = threadIdx.x, r = lane & 15, gr = lane >> 4;
+    const int W = (int)gridDim.y, H = G * KVH;
+    h8 qb[D / 32];
+    attn_load_q<D>(q, g, G, lane, qb);
+    float m = -INFINITY, l = 0.0f;
+    f4 o[DE];
+#pragma unroll
+    for (int e = 0; e < DE; e++) o[e] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    attn_wave_chunks<D>(k + (int64_t)g * D, v + (int64_t)g * D, (int64_t)KVH * D, qb, (int64_t)w * kDecChunk,
+                        (int64_t)W * kDecChunk, len, scale_log2, vs, lane, m, l, o);
+    if (r < G) {
+        float* pr = parts + ((int64_t)w * H + (int64_t)g * G + r) * (D + 4);
+#pragma unroll
+        for (int e = 0; e < DE; e++) *reinterpret_cast<f4*>(pr + 16 * e + 4 * gr) = o[e];
+        if (gr == 0) {
+            pr[D] = m;
+            pr[D + 1] = l;
+        }
+    }
 }
 
 __global__ void k_zero_u32(unsigned* __restrict__ p, int64_t n)
@@ -916,6 +974,21 @@ AttnDecodePlan attention_decode_plan(const void* q, int64_t len, int64_t H, int6
     }
     p.nb = (len + p.per_block - 1) / p.per_block;
     return p;
+}
+
+int launch_attention_parts(float* parts, const void* q, const void* k, const void* v, int64_t len, int64_t H,
+                           int64_t KVH, int64_t D, float scale, int nparts, void* stream)
+{
+    const dim3 grid((unsigned)KVH, (unsigned)nparts);
+    const float sl = (float)((double)scale * 1.4426950408889634);  // as launch_attention_decode
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (D == 64)
+        hipLaunchKernelGGL(k_attention_parts<64>, grid, dim3(64), 0, s, (const f16*)q, (const f16*)k, (const f16*)v,
+                           len, (int32_t)KVH, (int32_t)(H / KVH), sl, parts);
+    else
+        hipLaunchKernelGGL(k_attention_parts<128>, grid, dim3(64), 0, s, (const f16*)q, (const f16*)k, (const f16*)v,
+                           len, (int32_t)KVH, (int32_t)(H / KVH), sl, parts);
+    return (int)hipGetLastError();
 }
 
 int64_t attention_decode_ws_floats(const AttnDecodePlan& p, int64_t H, int64_t D)

@@ -1355,6 +1355,40 @@ VVH_API int vvh_linear_q8_dev_in(void* out, const void* inp, const int8_t* dev_w
     return run_call(a, K_DOT, act_dtype, out_dtype, stream);
 }
 
+VVH_API int vvh_linear_q8_dev_attn(void* out, const float* parts, size_t nparts, size_t head_dim,
+                                   const int8_t* dev_weight, const float* dev_scales, const float* dev_bias,
+                                   const void* residual, size_t N, size_t K, int out_dtype, void* stream)
+{
+    int st = validate_call(out, parts, dev_weight, dev_scales, 1, N, K, VVH_F16, out_dtype);
+    if (st != VVH_OK) return st;
+    if (nparts == 0 || nparts > (std::size_t)kAttnMaxParts)
+        return fail(VVH_ERR_INVALID_ARG, "nparts %zu outside 1..%d", nparts, kAttnMaxParts);
+    if (head_dim == 0 || head_dim % 4 != 0 || K % head_dim != 0)
+        return fail(VVH_ERR_INVALID_ARG, "K (%zu) must be a multiple of head_dim (%zu), itself of 4", K, head_dim);
+    if (K % 16 != 0 || K > (std::size_t)kAttnMergeMaxK || !dot_x_in_lds(1, (int64_t)K))
+        return fail(VVH_ERR_UNSUPPORTED, "attention merge stage needs K %% 16 == 0 and K <= %d (K=%zu)",
+                    (int)kAttnMergeMaxK, K);
+    if (N == 0) return VVH_OK;
+    REQUIRE_INIT();
+    if (!aligned16(dev_weight) || !aligned16(parts))
+        return fail(VVH_ERR_UNSUPPORTED, "attention merge stage needs 16-byte aligned weights and parts");
+    LinArgs a{};
+    a.out = out;
+    a.inp = parts;
+    a.res = residual;
+    a.w = dev_weight;
+    a.scales = dev_scales;
+    a.bias = dev_bias;
+    a.M = 1;
+    a.N = (int64_t)N;
+    a.K = (int64_t)K;
+    a.ksplit = 1;
+    a.xop = 3;
+    a.xparts = (int32_t)nparts;
+    a.xhd = (int32_t)head_dim;
+    return run_call(a, K_DOT, VVH_F16, out_dtype, stream);
+}
+
 VVH_API int vvh_linear_q8(void* out, const void* inp, vvh_weight weight, const void* residual, size_t M,
                           size_t N, size_t K, int act_dtype, int out_dtype, void* stream)
 {
@@ -1880,6 +1914,36 @@ VVH_API int vvh_attention(void* out, const void* q, const void* k, const void* v
     return ret_launch(launch_attention(out, q, k, v, (int64_t)n_q, (int64_t)len0, (int64_t)num_heads,
                                        (int64_t)num_kv_heads, (int64_t)head_dim, scale, dtype, stream),
                       "attention launch");
+}
+
+VVH_API int vvh_attention_parts(float* parts, size_t parts_floats, size_t* nparts, const void* q, const void* k,
+                                const void* v, size_t len0, size_t num_heads, size_t num_kv_heads,
+                                size_t head_dim, float scale, int dtype, void* stream)
+{
+    if (!nparts) return fail(VVH_ERR_INVALID_ARG, "nparts is null");
+    if (!act_ok(dtype)) return fail(VVH_ERR_INVALID_ARG, "bad dtype");
+    if (!parts || !q || !k || !v) return fail(VVH_ERR_INVALID_ARG, "null pointer");
+    if (num_heads == 0 || num_kv_heads == 0 || num_heads % num_kv_heads != 0)
+        return fail(VVH_ERR_INVALID_ARG, "num_heads %zu not a multiple of num_kv_heads %zu", num_heads, num_kv_heads);
+    if (len0 == 0) return fail(VVH_ERR_INVALID_ARG, "a query attends to at least one position");
+    if (dtype != VVH_F16 || (head_dim != 64 && head_dim != 128) || num_heads > 65535 ||
+        !attention_decode_ok(k, v, (int64_t)len0, (int64_t)num_heads, (int64_t)num_kv_heads, (int64_t)head_dim) ||
+        !aligned16(parts))
+        return fail(VVH_ERR_UNSUPPORTED, "attention parts need fp16, head_dim 64 or 128, num_heads / num_kv_heads "
+                    "<= 16 and 16-byte aligned q, k, v and parts");
+    const AttnDecodePlan p = attention_decode_plan(q, (int64_t)len0, (int64_t)num_heads, (int64_t)num_kv_heads,
+                                                   (int64_t)head_dim, dtype);
+    if (!p.mfma || p.nb != 1)
+        return fail(VVH_ERR_UNSUPPORTED, "a span of %zu positions is not one block per kv head (at most 512)", len0);
+    const std::size_t need = (std::size_t)p.waves * num_heads * (head_dim + 4);
+    if (parts_floats < need)
+        return fail(VVH_ERR_INVALID_ARG, "parts holds %zu floats, %zu needed", parts_floats, need);
+    REQUIRE_INIT();
+    const int st = ret_launch(launch_attention_parts(parts, q, k, v, (int64_t)len0, (int64_t)num_heads,
+                                                     (int64_t)num_kv_heads, (int64_t)head_dim, scale, p.waves, stream),
+                              "attention parts launch");
+    if (st == VVH_OK) *nparts = (std::size_t)p.waves;
+    return st;
 }
 
 VVH_API int vvh_dense(void* out, const void* x, const void* dev_weight, int wdtype, const float* dev_bias,

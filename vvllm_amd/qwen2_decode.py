@@ -19,8 +19,10 @@ fused=True (fp16 only) issues the same arithmetic in fewer launches: the
 RMSNorms before q/k/v and gate_up run in the input stage of those plans
 (vvh_plan_set_input_op), RoPE and the K/V cache rows are the epilogue of the
 q/k/v plan (vvh_plan_set_rope, vvh_plan_run_pos), the SiLU-mul is the
-epilogue of the gate_up plan (vvh_plan_set_glu), and the embedding row is
-gathered straight to fp16.  Each stage rounds exactly as the standalone
+epilogue of the gate_up plan (vvh_plan_set_glu), attention over spans of up
+to 512 positions runs as per-wave parts (vvh_attention_parts) that the o
+projection merges in its input stage (vvh_linear_q8_dev_attn), and the
+embedding row is gathered straight to fp16.  Each stage rounds exactly as the standalone
 operator, so the logits equal the unfused step's.  The final norm stays a
 launch of its own: every block of the LM head would repeat it.
 
@@ -62,6 +64,10 @@ class Config:
 
 # Qwen2.5-0.5B (src/config/config_test.cc:22-33 of the reference)
 QWEN25_05B = Config(hidden=896, heads=14, kv_heads=2, inter=4864, layers=24, vocab=151936)
+
+# Longest span that vvh_attention_parts takes (one block of 8 waves of 64
+# keys per kv head in the one-launch kernel).
+ATTN_PARTS_MAX_SPAN = 512
 
 
 class _Q8:
@@ -156,9 +162,18 @@ class Model:
                 capi.call("vvh_plan_set_input_op", h.value, capi.IN_RMS_NORM, L["ln1"].ptr, c.eps)
                 # RoPE and the K/V cache rows in the plan's epilogue (problems 0, 1, 2 = q, k, v)
                 capi.call("vvh_plan_set_rope", h.value, 0, 1, 2, c.head_dim, c.theta, L["kc"].ptr, L["vc"].ptr)
+        # fused: attention over spans of at most ATTN_PARTS_MAX_SPAN positions
+        # as per-wave parts (vvh_attention_parts), merged in the o projection's
+        # input stage (vvh_linear_q8_dev_attn): the same row as vvh_attention
+        # with the keys spread over more CUs; longer spans keep vvh_attention
+        self.parts = None
+        self.nparts = ctypes.c_size_t()
+        if fused and c.head_dim in (64, 128) and c.heads // c.kv_heads <= 16 and c.hidden <= 1024:
+            self.parts_floats = 8 * c.heads * (c.head_dim + 4)
+            self.parts = capi.DevBuf(self.parts_floats * 4)
+        self.mlp_plans = []
         # fused: gate/up as a one-problem plan that reads the residual stream
         # through the post-attention RMSNorm and writes silu(gate) * up
-        self.mlp_plans = []
         if fused:
             for L in self.layers:
                 g = L["gu"]
@@ -256,11 +271,19 @@ class Model:
         for L, plan, mlp in zip(self.layers, self.plans, self.mlp_plans):
             # q/k/v of rms_norm(x, ln1), RoPE'd, k and v rows written to the cache
             call("vvh_plan_run_pos", plan, pos, stream)
-            call("vvh_attention", self.attn.ptr, self.q.ptr, L["kc"].ptr, L["vc"].ptr, 1, pos + 1, c.heads,
-                 c.kv_heads, c.head_dim, scale, a, stream)
             o = L["o"]
-            call("vvh_linear_q8_dev", self.x.ptr, self.attn.ptr, o.q.ptr, o.s.ptr, None, self.x.ptr, 1, c.hidden,
-                 c.hidden, a, a, stream)
+            if self.parts is not None and pos + 1 <= ATTN_PARTS_MAX_SPAN:
+                # attention parts, then o (+ residual) of their merge
+                call("vvh_attention_parts", self.parts.ptr, self.parts_floats, ctypes.byref(self.nparts),
+                     self.q.ptr, L["kc"].ptr, L["vc"].ptr, pos + 1, c.heads, c.kv_heads, c.head_dim, scale, a,
+                     stream)
+                call("vvh_linear_q8_dev_attn", self.x.ptr, self.parts.ptr, self.nparts.value, c.head_dim, o.q.ptr,
+                     o.s.ptr, None, self.x.ptr, c.hidden, c.hidden, a, stream)
+            else:
+                call("vvh_attention", self.attn.ptr, self.q.ptr, L["kc"].ptr, L["vc"].ptr, 1, pos + 1, c.heads,
+                     c.kv_heads, c.head_dim, scale, a, stream)
+                call("vvh_linear_q8_dev", self.x.ptr, self.attn.ptr, o.q.ptr, o.s.ptr, None, self.x.ptr, 1,
+                     c.hidden, c.hidden, a, a, stream)
             # silu(gate) * up of rms_norm(x, ln2) in one launch
             call("vvh_plan_run", mlp, stream)
             d = L["down"]
