@@ -709,13 +709,19 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
     //   kFirstRms: the RMSNorm stage of an early launch whose rows take one
     //     batch of sum-of-squares loads and one round of chunks per thread
     //     (xop 1, M <= 4, K <= 2048);
-    //   kFirstAttn: the attention merge stage (xop 3, one row, K <= 1024).
+    //   kFirstAttn: the attention merge stage (xop 3, one row, K <= 1024);
+    //   kFirstX1/3/5: one row of plain activations (xop 0) in XR rounds of
+    //     256 chunks: loaded in the ring instead, each wave would request its
+    //     activation chunks with every weight step, as many bytes as the
+    //     weights through the texture unit.
     // A compile-time choice: chosen at run time, the other path's ring issue
     // comes before the stage's loads, and the compiler then waits for every
     // older load before the stage's first one (a whole round trip).
+    constexpr int XR = FS == kFirstX1 ? 1 : FS == kFirstX3 ? 3 : FS == kFirstX5 ? 5 : 0;
     constexpr bool rms_first = FS == kFirstRms && EARLY && XLDS && MT <= 4;
     constexpr bool attn_first = FS == kFirstAttn && EARLY && XLDS && MT == 1;
-    constexpr bool first = rms_first || attn_first;
+    constexpr bool x_first = XR > 0 && EARLY && XLDS && MT == 1;
+    constexpr bool first = rms_first || attn_first || x_first;
     if constexpr (EARLY) {
         const float* bp = a.bias ? a.bias : a.scales;  // absent bias / residual: in-bounds reads, unused
         const OT* rp = a.res ? static_cast<const OT*>(a.res) : reinterpret_cast<const OT*>(a.scales);
@@ -853,6 +859,28 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
                 const h4 v = {(f16)(num[0] / den[0]), (f16)(num[1] / den[1]), (f16)(num[2] / den[2]),
                               (f16)(num[3] / den[3])};
                 *reinterpret_cast<h4*>(xs + e0) = v;
+            }
+            __syncthreads();
+        } else if constexpr (x_first) {
+            // chunk i of the row: round i / 256 of thread i % 256; the loads
+            // of the rounds past the row re-read its last chunk, unused
+            const int32_t xchunks = (int32_t)(a.K / 8);
+            h8 xr[XR > 0 ? XR : 1];
+#pragma unroll
+            for (int i = 0; i < XR; i++) {
+                int32_t idx = (int32_t)threadIdx.x + 256 * i;
+                idx = idx < xchunks ? idx : xchunks - 1;
+                xr[i] = *gbl(reinterpret_cast<const h8*>(xg + 8 * idx));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int u = 0; u < D; u++) issue(u, (int32_t)c.s0 + u);
+            __builtin_amdgcn_sched_barrier(0);
+            rope_prep();
+#pragma unroll
+            for (int i = 0; i < XR; i++) {
+                const int32_t idx = (int32_t)threadIdx.x + 256 * i;
+                if (idx < xchunks) *reinterpret_cast<h8*>(xs + 8 * idx) = xr[i];
             }
             __syncthreads();
         }
@@ -1677,8 +1705,12 @@ static void dot_launch_e(const LinArgs& a, int out, bool early, int fs, int dept
     }
     if constexpr (XLDS && MT <= 4) {
         if (fs == kFirstRms) return dot_launch_d<MT, true, true, kFirstRms>(a, out, depth, grid, lds, s);
-        if constexpr (MT == 1)
+        if constexpr (MT == 1) {
             if (fs == kFirstAttn) return dot_launch_d<MT, true, true, kFirstAttn>(a, out, depth, grid, lds, s);
+            if (fs == kFirstX1) return dot_launch_d<MT, true, true, kFirstX1>(a, out, depth, grid, lds, s);
+            if (fs == kFirstX3) return dot_launch_d<MT, true, true, kFirstX3>(a, out, depth, grid, lds, s);
+            if (fs == kFirstX5) return dot_launch_d<MT, true, true, kFirstX5>(a, out, depth, grid, lds, s);
+        }
     }
     dot_launch_d<MT, XLDS, true, kFirstNone>(a, out, depth, grid, lds, s);
 }
@@ -1686,15 +1718,18 @@ static void dot_launch_e(const LinArgs& a, int out, bool early, int fs, int dept
 int launch_dot(const LinArgs& a, int out, bool early, int depth, void* stream)
 {
     const dim3 grid((unsigned)dot_blocks(a));
-    // early launches without an input stage load the activations with the
-    // weights (see dot_early)
-    const bool xl = dot_x_in_lds(a.M, a.K) && (a.xop != 0 || !early);
-    const size_t lds = (xl ? dot_lds_bytes(a.M, a.K) : (size_t)kDotRedBytes) + (a.M > 2 ? kDotWtBytes : 0);
-    // the attention merge stage exists only as a first stage (any block count)
+    // early launches without an input stage stage one row of activations
+    // with a first stage (dot_first_x); more rows they load with the
+    // weights (see dot_early).  The attention merge stage exists only as a
+    // first stage (any block count).
     if (a.xop == 3) early = true;
+    const int fx = a.xop == 0 ? dot_first_x(a.M, a.K, dot_blocks(a)) : kFirstNone;
+    const bool xl = dot_x_in_lds(a.M, a.K) && (a.xop != 0 || !early || fx != kFirstNone);
+    const size_t lds = (xl ? dot_lds_bytes(a.M, a.K) : (size_t)kDotRedBytes) + (a.M > 2 ? kDotWtBytes : 0);
     const int fs = !(early && xl) ? kFirstNone
                    : a.xop == 3 ? kFirstAttn
-                   : (a.xop == 1 && dot_first_rms_ok(a.M, a.K)) ? kFirstRms : kFirstNone;
+                   : (a.xop == 1 && dot_first_rms_ok(a.M, a.K)) ? kFirstRms
+                   : fx;
     if (a.M <= 1) {
         if (xl) dot_launch_e<1, true>(a, out, early, fs, depth, grid, lds, S(stream));
         else dot_launch_e<1, false>(a, out, early, fs, depth, grid, lds, S(stream));
