@@ -133,29 +133,6 @@ constexpr int kStageMaxM = 4;  // rows of a decode linear with an input stage
 // attention merge stage: at most kAttnMaxParts parts, K <= kAttnMergeMaxK (4 per thread)
 constexpr int kAttnMaxParts = 8;
 constexpr int kAttnMergeMaxK = 1024;
-// k_dot first stages (requested ahead of the weight ring, a template
-// parameter of the kernel): none, RMSNorm (xop 1, M <= 4, K <= 2048), the
-// attention merge (xop 3), plain activations (xop 0, M = 1)
-constexpr int kFirstNone = 0;
-constexpr int kFirstRms = 1;
-constexpr int kFirstAttn = 3;
-inline bool dot_first_rms_ok(int64_t M, int64_t K) { return M <= 4 && K <= 256 * 8; }
-// plain activations of one row staged in LDS, requested ahead of the ring in
-// 1, 3 or 5 rounds of 256 chunks of 8 halves (K <= 2048, 6144, 10240), for
-// launches of at most kDotXFirstMaxBlocks blocks.  Graph-replayed at M = 1
-// against the activations in the ring: 1.5B gate 8960 x 1536 (560 blocks)
-// 5.57 -> 5.28 us, q/o 3.05 -> 2.98, down 7.1 -> 6.98, the 0.5B shapes
-// unchanged, the LM head (2374 blocks, each with a barrier more) 23.1 -> 23.4.
-constexpr int kFirstX1 = 4;
-constexpr int kFirstX3 = 5;
-constexpr int kFirstX5 = 6;
-constexpr int64_t kDotXFirstMaxBlocks = 1024;
-inline int dot_first_x(int64_t M, int64_t K, int64_t blocks)
-{
-    if (M != 1 || blocks > kDotXFirstMaxBlocks) return kFirstNone;
-    const int64_t rounds = (K / 8 + 255) / 256;
-    return rounds <= 1 ? kFirstX1 : rounds <= 3 ? kFirstX3 : rounds <= 5 ? kFirstX5 : kFirstNone;
-}
 constexpr int kDotStep = 128;               // k codes per row per step
 constexpr int64_t kDotLdsMax = 80 * 1024;   // dynamic LDS of one block at most
 constexpr int64_t kDotRedBytes = 4 * kDotMaxM * 16 * 4;
@@ -184,6 +161,34 @@ inline __host__ __device__ bool dot_x_in_lds(int64_t M, int64_t K)
 inline __host__ __device__ int64_t dot_lds_bytes(int64_t M, int64_t K)
 {
     return kDotRedBytes + (dot_x_in_lds(M, K) ? M * (K + 8) * 2 : 0);
+}
+// k_dot first stages (requested ahead of the weight ring, a template
+// parameter of the kernel): none, RMSNorm (xop 1, M <= 4, K <= 2048), the
+// attention merge (xop 3), plain activations (xop 0, M = 1)
+constexpr int kFirstNone = 0;
+constexpr int kFirstRms = 1;   // rows of K <= 1024 (2 chunks of 8 per lane)
+constexpr int kFirstRms4 = 2;  // rows of K <= 2048 (4 chunks per lane)
+constexpr int kFirstAttn = 3;
+inline int dot_first_rms(int64_t M, int64_t K)
+{
+    if (M > 4 || K % 16 != 0 || !dot_x_in_lds(M, K)) return kFirstNone;
+    return K <= 1024 ? kFirstRms : K <= 2048 ? kFirstRms4 : kFirstNone;
+}
+// plain activations of one row staged in LDS, requested ahead of the ring in
+// 1, 3 or 5 rounds of 256 chunks of 8 halves (K <= 2048, 6144, 10240), for
+// launches of at most kDotXFirstMaxBlocks blocks.  Graph-replayed at M = 1
+// against the activations in the ring: 1.5B gate 8960 x 1536 (560 blocks)
+// 5.57 -> 5.28 us, q/o 3.05 -> 2.98, down 7.1 -> 6.98, the 0.5B shapes
+// unchanged, the LM head (2374 blocks, each with a barrier more) 23.1 -> 23.4.
+constexpr int kFirstX1 = 4;
+constexpr int kFirstX3 = 5;
+constexpr int kFirstX5 = 6;
+constexpr int64_t kDotXFirstMaxBlocks = 1024;
+inline int dot_first_x(int64_t M, int64_t K, int64_t blocks)
+{
+    if (M != 1 || blocks > kDotXFirstMaxBlocks) return kFirstNone;
+    const int64_t rounds = (K / 8 + 255) / 256;
+    return rounds <= 1 ? kFirstX1 : rounds <= 3 ? kFirstX3 : rounds <= 5 ? kFirstX5 : kFirstNone;
 }
 
 // GEMM tile shape.

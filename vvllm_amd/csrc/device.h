@@ -100,6 +100,33 @@ __device__ __forceinline__ float block_sum256(float v, float* red)
     return (red[0] + red[1]) + (red[2] + red[3]);
 }
 
+// RMSNorm's sum of squares in one wave, the order k_rms_norm and k_dot's
+// RMSNorm input stages share: lane l takes the chunks l, l + 64, l + 128, ...
+// of 8 consecutive values and adds their squares in order (values past the
+// row add an exact 0), then the wave adds its lanes with an xor butterfly,
+// which leaves every lane with the same bits (each step adds the same two
+// numbers on both partner lanes).  One wave holds the whole sum, so a block
+// needs no barrier for it.
+__device__ __forceinline__ float rms_sumsq8(float ss, const float (&v)[8])
+{
+#pragma unroll
+    for (int e = 0; e < 8; e++) ss = __builtin_fmaf(v[e], v[e], ss);
+    return ss;
+}
+__device__ __forceinline__ float rms_sumsq_h8(float ss, const h8 x, bool ok)
+{
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) v[e] = ok ? (float)x[e] : 0.0f;
+    return rms_sumsq8(ss, v);
+}
+__device__ __forceinline__ float wave_sum_xor(float v)
+{
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
 // RMSNorm's divisor and output, and the SiLU-gated product, in the
 // reference's fp32 operation order (backend_naive.cc:68-76, :297-298); used by
 // the standalone kernels and by the fused input stage of k_dot alike.  The

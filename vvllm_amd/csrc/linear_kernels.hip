@@ -24,6 +24,7 @@
 //               fused scale/bias/residual epilogue.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdlib>
 #include <utility>
 
@@ -543,6 +544,29 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
     // the step's weights go through the wave's LDS tile into the MFMA
     // operand layout, the activations are loaded as MFMA operands
     constexpr bool MF = MT >= 4;
+    // First stages (FS, chosen per launch by the host): the stage's operands
+    // are requested before the weight ring and the stage runs while the
+    // weights are in flight (the in-order wait counter lets a wait for them
+    // leave the younger ring loads outstanding).
+    //   kFirstRms / kFirstRms4: the RMSNorm stage of an early launch (xop 1,
+    //     M <= 4, K <= 1024 / 2048): every wave loads the whole rows (chunks
+    //     lane + 64 j, j < RJ) and sums their squares itself (rms_sumsq8,
+    //     wave_sum_xor), then thread (w, l) normalizes chunk l + 64 w, which
+    //     it holds; one barrier in all;
+    //   kFirstAttn: the attention merge stage (xop 3, one row, K <= 1024);
+    //   kFirstX1/3/5: one row of plain activations (xop 0) in XR rounds of
+    //     256 chunks: loaded in the ring instead, each wave would request its
+    //     activation chunks with every weight step, as many bytes as the
+    //     weights through the texture unit.
+    // A compile-time choice: chosen at run time, the other path's ring issue
+    // comes before the stage's loads, and the compiler then waits for every
+    // older load before the stage's first one (a whole round trip).
+    constexpr int XR = FS == kFirstX1 ? 1 : FS == kFirstX3 ? 3 : FS == kFirstX5 ? 5 : 0;
+    constexpr int RJ = FS == kFirstRms ? 2 : FS == kFirstRms4 ? 4 : 0;  // chunks of a row per lane
+    constexpr bool rms_first = RJ > 0 && EARLY && XLDS && MT <= 4;
+    constexpr bool attn_first = FS == kFirstAttn && EARLY && XLDS && MT == 1;
+    constexpr bool x_first = XR > 0 && EARLY && XLDS && MT == 1;
+    constexpr bool first = rms_first || attn_first || x_first;
     DotRed& red = *reinterpret_cast<DotRed*>(smem);
     f16* xs = reinterpret_cast<f16*>(smem + kDotRedBytes);
     const DecodeCoord c = dot_coord(a, block);
@@ -702,26 +726,6 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
             for (int m = 0; m < MT; m++) rope_cs_freq(pos + m, rfreq, rc[m], rs[m]);
         }
     };
-    // First stages (FS, chosen per launch by the host): the stage's operands
-    // are requested before the weight ring and the stage runs while the
-    // weights are in flight (the in-order wait counter lets a wait for them
-    // leave the younger ring loads outstanding).
-    //   kFirstRms: the RMSNorm stage of an early launch whose rows take one
-    //     batch of sum-of-squares loads and one round of chunks per thread
-    //     (xop 1, M <= 4, K <= 2048);
-    //   kFirstAttn: the attention merge stage (xop 3, one row, K <= 1024);
-    //   kFirstX1/3/5: one row of plain activations (xop 0) in XR rounds of
-    //     256 chunks: loaded in the ring instead, each wave would request its
-    //     activation chunks with every weight step, as many bytes as the
-    //     weights through the texture unit.
-    // A compile-time choice: chosen at run time, the other path's ring issue
-    // comes before the stage's loads, and the compiler then waits for every
-    // older load before the stage's first one (a whole round trip).
-    constexpr int XR = FS == kFirstX1 ? 1 : FS == kFirstX3 ? 3 : FS == kFirstX5 ? 5 : 0;
-    constexpr bool rms_first = FS == kFirstRms && EARLY && XLDS && MT <= 4;
-    constexpr bool attn_first = FS == kFirstAttn && EARLY && XLDS && MT == 1;
-    constexpr bool x_first = XR > 0 && EARLY && XLDS && MT == 1;
-    constexpr bool first = rms_first || attn_first || x_first;
     if constexpr (EARLY) {
         const float* bp = a.bias ? a.bias : a.scales;  // absent bias / residual: in-bounds reads, unused
         const OT* rp = a.res ? static_cast<const OT*>(a.res) : reinterpret_cast<const OT*>(a.scales);
@@ -744,75 +748,51 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
     }
     if constexpr (XLDS && MT <= 4) {
         if constexpr (rms_first) {
-            const int32_t K32 = (int32_t)a.K, xchunks = (int32_t)(a.M * a.K / 8);
-            // M <= MT rows of K <= 2048: at most MT chunks of 8 per thread
-            constexpr int XL = MT;
-            f16 raw[MT][8];
-            h8 xr[XL];
-            f4 w0[XL], w1[XL];
-    #pragma unroll
-            for (int m = 0; m < MT; m++) {
-                const f16* xrow = xg + (m < a.M ? m : 0) * a.K;
-    #pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    const int32_t i = (int32_t)threadIdx.x + 256 * j;
-                    raw[m][j] = *gbl(xrow + (i < K32 ? i : K32 - 1));
-                }
+            // lane l: chunks l + 64 j of every row (clamped into the row past
+            // its end: those add an exact 0), and the norm weights of its own
+            // chunk l + 64 w
+            const int32_t kc = (int32_t)(a.K / 8), co = c.lane + 64 * c.wave;
+            const int32_t cw = co < kc ? co : kc - 1;
+            h8 xv[MT][RJ > 0 ? RJ : 1];
+#pragma unroll
+            for (int j = 0; j < RJ; j++) {
+                const int32_t ci = c.lane + 64 * j < kc ? c.lane + 64 * j : kc - 1;
+#pragma unroll
+                for (int m = 0; m < MT; m++)
+                    xv[m][j] = *gbl(reinterpret_cast<const h8*>(xg + (m < a.M ? m : 0) * a.K + 8 * ci));
             }
-    #pragma unroll
-            for (int i = 0; i < XL; i++) {
-                int32_t idx = (int32_t)threadIdx.x + 256 * i;
-                idx = idx < xchunks ? idx : xchunks - 1;
-                const int32_t row = idx * 8 / K32, col = idx * 8 - row * K32;
-                xr[i] = *gbl(reinterpret_cast<const h8*>(xg + row * a.K + col));
-                w0[i] = *gbl(reinterpret_cast<const f4*>(a.xw + col));
-                w1[i] = *gbl(reinterpret_cast<const f4*>(a.xw + col + 4));
-            }
+            const f4 w0 = *gbl(reinterpret_cast<const f4*>(a.xw + 8 * cw));
+            const f4 w1 = *gbl(reinterpret_cast<const f4*>(a.xw + 8 * cw + 4));
             // keep every row load ahead of the ring in issue order, and issue the
             // ring in every wave (an inactive wave's slots read clamped, in-bounds
             // rows and steps, unused): a wait for a row value then always counts
             // exactly the ring's loads as younger
             __builtin_amdgcn_sched_barrier(0);
-    #pragma unroll
+#pragma unroll
             for (int u = 0; u < D; u++) issue(u, (int32_t)c.s0 + u);
             __builtin_amdgcn_sched_barrier(0);
             rope_prep();
-            // per row as k_rms_norm: thread t sums x[t], x[t + 256], ... in order
-            // (slots past the row add an exact 0), then the same block reduction
-            float* red4 = &red.v[0][0][0];
-            float rinv[MT];
-    #pragma unroll
+#pragma unroll
             for (int m = 0; m < MT; m++) {
-                rinv[m] = 1.0f;
                 if (m < a.M) {
-                    float v[8];
-    #pragma unroll
-                    for (int j = 0; j < 8; j++) {
-                        const int32_t i = (int32_t)threadIdx.x + 256 * j;
-                        v[j] = i < K32 ? (float)raw[m][j] : 0.0f;
-                    }
                     float ss = 0.0f;
-    #pragma unroll
-                    for (int j = 0; j < 8; j++) ss += v[j] * v[j];
-                    ss = block_sum256(ss, red4);
-                    rinv[m] = rms_of(ss, a.K, a.xeps);
+                    h8 own = xv[m][0];
+#pragma unroll
+                    for (int j = 0; j < RJ; j++) {
+                        ss = rms_sumsq_h8(ss, xv[m][j], c.lane + 64 * j < kc);
+                        own = j == c.wave ? xv[m][j] : own;
+                    }
+                    const float rv = rms_of(wave_sum_xor(ss), a.K, a.xeps);
+                    if (co < kc) {
+                        h8 v;
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            v[e] = (f16)rms_apply((float)own[e], rv, w0[e]);
+                            v[4 + e] = (f16)rms_apply((float)own[4 + e], rv, w1[e]);
+                        }
+                        *reinterpret_cast<h8*>(xs + m * ldx + 8 * co) = v;
+                    }
                 }
-            }
-    #pragma unroll
-            for (int i = 0; i < XL; i++) {
-                const int32_t idx = (int32_t)threadIdx.x + 256 * i;
-                if (idx >= xchunks) continue;
-                const int32_t row = idx * 8 / K32, col = idx * 8 - row * K32;
-                float rv = rinv[0];
-    #pragma unroll
-                for (int m = 1; m < MT; m++) rv = row == m ? rinv[m] : rv;
-                h8 v;
-    #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    v[j] = (f16)rms_apply((float)xr[i][j], rv, w0[i][j]);
-                    v[4 + j] = (f16)rms_apply((float)xr[i][4 + j], rv, w1[i][j]);
-                }
-                *reinterpret_cast<h8*>(xs + row * ldx + col) = v;
             }
             __syncthreads();
         } else if constexpr (attn_first) {
@@ -896,30 +876,15 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
 #pragma unroll
         for (int m = 0; m < MT; m++) rinv[m] = 1.0f;
         if (xop == 1) {
-            // per row as k_rms_norm: thread t sums x[t], x[t + 256], ... in
-            // order, then the same block reduction
-            float* red4 = &red.v[0][0][0];
+            // per row as k_rms_norm (every wave sums the whole row itself)
 #pragma unroll
             for (int m = 0; m < MT; m++) {
                 if (m < a.M) {
-                    // 8 loads in flight per batch; masked slots read a valid
-                    // element and add an exact 0, so the sum is the same
-                    // in-order sum as k_rms_norm's
                     const f16* xr = xg + m * a.K;
                     float ss = 0.0f;
-                    for (int32_t i0 = threadIdx.x; i0 < K32; i0 += 256 * 8) {
-                        float v[8];
-#pragma unroll
-                        for (int j = 0; j < 8; j++) {
-                            const int32_t i = i0 + 256 * j;
-                            const float e = (float)*gbl(xr + (i < K32 ? i : K32 - 1));
-                            v[j] = i < K32 ? e : 0.0f;
-                        }
-#pragma unroll
-                        for (int j = 0; j < 8; j++) ss += v[j] * v[j];
-                    }
-                    ss = block_sum256(ss, red4);
-                    rinv[m] = rms_of(ss, a.K, a.xeps);
+                    for (int32_t ci = c.lane; 8 * ci < K32; ci += 64)
+                        ss = rms_sumsq_h8(ss, *gbl(reinterpret_cast<const h8*>(xr + 8 * ci)), true);
+                    rinv[m] = rms_of(wave_sum_xor(ss), a.K, a.xeps);
                 }
             }
         }
@@ -1705,6 +1670,7 @@ static void dot_launch_e(const LinArgs& a, int out, bool early, int fs, int dept
     }
     if constexpr (XLDS && MT <= 4) {
         if (fs == kFirstRms) return dot_launch_d<MT, true, true, kFirstRms>(a, out, depth, grid, lds, s);
+        if (fs == kFirstRms4) return dot_launch_d<MT, true, true, kFirstRms4>(a, out, depth, grid, lds, s);
         if constexpr (MT == 1) {
             if (fs == kFirstAttn) return dot_launch_d<MT, true, true, kFirstAttn>(a, out, depth, grid, lds, s);
             if (fs == kFirstX1) return dot_launch_d<MT, true, true, kFirstX1>(a, out, depth, grid, lds, s);
@@ -1725,11 +1691,11 @@ int launch_dot(const LinArgs& a, int out, bool early, int depth, void* stream)
     if (a.xop == 3) early = true;
     const int fx = a.xop == 0 ? dot_first_x(a.M, a.K, dot_blocks(a)) : kFirstNone;
     const bool xl = dot_x_in_lds(a.M, a.K) && (a.xop != 0 || !early || fx != kFirstNone);
-    const size_t lds = (xl ? dot_lds_bytes(a.M, a.K) : (size_t)kDotRedBytes) + (a.M > 2 ? kDotWtBytes : 0);
     const int fs = !(early && xl) ? kFirstNone
                    : a.xop == 3 ? kFirstAttn
-                   : (a.xop == 1 && dot_first_rms_ok(a.M, a.K)) ? kFirstRms
+                   : a.xop == 1 ? dot_first_rms(a.M, a.K)
                    : fx;
+    const size_t lds = (xl ? dot_lds_bytes(a.M, a.K) : (size_t)kDotRedBytes) + (a.M > 2 ? kDotWtBytes : 0);
     if (a.M <= 1) {
         if (xl) dot_launch_e<1, true>(a, out, early, fs, depth, grid, lds, S(stream));
         else dot_launch_e<1, false>(a, out, early, fs, depth, grid, lds, S(stream));
@@ -1787,8 +1753,10 @@ static void dot_grouped_launch_e(const DotGroupArgs& k, int out, bool early, int
         dot_grouped_launch_d<MT, XLDS, false, kFirstNone>(k, out, depth, grid, lds, s);
         return;
     }
-    if constexpr (XLDS && MT <= 4)
+    if constexpr (XLDS && MT <= 4) {
         if (fs == kFirstRms) return dot_grouped_launch_d<MT, true, true, kFirstRms>(k, out, depth, grid, lds, s);
+        if (fs == kFirstRms4) return dot_grouped_launch_d<MT, true, true, kFirstRms4>(k, out, depth, grid, lds, s);
+    }
     dot_grouped_launch_d<MT, XLDS, true, kFirstNone>(k, out, depth, grid, lds, s);
 }
 
@@ -1810,10 +1778,13 @@ int launch_dot_grouped(const LinArgs* dev_table, const int32_t* dev_block_prob, 
             k.g.p[i] = args[i];
             if (i > 0) k.b[i - 1] = args[i].block_begin;
         }
-    // the RMSNorm first stage when every problem takes it
-    bool rms = early && x_in_lds && count > 0;
-    for (int i = 0; i < count; ++i) rms = rms && args[i].xop == 1 && dot_first_rms_ok(args[i].M, args[i].K);
-    const int fs = rms ? kFirstRms : kFirstNone;
+    // the RMSNorm first stage when every problem takes it (the larger of
+    // the problems' forms; each problem's rows fit it)
+    int fs = early && x_in_lds && count > 0 ? kFirstRms : kFirstNone;
+    for (int i = 0; i < count && fs != kFirstNone; ++i) {
+        const int f = args[i].xop == 1 ? dot_first_rms(args[i].M, args[i].K) : kFirstNone;
+        fs = f == kFirstNone ? kFirstNone : std::max(fs, f);
+    }
     if (max_m <= 1) {
         if (x_in_lds) dot_grouped_launch_e<1, true>(k, out, early, fs, depth, grid, lds_bytes, s);
         else dot_grouped_launch_e<1, false>(k, out, early, fs, depth, grid, lds_bytes, s);

@@ -85,50 +85,77 @@ int launch_eltwise(int op, void* out, const void* x, const void* y, int64_t n, i
 // ---------------------------------------------------------------------------
 // RMSNorm over `rows` rows of n: rms = sqrt(sum(x^2) / n + eps),
 // out = x / rms * w (a division, as the reference; backend_naive.cc:68-76).
+// One block of 4 waves per row; every wave sums the squares of the whole row
+// in the order of rms_sumsq8 / wave_sum_xor (k_dot's RMSNorm input stages
+// repeat it), so no barrier; thread (w, l) then writes chunk l + 64 w of 8
+// values (and l + 64 w + 256 j for rows past 2048).
 // ---------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ void rms_ld8(const T* p, float (&v)[8])
+{
+    if constexpr (sizeof(T) == 2) {
+        const h8 h = *reinterpret_cast<const h8*>(p);
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[e] = (float)h[e];
+    } else {
+        const f4 a0 = *reinterpret_cast<const f4*>(p), a1 = *reinterpret_cast<const f4*>(p + 4);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            v[e] = a0[e];
+            v[4 + e] = a1[e];
+        }
+    }
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void k_rms_norm(T* __restrict__ out, const T* __restrict__ x,
                                                   const float* __restrict__ w, int64_t n, float eps)
 {
-    __shared__ float red[4];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const T* xr = x + (int64_t)blockIdx.x * n;
     T* orow = out + (int64_t)blockIdx.x * n;
-    // thread t sums x[t]^2, x[t + 256]^2, ... in order, then the block sum:
-    // the order k_dot's RMSNorm input stage reproduces
-    constexpr int RC = 8;
-    if (n <= 256 * RC) {
-        // rows of up to 2048: the thread's elements and weights requested at
-        // once and kept for the output (one round trip instead of two);
-        // slots past the row add an exact 0
-        float v[RC], wv[RC];
+    if (n <= 0) return;
+    constexpr int RJ = 4;  // chunks of 8 per lane kept in registers: rows of up to 2048
+    const bool vec = n % 8 == 0 && ((reinterpret_cast<uintptr_t>(xr) | reinterpret_cast<uintptr_t>(w) |
+                                     reinterpret_cast<uintptr_t>(orow)) & 15) == 0;
+    if (vec && n <= 64 * 8 * RJ) {
+        // the lane's chunks requested at once (clamped into the row; past it
+        // they add an exact 0), and the weights of the thread's own chunk
+        const int64_t nc = n / 8, co = lane + 64 * wave, cw = co < nc ? co : nc - 1;
+        float v[RJ][8];
 #pragma unroll
-        for (int j = 0; j < RC; j++) {
-            const int64_t i = threadIdx.x + 256 * j, ic = i < n ? i : n - 1;
-            v[j] = ldf(xr, ic);
-            wv[j] = w[ic];
+        for (int j = 0; j < RJ; j++) rms_ld8(xr + 8 * (lane + 64 * j < nc ? lane + 64 * j : nc - 1), v[j]);
+        const f4 w0 = *reinterpret_cast<const f4*>(w + 8 * cw), w1 = *reinterpret_cast<const f4*>(w + 8 * cw + 4);
+        float ss = 0.0f, own[8];
+#pragma unroll
+        for (int j = 0; j < RJ; j++) {
+            float z[8];
+            const bool ok = lane + 64 * j < nc;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                z[e] = ok ? v[j][e] : 0.0f;
+                own[e] = j == wave ? v[j][e] : (j == 0 ? 0.0f : own[e]);
+            }
+            ss = rms_sumsq8(ss, z);
         }
-        float ss = 0.0f;
+        const float rms = rms_of(wave_sum_xor(ss), n, eps);
+        if (co < nc) {
 #pragma unroll
-        for (int j = 0; j < RC; j++) {
-            const float e = threadIdx.x + 256 * j < n ? v[j] : 0.0f;
-            ss += e * e;
-        }
-        ss = block_sum(ss, red);
-        const float rms = rms_of(ss, n, eps);
-#pragma unroll
-        for (int j = 0; j < RC; j++) {
-            const int64_t i = threadIdx.x + 256 * j;
-            if (i < n) stf(orow, i, rms_apply(v[j], rms, wv[j]));
+            for (int e = 0; e < 4; e++) {
+                stf(orow, 8 * co + e, rms_apply(own[e], rms, w0[e]));
+                stf(orow, 8 * co + 4 + e, rms_apply(own[4 + e], rms, w1[e]));
+            }
         }
         return;
     }
     float ss = 0.0f;
-    for (int64_t i = threadIdx.x; i < n; i += 256) {
-        const float v = ldf(xr, i);
-        ss += v * v;
+    for (int64_t c = lane; 8 * c < n; c += 64) {
+        float z[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) z[e] = 8 * c + e < n ? ldf(xr, 8 * c + e) : 0.0f;
+        ss = rms_sumsq8(ss, z);
     }
-    ss = block_sum(ss, red);
-    const float rms = rms_of(ss, n, eps);
+    const float rms = rms_of(wave_sum_xor(ss), n, eps);
     for (int64_t i = threadIdx.x; i < n; i += 256) stf(orow, i, rms_apply(ldf(xr, i), rms, w[i]));
 }
 
