@@ -439,14 +439,15 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--workload", choices=("decode", "prefill", "lm-head", "vendor-gemm", "copy", "configs",
-                                           "dense-head"),
+                                           "dense-head", "decode-ops"),
                     default="decode",
                     help="decode: configs[1] (the headline line); prefill: configs[3] gate/up GEMM only; "
                          "lm-head: configs[2] alone; "
                          "vendor-gemm: the int8 GEMM beside the vendor fp16 GEMM on the prefill shapes; "
                          "copy: a 256 MiB device-to-device copy, the calibration of the HBM traffic counters; "
                          "configs: every configs[3] and configs[4] (M = 1, 16, 256) shape, bracketed for "
-                         "rocprofv3 (see --trace-configs); dense-head: the dense fp16 tied LM head (vvh_dense)")
+                         "rocprofv3 (see --trace-configs); dense-head: the dense fp16 tied LM head (vvh_dense); "
+                         "decode-ops: each operator of the fused decode step alone (graph replay)")
     ap.add_argument("--trace-configs", metavar="KERNEL_TRACE_CSV",
                     help="summarise the rocprofv3 kernel trace of a --workload configs run per shape and kernel "
                          "(needs --configs-json, the run's JSON line; --pmc adds counter CSVs); no GPU is used")
@@ -493,6 +494,8 @@ def main():
         return configs_main(args, ev)
     if args.workload == "dense-head":
         return dense_head_main(args, ev)
+    if args.workload == "decode-ops":
+        return decode_ops_main(args, ev)
     h, kv, inter, L = QWEN05["hidden"], QWEN05["kv"], QWEN05["inter"], QWEN05["layers"]
     projs = layer_projs(h, kv, inter)
     tmp_w = capi.DevBuf(max(inter * h, 151936 * 896, 8960 * 1536) * 4)
@@ -804,6 +807,93 @@ def dense_head_main(args, ev):
     print(json.dumps({"workload": "dense fp16 LM head (vvh_dense, M=1, N=151936, K=896)", "us": round(ms * 1e3, 3),
                       "GBps": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": b,
                       "steps": args.steps, "replicas_rotated": reps}), flush=True)
+
+
+def decode_ops_main(args, ev):
+    """Each operator of the fused Qwen2.5-0.5B decode step alone: its 24
+    per-layer calls (the model's own buffers and plans, position 511 of a
+    filled KV cache) captured in one HIP graph and replayed; µs per call,
+    a graph node included.  Beside them: a near-empty kernel, the one-launch
+    attention and the o projection on its row, the gate/up plan without its
+    stage or epilogue, with either alone, and the same problem as one k_dot
+    call.  One JSON line."""
+    from vvllm_amd import qwen2_decode as qd
+    c, P, a = qd.QWEN25_05B, 511, F16
+    m = qd.Model(c, act=a, lm_head="int8", max_ctx=P + 1, seed=3, fused=True)
+    m.fill_kv(5)
+    st = ev.stream()
+    for _ in range(3):
+        m.step(1, P, st)
+    capi.sync()
+    call, scale, n = capi.call, float(1.0 / np.sqrt(np.float32(c.head_dim))), ctypes.c_size_t()
+
+    def gu_plan(L, rms, glu):
+        g = m.layers[L]["gu"]
+        pr = capi.Q8Problem(out=(m.gate if glu else m.gu).ptr, inp=m.x.ptr, residual=None, weight=g.q.ptr,
+                            scales=g.s.ptr, bias=None, M=1, N=2 * c.inter, K=c.hidden)
+        h = ctypes.c_uint64()
+        call("vvh_plan_create", (capi.Q8Problem * 1)(pr), 1, a, a, ctypes.byref(h))
+        if rms:
+            call("vvh_plan_set_input_op", h.value, capi.IN_RMS_NORM, m.layers[L]["ln2"].ptr, c.eps)
+        if glu:
+            call("vvh_plan_set_glu", h.value, 0)
+        return h.value
+
+    extra = {k: [gu_plan(L, *f) for L in range(c.layers)] for k, f in
+             (("rms", (True, False)), ("glu", (False, True)), ("plain", (False, False)))}
+
+    def attn_parts(L, s):
+        Ld = m.layers[L]
+        call("vvh_attention_parts", m.parts.ptr, m.parts_floats, ctypes.byref(n), m.q.ptr, Ld["kc"].ptr,
+             Ld["vc"].ptr, P + 1, c.heads, c.kv_heads, c.head_dim, scale, a, s)
+
+    def o_merge(L, s):
+        o = m.layers[L]["o"]
+        call("vvh_linear_q8_dev_attn", m.x.ptr, m.parts.ptr, n.value, c.head_dim, o.q.ptr, o.s.ptr, None, m.x.ptr,
+             c.hidden, c.hidden, a, s)
+
+    def attention(L, s):
+        Ld = m.layers[L]
+        call("vvh_attention", m.attn.ptr, m.q.ptr, Ld["kc"].ptr, Ld["vc"].ptr, 1, P + 1, c.heads, c.kv_heads,
+             c.head_dim, scale, a, s)
+
+    def lin(name, out, inp, res, N, K):
+        def f(L, s):
+            w = m.layers[L][name]
+            call("vvh_linear_q8_dev", out.ptr, inp.ptr, w.q.ptr, w.s.ptr, None, res.ptr if res else None, 1, N, K,
+                 a, a, s)
+        return f
+
+    ops = [("near-empty kernel (one-element fill)",
+            lambda L, s: call("vvh_fill_normal", m.token.ptr, F32, 1, 1, 0.0, 1.0, s)),
+           ("q/k/v plan (RMSNorm stage, RoPE + K/V append)", lambda L, s: call("vvh_plan_run_pos", m.plans[L], P, s)),
+           ("attention parts", attn_parts),
+           ("o + attention merge stage", o_merge),
+           ("gate/up plan (RMSNorm stage, SiLU-gated)", lambda L, s: call("vvh_plan_run", m.mlp_plans[L], s)),
+           ("down (+ residual)", lin("down", m.x, m.gate, m.x, c.hidden, c.inter)),
+           ("one-launch attention (vvh_attention)", attention),
+           ("o (+ residual) on that row", lin("o", m.x, m.attn, m.x, c.hidden, c.hidden)),
+           ("gate/up plan, RMSNorm stage only", lambda L, s: call("vvh_plan_run", extra["rms"][L], s)),
+           ("gate/up plan, SiLU-gated epilogue only", lambda L, s: call("vvh_plan_run", extra["glu"][L], s)),
+           ("gate/up plan, neither", lambda L, s: call("vvh_plan_run", extra["plain"][L], s)),
+           ("gate/up as one k_dot call", lin("gu", m.gu, m.norm_out, None, 2 * c.inter, c.hidden))]
+    out = {}
+    for name, f in ops:
+        for L in range(c.layers):
+            f(L, st)
+        capi.sync()
+        g = ev.graph(st, lambda s_: [f(L, s_) for L in range(c.layers)])
+        for _ in range(3):
+            ev.launch(g, st)
+        ms = timed(ev, lambda i: ev.launch(g, st), max(args.steps, 10), st)
+        ev.drop(g)
+        out[name] = round(ms * 1e3 / c.layers, 3)
+        print(f"[bench] {name}: {out[name]:.2f} us per call", file=sys.stderr, flush=True)
+    for h in extra["rms"] + extra["glu"] + extra["plain"]:
+        call("vvh_plan_destroy", h)
+    m.close()
+    print(json.dumps({"workload": "fused decode step operators, Qwen2.5-0.5B shapes, position 511, 24 layer calls "
+                                  "per graph", "us_per_call": out}), flush=True)
 
 
 def copy_main(args, ev):
