@@ -1,5 +1,6 @@
-"""HIP graph capture of the int8 linear path and of the split decode
-attention (launch-overhead removal by graph capture of the decode step).
+"""HIP graph capture of the int8 linear path, of the split decode attention
+and of a whole fused decode step (launch-overhead removal by graph capture
+of the decode step).
 
 A decode plan, a several-row decode call, a GEMM and a split-K GEMM are
 issued on one stream, captured into a graph and replayed several times, with
@@ -14,6 +15,7 @@ import numpy as np
 import pytest
 
 from vvllm_amd import capi
+from vvllm_amd import qwen2_decode as qd
 
 pytestmark = pytest.mark.gpu
 
@@ -229,3 +231,49 @@ def test_graph_split_attention(gpu, oracle):
     hip.hipGraphDestroy(graph)
     capi.call("vvh_workspace_release", stream)
     hip.hipStreamDestroy(stream)
+
+
+@pytest.mark.parametrize("pos", [200, 511])
+def test_graph_fused_decode_step(gpu, pos):
+    """A whole fused decode step (RMSNorm stages, RoPE + cache epilogue, the
+    attention as per-wave parts merged in the o projection, SiLU-gated
+    epilogue), small Qwen2-shaped model, captured at one position and
+    replayed three times with eager steps on the same stream between the
+    replays: every replay's logits equal the eager step's bit for bit."""
+    hip = _hip()
+    V = ctypes.c_void_p
+    for f, args in (("hipStreamCreate", [ctypes.POINTER(V)]), ("hipStreamSynchronize", [V]),
+                    ("hipStreamBeginCapture", [V, ctypes.c_int]), ("hipStreamEndCapture", [V, ctypes.POINTER(V)]),
+                    ("hipGraphInstantiate", [ctypes.POINTER(V), V, V, V, ctypes.c_size_t]),
+                    ("hipGraphLaunch", [V, V]), ("hipGraphExecDestroy", [V]), ("hipGraphDestroy", [V]),
+                    ("hipStreamDestroy", [V])):
+        getattr(hip, f).argtypes = args
+    stream = V()
+    _check(hip.hipStreamCreate(ctypes.byref(stream)), "hipStreamCreate")
+    cfg = qd.Config(hidden=512, heads=8, kv_heads=2, inter=1024, layers=2, vocab=2048)
+    m = qd.Model(cfg, act=F16, lm_head="int8", max_ctx=pos + 1, seed=5, fused=True)
+    try:
+        m.fill_kv(9)
+        print(f"[case] fused decode step graph at position {pos}", flush=True)
+        m.step(3, pos, stream.value)  # eager: sizes the stream's workspace
+        _check(hip.hipStreamSynchronize(stream), "sync")
+        eager = m.logits_host().view(np.uint32).copy()
+        graph, gexec = V(), V()
+        _check(hip.hipStreamBeginCapture(stream, 0), "hipStreamBeginCapture")
+        m.step(3, pos, stream.value)
+        _check(hip.hipStreamEndCapture(stream, ctypes.byref(graph)), "hipStreamEndCapture")
+        _check(hip.hipGraphInstantiate(ctypes.byref(gexec), graph, None, None, 0), "hipGraphInstantiate")
+        for rep in range(3):
+            capi.call("vvh_fill_normal", m.logits32.ptr, F32, cfg.vocab, rep, 0.0, 1.0, stream.value)
+            _check(hip.hipGraphLaunch(gexec, stream), "hipGraphLaunch")
+            _check(hip.hipStreamSynchronize(stream), "sync")
+            np.testing.assert_array_equal(m.logits_host().view(np.uint32), eager, err_msg=f"replay {rep}")
+            m.step(3, pos, stream.value)  # an eager step between the replays
+            _check(hip.hipStreamSynchronize(stream), "sync")
+            np.testing.assert_array_equal(m.logits_host().view(np.uint32), eager, err_msg=f"eager {rep}")
+        hip.hipGraphExecDestroy(gexec)
+        hip.hipGraphDestroy(graph)
+    finally:
+        m.close()
+        capi.call("vvh_workspace_release", stream.value)
+        hip.hipStreamDestroy(stream)

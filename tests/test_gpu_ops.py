@@ -62,7 +62,7 @@ def test_eltwise(gpu, oracle, op, n, d):
 
 
 @pytest.mark.parametrize("d", [F32, F16])
-@pytest.mark.parametrize("rows,n", [(1, 896), (3, 1536), (128, 1000), (2, 5)])
+@pytest.mark.parametrize("rows,n", [(1, 896), (3, 1536), (128, 1000), (2, 5), (2, 4864), (1, 8960), (3, 2055)])
 def test_rms_norm(gpu, oracle, rows, n, d):
     print(f"[case] rms_norm rows={rows} n={n} dtype={d}", flush=True)
     rng = np.random.default_rng(rows * n)
