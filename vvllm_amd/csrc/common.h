@@ -169,6 +169,12 @@ constexpr int kFirstNone = 0;
 constexpr int kFirstRms = 1;   // rows of K <= 1024 (2 chunks of 8 per lane)
 constexpr int kFirstRms4 = 2;  // rows of K <= 2048 (4 chunks per lane)
 constexpr int kFirstAttn = 3;
+// k_dot_grouped epilogue kinds (a template parameter): every epilogue behind
+// run-time tests, or only the plain store, the SiLU-gated or the RoPE one
+constexpr int kEpiAny = 0;
+constexpr int kEpiPlain = 1;
+constexpr int kEpiGlu = 2;
+constexpr int kEpiRope = 3;
 inline int dot_first_rms(int64_t M, int64_t K)
 {
     if (M > 4 || K % 16 != 0 || !dot_x_in_lds(M, K)) return kFirstNone;

@@ -1077,7 +1077,14 @@ __global__ __launch_bounds__(256) void k_dot(const int8_t* w, const void* inp, c
 // registers at dispatch); larger plans: block b serves problem
 // table[block_prob[b]].  `pos`: the position of activation row 0 for
 // problems with a RoPE epilogue.
-template <typename OT, int MT, bool XLDS, bool EARLY, int DEPTH, int FS>
+//
+// EP: the epilogue kinds the launch's problems use, fixed per launch by the
+// host where it pays (single-row plans of the decode step): kEpiAny keeps
+// every epilogue behind a run-time test; kEpiPlain, kEpiGlu and kEpiRope
+// compile in one kind only.  The code of an epilogue a kernel can take but
+// does not run still cost a one-row plan about 0.3 us per launch
+// (graph-replayed, a 9728 x 896 plan: 4.68 against 4.37 us).
+template <typename OT, int MT, bool XLDS, bool EARLY, int DEPTH, int FS, int EP>
 __global__ __launch_bounds__(256) void k_dot_grouped(int32_t b1, int32_t b2, int32_t b3, int32_t count, int64_t pos,
                                                      const LinArgs* __restrict__ table,
                                                      const int32_t* __restrict__ block_prob, const DotGroup g)
@@ -1087,6 +1094,15 @@ __global__ __launch_bounds__(256) void k_dot_grouped(int32_t b1, int32_t b2, int
     LinArgs a;
     if (count <= kDotInline) a = g.p[(b >= b1) + (b >= b2) + (b >= b3)];
     else a = table[*cst(block_prob + b)];
+    if constexpr (EP == kEpiPlain) {
+        a.rope = 0;
+        a.glu = 0;
+    } else if constexpr (EP == kEpiGlu) {
+        a.rope = 0;
+        a.glu = 1;
+    } else if constexpr (EP == kEpiRope) {
+        a.glu = 0;
+    }
     dot_body<OT, MT, XLDS, EARLY, DEPTH, FS>(a, b - a.block_begin, dot_smem, pos);
 }
 
@@ -1725,28 +1741,42 @@ struct DotGroupArgs {
     DotGroup g;
 };
 
-template <int MT, bool XLDS, bool EARLY, int DEPTH, int FS>
+template <int MT, bool XLDS, bool EARLY, int DEPTH, int FS, int EP>
 static void dot_grouped_launch(const DotGroupArgs& k, int out, dim3 grid, size_t lds, hipStream_t s)
 {
     if (out == VVH_F32)
-        hipLaunchKernelGGL((k_dot_grouped<float, MT, XLDS, EARLY, DEPTH, FS>), grid, dim3(256), lds, s, k.b[0],
+        hipLaunchKernelGGL((k_dot_grouped<float, MT, XLDS, EARLY, DEPTH, FS, EP>), grid, dim3(256), lds, s, k.b[0],
                            k.b[1], k.b[2], k.count, k.pos, k.table, k.block_prob, k.g);
     else
-        hipLaunchKernelGGL((k_dot_grouped<f16, MT, XLDS, EARLY, DEPTH, FS>), grid, dim3(256), lds, s, k.b[0],
+        hipLaunchKernelGGL((k_dot_grouped<f16, MT, XLDS, EARLY, DEPTH, FS, EP>), grid, dim3(256), lds, s, k.b[0],
                            k.b[1], k.b[2], k.count, k.pos, k.table, k.block_prob, k.g);
 }
 
-template <int MT, bool XLDS, bool EARLY, int FS>
+template <int MT, bool XLDS, bool EARLY, int FS, int EP = kEpiAny>
 static void dot_grouped_launch_d(const DotGroupArgs& k, int out, int depth, dim3 grid, size_t lds, hipStream_t s)
 {
-    if (depth <= 2) dot_grouped_launch<MT, XLDS, EARLY, 2, FS>(k, out, grid, lds, s);
-    else if (depth <= 4) dot_grouped_launch<MT, XLDS, EARLY, 4, FS>(k, out, grid, lds, s);
-    else dot_grouped_launch<MT, XLDS, EARLY, 7, FS>(k, out, grid, lds, s);
+    if (depth <= 2) dot_grouped_launch<MT, XLDS, EARLY, 2, FS, EP>(k, out, grid, lds, s);
+    else if (depth <= 4) dot_grouped_launch<MT, XLDS, EARLY, 4, FS, EP>(k, out, grid, lds, s);
+    else dot_grouped_launch<MT, XLDS, EARLY, 7, FS, EP>(k, out, grid, lds, s);
 }
 
-// plans take the RMSNorm first stage only (no attention merge stage)
+// plans take the RMSNorm first stage only (no attention merge stage); the
+// epilogue kinds are compiled in one at a time for the decode step's
+// single-row plans (q/k/v with RoPE, gate/up with SiLU-gating, the unfused
+// q/k/v plan), every epilogue behind run-time tests otherwise
+template <int MT, int FS>
+static void dot_grouped_launch_rms(const DotGroupArgs& k, int out, int ep, int depth, dim3 grid, size_t lds,
+                                   hipStream_t s)
+{
+    if constexpr (MT == 1) {
+        if (ep == kEpiGlu) return dot_grouped_launch_d<MT, true, true, FS, kEpiGlu>(k, out, depth, grid, lds, s);
+        if (ep == kEpiRope) return dot_grouped_launch_d<MT, true, true, FS, kEpiRope>(k, out, depth, grid, lds, s);
+    }
+    dot_grouped_launch_d<MT, true, true, FS>(k, out, depth, grid, lds, s);
+}
+
 template <int MT, bool XLDS>
-static void dot_grouped_launch_e(const DotGroupArgs& k, int out, bool early, int fs, int depth, dim3 grid,
+static void dot_grouped_launch_e(const DotGroupArgs& k, int out, bool early, int fs, int ep, int depth, dim3 grid,
                                  size_t lds, hipStream_t s)
 {
     if (!early) {
@@ -1754,9 +1784,11 @@ static void dot_grouped_launch_e(const DotGroupArgs& k, int out, bool early, int
         return;
     }
     if constexpr (XLDS && MT <= 4) {
-        if (fs == kFirstRms) return dot_grouped_launch_d<MT, true, true, kFirstRms>(k, out, depth, grid, lds, s);
-        if (fs == kFirstRms4) return dot_grouped_launch_d<MT, true, true, kFirstRms4>(k, out, depth, grid, lds, s);
+        if (fs == kFirstRms) return dot_grouped_launch_rms<MT, kFirstRms>(k, out, ep, depth, grid, lds, s);
+        if (fs == kFirstRms4) return dot_grouped_launch_rms<MT, kFirstRms4>(k, out, ep, depth, grid, lds, s);
     }
+    if constexpr (MT == 1 && !XLDS)
+        if (ep == kEpiPlain) return dot_grouped_launch_d<MT, false, true, kFirstNone, kEpiPlain>(k, out, depth, grid, lds, s);
     dot_grouped_launch_d<MT, XLDS, true, kFirstNone>(k, out, depth, grid, lds, s);
 }
 
@@ -1785,21 +1817,29 @@ int launch_dot_grouped(const LinArgs* dev_table, const int32_t* dev_block_prob, 
         const int f = args[i].xop == 1 ? dot_first_rms(args[i].M, args[i].K) : kFirstNone;
         fs = f == kFirstNone ? kFirstNone : std::max(fs, f);
     }
+    // the one epilogue kind every problem takes, where there is one
+    bool any_glu = false, all_glu = count > 0, any_rope = false;
+    for (int i = 0; i < count; ++i) {
+        any_glu = any_glu || args[i].glu != 0;
+        all_glu = all_glu && args[i].glu != 0;
+        any_rope = any_rope || args[i].rope != 0;
+    }
+    const int ep = all_glu && !any_rope ? kEpiGlu : !any_glu && any_rope ? kEpiRope : !any_glu ? kEpiPlain : kEpiAny;
     if (max_m <= 1) {
-        if (x_in_lds) dot_grouped_launch_e<1, true>(k, out, early, fs, depth, grid, lds_bytes, s);
-        else dot_grouped_launch_e<1, false>(k, out, early, fs, depth, grid, lds_bytes, s);
+        if (x_in_lds) dot_grouped_launch_e<1, true>(k, out, early, fs, ep, depth, grid, lds_bytes, s);
+        else dot_grouped_launch_e<1, false>(k, out, early, fs, ep, depth, grid, lds_bytes, s);
     } else if (max_m <= 2) {
-        if (x_in_lds) dot_grouped_launch_e<2, true>(k, out, early, fs, depth, grid, lds_bytes, s);
-        else dot_grouped_launch_e<2, false>(k, out, early, fs, depth, grid, lds_bytes, s);
+        if (x_in_lds) dot_grouped_launch_e<2, true>(k, out, early, fs, ep, depth, grid, lds_bytes, s);
+        else dot_grouped_launch_e<2, false>(k, out, early, fs, ep, depth, grid, lds_bytes, s);
     } else if (max_m <= 4) {
-        if (x_in_lds) dot_grouped_launch_e<4, true>(k, out, early, fs, depth, grid, lds_bytes, s);
-        else dot_grouped_launch_e<4, false>(k, out, early, fs, depth, grid, lds_bytes, s);
+        if (x_in_lds) dot_grouped_launch_e<4, true>(k, out, early, fs, ep, depth, grid, lds_bytes, s);
+        else dot_grouped_launch_e<4, false>(k, out, early, fs, ep, depth, grid, lds_bytes, s);
     } else if (max_m <= 8) {
-        if (x_in_lds) dot_grouped_launch_e<8, true>(k, out, early, fs, depth, grid, lds_bytes, s);
-        else dot_grouped_launch_e<8, false>(k, out, early, fs, depth, grid, lds_bytes, s);
+        if (x_in_lds) dot_grouped_launch_e<8, true>(k, out, early, fs, ep, depth, grid, lds_bytes, s);
+        else dot_grouped_launch_e<8, false>(k, out, early, fs, ep, depth, grid, lds_bytes, s);
     } else {
-        if (x_in_lds) dot_grouped_launch_e<16, true>(k, out, early, fs, depth, grid, lds_bytes, s);
-        else dot_grouped_launch_e<16, false>(k, out, early, fs, depth, grid, lds_bytes, s);
+        if (x_in_lds) dot_grouped_launch_e<16, true>(k, out, early, fs, ep, depth, grid, lds_bytes, s);
+        else dot_grouped_launch_e<16, false>(k, out, early, fs, ep, depth, grid, lds_bytes, s);
     }
     return (int)hipGetLastError();
 }
