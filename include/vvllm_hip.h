@@ -342,6 +342,18 @@ VVH_API int vvh_plan_set_input_op(vvh_plan plan, int in_op, const float* in_w, f
  * argument of each run: vvh_plan_run_pos (vvh_plan_run runs at position 0). */
 VVH_API int vvh_plan_set_rope(vvh_plan plan, size_t q_index, size_t k_index, size_t v_index, size_t head_dim,
                               float theta, void* k_cache, void* v_cache);
+/* Cosine/sine table of a plan's RoPE epilogue (no reference counterpart):
+ * the plan keeps cos and sin of every pair at positions [0, positions)
+ * (positions * head_dim floats, worked out once by vvh_rope's arithmetic),
+ * and runs whose rows all fall inside it read them instead of working them
+ * out (the fp64 argument reduction of each pair); later positions still work
+ * them out.  Changes no output bit.  Without it the table holds position 0
+ * only.  positions in [1, 2^20]; the plan must have its RoPE epilogue.  Like
+ * vvh_plan_set_rope it waits for the device and rewrites the plan's table in
+ * place: call it before capturing graphs that run the plan.  The table
+ * replaced stays allocated until the plan is destroyed (graphs captured
+ * before may read it). */
+VVH_API int vvh_plan_set_rope_table(vvh_plan plan, size_t positions);
 /* SiLU-gated epilogue (no reference counterpart): problem `index` of the
  * plan has weights [gate | up] (N = 2 * inter rows, inter % 8 == 0, no
  * residual) and writes, instead of its N outputs per row, M rows of inter

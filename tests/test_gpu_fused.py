@@ -238,22 +238,27 @@ def _qkv_plan(bufs, src, ws, M, K, outd):
     return h.value
 
 
-@pytest.mark.parametrize("M,H,KVH,D,pos,outd,stage", [
-    (1, 14, 2, 64, 511, F16, True),    # Qwen2.5-0.5B, as the fused decode step runs it
-    (1, 14, 2, 64, 0, F16, False),
-    (2, 4, 4, 128, 37, F16, True),     # two positions in one run, MHA, head_dim 128
-    (1, 8, 2, 32, 1000, F32, False),   # fp32 outputs and caches, head_dim 32
-    (2, 12, 2, 128, 5, F32, True),
-    (5, 4, 2, 64, 100, F16, False),    # 5-8 rows: the MFMA dot path's 8-row operands
-    (8, 8, 2, 128, 3, F32, False),
-    (1, 3, 1, 32, 9, F16, True),       # head_dim 32 and 48: tile counts that leave idle tiles in the last block
-    (1, 5, 1, 48, 3, F16, True),
+# tab: positions of the plan's cosine/sine table (vvh_plan_set_rope_table;
+# 0 = not called, the table holds position 0 only); runs whose rows all fall
+# inside it read the table, the others work the values out
+@pytest.mark.parametrize("M,H,KVH,D,pos,outd,stage,tab", [
+    (1, 14, 2, 64, 511, F16, True, 2048),  # Qwen2.5-0.5B, as the fused decode step runs it
+    (1, 14, 2, 64, 511, F16, True, 0),
+    (1, 14, 2, 64, 0, F16, False, 0),      # position 0: the default table
+    (2, 4, 4, 128, 37, F16, True, 38),     # two positions in one run, MHA, head_dim 128; row 1 past the table
+    (1, 8, 2, 32, 1000, F32, False, 1001),  # fp32 outputs and caches, head_dim 32; the table's last position
+    (2, 12, 2, 128, 5, F32, True, 7),
+    (5, 4, 2, 64, 100, F16, False, 4096),  # 5-8 rows: the MFMA dot path's 8-row operands
+    (8, 8, 2, 128, 3, F32, False, 11),
+    (8, 8, 2, 128, 3, F32, False, 0),
+    (1, 3, 1, 32, 9, F16, True, 0),        # head_dim 32 and 48: tile counts that leave idle tiles in the last block
+    (1, 5, 1, 48, 3, F16, True, 64),
 ])
-def test_plan_rope_epilogue(gpu, M, H, KVH, D, pos, outd, stage):
+def test_plan_rope_epilogue(gpu, M, H, KVH, D, pos, outd, stage, tab):
     """RoPE and the K/V cache append as the epilogue of the q/k/v plan
     (vvh_plan_set_rope, vvh_plan_run_pos) against the plan's plain run
     followed by vvh_rope_append, bit for bit: q, k, v and both caches."""
-    print(f"[case] plan rope M={M} H={H} KVH={KVH} D={D} pos={pos} out={outd} stage={stage}", flush=True)
+    print(f"[case] plan rope M={M} H={H} KVH={KVH} D={D} pos={pos} out={outd} stage={stage} tab={tab}", flush=True)
     rng = np.random.default_rng(M * 1000 + H * 10 + D + pos)
     K, theta, eps, cap = 896, 1e6, 1e-6, pos + M + 3
     dt = np.float16 if outd == F16 else np.float32
@@ -280,6 +285,8 @@ def test_plan_rope_epilogue(gpu, M, H, KVH, D, pos, outd, stage):
                           theta, outd, None)
             else:
                 capi.call("vvh_plan_set_rope", h, 0, 1, 2, D, theta, kc.ptr, vc.ptr)
+                if tab:
+                    capi.call("vvh_plan_set_rope_table", h, tab)
                 capi.call("vvh_plan_run_pos", h, pos, None)
             capi.sync()
         finally:
@@ -309,7 +316,11 @@ def test_plan_rope_limits(gpu):
         assert st(0, 1, 2, 48, 1e6, kc.ptr, vc.ptr) == invalid         # 128 rows are not whole heads of 48
         assert st(0, 1, 2, 32, 0.0, kc.ptr, vc.ptr) == invalid         # theta
         assert st(0, 1, 2, 32, 1e6, None, vc.ptr) == invalid           # no cache
+        tab = lambda n: capi.status_of("vvh_plan_set_rope_table", h, n)
+        assert tab(16) == invalid                                      # no RoPE epilogue yet
         assert st(0, 1, 2, 32, 1e6, kc.ptr, vc.ptr) == 0
+        assert tab(0) == invalid and tab((1 << 20) + 1) == invalid     # positions
+        assert tab(16) == 0 and tab(1 << 20) == 0
     finally:
         capi.call("vvh_plan_destroy", h)
 

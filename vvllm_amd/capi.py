@@ -73,6 +73,7 @@ SIGNATURES = {
     "vvh_plan_run": (c_int, [c_uint64, c_void_p]),
     "vvh_plan_set_input_op": (c_int, [c_uint64, c_int, c_void_p, c_float]),
     "vvh_plan_set_rope": (c_int, [c_uint64, c_size_t, c_size_t, c_size_t, c_size_t, c_float, c_void_p, c_void_p]),
+    "vvh_plan_set_rope_table": (c_int, [c_uint64, c_size_t]),
     "vvh_plan_run_pos": (c_int, [c_uint64, c_size_t, c_void_p]),
     "vvh_plan_set_glu": (c_int, [c_uint64, c_size_t]),
     "vvh_kv_append": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),

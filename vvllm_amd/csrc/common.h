@@ -59,6 +59,11 @@ struct LinArgs {
     float rope_theta;
     void* cache;
     const float* rope_freq;  // q and k rows: rope_freq(i, rope_d, rope_theta) for i < rope_d / 2
+    // q and k rows: rope_cs of pair i at position p in rope_cs[2 (p rope_d / 2
+    // + i)] (cosine) and the float after it (sine) for p < rope_cs_n
+    // (rope_cs_n >= 1); positions past the table work them out from rope_freq
+    const float* rope_cs;
+    int64_t rope_cs_n;
     int32_t src;  // plans: index of the problem in the caller's list
     // plans: 1 = SiLU-gated epilogue: the N rows are [gate | up] of N / 2
     // each and out gets M rows of N / 2 values silu(gate) * up
@@ -130,6 +135,8 @@ inline int64_t decode_blocks(const LinArgs& a)
 // k_dot (M <= 16): 16-row tiles, 128-wide k steps, ksplit waves per tile.
 constexpr int64_t kDotMaxM = 16;
 constexpr int kStageMaxM = 4;  // rows of a decode linear with an input stage
+// longest cosine/sine table of a plan's RoPE epilogue (vvh_plan_set_rope_table)
+constexpr int64_t kRopeTableMaxPositions = (int64_t)1 << 20;
 // attention merge stage: at most kAttnMaxParts parts, K <= kAttnMergeMaxK (4 per thread)
 constexpr int kAttnMaxParts = 8;
 constexpr int kAttnMergeMaxK = 1024;
@@ -253,6 +260,9 @@ int launch_rms_norm(void* out, const void* x, const float* w, int64_t rows, int6
 int launch_softmax(void* out, const void* x, int64_t rows, int64_t n, int dtype, void* stream);
 // out[i] = rope_freq(i, D, theta) for i < D / 2
 int launch_rope_freq(float* out, int64_t D, float theta, void* stream);
+// out[2 (p D / 2 + i)], out[2 (p D / 2 + i) + 1] = rope_cs_freq(p, freq[i])
+// (cosine, sine) for p < positions, i < D / 2
+int launch_rope_table(float* out, const float* freq, int64_t positions, int64_t D, void* stream);
 int launch_rope(void* q, void* k, int64_t S, int64_t H, int64_t KVH, int64_t D, int64_t pos, float theta, int dtype,
                 void* stream);
 int launch_rope_append(void* q, void* k, const void* v, void* kc, void* vc, int64_t S, int64_t H, int64_t KVH,

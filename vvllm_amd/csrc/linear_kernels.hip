@@ -582,10 +582,16 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
     // residuals and weights stay inside the problem; it stores nothing
     const int64_t tile_r = n0 < a.N ? c.tile : 0;
     int64_t rowA, rowB;
+    int32_t pidx = 0;  // rotated rows: the pair's index within its head, < rope_d / 2
     if (pair) {
-        const int64_t tph = a.rope_d / 16;
-        const int64_t hd = tile_r / tph, sd = tile_r - hd * tph;
-        rowA = hd * a.rope_d + 8 * sd + r;
+        // 32-bit wave-uniform division (rows < 2^31, checked with the
+        // epilogue, so tiles < 2^27): the rows feed the
+        // first weight loads, so a 64-bit division here delays the whole ring
+        const int32_t tph = a.rope_d >> 4;
+        const int32_t t = __builtin_amdgcn_readfirstlane((int32_t)tile_r);
+        const int32_t hd = t / tph, sd = t - hd * tph;
+        pidx = 8 * sd + r;
+        rowA = (int64_t)hd * a.rope_d + pidx;
         rowB = rowA + a.rope_d / 2;
     } else if (a.glu) {
         // gate row 8 t + r and its up row (N % 16 == 0: every tile is whole)
@@ -714,14 +720,25 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
     // k rows).  Early launches work them out right after requesting the
     // weights, while the loads are in flight: they take a long chain of fp64
     // operations that depends only on the position and the pair.
-    // The pair's frequency comes from the plan's table (rowA % rope_d is the
-    // pair's index within its head, < rope_d / 2).
+    // Positions the plan's cosine/sine table holds (every row's, tab) are
+    // read from it with the other epilogue operands and only used at the
+    // store; past the table they come from the pair's frequency.  Either
+    // way the values are rope_cs_freq's, so the table changes no bit.
     float rc[MT], rs[MT], rfreq = 0.0f;
+    f2 rt[MT];
+    const bool tab = pos >= 0 && pos + a.M <= a.rope_cs_n;
     auto rope_load = [&]() {
-        if (pair) rfreq = *gbl(a.rope_freq + rowA % a.rope_d);
+        if (pair) {
+            rfreq = *gbl(a.rope_freq + pidx);
+#pragma unroll
+            for (int m = 0; m < MT; m++) {
+                const int64_t pm = pos + m < a.rope_cs_n ? pos + m : a.rope_cs_n - 1;
+                rt[m] = *gbl(reinterpret_cast<const f2*>(a.rope_cs) + pm * (a.rope_d / 2) + pidx);
+            }
+        }
     };
     auto rope_prep = [&]() {
-        if (pair) {
+        if (pair && !tab) {
 #pragma unroll
             for (int m = 0; m < MT; m++) rope_cs_freq(pos + m, rfreq, rc[m], rs[m]);
         }
@@ -802,7 +819,6 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
             // around the loads (a conditional load would make the compiler
             // wait for every older one): slots past the part count re-read
             // part np - 1 and threads past K / 4 the last chunk, unused
-            typedef float f2 __attribute__((ext_vector_type(2)));
             typedef _Float16 h4 __attribute__((ext_vector_type(4)));
             const float* pp = static_cast<const float*>(a.inp);
             const int32_t hd = a.xhd, np = a.xparts, pitch = hd + 4;
@@ -1016,6 +1032,13 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
             if constexpr (!EARLY) {
                 rope_load();
                 rope_prep();
+            }
+            if (tab) {
+#pragma unroll
+                for (int m = 0; m < MT; m++) {
+                    rc[m] = rt[m][0];
+                    rs[m] = rt[m][1];
+                }
             }
             dot_store_rope<OT, MT, EARLY>(a, pos, rowA, rowB, accA, accB, e_sc, e_bi, e_res, rc, rs);
         }

@@ -269,6 +269,25 @@ int launch_rope_freq(float* out, int64_t D, float theta, void* stream)
     return (int)hipGetLastError();
 }
 
+__global__ __launch_bounds__(256) void k_rope_table(float2* __restrict__ out, const float* __restrict__ freq,
+                                                    int64_t n, int64_t half)
+{
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= n) return;
+    const int64_t p = e / half, i = e - p * half;
+    float c, sn;
+    rope_cs_freq(p, freq[i], c, sn);
+    out[e] = make_float2(c, sn);
+}
+
+int launch_rope_table(float* out, const float* freq, int64_t positions, int64_t D, void* stream)
+{
+    const int64_t n = positions * (D / 2);
+    hipLaunchKernelGGL(k_rope_table, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       reinterpret_cast<float2*>(out), freq, n, D / 2);
+    return (int)hipGetLastError();
+}
+
 int launch_rope(void* q, void* k, int64_t S, int64_t H, int64_t KVH, int64_t D, int64_t pos, float theta, int dtype,
                 void* stream)
 {

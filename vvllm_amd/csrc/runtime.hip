@@ -108,8 +108,10 @@ struct Plan {
     int max_m = 0;
     void* dev_stream = nullptr;  // tile_prob, list, list_off
     float* rope_freq = nullptr;  // RoPE epilogue: the pair frequencies of the q and k rows
-    // tables replaced by a later vvh_plan_set_rope: a graph captured before
-    // may still read them, so they are freed with the plan
+    float* rope_cs = nullptr;    // RoPE epilogue: cosine and sine of positions [0, rope_cs_n)
+    int64_t rope_cs_n = 0;
+    // tables replaced by a later vvh_plan_set_rope or vvh_plan_set_rope_table:
+    // a graph captured before may still read them, so they are freed with the plan
     std::vector<float*> rope_retired;
 };
 std::mutex g_pmu;
@@ -1599,6 +1601,8 @@ VVH_API int vvh_plan_set_rope(vvh_plan plan, size_t q_index, size_t k_index, siz
     if (!q || !k || !v) return fail(VVH_ERR_INVALID_ARG, "q, k or v index names no (non-empty) problem of the plan");
     if (q->glu || k->glu || v->glu)
         return fail(VVH_ERR_INVALID_ARG, "a problem with the SiLU-gated epilogue cannot take RoPE");
+    if (q->N > INT32_MAX || k->N > INT32_MAX)  // the epilogue maps tiles to row pairs in 32 bits
+        return fail(VVH_ERR_UNSUPPORTED, "RoPE epilogue needs q and k rows below 2^31");
     if (q->N % (int64_t)head_dim != 0 || k->N % (int64_t)head_dim != 0 || k->N != v->N || k->M != v->M ||
         q->M != k->M)
         return fail(VVH_ERR_INVALID_ARG, "q rows (%lld), k and v rows (%lld, %lld) must be whole heads of %zu, with "
@@ -1607,14 +1611,19 @@ VVH_API int vvh_plan_set_rope(vvh_plan plan, size_t q_index, size_t k_index, siz
     hipError_t fe = hipDeviceSynchronize();
     if (fe != hipSuccess) return fail_hip(fe, "plan RoPE epilogue: synchronize (no change made)");
     // the pair frequencies, worked out once on the device by the function
-    // vvh_rope uses
+    // vvh_rope uses, and the cosine/sine table of position 0 (a longer one
+    // comes from vvh_plan_set_rope_table)
     float* freq = nullptr;
+    float* cs = nullptr;
     fe = hipMalloc(&freq, head_dim / 2 * sizeof(float));
+    if (fe == hipSuccess) fe = hipMalloc(&cs, head_dim * sizeof(float));
     if (fe == hipSuccess) fe = (hipError_t)launch_rope_freq(freq, (int64_t)head_dim, theta, nullptr);
+    if (fe == hipSuccess) fe = (hipError_t)launch_rope_table(cs, freq, 1, (int64_t)head_dim, nullptr);
     if (fe == hipSuccess) fe = hipDeviceSynchronize();
     if (fe != hipSuccess) {
         (void)hipGetLastError();
         if (freq) (void)hipFree(freq);
+        if (cs) (void)hipFree(cs);
         return fail_hip(fe, "RoPE frequency table (no change made)");
     }
     q->rope = 1;
@@ -1628,6 +1637,8 @@ VVH_API int vvh_plan_set_rope(vvh_plan plan, size_t q_index, size_t k_index, siz
     k->cache = k_cache;
     v->cache = v_cache;
     q->rope_freq = k->rope_freq = freq;
+    q->rope_cs = k->rope_cs = cs;
+    q->rope_cs_n = k->rope_cs_n = 1;
     const hipError_t e = hipMemcpy(const_cast<LinArgs*>(p.sargs.table), next.data(), next.size() * sizeof(LinArgs),
                                    hipMemcpyHostToDevice);
     if (e != hipSuccess) {
@@ -1636,10 +1647,62 @@ VVH_API int vvh_plan_set_rope(vvh_plan plan, size_t q_index, size_t k_index, siz
         (void)hipMemcpy(const_cast<LinArgs*>(p.sargs.table), p.args.data(), p.args.size() * sizeof(LinArgs),
                         hipMemcpyHostToDevice);
         (void)hipFree(freq);
+        (void)hipFree(cs);
         return fail_hip(e, "plan table upload (no change made)");
     }
     if (p.rope_freq) p.rope_retired.push_back(p.rope_freq);
+    if (p.rope_cs) p.rope_retired.push_back(p.rope_cs);
     p.rope_freq = freq;
+    p.rope_cs = cs;
+    p.rope_cs_n = 1;
+    p.args = std::move(next);
+    return VVH_OK;
+}
+
+VVH_API int vvh_plan_set_rope_table(vvh_plan plan, size_t positions)
+{
+    REQUIRE_INIT();
+    std::lock_guard<std::mutex> lock(g_pmu);
+    auto it = g_plans.find(plan);
+    if (it == g_plans.end()) return fail(VVH_ERR_UNKNOWN_HANDLE, "unknown plan %llu", (unsigned long long)plan);
+    Plan& p = it->second;
+    if (!p.rope_freq) return fail(VVH_ERR_INVALID_ARG, "the plan has no RoPE epilogue (vvh_plan_set_rope first)");
+    if (positions < 1 || positions > kRopeTableMaxPositions)
+        return fail(VVH_ERR_INVALID_ARG, "RoPE table positions must be in [1, %lld] (got %zu)",
+                    (long long)kRopeTableMaxPositions, positions);
+    std::vector<LinArgs> next = p.args;
+    int64_t d = 0;
+    for (const LinArgs& a : next)
+        if (a.rope == 1) d = a.rope_d;
+    hipError_t fe = hipDeviceSynchronize();
+    if (fe != hipSuccess) return fail_hip(fe, "plan RoPE table: synchronize (no change made)");
+    float* cs = nullptr;
+    fe = hipMalloc(&cs, positions * (size_t)d * sizeof(float));
+    if (fe == hipSuccess) fe = (hipError_t)launch_rope_table(cs, p.rope_freq, (int64_t)positions, d, nullptr);
+    if (fe == hipSuccess) fe = hipDeviceSynchronize();
+    if (fe != hipSuccess) {
+        (void)hipGetLastError();
+        if (cs) (void)hipFree(cs);
+        return fail_hip(fe, "RoPE cosine/sine table (no change made)");
+    }
+    for (LinArgs& a : next) {
+        if (a.rope == 1 || a.rope == 2) {
+            a.rope_cs = cs;
+            a.rope_cs_n = (int64_t)positions;
+        }
+    }
+    const hipError_t e = hipMemcpy(const_cast<LinArgs*>(p.sargs.table), next.data(), next.size() * sizeof(LinArgs),
+                                   hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        (void)hipMemcpy(const_cast<LinArgs*>(p.sargs.table), p.args.data(), p.args.size() * sizeof(LinArgs),
+                        hipMemcpyHostToDevice);
+        (void)hipFree(cs);
+        return fail_hip(e, "plan table upload (no change made)");
+    }
+    p.rope_retired.push_back(p.rope_cs);
+    p.rope_cs = cs;
+    p.rope_cs_n = (int64_t)positions;
     p.args = std::move(next);
     return VVH_OK;
 }
@@ -1688,6 +1751,7 @@ VVH_API int vvh_plan_destroy(vvh_plan plan)
     if (it->second.dev_table) (void)hipFree(it->second.dev_table);
     if (it->second.dev_stream) (void)hipFree(it->second.dev_stream);
     if (it->second.rope_freq) (void)hipFree(it->second.rope_freq);
+    if (it->second.rope_cs) (void)hipFree(it->second.rope_cs);
     for (float* t : it->second.rope_retired) (void)hipFree(t);
     g_plans.erase(it);
     return VVH_OK;

@@ -18,7 +18,8 @@ codes through linear_q8 (the int8 LM head).
 fused=True (fp16 only) issues the same arithmetic in fewer launches: the
 RMSNorms before q/k/v and gate_up run in the input stage of those plans
 (vvh_plan_set_input_op), RoPE and the K/V cache rows are the epilogue of the
-q/k/v plan (vvh_plan_set_rope, vvh_plan_run_pos), the SiLU-mul is the
+q/k/v plan (vvh_plan_set_rope, vvh_plan_run_pos; its cosines and sines
+come from a per-plan table, vvh_plan_set_rope_table), the SiLU-mul is the
 epilogue of the gate_up plan (vvh_plan_set_glu), attention over spans of up
 to 512 positions runs as per-wave parts (vvh_attention_parts) that the o
 projection merges in its input stage (vvh_linear_q8_dev_attn), and the
@@ -162,6 +163,8 @@ class Model:
                 capi.call("vvh_plan_set_input_op", h.value, capi.IN_RMS_NORM, L["ln1"].ptr, c.eps)
                 # RoPE and the K/V cache rows in the plan's epilogue (problems 0, 1, 2 = q, k, v)
                 capi.call("vvh_plan_set_rope", h.value, 0, 1, 2, c.head_dim, c.theta, L["kc"].ptr, L["vc"].ptr)
+                # cosine/sine of every position the cache holds, read by the epilogue
+                capi.call("vvh_plan_set_rope_table", h.value, max_ctx)
         # fused: attention over spans of at most ATTN_PARTS_MAX_SPAN positions
         # as per-wave parts (vvh_attention_parts), merged in the o projection's
         # input stage (vvh_linear_q8_dev_attn): the same row as vvh_attention
