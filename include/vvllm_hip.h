@@ -467,8 +467,9 @@ VVH_API int vvh_attention_parts(float* parts, size_t parts_floats, size_t* npart
  * from nparts parts of vvh_attention_parts (K = num_heads * head_dim): the
  * attention output and the o projection (+ residual, may alias out) of a
  * decode step in one launch, on the k_dot family, equal to vvh_attention
- * followed by vvh_linear_q8_dev on that family.  K % 16 == 0, K <= 1024,
- * 16-byte aligned parts and weights; otherwise VVH_ERR_UNSUPPORTED. */
+ * followed by vvh_linear_q8_dev on that family.  head_dim a power of two
+ * dividing K (else VVH_ERR_INVALID_ARG); K % 16 == 0, K <= 1024, 16-byte
+ * aligned parts and weights; otherwise VVH_ERR_UNSUPPORTED. */
 VVH_API int vvh_linear_q8_dev_attn(void* out, const float* parts, size_t nparts, size_t head_dim,
                                    const int8_t* dev_weight, const float* dev_scales, const float* dev_bias,
                                    const void* residual, size_t N, size_t K, int out_dtype, void* stream);

@@ -390,6 +390,7 @@ def test_attention_parts_limits(gpu):
     assert so(out.ptr, parts.ptr, 0, D, dq.ptr, ds.ptr, None, None, 896, 896, F16, None) == invalid
     assert so(out.ptr, parts.ptr, 9, D, dq.ptr, ds.ptr, None, None, 896, 896, F16, None) == invalid
     assert so(out.ptr, parts.ptr, 8, 60, dq.ptr, ds.ptr, None, None, 896, 896, F16, None) == invalid
+    assert so(out.ptr, parts.ptr, 8, 112, dq.ptr, ds.ptr, None, None, 896, 896, F16, None) == invalid  # not 2^n
     big_q, big_s = q8_weight(rng, 16, 1536)
     assert so(out.ptr, parts.ptr, 8, 64, big_q.ptr, big_s.ptr, None, None, 16, 1536, F16, None) == unsupported
     assert so(out.ptr, parts.ptr, 8, D, dq.ptr, ds.ptr, None, None, 896, 896, F16, None) == 0

@@ -121,12 +121,11 @@ __device__ __forceinline__ float rms_sumsq_h8(float ss, const h8 x, bool ok)
     for (int e = 0; e < 8; e++) v[e] = ok ? (float)x[e] : 0.0f;
     return rms_sumsq8(ss, v);
 }
-__device__ __forceinline__ float wave_sum_xor(float v)
-{
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-    return v;
-}
+// Sum over the wave, every lane getting the same bits: group_sum(v, 64)
+// (pairs of lanes 1, 2, 4, 8 apart within rows of 16 as DPP moves, then the
+// four row sums as (R0 + R1) + (R2 + R3) through row broadcasts and a lane
+// read, no LDS-pipeline round trip).
+__device__ __forceinline__ float wave_sum_xor(float v);
 
 // RMSNorm's divisor and output, and the SiLU-gated product, in the
 // reference's fp32 operation order (backend_naive.cc:68-76, :297-298); used by
@@ -206,16 +205,27 @@ __device__ __forceinline__ float dpp_mov(float v)
 // Sum / max over aligned groups of L lanes (L = 1, 2, 4, ..., 64,
 // wave-uniform); every lane of a group gets the group's result.  DPP steps
 // within rows of 16, shuffles across rows.  All lanes must be active.
+// L = 64 adds the row sums as the xor-16 and xor-32 shuffles would, (R0 +
+// R1) + (R2 + R3) (each addition commutes, so the bits are the same), from
+// row_bcast15 (rows 1 and 3 add lane 15 of rows 0 and 2) and row_bcast31
+// (row 3 adds lane 31), then lane 63 read into a scalar register.
 __device__ __forceinline__ float group_sum(float v, int L)
 {
     if (L >= 2) v += dpp_mov<0xB1>(v);
     if (L >= 4) v += dpp_mov<0x4E>(v);
     if (L >= 8) v += dpp_mov<0x141>(v);
     if (L >= 16) v += dpp_mov<0x140>(v);
+    if (L >= 64) {
+        const int vi = __builtin_bit_cast(int, v);
+        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, vi, 0x142, 0xA, 0xF, false));
+        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x143, 0xC, 0xF,
+                                                                   false));
+        return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+    }
     if (L >= 32) v += __shfl_xor(v, 16);
-    if (L >= 64) v += __shfl_xor(v, 32);
     return v;
 }
+__device__ __forceinline__ float wave_sum_xor(float v) { return group_sum(v, 64); }
 __device__ __forceinline__ float group_max(float v, int L)
 {
     if (L >= 2) v = fmaxf(v, dpp_mov<0xB1>(v));

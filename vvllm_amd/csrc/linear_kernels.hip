@@ -821,10 +821,12 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
             // part np - 1 and threads past K / 4 the last chunk, unused
             typedef _Float16 h4 __attribute__((ext_vector_type(4)));
             const float* pp = static_cast<const float*>(a.inp);
-            const int32_t hd = a.xhd, np = a.xparts, pitch = hd + 4;
-            const int32_t heads = (int32_t)a.K / hd, chunks = (int32_t)a.K / 4;
+            // xhd is a power of two (checked by vvh_linear_q8_dev_attn): shifts
+            // instead of divisions ahead of the part loads
+            const int32_t hd = a.xhd, lg = __builtin_ctz((uint32_t)hd), np = a.xparts, pitch = hd + 4;
+            const int32_t heads = (int32_t)a.K >> lg, chunks = (int32_t)a.K / 4;
             const int32_t idx0 = (int32_t)threadIdx.x, idx = idx0 < chunks ? idx0 : chunks - 1;
-            const int32_t e0 = 4 * idx, h = e0 / hd, d0 = e0 - h * hd;
+            const int32_t e0 = 4 * idx, h = e0 >> lg, d0 = e0 & (hd - 1);
             f4 po[kAttnMaxParts];
             f2 pml[kAttnMaxParts];
 #pragma unroll
@@ -839,21 +841,25 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
             for (int u = 0; u < D; u++) issue(u, (int32_t)c.s0 + u);
             __builtin_amdgcn_sched_barrier(0);
             if (idx0 < chunks) {
+                // slots past np hold part np - 1 again: the maximum is the
+                // same, and their sums are computed and dropped by a select
+                // (no branch per part, and no 0 * inf where a part holds inf)
                 float M = -INFINITY;
 #pragma unroll
-                for (int pc = 0; pc < kAttnMaxParts; pc++)
-                    if (pc < np) M = fmaxf(M, pml[pc][0]);
-                float num[4] = {0.0f, 0.0f, 0.0f, 0.0f}, den[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                for (int pc = 0; pc < kAttnMaxParts; pc++) M = fmaxf(M, pml[pc][0]);
+                float num[4] = {0.0f, 0.0f, 0.0f, 0.0f}, den = 0.0f;
 #pragma unroll
                 for (int pc = 0; pc < kAttnMaxParts; pc++) {
-                    if (pc < np) {
+                    const bool live = pc < np;
 #pragma unroll
-                        for (int j = 0; j < 4; j++)
-                            attn_merge_add(num[j], den[j], pml[pc][0], M, po[pc][j], pml[pc][1]);
+                    for (int j = 0; j < 4; j++) {
+                        float nj = num[j], dj = den;
+                        attn_merge_add(nj, dj, pml[pc][0], M, po[pc][j], pml[pc][1]);
+                        num[j] = live ? nj : num[j];
+                        if (j == 0) den = live ? dj : den;
                     }
                 }
-                const h4 v = {(f16)(num[0] / den[0]), (f16)(num[1] / den[1]), (f16)(num[2] / den[2]),
-                              (f16)(num[3] / den[3])};
+                const h4 v = {(f16)(num[0] / den), (f16)(num[1] / den), (f16)(num[2] / den), (f16)(num[3] / den)};
                 *reinterpret_cast<h4*>(xs + e0) = v;
             }
             __syncthreads();
@@ -993,15 +999,12 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
             }
         }
     }
-    // sum the 8 chunk lanes of each row
+    // sum the 8 chunk lanes of each row (DPP steps: lanes 1, 2, then 4 apart)
     if constexpr (!MF) {
 #pragma unroll
         for (int m = 0; m < MT; m++) {
-#pragma unroll
-            for (int off = 1; off < 8; off <<= 1) {
-                accA[m] += __shfl_xor(accA[m], off);
-                accB[m] += __shfl_xor(accB[m], off);
-            }
+            accA[m] = group_sum(accA[m], 8);
+            accB[m] = group_sum(accB[m], 8);
         }
     }
     if (!MF && c.ksplit > 1) {
@@ -1069,13 +1072,16 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
 // XLDS = the activations are staged in LDS (dot_x_in_lds, decided on the
 // host for the launch: for a grouped launch it must hold for every problem).
 // The fields that the first loads of a block depend on come first, as scalar
-// arguments, which arrive preloaded into registers at dispatch (up to 16
-// dwords; the struct is read from the kernel-argument segment when used).
+// arguments, which arrive preloaded into registers at dispatch (14 dwords
+// here; the struct is read from the kernel-argument segment when used, and
+// its first read costs a block about 0.3 us before the loads that need it
+// can issue).  mk = M | ksplit << 8; xi = xparts | xhd << 8 for the
+// attention merge stage (its part loads need both), else 0.
 // A plain call has no RoPE or SiLU-gated epilogue.
 template <typename OT, int MT, bool XLDS, bool EARLY, int DEPTH, int FS>
 __global__ __launch_bounds__(256) void k_dot(const int8_t* w, const void* inp, const float* scales,
-                                             const float* bias, const void* res, int32_t N, int32_t M, int32_t K,
-                                             int32_t ksplit, const LinArgs a)
+                                             const float* bias, const void* res, int32_t N, int32_t K, int32_t mk,
+                                             int32_t xi, const LinArgs a)
 {
     extern __shared__ __attribute__((aligned(16))) char dot_smem[];
     LinArgs b = a;
@@ -1085,9 +1091,13 @@ __global__ __launch_bounds__(256) void k_dot(const int8_t* w, const void* inp, c
     b.bias = bias;
     b.res = res;
     b.N = N;
-    b.M = M;
+    b.M = mk & 0xff;
     b.K = K;
-    b.ksplit = ksplit;
+    b.ksplit = mk >> 8;
+    if constexpr (FS == kFirstAttn) {
+        b.xparts = xi & 0xff;
+        b.xhd = xi >> 8;
+    }
     b.rope = 0;
     b.glu = 0;
     dot_body<OT, MT, XLDS, EARLY, DEPTH, FS>(b, blockIdx.x, dot_smem, 0);
@@ -1680,14 +1690,18 @@ int launch_skinny_grouped(const LinArgs* dev_table, int count, int64_t total_blo
 template <int MT, bool XLDS, bool EARLY, int DEPTH, int FS>
 static void dot_launch(const LinArgs& a, int out, dim3 grid, size_t lds, hipStream_t s)
 {
-    // dot_fits(N, K) holds (checked by the runtime)
-    const int32_t N = (int32_t)a.N, M = (int32_t)a.M, K = (int32_t)a.K;
+    // dot_fits(N, K) holds (checked by the runtime); M <= kDotMaxM, ksplit
+    // <= 4, xparts <= kAttnMaxParts and xhd <= kAttnMergeMaxK (checked by
+    // vvh_linear_q8_dev_attn) fit their fields
+    const int32_t N = (int32_t)a.N, K = (int32_t)a.K;
+    const int32_t mk = (int32_t)a.M | a.ksplit << 8;
+    const int32_t xi = FS == kFirstAttn ? (a.xparts | a.xhd << 8) : 0;
     if (out == VVH_F32)
         hipLaunchKernelGGL((k_dot<float, MT, XLDS, EARLY, DEPTH, FS>), grid, dim3(256), lds, s, a.w, a.inp,
-                           a.scales, a.bias, a.res, N, M, K, a.ksplit, a);
+                           a.scales, a.bias, a.res, N, K, mk, xi, a);
     else
         hipLaunchKernelGGL((k_dot<f16, MT, XLDS, EARLY, DEPTH, FS>), grid, dim3(256), lds, s, a.w, a.inp,
-                           a.scales, a.bias, a.res, N, M, K, a.ksplit, a);
+                           a.scales, a.bias, a.res, N, K, mk, xi, a);
 }
 
 template <int MT, bool XLDS, bool EARLY, int FS>

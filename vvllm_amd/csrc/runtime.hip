@@ -1365,8 +1365,10 @@ VVH_API int vvh_linear_q8_dev_attn(void* out, const float* parts, size_t nparts,
     if (st != VVH_OK) return st;
     if (nparts == 0 || nparts > (std::size_t)kAttnMaxParts)
         return fail(VVH_ERR_INVALID_ARG, "nparts %zu outside 1..%d", nparts, kAttnMaxParts);
-    if (head_dim == 0 || head_dim % 4 != 0 || K % head_dim != 0)
-        return fail(VVH_ERR_INVALID_ARG, "K (%zu) must be a multiple of head_dim (%zu), itself of 4", K, head_dim);
+    if (head_dim < 4 || head_dim > (std::size_t)kAttnMergeMaxK || (head_dim & (head_dim - 1)) != 0 ||
+        K % head_dim != 0)
+        return fail(VVH_ERR_INVALID_ARG, "K (%zu) must be a multiple of head_dim (%zu), a power of two from 4",
+                    K, head_dim);
     if (K % 16 != 0 || K > (std::size_t)kAttnMergeMaxK || !dot_x_in_lds(1, (int64_t)K))
         return fail(VVH_ERR_UNSUPPORTED, "attention merge stage needs K %% 16 == 0 and K <= %d (K=%zu)",
                     (int)kAttnMergeMaxK, K);
