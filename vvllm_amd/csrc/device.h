@@ -202,9 +202,53 @@ __device__ __forceinline__ float dpp_mov(float v)
 {
     return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
+// The values of lanes l & ~16 and l | 16 (p16) or l & ~32 and l | 32 (p32),
+// lower lane first, in every lane: v_permlane16_swap / v_permlane32_swap with
+// both operands the same register (one VALU op each, no LDS-pipeline round
+// trip).  a + b over them is the xor-16 / xor-32 shuffle sum with its
+// operands in a fixed order: each addition commutes, so the bits are the same.
+__device__ __forceinline__ void lanes_x16(float v, float& lo, float& hi)
+{
+    const int vi = __builtin_bit_cast(int, v);
+    const auto q = __builtin_amdgcn_permlane16_swap(vi, vi, false, false);
+    lo = __builtin_bit_cast(float, (int)q[0]);
+    hi = __builtin_bit_cast(float, (int)q[1]);
+}
+__device__ __forceinline__ void lanes_x32(float v, float& lo, float& hi)
+{
+    const int vi = __builtin_bit_cast(int, v);
+    const auto q = __builtin_amdgcn_permlane32_swap(vi, vi, false, false);
+    lo = __builtin_bit_cast(float, (int)q[0]);
+    hi = __builtin_bit_cast(float, (int)q[1]);
+}
+__device__ __forceinline__ float sum_x16(float v)
+{
+    float lo, hi;
+    lanes_x16(v, lo, hi);
+    return lo + hi;
+}
+__device__ __forceinline__ float sum_x32(float v)
+{
+    float lo, hi;
+    lanes_x32(v, lo, hi);
+    return lo + hi;
+}
+__device__ __forceinline__ float max_x16(float v)
+{
+    float lo, hi;
+    lanes_x16(v, lo, hi);
+    return fmaxf(lo, hi);
+}
+__device__ __forceinline__ float max_x32(float v)
+{
+    float lo, hi;
+    lanes_x32(v, lo, hi);
+    return fmaxf(lo, hi);
+}
+
 // Sum / max over aligned groups of L lanes (L = 1, 2, 4, ..., 64,
 // wave-uniform); every lane of a group gets the group's result.  DPP steps
-// within rows of 16, shuffles across rows.  All lanes must be active.
+// within rows of 16, lane swaps across rows.  All lanes must be active.
 // L = 64 adds the row sums as the xor-16 and xor-32 shuffles would, (R0 +
 // R1) + (R2 + R3) (each addition commutes, so the bits are the same), from
 // row_bcast15 (rows 1 and 3 add lane 15 of rows 0 and 2) and row_bcast31
@@ -222,7 +266,7 @@ __device__ __forceinline__ float group_sum(float v, int L)
                                                                    false));
         return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
     }
-    if (L >= 32) v += __shfl_xor(v, 16);
+    if (L >= 32) v = sum_x16(v);
     return v;
 }
 __device__ __forceinline__ float wave_sum_xor(float v) { return group_sum(v, 64); }
@@ -232,8 +276,8 @@ __device__ __forceinline__ float group_max(float v, int L)
     if (L >= 4) v = fmaxf(v, dpp_mov<0x4E>(v));
     if (L >= 8) v = fmaxf(v, dpp_mov<0x141>(v));
     if (L >= 16) v = fmaxf(v, dpp_mov<0x140>(v));
-    if (L >= 32) v = fmaxf(v, __shfl_xor(v, 16));
-    if (L >= 64) v = fmaxf(v, __shfl_xor(v, 32));
+    if (L >= 32) v = max_x16(v);
+    if (L >= 64) v = max_x32(v);
     return v;
 }
 

@@ -160,8 +160,7 @@ __device__ __forceinline__ void gemv_f32_body(const LinArgs& a, int64_t block, i
     // combine the four 16-byte chunks of each channel (lanes l, l^16, l^32, l^48)
 #pragma unroll
     for (int m = 0; m < MT; m++) {
-        acc[m] += __shfl_xor(acc[m], 16);
-        acc[m] += __shfl_xor(acc[m], 32);
+        acc[m] = sum_x32(sum_x16(acc[m]));
     }
     if (c.ksplit > 1) {
         if (c.lane < 16) {

@@ -752,8 +752,8 @@ __device__ __forceinline__ void attn_wave_chunks(const f16* __restrict__ kh, con
                 sc[t][i] = x;
                 cm = fmaxf(cm, x);
             }
-        cm = fmaxf(cm, __shfl_xor(cm, 16));
-        cm = fmaxf(cm, __shfl_xor(cm, 32));  // finite: key c0 is in the span
+        cm = max_x16(cm);
+        cm = max_x32(cm);  // finite: key c0 is in the span
         const float mn = fmaxf(m, cm), corr = exp2f(m - mn);  // corr = 0 on the first chunk
         float ps = 0.0f;
         h8 ph[2], pl[2];
@@ -767,8 +767,8 @@ __device__ __forceinline__ void attn_wave_chunks(const f16* __restrict__ kh, con
                 ph[u][j] = hi;
                 pl[u][j] = (_Float16)(p - (float)hi);
             }
-        ps += __shfl_xor(ps, 16);
-        ps += __shfl_xor(ps, 32);
+        ps = sum_x16(ps);
+        ps = sum_x32(ps);
         l = l * corr + ps;
         m = mn;
 #pragma unroll
