@@ -742,8 +742,14 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
             for (int m = 0; m < MT; m++) rope_cs_freq(pos + m, rfreq, rc[m], rs[m]);
         }
     };
-    if constexpr (EARLY) {
-        const float* bp = a.bias ? a.bias : a.scales;  // absent bias / residual: in-bounds reads, unused
+    // the epilogue operands of an early launch (unconditional loads: an
+    // absent bias or residual reads the scales, unused); the attention merge
+    // stage requests them after the weight ring, behind its 16 part loads per
+    // thread (o + merge 3.67 -> 3.53 us graph-replayed); the other stages
+    // before their loads, where after the ring they measured slower (down
+    // 4.56 -> 4.95 us)
+    auto epi_load = [&]() {
+        const float* bp = a.bias ? a.bias : a.scales;
         const OT* rp = a.res ? static_cast<const OT*>(a.res) : reinterpret_cast<const OT*>(a.scales);
         const int64_t rows[2] = {rowA, rowB};
 #pragma unroll
@@ -753,6 +759,9 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
 #pragma unroll
             for (int m = 0; m < MT; m++) e_res[m][h] = *gbl(rp + (a.res && m < a.M ? m * a.N : 0) + rows[h]);
         }
+    };
+    if constexpr (EARLY) {
+        if constexpr (!attn_first) epi_load();
         rope_load();
         if constexpr (!first) {
             if (active) {
@@ -838,6 +847,7 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int u = 0; u < D; u++) issue(u, (int32_t)c.s0 + u);
+            epi_load();
             __builtin_amdgcn_sched_barrier(0);
             if (idx0 < chunks) {
                 // slots past np hold part np - 1 again: the maximum is the
