@@ -298,6 +298,53 @@ def test_plan_rope_epilogue(gpu, M, H, KVH, D, pos, outd, stage, tab):
         assert np.array_equal(a, b), name
 
 
+def test_plan_rope_table_replaced(gpu):
+    """A table set, then the epilogue set again (the table back to position
+    0), then a longer table: each run equals the plain run + vvh_rope_append,
+    and runs read whichever table the plan holds at the time."""
+    print("[case] plan rope table replaced", flush=True)
+    rng = np.random.default_rng(17)
+    M, H, KVH, D, K, theta = 1, 4, 2, 64, 256, 1e4
+    x = rng.normal(0, 1, (M, K)).astype(np.float16)
+    dx = capi.DevBuf.from_array(x)
+    shapes = [H * D, KVH * D, KVH * D]
+    ws = []
+    for N in shapes:
+        q, s = q8_weight(rng, N, K)
+        ws.append((q, s, capi.DevBuf.from_array(rng.normal(0, 0.1, N).astype(np.float32)), N))
+    cap = 300
+    cache = rng.normal(0, 1, (cap, KVH * D)).astype(np.float16)
+    ref_b = [capi.DevBuf(M * N * 2) for N in shapes]
+    ref_kc, ref_vc = capi.DevBuf.from_array(cache), capi.DevBuf.from_array(cache)
+    hr = _qkv_plan(ref_b, dx, ws, M, K, F16)
+    bufs = [capi.DevBuf(M * N * 2) for N in shapes]
+    kc, vc = capi.DevBuf.from_array(cache), capi.DevBuf.from_array(cache)
+    h = _qkv_plan(bufs, dx, ws, M, K, F16)
+    try:
+        capi.call("vvh_plan_set_rope", h, 0, 1, 2, D, theta, kc.ptr, vc.ptr)
+        capi.call("vvh_plan_set_rope_table", h, 64)
+        # steps: (what to set before the run, position)
+        for setup, pos in ((None, 10), ("rope", 10), ("rope", 0), ("table", 200), (None, 299), (None, 63)):
+            if setup == "rope":
+                capi.call("vvh_plan_set_rope", h, 0, 1, 2, D, theta, kc.ptr, vc.ptr)
+            elif setup == "table":
+                capi.call("vvh_plan_set_rope_table", h, 256)
+            capi.call("vvh_plan_run", hr, None)
+            capi.call("vvh_rope_append", ref_b[0].ptr, ref_b[1].ptr, ref_b[2].ptr, ref_kc.ptr, ref_vc.ptr, M, H, KVH,
+                      D, pos, theta, F16, None)
+            capi.call("vvh_plan_run_pos", h, pos, None)
+            capi.sync()
+            for name, a, b in zip(("q", "k", "v"), ref_b, bufs):
+                assert np.array_equal(a.to_array(np.uint16, (a.nbytes // 2,)), b.to_array(np.uint16, (b.nbytes // 2,))), \
+                    (setup, pos, name)
+            for name, a, b in (("k_cache", ref_kc, kc), ("v_cache", ref_vc, vc)):
+                assert np.array_equal(a.to_array(np.uint16, cache.shape), b.to_array(np.uint16, cache.shape)), \
+                    (setup, pos, name)
+    finally:
+        capi.call("vvh_plan_destroy", h)
+        capi.call("vvh_plan_destroy", hr)
+
+
 def test_plan_rope_limits(gpu):
     """The RoPE epilogue is refused where it cannot apply."""
     rng = np.random.default_rng(3)

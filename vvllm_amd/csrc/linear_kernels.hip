@@ -1082,10 +1082,9 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
 // host for the launch: for a grouped launch it must hold for every problem).
 // The fields that the first loads of a block depend on come first, as scalar
 // arguments, which arrive preloaded into registers at dispatch (14 dwords
-// here; the struct is read from the kernel-argument segment when used, and
-// its first read costs a block about 0.3 us before the loads that need it
-// can issue).  mk = M | ksplit << 8; xi = xparts | xhd << 8 for the
-// attention merge stage (its part loads need both), else 0.
+// here; the struct is read from the kernel-argument segment when used).
+// mk = M | ksplit << 8; xi = xparts | xhd << 8 for the attention merge stage
+// (its part loads need both), else 0.
 // A plain call has no RoPE or SiLU-gated epilogue.
 template <typename OT, int MT, bool XLDS, bool EARLY, int DEPTH, int FS>
 __global__ __launch_bounds__(256) void k_dot(const int8_t* w, const void* inp, const float* scales,
