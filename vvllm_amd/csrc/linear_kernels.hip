@@ -715,6 +715,10 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
     // TB/s on the grouped decode set).
     float e_sc[2] = {0.0f, 0.0f}, e_bi[2] = {0.0f, 0.0f};
     OT e_res[MT][2];
+    // MF, plain epilogue: the operands of the lane's outputs in the MFMA
+    // tile's own layout, activation row fi and columns n0 + 4 fg + q
+    float f_sc[4], f_bi[4];
+    OT f_res[4];
     // RoPE cosine and sine of the lane's pair for each activation row (q and
     // k rows).  Early launches work them out right after requesting the
     // weights, while the loads are in flight: they take a long chain of fp64
@@ -751,13 +755,26 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
     auto epi_load = [&]() {
         const float* bp = a.bias ? a.bias : a.scales;
         const OT* rp = a.res ? static_cast<const OT*>(a.res) : reinterpret_cast<const OT*>(a.scales);
-        const int64_t rows[2] = {rowA, rowB};
+        if constexpr (MF) {
+            // clamped into the problem: columns past N and rows past M are
+            // read again and not stored
+            const int64_t mo = a.res ? (int64_t)(fi < a.M ? fi : 0) * a.N : 0;
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            e_sc[h] = *gbl(a.scales + rows[h]);
-            e_bi[h] = *gbl(bp + rows[h]);
+            for (int q = 0; q < 4; q++) {
+                const int64_t n = n0 + 4 * fg + q < a.N ? n0 + 4 * fg + q : a.N - 1;
+                f_sc[q] = *gbl(a.scales + n);
+                f_bi[q] = *gbl(bp + n);
+                f_res[q] = *gbl(rp + mo + n);
+            }
+        } else {
+            const int64_t rows[2] = {rowA, rowB};
 #pragma unroll
-            for (int m = 0; m < MT; m++) e_res[m][h] = *gbl(rp + (a.res && m < a.M ? m * a.N : 0) + rows[h]);
+            for (int h = 0; h < 2; h++) {
+                e_sc[h] = *gbl(a.scales + rows[h]);
+                e_bi[h] = *gbl(bp + rows[h]);
+#pragma unroll
+                for (int m = 0; m < MT; m++) e_res[m][h] = *gbl(rp + (a.res && m < a.M ? m * a.N : 0) + rows[h]);
+            }
         }
     };
     if constexpr (EARLY) {
@@ -987,14 +1004,39 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
     }
     if constexpr (MF) {
         // the MFMA tile (rows 4 fg + q of column fi) into the reduction
-        // scratch, then every lane takes its rows r and 8 + r back, the
-        // ksplit waves of its tile added in wave order
+        // scratch, the ksplit waves of its tile added in wave order
         if (fi < MT) {
 #pragma unroll
             for (int q = 0; q < 4; q++) red.v[c.wave][fi][4 * fg + q] = facc[q];
         }
         __syncthreads();
         const int w0 = c.ks == 0 ? c.wave : c.wave - c.ks;
+        if (!a.glu && a.rope == 0) {
+            // plain epilogue in the MFMA layout: lane (fi, fg) of the tile's
+            // first wave stores activation row fi, columns n0 + 4 fg + q (the
+            // same sums in the same order as the row layout below; 4 stores
+            // per lane instead of 2 M per lane of one lane in eight)
+            if (c.ks == 0 && fi < a.M && n0 < a.N) {
+                if constexpr (!EARLY) epi_load();
+                float s4[4];
+#pragma unroll
+                for (int q = 0; q < 4; q++) s4[q] = red.v[w0][fi][4 * fg + q];
+                for (int j = 1; j < c.ksplit; j++) {
+#pragma unroll
+                    for (int q = 0; q < 4; q++) s4[q] += red.v[w0 + j][fi][4 * fg + q];
+                }
+                OT* out = static_cast<OT*>(a.out) + fi * a.N;
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const int64_t n = n0 + 4 * fg + q;
+                    if (n < a.N)
+                        *gbl(out + n) = (OT)dot_epi(s4[q], f_sc[q], a.bias != nullptr, f_bi[q], a.res != nullptr,
+                                                    (float)f_res[q]);
+                }
+            }
+            return;
+        }
+        // SiLU-gated and RoPE epilogues: every lane takes its rows r and 8 + r
 #pragma unroll
         for (int m = 0; m < MT; m++) {
             accA[m] = red.v[w0][m][r];
@@ -1035,8 +1077,11 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
             }
         }
     }
+    // (with MF these load their operands here: the early loads took the
+    // plain epilogue's layout)
     if (a.glu) {
-        if (c.ks == 0 && ch == 0 && n0 < a.N) dot_store_glu<OT, MT, EARLY>(a, rowA, rowB, accA, accB, e_sc, e_bi);
+        if (c.ks == 0 && ch == 0 && n0 < a.N)
+            dot_store_glu<OT, MT, EARLY && !MF>(a, rowA, rowB, accA, accB, e_sc, e_bi);
         return;
     }
     if (a.rope != 0) {
@@ -1052,10 +1097,11 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
                     rs[m] = rt[m][1];
                 }
             }
-            dot_store_rope<OT, MT, EARLY>(a, pos, rowA, rowB, accA, accB, e_sc, e_bi, e_res, rc, rs);
+            dot_store_rope<OT, MT, EARLY && !MF>(a, pos, rowA, rowB, accA, accB, e_sc, e_bi, e_res, rc, rs);
         }
         return;
     }
+    if constexpr (MF) return;  // (the plain epilogue took the MFMA layout above)
     if (c.ks == 0 && ch == 0 && n0 < a.N) {
 #pragma unroll
         for (int m = 0; m < MT; m++) {
