@@ -179,13 +179,13 @@ def test_dispatch_choice():
         assert ch(12, 896, 4864, capi.F16, capi.F16) == "dot"
         assert ch(16, 896, 4864, capi.F16, capi.F16) == "dot"         # M * K <= 16 * 4864
         assert ch(13, 1536, 8960, capi.F16, capi.F16) == "gemm"       # long rows, few tiles: split-K GEMM
-        assert ch(9, 8960, 1536, capi.F16, capi.F16) == "skinny"      # M > 8 below 1024 tiles
+        assert ch(9, 8960, 1536, capi.F16, capi.F16) == "dot"         # M > 8 below 1024 tiles, short rows
         assert ch(16, 17920, 1536, capi.F16, capi.F16) == "gemm"      # M > 8 on 1120 tiles
         assert ch(16, 4096, 8192, capi.F16, capi.F16) == "gemm"       # M > 8, long rows on 256 tiles
         assert ch(5, 151936, 896, capi.F16, capi.F32) == "skinny"     # streaming only when forced
-        assert ch(16, 4864, 896, capi.F16, capi.F16) == "skinny"      # M > 8 on 304 tiles
+        assert ch(16, 4864, 896, capi.F16, capi.F16) == "dot"         # M > 8 on 304 tiles
         assert ch(16, 1536, 8960, capi.F16, capi.F16) == "gemm"       # M > 12 on long rows
-        assert ch(16, 1536, 1536, capi.F16, capi.F16) == "skinny"     # M > 8, few tiles, short rows
+        assert ch(16, 1536, 1536, capi.F16, capi.F16) == "dot"        # M > 8, few tiles, short rows
         assert ch(17, 4864, 896, capi.F16, capi.F16) == "gemm"        # M > 16 on 304 tiles
         assert ch(17, 1152, 896, capi.F16, capi.F16) == "skinny"      # M > 16: 2-4 groups of 16 rows
         assert ch(64, 896, 896, capi.F16, capi.F16) == "skinny"       #   on few tiles, M * K <= 64 * 896

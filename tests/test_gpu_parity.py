@@ -235,7 +235,7 @@ def test_decode_dispatch_on_device(gpu):
     assert capi.kernel_choice(9, 1536, 8960, F16, F16) == "dot"
     assert capi.kernel_choice(13, 1536, 8960, F16, F16) == "gemm"
     assert capi.kernel_choice(5, 151936, 896, F16, F16) == "skinny"
-    assert capi.kernel_choice(16, 4864, 896, F16, F16) == "skinny"
+    assert capi.kernel_choice(16, 4864, 896, F16, F16) == "dot"
     assert capi.kernel_choice(16, 17920, 1536, F16, F16) == "gemm"
     assert capi.kernel_choice(64, 1152, 896, F16, F16) == "skinny"
     assert capi.kernel_choice(64, 1536, 1536, F16, F16) == "gemm"
@@ -243,6 +243,7 @@ def test_decode_dispatch_on_device(gpu):
 
 @pytest.mark.parametrize("M,N,K,family", [(8, 17920, 1536, "gemm"), (6, 17920, 1536, "gemm"), (5, 17920, 1536, "skinny"),
                                           (16, 896, 4864, "dot"), (13, 896, 4864, "dot"), (13, 1536, 8960, "gemm"),
+                                          (9, 8960, 1536, "dot"), (16, 1536, 1536, "dot"), (16, 9728, 896, "dot"),
                                           (64, 1152, 896, "skinny"), (33, 1536, 1536, "skinny")])
 def test_dispatch_edges_parity(gpu, oracle, M, N, K, family):
     """The automatic choice at the edges of the small-M dispatch rules, each
@@ -458,8 +459,10 @@ def test_dot_plan_up_to_eight_rows(gpu, oracle, outd):
 def test_dot_plan_up_to_sixteen_rows(gpu, oracle, outd):
     """k_dot_grouped forced on problems of up to 16 activation rows (16-row
     MFMA operands), one of them with activations read through the caches
-    (K = 20480 does not fit the block's LDS at M = 16)."""
+    (K = 20480 does not fit the block's LDS at M = 16); without that one,
+    the automatic dispatch takes k_dot for every problem too."""
     assert _plan_case(oracle, DOT_PLAN_M16, outd, capi.KERNEL_DOT, seed=570, expect="dot") == 1
+    assert _plan_case(oracle, DOT_PLAN_M16[:5], outd, capi.KERNEL_AUTO, seed=571, expect="dot") == 1
 
 
 def test_dot_plan_without_lds_activations(gpu, oracle):

@@ -442,13 +442,27 @@ constexpr std::size_t kGemmF32MinM = 16;
 //   151936 x 896 (9496 tiles), M = 4 6 8 12 16: skinny 34.8 36.0 37.1 57.9 63.4, gemm 52.6 52.7 52.3 53.3 54.5
 //   0.5B down 896 x 4864, M = 12 13 14 16: dot 9.42 9.77 10.17 10.77, skinny 10.6-11.0, gemm 11.4-11.5
 //   1.5B down 1536 x 8960, M = 12 13 14 16: dot 13.21 13.72 14.44 15.30, gemm 13.31 13.35 13.35 13.42
+// Then k_dot's MFMA path stored its plain epilogue in the MFMA layout (4
+// outputs per lane of the tile's first wave instead of 2 M from one lane in
+// eight), same graph replay, M = 3 / 8 / 9 / 12 / 16:
+//   q 896 x 896                  dot 3.16 3.27 3.32 3.46 3.62, skinny 4.79 5.31 5.40 4.58 4.65
+//   o 896 x 896                  dot 3.43 3.59 3.60 3.80 4.01, skinny 5.72 6.55 6.63 5.87 5.98
+//   gate 4864 x 896              dot 3.98 4.17 4.24 4.47 4.78, skinny 5.61 6.23 6.32 5.85 6.09
+//   gate_up 9728 x 896 (608)     dot 4.86 5.17 5.32 5.66 6.20, skinny 6.53 7.51 7.36 7.24 7.66, gemm 8.1-9.3
+//   down 896 x 4864              dot 6.13 6.62 6.89 7.55 8.54, skinny 10.9-12.4, gemm 10.4-10.9
+//   1.5B q/o 1536 x 1536         dot 3.82 4.08 4.15 4.35 4.65, skinny 5.66 5.28 5.30 5.43 5.55
+//   1.5B k/v 256 x 1536          dot 3.66 3.94 4.01 4.24 4.49, skinny 5.50 5.15 5.16 5.32 5.40
+//   1.5B gate 8960 x 1536 (560)  dot 6.68 7.56 7.83 8.48 9.43, skinny 8.36 9.07 9.15 9.96 10.70, gemm 10.4-10.9
+//   1.5B down 1536 x 8960 (96)   dot 8.77 9.67 10.13 11.29 13.10, gemm 11.6-11.9, 12.23 at 16
+//   1.5B gate_up 17920 x 1536 (1120)  dot 11.77 13.19 13.65 14.81 16.52, skinny 11.91 15.0 15.0 16.4 18.1,
+//                                     gemm 12.5-12.8
 // So: k_dot at M <= 2, and at M <= 8 below 1024 tiles; at M = 6..8 on more
 // tiles the GEMM when its 64 x 128 tiles fit one round over the CUs (not
 // the LM head: 1187 of them); from M = 9, rows of at least kLongK codes on
 // few tiles take k_dot up to M = 12 or M * K = 16 * 4864 and the split-K
 // GEMM above, 1024 and more tiles (or rows of kGemmLongRows codes) the
-// GEMM, the rest k_skinny; k_skinny also for M <= 8 on 1024 and more tiles
-// otherwise.  k_stream lost to k_skinny by 1.7-3.5x at every M and shape of the
+// GEMM, the rest (short rows below 1024 tiles) k_dot's 16-row path;
+// k_skinny for M <= 8 on 1024 and more tiles otherwise.  k_stream lost to k_skinny by 1.7-3.5x at every M and shape of the
 // sweep (e.g. 151936 x 896: 58-78 us), so it runs only when forced.
 constexpr std::size_t kDotAutoMaxM = 2;
 constexpr std::size_t kDotAutoMfMaxM = 8;    // k_dot's MFMA path below kDotMfTiles tiles
@@ -498,6 +512,8 @@ int natural_kernel(std::size_t M, std::size_t N, std::size_t K, int act)
             if (gemm_ok) return K_GEMM;
         } else if (gemm_ok && (tiles >= kDotMfTiles || (int64_t)K >= kGemmLongRows)) {
             return K_GEMM;
+        } else if (tiles < kDotMfTiles && dot_ok) {
+            return K_DOT;
         }
     }
     return K_SKINNY;
