@@ -140,15 +140,17 @@ def test_gemm_variant_choice():
     128 x 192 when that saves a round, split-K (on 64 x 128 tiles) for few
     tiles over a long K, k_gemm for K % 64 != 0."""
     assert capi.gemm_variant(512, 4864, 896) == "k_gemm3 128x128"     # 304 64-row tiles; 152, one round
-    assert capi.gemm_variant(128, 4864, 896) == "k_gemm3 64x128"      # 76 64-row tiles
-    assert capi.gemm_variant(512, 1152, 896) == "k_gemm3 64x128"      # 72
+    assert capi.gemm_variant(128, 4864, 896) == "k_gemm3 64x64"       # 152 64 x 64 tiles, one round
+    assert capi.gemm_variant(512, 1152, 896) == "k_gemm3 64x64"       # 144
+    assert capi.gemm_variant(256, 4864, 512) == "k_gemm3 64x128"      # 304 64 x 64 tiles, 152 64 x 128
     assert capi.gemm_variant(256, 8960, 1536) == "k_gemm3 128x128"    # 280 64-row tiles > 256 CUs
     assert capi.gemm_variant(2048, 4864, 896) == "k_gemm3 128x192"    # 3 rounds -> 2
     assert capi.gemm_variant(512, 896, 4864) == "k_gemm3 64x128 split 4"    # 56 64-row tiles, 76 k stages
     assert capi.gemm_variant(2048, 896, 4864) == "k_gemm3 64x128"   # 224 64-row tiles beat 2 splits
-    assert capi.gemm_variant(64, 1536, 1536) == "k_gemm3 64x128 split 6"    # 12 tiles, 24 k stages
-    assert capi.gemm_variant(128, 896, 4864) == "k_gemm3 64x128 split 7"    # 14 tiles, 76 k stages
-    assert capi.gemm_variant(256, 1536, 1536) == "k_gemm3 64x128"   # 48 64-row tiles beat 3 splits
+    assert capi.gemm_variant(64, 1536, 1536) == "k_gemm3 64x64 split 4"     # 24 tiles, 24 k stages
+    assert capi.gemm_variant(128, 896, 4864) == "k_gemm3 64x64 split 7"     # 28 tiles, 76 k stages
+    assert capi.gemm_variant(256, 1536, 8960) == "k_gemm3 64x128 split 5"   # 64 x 64 would halve the count
+    assert capi.gemm_variant(256, 1536, 1536) == "k_gemm3 64x64"    # 96 64 x 64 tiles beat splits
     assert capi.gemm_variant(300, 1000, 80) == "k_gemm"               # K % 64 != 0
     assert capi.load().vvh_gemm_variant(0, 16, 64, None, None) == -1  # -VVH_ERR_INVALID_ARG
 

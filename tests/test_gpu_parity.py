@@ -183,14 +183,15 @@ def test_gemm_kernel(gpu, oracle, M, N, K, outd):
 
 @pytest.mark.parametrize("res", ["sep", "inplace"])
 @pytest.mark.parametrize("outd", [F16, F32])
-@pytest.mark.parametrize("M,N,K,variant", [(256, 768, 512, "k_gemm3 64x128"), (2048, 2304, 128, "k_gemm3 128x192"),
-                                           (300, 776, 256, "k_gemm3 64x128"), (1024, 2176, 256, "k_gemm3 128x128"),
+@pytest.mark.parametrize("M,N,K,variant", [(256, 768, 512, "k_gemm3 64x64"), (256, 4864, 512, "k_gemm3 64x128"),
+                                           (2048, 2304, 128, "k_gemm3 128x192"), (300, 776, 256, "k_gemm3 64x64"),
+                                           (300, 3500, 256, "k_gemm3 64x128"), (1024, 2176, 256, "k_gemm3 128x128"),
                                            (1000, 2200, 256, "k_gemm3 128x128")])
 def test_gemm3_epilogue(gpu, oracle, M, N, K, variant, outd, res):
     """k_gemm3's epilogue with bias and residual together, on every tile
     shape the dispatch picks: tiles wholly inside the problem take the
-    branch-free path, the others (M = 300, N = 776 and M = 1000, N = 2200:
-    partial rows and columns) the general one."""
+    branch-free path, the others (M = 300 with N = 776 or 3500, M = 1000
+    with N = 2200: partial rows and columns) the general one."""
     assert capi.gemm_variant(M, N, K) == variant
     rows = None if M <= 300 else [r for r in (0, 1, 63, 64, 127, 128, 1000, 1919, 1920) if r < M] + [M - 1]
     run_case(oracle, M, N, K, F16, outd, bias=True, res=res, kernel=capi.KERNEL_GEMM, seed=M + K, rows=rows)

@@ -515,9 +515,11 @@ __global__ __launch_bounds__(64 * (BM / 32 / TI) * WN, BM == 64 ? 2 : 1) void k_
 // fragment feeds 4 row tiles, 2.5 conversion VALU per MFMA; measured against
 // 4 waves of 64 x 64 in the same runs: M=512 gate/up 11.13 -> 10.78 us,
 // M=2048 33.7 -> 33.3 us, split-K down M=2048 32.7 -> 32.0 us), 4 = 64 x 128
-// (4 waves of 64 x 32, two blocks per CU).
-int gemm3_tile_n(int layout) { return layout == 1 ? 192 : 128; }
-int gemm3_tile_m(int layout) { return layout == 4 ? 64 : 128; }
+// (4 waves of 64 x 32, two blocks per CU), 5 = 64 x 64 (2 waves of 64 x 32:
+// a block fills 12 KB of LDS per stage instead of 16, for calls whose 64 x 64
+// tiles, or split tiles, fit one round over the CUs).
+int gemm3_tile_n(int layout) { return layout == 1 ? 192 : layout == 5 ? 64 : 128; }
+int gemm3_tile_m(int layout) { return (layout == 4 || layout == 5) ? 64 : 128; }
 
 template <int WN, int TJ, int TI, int BM>
 static void gemm3_go(const LinArgs& a, bool f32, hipStream_t s)
@@ -536,6 +538,7 @@ int launch_gemm3(const LinArgs& a, int out, int layout, void* stream)
     const bool f32 = out == VVH_F32;
     if (layout == 3) gemm3_go<4, 1, 4, 128>(a, f32, s);
     else if (layout == 4) gemm3_go<4, 1, 2, 64>(a, f32, s);
+    else if (layout == 5) gemm3_go<2, 1, 2, 64>(a, f32, s);
     else gemm3_go<2, 3, 2, 128>(a, f32, s);
     return (int)hipGetLastError();
 }

@@ -243,8 +243,7 @@ int workspace_get(const WsSource* src, void* stream, std::size_t bytes, float** 
 // split GEMM pays a second launch and, per split, one M x N fp32 partial
 // plane written by the GEMM and read back by the reduction, so it only pays
 // for long reductions over few tiles: split when the 64 x 128 tiles would
-// leave half of the CUs idle and K has at least 8 stages.  Split and
-// unsplit calls at that size run on 64 x 128 tiles (gemm3_layout).  The
+// leave half of the CUs idle and K has at least 8 stages.  The
 // count minimises a cost model fitted to sweeps of forced counts (graph
 // replay): 0.25 us per k stage of a split block, 2.5 us for the
 // reduction's launch, each plane at 1.6 TB/s, and 0.3 us per stage for an
@@ -256,27 +255,45 @@ int workspace_get(const WsSource* src, void* stream, std::size_t bytes, float** 
 // (22.0); 1.5B q/o at M = 64: 6 splits 9.73 (10.9), k/v: 12 splits 8.41
 // (9.18).  Splits may be as short as 2 stages (k/v at M = 64: 12 splits
 // against 6 at a floor of 4 stages, 9.18 against 10.12 us on 128 x 128).
-int gemm_splits(int64_t M, int64_t N, int64_t stages)
+// Split tiles of 64 x 64 (layout 5) enter the same model with a stage cost of
+// 0.75 that of 64 x 128 (12 KB of LDS filled per stage instead of 16):
+// measured with the counts it picks, down at M = 128 12.71 -> 11.70 us (7
+// splits), 1.5B down at M = 64 14.40 -> 13.28 (10 splits), 1.5B q/o at M = 64
+// / 128 9.85 / 10.36 -> 9.24 / 9.62, k/v at M = 64 / 256 8.56 / 9.20 -> 8.07 /
+// 8.64; where 64 x 64 would halve the count (down at M = 512: 4 -> 2 splits,
+// 16.83 -> 17.72 us; 1.5B down at M = 256: 19.79 -> 24.91) the model keeps
+// 64 x 128.  *split_layout: the tile layout of a split call (4 or 5).
+int gemm_splits(int64_t M, int64_t N, int64_t stages, int* split_layout)
 {
     const int64_t cus = g_cu_count > 0 ? g_cu_count : 256;
     const int64_t tiles = ((M + 63) / 64) * ((N + 127) / 128);  // 64 x 128 tiles
     const double plane_bytes = (double)M * (double)N * 4.0;
     int64_t s = 1;
+    int lay = 4;
     if (tiles * 2 <= cus && stages >= 8) {
-        const int64_t smax = std::min<int64_t>(cus / tiles, stages / 2);
-        double best = 0;
-        for (int64_t c = 1; c <= smax; c++) {
-            const int64_t kst = (stages + c - 1) / c, ce = (stages + kst - 1) / kst;  // no empty split
-            const int64_t rounds = (tiles * ce + cus - 1) / cus;
-            const double t = ce == 1 ? 0.3 * (double)stages
-                                     : 0.25 * (double)(rounds * kst) + 2.5 + (double)ce * plane_bytes / 1.6e6;
-            if (c == 1 || t < best) {
-                best = t;
-                s = c;
+        // unsplit: 64 x 64 tiles where they fit one round (gemm3_layout), about
+        // 0.85 of the 64 x 128 time
+        const bool one64 = ((M + 63) / 64) * ((N + 63) / 64) <= cus;
+        double best = 0.3 * (double)stages * (one64 ? 0.85 : 1.0);
+        for (const int L : {4, 5}) {
+            const int64_t tl = L == 4 ? tiles : ((M + 63) / 64) * ((N + 63) / 64);
+            const double f = L == 4 ? 1.0 : 0.75;
+            const int64_t smax = std::min<int64_t>(cus / tl, stages / 2);
+            for (int64_t c = 2; c <= smax; c++) {
+                const int64_t kst = (stages + c - 1) / c, ce = (stages + kst - 1) / kst;  // no empty split
+                if (ce == 1) continue;
+                const int64_t rounds = (tl * ce + cus - 1) / cus;
+                const double t = f * 0.25 * (double)(rounds * kst) + 2.5 + (double)ce * plane_bytes / 1.6e6;
+                if (t < best) {
+                    best = t;
+                    s = c;
+                    lay = L;
+                }
             }
         }
     }
     s = std::max<int64_t>(1, std::min<int64_t>(s, stages));
+    if (split_layout) *split_layout = lay;
     return (int)s;
 }
 
@@ -305,8 +322,13 @@ int gemm3_norder(int64_t M, int64_t N, int64_t act_row_halfs, int64_t krange_cod
     return fp_n < fp_m ? 1 : 0;
 }
 
-// k_gemm3 tile shape: split-K problems (few tiles, long K) take 64 x 128.
-// Unsplit ones take 64 x 128 when those tiles give every block a CU of its
+// k_gemm3 tile shape: split-K problems (few tiles, long K) take the layout
+// gemm_splits chose (64 x 128 or 64 x 64).  Unsplit ones take 64 x 64 when
+// those tiles give every block a CU of its own (gate/up N=4864 K=896 at
+// M=128 8.42 -> 7.47 us against 64 x 128; q/k/v N=1152 at M=512 8.19 ->
+// 7.19; 1.5B gate at M=64 12.04 -> 10.47; 1.5B q/o at M=256 11.48 -> 9.74;
+// with two rounds of them, gate/up N=9728 at M=128, 8.64 -> 10.28, so not
+// then), else 64 x 128 when those tiles give every block a CU of its
 // own (then more CUs work than with 128-row tiles, each on half a tile:
 // gate/up N=4864 K=896 at M=128 and 256, 10.5 -> 8.2 us; q/k/v N=1152 at
 // M=512, 10.3 -> 8.0 us; with more 64-row tiles than CUs, two share a CU
@@ -316,10 +338,11 @@ int gemm3_norder(int64_t M, int64_t N, int64_t act_row_halfs, int64_t krange_cod
 // 128 x 128 one on MI355X), else 128 x 128.  (128 x 128 as 8 waves of
 // 64 x 32 measured the same as 4 waves of 128 x 32 at M=512: the loads
 // into LDS, not latency within a SIMD, bound a block.)
-int gemm3_layout(int64_t M, int64_t N, int splits)
+int gemm3_layout(int64_t M, int64_t N, int splits, int split_layout)
 {
-    if (splits > 1) return 4;
+    if (splits > 1) return split_layout;
     const int64_t cus = g_cu_count > 0 ? g_cu_count : 256;
+    if (((M + 63) / 64) * ((N + 63) / 64) <= cus) return 5;
     if (((M + 63) / 64) * ((N + 127) / 128) <= cus) return 4;
     const int64_t nbm = (M + kGemmBM - 1) / kGemmBM;
     const int64_t r128 = (nbm * ((N + 127) / 128) + cus - 1) / cus;
@@ -632,7 +655,8 @@ int run_call(const LinArgs& base, int kernel, int act, int outd, void* stream, c
                     rs_bytes = align_up((uint64_t)a.M * 4);
                 }
                 const int64_t stages = (f32 ? 2 * a.K : a.K) / kGemmBK;
-                int s = gemm_splits(a.M, a.N, stages);
+                int split_layout = 4;
+                int s = gemm_splits(a.M, a.N, stages, &split_layout);
                 uint64_t plane = 0;
                 if (s > 1) {
                     const int64_t kst = (stages + s - 1) / s;
@@ -661,7 +685,7 @@ int run_call(const LinArgs& base, int kernel, int act, int outd, void* stream, c
                     if (a.nsplit > 1) a.ws = reinterpret_cast<float*>(wb + xs_bytes + rs_bytes);
                 }
                 {
-                    const int layout = gemm3_layout(a.M, a.N, a.nsplit);
+                    const int layout = gemm3_layout(a.M, a.N, a.nsplit, split_layout);
                     const int64_t krange = a.nsplit > 1 ? (int64_t)a.kstages * kGemmBK : (a.bk ? a.bk : a.K);
                     const int64_t arow = a.nsplit > 1 ? (int64_t)a.kstages * kGemmBK : a.K;
                     a.norder = gemm3_norder(a.M, a.N, arow, krange, layout, a.nsplit);
@@ -1844,12 +1868,13 @@ VVH_API int vvh_gemm_variant(size_t M, size_t N, size_t K, int* tile_n, int* spl
     int tn = kGemmBN, s = 1, v = 1;
     if (K % kGemmBK == 0) {
         const int64_t stages = (int64_t)K / kGemmBK;
-        s = gemm_splits((int64_t)M, (int64_t)N, stages);
+        int split_layout = 4;
+        s = gemm_splits((int64_t)M, (int64_t)N, stages, &split_layout);
         if (s > 1) {  // as the dispatch: no empty split
             const int64_t kst = (stages + s - 1) / s;
             s = (int)((stages + kst - 1) / kst);
         }
-        const int layout = gemm3_layout((int64_t)M, (int64_t)N, s);
+        const int layout = gemm3_layout((int64_t)M, (int64_t)N, s, split_layout);
         v = gemm3_tile_m(layout) == 64 ? 4 : 3;
         tn = gemm3_tile_n(layout);
     }
