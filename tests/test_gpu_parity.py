@@ -197,6 +197,28 @@ def test_gemm3_epilogue(gpu, oracle, M, N, K, variant, outd, res):
     run_case(oracle, M, N, K, F16, outd, bias=True, res=res, kernel=capi.KERNEL_GEMM, seed=M + K, rows=rows)
 
 
+def reduce_groups(M, N, splits):
+    """Split groups per block of the split-K reduction (k_splitk_reduce8):
+    4 or 2 when one group's blocks would be few (< 128) and carry 8+ or 4+
+    splits each, else 1."""
+    blocks1 = (M * (N // 8) + 255) // 256
+    return 1 if blocks1 >= 128 else 4 if splits >= 8 else 2 if splits >= 4 else 1
+
+
+@pytest.mark.parametrize("res", ["sep", "inplace", None])
+@pytest.mark.parametrize("outd", [F16, F32])
+@pytest.mark.parametrize("M,N,K,splits,groups", [(24, 1544, 8960, 10, 4), (56, 904, 4864, 11, 4), (72, 1032, 3072, 7, 2),
+                                                 (100, 1000, 1536, 4, 2), (200, 1000, 1536, 3, 1)])
+def test_splitk_reduce_groups(gpu, oracle, M, N, K, splits, groups, outd, res):
+    """The split-K reduction with 4, 2 and 1 split groups per block: groups
+    of unequal split counts (10 over 4: 2, 3, 2, 3; 11; 7 over 2: 3, 4) and a
+    last block whose chunk count leaves threads of every group idle."""
+    assert capi.gemm_variant(M, N, K) == f"k_gemm3 64x64 split {splits}"
+    assert reduce_groups(M, N, splits) == groups
+    assert (M * N // 8) % (256 // groups) != 0
+    run_case(oracle, M, N, K, F16, outd, bias=bool(M % 3), res=res, kernel=capi.KERNEL_GEMM, seed=M + N + splits)
+
+
 @pytest.mark.parametrize("outd", [F16, F32])
 @pytest.mark.parametrize("M", [1, 2, 4, 5, 16])
 @pytest.mark.parametrize("N,K", [(1, 512), (17, 592), (130, 896), (896, 4864), (300, 1040), (4099, 768)])

@@ -1590,37 +1590,76 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(LinArgs a)
 }
 
 // The same reduction for N % 8 == 0 with 8 outputs per thread: 16-byte
-// partial loads, four splits (8 loads) in flight, vector scale / bias /
-// residual loads and one 16-byte (fp16) or two 16-byte (fp32) stores.  The
-// splits are summed in split order, as above.
-template <typename OT>
+// partial loads, vector scale / bias / residual loads and one 16-byte (fp16)
+// or two 16-byte (fp32) stores.  The call moves a few MB at most and is
+// bound by latency, or, with many splits over few outputs, by the few CUs
+// its blocks occupy.  So the epilogue operands are requested first, the
+// partials of up to G splits (2 G loads) go out together, and with GR > 1
+// a block's threads form GR groups over the same 256 / GR chunks of 8
+// outputs, group g summing the contiguous splits [S g / GR, S (g + 1) / GR)
+// in order; the group sums are added in group order through LDS.  The
+// result is ((sum of group 0) + sum of group 1) + ..., the same on every
+// run for a given split count.
+template <typename OT, int GR>
 __global__ __launch_bounds__(256) void k_splitk_reduce8(LinArgs a)
 {
-    const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    constexpr int G = 8;
+    constexpr int CPB = 256 / GR;  // chunks per block, a multiple of 64: groups are whole waves
+    __shared__ f4 part[GR > 1 ? GR - 1 : 1][CPB][2];
+    const int t = threadIdx.x;
+    const int g = t / CPB, lc = t % CPB;
+    const int64_t q = (int64_t)blockIdx.x * CPB + lc;
     const int64_t per_row = a.N / 8;
-    if (q >= a.M * per_row) return;
-    const int64_t m = q / per_row, n = (q - m * per_row) * 8;
+    const bool live = q < a.M * per_row;
+    const int64_t m = live ? q / per_row : 0, n = live ? (q - m * per_row) * 8 : 0;
     const int64_t o = m * a.N + n, plane = a.M * a.N;
+    const int32_t s_lo = (int32_t)((int64_t)a.nsplit * g / GR), s_hi = (int32_t)((int64_t)a.nsplit * (g + 1) / GR);
+    f4 s0 = {}, s1 = {}, b0 = {}, b1 = {};
+    u4 r0 = {}, r1 = {};  // residual: 8 fp16 in r0, or 8 fp32 in r0 and r1
+    if (g == 0 && live) {
+        s0 = *reinterpret_cast<const f4*>(a.scales + n);
+        s1 = *reinterpret_cast<const f4*>(a.scales + n + 4);
+        if (a.bias) {
+            b0 = *reinterpret_cast<const f4*>(a.bias + n);
+            b1 = *reinterpret_cast<const f4*>(a.bias + n + 4);
+        }
+        if (a.res) {
+            r0 = *reinterpret_cast<const u4*>(static_cast<const OT*>(a.res) + o);
+            if constexpr (sizeof(OT) == 4) r1 = *reinterpret_cast<const u4*>(static_cast<const OT*>(a.res) + o + 4);
+        }
+    }
     f4 v0 = {}, v1 = {};
-    int32_t s = 0;
-    for (; s + 4 <= a.nsplit; s += 4) {
-        f4 p[8];
+    if (live) {
+        for (int32_t s = s_lo; s < s_hi; s += G) {
+            f4 p[2 * G];
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            p[2 * j] = *reinterpret_cast<const f4*>(a.ws + (s + j) * plane + o);
-            p[2 * j + 1] = *reinterpret_cast<const f4*>(a.ws + (s + j) * plane + o + 4);
-        }
+            for (int j = 0; j < G; j++)
+                if (s + j < s_hi) {  // uniform over the wave
+                    p[2 * j] = *reinterpret_cast<const f4*>(a.ws + (s + j) * plane + o);
+                    p[2 * j + 1] = *reinterpret_cast<const f4*>(a.ws + (s + j) * plane + o + 4);
+                }
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            v0 += p[2 * j];
-            v1 += p[2 * j + 1];
+            for (int j = 0; j < G; j++)
+                if (s + j < s_hi) {
+                    v0 += p[2 * j];
+                    v1 += p[2 * j + 1];
+                }
         }
     }
-    for (; s < a.nsplit; s++) {
-        v0 += *reinterpret_cast<const f4*>(a.ws + s * plane + o);
-        v1 += *reinterpret_cast<const f4*>(a.ws + s * plane + o + 4);
+    if constexpr (GR > 1) {
+        if (g > 0) {
+            part[g - 1][lc][0] = v0;
+            part[g - 1][lc][1] = v1;
+        }
+        __syncthreads();
+        if (g > 0) return;
+#pragma unroll
+        for (int j = 0; j < GR - 1; j++) {
+            v0 += part[j][lc][0];
+            v1 += part[j][lc][1];
+        }
     }
-    const f4 s0 = *reinterpret_cast<const f4*>(a.scales + n), s1 = *reinterpret_cast<const f4*>(a.scales + n + 4);
+    if (!live) return;
     float v[8];
 #pragma unroll
     for (int e = 0; e < 4; e++) {
@@ -1628,7 +1667,6 @@ __global__ __launch_bounds__(256) void k_splitk_reduce8(LinArgs a)
         v[4 + e] = v1[e] * s1[e];
     }
     if (a.bias) {
-        const f4 b0 = *reinterpret_cast<const f4*>(a.bias + n), b1 = *reinterpret_cast<const f4*>(a.bias + n + 4);
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             v[e] += b0[e];
@@ -1637,7 +1675,7 @@ __global__ __launch_bounds__(256) void k_splitk_reduce8(LinArgs a)
     }
     if constexpr (sizeof(OT) == 2) {
         if (a.res) {
-            const h8 r8 = *reinterpret_cast<const h8*>(static_cast<const f16*>(a.res) + o);
+            const h8 r8 = __builtin_bit_cast(h8, r0);
 #pragma unroll
             for (int e = 0; e < 8; e++) v[e] += (float)r8[e];
         }
@@ -1647,17 +1685,37 @@ __global__ __launch_bounds__(256) void k_splitk_reduce8(LinArgs a)
         *reinterpret_cast<h8*>(static_cast<f16*>(a.out) + o) = o8;
     } else {
         if (a.res) {
-            const f4 r0 = *reinterpret_cast<const f4*>(static_cast<const float*>(a.res) + o);
-            const f4 r1 = *reinterpret_cast<const f4*>(static_cast<const float*>(a.res) + o + 4);
+            const f4 x0 = __builtin_bit_cast(f4, r0), x1 = __builtin_bit_cast(f4, r1);
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                v[e] += r0[e];
-                v[4 + e] += r1[e];
+                v[e] += x0[e];
+                v[4 + e] += x1[e];
             }
         }
         *reinterpret_cast<f4*>(static_cast<float*>(a.out) + o) = f4{v[0], v[1], v[2], v[3]};
         *reinterpret_cast<f4*>(static_cast<float*>(a.out) + o + 4) = f4{v[4], v[5], v[6], v[7]};
     }
+}
+
+// Split groups per block of k_splitk_reduce8: more when few blocks of one
+// group would carry many splits each.
+int splitk_reduce_groups(int64_t M, int64_t N, int32_t nsplit)
+{
+    const int64_t blocks1 = (M * (N / 8) + 255) / 256;
+    if (blocks1 >= 128) return 1;
+    if (nsplit >= 8) return 4;
+    return nsplit >= 4 ? 2 : 1;
+}
+
+template <typename OT>
+static void reduce8_go(const LinArgs& a, hipStream_t s)
+{
+    const int gr = splitk_reduce_groups(a.M, a.N, a.nsplit);
+    const int64_t chunks = a.M * (a.N / 8), cpb = 256 / gr;
+    const dim3 grid((unsigned)((chunks + cpb - 1) / cpb));
+    if (gr == 4) hipLaunchKernelGGL((k_splitk_reduce8<OT, 4>), grid, dim3(256), 0, s, a);
+    else if (gr == 2) hipLaunchKernelGGL((k_splitk_reduce8<OT, 2>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((k_splitk_reduce8<OT, 1>), grid, dim3(256), 0, s, a);
 }
 
 int launch_splitk_reduce(const LinArgs& a, int out, void* stream)
@@ -1668,9 +1726,8 @@ int launch_splitk_reduce(const LinArgs& a, int out, void* stream)
                      reinterpret_cast<uintptr_t>(a.scales) % 16 == 0 &&
                      (!a.bias || reinterpret_cast<uintptr_t>(a.bias) % 16 == 0);
     if (vec) {
-        const dim3 grid((unsigned)((a.M * (a.N / 8) + 255) / 256));
-        if (out == VVH_F32) hipLaunchKernelGGL((k_splitk_reduce8<float>), grid, dim3(256), 0, s, a);
-        else hipLaunchKernelGGL((k_splitk_reduce8<f16>), grid, dim3(256), 0, s, a);
+        if (out == VVH_F32) reduce8_go<float>(a, s);
+        else reduce8_go<f16>(a, s);
         return (int)hipGetLastError();
     }
     const int64_t threads = a.M * ((a.N + 3) / 4);
