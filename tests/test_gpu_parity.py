@@ -242,6 +242,26 @@ def test_dot_kernel(gpu, oracle, M, N, K, outd):
              kernel=capi.KERNEL_DOT, seed=13 * N + K + M)
 
 
+def dot_x_reread_bytes(M, N, K):
+    """Activation bytes a k_dot launch's 16-row tiles re-read (each tile
+    reads all M rows); from 5 MB, launches that load the activations with
+    the weights take them in whole lines through the wave's LDS tile, when
+    their waves have at most 12 k steps each (48 at ksplit 4)."""
+    return -(-N // 16) * M * K * 2
+
+
+@pytest.mark.parametrize("outd", [F16, F32])
+@pytest.mark.parametrize("M,N,K", [(16, 4099, 1040), (12, 896, 4864), (5, 8960, 1040), (4, 8960, 1536),
+                                   (3, 8960, 1616), (16, 8960, 1536)])
+def test_dot_activation_tile(gpu, oracle, M, N, K, outd):
+    """k_dot's MFMA path with its activations loaded in whole lines and
+    regathered through LDS (4-, 8- and 16-row instantiations; K tails of
+    16 and 80 codes past a step at K = 1040 and 1616; N % 16 != 0)."""
+    assert dot_x_reread_bytes(M, N, K) >= 5 << 20 and -(-K // 128) <= 48
+    run_case(oracle, M, N, K, F16, outd, bias=bool(M % 2), res=["sep", "inplace", None][(N + M) % 3],
+             kernel=capi.KERNEL_DOT, seed=17 * M + N)
+
+
 def test_decode_dispatch_on_device(gpu):
     assert capi.kernel_choice(1, 151936, 896, F16, F32) == "dot"
     assert capi.kernel_choice(1, 9728, 896, F16, F16) == "dot"
@@ -486,6 +506,19 @@ def test_dot_plan_up_to_sixteen_rows(gpu, oracle, outd):
     the automatic dispatch takes k_dot for every problem too."""
     assert _plan_case(oracle, DOT_PLAN_M16, outd, capi.KERNEL_DOT, seed=570, expect="dot") == 1
     assert _plan_case(oracle, DOT_PLAN_M16[:5], outd, capi.KERNEL_AUTO, seed=571, expect="dot") == 1
+
+
+@pytest.mark.parametrize("outd", [F16, F32])
+def test_dot_plan_activation_tile(gpu, oracle, outd):
+    """A grouped launch on the activation tile: gate and up at M = 16 and a
+    ragged 12-row problem (17.4 + 1.6 MB of activations re-read across the
+    tiles, 2-3 k steps per wave), and the same with 3-8 rows."""
+    specs = [(16, 4864, 896, True, None), (16, 4864, 896, False, "sep"), (12, 300, 1040, False, "inplace")]
+    assert sum(dot_x_reread_bytes(M, N, K) for M, N, K, _, _ in specs) >= 5 << 20
+    assert _plan_case(oracle, specs, outd, capi.KERNEL_DOT, seed=640, expect="dot") == 1
+    specs = [(8, 4864, 896, True, None), (3, 4864, 896, False, "sep"), (5, 4099, 1040, False, "inplace")]
+    assert sum(dot_x_reread_bytes(M, N, K) for M, N, K, _, _ in specs) >= 5 << 20
+    assert _plan_case(oracle, specs, outd, capi.KERNEL_DOT, seed=641, expect="dot") == 1
 
 
 def test_dot_plan_without_lds_activations(gpu, oracle):

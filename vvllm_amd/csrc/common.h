@@ -148,6 +148,35 @@ constexpr int64_t kDotRedBytes = 4 * kDotMaxM * 16 * 4;
 // kDotWtPitch bytes) to gather the MFMA operand fragments
 constexpr int kDotWtPitch = 144;
 constexpr int64_t kDotWtBytes = 4 * 16 * kDotWtPitch;
+// ... and, when its activations are not staged in LDS, loads them in whole
+// 128-byte lines (8 rows per instruction) and passes each step's rows of
+// 128 values through a per-wave LDS tile (rows of kDotXtPitch bytes) too
+constexpr int kDotXtPitch = 272;
+constexpr int64_t kDotXtBytes = 4 * 16 * kDotXtPitch;
+// k_dot's activation source: staged in LDS, loaded with the weights as MFMA
+// operands (or per row for M <= 2), or loaded with the weights in whole lines
+// and regathered through the wave's LDS tile (MFMA path only)
+constexpr int kXDirect = 0, kXLds = 1, kXTile = 2;
+// The tile pays where a launch's tiles re-read many activation bytes (each
+// 16-row tile reads all M rows): from about 5 MB (graph replay, A/B of both
+// sources: 1.5B gate 8960 x 1536 at M = 16 9.6 -> 8.4 us, at M = 4 7.0 ->
+// 6.5; 0.5B down 896 x 4864 at M = 16 8.5 -> 7.9; 0.5B q at M = 4 3.16 ->
+// 3.40 and down at M = 4 6.2 -> 6.5 below the threshold).
+// Waves with long k ranges pay the regathering once per step in series, so
+// it needs at most kDotXTileSteps steps per wave (1.5B down 1536 x 8960 at
+// M = 4, 18 steps per wave: 8.95 -> 9.47 us with it; 0.5B down at M = 16,
+// 10 steps: 8.5 -> 7.9 us).
+constexpr int64_t kDotXTileBytes = 5ll << 20;
+constexpr int64_t kDotXTileSteps = 12;
+inline int64_t dot_x_reread_bytes(int64_t M, int64_t N, int64_t K)
+{
+    return ((N + kDecodeTileN - 1) / kDecodeTileN) * M * K * 2;
+}
+inline int64_t dot_wave_steps(int64_t K, int32_t ksplit)
+{
+    const int64_t steps = (K + kDotStep - 1) / kDotStep;
+    return (steps + ksplit - 1) / (ksplit > 0 ? ksplit : 1);
+}
 // k_dot takes N, M and K as 32-bit kernel arguments and 32-bit k offsets
 inline bool dot_fits(int64_t N, int64_t K)
 {

@@ -529,9 +529,16 @@ __device__ __forceinline__ void dot_store_glu(const LinArgs& a, int64_t rowA, in
     }
 }
 
-template <typename OT, int MT, bool XLDS, bool EARLY, int DEPTH, int FS>
+template <typename OT, int MT, int XS, bool EARLY, int DEPTH, int FS>
 __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* smem, int64_t pos)
 {
+    // where the activations come from (XS, chosen per launch on the host):
+    // kXLds staged once per block in LDS; kXDirect loaded with the weights,
+    // as MFMA operands on the MF path; kXTile (MF only) loaded with the
+    // weights in whole lines and regathered through the wave's LDS tile
+    constexpr bool XLDS = XS == kXLds;
+    constexpr bool XW = XS == kXTile;
+    static_assert(!XW || MT >= 4, "the activation tile serves the MFMA path");
     // activations in the ring take 8 VGPRs per row and slot: halve the ring
     // for several rows so the wave keeps two waves per SIMD's worth of VGPRs,
     // except in early launches, whose few blocks occupancy does not bound
@@ -541,8 +548,14 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
     // MF (3-16 activation rows): the dot products on MFMA (16 rows x 16
     // columns, M of them used, 32 codes per instruction) instead of v_dot2:
     // the step's weights go through the wave's LDS tile into the MFMA
-    // operand layout, the activations are loaded as MFMA operands
+    // operand layout.  The activations (kXDirect) load as MFMA operands,
+    // 16 rows x 64 B per instruction, which take the texture unit twice the
+    // time per byte of whole-line loads; kXTile loads them in whole lines
+    // (8 rows x 128 B, XI per step: rows 0-7, and 8-15 when MT = 16) and
+    // regathers them through LDS as well, for launches whose tiles re-read
+    // many activation bytes (the regathering adds latency to each step)
     constexpr bool MF = MT >= 4;
+    constexpr int XI = XW ? (MT > 8 ? 4 : 2) : 4;
     // First stages (FS, chosen per launch by the host): the stage's operands
     // are requested before the weight ring and the stage runs while the
     // weights are in flight (the in-order wait counter lets a wait for them
@@ -611,6 +624,7 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
     const int fi = c.lane & 15, fg = c.lane >> 4;
     const int32_t fm = fi < a.M ? fi : 0;
     char* wt = smem + kDotRedBytes + (XLDS ? a.M * ldx * 2 : 0) + c.wave * (16 * kDotWtPitch);
+    char* xt = smem + kDotRedBytes + kDotWtBytes + c.wave * (16 * kDotXtPitch);  // XW
 
     // Ring of D slots, one k step each: the two weight chunks of the step
     // and, when the activations are not in LDS, their activation chunks
@@ -618,7 +632,7 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
     // load).  Slot u is consumed, then refilled with the step D ahead.
     struct Slot {
         u4 w[2];
-        h8 x[XLDS ? 1 : (MF ? 4 : MT)][MF ? 1 : 2];  // MF: the step's 4 operand fragments
+        h8 x[XLDS ? 1 : (MF ? XI : MT)][MF ? 1 : 2];  // MF: the step's 4 operand fragments or XI whole-line chunks
     };
     Slot ring[D];
     auto issue = [&](int u, int32_t st) {
@@ -628,7 +642,18 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
         k = k < kmax ? k : kmax;
         ring[u].w[0] = ld_stream_g(wpA + k);
         ring[u].w[1] = ld_stream_g(wpB + k);
-        if (!XLDS && MF) {
+        if (XW) {
+            // chunk i: activation row 8 (i / 2) + r (clamped: rows past M
+            // read row 0, computed and unused), values 64 (i % 2) + 8 ch ..
+            // + 7 of the step (clamped into the row; masked when consumed)
+#pragma unroll
+            for (int i = 0; i < XI; i++) {
+                const int xr = 8 * (i >> 1) + r;
+                int32_t kx = st * kDotStep + 64 * (i & 1) + 8 * ch;
+                kx = kx < (int32_t)a.K - 8 ? kx : (int32_t)a.K - 8;
+                ring[u].x[i][0] = *gbl(reinterpret_cast<const h8*>(xg + (xr < a.M ? xr : 0) * a.K + kx));
+            }
+        } else if (!XLDS && MF) {
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 int32_t kx = st * kDotStep + 32 * j + 8 * fg;
@@ -661,6 +686,13 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
             // writes and the next step's writes follow these reads
             *reinterpret_cast<u4*>(wt + r * kDotWtPitch + 16 * ch) = ring[u].w[0];
             *reinterpret_cast<u4*>(wt + (8 + r) * kDotWtPitch + 16 * ch) = ring[u].w[1];
+            if (XW) {
+                // the step's activation rows, 128 values (256 B) each
+#pragma unroll
+                for (int i = 0; i < XI; i++)
+                    *reinterpret_cast<h8*>(xt + (8 * (i >> 1) + r) * kDotXtPitch + 128 * (i & 1) + 16 * ch) =
+                        ring[u].x[i][0];
+            }
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 // codes 32 j + 8 fg .. + 7 of row fi against the same k of activation row fi
@@ -672,6 +704,10 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
                 if (XLDS) {
                     const int32_t kc = kx < (int32_t)a.K - 8 ? kx : (int32_t)a.K - 8;
                     bf = *reinterpret_cast<const h8*>(xs + fm * ldx + kc);
+                } else if (XW) {
+                    // activation row fi of the tile (rows 0-7 only when MT <= 8)
+                    const int xr = MT > 8 ? fi : (fi & 7);
+                    bf = *reinterpret_cast<const h8*>(xt + xr * kDotXtPitch + 2 * (32 * j + 8 * fg));
                 } else {
                     bf = ring[u].x[j][0];
                 }
@@ -1124,15 +1160,16 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
     }
 }
 
-// XLDS = the activations are staged in LDS (dot_x_in_lds, decided on the
-// host for the launch: for a grouped launch it must hold for every problem).
+// XS = the activations' source (kXLds: staged in LDS, dot_x_in_lds, decided
+// on the host for the launch: for a grouped launch it must hold for every
+// problem; kXDirect, kXTile: loaded with the weights).
 // The fields that the first loads of a block depend on come first, as scalar
 // arguments, which arrive preloaded into registers at dispatch (14 dwords
 // here; the struct is read from the kernel-argument segment when used).
 // mk = M | ksplit << 8; xi = xparts | xhd << 8 for the attention merge stage
 // (its part loads need both), else 0.
 // A plain call has no RoPE or SiLU-gated epilogue.
-template <typename OT, int MT, bool XLDS, bool EARLY, int DEPTH, int FS>
+template <typename OT, int MT, int XS, bool EARLY, int DEPTH, int FS>
 __global__ __launch_bounds__(256) void k_dot(const int8_t* w, const void* inp, const float* scales,
                                              const float* bias, const void* res, int32_t N, int32_t K, int32_t mk,
                                              int32_t xi, const LinArgs a)
@@ -1154,7 +1191,7 @@ __global__ __launch_bounds__(256) void k_dot(const int8_t* w, const void* inp, c
     }
     b.rope = 0;
     b.glu = 0;
-    dot_body<OT, MT, XLDS, EARLY, DEPTH, FS>(b, blockIdx.x, dot_smem, 0);
+    dot_body<OT, MT, XS, EARLY, DEPTH, FS>(b, blockIdx.x, dot_smem, 0);
 }
 
 // Grouped launch.  count <= kDotInline: the problems are g.p[0, count) and
@@ -1171,7 +1208,7 @@ __global__ __launch_bounds__(256) void k_dot(const int8_t* w, const void* inp, c
 // compile in one kind only.  The code of an epilogue a kernel can take but
 // does not run still cost a one-row plan about 0.3 us per launch
 // (graph-replayed, a 9728 x 896 plan: 4.68 against 4.37 us).
-template <typename OT, int MT, bool XLDS, bool EARLY, int DEPTH, int FS, int EP>
+template <typename OT, int MT, int XS, bool EARLY, int DEPTH, int FS, int EP>
 __global__ __launch_bounds__(256) void k_dot_grouped(int32_t b1, int32_t b2, int32_t b3, int32_t count, int64_t pos,
                                                      const LinArgs* __restrict__ table,
                                                      const int32_t* __restrict__ block_prob, const DotGroup g)
@@ -1190,7 +1227,7 @@ __global__ __launch_bounds__(256) void k_dot_grouped(int32_t b1, int32_t b2, int
     } else if constexpr (EP == kEpiRope) {
         a.glu = 0;
     }
-    dot_body<OT, MT, XLDS, EARLY, DEPTH, FS>(a, b - a.block_begin, dot_smem, pos);
+    dot_body<OT, MT, XS, EARLY, DEPTH, FS>(a, b - a.block_begin, dot_smem, pos);
 }
 
 // ---------------------------------------------------------------------------
@@ -1798,7 +1835,7 @@ int launch_skinny_grouped(const LinArgs* dev_table, int count, int64_t total_blo
     return (int)hipGetLastError();
 }
 
-template <int MT, bool XLDS, bool EARLY, int DEPTH, int FS>
+template <int MT, int XS, bool EARLY, int DEPTH, int FS>
 static void dot_launch(const LinArgs& a, int out, dim3 grid, size_t lds, hipStream_t s)
 {
     // dot_fits(N, K) holds (checked by the runtime); M <= kDotMaxM, ksplit
@@ -1808,31 +1845,31 @@ static void dot_launch(const LinArgs& a, int out, dim3 grid, size_t lds, hipStre
     const int32_t mk = (int32_t)a.M | a.ksplit << 8;
     const int32_t xi = FS == kFirstAttn ? (a.xparts | a.xhd << 8) : 0;
     if (out == VVH_F32)
-        hipLaunchKernelGGL((k_dot<float, MT, XLDS, EARLY, DEPTH, FS>), grid, dim3(256), lds, s, a.w, a.inp,
+        hipLaunchKernelGGL((k_dot<float, MT, XS, EARLY, DEPTH, FS>), grid, dim3(256), lds, s, a.w, a.inp,
                            a.scales, a.bias, a.res, N, K, mk, xi, a);
     else
-        hipLaunchKernelGGL((k_dot<f16, MT, XLDS, EARLY, DEPTH, FS>), grid, dim3(256), lds, s, a.w, a.inp,
+        hipLaunchKernelGGL((k_dot<f16, MT, XS, EARLY, DEPTH, FS>), grid, dim3(256), lds, s, a.w, a.inp,
                            a.scales, a.bias, a.res, N, K, mk, xi, a);
 }
 
-template <int MT, bool XLDS, bool EARLY, int FS>
+template <int MT, int XS, bool EARLY, int FS>
 static void dot_launch_d(const LinArgs& a, int out, int depth, dim3 grid, size_t lds, hipStream_t s)
 {
-    if (depth <= 2) dot_launch<MT, XLDS, EARLY, 2, FS>(a, out, grid, lds, s);
-    else if (depth <= 4) dot_launch<MT, XLDS, EARLY, 4, FS>(a, out, grid, lds, s);
-    else dot_launch<MT, XLDS, EARLY, 7, FS>(a, out, grid, lds, s);
+    if (depth <= 2) dot_launch<MT, XS, EARLY, 2, FS>(a, out, grid, lds, s);
+    else if (depth <= 4) dot_launch<MT, XS, EARLY, 4, FS>(a, out, grid, lds, s);
+    else dot_launch<MT, XS, EARLY, 7, FS>(a, out, grid, lds, s);
 }
 
 // first stages exist for early launches with staged activations only
-template <int MT, bool XLDS>
+template <int MT, int XS>
 static void dot_launch_e(const LinArgs& a, int out, bool early, int fs, int depth, dim3 grid, size_t lds,
                          hipStream_t s)
 {
     if (!early) {
-        dot_launch_d<MT, XLDS, false, kFirstNone>(a, out, depth, grid, lds, s);
+        dot_launch_d<MT, XS, false, kFirstNone>(a, out, depth, grid, lds, s);
         return;
     }
-    if constexpr (XLDS && MT <= 4) {
+    if constexpr (XS == kXLds && MT <= 4) {
         if (fs == kFirstRms) return dot_launch_d<MT, true, true, kFirstRms>(a, out, depth, grid, lds, s);
         if (fs == kFirstRms4) return dot_launch_d<MT, true, true, kFirstRms4>(a, out, depth, grid, lds, s);
         if constexpr (MT == 1) {
@@ -1842,7 +1879,7 @@ static void dot_launch_e(const LinArgs& a, int out, bool early, int fs, int dept
             if (fs == kFirstX5) return dot_launch_d<MT, true, true, kFirstX5>(a, out, depth, grid, lds, s);
         }
     }
-    dot_launch_d<MT, XLDS, true, kFirstNone>(a, out, depth, grid, lds, s);
+    dot_launch_d<MT, XS, true, kFirstNone>(a, out, depth, grid, lds, s);
 }
 
 int launch_dot(const LinArgs& a, int out, bool early, int depth, void* stream)
@@ -1859,22 +1896,31 @@ int launch_dot(const LinArgs& a, int out, bool early, int depth, void* stream)
                    : a.xop == 3 ? kFirstAttn
                    : a.xop == 1 ? dot_first_rms(a.M, a.K)
                    : fx;
-    const size_t lds = (xl ? dot_lds_bytes(a.M, a.K) : (size_t)kDotRedBytes) + (a.M > 2 ? kDotWtBytes : 0);
+    // the activation tile: MFMA path (M > 2), early launches loading the
+    // activations with the weights, tiles re-reading many activation bytes
+    const bool xt = a.M > 2 && early && !xl && dot_x_reread_bytes(a.M, a.N, a.K) >= kDotXTileBytes &&
+                    dot_wave_steps(a.K, a.ksplit) <= kDotXTileSteps;
+    const size_t lds = (xl ? dot_lds_bytes(a.M, a.K) : (size_t)kDotRedBytes) + (a.M > 2 ? kDotWtBytes : 0) +
+                       (xt ? kDotXtBytes : 0);
+    hipStream_t st = S(stream);
     if (a.M <= 1) {
-        if (xl) dot_launch_e<1, true>(a, out, early, fs, depth, grid, lds, S(stream));
-        else dot_launch_e<1, false>(a, out, early, fs, depth, grid, lds, S(stream));
+        if (xl) dot_launch_e<1, kXLds>(a, out, early, fs, depth, grid, lds, st);
+        else dot_launch_e<1, kXDirect>(a, out, early, fs, depth, grid, lds, st);
     } else if (a.M <= 2) {
-        if (xl) dot_launch_e<2, true>(a, out, early, fs, depth, grid, lds, S(stream));
-        else dot_launch_e<2, false>(a, out, early, fs, depth, grid, lds, S(stream));
+        if (xl) dot_launch_e<2, kXLds>(a, out, early, fs, depth, grid, lds, st);
+        else dot_launch_e<2, kXDirect>(a, out, early, fs, depth, grid, lds, st);
     } else if (a.M <= 4) {
-        if (xl) dot_launch_e<4, true>(a, out, early, fs, depth, grid, lds, S(stream));
-        else dot_launch_e<4, false>(a, out, early, fs, depth, grid, lds, S(stream));
+        if (xl) dot_launch_e<4, kXLds>(a, out, early, fs, depth, grid, lds, st);
+        else if (xt) dot_launch_d<4, kXTile, true, kFirstNone>(a, out, depth, grid, lds, st);
+        else dot_launch_e<4, kXDirect>(a, out, early, fs, depth, grid, lds, st);
     } else if (a.M <= 8) {
-        if (xl) dot_launch_e<8, true>(a, out, early, fs, depth, grid, lds, S(stream));
-        else dot_launch_e<8, false>(a, out, early, fs, depth, grid, lds, S(stream));
+        if (xl) dot_launch_e<8, kXLds>(a, out, early, fs, depth, grid, lds, st);
+        else if (xt) dot_launch_d<8, kXTile, true, kFirstNone>(a, out, depth, grid, lds, st);
+        else dot_launch_e<8, kXDirect>(a, out, early, fs, depth, grid, lds, st);
     } else {
-        if (xl) dot_launch_e<16, true>(a, out, early, fs, depth, grid, lds, S(stream));
-        else dot_launch_e<16, false>(a, out, early, fs, depth, grid, lds, S(stream));
+        if (xl) dot_launch_e<16, kXLds>(a, out, early, fs, depth, grid, lds, st);
+        else if (xt) dot_launch_d<16, kXTile, true, kFirstNone>(a, out, depth, grid, lds, st);
+        else dot_launch_e<16, kXDirect>(a, out, early, fs, depth, grid, lds, st);
     }
     return (int)hipGetLastError();
 }
@@ -1889,23 +1935,23 @@ struct DotGroupArgs {
     DotGroup g;
 };
 
-template <int MT, bool XLDS, bool EARLY, int DEPTH, int FS, int EP>
+template <int MT, int XS, bool EARLY, int DEPTH, int FS, int EP>
 static void dot_grouped_launch(const DotGroupArgs& k, int out, dim3 grid, size_t lds, hipStream_t s)
 {
     if (out == VVH_F32)
-        hipLaunchKernelGGL((k_dot_grouped<float, MT, XLDS, EARLY, DEPTH, FS, EP>), grid, dim3(256), lds, s, k.b[0],
+        hipLaunchKernelGGL((k_dot_grouped<float, MT, XS, EARLY, DEPTH, FS, EP>), grid, dim3(256), lds, s, k.b[0],
                            k.b[1], k.b[2], k.count, k.pos, k.table, k.block_prob, k.g);
     else
-        hipLaunchKernelGGL((k_dot_grouped<f16, MT, XLDS, EARLY, DEPTH, FS, EP>), grid, dim3(256), lds, s, k.b[0],
+        hipLaunchKernelGGL((k_dot_grouped<f16, MT, XS, EARLY, DEPTH, FS, EP>), grid, dim3(256), lds, s, k.b[0],
                            k.b[1], k.b[2], k.count, k.pos, k.table, k.block_prob, k.g);
 }
 
-template <int MT, bool XLDS, bool EARLY, int FS, int EP = kEpiAny>
+template <int MT, int XS, bool EARLY, int FS, int EP = kEpiAny>
 static void dot_grouped_launch_d(const DotGroupArgs& k, int out, int depth, dim3 grid, size_t lds, hipStream_t s)
 {
-    if (depth <= 2) dot_grouped_launch<MT, XLDS, EARLY, 2, FS, EP>(k, out, grid, lds, s);
-    else if (depth <= 4) dot_grouped_launch<MT, XLDS, EARLY, 4, FS, EP>(k, out, grid, lds, s);
-    else dot_grouped_launch<MT, XLDS, EARLY, 7, FS, EP>(k, out, grid, lds, s);
+    if (depth <= 2) dot_grouped_launch<MT, XS, EARLY, 2, FS, EP>(k, out, grid, lds, s);
+    else if (depth <= 4) dot_grouped_launch<MT, XS, EARLY, 4, FS, EP>(k, out, grid, lds, s);
+    else dot_grouped_launch<MT, XS, EARLY, 7, FS, EP>(k, out, grid, lds, s);
 }
 
 // plans take the RMSNorm first stage only (no attention merge stage); the
@@ -1923,21 +1969,21 @@ static void dot_grouped_launch_rms(const DotGroupArgs& k, int out, int ep, int d
     dot_grouped_launch_d<MT, true, true, FS>(k, out, depth, grid, lds, s);
 }
 
-template <int MT, bool XLDS>
+template <int MT, int XS>
 static void dot_grouped_launch_e(const DotGroupArgs& k, int out, bool early, int fs, int ep, int depth, dim3 grid,
                                  size_t lds, hipStream_t s)
 {
     if (!early) {
-        dot_grouped_launch_d<MT, XLDS, false, kFirstNone>(k, out, depth, grid, lds, s);
+        dot_grouped_launch_d<MT, XS, false, kFirstNone>(k, out, depth, grid, lds, s);
         return;
     }
-    if constexpr (XLDS && MT <= 4) {
+    if constexpr (XS == kXLds && MT <= 4) {
         if (fs == kFirstRms) return dot_grouped_launch_rms<MT, kFirstRms>(k, out, ep, depth, grid, lds, s);
         if (fs == kFirstRms4) return dot_grouped_launch_rms<MT, kFirstRms4>(k, out, ep, depth, grid, lds, s);
     }
-    if constexpr (MT == 1 && !XLDS)
+    if constexpr (MT == 1 && XS == kXDirect)
         if (ep == kEpiPlain) return dot_grouped_launch_d<MT, false, true, kFirstNone, kEpiPlain>(k, out, depth, grid, lds, s);
-    dot_grouped_launch_d<MT, XLDS, true, kFirstNone>(k, out, depth, grid, lds, s);
+    dot_grouped_launch_d<MT, XS, true, kFirstNone>(k, out, depth, grid, lds, s);
 }
 
 int launch_dot_grouped(const LinArgs* dev_table, const int32_t* dev_block_prob, const LinArgs* args, int count,
@@ -1946,7 +1992,16 @@ int launch_dot_grouped(const LinArgs* dev_table, const int32_t* dev_block_prob, 
 {
     const dim3 grid((unsigned)total_blocks);
     hipStream_t s = S(stream);
-    if (max_m > 2) lds_bytes += kDotWtBytes;  // the MFMA path's code tiles
+    // the MFMA path's code tiles, and its activation tiles where the
+    // launch's tiles re-read many activation bytes (as launch_dot)
+    int64_t reread = 0, wsteps = 0;
+    for (int i = 0; i < count; ++i) {
+        reread += dot_x_reread_bytes(args[i].M, args[i].N, args[i].K);
+        wsteps = std::max(wsteps, dot_wave_steps(args[i].K, args[i].ksplit));
+    }
+    const bool xt = max_m > 2 && early && !x_in_lds && reread >= kDotXTileBytes && wsteps <= kDotXTileSteps;
+    if (max_m > 2) lds_bytes += kDotWtBytes;
+    if (xt) lds_bytes += kDotXtBytes;
     DotGroupArgs k{};
     k.count = count;
     k.pos = pos;
@@ -1974,20 +2029,23 @@ int launch_dot_grouped(const LinArgs* dev_table, const int32_t* dev_block_prob, 
     }
     const int ep = all_glu && !any_rope ? kEpiGlu : !any_glu && any_rope ? kEpiRope : !any_glu ? kEpiPlain : kEpiAny;
     if (max_m <= 1) {
-        if (x_in_lds) dot_grouped_launch_e<1, true>(k, out, early, fs, ep, depth, grid, lds_bytes, s);
-        else dot_grouped_launch_e<1, false>(k, out, early, fs, ep, depth, grid, lds_bytes, s);
+        if (x_in_lds) dot_grouped_launch_e<1, kXLds>(k, out, early, fs, ep, depth, grid, lds_bytes, s);
+        else dot_grouped_launch_e<1, kXDirect>(k, out, early, fs, ep, depth, grid, lds_bytes, s);
     } else if (max_m <= 2) {
-        if (x_in_lds) dot_grouped_launch_e<2, true>(k, out, early, fs, ep, depth, grid, lds_bytes, s);
-        else dot_grouped_launch_e<2, false>(k, out, early, fs, ep, depth, grid, lds_bytes, s);
+        if (x_in_lds) dot_grouped_launch_e<2, kXLds>(k, out, early, fs, ep, depth, grid, lds_bytes, s);
+        else dot_grouped_launch_e<2, kXDirect>(k, out, early, fs, ep, depth, grid, lds_bytes, s);
     } else if (max_m <= 4) {
-        if (x_in_lds) dot_grouped_launch_e<4, true>(k, out, early, fs, ep, depth, grid, lds_bytes, s);
-        else dot_grouped_launch_e<4, false>(k, out, early, fs, ep, depth, grid, lds_bytes, s);
+        if (x_in_lds) dot_grouped_launch_e<4, kXLds>(k, out, early, fs, ep, depth, grid, lds_bytes, s);
+        else if (xt) dot_grouped_launch_d<4, kXTile, true, kFirstNone>(k, out, depth, grid, lds_bytes, s);
+        else dot_grouped_launch_e<4, kXDirect>(k, out, early, fs, ep, depth, grid, lds_bytes, s);
     } else if (max_m <= 8) {
-        if (x_in_lds) dot_grouped_launch_e<8, true>(k, out, early, fs, ep, depth, grid, lds_bytes, s);
-        else dot_grouped_launch_e<8, false>(k, out, early, fs, ep, depth, grid, lds_bytes, s);
+        if (x_in_lds) dot_grouped_launch_e<8, kXLds>(k, out, early, fs, ep, depth, grid, lds_bytes, s);
+        else if (xt) dot_grouped_launch_d<8, kXTile, true, kFirstNone>(k, out, depth, grid, lds_bytes, s);
+        else dot_grouped_launch_e<8, kXDirect>(k, out, early, fs, ep, depth, grid, lds_bytes, s);
     } else {
-        if (x_in_lds) dot_grouped_launch_e<16, true>(k, out, early, fs, ep, depth, grid, lds_bytes, s);
-        else dot_grouped_launch_e<16, false>(k, out, early, fs, ep, depth, grid, lds_bytes, s);
+        if (x_in_lds) dot_grouped_launch_e<16, kXLds>(k, out, early, fs, ep, depth, grid, lds_bytes, s);
+        else if (xt) dot_grouped_launch_d<16, kXTile, true, kFirstNone>(k, out, depth, grid, lds_bytes, s);
+        else dot_grouped_launch_e<16, kXDirect>(k, out, early, fs, ep, depth, grid, lds_bytes, s);
     }
     return (int)hipGetLastError();
 }
