@@ -170,23 +170,28 @@ def test_dispatch_choice():
         assert ch(4, 896, 896, capi.F16, capi.F16) == "dot"           # M = 3, 4 on few tiles
         assert ch(4, 1536, 8960, capi.F16, capi.F16) == "dot"
         assert ch(3, 9728, 896, capi.F16, capi.F16) == "dot"          # M = 3, 608 tiles
-        assert ch(3, 17920, 1536, capi.F16, capi.F16) == "skinny"     # M = 3, 1120 tiles
+        assert ch(3, 17920, 1536, capi.F16, capi.F16) == "dot"        # M = 3, 1120 tiles: the activation tile
         assert ch(5, 1536, 8960, capi.F16, capi.F16) == "dot"         # M = 5..8 below 1024 tiles
         assert ch(8, 896, 4864, capi.F16, capi.F16) == "dot"
         assert ch(8, 4864, 896, capi.F16, capi.F16) == "dot"
-        assert ch(5, 17920, 1536, capi.F16, capi.F16) == "skinny"     # M <= 5 on 1120 tiles
-        assert ch(8, 17920, 1536, capi.F16, capi.F16) == "gemm"       # M = 6..8: 140 GEMM tiles, one round
-        assert ch(8, 151936, 896, capi.F16, capi.F16) == "skinny"     # 1187 GEMM tiles
-        assert ch(9, 1536, 8960, capi.F16, capi.F16) == "dot"         # long rows, few tiles, M <= 12
+        assert ch(5, 17920, 1536, capi.F16, capi.F16) == "dot"        # >= 1024 tiles, early launch re-reading
+        assert ch(8, 17920, 1536, capi.F16, capi.F16) == "dot"        #   >= 5 MB of activations, <= 12 k steps
+        assert ch(8, 151936, 896, capi.F16, capi.F16) == "dot"        #   per wave
+        assert ch(16, 151936, 896, capi.F16, capi.F16) == "dot"
+        assert ch(16, 200000, 896, capi.F16, capi.F16) == "gemm"      # not an early launch: no activation tile
+        assert ch(4, 65536, 4096, capi.F16, capi.F16) == "skinny"     # 32 k steps per wave: no activation tile
+        assert ch(9, 1536, 8960, capi.F16, capi.F16) == "dot"         # long rows, few tiles, M <= 10
+        assert ch(10, 1536, 8960, capi.F16, capi.F16) == "dot"
+        assert ch(11, 1536, 8960, capi.F16, capi.F16) == "gemm"
         assert ch(12, 896, 4864, capi.F16, capi.F16) == "dot"
         assert ch(16, 896, 4864, capi.F16, capi.F16) == "dot"         # M * K <= 16 * 4864
         assert ch(13, 1536, 8960, capi.F16, capi.F16) == "gemm"       # long rows, few tiles: split-K GEMM
         assert ch(9, 8960, 1536, capi.F16, capi.F16) == "dot"         # M > 8 below 1024 tiles, short rows
-        assert ch(16, 17920, 1536, capi.F16, capi.F16) == "gemm"      # M > 8 on 1120 tiles
+        assert ch(16, 17920, 1536, capi.F16, capi.F16) == "dot"       # M > 8 on 1120 tiles (activation tile)
         assert ch(16, 4096, 8192, capi.F16, capi.F16) == "gemm"       # M > 8, long rows on 256 tiles
-        assert ch(5, 151936, 896, capi.F16, capi.F32) == "skinny"     # streaming only when forced
+        assert ch(5, 151936, 896, capi.F16, capi.F32) == "dot"        # streaming only when forced
         assert ch(16, 4864, 896, capi.F16, capi.F16) == "dot"         # M > 8 on 304 tiles
-        assert ch(16, 1536, 8960, capi.F16, capi.F16) == "gemm"       # M > 12 on long rows
+        assert ch(16, 1536, 8960, capi.F16, capi.F16) == "gemm"       # M > 10 on long rows
         assert ch(16, 1536, 1536, capi.F16, capi.F16) == "dot"        # M > 8, few tiles, short rows
         assert ch(17, 4864, 896, capi.F16, capi.F16) == "gemm"        # M > 16 on 304 tiles
         assert ch(17, 1152, 896, capi.F16, capi.F16) == "skinny"      # M > 16: 2-4 groups of 16 rows

@@ -269,22 +269,24 @@ def test_decode_dispatch_on_device(gpu):
     assert capi.kernel_choice(4, 896, 896, F16, F16) == "dot"
     assert capi.kernel_choice(4, 1536, 8960, F16, F16) == "dot"
     assert capi.kernel_choice(4, 9728, 896, F16, F16) == "dot"
-    assert capi.kernel_choice(4, 17920, 1536, F16, F16) == "skinny"
+    assert capi.kernel_choice(4, 17920, 1536, F16, F16) == "dot"
     assert capi.kernel_choice(5, 1536, 8960, F16, F16) == "dot"
     assert capi.kernel_choice(8, 896, 4864, F16, F16) == "dot"
-    assert capi.kernel_choice(8, 17920, 1536, F16, F16) == "gemm"
-    assert capi.kernel_choice(8, 151936, 896, F16, F16) == "skinny"
+    assert capi.kernel_choice(8, 17920, 1536, F16, F16) == "dot"
+    assert capi.kernel_choice(8, 151936, 896, F16, F16) == "dot"
     assert capi.kernel_choice(16, 896, 4864, F16, F16) == "dot"
     assert capi.kernel_choice(9, 1536, 8960, F16, F16) == "dot"
     assert capi.kernel_choice(13, 1536, 8960, F16, F16) == "gemm"
-    assert capi.kernel_choice(5, 151936, 896, F16, F16) == "skinny"
+    assert capi.kernel_choice(5, 151936, 896, F16, F16) == "dot"
     assert capi.kernel_choice(16, 4864, 896, F16, F16) == "dot"
-    assert capi.kernel_choice(16, 17920, 1536, F16, F16) == "gemm"
+    assert capi.kernel_choice(16, 17920, 1536, F16, F16) == "dot"
+    assert capi.kernel_choice(11, 1536, 8960, F16, F16) == "gemm"
     assert capi.kernel_choice(64, 1152, 896, F16, F16) == "skinny"
     assert capi.kernel_choice(64, 1536, 1536, F16, F16) == "gemm"
 
 
-@pytest.mark.parametrize("M,N,K,family", [(8, 17920, 1536, "gemm"), (6, 17920, 1536, "gemm"), (5, 17920, 1536, "skinny"),
+@pytest.mark.parametrize("M,N,K,family", [(8, 17920, 1536, "dot"), (16, 17920, 1536, "dot"), (3, 17920, 1536, "dot"),
+                                          (10, 1536, 8960, "dot"), (11, 1536, 8960, "gemm"), (4, 32768, 2048, "skinny"),
                                           (16, 896, 4864, "dot"), (13, 896, 4864, "dot"), (13, 1536, 8960, "gemm"),
                                           (9, 8960, 1536, "dot"), (16, 1536, 1536, "dot"), (16, 9728, 896, "dot"),
                                           (64, 1152, 896, "skinny"), (33, 1536, 1536, "skinny")])
@@ -482,12 +484,16 @@ def test_dot_plan_single_launch(gpu, oracle, outd):
 
 def test_dot_plan_several_rows(gpu, oracle):
     """k_dot_grouped with up to 4 activation rows (automatic dispatch takes
-    k_dot for M <= 8 below 1024 tiles); one problem of M = 3 on 1120 tiles
-    takes k_skinny, and with it the whole plan runs on k_skinny_grouped."""
+    k_dot for M <= 8 below 1024 tiles, and on more tiles where the launch
+    takes the activation tile: M = 3 on 1120 tiles); one problem of M = 4 on
+    2048 tiles with 16 k steps per wave takes k_skinny, and with it the
+    whole plan runs on k_skinny_grouped."""
     assert _plan_case(oracle, DOT_PLAN_M4, F16, capi.KERNEL_DOT, seed=550, expect="dot") == 1
     assert _plan_case(oracle, DOT_PLAN_M4, F16, capi.KERNEL_AUTO, seed=551, expect="dot") == 1
     specs = DOT_PLAN_M4 + [(3, 17920, 1536, False, None)]
-    assert _plan_case(oracle, specs, F16, capi.KERNEL_AUTO, seed=552, expect="skinny") == 1
+    assert _plan_case(oracle, specs, F16, capi.KERNEL_AUTO, seed=552, expect="dot") == 1
+    specs = DOT_PLAN_M4 + [(4, 32768, 2048, False, None)]
+    assert _plan_case(oracle, specs, F16, capi.KERNEL_AUTO, seed=553, expect="skinny") == 1
 
 
 @pytest.mark.parametrize("outd", [F16, F32])

@@ -479,17 +479,30 @@ constexpr std::size_t kGemmF32MinM = 16;
 //   1.5B down 1536 x 8960 (96)   dot 8.77 9.67 10.13 11.29 13.10, gemm 11.6-11.9, 12.23 at 16
 //   1.5B gate_up 17920 x 1536 (1120)  dot 11.77 13.19 13.65 14.81 16.52, skinny 11.91 15.0 15.0 16.4 18.1,
 //                                     gemm 12.5-12.8
-// So: k_dot at M <= 2, and at M <= 8 below 1024 tiles; at M = 6..8 on more
-// tiles the GEMM when its 64 x 128 tiles fit one round over the CUs (not
-// the LM head: 1187 of them); from M = 9, rows of at least kLongK codes on
-// few tiles take k_dot up to M = 12 or M * K = 16 * 4864 and the split-K
-// GEMM above, 1024 and more tiles (or rows of kGemmLongRows codes) the
-// GEMM, the rest (short rows below 1024 tiles) k_dot's 16-row path;
-// k_skinny for M <= 8 on 1024 and more tiles otherwise.  k_stream lost to k_skinny by 1.7-3.5x at every M and shape of the
-// sweep (e.g. 151936 x 896: 58-78 us), so it runs only when forced.
+// Then k_dot's MFMA path took the activation tile (whole-line activation
+// loads regathered through LDS) in early launches re-reading >= 5 MB of
+// activations with <= 12 k steps per wave, and the split-K reduction its
+// split groups; same graph replay, M = 3 / 4 / 5 / 6 / 8 / 9 / 12 / 16:
+//   1.5B gate_up 17920 x 1536 (1120)  dot 9.69 9.81 9.84 10.00 10.30 11.67 12.11 12.76,
+//                                     skinny 11.88-17.86, gemm 12.50-12.83
+//   151936 x 896 (9496 tiles)         dot 28.66 28.55 29.49 28.67 30.09 37.55 38.18 40.02,
+//                                     skinny 34.2 35.2 35.8 36.2 37.4 37.4 57.6 63.0, gemm 53.6-55.9
+//   1.5B down 1536 x 8960 (96)        dot 8.86 8.92 9.00 9.15 9.73 10.13 11.32 13.10,
+//                                     gemm 10.36 10.40 10.43 10.39 10.75 10.37 10.57 11.37
+//   (below 1024 tiles k_dot kept its lead at every M on every other shape)
+// So: k_dot at M <= 2, and at M <= 8 below 1024 tiles; on 1024 and more
+// tiles k_dot at M <= 16 where its launch takes the activation tile
+// (dot_call_takes_x_tile); otherwise at M = 6..8 the GEMM when its 64 x 128
+// tiles fit one round over the CUs; from M = 9, rows of at least kLongK
+// codes on few tiles take k_dot up to M = 10 or M * K = 16 * 4864 and the
+// split-K GEMM above, 1024 and more tiles (or rows of kGemmLongRows codes)
+// the GEMM, the rest (short rows below 1024 tiles) k_dot's 16-row path;
+// k_skinny for M <= 8 on 1024 and more tiles otherwise.  k_stream lost to
+// k_skinny by 1.7-3.5x at every M and shape of the sweep (e.g. 151936 x 896:
+// 58-78 us), so it runs only when forced.
 constexpr std::size_t kDotAutoMaxM = 2;
 constexpr std::size_t kDotAutoMfMaxM = 8;    // k_dot's MFMA path below kDotMfTiles tiles
-constexpr std::size_t kDotLongMaxM = 12;     // M > 8: k_dot on long rows over few tiles up to this M,
+constexpr std::size_t kDotLongMaxM = 10;     // M > 8: k_dot on long rows over few tiles up to this M,
 constexpr int64_t kDotLongMaxMK = 16 * 4864; // or while M * K is at most this
 constexpr std::size_t kGemmWideMinM = 6;     // M = 6..8 on >= kDotMfTiles tiles: the GEMM when its
                                              // 64 x 128 tiles fit one round over the CUs
@@ -511,12 +524,31 @@ constexpr int64_t kGemmLongRows = 4096;      // M > 8: the GEMM on rows of this 
 // so k_skinny at most kLongKMaxTiles tiles with M * K <= kSkinnyMgMaxMK.
 constexpr int64_t kSkinnyMgMaxMK = 64 * 896;
 
+int choose_ksplit(int64_t tiles, int64_t K, int64_t step);
+
+// Whether a plain k_dot call with M > 2 rows takes the activation tile
+// (launch_dot's choice for the call run_call makes, restated here).
+bool dot_call_takes_x_tile(int64_t M, int64_t N, int64_t K)
+{
+    LinArgs a{};
+    a.N = N;
+    a.K = K;
+    a.ksplit = choose_ksplit((N + kDecodeTileN - 1) / kDecodeTileN, K, kDotStep);
+    const bool early = dot_early(dot_blocks(a));  // early: activations loaded with the weights
+    return M > 2 && early && dot_x_reread_bytes(M, N, K) >= kDotXTileBytes &&
+           dot_wave_steps(K, a.ksplit) <= kDotXTileSteps;
+}
+
 int natural_kernel(std::size_t M, std::size_t N, std::size_t K, int act)
 {
     if (act == VVH_F32) return (M >= kGemmF32MinM && K % kGemmBK == 0) ? K_GEMM : K_GEMV_F32;
     const int64_t tiles = ((int64_t)N + kDecodeTileN - 1) / kDecodeTileN;
     const bool dot_ok = dot_fits((int64_t)N, (int64_t)K);
     if ((M <= kDotAutoMaxM || (M <= kDotAutoMfMaxM && tiles < kDotMfTiles)) && dot_ok) return K_DOT;
+    // 3-16 rows on many tiles: k_dot where its launch takes the activation tile
+    if (M <= (std::size_t)kSkinnyMaxM && tiles >= kDotMfTiles && dot_ok &&
+        dot_call_takes_x_tile((int64_t)M, (int64_t)N, (int64_t)K))
+        return K_DOT;
     const int64_t cus = g_cu_count > 0 ? g_cu_count : 256;
     if (M >= kGemmWideMinM && M <= kSkinnyAutoMaxM && K % kGemmBK == 0 && ((int64_t)N + 127) / 128 <= cus)
         return K_GEMM;
