@@ -566,10 +566,10 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
     //     wave_sum_xor), then thread (w, l) normalizes chunk l + 64 w, which
     //     it holds; one barrier in all;
     //   kFirstAttn: the attention merge stage (xop 3, one row, K <= 1024);
-    //   kFirstX1/3/5: one row of plain activations (xop 0) in XR rounds of
-    //     256 chunks: loaded in the ring instead, each wave would request its
-    //     activation chunks with every weight step, as many bytes as the
-    //     weights through the texture unit.
+    //   kFirstX1/3/5: one or two rows of plain activations (xop 0) in XR
+    //     rounds of 256 chunks: loaded in the ring instead, each wave would
+    //     request its activation chunks with every weight step, as many
+    //     bytes per row as the weights through the texture unit.
     // A compile-time choice: chosen at run time, the other path's ring issue
     // comes before the stage's loads, and the compiler then waits for every
     // older load before the stage's first one (a whole round trip).
@@ -577,7 +577,7 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
     constexpr int RJ = FS == kFirstRms ? 2 : FS == kFirstRms4 ? 4 : 0;  // chunks of a row per lane
     constexpr bool rms_first = RJ > 0 && EARLY && XLDS && MT <= 4;
     constexpr bool attn_first = FS == kFirstAttn && EARLY && XLDS && MT == 1;
-    constexpr bool x_first = XR > 0 && EARLY && XLDS && MT == 1;
+    constexpr bool x_first = XR > 0 && EARLY && XLDS && MT <= 2;
     constexpr bool first = rms_first || attn_first || x_first;
     DotRed& red = *reinterpret_cast<DotRed*>(smem);
     f16* xs = reinterpret_cast<f16*>(smem + kDotRedBytes);
@@ -926,15 +926,16 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
             }
             __syncthreads();
         } else if constexpr (x_first) {
-            // chunk i of the row: round i / 256 of thread i % 256; the loads
-            // of the rounds past the row re-read its last chunk, unused
-            const int32_t xchunks = (int32_t)(a.K / 8);
+            // chunk i of the rows (row i / (K / 8)): round i / 256 of thread
+            // i % 256; the loads of the rounds past the rows re-read the last
+            // chunk, unused
+            const int32_t rchunks = (int32_t)(a.K / 8), xchunks = (int32_t)a.M * rchunks;
             h8 xr[XR > 0 ? XR : 1];
 #pragma unroll
             for (int i = 0; i < XR; i++) {
                 int32_t idx = (int32_t)threadIdx.x + 256 * i;
                 idx = idx < xchunks ? idx : xchunks - 1;
-                xr[i] = *gbl(reinterpret_cast<const h8*>(xg + 8 * idx));
+                xr[i] = *gbl(reinterpret_cast<const h8*>(xg + 8 * idx));  // rows are contiguous in the input
             }
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -944,7 +945,8 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
 #pragma unroll
             for (int i = 0; i < XR; i++) {
                 const int32_t idx = (int32_t)threadIdx.x + 256 * i;
-                if (idx < xchunks) *reinterpret_cast<h8*>(xs + 8 * idx) = xr[i];
+                const int32_t m = MT > 1 && idx >= rchunks ? 1 : 0;  // LDS rows of K + 8 halves
+                if (idx < xchunks) *reinterpret_cast<h8*>(xs + m * ldx + 8 * (idx - m * rchunks)) = xr[i];
             }
             __syncthreads();
         }
@@ -1872,8 +1874,9 @@ static void dot_launch_e(const LinArgs& a, int out, bool early, int fs, int dept
     if constexpr (XS == kXLds && MT <= 4) {
         if (fs == kFirstRms) return dot_launch_d<MT, true, true, kFirstRms>(a, out, depth, grid, lds, s);
         if (fs == kFirstRms4) return dot_launch_d<MT, true, true, kFirstRms4>(a, out, depth, grid, lds, s);
-        if constexpr (MT == 1) {
+        if constexpr (MT == 1)
             if (fs == kFirstAttn) return dot_launch_d<MT, true, true, kFirstAttn>(a, out, depth, grid, lds, s);
+        if constexpr (MT <= 2) {
             if (fs == kFirstX1) return dot_launch_d<MT, true, true, kFirstX1>(a, out, depth, grid, lds, s);
             if (fs == kFirstX3) return dot_launch_d<MT, true, true, kFirstX3>(a, out, depth, grid, lds, s);
             if (fs == kFirstX5) return dot_launch_d<MT, true, true, kFirstX5>(a, out, depth, grid, lds, s);
@@ -1885,8 +1888,8 @@ static void dot_launch_e(const LinArgs& a, int out, bool early, int fs, int dept
 int launch_dot(const LinArgs& a, int out, bool early, int depth, void* stream)
 {
     const dim3 grid((unsigned)dot_blocks(a));
-    // early launches without an input stage stage one row of activations
-    // with a first stage (dot_first_x); more rows they load with the
+    // early launches without an input stage stage one or two rows of
+    // activations with a first stage (dot_first_x); more rows they load with the
     // weights (see dot_early).  The attention merge stage exists only as a
     // first stage (any block count).
     if (a.xop == 3) early = true;
