@@ -216,9 +216,12 @@ inline int dot_first_rms(int64_t M, int64_t K)
     if (M > 4 || K % 16 != 0 || !dot_x_in_lds(M, K)) return kFirstNone;
     return K <= 1024 ? kFirstRms : K <= 2048 ? kFirstRms4 : kFirstNone;
 }
-// plain activations of one or two rows staged in LDS, requested ahead of
+// plain activations of one to four rows staged in LDS, requested ahead of
 // the ring in 1, 3 or 5 rounds of 256 chunks of 8 halves (M K <= 2048,
-// 6144, 10240), for launches of at most kDotXFirstMaxBlocks blocks.
+// 6144, 10240), for launches of at most kDotXFirstMaxBlocks blocks (3-4
+// rows: K >= 1024 only; graph replay, 1.5B q/o at M = 3 / 4 3.82 / 3.90 ->
+// 3.67, k/v 3.66 / 3.70 -> 3.48, gate at M = 3 6.77 -> 6.15 us, while the
+// 0.5B q/k/v/o/gate (K = 896, two k steps per wave) lost 0.1-0.2 us).
 // Graph-replayed at M = 1 against the activations in the ring: 1.5B gate
 // 8960 x 1536 (560 blocks) 5.57 -> 5.28 us, q/o 3.05 -> 2.98, down 7.1 ->
 // 6.98, the 0.5B shapes unchanged, the LM head (2374 blocks, each with a
@@ -229,7 +232,7 @@ constexpr int kFirstX5 = 6;
 constexpr int64_t kDotXFirstMaxBlocks = 1024;
 inline int dot_first_x(int64_t M, int64_t K, int64_t blocks)
 {
-    if (M < 1 || M > 2 || blocks > kDotXFirstMaxBlocks) return kFirstNone;
+    if (M < 1 || M > 4 || (M > 2 && K < 1024) || blocks > kDotXFirstMaxBlocks) return kFirstNone;
     const int64_t rounds = (M * K / 8 + 255) / 256;
     return rounds <= 1 ? kFirstX1 : rounds <= 3 ? kFirstX3 : rounds <= 5 ? kFirstX5 : kFirstNone;
 }

@@ -566,7 +566,7 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
     //     wave_sum_xor), then thread (w, l) normalizes chunk l + 64 w, which
     //     it holds; one barrier in all;
     //   kFirstAttn: the attention merge stage (xop 3, one row, K <= 1024);
-    //   kFirstX1/3/5: one or two rows of plain activations (xop 0) in XR
+    //   kFirstX1/3/5: one to four rows of plain activations (xop 0) in XR
     //     rounds of 256 chunks: loaded in the ring instead, each wave would
     //     request its activation chunks with every weight step, as many
     //     bytes per row as the weights through the texture unit.
@@ -577,7 +577,7 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
     constexpr int RJ = FS == kFirstRms ? 2 : FS == kFirstRms4 ? 4 : 0;  // chunks of a row per lane
     constexpr bool rms_first = RJ > 0 && EARLY && XLDS && MT <= 4;
     constexpr bool attn_first = FS == kFirstAttn && EARLY && XLDS && MT == 1;
-    constexpr bool x_first = XR > 0 && EARLY && XLDS && MT <= 2;
+    constexpr bool x_first = XR > 0 && EARLY && XLDS && MT <= 4;
     constexpr bool first = rms_first || attn_first || x_first;
     DotRed& red = *reinterpret_cast<DotRed*>(smem);
     f16* xs = reinterpret_cast<f16*>(smem + kDotRedBytes);
@@ -945,7 +945,9 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
 #pragma unroll
             for (int i = 0; i < XR; i++) {
                 const int32_t idx = (int32_t)threadIdx.x + 256 * i;
-                const int32_t m = MT > 1 && idx >= rchunks ? 1 : 0;  // LDS rows of K + 8 halves
+                int32_t m = 0;  // LDS rows of K + 8 halves
+#pragma unroll
+                for (int q = 1; q < MT; q++) m += idx >= q * rchunks ? 1 : 0;
                 if (idx < xchunks) *reinterpret_cast<h8*>(xs + m * ldx + 8 * (idx - m * rchunks)) = xr[i];
             }
             __syncthreads();
@@ -1876,7 +1878,7 @@ static void dot_launch_e(const LinArgs& a, int out, bool early, int fs, int dept
         if (fs == kFirstRms4) return dot_launch_d<MT, true, true, kFirstRms4>(a, out, depth, grid, lds, s);
         if constexpr (MT == 1)
             if (fs == kFirstAttn) return dot_launch_d<MT, true, true, kFirstAttn>(a, out, depth, grid, lds, s);
-        if constexpr (MT <= 2) {
+        if constexpr (MT <= 4) {
             if (fs == kFirstX1) return dot_launch_d<MT, true, true, kFirstX1>(a, out, depth, grid, lds, s);
             if (fs == kFirstX3) return dot_launch_d<MT, true, true, kFirstX3>(a, out, depth, grid, lds, s);
             if (fs == kFirstX5) return dot_launch_d<MT, true, true, kFirstX5>(a, out, depth, grid, lds, s);
@@ -1888,12 +1890,15 @@ static void dot_launch_e(const LinArgs& a, int out, bool early, int fs, int dept
 int launch_dot(const LinArgs& a, int out, bool early, int depth, void* stream)
 {
     const dim3 grid((unsigned)dot_blocks(a));
-    // early launches without an input stage stage one or two rows of
+    // early launches without an input stage stage one to four rows of
     // activations with a first stage (dot_first_x); more rows they load with the
     // weights (see dot_early).  The attention merge stage exists only as a
     // first stage (any block count).
     if (a.xop == 3) early = true;
-    const int fx = a.xop == 0 ? dot_first_x(a.M, a.K, dot_blocks(a)) : kFirstNone;
+    // (the activation tile, where it applies, takes precedence)
+    const bool tile = a.M > 2 && early && a.xop == 0 && dot_x_reread_bytes(a.M, a.N, a.K) >= kDotXTileBytes &&
+                      dot_wave_steps(a.K, a.ksplit) <= kDotXTileSteps;
+    const int fx = a.xop == 0 && !tile ? dot_first_x(a.M, a.K, dot_blocks(a)) : kFirstNone;
     const bool xl = dot_x_in_lds(a.M, a.K) && (a.xop != 0 || !early || fx != kFirstNone);
     const int fs = !(early && xl) ? kFirstNone
                    : a.xop == 3 ? kFirstAttn
