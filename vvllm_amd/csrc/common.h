@@ -221,7 +221,9 @@ inline int dot_first_rms(int64_t M, int64_t K)
 // 6144, 10240), for launches of at most kDotXFirstMaxBlocks blocks (3-4
 // rows: K >= 1024 only; graph replay, 1.5B q/o at M = 3 / 4 3.82 / 3.90 ->
 // 3.67, k/v 3.66 / 3.70 -> 3.48, gate at M = 3 6.77 -> 6.15 us, while the
-// 0.5B q/k/v/o/gate (K = 896, two k steps per wave) lost 0.1-0.2 us).
+// 0.5B q/k/v/o/gate (K = 896, two k steps per wave) lost 0.1-0.2 us; 5-16
+// rows in up to 12 rounds measured slower: 1.5B q/o at M = 12 / 16 4.35 /
+// 4.65 -> 4.95 / 5.30 us, 0.5B down at M = 5 6.2 -> 7.0).
 // Graph-replayed at M = 1 against the activations in the ring: 1.5B gate
 // 8960 x 1536 (560 blocks) 5.57 -> 5.28 us, q/o 3.05 -> 2.98, down 7.1 ->
 // 6.98, the 0.5B shapes unchanged, the LM head (2374 blocks, each with a

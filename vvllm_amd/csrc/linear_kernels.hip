@@ -579,6 +579,7 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
     constexpr bool attn_first = FS == kFirstAttn && EARLY && XLDS && MT == 1;
     constexpr bool x_first = XR > 0 && EARLY && XLDS && MT <= 4;
     constexpr bool first = rms_first || attn_first || x_first;
+    static_assert(FS == kFirstNone || first, "a first stage this launch cannot run");
     DotRed& red = *reinterpret_cast<DotRed*>(smem);
     f16* xs = reinterpret_cast<f16*>(smem + kDotRedBytes);
     const DecodeCoord c = dot_coord(a, block);
@@ -824,7 +825,7 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
             rope_prep();
         }
     }
-    if constexpr (XLDS && MT <= 4) {
+    if constexpr (first) {
         if constexpr (rms_first) {
             // lane l: chunks l + 64 j of every row (clamped into the row past
             // its end: those add an exact 0), and the norm weights of its own
@@ -1873,12 +1874,14 @@ static void dot_launch_e(const LinArgs& a, int out, bool early, int fs, int dept
         dot_launch_d<MT, XS, false, kFirstNone>(a, out, depth, grid, lds, s);
         return;
     }
-    if constexpr (XS == kXLds && MT <= 4) {
-        if (fs == kFirstRms) return dot_launch_d<MT, true, true, kFirstRms>(a, out, depth, grid, lds, s);
-        if (fs == kFirstRms4) return dot_launch_d<MT, true, true, kFirstRms4>(a, out, depth, grid, lds, s);
+    if constexpr (XS == kXLds) {
+        if constexpr (MT <= 4) {
+            if (fs == kFirstRms) return dot_launch_d<MT, true, true, kFirstRms>(a, out, depth, grid, lds, s);
+            if (fs == kFirstRms4) return dot_launch_d<MT, true, true, kFirstRms4>(a, out, depth, grid, lds, s);
+        }
         if constexpr (MT == 1)
             if (fs == kFirstAttn) return dot_launch_d<MT, true, true, kFirstAttn>(a, out, depth, grid, lds, s);
-        if constexpr (MT <= 4) {
+        if constexpr (MT <= 4) {  // dot_first_x: 1-4 rows
             if (fs == kFirstX1) return dot_launch_d<MT, true, true, kFirstX1>(a, out, depth, grid, lds, s);
             if (fs == kFirstX3) return dot_launch_d<MT, true, true, kFirstX3>(a, out, depth, grid, lds, s);
             if (fs == kFirstX5) return dot_launch_d<MT, true, true, kFirstX5>(a, out, depth, grid, lds, s);
