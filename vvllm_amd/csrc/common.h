@@ -177,6 +177,13 @@ inline int64_t dot_wave_steps(int64_t K, int32_t ksplit)
     const int64_t steps = (K + kDotStep - 1) / kDotStep;
     return (steps + ksplit - 1) / (ksplit > 0 ? ksplit : 1);
 }
+// The activation tile's rule, for a launch of max_m rows whose problems
+// re-read `reread` activation bytes over their tiles and give a wave at most
+// `wave_steps` k steps (launch_dot, launch_dot_grouped and the dispatcher).
+inline bool dot_takes_x_tile(int64_t max_m, bool early, bool x_in_lds, int64_t reread, int64_t wave_steps)
+{
+    return max_m > 2 && early && !x_in_lds && reread >= kDotXTileBytes && wave_steps <= kDotXTileSteps;
+}
 // k_dot takes N, M and K as 32-bit kernel arguments and 32-bit k offsets
 inline bool dot_fits(int64_t N, int64_t K)
 {

@@ -1899,8 +1899,8 @@ int launch_dot(const LinArgs& a, int out, bool early, int depth, void* stream)
     // first stage (any block count).
     if (a.xop == 3) early = true;
     // (the activation tile, where it applies, takes precedence)
-    const bool tile = a.M > 2 && early && a.xop == 0 && dot_x_reread_bytes(a.M, a.N, a.K) >= kDotXTileBytes &&
-                      dot_wave_steps(a.K, a.ksplit) <= kDotXTileSteps;
+    const int64_t reread = dot_x_reread_bytes(a.M, a.N, a.K), wsteps = dot_wave_steps(a.K, a.ksplit);
+    const bool tile = a.xop == 0 && dot_takes_x_tile(a.M, early, false, reread, wsteps);
     const int fx = a.xop == 0 && !tile ? dot_first_x(a.M, a.K, dot_blocks(a)) : kFirstNone;
     const bool xl = dot_x_in_lds(a.M, a.K) && (a.xop != 0 || !early || fx != kFirstNone);
     const int fs = !(early && xl) ? kFirstNone
@@ -1909,8 +1909,7 @@ int launch_dot(const LinArgs& a, int out, bool early, int depth, void* stream)
                    : fx;
     // the activation tile: MFMA path (M > 2), early launches loading the
     // activations with the weights, tiles re-reading many activation bytes
-    const bool xt = a.M > 2 && early && !xl && dot_x_reread_bytes(a.M, a.N, a.K) >= kDotXTileBytes &&
-                    dot_wave_steps(a.K, a.ksplit) <= kDotXTileSteps;
+    const bool xt = dot_takes_x_tile(a.M, early, xl, reread, wsteps);
     const size_t lds = (xl ? dot_lds_bytes(a.M, a.K) : (size_t)kDotRedBytes) + (a.M > 2 ? kDotWtBytes : 0) +
                        (xt ? kDotXtBytes : 0);
     hipStream_t st = S(stream);
@@ -2010,7 +2009,7 @@ int launch_dot_grouped(const LinArgs* dev_table, const int32_t* dev_block_prob, 
         reread += dot_x_reread_bytes(args[i].M, args[i].N, args[i].K);
         wsteps = std::max(wsteps, dot_wave_steps(args[i].K, args[i].ksplit));
     }
-    const bool xt = max_m > 2 && early && !x_in_lds && reread >= kDotXTileBytes && wsteps <= kDotXTileSteps;
+    const bool xt = dot_takes_x_tile(max_m, early, x_in_lds, reread, wsteps);
     if (max_m > 2) lds_bytes += kDotWtBytes;
     if (xt) lds_bytes += kDotXtBytes;
     DotGroupArgs k{};

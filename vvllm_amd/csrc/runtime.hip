@@ -534,9 +534,9 @@ bool dot_call_takes_x_tile(int64_t M, int64_t N, int64_t K)
     a.N = N;
     a.K = K;
     a.ksplit = choose_ksplit((N + kDecodeTileN - 1) / kDecodeTileN, K, kDotStep);
-    const bool early = dot_early(dot_blocks(a));  // early: activations loaded with the weights
-    return M > 2 && early && dot_x_reread_bytes(M, N, K) >= kDotXTileBytes &&
-           dot_wave_steps(K, a.ksplit) <= kDotXTileSteps;
+    // early plain calls load their activations with the weights (not in LDS)
+    return dot_takes_x_tile(M, dot_early(dot_blocks(a)), false, dot_x_reread_bytes(M, N, K),
+                            dot_wave_steps(K, a.ksplit));
 }
 
 int natural_kernel(std::size_t M, std::size_t N, std::size_t K, int act)
