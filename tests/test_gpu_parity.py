@@ -297,6 +297,41 @@ def test_dispatch_edges_parity(gpu, oracle, M, N, K, family):
     run_case(oracle, M, N, K, F16, F16, bias=True, res="sep", kernel=capi.KERNEL_AUTO, seed=17 * M + N)
 
 
+def random_shapes(n=40, seed=20261202):
+    """Seeded shapes over the automatic dispatch: M across every small-M rule
+    (1-17 rows) and into the GEMM, K up to 10240 with some K % 16 != 0 (the
+    generic kernel), N up to 16 M codes per call, fp32 activations and fp32
+    outputs, bias and residual (separate or in place) drawn per case."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        M = int(rng.choice([1, 1, 2, 3, 4, 5, 6, 8, 9, 11, 12, 13, 16, 17, 24, 40, 96]))
+        K = int(rng.integers(1, 641)) * 16
+        if rng.random() < 0.12:
+            K = max(1, K - int(rng.integers(1, 16)))
+        N = int(rng.integers(1, 1 + min(40000, 16_000_000 // K)))
+        act = F32 if rng.random() < 0.15 else F16
+        outd = F32 if rng.random() < 0.4 else F16
+        out.append((M, N, K, act, outd, bool(rng.random() < 0.6), ["sep", "inplace", None][int(rng.integers(3))]))
+    return out
+
+
+@pytest.mark.parametrize("i", range(40))
+def test_auto_dispatch_random_shapes(gpu, oracle, i):
+    """Whatever family the automatic dispatch picks for a seeded random shape
+    (with its split count, ring depth, first stage and activation tile),
+    against the oracle."""
+    M, N, K, act, outd, bias, res = random_shapes()[i]
+    run_case(oracle, M, N, K, act, outd, bias=bias, res=res, kernel=capi.KERNEL_AUTO, seed=1000 + i)
+
+
+def test_random_shapes_cover_the_families():
+    """The seeded draw reaches every family the automatic dispatch picks
+    (the streaming kernel runs only when forced)."""
+    fams = {capi.kernel_choice(M, N, K, act, outd) for M, N, K, act, outd, _, _ in random_shapes()}
+    assert fams == {"dot", "gemm", "skinny", "generic", "gemv_f32"}
+
+
 def test_misaligned_activations_fall_back(gpu, oracle):
     """A 2-byte-offset fp16 activation base cannot take 16-byte loads: the
     dispatcher must route it to the generic kernel and stay correct."""
