@@ -262,6 +262,28 @@ def test_dot_activation_tile(gpu, oracle, M, N, K, outd):
              kernel=capi.KERNEL_DOT, seed=17 * M + N)
 
 
+def dot_split8(M, N, K, cus=256):
+    """Whether a plain k_dot call runs blocks of 8 waves (k split 8): 9-16
+    rows over at most one block per CU whose waves would have exactly 3 k
+    steps each at k split 4 (K of 1025-1536)."""
+    tiles = -(-N // 16)
+    return 8 < M <= 16 and tiles <= cus and -(-(-(-K // 128)) // 4) == 3
+
+
+@pytest.mark.parametrize("outd", [F16, F32])
+@pytest.mark.parametrize("M,N,K", [(16, 1536, 1536), (9, 256, 1536), (12, 300, 1040), (13, 4095, 1152),
+                                   (16, 4096, 1536), (11, 17, 1424)])
+def test_dot_split8(gpu, oracle, M, N, K, outd):
+    """k_dot's 8-wave blocks: one 16-row tile per block, its k steps over 8
+    waves (waves past the k range idle), the 8 partial tiles added in wave
+    order; N % 16 != 0, K tails of 16 and 16 + 64 codes, the activation
+    tile (4096 x 1536 at M = 16 re-reads 12.6 MB of activations)."""
+    assert dot_split8(M, N, K)
+    assert capi.kernel_choice(M, N, K, F16, outd) == "dot"
+    run_case(oracle, M, N, K, F16, outd, bias=bool(N % 2), res=["sep", "inplace", None][(M + N) % 3],
+             kernel=capi.KERNEL_AUTO, seed=19 * M + K)
+
+
 def test_decode_dispatch_on_device(gpu):
     assert capi.kernel_choice(1, 151936, 896, F16, F32) == "dot"
     assert capi.kernel_choice(1, 9728, 896, F16, F16) == "dot"

@@ -177,6 +177,18 @@ inline int64_t dot_wave_steps(int64_t K, int32_t ksplit)
     const int64_t steps = (K + kDotStep - 1) / kDotStep;
     return (steps + ksplit - 1) / (ksplit > 0 ? ksplit : 1);
 }
+// k_dot's k split 8 (blocks of 8 waves, one tile each) for plain calls of
+// 9-16 rows (the MFMA path, activations loaded with the weights) over at
+// most one block per CU whose waves would have exactly 3 k steps each at
+// k split 4 (K of 1025-1536): graph replay, 1.5B q/o 1536 x 1536 at M = 16
+// 4.64 -> 4.44 us, k/v 256 x 1536 4.49 -> 4.30.  On longer rows the second
+// wave per SIMD costs more than the shorter chain saves (0.5B down 896 x
+// 4864 at M = 8 / 16: 6.42 / 7.56 -> 8.09 / 9.01 us; 1.5B down at M = 8
+// 9.46 -> 9.75), and at 8 rows it gains nothing (q/o 4.08 -> 4.06).
+inline bool dot_split8(int64_t M, int64_t tiles, int64_t K, int64_t cus)
+{
+    return M > 8 && M <= kDotMaxM && tiles <= cus && dot_wave_steps(K, 4) == 3;
+}
 // The activation tile's rule, for a launch of max_m rows whose problems
 // re-read `reread` activation bytes over their tiles and give a wave at most
 // `wave_steps` k steps (launch_dot, launch_dot_grouped and the dispatcher).
@@ -192,7 +204,7 @@ inline bool dot_fits(int64_t N, int64_t K)
 inline int64_t dot_blocks(const LinArgs& a)
 {
     const int64_t tiles = (a.N + kDecodeTileN - 1) / kDecodeTileN;
-    const int64_t tiles_per_block = 4 / a.ksplit;
+    const int64_t tiles_per_block = (a.ksplit > 4 ? 8 : 4) / a.ksplit;  // blocks of 4 waves, of 8 at k split 8
     return (tiles + tiles_per_block - 1) / tiles_per_block;
 }
 // Activations are staged in LDS when M rows of K + 8 halves fit beside the

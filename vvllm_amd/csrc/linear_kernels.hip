@@ -396,10 +396,10 @@ __device__ __forceinline__ DecodeCoord dot_coord(const LinArgs& a, int64_t block
     DecodeCoord c;
     c.lane = threadIdx.x & 63;
     c.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: keeps the loops scalar
-    c.ksplit = a.ksplit;  // 1, 2 or 4: shifts, not divisions
+    c.ksplit = a.ksplit;  // 1, 2 or 4 (blocks of 4 waves), 8 (of 8): shifts, not divisions
     const int lg = __builtin_ctz(c.ksplit);
     c.ks = c.wave & (c.ksplit - 1);
-    c.tile = block * (4 >> lg) + (c.wave >> lg);
+    c.tile = block * ((c.ksplit > 4 ? 8 : 4) >> lg) + (c.wave >> lg);
     const int32_t steps = ((int32_t)a.K + kDotStep - 1) / kDotStep;  // K <= INT32_MAX - kDotStep
     const int32_t per = (steps + c.ksplit - 1) >> lg;
     c.s0 = c.ks * per < steps ? c.ks * per : steps;
@@ -411,9 +411,11 @@ __device__ __forceinline__ DecodeCoord dot_coord(const LinArgs& a, int64_t block
 // wave, then (when they fit) the staged activations, M rows with a row
 // stride of K + 8 halves.  The launcher sizes the dynamic LDS with the same
 // rule (dot_lds_bytes), so kernel and launcher agree on where x lives.
-struct DotRed {
-    float v[4][kDotMaxM][16];  // [wave][m][row]
+template <int NW>
+struct DotRedN {
+    float v[NW][kDotMaxM][16];  // [wave][m][row]
 };
+using DotRed = DotRedN<4>;
 static_assert(sizeof(DotRed) == kDotRedBytes, "reduction scratch size");
 
 // 16 fp16 activations times 16 exact fp16 codes, accumulated in fp32.
@@ -529,7 +531,7 @@ __device__ __forceinline__ void dot_store_glu(const LinArgs& a, int64_t rowA, in
     }
 }
 
-template <typename OT, int MT, int XS, bool EARLY, int DEPTH, int FS>
+template <typename OT, int MT, int XS, bool EARLY, int DEPTH, int FS, int NW = 4>
 __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* smem, int64_t pos)
 {
     // where the activations come from (XS, chosen per launch on the host):
@@ -580,8 +582,13 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
     constexpr bool x_first = XR > 0 && EARLY && XLDS && MT <= 4;
     constexpr bool first = rms_first || attn_first || x_first;
     static_assert(FS == kFirstNone || first, "a first stage this launch cannot run");
-    DotRed& red = *reinterpret_cast<DotRed*>(smem);
-    f16* xs = reinterpret_cast<f16*>(smem + kDotRedBytes);
+    // NW waves per block: 4, or 8 (k split 8) on the plain MFMA path with
+    // the activations loaded with the weights; the reduction scratch and the
+    // per-wave LDS tiles scale with it
+    static_assert(NW == 4 || (NW == 8 && MT >= 4 && !XLDS && FS == kFirstNone), "8-wave blocks: plain MFMA path");
+    constexpr int64_t RB = kDotRedBytes * NW / 4, WB = kDotWtBytes * NW / 4;
+    DotRedN<NW>& red = *reinterpret_cast<DotRedN<NW>*>(smem);
+    f16* xs = reinterpret_cast<f16*>(smem + RB);
     const DecodeCoord c = dot_coord(a, block);
     const int r = c.lane >> 3, ch = c.lane & 7;
     const int64_t n0 = c.tile * kDecodeTileN;
@@ -624,8 +631,8 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
     // its activation row (clamped: columns past M are computed and unused)
     const int fi = c.lane & 15, fg = c.lane >> 4;
     const int32_t fm = fi < a.M ? fi : 0;
-    char* wt = smem + kDotRedBytes + (XLDS ? a.M * ldx * 2 : 0) + c.wave * (16 * kDotWtPitch);
-    char* xt = smem + kDotRedBytes + kDotWtBytes + c.wave * (16 * kDotXtPitch);  // XW
+    char* wt = smem + RB + (XLDS ? a.M * ldx * 2 : 0) + c.wave * (16 * kDotWtPitch);
+    char* xt = smem + RB + WB + c.wave * (16 * kDotXtPitch);  // XW
 
     // Ring of D slots, one k step each: the two weight chunks of the step
     // and, when the activations are not in LDS, their activation chunks
@@ -1174,8 +1181,8 @@ __device__ __forceinline__ void dot_body(const LinArgs& a, int64_t block, char* 
 // mk = M | ksplit << 8; xi = xparts | xhd << 8 for the attention merge stage
 // (its part loads need both), else 0.
 // A plain call has no RoPE or SiLU-gated epilogue.
-template <typename OT, int MT, int XS, bool EARLY, int DEPTH, int FS>
-__global__ __launch_bounds__(256) void k_dot(const int8_t* w, const void* inp, const float* scales,
+template <typename OT, int MT, int XS, bool EARLY, int DEPTH, int FS, int NW>
+__global__ __launch_bounds__(64 * NW) void k_dot(const int8_t* w, const void* inp, const float* scales,
                                              const float* bias, const void* res, int32_t N, int32_t K, int32_t mk,
                                              int32_t xi, const LinArgs a)
 {
@@ -1196,7 +1203,7 @@ __global__ __launch_bounds__(256) void k_dot(const int8_t* w, const void* inp, c
     }
     b.rope = 0;
     b.glu = 0;
-    dot_body<OT, MT, XS, EARLY, DEPTH, FS>(b, blockIdx.x, dot_smem, 0);
+    dot_body<OT, MT, XS, EARLY, DEPTH, FS, NW>(b, blockIdx.x, dot_smem, 0);
 }
 
 // Grouped launch.  count <= kDotInline: the problems are g.p[0, count) and
@@ -1840,29 +1847,29 @@ int launch_skinny_grouped(const LinArgs* dev_table, int count, int64_t total_blo
     return (int)hipGetLastError();
 }
 
-template <int MT, int XS, bool EARLY, int DEPTH, int FS>
+template <int MT, int XS, bool EARLY, int DEPTH, int FS, int NW = 4>
 static void dot_launch(const LinArgs& a, int out, dim3 grid, size_t lds, hipStream_t s)
 {
     // dot_fits(N, K) holds (checked by the runtime); M <= kDotMaxM, ksplit
-    // <= 4, xparts <= kAttnMaxParts and xhd <= kAttnMergeMaxK (checked by
+    // <= 8, xparts <= kAttnMaxParts and xhd <= kAttnMergeMaxK (checked by
     // vvh_linear_q8_dev_attn) fit their fields
     const int32_t N = (int32_t)a.N, K = (int32_t)a.K;
     const int32_t mk = (int32_t)a.M | a.ksplit << 8;
     const int32_t xi = FS == kFirstAttn ? (a.xparts | a.xhd << 8) : 0;
     if (out == VVH_F32)
-        hipLaunchKernelGGL((k_dot<float, MT, XS, EARLY, DEPTH, FS>), grid, dim3(256), lds, s, a.w, a.inp,
+        hipLaunchKernelGGL((k_dot<float, MT, XS, EARLY, DEPTH, FS, NW>), grid, dim3(64 * NW), lds, s, a.w, a.inp,
                            a.scales, a.bias, a.res, N, K, mk, xi, a);
     else
-        hipLaunchKernelGGL((k_dot<f16, MT, XS, EARLY, DEPTH, FS>), grid, dim3(256), lds, s, a.w, a.inp,
+        hipLaunchKernelGGL((k_dot<f16, MT, XS, EARLY, DEPTH, FS, NW>), grid, dim3(64 * NW), lds, s, a.w, a.inp,
                            a.scales, a.bias, a.res, N, K, mk, xi, a);
 }
 
-template <int MT, int XS, bool EARLY, int FS>
+template <int MT, int XS, bool EARLY, int FS, int NW = 4>
 static void dot_launch_d(const LinArgs& a, int out, int depth, dim3 grid, size_t lds, hipStream_t s)
 {
-    if (depth <= 2) dot_launch<MT, XS, EARLY, 2, FS>(a, out, grid, lds, s);
-    else if (depth <= 4) dot_launch<MT, XS, EARLY, 4, FS>(a, out, grid, lds, s);
-    else dot_launch<MT, XS, EARLY, 7, FS>(a, out, grid, lds, s);
+    if (depth <= 2) dot_launch<MT, XS, EARLY, 2, FS, NW>(a, out, grid, lds, s);
+    else if (depth <= 4) dot_launch<MT, XS, EARLY, 4, FS, NW>(a, out, grid, lds, s);
+    else dot_launch<MT, XS, EARLY, 7, FS, NW>(a, out, grid, lds, s);
 }
 
 // first stages exist for early launches with staged activations only
@@ -1910,9 +1917,19 @@ int launch_dot(const LinArgs& a, int out, bool early, int depth, void* stream)
     // the activation tile: MFMA path (M > 2), early launches loading the
     // activations with the weights, tiles re-reading many activation bytes
     const bool xt = dot_takes_x_tile(a.M, early, xl, reread, wsteps);
+    hipStream_t st = S(stream);
+    if (a.ksplit == 8) {
+        // blocks of 8 waves (dot_split8): the plain MFMA path of an early
+        // launch loading its activations with the weights, nothing else
+        if (a.M <= 8 || a.M > kDotMaxM || !early || a.xop != 0 || xl || fs != kFirstNone)
+            return (int)hipErrorInvalidValue;
+        const size_t lds8 = 2 * (kDotRedBytes + kDotWtBytes + (xt ? kDotXtBytes : 0));
+        if (xt) dot_launch_d<16, kXTile, true, kFirstNone, 8>(a, out, depth, grid, lds8, st);
+        else dot_launch_d<16, kXDirect, true, kFirstNone, 8>(a, out, depth, grid, lds8, st);
+        return (int)hipGetLastError();
+    }
     const size_t lds = (xl ? dot_lds_bytes(a.M, a.K) : (size_t)kDotRedBytes) + (a.M > 2 ? kDotWtBytes : 0) +
                        (xt ? kDotXtBytes : 0);
-    hipStream_t st = S(stream);
     if (a.M <= 1) {
         if (xl) dot_launch_e<1, kXLds>(a, out, early, fs, depth, grid, lds, st);
         else dot_launch_e<1, kXDirect>(a, out, early, fs, depth, grid, lds, st);

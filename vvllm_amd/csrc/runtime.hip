@@ -653,6 +653,8 @@ int run_call(const LinArgs& base, int kernel, int act, int outd, void* stream, c
         case K_DOT: {
             const int64_t tiles = (a.N + kDecodeTileN - 1) / kDecodeTileN;
             a.ksplit = choose_ksplit(tiles, a.K, kDotStep);
+            if (a.ksplit == 4 && a.xop == 0 && dot_split8(a.M, tiles, a.K, g_cu_count > 0 ? g_cu_count : 256))
+                a.ksplit = 8;
             if (dot_blocks(a) > INT32_MAX) return fail(VVH_ERR_UNSUPPORTED, "problem too large for the decode grid");
             if (!dot_fits(a.N, a.K))
                 return fail(VVH_ERR_UNSUPPORTED, "N (%lld) or K (%lld) too large for the decode kernel",
