@@ -184,7 +184,9 @@ inline int64_t dot_wave_steps(int64_t K, int32_t ksplit)
 // 4.64 -> 4.44 us, k/v 256 x 1536 4.49 -> 4.30.  On longer rows the second
 // wave per SIMD costs more than the shorter chain saves (0.5B down 896 x
 // 4864 at M = 8 / 16: 6.42 / 7.56 -> 8.09 / 9.01 us; 1.5B down at M = 8
-// 9.46 -> 9.75), and at 8 rows it gains nothing (q/o 4.08 -> 4.06).
+// 9.46 -> 9.75), on rows of 2 steps per wave at split 4 it loses too
+// (0.5B q/o 896 x 896 at M = 16 3.61 -> 4.45 us, 1024 x 1024 3.61 -> 4.68),
+// and at 8 rows it gains nothing (q/o 4.08 -> 4.06).
 inline bool dot_split8(int64_t M, int64_t tiles, int64_t K, int64_t cus)
 {
     return M > 8 && M <= kDotMaxM && tiles <= cus && dot_wave_steps(K, 4) == 3;
